@@ -1,0 +1,104 @@
+/* libmiq -- MI355X (gfx950) quantized-linear hot path, C ABI.
+ *
+ * Every entry point takes raw device pointers, element counts and a hipStream_t (passed as
+ * void*; NULL is the default stream). Work is enqueued on that stream and the call returns
+ * without synchronising. The caller owns all memory (inputs, outputs, workspace); the library
+ * keeps no pointers between calls. Return value: MIQ_OK (0) or a negative MIQ_ERR_* code, with
+ * a message for the calling thread in miq_last_error(). No exception crosses this boundary.
+ *
+ * Reference interfaces replaced (xnetsc/webpytorch, "webtorch"): each declaration cites the
+ * reference function whose work it performs. In the reference those functions dispatch WGSL
+ * through `plat.runKernel` (webgpu/wgpy_backends/webgpu/platform.py:39-43) or fall back to
+ * numpy; here they are HIP kernels.
+ */
+#ifndef MIQ_H
+#define MIQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIQ_VERSION 1
+
+/* return codes */
+#define MIQ_OK 0
+#define MIQ_ERR_INVALID (-1)     /* bad shape or argument (reference: AssertionError/ValueError) */
+#define MIQ_ERR_ALIGN (-2)       /* pointer or leading dimension not aligned as required */
+#define MIQ_ERR_UNSUPPORTED (-3) /* variant not implemented (reference: NotImplementedError) */
+#define MIQ_ERR_HIP (-4)         /* a HIP runtime call or kernel launch failed */
+
+/* element types of activations, outputs and scales */
+#define MIQ_F32 0
+#define MIQ_F16 1
+
+/* Message describing the last error on the calling thread ("" if none). */
+const char* miq_last_error(void);
+/* MIQ_VERSION of the built library. */
+int miq_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * GPTQ int4/int8 (AutoGPTQ layout)
+ *   qweight int32 [K/per][N] (per = 32/bits), qzeros int32 [K/gs][N/per],
+ *   scales fp16 or fp32 [K/gs][N], W[k][n] = s[g][n] * (q[k][n] - (z[g][n] + zero_offset)).
+ * ------------------------------------------------------------------------------------- */
+
+/* Full fp32 dequant, out [K][N]. g_idx (int32 [K], nullable) maps row -> group (act-order);
+ * NULL means g = k / gs. Bit-exact with the reference's float64 product rounded to float32
+ * for integer zero offsets.
+ * Replaces: `_dequant_full` (webtorch/_core.py:4696-4720) and the dequant step of
+ * `_gptq_matmul_np` (webtorch/_core.py:4046-4072). */
+int miq_gptq_dequant_f32(const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                         int scales_dtype, const int32_t* g_idx, float* out, int K, int N,
+                         int gs, int bits, float zero_offset, void* stream);
+
+/* Act-order load-time repack: out row block r holds original rows perm[r*per + j]. With
+ * perm = stable argsort(g_idx), groups become consecutive runs of gs rows and the layer runs
+ * on the plain kernels with the activation gathered through the same perm.
+ * Replaces: nothing in the reference, which ignores g_idx (webtorch/llm.py:569-573,
+ * webtorch/_core.py:4420-4430); it is the load step behind `from_autogptq(..., g_idx=)`. */
+int miq_gptq_repack_rows(const int32_t* qweight, const int32_t* perm, int32_t* out, int K, int N,
+                         int bits, void* stream);
+
+/* Decode GEMV / skinny GEMM: out[M][N] = x[M][K] (gathered through perm if non-NULL)
+ * @ W + bias (nullable, fp32). x fp16|fp32, out fp16|fp32, fp32 accumulation. Requires
+ * qweight 16-byte aligned; any M (efficient for M <= 8).
+ * Replaces: `_gptq_matmul` M == 1 dispatch to `_GPTQ_GEMV_WGSL`
+ * (webtorch/_core.py:3926-3978, 4008-4027) and the bias add of `QuantizedLinear.forward`
+ * (webtorch/_core.py:4446-4456). */
+int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, const int32_t* qweight,
+                  const int32_t* qzeros, const void* scales, int scales_dtype, const float* bias,
+                  void* out, int out_dtype, int M, int K, int N, int gs, int bits,
+                  float zero_offset, void* stream);
+
+/* Asymmetric min-max quantizer to the GPTQ layout (zero_offset 0, fp32 scales), bit-exact
+ * with the reference's float32 numpy arithmetic (IEEE division, round-half-even). W is
+ * [K][N] or, with from_out_in = 1, [N][K]; fp16 or fp32. Outputs qweight [K/per][N],
+ * qzeros [K/gs][N/per], scales [K/gs][N].
+ * Replaces: `_gptq_quantize` (webtorch/_core.py:3782-3824) as used by
+ * `QuantizedLinear.from_linear` (4433-4444), the tied-head requantization
+ * `CausalLM._quantize_head` (webtorch/llm.py:594-602) and `_gquant` (llm.py:835-853). */
+int miq_gptq_quantize(const void* W, int w_dtype, int from_out_in, int K, int N, int gs, int bits,
+                      int32_t* qweight, int32_t* qzeros, float* scales, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * GGUF Q4_K (llama.cpp block_q4_K, 144-byte super-blocks of 256 weights)
+ * ------------------------------------------------------------------------------------- */
+
+/* Dequant n_blocks super-blocks to fp32 (256 values each). blocks 16-byte aligned.
+ * Replaces: `ggufload.dequant` Q4_K (webtorch/ggufload.py:116-130, 188-202). */
+int miq_q4k_dequant_f32(const uint8_t* blocks, float* out, int64_t n_blocks, void* stream);
+
+/* out[M][N] = x[M][K] @ W^T + bias, W = N rows of K/256 native super-blocks.
+ * Replaces: `ggml_matmul` / `_ggml_run` for Q4_K (webtorch/_core.py:3720-3779) with the
+ * decode kernel `_GGML_GEMV_*` + `_Q4K_DEC` (webtorch/_core.py:2985-3044, 3117-3133). */
+int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out,
+                 int out_dtype, int M, int K, int N, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIQ_H */

@@ -1,0 +1,128 @@
+"""CPU greedy decode of a Qwen2-shaped int4 model (test infrastructure only; see
+`oracle/__init__.py`).
+
+Follows the reference's growing-cache forward: `CausalLM._kv_forward` (`webtorch/llm.py:
+1619-1636`) with `KVCache.attn` (`webtorch/_core.py:1543-1596`), `gqa_attention`
+(`_core.py:1319-1340`), the numpy `softmax` (`_core.py:1764-1787`), RMSNorm as an
+expression (`llm.py:1260-1268`), HF rotate-half RoPE with float64 angles (`llm.py:1270-1304`),
+SwiGLU (`llm.py:1489-1496`, `silu` `_core.py:503-504`), the tied head re-quantized with
+`_gptq_quantize` in 4096-row blocks (`llm.py:594-602`) and greedy `argmax` (`llm.py:1336`).
+`generate` with no end token yields the prefill's token then one per decode step
+(`llm.py:1775-1787`).
+
+Pins: golden token ids written by the reference's own `CausalLM` CPU path at a reduced
+shape (`tests/golden/`); every building block is also pinned on its own (RMSNorm, RoPE and
+softmax closed forms, `gptq.gptq_matmul_np`).
+"""
+import math
+
+import numpy as np
+
+from . import gptq
+
+
+class Qwen2Oracle:
+    def __init__(self, weights, lmax=256, head_block=4096):
+        c = weights["cfg"]
+        self.L, self.H, self.NH, self.NKV, self.HD = c["L"], c["H"], c["NH"], c["NKV"], c["HD"]
+        self.V, self.gs, self.bits = c["V"], c["gs"], c["bits"]
+        self.eps, self.theta = c.get("eps", 1e-6), c.get("theta", 1e6)
+        self.lmax = lmax
+        self.layers = weights["layers"]
+        self.embed = weights["embed"]                      # (V, H) fp16
+        self.final_norm = np.asarray(weights["final_norm"], np.float32)
+        self.head = self.quantize_head(self.embed, head_block)
+
+    def quantize_head(self, emb, blk):
+        out = []
+        for v0 in range(0, emb.shape[0], blk):
+            v1 = min(emb.shape[0], v0 + blk)
+            qw, qz, sc, _, _ = gptq.gptq_quantize(
+                np.ascontiguousarray(emb[v0:v1].astype(np.float32).T), self.gs, self.bits)
+            out.append({"qweight": qw, "qzeros": qz, "scales": sc, "K": self.H, "N": v1 - v0,
+                        "gs": self.gs, "bits": self.bits})
+        return out
+
+    # ---- building blocks ----
+    def rms(self, x, w):
+        return (x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + self.eps)) * \
+            np.asarray(w, np.float32)
+
+    def lin(self, d, x, zoff=1.0):
+        y = gptq.gptq_matmul_np(x, d["qweight"], d["qzeros"], d["scales"], d["K"], d["N"],
+                                d["gs"], d["bits"], zoff)
+        b = d.get("bias")
+        return y + (np.zeros(d["N"], np.float32) if b is None else np.asarray(b, np.float32))
+
+    def rope_tables(self, pos, T):
+        inv = 1.0 / (self.theta ** (np.arange(0, self.HD, 2, dtype=np.float64) / self.HD))
+        ang = np.arange(pos, pos + T, dtype=np.float64)[:, None] * inv[None, :]
+        emb = np.concatenate([ang, ang], -1)
+        return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
+
+    def rot(self, x):
+        h = self.HD // 2
+        return np.concatenate([x[..., h:] * -1.0, x[..., :h]], axis=-1).astype(np.float32)
+
+    @staticmethod
+    def softmax(a):
+        m = a.max(axis=-1, keepdims=True)
+        e = np.exp(a - m)
+        return e / e.sum(axis=-1, keepdims=True)
+
+    @staticmethod
+    def silu(x):
+        return x * (1.0 / (1.0 + np.exp(-x)))
+
+    def attend(self, q, K, V, mask, scale):
+        nh, T, hd = q.shape
+        nkv, S, _ = K.shape
+        rep = nh // nkv
+        a = (q.reshape(nkv, rep * T, hd) @ np.ascontiguousarray(K.transpose(0, 2, 1))) * scale
+        if mask is not None:
+            a = (a.reshape(nkv, rep, T, S) + mask).reshape(nkv, rep * T, S)
+        return (self.softmax(a) @ V).reshape(nh, T, hd)
+
+    # ---- forward ----
+    def forward(self, ids, pos, cache):
+        """One `_kv_forward` call: T tokens at positions pos.. -> greedy next id, logits."""
+        T = len(ids)
+        cos, sin = self.rope_tables(pos, T)
+        h = np.asarray(self.embed[np.asarray(ids, np.int64)], np.float32)
+        scale = 1.0 / math.sqrt(self.HD)
+        for i, lay in enumerate(self.layers):
+            x = self.rms(h, lay["in_ln"])
+            q = self.lin(lay["q"], x).reshape(T, self.NH, self.HD).transpose(1, 0, 2)
+            k = self.lin(lay["k"], x).reshape(T, self.NKV, self.HD).transpose(1, 0, 2)
+            v = self.lin(lay["v"], x).reshape(T, self.NKV, self.HD).transpose(1, 0, 2)
+            q = q * cos + self.rot(q) * sin
+            k = k * cos + self.rot(k) * sin
+            if cache[i] is None:
+                cache[i] = (np.ascontiguousarray(k), np.ascontiguousarray(v))
+            else:
+                cache[i] = (np.concatenate([cache[i][0], k], 1), np.concatenate([cache[i][1], v], 1))
+            Kc, Vc = cache[i]
+            S = Kc.shape[1]
+            mask = None
+            if T > 1:
+                mask = np.triu(np.full((T, S), -1e9, np.float32), 1 + (S - T)).reshape(1, T, S)
+            o = self.attend(q, Kc, Vc, mask, scale)
+            h = h + self.lin(lay["o"], o.transpose(1, 0, 2).reshape(T, self.NH * self.HD))
+            x = self.rms(h, lay["post_ln"])
+            h = h + self.lin(lay["down"], self.silu(self.lin(lay["gate"], x)) * self.lin(lay["up"], x))
+        last = self.rms(h, self.final_norm)[-1:]
+        logits = np.concatenate([self.lin(b, last, zoff=0.0) for b in self.head], axis=-1)[0]
+        return int(logits.argmax()), logits
+
+    def generate(self, ids, max_new, keep_logits=False):
+        """Greedy decode, no end token: returns (token ids, per-step logits or None)."""
+        cache = [None] * self.L
+        nxt, lg = self.forward(list(ids), 0, cache)
+        out, logs, pos = [nxt], [lg] if keep_logits else None, len(ids)
+        while len(out) < max_new:
+            nxt, lg = self.forward([nxt], pos, cache)
+            pos += 1
+            out.append(nxt)
+            if keep_logits:
+                logs.append(lg)
+        return out, logs

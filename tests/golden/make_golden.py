@@ -1,0 +1,164 @@
+"""Write golden vectors by running the REFERENCE's own numpy path (run in the build container
+only; `/root/reference` never travels with the repository).
+
+Only functions that no closed form pins are recorded here:
+  * `_gptq_quantize` bit patterns (round-half-even ties, constant groups, int8,
+    from_out_in) -- `webtorch/_core.py:3782-3824`
+  * `lm_engine.moe_mlp` output on a small seeded instance -- `webtorch/lm_engine.py:294-333`
+  * `CausalLM.generate` greedy token ids on the CPU growing-cache path, at a reduced shape and
+    at the full Qwen2-0.5B shape -- `webtorch/llm.py:1716-1787`
+
+Inputs are regenerated from seeds by `webpytorch_amd.synth`; the fixtures hold the seeds,
+the shapes and the reference's outputs. Usage: python tests/golden/make_golden.py [--full]
+"""
+import argparse
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.abspath(os.path.join(HERE, "..", "..")))
+REF = "/root/reference"
+
+from webpytorch_amd import synth  # noqa: E402
+
+
+def import_reference():
+    # The reference falls back to numpy when its browser array backend cannot be imported
+    # (`webtorch/_core.py:11-17`); that fallback is the CPU path recorded here.
+    sys.path.insert(0, REF)
+    from webtorch import _core as wt
+    from webtorch import lm_engine, llm
+    assert wt.xp is np and not wt.GPU, "reference did not take its numpy fallback"
+    return wt, lm_engine, llm
+
+
+def quantize_cases():
+    g = np.random.default_rng(1234)
+    cases = []
+    # plain random weights, int4 gs=32
+    cases.append(("rand_b4_g32", (g.standard_normal((256, 64)) * 0.1).astype(np.float32), 32, 4, False))
+    # values on a coarse grid: many w/scale land exactly on .5 (half-even ties)
+    grid = (g.integers(-8, 8, (256, 64)) * 0.125).astype(np.float32)
+    cases.append(("ties_b4_g32", grid, 32, 4, False))
+    # constant groups (scale 0 -> 1e-8), mixed with a normal column block
+    const = np.repeat(g.standard_normal((1, 64)).astype(np.float32), 128, 0)
+    const[:, 32:] = (g.standard_normal((128, 32)) * 0.05).astype(np.float32)
+    cases.append(("const_b4_g64", const, 64, 4, False))
+    # all-zero weight
+    cases.append(("zeros_b4_g32", np.zeros((64, 16), np.float32), 32, 4, False))
+    # int8 groups of 128
+    cases.append(("rand_b8_g128", (g.standard_normal((256, 64)) * 0.1).astype(np.float32), 128, 8, False))
+    # (out, in) layout with a column block smaller than N
+    cases.append(("outin_b4_g128", (g.standard_normal((96, 256)) * 0.02).astype(np.float32), 128, 4, True))
+    # fp16-origin head rows (the tied-embedding head requantization)
+    emb = (g.standard_normal((40, 128)) * 0.02).astype(np.float16)
+    cases.append(("head_b4_g128", np.ascontiguousarray(emb.astype(np.float32).T), 128, 4, False))
+    return cases
+
+
+def make_quantize(wt, out):
+    d = {}
+    for name, W, gs, bits, oi in quantize_cases():
+        kw = {"from_out_in": True, "block": 32} if oi else {}
+        qw, qz, sc, K, N = wt._gptq_quantize(W, gs, bits, **kw)
+        d[name + ".W"] = W
+        d[name + ".meta"] = np.array([gs, bits, int(oi), K, N], np.int64)
+        d[name + ".qweight"] = qw
+        d[name + ".qzeros"] = qz
+        d[name + ".scales"] = sc
+    np.savez_compressed(out, **d)
+
+
+class _Lm:
+    def __init__(self, H):
+        self.H = H
+
+
+def make_moe(wt, lm_engine, out, seed=7, T=12, H=128, E=8, I=64, top_k=2, gs=64):
+    w = synth.moe_workload(seed, T=T, H=H, E=E, I=I, top_k=top_k, gs=gs)
+    experts = []
+    for ex in w["experts"]:
+        experts.append({k: wt.QuantizedLinear.from_autogptq(v["qweight"], v["qzeros"],
+                                                             v["scales"], None, gs, 4)
+                        for k, v in ex.items()})
+    logits = w["logits"]
+    moe = {"gate": lambda x: wt.Tensor(logits), "top_k": top_k, "norm_topk_prob": True,
+           "experts": experts, "shared": None}
+    x = wt.Tensor(w["x"].astype(np.float32))
+    y = lm_engine.moe_mlp(_Lm(H), {"moe": moe}, x).numpy()
+    np.savez_compressed(out, seed=seed, dims=np.array([T, H, E, I, top_k, gs]), y=y)
+
+
+class _Tok:
+    eot = -1
+    eos_ids = []
+
+    def decode(self, ids):
+        return ""
+
+
+def build_reference_lm(wt, llm, wts, lmax):
+    c = wts["cfg"]
+    m = llm.CausalLM("")
+    m._apply_cfg({"hidden_size": c["H"], "num_hidden_layers": c["L"],
+                  "num_attention_heads": c["NH"], "num_key_value_heads": c["NKV"],
+                  "head_dim": c["HD"], "vocab_size": c["V"], "rms_norm_eps": 1e-6,
+                  "rope_theta": 1e6, "tie_word_embeddings": True})
+    m.gs, m.bits, m.lmax = c["gs"], c["bits"], lmax
+    m.tok = _Tok()
+    m.gen_defaults = {}
+    m._gpu = False
+    m.embed = wts["embed"]
+    m.head = m._quantize_head(m.embed)
+
+    def ql(d):
+        b = d.get("bias")
+        return wt.QuantizedLinear.from_autogptq(d["qweight"], d["qzeros"], d["scales"],
+                                                None if b is None else b.astype(np.float32),
+                                                d["gs"], d["bits"])
+    m.layers = []
+    for lay in wts["layers"]:
+        m.layers.append({"in_ln": wt.Tensor(lay["in_ln"].astype(np.float32)),
+                         "post_ln": wt.Tensor(lay["post_ln"].astype(np.float32)),
+                         "q": ql(lay["q"]), "k": ql(lay["k"]), "v": ql(lay["v"]),
+                         "o": ql(lay["o"]), "qn": None, "kn": None,
+                         "gate": ql(lay["gate"]), "up": ql(lay["up"]), "down": ql(lay["down"])})
+    m.final_norm = wt.Tensor(wts["final_norm"].astype(np.float32))
+    m._init_state()
+    return m
+
+
+def make_decode(wt, llm, out, seed, shape, prompt_len, max_new, lmax):
+    wts = synth.decoder_weights(seed, **shape)
+    ids = synth.prompt_ids(seed, prompt_len, shape["V"])
+    m = build_reference_lm(wt, llm, wts, lmax)
+    t0 = time.time()
+    res = m.generate(ids=[int(i) for i in ids], max_new=max_new)
+    dt = time.time() - t0
+    print("%s: %d tokens in %.1fs" % (os.path.basename(out), len(res.tokens), dt))
+    np.savez_compressed(out, seed=seed, prompt_len=prompt_len, max_new=max_new, lmax=lmax,
+                        shape=np.array([shape[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits")]),
+                        tokens=np.asarray(res.tokens, np.int64))
+
+
+SMALL = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--full", action="store_true", help="also the full Qwen2-0.5B-shaped decode")
+    a = ap.parse_args()
+    wt, lm_engine, llm = import_reference()
+    make_quantize(wt, os.path.join(HERE, "gptq_quantize.npz"))
+    make_moe(wt, lm_engine, os.path.join(HERE, "moe_small.npz"))
+    make_decode(wt, llm, os.path.join(HERE, "decode_small.npz"), 11, SMALL, 16, 24, 64)
+    if a.full:
+        make_decode(wt, llm, os.path.join(HERE, "decode_qwen2_05b.npz"), 5, dict(synth.QWEN2_05B),
+                    64, 128, 256)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,162 @@
+"""GPU parity: GPTQ dequant / quantizer (bit-exact) and GEMV (tolerance) against the oracle."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import gptq
+from webpytorch_amd import synth
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _close(got, ref, rtol=1e-2, atol=1e-3):
+    """|got - ref| <= atol + rtol * |ref| elementwise."""
+    got = np.asarray(got, np.float64); ref = np.asarray(ref, np.float64)
+    bad = np.abs(got - ref) > atol + rtol * np.abs(ref)
+    assert not bad.any(), "max err %.3g at %s" % (np.abs(got - ref).max(), np.argwhere(bad)[:3])
+
+
+def _rel(got, ref):
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / (np.abs(ref).max() + 1e-30))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("sdt", ["f16", "f32"])
+@pytest.mark.parametrize("zoff", [0.0, 1.0])
+@pytest.mark.parametrize("act", [False, True])
+def test_dequant_bit_exact(gpu, bits, sdt, zoff, act):
+    import torch
+    from webpytorch_amd import core
+    L = synth.gptq_layer(21, 512, 264, 128, bits, act_order=act)
+    sc = L["scales"] if sdt == "f16" else (L["scales"].astype(np.float32) * np.float32(1.37))
+    g_idx = L["g_idx"] if act else None
+    W = core.gptq_dequant(core.to_device(L["qweight"]), core.to_device(L["qzeros"]), core.to_device(sc),
+                          512, 264, 128, bits, zoff, None if g_idx is None else core.to_device(g_idx))
+    ref = gptq.dequant_closed_form(L["qweight"], L["qzeros"], sc, 128, bits, zoff, g_idx=g_idx)
+    torch.cuda.synchronize()
+    assert np.array_equal(W.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+def test_quantizer_bit_exact_with_reference_golden(gpu):
+    from webpytorch_amd import core
+    d = np.load(os.path.join(GOLDEN, "gptq_quantize.npz"))
+    for n in sorted({k.split(".")[0] for k in d.files}):
+        gs, bits, oi, K, N = [int(v) for v in d[n + ".meta"]]
+        qw, qz, sc, _, _ = core.gptq_quantize(d[n + ".W"], gs, bits, from_out_in=bool(oi))
+        assert np.array_equal(qw.cpu().numpy(), d[n + ".qweight"]), n
+        assert np.array_equal(qz.cpu().numpy(), d[n + ".qzeros"]), n
+        assert np.array_equal(sc.cpu().numpy().view(np.uint32), d[n + ".scales"].view(np.uint32)), n
+
+
+def test_quantizer_bit_exact_fp16_head_block(gpu):
+    # a head block of the tied embedding: (V, H) fp16 rows quantized from the (out, in) layout
+    from webpytorch_amd import core
+    emb = (np.random.default_rng(3).standard_normal((4096, 896)) * 0.02).astype(np.float16)
+    qw, qz, sc, _, _ = core.gptq_quantize(emb, 128, 4, from_out_in=True)
+    r = gptq.gptq_quantize(np.ascontiguousarray(emb.astype(np.float32).T), 128, 4)
+    assert np.array_equal(qw.cpu().numpy(), r[0]) and np.array_equal(qz.cpu().numpy(), r[1])
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), r[2].view(np.uint32))
+
+
+# shapes of the reference's own kernel check (examples/gptq_int4_correctness.py:30-31)
+REF_SHAPES = [(128, 64, 32, 4), (256, 128, 128, 4), (3584, 512, 128, 4), (512, 1536, 128, 4),
+              (128, 24, 32, 4), (256, 64, 32, 8)]
+
+
+@pytest.mark.parametrize("K,N,gs,bits", REF_SHAPES)
+def test_quantized_linear_matches_numpy_dequant(gpu, K, N, gs, bits):
+    """Same procedure as the reference's check: quantize a random weight, compare the layer
+    with x @ dequant(W) for M in (1, 3, 4, 5, 32), rel err < 1e-4."""
+    import torch
+    from webpytorch_amd import core
+    rng = np.random.default_rng(0)
+    W = (rng.standard_normal((K, N)) * 0.1).astype(np.float32)
+    qw, qz, sc, _, _ = gptq.gptq_quantize(W, gs, bits)
+    ql = core.QuantizedLinear(qw, qz, sc, np.zeros(N, np.float32), K, N, K, N, gs, bits)
+    Wd = gptq.dequant_closed_form(qw, qz, sc, gs, bits, 0.0)
+    for M in (1, 3, 4, 5, 32):
+        x = (rng.standard_normal((M, K)) * 0.5).astype(np.float32)
+        got = ql(torch.from_numpy(x)).cpu().numpy()
+        ref = gptq.gptq_matmul_np(x, qw, qz, sc, K, N, gs, bits, 0.0)
+        assert _rel(got, ref) < 1e-4, (M, _rel(got, ref))
+        assert _rel(got, x.astype(np.float64) @ Wd) < 1e-4
+
+
+def test_config0_gemv_fp16(gpu):
+    """GPTQ int4 GEMV at the Qwen2-0.5B gate_proj shape (x fp16 (1, 896) -> y fp16 (1, 4864))."""
+    import torch
+    from webpytorch_amd import core
+    L = synth.gptq_layer(0, 896, 4864, 128, 4)
+    x = synth.activations(0, 1, 896, np.float16)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 128, 4)
+    y = ql(torch.from_numpy(x))
+    assert y.dtype == torch.float16 and tuple(y.shape) == (1, 4864)
+    ref = gptq.gptq_matmul_np(x, L["qweight"], L["qzeros"], L["scales"], 896, 4864, 128, 4, 1.0)
+    _close(y.float().cpu().numpy(), ref)
+    y32 = ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy()
+    assert _rel(y32, ref) < 1e-5
+    # repeated calls are deterministic (fixed-order reduction)
+    assert np.array_equal(y32, ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy())
+
+
+@pytest.mark.parametrize("M", [1, 4, 7])
+def test_act_order_gemv(gpu, M):
+    import torch
+    from webpytorch_amd import core
+    L = synth.gptq_layer(2, 4096, 4096, 128, 4, act_order=True)
+    x = synth.activations(2, M, 4096, np.float16)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 128, 4,
+                                            g_idx=L["g_idx"])
+    got = ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy()
+    ref = gptq.linear_forward(x, L, zoff=1.0, g_idx=L["g_idx"])
+    _close(got, ref)
+    assert _rel(got, ref) < 1e-5
+    W = ql.dequantize().cpu().numpy()
+    assert np.array_equal(W, gptq.dequant_closed_form(L["qweight"], L["qzeros"], L["scales"], 128, 4, 1.0,
+                                                      g_idx=L["g_idx"]))
+
+
+def test_int8_per_channel_gemv(gpu):
+    import torch
+    from webpytorch_amd import core
+    L = synth.int8_per_channel_layer(3, 4096, 4096)
+    x = synth.activations(3, 2, 4096, np.float16)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 4096, 8)
+    got = ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy()
+    ref = gptq.gptq_matmul_np(x, L["qweight"], L["qzeros"], L["scales"], 4096, 4096, 4096, 8, 1.0)
+    _close(got, ref)
+    assert _rel(got, ref) < 1e-5
+
+
+def test_bias_padding_and_leading_dims(gpu):
+    import torch
+    from webpytorch_amd import core
+
+    class Lin:  # the reference's Linear stores weight as (in, out)
+        pass
+    lin = Lin()
+    rng = np.random.default_rng(5)
+    lin.weight = (rng.standard_normal((200, 60)) * 0.1).astype(np.float32)   # K=200, N=60 -> padded
+    lin.bias = rng.standard_normal(60).astype(np.float32)
+    ql = core.QuantizedLinear.from_linear(lin, group_size=32, bits=4)
+    assert (ql.Kp, ql.Np, ql.Kt, ql.Nt) == (224, 64, 200, 60)
+    x = rng.standard_normal((2, 3, 200)).astype(np.float32)
+    got = ql(torch.from_numpy(x)).cpu().numpy()
+    Wp = np.pad(lin.weight, ((0, 24), (0, 4)))
+    qw, qz, sc, _, _ = gptq.gptq_quantize(Wp, 32, 4)
+    xp = np.pad(x.reshape(6, 200), ((0, 0), (0, 24)))
+    ref = gptq.gptq_matmul_np(xp, qw, qz, sc, 224, 64, 32, 4, 0.0)[:, :60] + lin.bias
+    assert got.shape == (2, 3, 60)
+    assert _rel(got.reshape(6, 60), ref) < 1e-5
+
+
+def test_errors_are_raised(gpu):
+    import torch
+    from webpytorch_amd import core
+    with pytest.raises(AssertionError):
+        core.QuantizedLinear(np.zeros((4, 8), np.int32), np.zeros((1, 1), np.int32), np.ones((1, 8), np.float16),
+                             None, 30, 8, 30, 8, 32, 4)
+    with pytest.raises(ValueError, match="g_idx"):
+        core.act_order_perm(np.zeros(64, np.int32), 32)

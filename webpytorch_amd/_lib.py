@@ -1,0 +1,60 @@
+"""ctypes binding of libmiq.so (the C ABI declared in include/miq.h).
+
+The library is loaded from this package directory only. There is no fallback: if it is
+missing or does not load, every operator raises. Build it with
+`python -m webpytorch_amd.build`.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmiq.so")
+
+MIQ_F32, MIQ_F16 = 0, 1
+ERRORS = {-1: ValueError, -2: ValueError, -3: NotImplementedError, -4: RuntimeError}
+
+_p, _i, _f, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_size_t
+
+# name -> argument types (restype is int for every compute entry point)
+SIGNATURES = {
+    "miq_gptq_dequant_f32": [_p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _f, _p],
+    "miq_gptq_repack_rows": [_p, _p, _p, _i, _i, _i, _p],
+    "miq_gptq_gemv": [_p, _i, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p],
+    "miq_gptq_quantize": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p],
+    "miq_q4k_dequant_f32": [_p, _p, _i64, _p],
+    "miq_q4k_gemv": [_p, _i, _p, _p, _p, _i, _i, _i, _i, _p],
+}
+
+_lib = None
+
+
+class MiqError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libmiq.so once; raise if it is absent (no CPU fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MiqError("libmiq.so is not built (%s); run `python -m webpytorch_amd.build`"
+                           % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        L.miq_last_error.restype = ctypes.c_char_p
+        L.miq_last_error.argtypes = []
+        L.miq_version.restype = ctypes.c_int
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def call(name, *args):
+    """Invoke an entry point and turn a negative return code into a Python exception."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().miq_last_error().decode(errors="replace")
+        raise ERRORS.get(rc, MiqError)("%s failed (%d): %s" % (name, rc, msg))
+    return rc

@@ -1,0 +1,302 @@
+"""Quantized linear operators on MI355X: drop-in counterparts of the reference's
+`QuantizedLinear`, `GGMLLinear`, `_gptq_matmul`, `ggml_matmul`, `ggml_native_supported` and
+`_gptq_quantize` (`webtorch/_core.py:3644-3824, 4008-4043, 4377-4459`).
+
+Host code is PyTorch-ROCm: torch owns device memory and the current HIP stream, and every
+operator enqueues hand-written HIP kernels from libmiq.so through its C ABI. There is no CPU
+path: without the library (or without a GPU) every call raises.
+
+Tensors may be given as numpy arrays (uploaded once, at construction) or torch tensors. The
+weight layouts are the reference's: qweight int32 (K/per, N), qzeros int32 (K/gs, N/per),
+scales (K/gs, N), Q4_K rows of 144-byte super-blocks.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import MIQ_F16, MIQ_F32
+
+# M above which a GPTQ matmul leaves the GEMV kernel for the MFMA GEMM.
+GEMV_MAX_M = 8
+
+
+# ---- plumbing --------------------------------------------------------------------------
+def device():
+    if not torch.cuda.is_available():
+        raise RuntimeError("webpytorch_amd needs a ROCm GPU (torch.cuda.is_available() is False)")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def stream_handle():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def dtype_code(t):
+    if t.dtype == torch.float16:
+        return MIQ_F16
+    if t.dtype == torch.float32:
+        return MIQ_F32
+    raise TypeError("unsupported dtype %s (float16 or float32)" % t.dtype)
+
+
+def to_device(a, dtype=None):
+    """numpy / torch -> contiguous tensor on the current GPU (no copy if already there)."""
+    if isinstance(a, torch.Tensor):
+        t = a
+    else:
+        arr = np.ascontiguousarray(a)
+        if arr.dtype == np.uint32:
+            arr = arr.view(np.int32)
+        t = torch.from_numpy(arr)
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t.to(device()).contiguous()
+
+
+def as_activation(x):
+    """Activation tensor on the GPU as float16 or float32 (other dtypes become float32)."""
+    t = getattr(x, "data", x) if not isinstance(x, (torch.Tensor, np.ndarray)) else x
+    t = to_device(t)
+    if t.dtype not in (torch.float16, torch.float32):
+        t = t.float()
+    return t
+
+
+def _scales(s):
+    t = to_device(s)
+    return t if t.dtype in (torch.float16, torch.float32) else t.float()
+
+
+# ---- GPTQ ----------------------------------------------------------------------------
+def gptq_dequant(qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, g_idx=None):
+    """Full fp32 weight (K, N); bit-exact with the reference's dequant for integer zoff."""
+    out = torch.empty((K, N), dtype=torch.float32, device=device())
+    _lib.call("miq_gptq_dequant_f32", ptr(qweight), ptr(qzeros), ptr(scales), dtype_code(scales),
+              ptr(g_idx), ptr(out), K, N, gs, bits, float(zoff), stream_handle())
+    return out
+
+
+def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=None, perm=None,
+                 out_dtype=None, out=None):
+    """xf (M, K) @ dequant(W) (+ bias) -> (M, N) on the current stream
+    (`webtorch/_core.py:4008-4043`). M <= GEMV_MAX_M runs the split-K GEMV; larger M the
+    MFMA GEMM."""
+    M = int(xf.shape[0])
+    od = out_dtype or xf.dtype
+    if out is None:
+        out = torch.empty((M, N), dtype=od, device=xf.device)
+    if M == 0:
+        return out
+    if M > GEMV_MAX_M and hasattr(_lib.lib(), "miq_gptq_gemm"):
+        return _gptq_gemm(xf, qweight, qzeros, scales, K, N, gs, bits, zoff, bias, perm, out)
+    _lib.call("miq_gptq_gemv", ptr(xf), dtype_code(xf), ptr(perm), ptr(qweight), ptr(qzeros),
+              ptr(scales), dtype_code(scales), ptr(bias), ptr(out), dtype_code(out), M, K, N, gs,
+              bits, float(zoff), stream_handle())
+    return out
+
+
+def _gptq_gemm(xf, qweight, qzeros, scales, K, N, gs, bits, zoff, bias, perm, out):
+    raise NotImplementedError("MFMA GEMM not built")
+
+
+def gptq_quantize(W, group_size=32, bits=4, from_out_in=False):
+    """Device quantizer, bit-exact with `_gptq_quantize` (`webtorch/_core.py:3782-3824`).
+    W (K, N) or (N, K) with from_out_in, float16/float32. Returns (qweight, qzeros, scales
+    float32, K, N) as GPU tensors."""
+    Wt = as_activation(W)
+    K, N = (Wt.shape[1], Wt.shape[0]) if from_out_in else Wt.shape
+    per = 32 // bits
+    if K % group_size or K % per or N % per:
+        raise AssertionError("dims must divide group/pack size")
+    qw = torch.empty((K // per, N), dtype=torch.int32, device=Wt.device)
+    qz = torch.empty((K // group_size, N // per), dtype=torch.int32, device=Wt.device)
+    sc = torch.empty((K // group_size, N), dtype=torch.float32, device=Wt.device)
+    _lib.call("miq_gptq_quantize", ptr(Wt), dtype_code(Wt), int(bool(from_out_in)), K, N, group_size,
+              bits, ptr(qw), ptr(qz), ptr(sc), stream_handle())
+    return qw, qz, sc, K, N
+
+
+def act_order_perm(g_idx, gs):
+    """Stable argsort of g_idx (host, load time): groups become consecutive runs of gs rows.
+    Raises if g_idx does not hold exactly gs rows per group."""
+    g = np.asarray(g_idx.cpu() if isinstance(g_idx, torch.Tensor) else g_idx).astype(np.int64)
+    perm = np.argsort(g, kind="stable")
+    if np.any(g[perm] != np.arange(g.size) // gs):
+        raise ValueError("g_idx must assign exactly group_size rows to every group")
+    return perm.astype(np.int32)
+
+
+class QuantizedLinear:
+    """Inference-only GPTQ-format weight-quantized Linear (group-wise int4/int8), same
+    constructor and attributes as the reference (`webtorch/_core.py:4409-4459`).
+
+    Differences, all invisible to results: scales stay in the dtype they are given (fp16
+    AutoGPTQ scales are not widened to fp32; both dequantize to identical values), the bias
+    is fused into the kernel, and an optional `g_idx` (act-order, which the reference ignores)
+    is honoured by a load-time row repack plus an activation gather."""
+
+    def __init__(self, qweight, qzeros, scales, bias, Kt, Nt, Kp, Np, gs, bits, zero_offset=0.0,
+                 g_idx=None):
+        self.Kt, self.Nt, self.Kp, self.Np = int(Kt), int(Nt), int(Kp), int(Np)
+        self.gs, self.bits = int(gs), int(bits)
+        self.zero_offset = float(zero_offset)
+        per = 32 // self.bits
+        if self.Kp % self.gs or self.Kp % per or self.Np % per:
+            raise AssertionError("dims must divide group/pack size")
+        self.qweight = to_device(qweight, torch.int32)
+        self.qzeros = to_device(qzeros, torch.int32)
+        self.scales = _scales(scales)
+        if tuple(self.qweight.shape) != (self.Kp // per, self.Np):
+            raise ValueError("qweight shape %s != (%d, %d)" % (tuple(self.qweight.shape), self.Kp // per, self.Np))
+        b = torch.zeros(self.Np, dtype=torch.float32)
+        if bias is not None:
+            bb = torch.as_tensor(np.asarray(bias.cpu() if isinstance(bias, torch.Tensor) else bias, np.float32))
+            b[:bb.numel()] = bb.reshape(-1)
+        self.bias = b.to(device())
+        self.perm = None
+        self.g_idx = None
+        if g_idx is not None:
+            gi = np.asarray(g_idx.cpu() if isinstance(g_idx, torch.Tensor) else g_idx).astype(np.int64)
+            if np.any(gi != np.arange(gi.size) // self.gs):
+                perm = act_order_perm(gi, self.gs)
+                self.g_idx = to_device(gi.astype(np.int32))
+                self.perm = to_device(perm)
+                rep = torch.empty_like(self.qweight)
+                _lib.call("miq_gptq_repack_rows", ptr(self.qweight), ptr(self.perm), ptr(rep),
+                          self.Kp, self.Np, self.bits, stream_handle())
+                self.qweight = rep
+
+    @staticmethod
+    def from_autogptq(qweight, qzeros, scales, bias, gs, bits, g_idx=None):
+        """AutoGPTQ tensors (`webtorch/_core.py:4420-4430`): zero points use the +1
+        convention (zero_offset 1.0). `g_idx` (desc_act=True) is an extension."""
+        per = 32 // bits
+        K = int(np.shape(qweight)[0]) * per
+        N = int(np.shape(qweight)[1])
+        return QuantizedLinear(qweight, qzeros, scales, bias, K, N, K, N, gs, bits, zero_offset=1.0,
+                               g_idx=g_idx)
+
+    @staticmethod
+    def from_linear(lin, group_size=32, bits=4):
+        """Quantize a float Linear whose weight is (in, out) = (K, N), as the reference's
+        `Linear` stores it (`webtorch/_core.py:4433-4444`), on the device."""
+        W = to_device(getattr(lin.weight, "data", lin.weight)).float()
+        bsrc = getattr(lin, "bias", None)
+        b = None if bsrc is None else to_device(getattr(bsrc, "data", bsrc)).float()
+        K, N = W.shape
+        per = 32 // bits
+        kmul = group_size if group_size % per == 0 else group_size * per
+        Kp, Np = K + (-K) % kmul, N + (-N) % per
+        if Kp != K or Np != N:
+            W = torch.nn.functional.pad(W, (0, Np - N, 0, Kp - K))
+        qw, qz, sc, _, _ = gptq_quantize(W, group_size, bits)
+        return QuantizedLinear(qw, qz, sc, b, K, N, Kp, Np, group_size, bits)
+
+    def forward(self, x, out_dtype=None):
+        xt = as_activation(x)
+        lead = xt.shape[:-1]
+        xf = xt.reshape(-1, self.Kt)
+        if self.Kp != self.Kt:
+            xf = torch.nn.functional.pad(xf, (0, self.Kp - self.Kt))
+        xf = xf.contiguous()
+        of = _gptq_matmul(xf, self.qweight, self.qzeros, self.scales, self.Kp, self.Np, self.gs,
+                          self.bits, self.zero_offset, bias=self.bias, perm=self.perm,
+                          out_dtype=out_dtype)
+        if self.Np != self.Nt:
+            of = of[:, :self.Nt].contiguous()
+        return of.reshape(*lead, self.Nt)
+
+    __call__ = forward
+
+    def dequantize(self):
+        """fp32 (Kp, Np) weight in the original row order."""
+        if self.perm is None:
+            return gptq_dequant(self.qweight, self.qzeros, self.scales, self.Kp, self.Np, self.gs,
+                                self.bits, self.zero_offset)
+        W = gptq_dequant(self.qweight, self.qzeros, self.scales, self.Kp, self.Np, self.gs, self.bits,
+                         self.zero_offset)
+        out = torch.empty_like(W)
+        out[self.perm.long()] = W
+        return out
+
+    def nbytes(self):
+        return int(self.qweight.numel() * 4 + self.qzeros.numel() * 4 +
+                   self.scales.numel() * self.scales.element_size() + self.bias.numel() * 4)
+
+
+# ---- GGUF native ---------------------------------------------------------------------
+_NATIVE_TYPES = {"Q4_K": (256, 144)}
+
+
+def ggml_native_supported(type_name):
+    """Can this ggml type be multiplied straight from the file's bytes
+    (`webtorch/_core.py:3644-3646`)? Q4_K is; the other ggml types are not built yet."""
+    return type_name in _NATIVE_TYPES
+
+
+def q4k_dequant(blocks, n_blocks):
+    out = torch.empty(int(n_blocks) * 256, dtype=torch.float32, device=blocks.device)
+    _lib.call("miq_q4k_dequant_f32", ptr(blocks), ptr(out), int(n_blocks), stream_handle())
+    return out
+
+
+def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32, out=None):
+    """xf (M, K) @ W.T -> (M, N), decoding ggml blocks in the kernel
+    (`webtorch/_core.py:3720-3734`). `packed` is the file's row layout (N rows of K/256
+    super-blocks), uint8 on the GPU."""
+    if type_name != "Q4_K":
+        raise NotImplementedError("native ggml type %s" % type_name)
+    xf = as_activation(xf).contiguous()
+    M = int(xf.shape[0])
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=xf.device)
+    _lib.call("miq_q4k_gemv", ptr(xf), dtype_code(xf), ptr(packed), ptr(bias), ptr(out), dtype_code(out),
+              M, int(K), int(N), stream_handle())
+    return out
+
+
+class GGMLLinear:
+    """Inference-only Linear whose weight stays in the GGUF encoding
+    (`webtorch/_core.py:4377-4406`). The reference transposes the bytes to a (word, row)
+    layout at upload for WebGPU coalescing; on MI355X the kernel reads the native row layout
+    with 16-byte loads, so the bytes are uploaded unchanged."""
+
+    def __init__(self, raw, type_name, K, N, bias=None):
+        if type_name not in _NATIVE_TYPES:
+            raise NotImplementedError("native ggml type %s" % type_name)
+        vals, blk = _NATIVE_TYPES[type_name]
+        self.type_name = type_name
+        self.Kt, self.Nt = int(K), int(N)
+        nbytes = self.Nt * (self.Kt // vals) * blk
+        if isinstance(raw, torch.Tensor):
+            b = raw.reshape(-1).view(torch.uint8)
+        else:
+            b = torch.from_numpy(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray))
+                                 else np.ascontiguousarray(raw).reshape(-1).view(np.uint8))
+        if b.numel() < nbytes:
+            raise ValueError("raw holds %d bytes, %s (%d x %d) needs %d" % (b.numel(), type_name, N, K, nbytes))
+        self.packed = b[:nbytes].to(device()).contiguous().reshape(self.Nt, -1)
+        self.bias = None if bias is None else to_device(np.asarray(bias, np.float32))
+
+    def forward(self, x, out_dtype=torch.float32):
+        xt = as_activation(x)
+        lead = xt.shape[:-1]
+        of = ggml_matmul(xt.reshape(-1, self.Kt), self.packed, self.type_name, self.Kt, self.Nt,
+                         bias=self.bias, out_dtype=out_dtype)
+        return of.reshape(*lead, self.Nt)
+
+    __call__ = forward
+
+    def dequantize(self):
+        """fp32 (N, K) weight."""
+        nb = self.Nt * (self.Kt // 256)
+        return q4k_dequant(self.packed, nb).reshape(self.Nt, self.Kt)
+
+    def nbytes(self):
+        return int(self.packed.numel() + (0 if self.bias is None else self.bias.numel() * 4))

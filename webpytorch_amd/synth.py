@@ -1,0 +1,162 @@
+"""Seeded synthetic weights and activations for the quantized-linear workloads.
+
+Every tensor comes from its own `numpy.random.default_rng((seed, tag))` stream, so a given
+(seed, shape) always yields the same bytes on any host. Nothing here touches the GPU; the
+results are plain numpy arrays in the on-disk layouts the loaders accept:
+
+* GPTQ (AutoGPTQ) -- qweight int32 (K/per, N) holding `per = 32/bits` rows of a column per
+  word, row k at bit offset (k % per) * bits (`webtorch/quantize.py:96-106`); qzeros int32
+  (K/gs, N/per) packed along N; scales fp16 (K/gs, N); g_idx int32 (K,).
+* GGUF Q4_K -- 144-byte super-blocks of 256 weights: fp16 d, fp16 dmin, 12 bytes of packed
+  6-bit sub-block scales/mins (the layout `get_scale_min_k4` reads,
+  `webtorch/ggufload.py:120-130`), then 128 bytes of 4-bit quants.
+"""
+import zlib
+
+import numpy as np
+
+# Distinct stream tags so that two tensors of one workload never share random bits.
+_TAGS = {}
+
+
+def rng(seed, tag):
+    """Independent generator for tensor `tag` of workload `seed`."""
+    t = _TAGS.get(tag)
+    if t is None:
+        t = _TAGS[tag] = zlib.crc32(tag.encode()) & 0x7FFFFFFF
+    return np.random.default_rng((int(seed), t))
+
+
+def random_words(g, shape):
+    """int32 array of uniformly random bits (so every packed nibble/byte is uniform)."""
+    return g.integers(0, 1 << 32, size=shape, dtype=np.uint64).astype(np.uint32).view(np.int32)
+
+
+def gptq_scales(g, shape):
+    """fp16 scales = |N(0,1)| * 0.01 + 1e-3."""
+    return (np.abs(g.standard_normal(shape)) * 0.01 + 1e-3).astype(np.float16)
+
+
+def gptq_layer(seed, K, N, gs=128, bits=4, act_order=False, name="w"):
+    """Random AutoGPTQ layer: uniform packed codes, uniform stored zeros, |N|*0.01+1e-3 scales.
+
+    With `act_order`, g_idx is a seeded permutation of arange(K)//gs (desc_act=True)."""
+    per = 32 // bits
+    if K % per or N % per or K % gs:
+        raise ValueError("K must divide by group size and pack factor, N by pack factor")
+    qweight = random_words(rng(seed, name + ".qweight"), (K // per, N))
+    qzeros = random_words(rng(seed, name + ".qzeros"), (K // gs, N // per))
+    scales = gptq_scales(rng(seed, name + ".scales"), (K // gs, N))
+    g_idx = (np.arange(K, dtype=np.int32) // gs).astype(np.int32)
+    if act_order:
+        g_idx = rng(seed, name + ".g_idx").permutation(g_idx).astype(np.int32)
+    return {"qweight": qweight, "qzeros": qzeros, "scales": scales, "g_idx": g_idx,
+            "K": K, "N": N, "gs": gs, "bits": bits}
+
+
+def int8_per_channel_layer(seed, K, N, name="w8"):
+    """Per-output-channel symmetric int8 (q ~ U[-127,127], fp16 scales |N|*0.01), written in
+    the GPTQ int8 layout with one group spanning all of K: stored code u = q + 128, stored
+    zero 127 (zero_offset 1 makes the effective zero 128), so s * (u - 128) = s * q."""
+    g = rng(seed, name + ".q")
+    q = g.integers(-127, 128, size=(K, N), dtype=np.int32)
+    u = (q + 128).astype(np.uint32)
+    qweight = np.zeros((K // 4, N), np.uint32)
+    for r in range(4):
+        qweight |= u[r::4] << np.uint32(8 * r)
+    qzeros = np.full((1, N // 4), 0x7F7F7F7F, np.uint32)
+    scales = (np.abs(rng(seed, name + ".scales").standard_normal((1, N))) * 0.01).astype(np.float16)
+    return {"qweight": qweight.view(np.int32), "qzeros": qzeros.view(np.int32), "scales": scales,
+            "g_idx": np.zeros(K, np.int32), "K": K, "N": N, "gs": K, "bits": 8, "q": q}
+
+
+def pack_q4k_scales(sc, m):
+    """Inverse of `get_scale_min_k4`: 8 six-bit scales and 8 six-bit mins -> 12 bytes/block.
+
+    sc, m: (blocks, 8) integer arrays in 0..63. Bytes 0-3 hold sc[0..3] plus the top two bits
+    of sc[4..7]; bytes 4-7 hold m[0..3] plus the top two bits of m[4..7]; bytes 8-11 hold the
+    low nibbles of sc[4..7] (low half) and m[4..7] (high half)."""
+    sc = np.asarray(sc, np.uint8); m = np.asarray(m, np.uint8)
+    out = np.empty((sc.shape[0], 12), np.uint8)
+    out[:, 0:4] = (sc[:, 0:4] & 63) | ((sc[:, 4:8] >> 4) << 6)
+    out[:, 4:8] = (m[:, 0:4] & 63) | ((m[:, 4:8] >> 4) << 6)
+    out[:, 8:12] = (sc[:, 4:8] & 15) | ((m[:, 4:8] & 15) << 4)
+    return out
+
+
+def q4k_blocks(seed, n_blocks, name="q4k"):
+    """Random Q4_K super-blocks as a (n_blocks, 144) uint8 array.
+
+    d, dmin = fp16 |N(0,1)|*0.01; sub-block scales and mins uniform over 0..63; quants
+    uniform random bytes."""
+    d = (np.abs(rng(seed, name + ".d").standard_normal(n_blocks)) * 0.01).astype(np.float16)
+    dmin = (np.abs(rng(seed, name + ".dmin").standard_normal(n_blocks)) * 0.01).astype(np.float16)
+    g = rng(seed, name + ".sm")
+    sc = g.integers(0, 64, size=(n_blocks, 8), dtype=np.uint8)
+    m = g.integers(0, 64, size=(n_blocks, 8), dtype=np.uint8)
+    qs = rng(seed, name + ".qs").integers(0, 256, size=(n_blocks, 128), dtype=np.uint8)
+    blk = np.empty((n_blocks, 144), np.uint8)
+    blk[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 2:4] = dmin.view(np.uint8).reshape(n_blocks, 2)
+    blk[:, 4:16] = pack_q4k_scales(sc, m)
+    blk[:, 16:144] = qs
+    return blk
+
+
+def q4k_layer(seed, K, N, name="q4k"):
+    """Q4_K weight of N rows by K columns: row n is K/256 consecutive super-blocks."""
+    if K % 256:
+        raise ValueError("Q4_K needs K % 256 == 0")
+    return q4k_blocks(seed, N * (K // 256), name).reshape(N, (K // 256) * 144)
+
+
+def activations(seed, M, K, dtype=np.float16, name="x"):
+    return rng(seed, name).standard_normal((M, K)).astype(dtype)
+
+
+# ---- workload shapes ------------------------------------------------------------------
+QWEN2_05B = dict(L=24, H=896, NH=14, NKV=2, HD=64, I=4864, V=151936, eps=1e-6,
+                 theta=1e6, gs=128, bits=4)
+
+
+def moe_workload(seed, T=256, H=2048, E=128, I=768, top_k=8, gs=128, experts=True):
+    """Qwen3-MoE-shaped expert block: tokens, router logits and E int4 experts."""
+    x = activations(seed, T, H, np.float16, "moe.x")
+    logits = rng(seed, "moe.logits").standard_normal((T, E)).astype(np.float32)
+    ex = None
+    if experts:
+        ex = [{"gate": gptq_layer(seed, H, I, gs, 4, name="moe.%d.gate" % e),
+               "up": gptq_layer(seed, H, I, gs, 4, name="moe.%d.up" % e),
+               "down": gptq_layer(seed, I, H, gs, 4, name="moe.%d.down" % e)}
+              for e in range(E)]
+    return {"x": x, "logits": logits, "experts": ex, "top_k": top_k, "T": T, "H": H,
+            "E": E, "I": I, "gs": gs}
+
+
+def decoder_weights(seed, L=24, H=896, NH=14, NKV=2, HD=64, I=4864, V=151936, gs=128,
+                    bits=4, **_):
+    """Random-init Qwen2-shaped int4 decoder: AutoGPTQ int4 linears (q/k/v with fp16 bias),
+    RMSNorm weights near 1, fp16 embeddings ~N(0, 0.02) (the head is tied to them)."""
+    layers = []
+    for i in range(L):
+        p = "l%d." % i
+        lay = {"q": gptq_layer(seed, H, NH * HD, gs, bits, name=p + "q"),
+               "k": gptq_layer(seed, H, NKV * HD, gs, bits, name=p + "k"),
+               "v": gptq_layer(seed, H, NKV * HD, gs, bits, name=p + "v"),
+               "o": gptq_layer(seed, NH * HD, H, gs, bits, name=p + "o"),
+               "gate": gptq_layer(seed, H, I, gs, bits, name=p + "gate"),
+               "up": gptq_layer(seed, H, I, gs, bits, name=p + "up"),
+               "down": gptq_layer(seed, I, H, gs, bits, name=p + "down")}
+        for nm, n in (("q", NH * HD), ("k", NKV * HD), ("v", NKV * HD)):
+            lay[nm]["bias"] = (rng(seed, p + nm + ".bias").standard_normal(n) * 0.02).astype(np.float16)
+        lay["in_ln"] = (1.0 + 0.02 * rng(seed, p + "in_ln").standard_normal(H)).astype(np.float16)
+        lay["post_ln"] = (1.0 + 0.02 * rng(seed, p + "post_ln").standard_normal(H)).astype(np.float16)
+        layers.append(lay)
+    embed = (rng(seed, "embed").standard_normal((V, H)) * 0.02).astype(np.float16)
+    final_norm = (1.0 + 0.02 * rng(seed, "final_norm").standard_normal(H)).astype(np.float16)
+    return {"layers": layers, "embed": embed, "final_norm": final_norm,
+            "cfg": dict(L=L, H=H, NH=NH, NKV=NKV, HD=HD, I=I, V=V, gs=gs, bits=bits)}
+
+
+def prompt_ids(seed, T=64, V=151936):
+    return rng(seed, "prompt").integers(0, V, size=T).astype(np.int64)
