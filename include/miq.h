@@ -62,16 +62,25 @@ int miq_gptq_dequant_f32(const int32_t* qweight, const int32_t* qzeros, const vo
 int miq_gptq_repack_rows(const int32_t* qweight, const int32_t* perm, int32_t* out, int K, int N,
                          int bits, void* stream);
 
+/* Bytes of workspace miq_gptq_gemv needs for this problem (0 if none). The first bytes hold
+ * per-tile arrival counters that must be zero before the first call on a workspace; every
+ * call leaves them zero again. One workspace must not serve two calls that run concurrently. */
+int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, int x_dtype, size_t* bytes);
+
 /* Decode GEMV / skinny GEMM: out[M][N] = x[M][K] (gathered through perm if non-NULL)
- * @ W + bias (nullable, fp32). x fp16|fp32, out fp16|fp32, fp32 accumulation. Requires
- * qweight 16-byte aligned; any M (efficient for M <= 8).
+ * @ W + bias (nullable, fp32). x fp16|fp32, scales fp16|fp32, out fp16|fp32, fp32
+ * accumulation; fp16 x uses fp16 products (exact) with fp32 sums. Requires qweight 16-byte
+ * aligned, N % 4 == 0 and gs a multiple of 32 (int4) or 16 (int8); efficient for M <= 8.
+ * workspace (256-byte aligned, workspace_bytes >= miq_gptq_gemv_workspace) lets the K
+ * dimension be split across workgroups; with NULL the call uses one workgroup per column
+ * tile (slower) and fails for K too large to stage.
  * Replaces: `_gptq_matmul` M == 1 dispatch to `_GPTQ_GEMV_WGSL`
  * (webtorch/_core.py:3926-3978, 4008-4027) and the bias add of `QuantizedLinear.forward`
  * (webtorch/_core.py:4446-4456). */
 int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, const int32_t* qweight,
                   const int32_t* qzeros, const void* scales, int scales_dtype, const float* bias,
                   void* out, int out_dtype, int M, int K, int N, int gs, int bits,
-                  float zero_offset, void* stream);
+                  float zero_offset, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Asymmetric min-max quantizer to the GPTQ layout (zero_offset 0, fp32 scales), bit-exact
  * with the reference's float32 numpy arithmetic (IEEE division, round-half-even). W is

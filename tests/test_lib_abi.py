@@ -37,9 +37,11 @@ def test_binding_covers_every_compute_entry_point():
 def test_validation_errors_raise_without_gpu():
     # rejected before any HIP call: unsupported bit width, bad divisibility, bad Q4_K K
     with pytest.raises(NotImplementedError, match="bits=3"):
-        _lib.call("miq_gptq_gemv", None, 1, None, None, None, None, 1, None, None, 1, 1, 64, 64, 32, 3, 0.0, None)
+        _lib.call("miq_gptq_gemv", None, 1, None, None, None, None, 1, None, None, 1, 1, 64, 64, 32, 3, 0.0,
+                  None, 0, None)
     with pytest.raises(ValueError, match="divide"):
-        _lib.call("miq_gptq_gemv", None, 1, None, None, None, None, 1, None, None, 1, 1, 100, 64, 32, 4, 0.0, None)
+        _lib.call("miq_gptq_gemv", None, 1, None, None, None, None, 1, None, None, 1, 1, 100, 64, 32, 4, 0.0,
+                  None, 0, None)
     with pytest.raises(ValueError, match="multiple of 256"):
         _lib.call("miq_q4k_gemv", None, 1, None, None, None, 0, 1, 300, 8, None)
     with pytest.raises(ValueError, match="divide"):
@@ -53,3 +55,16 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(_lib.MiqError, match="not built"):
         _lib.lib()
+
+
+def test_gemv_workspace_query_is_host_only():
+    """The split-K plan is computed on the host: a K range longer than one workgroup's batches
+    gets a workspace (counters + partials), a short one none."""
+    from webpytorch_amd import core
+    small = core.gemv_workspace_bytes(1, 896, 4864, 128, 4, _lib.MIQ_F16)
+    assert small > 0 and small % 4 == 0
+    assert small >= 4864 * 4 * 2  # at least two K slices of fp32 partials
+    assert core.gemv_workspace_bytes(1, 128, 151936, 128, 4, _lib.MIQ_F16) == 0
+    assert core.gemv_workspace_bytes(0, 896, 4864, 128, 4, _lib.MIQ_F16) == 0
+    with pytest.raises(NotImplementedError, match="group size"):
+        core.gemv_workspace_bytes(1, 896, 4864, 16, 4, _lib.MIQ_F16)

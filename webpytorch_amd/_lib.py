@@ -19,7 +19,8 @@ _p, _i, _f, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_
 SIGNATURES = {
     "miq_gptq_dequant_f32": [_p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _f, _p],
     "miq_gptq_repack_rows": [_p, _p, _p, _i, _i, _i, _p],
-    "miq_gptq_gemv": [_p, _i, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p],
+    "miq_gptq_gemv_workspace": [_i, _i, _i, _i, _i, _i, _p],
+    "miq_gptq_gemv": [_p, _i, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
     "miq_gptq_quantize": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p],
     "miq_q4k_dequant_f32": [_p, _p, _i64, _p],
     "miq_q4k_gemv": [_p, _i, _p, _p, _p, _i, _i, _i, _i, _p],

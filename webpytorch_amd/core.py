@@ -68,6 +68,42 @@ def as_activation(x):
     return t
 
 
+_WORKSPACE = {}
+_WS_BYTES = {}
+
+
+def gemv_workspace_bytes(M, K, N, gs, bits, x_dtype):
+    """Bytes of split-K workspace the GEMV needs for this problem (cached per shape)."""
+    key = (M, K, N, gs, bits, x_dtype)
+    b = _WS_BYTES.get(key)
+    if b is None:
+        n = ctypes.c_size_t(0)
+        _lib.call("miq_gptq_gemv_workspace", M, K, N, gs, bits, x_dtype, ctypes.byref(n))
+        b = _WS_BYTES[key] = int(n.value)
+    return b
+
+
+def workspace(nbytes):
+    """The current device's GEMV workspace, grown on demand and zeroed when allocated (the
+    kernels leave its arrival counters zero). Calls that share it must not run concurrently:
+    calls issued on one stream are ordered, which is how every operator here uses it."""
+    if nbytes == 0:
+        return None
+    dev = torch.cuda.current_device()
+    t = _WORKSPACE.get(dev)
+    if t is None or t.numel() < nbytes:
+        if t is not None:
+            torch.cuda.current_stream().synchronize()
+        t = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device())
+        _WORKSPACE[dev] = t
+    return t
+
+
+def aligned16(t):
+    """The kernels read activations with 16-byte loads: copy a misaligned view."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _scales(s):
     t = to_device(s)
     return t if t.dtype in (torch.float16, torch.float32) else t.float()
@@ -83,7 +119,7 @@ def gptq_dequant(qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, g_idx=None):
 
 
 def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=None, perm=None,
-                 out_dtype=None, out=None):
+                 out_dtype=None, out=None, ws=None):
     """xf (M, K) @ dequant(W) (+ bias) -> (M, N) on the current stream
     (`webtorch/_core.py:4008-4043`). M <= GEMV_MAX_M runs the split-K GEMV; larger M the
     MFMA GEMM."""
@@ -95,9 +131,13 @@ def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=
         return out
     if M > GEMV_MAX_M and hasattr(_lib.lib(), "miq_gptq_gemm"):
         return _gptq_gemm(xf, qweight, qzeros, scales, K, N, gs, bits, zoff, bias, perm, out)
-    _lib.call("miq_gptq_gemv", ptr(xf), dtype_code(xf), ptr(perm), ptr(qweight), ptr(qzeros),
+    xf = aligned16(xf)
+    xd = dtype_code(xf)
+    if ws is None:
+        ws = workspace(gemv_workspace_bytes(M, K, N, gs, bits, xd))
+    _lib.call("miq_gptq_gemv", ptr(xf), xd, ptr(perm), ptr(qweight), ptr(qzeros),
               ptr(scales), dtype_code(scales), ptr(bias), ptr(out), dtype_code(out), M, K, N, gs,
-              bits, float(zoff), stream_handle())
+              bits, float(zoff), ptr(ws), 0 if ws is None else ws.numel(), stream_handle())
     return out
 
 
@@ -252,7 +292,7 @@ def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32,
     super-blocks), uint8 on the GPU."""
     if type_name != "Q4_K":
         raise NotImplementedError("native ggml type %s" % type_name)
-    xf = as_activation(xf).contiguous()
+    xf = aligned16(as_activation(xf).contiguous())
     M = int(xf.shape[0])
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=xf.device)

@@ -11,6 +11,8 @@
 // through an act-order permutation) are staged once per workgroup in LDS as fp32, with
 // per-chunk sums so the zero point is applied once per chunk: sum x*(q - z) is computed as
 // sum x*q - z * sum x.
+#include <type_traits>
+
 #include "miq_common.h"
 
 namespace miq {
@@ -63,16 +65,46 @@ __global__ __launch_bounds__(256) void gptq_repack_kernel(const uint32_t* __rest
 }
 
 // ------------------------------------------------------------------------------------
-// GEMV / skinny GEMM (M <= 8).
-template <int BITS> struct Unpack;
+// Decode GEMV / skinny GEMM: out[M][N] = x[M][K] @ W + bias, MR rows of x per workgroup.
+//
+// Grid (tiles, ksplit, ceil(M / MR)), W waves per workgroup. A wave covers 256 columns: a lane
+// owns 4 adjacent columns and reads them with one 16-byte load per packed row, so a wave reads
+// 1 KB contiguous per row. The K dimension is cut into batches of RPW packed rows (BK = RPW *
+// per activations; BK divides gs, so a batch lies in one group). A workgroup takes W
+// consecutive batches of its column tile, one per wave (with no workspace, a wave loops over
+// every W-th batch of the whole K range). Latency is hidden by occupancy: every wave issues
+// its whole batch (RPW 16-byte loads per lane) at once, before the workgroup stages x.
+// Per batch and column: part = sum_k x_k q_k, acc += s * (part - (z + zoff) * sum_k x_k).
+// fp16 activations take the v_dot2 path (codes converted to exact fp16 pairs); fp32
+// activations take an fp32 FMA path. The waves are summed in a fixed order through LDS.
+// With ksplit > 1 the workgroups of one column tile store fp32 partials in the workspace;
+// the last to arrive (device-scope atomic counter) sums them in ksplit order, adds the bias,
+// writes the output and re-arms the counter to zero, so results are deterministic.
 
-// int4: one word = 8 consecutive rows of one column.
-template <> struct Unpack<4> {
-  static constexpr int PER = 8;
-  // part += sum_j x[j] * code_j  for the 8 rows held in w
-  __device__ __forceinline__ static float dot(uint32_t w, const float* x, float part) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;         // codes of rows 0,2,4,6
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // codes of rows 1,3,5,7
+#ifndef MIQ_GEMV_MIN_WGS
+#define MIQ_GEMV_MIN_WGS 128  // split K further while fewer workgroups than this would run
+#endif
+#ifndef MIQ_GEMV_MAX_WAVES
+#define MIQ_GEMV_MAX_WAVES 4  // waves per workgroup (256 threads)
+#endif
+constexpr int kGemvStageBytes = 64 * 1024;  // LDS for the staged activations (no workspace)
+
+template <int BITS> struct Codes;
+
+// int4: one word = 8 consecutive rows of one column, row j in bits 4j..4j+3.
+template <> struct Codes<4> {
+  static constexpr int PER = 8, PAIRS = 4;
+  // the codes as fp16 pairs (c0,c4) (c1,c5) (c2,c6) (c3,c7)
+  __device__ __forceinline__ static void pairs(uint32_t w, half2v* p) {
+    const uint32_t w8 = w >> 8;
+    p[0] = nib_lo(w);
+    p[1] = nib_hi(w);
+    p[2] = nib_lo(w8);
+    p[3] = nib_hi(w8);
+  }
+  __device__ __forceinline__ static float dotf(uint32_t w, const float* x, float part) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;         // rows 0,2,4,6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // rows 1,3,5,7
     part = fmaf(x[0], (float)(lo & 0xFFu), part);
     part = fmaf(x[1], (float)(hi & 0xFFu), part);
     part = fmaf(x[2], (float)((lo >> 8) & 0xFFu), part);
@@ -85,10 +117,15 @@ template <> struct Unpack<4> {
   }
 };
 
-// int8: one word = 4 consecutive rows of one column.
-template <> struct Unpack<8> {
-  static constexpr int PER = 4;
-  __device__ __forceinline__ static float dot(uint32_t w, const float* x, float part) {
+// int8: one word = 4 consecutive rows of one column, row j in bits 8j..8j+7.
+template <> struct Codes<8> {
+  static constexpr int PER = 4, PAIRS = 2;
+  // the codes as fp16 pairs (c0,c2) (c1,c3)
+  __device__ __forceinline__ static void pairs(uint32_t w, half2v* p) {
+    p[0] = byte02(w);
+    p[1] = byte02(w >> 8);
+  }
+  __device__ __forceinline__ static float dotf(uint32_t w, const float* x, float part) {
     part = fmaf(x[0], (float)(w & 0xFFu), part);
     part = fmaf(x[1], (float)((w >> 8) & 0xFFu), part);
     part = fmaf(x[2], (float)((w >> 16) & 0xFFu), part);
@@ -97,163 +134,310 @@ template <> struct Unpack<8> {
   }
 };
 
-template <typename ST> __device__ __forceinline__ void load4(const ST* p, float* v);
-template <> __device__ __forceinline__ void load4<float>(const float* p, float* v) {
-  const float4 t = *reinterpret_cast<const float4*>(p);
-  v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+// Raw scale words of 4 adjacent columns (fp16: 8 bytes, fp32: 16 bytes); converted only when
+// used, so that issuing a batch's loads never waits for them.
+template <typename ST> __device__ __forceinline__ uint4 load_scales4(const ST* p);
+template <> __device__ __forceinline__ uint4 load_scales4<float>(const float* p) {
+  return *reinterpret_cast<const uint4*>(p);
 }
-template <> __device__ __forceinline__ void load4<__half>(const __half* p, float* v) {
+template <> __device__ __forceinline__ uint4 load_scales4<__half>(const __half* p) {
   const uint2 t = *reinterpret_cast<const uint2*>(p);
-  v[0] = __half2float(__ushort_as_half((unsigned short)(t.x & 0xFFFF)));
-  v[1] = __half2float(__ushort_as_half((unsigned short)(t.x >> 16)));
-  v[2] = __half2float(__ushort_as_half((unsigned short)(t.y & 0xFFFF)));
-  v[3] = __half2float(__ushort_as_half((unsigned short)(t.y >> 16)));
+  return make_uint4(t.x, t.y, 0u, 0u);
+}
+template <typename ST> __device__ __forceinline__ void scales4(uint4 r, float* v);
+template <> __device__ __forceinline__ void scales4<float>(uint4 r, float* v) {
+  v[0] = __uint_as_float(r.x); v[1] = __uint_as_float(r.y); v[2] = __uint_as_float(r.z); v[3] = __uint_as_float(r.w);
+}
+template <> __device__ __forceinline__ void scales4<__half>(uint4 r, float* v) {
+  v[0] = __half2float(__ushort_as_half((unsigned short)(r.x & 0xFFFF)));
+  v[1] = __half2float(__ushort_as_half((unsigned short)(r.x >> 16)));
+  v[2] = __half2float(__ushort_as_half((unsigned short)(r.y & 0xFFFF)));
+  v[3] = __half2float(__ushort_as_half((unsigned short)(r.y >> 16)));
 }
 
-// LDS: xs[MR][K] fp32 activations, then xsum[MR][K/CK] chunk sums. Re-used for the
-// cross-wave reduction, red[S][MR][256].
-// At most 32 / MR waves per workgroup (the reduction buffer is S * MR KB), which bounds the
-// workgroup size and so the register budget per lane.
-template <int MR> constexpr int gemv_threads() { return MR >= 8 ? 256 : (MR >= 4 ? 512 : 1024); }
+template <int RPW> struct GemvBatch {
+  uint4 w[RPW];
+  uint4 s;     // raw scale words
+  uint32_t z;  // raw packed zero word (shifted to this lane's columns when used)
+};
 
-template <int BITS, int MR, int CK, typename XT, typename ST, typename OT>
-__global__ __launch_bounds__(gemv_threads<MR>()) void gptq_gemv_kernel(
+template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT>
+__global__ __launch_bounds__(256) void gptq_gemv_kernel(
     const XT* __restrict__ x, const int32_t* __restrict__ perm, const uint32_t* __restrict__ qw,
     const uint32_t* __restrict__ qz, const ST* __restrict__ sc, const float* __restrict__ bias,
-    OT* __restrict__ out, int M, int K, int N, int gs, float zoff) {
-  constexpr int PER = Unpack<BITS>::PER;
-  constexpr int RPC = CK / PER;  // packed rows per chunk
+    OT* __restrict__ out, float* __restrict__ ws, int* __restrict__ counters, int M, int K, int N,
+    int gs, float zoff, int rows_per_wg, int ksplit) {
+  using C = Codes<BITS>;
+  constexpr int PER = C::PER, PAIRS = C::PAIRS;
+  constexpr int BK = RPW * PER;
+  constexpr bool kHalf = std::is_same<XT, __half>::value;
+  constexpr int XB = kHalf ? 2 : 4;
   constexpr uint32_t MASK = (1u << BITS) - 1u;
-  extern __shared__ float lds[];
-  float* xs = lds;
-  const int NC = K / CK;
-  float* xsum = lds + MR * K;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  __shared__ int is_last;
 
-  const int S = blockDim.x >> 6;
-  const int wave = uniform(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int m0 = blockIdx.y * MR;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int tile = blockIdx.x, ks = blockIdx.y, m0 = blockIdx.z * MR;
+  const int r0 = ks * rows_per_wg;
+  const int r1 = min(K / PER, r0 + rows_per_wg);
+  const int L = (r1 - r0) * PER;   // staged activations per row of x (a multiple of BK)
+  const int nb = (r1 - r0) / RPW;  // batches in this workgroup
+  const int n0 = tile * 256 + lane * 4;
+  const bool colok = n0 < N;
+  const int NZ = N / PER;
+  const int zshift = (n0 % PER) * BITS;
 
-  // ---- stage activations (gathered through perm for act-order) ----
-  for (int i = threadIdx.x; i < MR * K; i += blockDim.x) {
-    const int m = i / K, k = i - m * K;
-    const int src = perm ? perm[k] : k;
-    xs[i] = (m0 + m < M) ? to_f32(x[(size_t)(m0 + m) * K + src]) : 0.f;
+  auto load_batch = [&](int b, GemvBatch<RPW>& B) {
+    const int rb = r0 + b * RPW;
+    const uint32_t* base = qw + (size_t)rb * N + n0;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) B.w[r] = *reinterpret_cast<const uint4*>(base + (size_t)r * N);
+    const int g = rb * PER / gs;
+    B.s = load_scales4<ST>(sc + (size_t)g * N + n0);
+    B.z = qz[(size_t)g * NZ + n0 / PER];
+  };
+
+  // ---- first batch of weights, issued before the activations are staged ----
+  GemvBatch<RPW> B;
+  int b = wave;
+  if (colok && b < nb) load_batch(b, B);
+
+  // ---- stage x (through perm) in LDS and the per-batch sums of x ----
+  _Float16* xs_h = reinterpret_cast<_Float16*>(lds_raw);
+  float* xs_f = reinterpret_cast<float*>(lds_raw);
+  const size_t xs_bytes = ((size_t)MR * L * XB + 15) & ~(size_t)15;
+  float* xsum = reinterpret_cast<float*>(lds_raw + xs_bytes);
+  // 8 consecutive activations per thread and step (one int4 packed row, two int8 rows)
+  constexpr int SEG = BK / 8;  // threads per batch
+  const int cpr = L / 8;       // chunks per row of x
+  for (int ci = threadIdx.x; ci < MR * cpr; ci += blockDim.x) {
+    const int m = ci / cpr, kk = (ci - m * cpr) * 8;
+    const int k = r0 * PER + kk;
+    float v[8];
+    if (m0 + m < M) {
+      const XT* xr = x + (size_t)(m0 + m) * K;
+      if (perm) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = to_f32(xr[perm[k + j]]);
+      } else {
+        load8(xr + k, v);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.f;
+    }
+    // every aligned run of SEG threads is one batch of one row of x, all of them present
+    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+#pragma unroll
+    for (int o = 1; o < SEG; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    if ((lane & (SEG - 1)) == 0) xsum[m * nb + kk / BK] = sum;
+    if constexpr (kHalf) {
+      uint4 t;
+      if constexpr (BITS == 4) {  // pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+        t = make_uint4(pack_h2(v[0], v[4]), pack_h2(v[1], v[5]), pack_h2(v[2], v[6]), pack_h2(v[3], v[7]));
+      } else {                    // per 4-row word: (x0,x2) (x1,x3)
+        t = make_uint4(pack_h2(v[0], v[2]), pack_h2(v[1], v[3]), pack_h2(v[4], v[6]), pack_h2(v[5], v[7]));
+      }
+      *reinterpret_cast<uint4*>(xs_h + (size_t)m * L + kk) = t;
+    } else {
+      float4* d = reinterpret_cast<float4*>(xs_f + (size_t)m * L + kk);
+      d[0] = make_float4(v[0], v[1], v[2], v[3]);
+      d[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
   }
   __syncthreads();
-  for (int it = wave; it < MR * NC; it += S) {
-    const float* p = xs + (it / NC) * K + (it % NC) * CK;
-    float s = 0.f;
-    for (int j = lane; j < CK; j += 64) s += p[j];
-    s = wave_sum(s);
-    if (lane == 0) xsum[it] = s;
-  }
-  __syncthreads();
 
-  const int n0 = (blockIdx.x * 64 + lane) * 4;
-  const int c0 = wave * NC / S, c1 = (wave + 1) * NC / S;
   float acc[MR][4];
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.f;
 
-  if (n0 < N && c0 < c1) {
-    const int NZ = N / PER;
-    int g = -1;
-    float s4[4], z4[4], part[MR][4], xg[MR];
-    for (int ch = c0; ch < c1; ++ch) {
-      const int k0 = ch * CK;
-      const int gc = k0 / gs;
-      if (gc != g) {
-        if (g >= 0) {
-#pragma unroll
-          for (int m = 0; m < MR; ++m)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(s4[c], part[m][c] - z4[c] * xg[m], acc[m][c]);
-        }
-        g = gc;
-        load4<ST>(sc + (size_t)g * N + n0, s4);
-        const uint32_t zw = qz[(size_t)g * NZ + n0 / PER] >> ((n0 % PER) * BITS);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) z4[c] = (float)((zw >> (c * BITS)) & MASK) + zoff;
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-          xg[m] = 0.f;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) part[m][c] = 0.f;
-        }
-      }
-      // all loads of the chunk first, then the math
-      uint4 w[RPC];
-      const uint32_t* base = qw + (size_t)(k0 / PER) * N + n0;
-#pragma unroll
-      for (int r = 0; r < RPC; ++r) w[r] = *reinterpret_cast<const uint4*>(base + (size_t)r * N);
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        xg[m] += xsum[m * NC + ch];
-        const float* xr = xs + m * K + k0;
-#pragma unroll
-        for (int r = 0; r < RPC; ++r) {
-          float xv[PER];
-#pragma unroll
-          for (int j = 0; j < PER; j += 4) {
-            const float4 t = *reinterpret_cast<const float4*>(xr + r * PER + j);
-            xv[j] = t.x; xv[j + 1] = t.y; xv[j + 2] = t.z; xv[j + 3] = t.w;
-          }
-          part[m][0] = Unpack<BITS>::dot(w[r].x, xv, part[m][0]);
-          part[m][1] = Unpack<BITS>::dot(w[r].y, xv, part[m][1]);
-          part[m][2] = Unpack<BITS>::dot(w[r].z, xv, part[m][2]);
-          part[m][3] = Unpack<BITS>::dot(w[r].w, xv, part[m][3]);
-        }
-      }
-    }
+  auto compute = [&](int bb) {
+    float part[MR][4];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(s4[c], part[m][c] - z4[c] * xg[m], acc[m][c]);
+      for (int c = 0; c < 4; ++c) part[m][c] = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      uint32_t wv[4] = {B.w[r].x, B.w[r].y, B.w[r].z, B.w[r].w};
+      // An empty asm that takes this row's words and the running sums keeps the rows in order:
+      // the compiler would otherwise unpack every row of the batch at once (4x the registers)
+      // and spill.
+      asm volatile("" : "+v"(wv[0]), "+v"(wv[1]), "+v"(wv[2]), "+v"(wv[3]), "+v"(part[0][0]), "+v"(part[0][1]),
+                   "+v"(part[0][2]), "+v"(part[0][3]));
+      const int row = bb * RPW + r;  // local packed row
+      if constexpr (kHalf) {
+        half2v p[4][PAIRS];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) C::pairs(wv[c], p[c]);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const half2v* xp = reinterpret_cast<const half2v*>(xs_h + (size_t)m * L + row * PER);
+          half2v xv[PAIRS];
+#pragma unroll
+          for (int i = 0; i < PAIRS; ++i) xv[i] = xp[i];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int i = 0; i < PAIRS; ++i) part[m][c] = dot2(xv[i], p[c][i], part[m][c]);
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const float* xp = xs_f + (size_t)m * L + row * PER;
+          float xv[PER];
+#pragma unroll
+          for (int j = 0; j < PER; j += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(xp + j);
+            xv[j] = t.x; xv[j + 1] = t.y; xv[j + 2] = t.z; xv[j + 3] = t.w;
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) part[m][c] = C::dotf(wv[c], xv, part[m][c]);
+        }
+      }
+    }
+    float zf[4], sf[4];
+    scales4<ST>(B.s, sf);
+    const uint32_t zw = B.z >> zshift;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) zf[c] = (float)((zw >> (c * BITS)) & MASK) + zoff;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float xb = xsum[m * nb + bb];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(sf[c], fmaf(-zf[c], xb, part[m][c]), acc[m][c]);
+    }
+  };
+
+  if (colok) {
+    while (b < nb) {
+      compute(b);
+      b += W;
+      if (b < nb) load_batch(b, B);
+    }
   }
 
-  // ---- deterministic cross-wave reduction ----
-  __syncthreads();
-  float* red = lds;  // [S][MR][256]
+  // ---- fixed-order reduction of the W waves ----
+  const size_t stage = xs_bytes + (((size_t)MR * nb * 4 + 15) & ~(size_t)15);
+  float* red = reinterpret_cast<float*>(lds_raw + stage);  // [W][MR][256]
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
     for (int c = 0; c < 4; ++c) red[(wave * MR + m) * 256 + lane * 4 + c] = acc[m][c];
   __syncthreads();
+
+  if (ksplit == 1) {
+    for (int i = threadIdx.x; i < MR * 256; i += blockDim.x) {
+      const int m = i >> 8, q = i & 255, n = tile * 256 + q;
+      if (m0 + m >= M || n >= N) continue;
+      float s = 0.f;
+      for (int w = 0; w < W; ++w) s += red[(w * MR + m) * 256 + q];
+      if (bias) s += bias[n];
+      out[(size_t)(m0 + m) * N + n] = from_f32<OT>(s);
+    }
+    return;
+  }
+
+  // Partials are exchanged with device-scope (agent) atomic stores and loads, which bypass
+  // the per-XCD L2, so no cache-wide writeback or invalidate is needed: each thread waits for
+  // its stores to complete before the workgroup counts itself in, and the last workgroup reads
+  // the partials with device-scope loads after it has seen the final count.
   for (int i = threadIdx.x; i < MR * 256; i += blockDim.x) {
-    const int m = i >> 8, q = i & 255;
-    const int n = blockIdx.x * 256 + q;
+    const int m = i >> 8, q = i & 255, n = tile * 256 + q;
     if (m0 + m >= M || n >= N) continue;
     float s = 0.f;
-    for (int w = 0; w < S; ++w) s += red[(w * MR + m) * 256 + q];
+    for (int w = 0; w < W; ++w) s += red[(w * MR + m) * 256 + q];
+    __hip_atomic_store(ws + ((size_t)ks * M + m0 + m) * N + n, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int* ctr = counters + (size_t)blockIdx.z * gridDim.x + tile;
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ksplit - 1;
+  __syncthreads();
+  if (!is_last) return;
+  for (int i = threadIdx.x; i < MR * 256; i += blockDim.x) {
+    const int m = i >> 8, q = i & 255, n = tile * 256 + q;
+    if (m0 + m >= M || n >= N) continue;
+    // issue the partial loads four at a time; the sum stays in ksplit order
+    const float* pp = ws + (size_t)(m0 + m) * N + n;
+    const size_t stride = (size_t)M * N;
+    float s = 0.f;
+    int k2 = 0;
+    for (; k2 + 4 <= ksplit; k2 += 4) {
+      const float a0 = __hip_atomic_load(pp + (k2 + 0) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float a1 = __hip_atomic_load(pp + (k2 + 1) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float a2 = __hip_atomic_load(pp + (k2 + 2) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float a3 = __hip_atomic_load(pp + (k2 + 3) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s = (((s + a0) + a1) + a2) + a3;
+    }
+    for (; k2 < ksplit; ++k2) s += __hip_atomic_load(pp + k2 * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (bias) s += bias[n];
     out[(size_t)(m0 + m) * N + n] = from_f32<OT>(s);
   }
+  if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed
 }
 
-// ------------------------------------------------------------------------------------
-template <int BITS, int MR, int CK, typename XT, typename ST, typename OT>
-static int launch_gemv(const void* x, const int32_t* perm, const int32_t* qw, const int32_t* qz,
-                       const void* sc, const float* bias, void* out, int M, int K, int N, int gs,
-                       float zoff, hipStream_t st) {
-  const int tiles = (N + 255) / 256;
-  const int NC = K / CK;
-  // Waves per workgroup: enough workgroups x waves to fill 256 CUs several times, no more
-  // waves than chunks, and a reduction buffer that fits beside the staged activations.
-  int S = (8 * kCUs + tiles - 1) / tiles;
-  S = S < 1 ? 1 : S;
-  S = S > 16 ? 16 : S;
-  S = S > NC ? NC : S;
-  while (S > 1 && 64 * S > gemv_threads<MR>()) --S;
-  size_t stage = (size_t)MR * K * 4 + (size_t)MR * NC * 4;
-  size_t redb = (size_t)S * MR * 256 * 4;
-  size_t lds = stage > redb ? stage : redb;
-  MIQ_REQUIRE(lds <= 160 * 1024, MIQ_ERR_UNSUPPORTED, "gptq_gemv: K=%d too large for one LDS stage", K);
-  auto kern = gptq_gemv_kernel<BITS, MR, CK, XT, ST, OT>;
-  if (lds > 64 * 1024) {
-    static bool raised = false;  // once per instantiation: allow up to the 160 KB of gfx950 LDS
+// Launch geometry shared by the workspace query and the launch.
+struct GemvPlan {
+  int mr, rpw, waves, tiles, mblocks, ksplit, rows_per_wg;
+  size_t lds, counter_bytes, ws_bytes;
+};
+
+static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool have_ws, GemvPlan* p) {
+  const int per = 32 / bits;
+  int rpw = 0;
+  for (int r = 8; r >= 4; r >>= 1)
+    if (gs % (r * per) == 0) { rpw = r; break; }
+  MIQ_REQUIRE(rpw, MIQ_ERR_UNSUPPORTED, "gptq_gemv: group size %d (needs a multiple of %d)", gs, 4 * per);
+  p->rpw = rpw;
+  p->mr = M >= 8 ? 8 : (M >= 4 ? 4 : 1);
+  p->tiles = (N + 255) / 256;
+  p->mblocks = (M + p->mr - 1) / p->mr;
+  const int xb = x_dtype == MIQ_F16 ? 2 : 4;
+  const int nbt = K / per / rpw;  // batches per column tile
+  const int wmax = MIQ_GEMV_MAX_WAVES;
+  const int base = p->tiles * p->mblocks;
+  int waves, ksplit;
+  if (have_ws) {
+    // one batch per wave; fewer waves per workgroup while too few workgroups would run
+    waves = nbt < wmax ? nbt : wmax;
+    ksplit = (nbt + waves - 1) / waves;
+    while (waves > 1 && base * ksplit < MIQ_GEMV_MIN_WGS) {
+      waves = (waves + 1) / 2;
+      ksplit = (nbt + waves - 1) / waves;
+    }
+  } else {
+    waves = nbt < wmax ? nbt : wmax;
+    ksplit = 1;
+    MIQ_REQUIRE((size_t)p->mr * K * xb <= (size_t)kGemvStageBytes, MIQ_ERR_INVALID,
+                "gptq_gemv: K=%d needs a workspace (see miq_gptq_gemv_workspace)", K);
+  }
+  const int rows_per_wg = ksplit == 1 ? K / per : waves * rpw;
+  p->waves = waves;
+  p->ksplit = ksplit;
+  p->rows_per_wg = rows_per_wg;
+  const int L = rows_per_wg * per, nb = rows_per_wg / rpw;
+  p->lds = (((size_t)p->mr * L * xb + 15) & ~(size_t)15) + (((size_t)p->mr * nb * 4 + 15) & ~(size_t)15) +
+           (size_t)waves * p->mr * 256 * 4;
+  p->counter_bytes = ksplit > 1 ? (((size_t)p->tiles * p->mblocks * 4 + 255) & ~(size_t)255) : 0;
+  p->ws_bytes = ksplit > 1 ? p->counter_bytes + (size_t)ksplit * M * N * 4 : 0;
+  return MIQ_OK;
+}
+
+template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT>
+static int launch_gemv(const GemvPlan& p, const void* x, const int32_t* perm, const int32_t* qw,
+                       const int32_t* qz, const void* sc, const float* bias, void* out, void* ws,
+                       int M, int K, int N, int gs, float zoff, hipStream_t st) {
+  auto kern = gptq_gemv_kernel<BITS, MR, RPW, XT, ST, OT>;
+  int* counters = p.ksplit > 1 ? static_cast<int*>(ws) : nullptr;
+  float* partials = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes) : nullptr;
+  if (p.lds > 64 * 1024) {
+    static bool raised = false;  // once per instantiation
     if (!raised) {
       hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -261,20 +445,20 @@ static int launch_gemv(const void* x, const int32_t* perm, const int32_t* qw, co
       raised = true;
     }
   }
-  dim3 grid(tiles, (M + MR - 1) / MR);
-  hipLaunchKernelGGL(kern, grid, dim3(64 * S), lds, st,
-                     static_cast<const XT*>(x), perm, reinterpret_cast<const uint32_t*>(qw),
-                     reinterpret_cast<const uint32_t*>(qz), static_cast<const ST*>(sc), bias,
-                     static_cast<OT*>(out), M, K, N, gs, zoff);
+  dim3 grid(p.tiles, p.ksplit, p.mblocks);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * p.waves), p.lds, st, static_cast<const XT*>(x), perm,
+                     reinterpret_cast<const uint32_t*>(qw), reinterpret_cast<const uint32_t*>(qz),
+                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, M, K, N,
+                     gs, zoff, p.rows_per_wg, p.ksplit);
   return check_launch("gptq_gemv");
 }
 
-template <int BITS, int MR, int CK>
-static int gemv_types(const void* x, int xd, const int32_t* perm, const int32_t* qw, const int32_t* qz,
-                      const void* sc, int sd, const float* bias, void* out, int od, int M, int K, int N,
-                      int gs, float zoff, hipStream_t st) {
-#define MIQ_GEMV_CASE(XT, ST, OT)                                                                   \
-  return launch_gemv<BITS, MR, CK, XT, ST, OT>(x, perm, qw, qz, sc, bias, out, M, K, N, gs, zoff, st)
+template <int BITS, int MR, int RPW>
+static int gemv_types(const GemvPlan& p, const void* x, int xd, const int32_t* perm, const int32_t* qw,
+                      const int32_t* qz, const void* sc, int sd, const float* bias, void* out, int od,
+                      void* ws, int M, int K, int N, int gs, float zoff, hipStream_t st) {
+#define MIQ_GEMV_CASE(XT, ST, OT) \
+  return launch_gemv<BITS, MR, RPW, XT, ST, OT>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st)
   if (xd == MIQ_F16) {
     if (sd == MIQ_F16) { if (od == MIQ_F16) MIQ_GEMV_CASE(__half, __half, __half); MIQ_GEMV_CASE(__half, __half, float); }
     if (od == MIQ_F16) MIQ_GEMV_CASE(__half, float, __half);
@@ -286,18 +470,17 @@ static int gemv_types(const void* x, int xd, const int32_t* perm, const int32_t*
 #undef MIQ_GEMV_CASE
 }
 
-template <int BITS, int CK>
-static int gemv_mr(const void* x, int xd, const int32_t* perm, const int32_t* qw, const int32_t* qz,
-                   const void* sc, int sd, const float* bias, void* out, int od, int M, int K, int N,
-                   int gs, float zoff, hipStream_t st) {
-  // rows of x per workgroup; the activation stage must fit LDS
-  if (M >= 8 && (size_t)8 * K * 4 <= 64 * 1024)
-    return gemv_types<BITS, 8, CK>(x, xd, perm, qw, qz, sc, sd, bias, out, od, M, K, N, gs, zoff, st);
-  if (M >= 4 && (size_t)4 * K * 4 <= 96 * 1024)
-    return gemv_types<BITS, 4, CK>(x, xd, perm, qw, qz, sc, sd, bias, out, od, M, K, N, gs, zoff, st);
-  if (M >= 2 && (size_t)2 * K * 4 <= 128 * 1024)
-    return gemv_types<BITS, 2, CK>(x, xd, perm, qw, qz, sc, sd, bias, out, od, M, K, N, gs, zoff, st);
-  return gemv_types<BITS, 1, CK>(x, xd, perm, qw, qz, sc, sd, bias, out, od, M, K, N, gs, zoff, st);
+template <int BITS>
+static int gemv_dispatch(const GemvPlan& p, const void* x, int xd, const int32_t* perm, const int32_t* qw,
+                         const int32_t* qz, const void* sc, int sd, const float* bias, void* out, int od,
+                         void* ws, int M, int K, int N, int gs, float zoff, hipStream_t st) {
+#define MIQ_GEMV_MR(MR, RPW) \
+  if (p.mr == MR && p.rpw == RPW) \
+    return gemv_types<BITS, MR, RPW>(p, x, xd, perm, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st)
+  MIQ_GEMV_MR(1, 8); MIQ_GEMV_MR(4, 8); MIQ_GEMV_MR(8, 8);
+  MIQ_GEMV_MR(1, 4); MIQ_GEMV_MR(4, 4); MIQ_GEMV_MR(8, 4);
+#undef MIQ_GEMV_MR
+  return fail(MIQ_ERR_UNSUPPORTED, "gptq_gemv: no kernel for mr=%d rpw=%d", p.mr, p.rpw);
 }
 
 int check_gptq_dims(const char* who, int K, int N, int gs, int bits) {
@@ -358,28 +541,56 @@ extern "C" int miq_gptq_repack_rows(const int32_t* qweight, const int32_t* perm,
   return check_launch("gptq_repack_rows");
 }
 
+static int gemv_check(const char* who, const void* x, int x_dtype, const int32_t* qweight, const int32_t* qzeros,
+                      const void* scales, int scales_dtype, void* out, int out_dtype, int M, int K, int N,
+                      int gs, int bits) {
+  int rc = check_gptq_dims(who, K, N, gs, bits);
+  if (rc) return rc;
+  MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "%s: M=%d", who, M);
+  if (M == 0) return MIQ_OK;
+  MIQ_REQUIRE(x && qweight && qzeros && scales && out, MIQ_ERR_INVALID, "%s: null pointer", who);
+  MIQ_REQUIRE(N % 4 == 0 && aligned(qweight, 16) && aligned(scales, scales_dtype == MIQ_F16 ? 8 : 16) &&
+                  aligned(x, 16) && K % 8 == 0,
+              MIQ_ERR_ALIGN, "%s: x and qweight must be 16-byte aligned, N %% 4 == 0 and K %% 8 == 0", who);
+  MIQ_REQUIRE(x_dtype == MIQ_F16 || x_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "%s: x dtype", who);
+  MIQ_REQUIRE(scales_dtype == MIQ_F16 || scales_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "%s: scales dtype", who);
+  MIQ_REQUIRE(out_dtype == MIQ_F16 || out_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "%s: out dtype", who);
+  return MIQ_OK;
+}
+
+extern "C" int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, int x_dtype, size_t* bytes) {
+  MIQ_REQUIRE(bytes, MIQ_ERR_INVALID, "gptq_gemv_workspace: null output");
+  *bytes = 0;
+  int rc = check_gptq_dims("gptq_gemv_workspace", K, N, gs, bits);
+  if (rc) return rc;
+  MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "gptq_gemv_workspace: M=%d", M);
+  if (M == 0) return MIQ_OK;
+  GemvPlan p;
+  rc = gemv_plan(M, K, N, gs, bits, x_dtype, true, &p);
+  if (rc) return rc;
+  *bytes = p.ws_bytes;
+  return MIQ_OK;
+}
+
 extern "C" int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, const int32_t* qweight,
                              const int32_t* qzeros, const void* scales, int scales_dtype, const float* bias,
                              void* out, int out_dtype, int M, int K, int N, int gs, int bits,
-                             float zero_offset, void* stream) {
-  int rc = check_gptq_dims("gptq_gemv", K, N, gs, bits);
+                             float zero_offset, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = gemv_check("gptq_gemv", x, x_dtype, qweight, qzeros, scales, scales_dtype, out, out_dtype, M, K, N,
+                      gs, bits);
+  if (rc || M == 0) return rc;
+  GemvPlan p;
+  rc = gemv_plan(M, K, N, gs, bits, x_dtype, workspace != nullptr, &p);
   if (rc) return rc;
-  MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "gptq_gemv: M=%d", M);
-  if (M == 0) return MIQ_OK;
-  MIQ_REQUIRE(x && qweight && qzeros && scales && out, MIQ_ERR_INVALID, "gptq_gemv: null pointer");
-  MIQ_REQUIRE(N % 4 == 0 && aligned(qweight, 16) && aligned(scales, scales_dtype == MIQ_F16 ? 8 : 16),
-              MIQ_ERR_ALIGN, "gptq_gemv: qweight must be 16-byte aligned and N %% 4 == 0");
-  MIQ_REQUIRE(x_dtype == MIQ_F16 || x_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "gptq_gemv: x dtype");
-  MIQ_REQUIRE(out_dtype == MIQ_F16 || out_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "gptq_gemv: out dtype");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int per = 32 / bits;
-  // chunk of 64 activations (or 32 when the group is smaller)
-  if (gs % 64 == 0 && K % 64 == 0) {
-    if (bits == 4) return gemv_mr<4, 64>(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs, zero_offset, st);
-    return gemv_mr<8, 64>(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs, zero_offset, st);
+  if (p.ksplit > 1) {
+    MIQ_REQUIRE(workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
+                "gptq_gemv: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes,
+                workspace_bytes);
   }
-  MIQ_REQUIRE(gs % 32 == 0, MIQ_ERR_UNSUPPORTED, "gptq_gemv: group size %d (needs a multiple of 32)", gs);
-  (void)per;
-  if (bits == 4) return gemv_mr<4, 32>(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs, zero_offset, st);
-  return gemv_mr<8, 32>(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs, zero_offset, st);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (bits == 4)
+    return gemv_dispatch<4>(p, x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype,
+                            workspace, M, K, N, gs, zero_offset, st);
+  return gemv_dispatch<8>(p, x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype,
+                          workspace, M, K, N, gs, zero_offset, st);
 }

@@ -29,6 +29,26 @@ template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ __half from_f32<__half>(float v) { return __float2half_rn(v); }
 
+// ---- 8 consecutive activations as fp32 (one 16-byte load for fp16, two for fp32) --------
+__device__ __forceinline__ void load8(const __half* p, float* v) {
+  const uint4 t = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __half2float(__ushort_as_half((unsigned short)(w[i] & 0xFFFF)));
+    v[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w[i] >> 16)));
+  }
+}
+__device__ __forceinline__ void load8(const float* p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+// two fp32 values (exact fp16 inputs) packed as an fp16 pair
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
+}
+
 // ---- wavefront (64 lanes) reductions --------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -40,6 +60,36 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+
+// ---- fp16 pairs: 4-bit codes to exact fp16 without a conversion per value ---------------
+// OR-ing a code c into the low mantissa bits of 1024.0 (0x6400) gives 1024 + c (or 1024 + 16c
+// for a code in bits 4..7) exactly; one packed subtract / fma recovers c. v_dot2 then takes
+// two products per instruction with fp32 accumulation.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+// (a & m) | o in one VALU instruction (the compiler otherwise splits it in two, each with a
+// literal); m and o stay in registers across the loop.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(m), "v"(o));
+  return d;
+}
+// codes in bits 0-3 and 16-19 of w
+__device__ __forceinline__ half2v nib_lo(uint32_t w) {
+  return as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) - (half2v){(_Float16)1024, (_Float16)1024};
+}
+// codes in bits 4-7 and 20-23 of w
+__device__ __forceinline__ half2v nib_hi(uint32_t w) {
+  return __builtin_elementwise_fma(as_h2(and_or(w, 0x00F000F0u, 0x64006400u)),
+                                   (half2v){(_Float16)0.0625f, (_Float16)0.0625f},
+                                   (half2v){(_Float16)-64, (_Float16)-64});
+}
+// bytes 0 and 2 of w (8-bit codes, 1024 + c is exact for c < 1024)
+__device__ __forceinline__ half2v byte02(uint32_t w) {
+  return as_h2(and_or(w, 0x00FF00FFu, 0x64006400u)) - (half2v){(_Float16)1024, (_Float16)1024};
+}
+__device__ __forceinline__ float dot2(half2v a, half2v b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 
 // Uniform (scalar) copy of a value that is the same in every lane.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }

@@ -8,7 +8,9 @@
 //
 // GEMV mapping: four lanes share a super-block, lane (b, q) owning its 32-byte code group
 // (64 weights, two sub-blocks), so a wave covers 16 super-blocks (4096 activations) of a row
-// with 16-byte loads; the lane keeps its 64 activations in registers and walks R rows.
+// with 16-byte loads; the lane reads its 64 activations from LDS once and walks R rows.
+#include <type_traits>
+
 #include "miq_common.h"
 
 namespace miq {
@@ -66,105 +68,214 @@ __global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restr
   }
 }
 
-// y[m][n] = sum_k x[m][k] * W[n][k]  (+ bias[n])
+// fp16 pair layout of a 64-wide code group in LDS: for code word wq (bytes 4wq..4wq+3) the
+// 8 halves at 8wq are the pairs (4wq, 4wq+2), (4wq+1, 4wq+3) of the low sub-block and the same
+// 32 further on for the high sub-block, matching nib_lo/nib_hi of the word and of the word
+// shifted by 8.
+
+// y[m][n] = sum_k x[m][k] * W[n][k] (+ bias[n]).
+// A wave owns R consecutive rows per step (steps strided over the grid). Lane (slot, q) =
+// (lane / 4, lane % 4) takes super-block p * 16 + slot of each row in pass p, and its 32-byte
+// code group q: 64 weights of sub-blocks 2q (low nibbles) and 2q + 1 (high nibbles), at
+// activations b * 256 + 64 q .. + 63. The workgroup stages x once in LDS (fp16 in the pair
+// order of the nibble unpack, or fp32) with sums over each 32 activations; a lane reads its 64
+// activations once per pass and reuses them for the R rows. The weight loads of the first step
+// are issued before x is staged.
 template <int R, int MR, typename XT, typename OT>
 __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x, const uint8_t* __restrict__ w,
                                                        const float* __restrict__ bias, OT* __restrict__ out,
                                                        int M, int K, int N) {
-  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  constexpr bool kHalf = std::is_same<XT, __half>::value;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  _Float16* xs_h = reinterpret_cast<_Float16*>(lds_raw);
+  float* xs_f = reinterpret_cast<float*>(lds_raw);
+  float* xsum = reinterpret_cast<float*>(lds_raw + (size_t)MR * K * (kHalf ? 2 : 4));
+
   const int lane = threadIdx.x & 63;
-  const int row0 = wave * R;
-  if (row0 >= N) return;  // uniform per wave
+  const int wave = uniform(threadIdx.x >> 6);
   const int m0 = blockIdx.y * MR;
   const int nb = K / 256;
   const size_t row_bytes = (size_t)nb * 144;
-  const int bl = lane >> 2, q = lane & 3;
+  const int slot = lane >> 2, q = lane & 3;
+  const int groups = (N + R - 1) / R;
+  const int wstride = gridDim.x * 4;
+  int grp = blockIdx.x * 4 + wave;
 
-  float acc[MR][R];
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
-
-  for (int pass = 0; pass < nb; pass += 16) {
-    const int b = pass + bl;
-    if (b >= nb) continue;  // lane idles for the tail of a row
-    // activations of this lane's 64 weights, and the two sub-block sums
-    float xv[MR][64], xs1[MR], xs2[MR];
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const bool ok = m0 + m < M;
-      const XT* xp = x + (size_t)(ok ? m0 + m : 0) * K + b * 256 + 64 * q;
-      float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-      for (int i = 0; i < 64; ++i) {
-        xv[m][i] = ok ? to_f32(xp[i]) : 0.f;
-        if (i < 32) s1 += xv[m][i]; else s2 += xv[m][i];
-      }
-      xs1[m] = s1;
-      xs2[m] = s2;
-    }
+  uint4 hd[R], c0[R], c1[R];
+  auto load_rows = [&](int g, int pass) {
+    const int b = pass * 16 + slot;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int n = row0 + r;
-      if (n >= N) break;
-      const uint8_t* blk = w + (size_t)n * row_bytes + (size_t)b * 144;
-      const uint4 h = *reinterpret_cast<const uint4*>(blk);
-      const uint4 c0 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * q);
-      const uint4 c1 = *reinterpret_cast<const uint4*>(blk + 32 + 32 * q);
-      const Q4kScales s = q4k_scales(h, q);
-      const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        float lo = 0.f, hi = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t l4 = cw[i] & 0x0F0F0F0Fu, h4 = (cw[i] >> 4) & 0x0F0F0F0Fu;
-          lo = fmaf(xv[m][4 * i + 0], (float)(l4 & 0xFF), lo);
-          lo = fmaf(xv[m][4 * i + 1], (float)((l4 >> 8) & 0xFF), lo);
-          lo = fmaf(xv[m][4 * i + 2], (float)((l4 >> 16) & 0xFF), lo);
-          lo = fmaf(xv[m][4 * i + 3], (float)(l4 >> 24), lo);
-          hi = fmaf(xv[m][32 + 4 * i + 0], (float)(h4 & 0xFF), hi);
-          hi = fmaf(xv[m][32 + 4 * i + 1], (float)((h4 >> 8) & 0xFF), hi);
-          hi = fmaf(xv[m][32 + 4 * i + 2], (float)((h4 >> 16) & 0xFF), hi);
-          hi = fmaf(xv[m][32 + 4 * i + 3], (float)(h4 >> 24), hi);
-        }
-        float t = s.d1 * lo - s.m1 * xs1[m];
-        t = fmaf(s.d2, hi, t);
-        t = fmaf(-s.m2, xs2[m], t);
-        acc[m][r] += t;
+      const int n = g * R + r;
+      if (n < N && b < nb) {
+        const uint8_t* blk = w + (size_t)n * row_bytes + (size_t)b * 144;
+        hd[r] = *reinterpret_cast<const uint4*>(blk);
+        c0[r] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * q);
+        c1[r] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * q);
       }
     }
+  };
+  if (grp < groups) load_rows(grp, 0);
+
+  // ---- stage x and its 32-wide sums ----
+  // 8 consecutive activations per thread and step; 4 threads make one 32-wide sum
+  for (int ci = threadIdx.x; ci < MR * K / 8; ci += 256) {
+    const int m = ci / (K / 8), k = (ci - m * (K / 8)) * 8;
+    float v[8];
+    if (m0 + m < M) {
+      load8(x + (size_t)(m0 + m) * K + k, v);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.f;
+    }
+    float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if ((lane & 3) == 0) xsum[m * (K / 32) + k / 32] = sum;
+    if constexpr (kHalf) {
+      // activations c0..c0+7 of a 64-wide group land in code words wq and wq+1 (wq = (c0 % 32) / 4)
+      // at slots 4h..4h+3 (h = c0 / 32), in the order (x0, x2, x1, x3)
+      const int c0 = k & 63, h = c0 >> 5, wq = (c0 & 31) >> 2;
+      _Float16* base = xs_h + (size_t)m * K + (k & ~63) + wq * 8 + h * 4;
+      *reinterpret_cast<uint2*>(base) = make_uint2(pack_h2(v[0], v[2]), pack_h2(v[1], v[3]));
+      *reinterpret_cast<uint2*>(base + 8) = make_uint2(pack_h2(v[4], v[6]), pack_h2(v[5], v[7]));
+    } else {
+      float4* d = reinterpret_cast<float4*>(xs_f + (size_t)m * K + k);
+      d[0] = make_float4(v[0], v[1], v[2], v[3]);
+      d[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
   }
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[m][r] = wave_sum(acc[m][r]);
-  if (lane < R * MR) {
-    // lane (m, r) writes row r of activation row m; select from registers without
-    // dynamic indexing
-    float v = 0.f;
-    int mm = 0, rr = 0;
+  __syncthreads();
+
+  const int passes = (nb + 15) / 16;
+  for (; grp < groups; grp += wstride) {
+    float acc[MR][R];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (lane == m * R + r) { v = acc[m][r]; mm = m; rr = r; }
-    const int n = row0 + rr;
-    if (n < N && m0 + mm < M) {
-      if (bias) v += bias[n];
-      out[(size_t)(m0 + mm) * N + n] = from_f32<OT>(v);
+      for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+    for (int pass = 0; pass < passes; ++pass) {
+      if (pass > 0) load_rows(grp, pass);
+      const int b = pass * 16 + slot;
+      if (b < nb) {
+        const int kb = b * 256 + 64 * q;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const float sA = xsum[m * (K / 32) + kb / 32], sB = xsum[m * (K / 32) + kb / 32 + 1];
+          if constexpr (kHalf) {
+            half2v xv[8][4];
+            const uint4* xp = reinterpret_cast<const uint4*>(xs_h + (size_t)m * K + kb);
+#pragma unroll
+            for (int wq = 0; wq < 8; ++wq) {
+              const uint4 t = xp[wq];
+              xv[wq][0] = as_h2(t.x); xv[wq][1] = as_h2(t.y); xv[wq][2] = as_h2(t.z); xv[wq][3] = as_h2(t.w);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              const int n = grp * R + r;
+              if (n >= N) break;
+              uint4 h4 = hd[r];
+              uint32_t cw[8] = {c0[r].x, c0[r].y, c0[r].z, c0[r].w, c1[r].x, c1[r].y, c1[r].z, c1[r].w};
+              // An empty asm that takes this row's words and the previous row's sum keeps the rows
+              // in order (otherwise every row is unpacked at once and the registers run out).
+              asm volatile("" : "+v"(cw[0]), "+v"(cw[1]), "+v"(cw[2]), "+v"(cw[3]), "+v"(cw[4]), "+v"(cw[5]),
+                           "+v"(cw[6]), "+v"(cw[7]), "+v"(h4.x), "+v"(h4.y), "+v"(h4.z), "+v"(h4.w),
+                           "+v"(acc[m][r > 0 ? r - 1 : 0]));
+              const Q4kScales s = q4k_scales(h4, q);
+              float pa = 0.f, pb = 0.f;
+#pragma unroll
+              for (int wq = 0; wq < 8; ++wq) {
+                const uint32_t v0 = cw[wq], v8 = cw[wq] >> 8;
+                pa = dot2(xv[wq][0], nib_lo(v0), pa);
+                pa = dot2(xv[wq][1], nib_lo(v8), pa);
+                pb = dot2(xv[wq][2], nib_hi(v0), pb);
+                pb = dot2(xv[wq][3], nib_hi(v8), pb);
+              }
+              float t = fmaf(s.d1, pa, -s.m1 * sA);
+              t = fmaf(s.d2, pb, t);
+              acc[m][r] += fmaf(-s.m2, sB, t);
+            }
+          } else {
+            const float* xf = xs_f + (size_t)m * K + kb;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              const int n = grp * R + r;
+              if (n >= N) break;
+              uint4 h4 = hd[r];
+              uint32_t cw[8] = {c0[r].x, c0[r].y, c0[r].z, c0[r].w, c1[r].x, c1[r].y, c1[r].z, c1[r].w};
+              // An empty asm that takes this row's words and the previous row's sum keeps the rows
+              // in order (otherwise every row is unpacked at once and the registers run out).
+              asm volatile("" : "+v"(cw[0]), "+v"(cw[1]), "+v"(cw[2]), "+v"(cw[3]), "+v"(cw[4]), "+v"(cw[5]),
+                           "+v"(cw[6]), "+v"(cw[7]), "+v"(h4.x), "+v"(h4.y), "+v"(h4.z), "+v"(h4.w),
+                           "+v"(acc[m][r > 0 ? r - 1 : 0]));
+              const Q4kScales s = q4k_scales(h4, q);
+              float pa = 0.f, pb = 0.f;
+#pragma unroll
+              for (int wq = 0; wq < 8; ++wq) {
+                const float4 xa = *reinterpret_cast<const float4*>(xf + 4 * wq);
+                const float4 xb = *reinterpret_cast<const float4*>(xf + 32 + 4 * wq);
+                const uint32_t l4 = cw[wq] & 0x0F0F0F0Fu, h4 = (cw[wq] >> 4) & 0x0F0F0F0Fu;
+                pa = fmaf(xa.x, (float)(l4 & 0xFF), pa);
+                pa = fmaf(xa.y, (float)((l4 >> 8) & 0xFF), pa);
+                pa = fmaf(xa.z, (float)((l4 >> 16) & 0xFF), pa);
+                pa = fmaf(xa.w, (float)(l4 >> 24), pa);
+                pb = fmaf(xb.x, (float)(h4 & 0xFF), pb);
+                pb = fmaf(xb.y, (float)((h4 >> 8) & 0xFF), pb);
+                pb = fmaf(xb.z, (float)((h4 >> 16) & 0xFF), pb);
+                pb = fmaf(xb.w, (float)(h4 >> 24), pb);
+              }
+              float t = fmaf(s.d1, pa, -s.m1 * sA);
+              t = fmaf(s.d2, pb, t);
+              acc[m][r] += fmaf(-s.m2, sB, t);
+            }
+          }
+        }
+      }
     }
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[m][r] = wave_sum(acc[m][r]);
+    if (lane < R * MR) {
+      // lane (m, r) writes row r of activation row m; registers selected without dynamic indexing
+      float v = 0.f;
+      int mm = 0, rr = 0;
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (lane == m * R + r) { v = acc[m][r]; mm = m; rr = r; }
+      const int n = grp * R + rr;
+      if (n < N && m0 + mm < M) {
+        if (bias) v += bias[n];
+        out[(size_t)(m0 + mm) * N + n] = from_f32<OT>(v);
+      }
+    }
+    if (grp + wstride < groups) load_rows(grp + wstride, 0);
   }
 }
 
 template <int R, int MR, typename XT, typename OT>
 static int launch_q4k(const void* x, const uint8_t* w, const float* bias, void* out, int M, int K, int N,
                       hipStream_t st) {
-  const int waves = (N + R - 1) / R;
-  dim3 grid((waves + 3) / 4, (M + MR - 1) / MR);
-  hipLaunchKernelGGL((q4k_gemv_kernel<R, MR, XT, OT>), grid, dim3(256), 0, st, static_cast<const XT*>(x), w,
-                     bias, static_cast<OT*>(out), M, K, N);
+  auto kern = q4k_gemv_kernel<R, MR, XT, OT>;
+  const size_t lds = (size_t)MR * K * sizeof(XT) + (size_t)MR * (K / 32) * 4;
+  MIQ_REQUIRE(lds <= 160 * 1024, MIQ_ERR_UNSUPPORTED, "q4k_gemv: K=%d too large to stage", K);
+  if (lds > 64 * 1024) {
+    static bool raised = false;  // once per instantiation
+    if (!raised) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      MIQ_REQUIRE(e == hipSuccess, MIQ_ERR_HIP, "q4k_gemv: LDS attribute: %s", hipGetErrorString(e));
+      raised = true;
+    }
+  }
+  const int groups = (N + R - 1) / R;
+  int wgs = (groups + 3) / 4;
+  if (wgs > 4 * kCUs) wgs = 4 * kCUs;
+  dim3 grid(wgs, (M + MR - 1) / MR);
+  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, static_cast<const XT*>(x), w, bias,
+                     static_cast<OT*>(out), M, K, N);
   return check_launch("q4k_gemv");
 }
 
@@ -201,7 +312,7 @@ extern "C" int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const 
   MIQ_REQUIRE(K % 256 == 0, MIQ_ERR_INVALID, "q4k_gemv: K=%d is not a multiple of 256", K);
   if (M == 0) return MIQ_OK;
   MIQ_REQUIRE(x && w && out, MIQ_ERR_INVALID, "q4k_gemv: null pointer");
-  MIQ_REQUIRE(aligned(w, 16), MIQ_ERR_ALIGN, "q4k_gemv: weight must be 16-byte aligned");
+  MIQ_REQUIRE(aligned(w, 16) && aligned(x, 16), MIQ_ERR_ALIGN, "q4k_gemv: x and weight must be 16-byte aligned");
   MIQ_REQUIRE(x_dtype == MIQ_F16 || x_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "q4k_gemv: x dtype");
   MIQ_REQUIRE(out_dtype == MIQ_F16 || out_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "q4k_gemv: out dtype");
   hipStream_t st = static_cast<hipStream_t>(stream);
