@@ -100,6 +100,37 @@ def q4k_bench(torch, core, copies=16, reps=32):
             "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
+
+
+def gemm_bench(torch, core, Ms=(16, 128, 512), copies=32, reps=32):
+    """GPTQ int4 prefill GEMM, act-order (rows repacked at load), K = N = 4096, gs = 128:
+    x fp16 (M, 4096) -> y fp16 (M, 4096), over `copies` distinct weight copies."""
+    K = N = 4096
+    perm = torch.randperm(K, device="cuda").int()
+    ws = [make_layer(torch, K, N, "f16", False) for _ in range(copies)]
+    res = {}
+    for M in Ms:
+        x = torch.randn((M, K), device="cuda").half()
+        y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+
+        def run(M=M, x=x, y=y):
+            for i in range(reps):
+                qw, qz, sc, _ = ws[i % copies]
+                core._gptq_matmul(x, qw, qz, sc, K, N, GS, 4, 1.0, perm=perm, out=y)
+        run()
+        torch.cuda.synchronize()
+        g = capture(torch, run)
+        t = timed(torch, g.replay, 5) / reps
+        flops = 2.0 * M * K * N
+        nbytes = gemv_bytes(K, N, "f16", False) - K * 2 - N * 2 + 2 * M * K * 2
+        res["M%d" % M] = {"us": round(t * 1e6, 3), "TFLOPs": round(flops / t / 1e12, 1),
+                          "mfma_frac": round(flops / t / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                          "GBs": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+        del g
+    return res
+
+
 def cpu_baseline(seconds=10.0):
     """The reference's numpy-fallback GEMV path (`_gptq_matmul_np`, restated in oracle/) on a
     bounded sample: one decoder layer's seven linears (q, k, v, o, gate, up, down as separate
@@ -221,6 +252,7 @@ def main():
         kernels[name] = {"K": K, "N": N, "bytes": nb, "us": round(t * 1e6, 3), "GBs": round(nb / t / 1e9, 1)}
         del g
     q4k = q4k_bench(torch, core)
+    gemm = gemm_bench(torch, core)
 
     res = {
         "metric": "int4 GEMV achieved HBM GB/s (% of peak) + decode tokens/s, Qwen2-0.5B shape",
@@ -237,6 +269,7 @@ def main():
                      "avg_bytes_per_launch": step_bytes // launches},
         "gemv_shapes": kernels,
         "q4k_gemv_llama3_8b_up": q4k,
+        "gptq_gemm_act_order_4096": gemm,
     }
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a.cpu_seconds)

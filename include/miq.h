@@ -62,9 +62,10 @@ int miq_gptq_dequant_f32(const int32_t* qweight, const int32_t* qzeros, const vo
 int miq_gptq_repack_rows(const int32_t* qweight, const int32_t* perm, int32_t* out, int K, int N,
                          int bits, void* stream);
 
-/* Bytes of workspace miq_gptq_gemv needs for this problem (0 if none). The first bytes hold
- * per-tile arrival counters that must be zero before the first call on a workspace; every
- * call leaves them zero again. One workspace must not serve two calls that run concurrently. */
+/* Bytes of workspace miq_gptq_gemv needs for this problem (0 if none). The first 256 KiB of a
+ * workspace hold arrival counters, shared by every split-K entry point, that must be zero
+ * before the first call on it; every call leaves them zero again. Partial sums follow them.
+ * One workspace must not serve two calls that run concurrently. */
 int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, int x_dtype, size_t* bytes);
 
 /* Decode GEMV / skinny GEMM: out[M][N] = x[M][K] (gathered through perm if non-NULL)
@@ -81,6 +82,24 @@ int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, const int32_t
                   const int32_t* qzeros, const void* scales, int scales_dtype, const float* bias,
                   void* out, int out_dtype, int M, int K, int N, int gs, int bits,
                   float zero_offset, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace miq_gptq_gemm needs (0 if none); same contract as
+ * miq_gptq_gemv_workspace (zeroed counters first, not shared by concurrent calls). */
+int miq_gptq_gemm_workspace(int M, int K, int N, int gs, int bits, size_t* bytes);
+
+/* Prefill / batched GEMM on the matrix cores: out[M][N] = x[M][K] (fp16, gathered through perm
+ * if non-NULL) @ W + bias (nullable, fp32). W is dequantized exactly to the small integers
+ * q - (z + zero_offset) in fp16 (zero_offset must be a small non-negative integer), fp16 x
+ * fp16 products accumulate in fp32 and the fp32 group scale multiplies each chunk's sums.
+ * scales fp16|fp32, out fp16|fp32. Requires x and qweight 16-byte aligned, N % 4 == 0 and
+ * gs in {32, 64} or a multiple of 128. workspace as for miq_gptq_gemv.
+ * Replaces: `_gptq_matmul` M > 1 dispatch to the tiled `_GPTQ_WGSL` kernel
+ * (webtorch/_core.py:3833-3888, 3995-4027) and the bias add of `QuantizedLinear.forward`
+ * (webtorch/_core.py:4446-4456). */
+int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* qweight, const int32_t* qzeros,
+                  const void* scales, int scales_dtype, const float* bias, void* out, int out_dtype,
+                  int M, int K, int N, int gs, int bits, float zero_offset, void* workspace,
+                  size_t workspace_bytes, void* stream);
 
 /* Asymmetric min-max quantizer to the GPTQ layout (zero_offset 0, fp32 scales), bit-exact
  * with the reference's float32 numpy arithmetic (IEEE division, round-half-even). W is

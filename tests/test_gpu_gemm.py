@@ -1,0 +1,80 @@
+"""GPU parity: the matrix-core GPTQ GEMM (M > 8 rows of fp16 activations) against the oracle,
+at the prefill shapes (K = N = 4096, act-order, int8 per-channel) and at ragged ones."""
+import numpy as np
+import pytest
+
+from oracle import gptq
+from webpytorch_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, ref, rel=1e-4):
+    """North-star bar elementwise (|d| <= 1e-3 + 1e-2 |ref|) and a tight max-relative bound."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    bad = np.abs(got - ref) > 1e-3 + 1e-2 * np.abs(ref)
+    assert not bad.any(), "max err %.3g at %s" % (np.abs(got - ref).max(), np.argwhere(bad)[:3])
+    r = np.abs(got - ref).max() / (np.abs(ref).max() + 1e-30)
+    assert r < rel, r
+
+
+@pytest.mark.parametrize("M", [9, 16, 128, 512])
+@pytest.mark.parametrize("act", [False, True])
+def test_prefill_gemm_config2(gpu, M, act):
+    """GPTQ int4 prefill GEMM, K = N = 4096, gs = 128, with and without act-order."""
+    import torch
+    from webpytorch_amd import core
+    L = synth.gptq_layer(30, 4096, 4096, 128, 4, act_order=act)
+    x = synth.activations(30 + M, M, 4096, np.float16)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 128, 4,
+                                            g_idx=L["g_idx"] if act else None)
+    got = ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy()
+    ref = gptq.linear_forward(x, L, zoff=1.0, g_idx=L["g_idx"] if act else None)
+    _check(got, ref)
+    # fp16 output rounds the same sums once
+    y16 = ql(torch.from_numpy(x))
+    assert y16.dtype == torch.float16
+    _check(y16.float().cpu().numpy(), ref, rel=2e-3)
+
+
+@pytest.mark.parametrize("M", [16, 128])
+def test_int8_per_channel_gemm(gpu, M):
+    import torch
+    from webpytorch_amd import core
+    L = synth.int8_per_channel_layer(31, 4096, 4096)
+    x = synth.activations(31 + M, M, 4096, np.float16)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 4096, 8)
+    got = ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy()
+    ref = gptq.gptq_matmul_np(x, L["qweight"], L["qzeros"], L["scales"], 4096, 4096, 4096, 8, 1.0)
+    _check(got, ref)
+
+
+@pytest.mark.parametrize("K,N,gs,bits,M", [(256, 264, 32, 4, 20), (384, 136, 64, 4, 33), (512, 520, 128, 8, 17),
+                                           (256, 64, 32, 8, 70)])
+def test_gemm_ragged_shapes_fp32_scales_bias(gpu, K, N, gs, bits, M):
+    """Self-quantized layers (fp32 scales, zero offset 0) with a bias, M not a multiple of 16,
+    N not a multiple of 256, small groups."""
+    import torch
+    from webpytorch_amd import core
+    rng = np.random.default_rng(K + N + M)
+    W = (rng.standard_normal((K, N)) * 0.1).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    qw, qz, sc, _, _ = gptq.gptq_quantize(W, gs, bits)
+    ql = core.QuantizedLinear(qw, qz, sc, b, K, N, K, N, gs, bits)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    got = ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy()
+    ref = gptq.gptq_matmul_np(x, qw, qz, sc, K, N, gs, bits, 0.0) + b
+    _check(got, ref)
+
+
+def test_gemm_repeated_calls_are_deterministic(gpu):
+    """Split-K slices are summed in a fixed order, and the counters re-arm between calls."""
+    import torch
+    from webpytorch_amd import core
+    L = synth.gptq_layer(32, 4096, 1024, 128, 4)
+    x = torch.from_numpy(synth.activations(32, 64, 4096, np.float16))
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 128, 4)
+    a = ql.forward(x, out_dtype=torch.float32).cpu().numpy()
+    for _ in range(3):
+        assert np.array_equal(a, ql.forward(x, out_dtype=torch.float32).cpu().numpy())

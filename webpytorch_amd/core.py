@@ -69,6 +69,7 @@ def as_activation(x):
 
 
 _WORKSPACE = {}
+_RETIRED = []
 _WS_BYTES = {}
 
 
@@ -83,6 +84,17 @@ def gemv_workspace_bytes(M, K, N, gs, bits, x_dtype):
     return b
 
 
+def gemm_workspace_bytes(M, K, N, gs, bits):
+    """Bytes of split-K workspace the MFMA GEMM needs for this problem (cached per shape)."""
+    key = ("gemm", M, K, N, gs, bits)
+    b = _WS_BYTES.get(key)
+    if b is None:
+        n = ctypes.c_size_t(0)
+        _lib.call("miq_gptq_gemm_workspace", M, K, N, gs, bits, ctypes.byref(n))
+        b = _WS_BYTES[key] = int(n.value)
+    return b
+
+
 def workspace(nbytes):
     """The current device's GEMV workspace, grown on demand and zeroed when allocated (the
     kernels leave its arrival counters zero). Calls that share it must not run concurrently:
@@ -93,8 +105,9 @@ def workspace(nbytes):
     t = _WORKSPACE.get(dev)
     if t is None or t.numel() < nbytes:
         if t is not None:
-            torch.cuda.current_stream().synchronize()
-        t = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device())
+            # a captured graph may still point at the old buffer: keep it alive
+            _RETIRED.append(t)
+        t = torch.zeros(max(nbytes, 4 << 20), dtype=torch.uint8, device=device())
         _WORKSPACE[dev] = t
     return t
 
@@ -121,28 +134,30 @@ def gptq_dequant(qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, g_idx=None):
 def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=None, perm=None,
                  out_dtype=None, out=None, ws=None):
     """xf (M, K) @ dequant(W) (+ bias) -> (M, N) on the current stream
-    (`webtorch/_core.py:4008-4043`). M <= GEMV_MAX_M runs the split-K GEMV; larger M the
-    MFMA GEMM."""
+    (`webtorch/_core.py:4008-4043`). Up to GEMV_MAX_M rows run the split-K GEMV; more rows
+    of fp16 activations run the matrix-core GEMM (fp32 activations stay on the GEMV, which
+    keeps them in fp32)."""
     M = int(xf.shape[0])
     od = out_dtype or xf.dtype
     if out is None:
         out = torch.empty((M, N), dtype=od, device=xf.device)
     if M == 0:
         return out
-    if M > GEMV_MAX_M and hasattr(_lib.lib(), "miq_gptq_gemm"):
-        return _gptq_gemm(xf, qweight, qzeros, scales, K, N, gs, bits, zoff, bias, perm, out)
     xf = aligned16(xf)
     xd = dtype_code(xf)
+    if M > GEMV_MAX_M and xd == MIQ_F16 and float(zoff).is_integer() and 0 <= zoff <= 8:
+        if ws is None:
+            ws = workspace(gemm_workspace_bytes(M, K, N, gs, bits))
+        _lib.call("miq_gptq_gemm", ptr(xf), ptr(perm), ptr(qweight), ptr(qzeros), ptr(scales),
+                  dtype_code(scales), ptr(bias), ptr(out), dtype_code(out), M, K, N, gs, bits,
+                  float(zoff), ptr(ws), 0 if ws is None else ws.numel(), stream_handle())
+        return out
     if ws is None:
         ws = workspace(gemv_workspace_bytes(M, K, N, gs, bits, xd))
     _lib.call("miq_gptq_gemv", ptr(xf), xd, ptr(perm), ptr(qweight), ptr(qzeros),
               ptr(scales), dtype_code(scales), ptr(bias), ptr(out), dtype_code(out), M, K, N, gs,
               bits, float(zoff), ptr(ws), 0 if ws is None else ws.numel(), stream_handle())
     return out
-
-
-def _gptq_gemm(xf, qweight, qzeros, scales, K, N, gs, bits, zoff, bias, perm, out):
-    raise NotImplementedError("MFMA GEMM not built")
 
 
 def gptq_quantize(W, group_size=32, bits=4, from_out_in=False):

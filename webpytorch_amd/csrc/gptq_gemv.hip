@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void gptq_repack_kernel(const uint32_t* __rest
 // writes the output and re-arms the counter to zero, so results are deterministic.
 
 #ifndef MIQ_GEMV_MIN_WGS
-#define MIQ_GEMV_MIN_WGS 128  // split K further while fewer workgroups than this would run
+#define MIQ_GEMV_MIN_WGS 1  // split K further while fewer workgroups than this would run
 #endif
 #ifndef MIQ_GEMV_MAX_WAVES
 #define MIQ_GEMV_MAX_WAVES 4  // waves per workgroup (256 threads)
@@ -133,27 +133,6 @@ template <> struct Codes<8> {
     return part;
   }
 };
-
-// Raw scale words of 4 adjacent columns (fp16: 8 bytes, fp32: 16 bytes); converted only when
-// used, so that issuing a batch's loads never waits for them.
-template <typename ST> __device__ __forceinline__ uint4 load_scales4(const ST* p);
-template <> __device__ __forceinline__ uint4 load_scales4<float>(const float* p) {
-  return *reinterpret_cast<const uint4*>(p);
-}
-template <> __device__ __forceinline__ uint4 load_scales4<__half>(const __half* p) {
-  const uint2 t = *reinterpret_cast<const uint2*>(p);
-  return make_uint4(t.x, t.y, 0u, 0u);
-}
-template <typename ST> __device__ __forceinline__ void scales4(uint4 r, float* v);
-template <> __device__ __forceinline__ void scales4<float>(uint4 r, float* v) {
-  v[0] = __uint_as_float(r.x); v[1] = __uint_as_float(r.y); v[2] = __uint_as_float(r.z); v[3] = __uint_as_float(r.w);
-}
-template <> __device__ __forceinline__ void scales4<__half>(uint4 r, float* v) {
-  v[0] = __half2float(__ushort_as_half((unsigned short)(r.x & 0xFFFF)));
-  v[1] = __half2float(__ushort_as_half((unsigned short)(r.x >> 16)));
-  v[2] = __half2float(__ushort_as_half((unsigned short)(r.y & 0xFFFF)));
-  v[3] = __half2float(__ushort_as_half((unsigned short)(r.y >> 16)));
-}
 
 template <int RPW> struct GemvBatch {
   uint4 w[RPW];
@@ -234,13 +213,7 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
     for (int o = 1; o < SEG; o <<= 1) sum += __shfl_xor(sum, o, 64);
     if ((lane & (SEG - 1)) == 0) xsum[m * nb + kk / BK] = sum;
     if constexpr (kHalf) {
-      uint4 t;
-      if constexpr (BITS == 4) {  // pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7)
-        t = make_uint4(pack_h2(v[0], v[4]), pack_h2(v[1], v[5]), pack_h2(v[2], v[6]), pack_h2(v[3], v[7]));
-      } else {                    // per 4-row word: (x0,x2) (x1,x3)
-        t = make_uint4(pack_h2(v[0], v[2]), pack_h2(v[1], v[3]), pack_h2(v[4], v[6]), pack_h2(v[5], v[7]));
-      }
-      *reinterpret_cast<uint4*>(xs_h + (size_t)m * L + kk) = t;
+      *reinterpret_cast<uint4*>(xs_h + (size_t)m * L + kk) = pack8_pairs<BITS>(v);
     } else {
       float4* d = reinterpret_cast<float4*>(xs_f + (size_t)m * L + kk);
       d[0] = make_float4(v[0], v[1], v[2], v[3]);
@@ -403,7 +376,7 @@ static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool ha
   const int wmax = MIQ_GEMV_MAX_WAVES;
   const int base = p->tiles * p->mblocks;
   int waves, ksplit;
-  if (have_ws) {
+  if (have_ws && base <= kMaxCounters) {
     // one batch per wave; fewer waves per workgroup while too few workgroups would run
     waves = nbt < wmax ? nbt : wmax;
     ksplit = (nbt + waves - 1) / waves;
@@ -424,7 +397,7 @@ static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool ha
   const int L = rows_per_wg * per, nb = rows_per_wg / rpw;
   p->lds = (((size_t)p->mr * L * xb + 15) & ~(size_t)15) + (((size_t)p->mr * nb * 4 + 15) & ~(size_t)15) +
            (size_t)waves * p->mr * 256 * 4;
-  p->counter_bytes = ksplit > 1 ? (((size_t)p->tiles * p->mblocks * 4 + 255) & ~(size_t)255) : 0;
+  p->counter_bytes = ksplit > 1 ? kCounterBytes : 0;
   p->ws_bytes = ksplit > 1 ? p->counter_bytes + (size_t)ksplit * M * N * 4 : 0;
   return MIQ_OK;
 }

@@ -49,6 +49,16 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
 }
 
+// 8 consecutive activations (one int4 packed row, or two int8 rows) as fp16 in the pair order
+// that the code unpack produces: int4 (x0,x4) (x1,x5) (x2,x6) (x3,x7); int8, per 4-row word,
+// (x0,x2) (x1,x3). A dot product over a packed row is the same sum in that order.
+template <int BITS> __device__ __forceinline__ uint4 pack8_pairs(const float* v) {
+  if constexpr (BITS == 4)
+    return make_uint4(pack_h2(v[0], v[4]), pack_h2(v[1], v[5]), pack_h2(v[2], v[6]), pack_h2(v[3], v[7]));
+  else
+    return make_uint4(pack_h2(v[0], v[2]), pack_h2(v[1], v[3]), pack_h2(v[4], v[6]), pack_h2(v[5], v[7]));
+}
+
 // ---- wavefront (64 lanes) reductions --------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -91,10 +101,37 @@ __device__ __forceinline__ half2v byte02(uint32_t w) {
 }
 __device__ __forceinline__ float dot2(half2v a, half2v b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 
+// Raw scale words of 4 adjacent columns (fp16: 8 bytes, fp32: 16 bytes); converted only when
+// used, so that issuing a batch's loads never waits for them.
+template <typename ST> __device__ __forceinline__ uint4 load_scales4(const ST* p);
+template <> __device__ __forceinline__ uint4 load_scales4<float>(const float* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+template <> __device__ __forceinline__ uint4 load_scales4<__half>(const __half* p) {
+  const uint2 t = *reinterpret_cast<const uint2*>(p);
+  return make_uint4(t.x, t.y, 0u, 0u);
+}
+template <typename ST> __device__ __forceinline__ void scales4(uint4 r, float* v);
+template <> __device__ __forceinline__ void scales4<float>(uint4 r, float* v) {
+  v[0] = __uint_as_float(r.x); v[1] = __uint_as_float(r.y); v[2] = __uint_as_float(r.z); v[3] = __uint_as_float(r.w);
+}
+template <> __device__ __forceinline__ void scales4<__half>(uint4 r, float* v) {
+  v[0] = __half2float(__ushort_as_half((unsigned short)(r.x & 0xFFFF)));
+  v[1] = __half2float(__ushort_as_half((unsigned short)(r.x >> 16)));
+  v[2] = __half2float(__ushort_as_half((unsigned short)(r.y & 0xFFFF)));
+  v[3] = __half2float(__ushort_as_half((unsigned short)(r.y >> 16)));
+}
+
 // Uniform (scalar) copy of a value that is the same in every lane.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Number of workgroups worth launching to cover the whole chip several times over.
 constexpr int kCUs = 256;
+
+// Split-K workspaces: every kernel keeps its arrival counters in the same fixed region at the
+// start of the workspace (so one call's partial sums can never land on another call's
+// counters) and its partials after it.
+constexpr size_t kCounterBytes = 256 * 1024;
+constexpr int kMaxCounters = (int)(kCounterBytes / 4);
 
 }  // namespace miq
