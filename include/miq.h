@@ -125,6 +125,44 @@ int miq_q4k_dequant_f32(const uint8_t* blocks, float* out, int64_t n_blocks, voi
 int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out,
                  int out_dtype, int M, int K, int N, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Sparse MoE MLP (router + experts), all on the device
+ *   route buffer: opaque int32 words laid out by (T, E, k), miq_moe_route_bytes long.
+ *   expert weights are stacked: qweight [E][K/per][N], qzeros [E][K/gs][N/per], scales [E][K/gs][N].
+ * ------------------------------------------------------------------------------------- */
+
+/* Size of the route buffer for T tokens, E experts and top-k (T * k <= 4096, E <= 1024). */
+int miq_moe_route_bytes(int T, int E, int k, size_t* bytes);
+
+/* logits fp32 [T][E] -> float64 softmax, top-k (ties to the lower expert index), renormalised
+ * over the k picks when norm_topk != 0; per-expert sorted token slots and row tiles.
+ * Replaces: the host routing of `moe_mlp` and `_softmax_rows` (webtorch/lm_engine.py:294-307,
+ * 331-333), which reads the logits back to the host. */
+int miq_moe_route(const float* logits, int T, int E, int k, int norm_topk, void* route,
+                  size_t route_bytes, void* stream);
+
+/* h = silu(x @ Wgate[e]) * (x @ Wup[e]) for each sorted slot's token and expert, x fp16 [T][H];
+ * h is fp32-accurate, stored as two fp16 planes [2][T*k][I]: hi = fp16(h), lo = fp16(h - hi).
+ * Replaces: the per-expert `silu(exp["gate"](xe)) * exp["up"](xe)` of `moe_mlp`
+ * (webtorch/lm_engine.py:310-316). */
+int miq_moe_gate_up(const void* x, const void* route, int T, int E, int k, const int32_t* qw_gate,
+                    const int32_t* qz_gate, const void* sc_gate, const int32_t* qw_up,
+                    const int32_t* qz_up, const void* sc_up, int scales_dtype, void* h, int H, int I,
+                    int gs, int bits, float zero_offset, void* stream);
+
+/* y[T*k][H] fp32 = routing weight * ((hi + lo) @ Wdown[e]) per sorted slot, h as written by
+ * miq_moe_gate_up.
+ * Replaces: `exp["down"](...)` and `ye * w` of `moe_mlp` (webtorch/lm_engine.py:316-318). */
+int miq_moe_down(const void* h, const void* route, int T, int E, int k, const int32_t* qw,
+                 const int32_t* qz, const void* sc, int scales_dtype, float* y, int I, int H, int gs,
+                 int bits, float zero_offset, void* stream);
+
+/* out[T][H] fp32 = sum of each token's k slot outputs in ascending expert order, from zero.
+ * Replaces: the scatter-add `acc[rows] = acc[rows] + ye` of `moe_mlp`
+ * (webtorch/lm_engine.py:308-321). */
+int miq_moe_combine(const float* y, const void* route, int T, int E, int k, float* out, int H,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -355,3 +355,96 @@ class GGMLLinear:
 
     def nbytes(self):
         return int(self.packed.numel() + (0 if self.bias is None else self.bias.numel() * 4))
+
+
+# ---- sparse MoE ----------------------------------------------------------------------
+def moe_route_bytes(T, E, k):
+    n = ctypes.c_size_t(0)
+    _lib.call("miq_moe_route_bytes", T, E, k, ctypes.byref(n))
+    return int(n.value)
+
+
+class MoEExperts:
+    """The experts of one sparse-MoE layer, stacked on the device for the grouped kernels.
+
+    `experts` is the reference's list of {"gate", "up", "down"} GPTQ linears
+    (`webtorch/lm_engine.py:294-299`; built by `webtorch/llm.py:522-534`), here
+    `QuantizedLinear` objects (or AutoGPTQ layer dicts) that share group size, bit width, zero
+    offset and scale dtype. Calling it runs routing, gate/up, down and combine on the current
+    stream with no host synchronisation."""
+
+    def __init__(self, experts):
+        def as_ql(d):
+            if isinstance(d, QuantizedLinear):
+                return d
+            return QuantizedLinear.from_autogptq(d["qweight"], d["qzeros"], d["scales"], d.get("bias"),
+                                                 d["gs"], d["bits"])
+        exps = [{k: as_ql(e[k]) for k in ("gate", "up", "down")} for e in experts]
+        g0 = exps[0]["gate"]
+        self.E = len(exps)
+        self.H, self.I = g0.Kp, g0.Np
+        self.gs, self.bits, self.zoff = g0.gs, g0.bits, g0.zero_offset
+        for e in exps:
+            for name, (K, N) in (("gate", (self.H, self.I)), ("up", (self.H, self.I)), ("down", (self.I, self.H))):
+                q = e[name]
+                if (q.Kp, q.Np, q.gs, q.bits, q.zero_offset) != (K, N, self.gs, self.bits, self.zoff):
+                    raise ValueError("experts must share shapes, group size, bits and zero offset")
+                if q.perm is not None:
+                    raise NotImplementedError("act-order (g_idx) experts")
+                if q.bias is not None and bool(torch.any(q.bias != 0)):
+                    raise NotImplementedError("expert linears with a bias")
+        self.sdt = exps[0]["gate"].scales.dtype
+        self.w = {}
+        for name in ("gate", "up", "down"):
+            self.w[name] = tuple(torch.stack([getattr(e[name], a).to(self.sdt) if a == "scales" else getattr(e[name], a)
+                                              for e in exps]).contiguous()
+                                 for a in ("qweight", "qzeros", "scales"))
+
+    def __call__(self, x, logits, top_k, norm_topk_prob=True):
+        """x (T, H) -> (T, H) float32; logits (T, E) router outputs."""
+        xt = as_activation(x)
+        T = int(xt.shape[0])
+        xh = aligned16(xt.reshape(T, self.H).to(torch.float16).contiguous())
+        lg = as_activation(logits).float().reshape(T, self.E).contiguous()
+        out = torch.empty((T, self.H), dtype=torch.float32, device=xh.device)
+        if T == 0:
+            return out
+        k = int(top_k)
+        route = torch.empty(moe_route_bytes(T, self.E, k), dtype=torch.uint8, device=xh.device)
+        h = torch.empty((2, T * k, self.I), dtype=torch.float16, device=xh.device)  # hi, lo planes
+        y = torch.empty((T * k, self.H), dtype=torch.float32, device=xh.device)
+        st = stream_handle()
+        sd = dtype_code(self.w["gate"][2])
+        _lib.call("miq_moe_route", ptr(lg), T, self.E, k, int(bool(norm_topk_prob)), ptr(route), route.numel(), st)
+        g, u, d = self.w["gate"], self.w["up"], self.w["down"]
+        _lib.call("miq_moe_gate_up", ptr(xh), ptr(route), T, self.E, k, ptr(g[0]), ptr(g[1]), ptr(g[2]), ptr(u[0]),
+                  ptr(u[1]), ptr(u[2]), sd, ptr(h), self.H, self.I, self.gs, self.bits, float(self.zoff), st)
+        _lib.call("miq_moe_down", ptr(h), ptr(route), T, self.E, k, ptr(d[0]), ptr(d[1]), ptr(d[2]), sd, ptr(y),
+                  self.I, self.H, self.gs, self.bits, float(self.zoff), st)
+        _lib.call("miq_moe_combine", ptr(y), ptr(route), T, self.E, k, ptr(out), self.H, st)
+        self.last_route = route
+        return out
+
+
+def moe_mlp(lm, lay, x):
+    """Sparse MoE MLP, drop-in for `moe_mlp(lm, lay, x)` (`webtorch/lm_engine.py:294-329`) with
+    the same `lay["moe"]` schema: gate (router linear), experts [{gate, up, down}], top_k,
+    norm_topk_prob, shared {gate, up, down} | None, shared_gate | None. Routing runs on the
+    device (the reference reads the router logits back to the host); the stacked experts are
+    cached in the dict under "_grouped". The activations enter the expert GEMMs as fp16."""
+    m = lay["moe"]
+    xt = as_activation(x)
+    T = int(xt.shape[0])
+    logits = m["gate"](xt)
+    ex = m.get("_grouped")
+    if ex is None:
+        ex = m["_grouped"] = MoEExperts(m["experts"])
+    out = ex(xt, logits, m["top_k"], m.get("norm_topk_prob", True))
+    s = m.get("shared")
+    if s:
+        g = s["gate"](xt).float()
+        ys = s["down"]((g * torch.sigmoid(g) * s["up"](xt).float()).to(xt.dtype)).float()
+        if m.get("shared_gate") is not None:
+            ys = ys * torch.sigmoid(m["shared_gate"](xt).float())
+        out = out + ys.reshape(T, -1)
+    return out

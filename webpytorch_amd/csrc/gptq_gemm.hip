@@ -22,16 +22,9 @@
 
 namespace miq {
 
-typedef _Float16 half8v __attribute__((ext_vector_type(8)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-
 #ifndef MIQ_GEMM_TARGET_WGS
 #define MIQ_GEMM_TARGET_WGS 256
 #endif
-
-__device__ __forceinline__ half8v cat4(half2v a, half2v b, half2v c, half2v d) {
-  return (half8v){a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
-}
 
 template <int BITS, int TM, int KC, typename ST, typename OT>
 __global__ __launch_bounds__(256) void gptq_gemm_kernel(
@@ -43,7 +36,6 @@ __global__ __launch_bounds__(256) void gptq_gemm_kernel(
   constexpr int BM = 16 * TM;
   constexpr int STEPS = KC / 32;
   constexpr int RB = BITS == 4 ? 1 : 2;  // 16-byte weight loads per lane and step
-  constexpr uint32_t MASK = (1u << BITS) - 1u;
   __shared__ __align__(16) _Float16 xs[BM * KC];  // activation chunk [BM][KC], pair order
   __shared__ int is_last;
 
@@ -115,15 +107,8 @@ __global__ __launch_bounds__(256) void gptq_gemm_kernel(
     if (!wave_active) continue;  // wave-uniform: the whole wave is past N
 
     // ---- zero points folded into the fp16 conversion: (1024 + q) - (1024 + z + zoff) ----
-    const uint32_t zw = zraw >> zshift;
     half2v zl[4], zh[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float zf = (float)((zw >> (s * BITS)) & MASK) + zoff;
-      const _Float16 l = (_Float16)(1024.f + zf), h = (_Float16)(64.f + zf);
-      zl[s] = (half2v){l, l};
-      zh[s] = (half2v){(_Float16)-h, (_Float16)-h};
-    }
+    zero_pairs<BITS>(zraw >> zshift, zoff, zl, zh);
     float4v part[TM][4];
 #pragma unroll
     for (int t = 0; t < TM; ++t)
@@ -133,23 +118,7 @@ __global__ __launch_bounds__(256) void gptq_gemm_kernel(
     for (int st = 0; st < STEPS; ++st) {
       half8v bf[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint32_t w0 = (&bw[st][0].x)[s];
-        if constexpr (BITS == 4) {
-          const uint32_t w8 = w0 >> 8;
-          const half2v h16 = (half2v){(_Float16)0.0625f, (_Float16)0.0625f};
-          bf[s] = cat4(as_h2(and_or(w0, 0x000F000Fu, 0x64006400u)) - zl[s],
-                       __builtin_elementwise_fma(as_h2(and_or(w0, 0x00F000F0u, 0x64006400u)), h16, zh[s]),
-                       as_h2(and_or(w8, 0x000F000Fu, 0x64006400u)) - zl[s],
-                       __builtin_elementwise_fma(as_h2(and_or(w8, 0x00F000F0u, 0x64006400u)), h16, zh[s]));
-        } else {
-          const uint32_t w1 = (&bw[st][1].x)[s];
-          bf[s] = cat4(as_h2(and_or(w0, 0x00FF00FFu, 0x64006400u)) - zl[s],
-                       as_h2(and_or(w0 >> 8, 0x00FF00FFu, 0x64006400u)) - zl[s],
-                       as_h2(and_or(w1, 0x00FF00FFu, 0x64006400u)) - zl[s],
-                       as_h2(and_or(w1 >> 8, 0x00FF00FFu, 0x64006400u)) - zl[s]);
-        }
-      }
+      for (int s = 0; s < 4; ++s) bf[s] = b_fragment<BITS>(bw[st], s, zl[s], zh[s]);
 #pragma unroll
       for (int t = 0; t < TM; ++t) {
         const half8v af = *reinterpret_cast<const half8v*>(xs + (16 * t + p) * KC + st * 32 + 8 * kb);

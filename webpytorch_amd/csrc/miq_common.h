@@ -122,6 +122,47 @@ template <> __device__ __forceinline__ void scales4<__half>(uint4 r, float* v) {
   v[3] = __half2float(__ushort_as_half((unsigned short)(r.y >> 16)));
 }
 
+// ---- matrix-core operands (v_mfma_f32_16x16x32_f16) --------------------------------------
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ half8v cat4(half2v a, half2v b, half2v c, half2v d) {
+  return (half8v){a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// Zero points of 4 adjacent columns (packed codes zw, column s in bits s*BITS) folded into the
+// fp16 conversion: zl = 1024 + z + zoff (subtracted from 1024 + q), zh = -(64 + z + zoff).
+template <int BITS>
+__device__ __forceinline__ void zero_pairs(uint32_t zw, float zoff, half2v* zl, half2v* zh) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const float zf = (float)((zw >> (s * BITS)) & ((1u << BITS) - 1u)) + zoff;
+    const _Float16 l = (_Float16)(1024.f + zf), h = (_Float16)(64.f + zf);
+    zl[s] = (half2v){l, l};
+    zh[s] = (half2v){(_Float16)-h, (_Float16)-h};
+  }
+}
+
+// MFMA B operand for column s of a lane's 4 columns: the 8 exact integers q - (z + zoff) of one
+// 32-wide k step, in the order c0 c4 c1 c5 c2 c6 c3 c7 (int4: one packed word, w[0]) or
+// c0 c2 c1 c3 c4 c6 c5 c7 (int8: two words, w[0] and w[1]).
+template <int BITS>
+__device__ __forceinline__ half8v b_fragment(const uint4* w, int s, half2v zl, half2v zh) {
+  const uint32_t w0 = (&w[0].x)[s];
+  if constexpr (BITS == 4) {
+    const uint32_t w8 = w0 >> 8;
+    const half2v h16 = (half2v){(_Float16)0.0625f, (_Float16)0.0625f};
+    return cat4(as_h2(and_or(w0, 0x000F000Fu, 0x64006400u)) - zl,
+                __builtin_elementwise_fma(as_h2(and_or(w0, 0x00F000F0u, 0x64006400u)), h16, zh),
+                as_h2(and_or(w8, 0x000F000Fu, 0x64006400u)) - zl,
+                __builtin_elementwise_fma(as_h2(and_or(w8, 0x00F000F0u, 0x64006400u)), h16, zh));
+  } else {
+    const uint32_t w1 = (&w[1].x)[s];
+    return cat4(as_h2(and_or(w0, 0x00FF00FFu, 0x64006400u)) - zl, as_h2(and_or(w0 >> 8, 0x00FF00FFu, 0x64006400u)) - zl,
+                as_h2(and_or(w1, 0x00FF00FFu, 0x64006400u)) - zl, as_h2(and_or(w1 >> 8, 0x00FF00FFu, 0x64006400u)) - zl);
+  }
+}
+
 // Uniform (scalar) copy of a value that is the same in every lane.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
