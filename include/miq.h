@@ -74,7 +74,8 @@ int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, int x_dtype, 
  * aligned, N % 4 == 0 and gs a multiple of 32 (int4) or 16 (int8); efficient for M <= 8.
  * workspace (256-byte aligned, workspace_bytes >= miq_gptq_gemv_workspace) lets the K
  * dimension be split across workgroups; with NULL the call uses one workgroup per column
- * tile (slower) and fails for K too large to stage.
+ * tile (slower) and fails for K too large to stage. For M == 1, bias may alias out (fp32):
+ * out = out + x @ W, an in-place residual add.
  * Replaces: `_gptq_matmul` M == 1 dispatch to `_GPTQ_GEMV_WGSL`
  * (webtorch/_core.py:3926-3978, 4008-4027) and the bias add of `QuantizedLinear.forward`
  * (webtorch/_core.py:4446-4456). */
@@ -162,6 +163,52 @@ int miq_moe_down(const void* h, const void* route, int T, int E, int k, const in
  * (webtorch/lm_engine.py:308-321). */
 int miq_moe_combine(const float* y, const void* route, int T, int E, int k, float* out, int H,
                     void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Decode-step operators (fp32 activations). Positions and token ids live in a device
+ * "decode state" of miq_decode_state_words() int32 words: [0] position of the next token,
+ * [1] tokens generated, [2] zero between calls, [3] last token id; zero it before a sequence.
+ * ------------------------------------------------------------------------------------- */
+int miq_decode_state_words(void);
+
+/* out[t][:] = embed[ids[t]][:] (fp16 table [V][H] -> fp32); out-of-range ids give zeros.
+ * Replaces: `CausalLM._embed_ids` (webtorch/llm.py:1530-1536). */
+int miq_embed(const int32_t* ids, const void* embed, float* out, int T, int H, int V, void* stream);
+
+/* out[t] = (x[t] / sqrt(mean(x[t]^2) + eps)) * w, fp32.
+ * Replaces: `CausalLM._rms` (webtorch/llm.py:1259-1268) and `rmsnorm` (webtorch/_core.py:2234-2263). */
+int miq_rmsnorm(const float* x, const float* w, float* out, int T, int H, float eps, void* stream);
+
+/* Rotate-half RoPE (theta, float64 angles rounded to fp32) at positions state[0] + t of the
+ * fused q|k|v rows qkv [T][(NH + 2 NKV) HD]; q to q_out [T][NH][HD]; k, v written into the
+ * caches [NKV][LMAX][HD] at their positions (positions >= LMAX are dropped).
+ * Replaces: `_rope_np`, `_rot` and the rope step of `_kv_forward` (webtorch/llm.py:1270-1304,
+ * 1626-1627), `rope_decode` (webtorch/_core.py:2302-2330) and `kv_write`
+ * (webtorch/_core.py:1504-1540). */
+int miq_rope_kv(const float* qkv, const int32_t* state, float* q_out, float* kcache, float* vcache,
+                int T, int NH, int NKV, int HD, int LMAX, double theta, void* stream);
+
+/* Causal GQA attention: token t (position state[0] + t) of head h attends to cache positions
+ * 0..state[0] + t of kv head h / (NH / NKV); out [T][NH][HD] fp32.
+ * Replaces: `KVCache.attn` + `gqa_attention` + `softmax` (webtorch/_core.py:1543-1596,
+ * 1319-1340, 1764-1787). */
+int miq_attention(const float* q, const float* kcache, const float* vcache, const int32_t* state,
+                  float* out, int T, int NH, int NKV, int HD, int LMAX, float scale, void* stream);
+
+/* out[t][i] = silu(gu[t][i]) * gu[t][I + i] for the fused gate|up rows.
+ * Replaces: `silu(gate(x)) * up(x)` of `CausalLM._mlp` (webtorch/llm.py:1489-1496,
+ * webtorch/_core.py:503-504). */
+int miq_silu_mul(const float* gu, float* out, int T, int I, void* stream);
+
+/* h[i] += y[i] (residual add). */
+int miq_add(float* h, const float* y, int64_t n, void* stream);
+
+/* Greedy pick on the device: argmax of logits[V] (first index on ties) -> ids[0],
+ * history[state[1]] (if < hist_len), state[3]; state[1] += 1; state[0] += advance.
+ * Replaces: `_head_argmax` / `_pick` greedy branch (webtorch/llm.py:1309-1336), which reads
+ * the logits back to the host every token. */
+int miq_argmax_advance(const float* logits, int V, int32_t* ids, int32_t* history, int hist_len,
+                       int32_t* state, int advance, void* stream);
 
 #ifdef __cplusplus
 }

@@ -150,12 +150,14 @@ SMALL = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--full", action="store_true", help="also the full Qwen2-0.5B-shaped decode")
+    ap.add_argument("--full-only", action="store_true", help="only the full Qwen2-0.5B-shaped decode")
     a = ap.parse_args()
     wt, lm_engine, llm = import_reference()
-    make_quantize(wt, os.path.join(HERE, "gptq_quantize.npz"))
-    make_moe(wt, lm_engine, os.path.join(HERE, "moe_small.npz"))
-    make_decode(wt, llm, os.path.join(HERE, "decode_small.npz"), 11, SMALL, 16, 24, 64)
-    if a.full:
+    if not a.full_only:
+        make_quantize(wt, os.path.join(HERE, "gptq_quantize.npz"))
+        make_moe(wt, lm_engine, os.path.join(HERE, "moe_small.npz"))
+        make_decode(wt, llm, os.path.join(HERE, "decode_small.npz"), 11, SMALL, 16, 24, 64)
+    if a.full or a.full_only:
         make_decode(wt, llm, os.path.join(HERE, "decode_qwen2_05b.npz"), 5, dict(synth.QWEN2_05B),
                     64, 128, 256)
 

@@ -1,0 +1,150 @@
+"""GPU parity of the decode engine: each decode-step operator against the oracle's building
+blocks, and end-to-end greedy token ids against the reference's own CPU decode (fixtures)."""
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import decode
+from webpytorch_amd import synth
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+SHAPE_KEYS = ["L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits"]
+
+
+def _state(torch, pos):
+    from webpytorch_amd import _lib
+    st = torch.zeros(_lib.lib().miq_decode_state_words(), dtype=torch.int32, device="cuda")
+    st[0] = pos
+    return st
+
+
+def test_rmsnorm_rope_silu_match_oracle(gpu):
+    import torch
+    from webpytorch_amd import _lib
+    from webpytorch_amd.core import ptr
+    o = decode.Qwen2Oracle(synth.decoder_weights(1, L=1, H=128, NH=4, NKV=2, HD=64, I=128, V=64, gs=64), lmax=32)
+    rng = np.random.default_rng(0)
+    T, H = 5, 128
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32)
+    out = torch.empty((T, H), device="cuda")
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()  # held: raw pointers do not keep tensors alive
+    _lib.call("miq_rmsnorm", ptr(xd), ptr(wd), ptr(out), T, H, 1e-6, None)
+    np.testing.assert_allclose(out.cpu().numpy(), o.rms(x, w), rtol=2e-6, atol=1e-6)
+    # rope + kv write at position 7
+    NH, NKV, HD, LMAX, pos = 4, 2, 64, 32, 7
+    qkv = rng.standard_normal((T, (NH + 2 * NKV) * HD)).astype(np.float32)
+    q = torch.empty((T, NH * HD), device="cuda")
+    kc = torch.zeros((NKV, LMAX, HD), device="cuda")
+    vc = torch.zeros_like(kc)
+    qkvd, st = torch.from_numpy(qkv).cuda(), _state(torch, pos)
+    _lib.call("miq_rope_kv", ptr(qkvd), ptr(st), ptr(q), ptr(kc), ptr(vc), T, NH, NKV, HD, LMAX, 1e6, None)
+    cos, sin = o.rope_tables(pos, T)
+    qr = qkv[:, :NH * HD].reshape(T, NH, HD).transpose(1, 0, 2)
+    kr = qkv[:, NH * HD:(NH + NKV) * HD].reshape(T, NKV, HD).transpose(1, 0, 2)
+    vr = qkv[:, (NH + NKV) * HD:].reshape(T, NKV, HD).transpose(1, 0, 2)
+    qref = qr * cos + o.rot(qr) * sin
+    kref = kr * cos + o.rot(kr) * sin
+    assert np.array_equal(q.cpu().numpy().reshape(T, NH, HD).transpose(1, 0, 2), qref)
+    assert np.array_equal(kc.cpu().numpy()[:, pos:pos + T], kref)
+    assert np.array_equal(vc.cpu().numpy()[:, pos:pos + T], vr)
+    assert not kc.cpu().numpy()[:, :pos].any() and not kc.cpu().numpy()[:, pos + T:].any()
+    # silu * mul
+    gu = rng.standard_normal((T, 2 * 96)).astype(np.float32)
+    act = torch.empty((T, 96), device="cuda")
+    gud = torch.from_numpy(gu).cuda()
+    _lib.call("miq_silu_mul", ptr(gud), ptr(act), T, 96, None)
+    np.testing.assert_allclose(act.cpu().numpy(), o.silu(gu[:, :96]) * gu[:, 96:], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("pos,T", [(0, 1), (9, 1), (0, 6), (20, 4)])
+def test_attention_matches_oracle(gpu, pos, T):
+    import torch
+    from webpytorch_amd import _lib
+    from webpytorch_amd.core import ptr
+    NH, NKV, HD, LMAX = 14, 2, 64, 64
+    o = decode.Qwen2Oracle(synth.decoder_weights(1, L=1, H=128, NH=2, NKV=1, HD=64, I=128, V=64, gs=64), lmax=LMAX)
+    rng = np.random.default_rng(pos * 7 + T)
+    kc = rng.standard_normal((NKV, LMAX, HD)).astype(np.float32)
+    vc = rng.standard_normal((NKV, LMAX, HD)).astype(np.float32)
+    q = rng.standard_normal((T, NH, HD)).astype(np.float32)
+    out = torch.empty((T, NH * HD), device="cuda")
+    scale = 1.0 / math.sqrt(HD)
+    qd, kd, vd, st = (torch.from_numpy(q).cuda(), torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda(),
+                      _state(torch, pos))
+    _lib.call("miq_attention", ptr(qd), ptr(kd), ptr(vd), ptr(st), ptr(out), T, NH, NKV, HD, LMAX, scale, None)
+    S = pos + T
+    mask = None
+    if T > 1:
+        mask = np.triu(np.full((T, S), -1e9, np.float32), 1 + (S - T)).reshape(1, T, S)
+    ref = o.attend(q.transpose(1, 0, 2), kc[:, :S], vc[:, :S], mask, scale).transpose(1, 0, 2).reshape(T, NH * HD)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_argmax_first_index_and_state(gpu):
+    import torch
+    from webpytorch_amd import _lib
+    from webpytorch_amd.core import ptr
+    V = 151936
+    lg = np.random.default_rng(1).standard_normal(V).astype(np.float32)
+    lg[[5000, 90000, 151935]] = lg.max() + 1.0  # ties: the first index wins
+    st = _state(torch, 10)
+    ids = torch.zeros(4, dtype=torch.int32, device="cuda")
+    hist = torch.full((8,), -1, dtype=torch.int32, device="cuda")
+    d = torch.from_numpy(lg).cuda()
+    for step in range(3):
+        _lib.call("miq_argmax_advance", ptr(d), V, ptr(ids), ptr(hist), 8, ptr(st), 1, None)
+    s = st.cpu().numpy()
+    assert int(ids[0]) == 5000 and list(hist.cpu().numpy()[:4]) == [5000, 5000, 5000, -1]
+    assert s[0] == 13 and s[1] == 3 and s[2] == 0 and s[3] == 5000
+
+
+def _engine(g, lmax):
+    from webpytorch_amd import llm
+    sh = dict(zip(SHAPE_KEYS, [int(v) for v in g["shape"]]))
+    w = synth.decoder_weights(int(g["seed"]), **sh)
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    return llm.CausalLM.from_weights(w, lmax=lmax), ids, w
+
+
+def test_decode_matches_reference_golden_small(gpu):
+    """Greedy ids of the reference's own CPU decode (fixture), reduced shape: eager and replayed."""
+    g = np.load(os.path.join(GOLDEN, "decode_small.npz"))
+    m, ids, _ = _engine(g, int(g["lmax"]))
+    want = [int(t) for t in g["tokens"]]
+    assert m.generate(ids, int(g["max_new"]), use_graph=False).tokens == want
+    assert m.generate(ids, int(g["max_new"]), use_graph=True).tokens == want
+    assert m.generate(ids, int(g["max_new"]), use_graph=True).tokens == want  # graph reused
+
+
+def test_head_requantization_bit_exact(gpu):
+    """The device head equals the oracle's block-wise `_gptq_quantize` of the tied embedding."""
+    g = np.load(os.path.join(GOLDEN, "decode_small.npz"))
+    m, _, w = _engine(g, 32)
+    o = decode.Qwen2Oracle(w, lmax=32)
+    qw = np.concatenate([b["qweight"] for b in o.head], axis=1)
+    qz = np.concatenate([b["qzeros"] for b in o.head], axis=1)
+    sc = np.concatenate([b["scales"] for b in o.head], axis=1)
+    assert np.array_equal(m.head.qweight.cpu().numpy(), qw)
+    assert np.array_equal(m.head.qzeros.cpu().numpy(), qz)
+    assert np.array_equal(m.head.scales.cpu().numpy().view(np.uint32), sc.view(np.uint32))
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(GOLDEN, "decode_qwen2_05b.npz")),
+                    reason="full-shape fixture not generated")
+def test_decode_matches_reference_golden_qwen2_05b(gpu):
+    """End-to-end config: Qwen2-0.5B shape, 64-token prompt, 128 greedy tokens, identical ids."""
+    g = np.load(os.path.join(GOLDEN, "decode_qwen2_05b.npz"))
+    m, ids, _ = _engine(g, int(g["lmax"]))
+    res = m.generate(ids, int(g["max_new"]))
+    assert res.tokens == [int(t) for t in g["tokens"]]
+
+
+def test_generate_refuses_overlong(gpu):
+    g = np.load(os.path.join(GOLDEN, "decode_small.npz"))
+    m, ids, _ = _engine(g, 20)
+    with pytest.raises(ValueError, match="lmax"):
+        m.generate(ids, 10)

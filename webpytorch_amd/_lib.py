@@ -14,6 +14,7 @@ MIQ_F32, MIQ_F16 = 0, 1
 ERRORS = {-1: ValueError, -2: ValueError, -3: NotImplementedError, -4: RuntimeError}
 
 _p, _i, _f, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_size_t
+_d = ctypes.c_double
 
 # name -> argument types (restype is int for every compute entry point)
 SIGNATURES = {
@@ -29,6 +30,13 @@ SIGNATURES = {
     "miq_moe_gate_up": [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _p],
     "miq_moe_down": [_p, _p, _i, _i, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _p],
     "miq_moe_combine": [_p, _p, _i, _i, _i, _p, _i, _p],
+    "miq_embed": [_p, _p, _p, _i, _i, _i, _p],
+    "miq_rmsnorm": [_p, _p, _p, _i, _i, _f, _p],
+    "miq_rope_kv": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _d, _p],
+    "miq_attention": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _p],
+    "miq_silu_mul": [_p, _p, _i, _i, _p],
+    "miq_add": [_p, _p, _i64, _p],
+    "miq_argmax_advance": [_p, _i, _p, _p, _i, _p, _i, _p],
     "miq_q4k_dequant_f32": [_p, _p, _i64, _p],
     "miq_q4k_gemv": [_p, _i, _p, _p, _p, _i, _i, _i, _i, _p],
 }
@@ -51,6 +59,8 @@ def lib():
         L.miq_last_error.restype = ctypes.c_char_p
         L.miq_last_error.argtypes = []
         L.miq_version.restype = ctypes.c_int
+        L.miq_decode_state_words.restype = ctypes.c_int
+        L.miq_decode_state_words.argtypes = []
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args

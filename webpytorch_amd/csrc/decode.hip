@@ -1,0 +1,283 @@
+// Decode-step operators of a Qwen2-style decoder for gfx950, in fp32 like the reference's
+// numpy decode path (`webtorch/llm.py:1258-1304, 1489-1536, 1619-1636`;
+// `webtorch/_core.py:1319-1340, 1543-1596, 1764-1787`).
+//
+// Every position and token id lives in device memory (the decode state), so a whole decode
+// step -- embedding, 24 layers, head and argmax -- replays from a captured graph with no host
+// work between tokens: the argmax writes the next token id, appends it to the history and
+// advances the position.
+//
+// Decode state (int32 words): [0] position of the next token, [1] tokens generated,
+// [2] argmax arrival counter (zero between calls), [3] last token id, then per argmax
+// workgroup its (value bits, index) partial.
+#include <math.h>
+
+#include "miq_common.h"
+
+// The operators that restate the reference's elementwise numpy arithmetic round every product
+// and sum separately (no fused multiply-add), so that their results match it bit for bit;
+// explicit fmaf() calls (the attention dot products) are unaffected.
+#pragma clang fp contract(off)
+
+namespace miq {
+
+constexpr int kArgmaxWGs = 64;
+
+// h[t][:] = embed[ids[t]][:] as fp32
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ ids, const __half* __restrict__ emb,
+                                                    float* __restrict__ out, int H, int V) {
+  const int t = blockIdx.y;
+  const int id = ids[t];
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= H) return;
+  out[(size_t)t * H + c] = (id >= 0 && id < V) ? __half2float(emb[(size_t)id * H + c]) : 0.f;
+}
+
+// out = (x / sqrt(mean(x^2) + eps)) * w, one workgroup per row
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      float* __restrict__ out, int H, float eps) {
+  __shared__ float red[4];
+  const float* xr = x + (size_t)blockIdx.x * H;
+  float s = 0.f;
+  for (int c = threadIdx.x; c < H; c += 256) s = s + xr[c] * xr[c];  // products rounded
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float ms = ((red[0] + red[1]) + (red[2] + red[3])) / (float)H;
+  const float r = sqrtf(ms + eps);
+  float* o = out + (size_t)blockIdx.x * H;
+  for (int c = threadIdx.x; c < H; c += 256) o[c] = (xr[c] / r) * w[c];
+}
+
+// Rotate-half RoPE at positions pos0 + t (pos0 read from the device), float64 angles rounded to
+// fp32 cos/sin, then x*cos + rot(x)*sin with separate fp32 roundings. q goes to q_out
+// [T][NH][HD]; k and v go into the caches [NKV][LMAX][HD] at their positions (positions past
+// LMAX are not written).
+__global__ __launch_bounds__(256) void rope_kv_kernel(const float* __restrict__ qkv, const int32_t* __restrict__ state,
+                                                      float* __restrict__ q_out, float* __restrict__ kc,
+                                                      float* __restrict__ vc, int NH, int NKV, int HD, int LMAX,
+                                                      double theta) {
+  const int t = blockIdx.y;
+  const int pos = state[0] + t;
+  const int W = (NH + 2 * NKV) * HD;
+  const float* row = qkv + (size_t)t * W;
+  const int half = HD / 2;
+  for (int i = threadIdx.x; i < W; i += 256) {
+    const int head = i / HD, d = i - head * HD;
+    if (head >= NH + NKV) {  // v: copied into the cache
+      const int kv = head - NH - NKV;
+      if (pos < LMAX) vc[((size_t)kv * LMAX + pos) * HD + d] = row[i];
+      continue;
+    }
+    const int j = d < half ? d : d - half;
+    const double inv = 1.0 / pow(theta, (double)(2 * j) / (double)HD);
+    const double ang = (double)pos * inv;
+    const float c = (float)cos(ang), s = (float)sin(ang);
+    const float xv = row[i];
+    const float rv = d < half ? -row[i + half] : row[i - half];
+    const float y = xv * c + rv * s;
+    if (head < NH) {
+      q_out[((size_t)t * NH + head) * HD + d] = y;
+    } else if (pos < LMAX) {
+      kc[((size_t)(head - NH) * LMAX + pos) * HD + d] = y;
+    }
+  }
+}
+
+// Causal grouped-query attention: token t (position pos0 + t) of query head h attends to
+// cache positions 0 .. pos0 + t of kv head h / (NH / NKV). One wave per (head, token):
+// lanes over positions for the scores, lanes over the head dimension for the output.
+// scores = (q . k) * scale; p = exp(s - max) / sum; out = sum p v.
+__global__ __launch_bounds__(64) void attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                       const float* __restrict__ vc, const int32_t* __restrict__ state,
+                                                       float* __restrict__ out, int NH, int NKV, int HD, int LMAX,
+                                                       float scale) {
+  extern __shared__ float sp[];  // [LMAX] scores, then probabilities
+  __shared__ float qs[256];
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int kv = h / (NH / NKV);
+  int S = state[0] + t + 1;
+  S = S > LMAX ? LMAX : S;
+  for (int d = lane; d < HD; d += 64) qs[d] = q[((size_t)t * NH + h) * HD + d];
+  __syncthreads();
+  const float* K = kc + (size_t)kv * LMAX * HD;
+  const float* Vv = vc + (size_t)kv * LMAX * HD;
+  float mx = -INFINITY;
+  for (int j = lane; j < S; j += 64) {
+    const float* kr = K + (size_t)j * HD;
+    float a = 0.f;
+    for (int d = 0; d < HD; d += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+      a = fmaf(qs[d], k4.x, a);
+      a = fmaf(qs[d + 1], k4.y, a);
+      a = fmaf(qs[d + 2], k4.z, a);
+      a = fmaf(qs[d + 3], k4.w, a);
+    }
+    a *= scale;
+    sp[j] = a;
+    mx = fmaxf(mx, a);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int j = lane; j < S; j += 64) {
+    const float e = expf(sp[j] - mx);
+    sp[j] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  for (int j = lane; j < S; j += 64) sp[j] = sp[j] / sum;
+  __syncthreads();
+  for (int d = lane; d < HD; d += 64) {
+    float o = 0.f;
+    for (int j = 0; j < S; ++j) o = fmaf(sp[j], Vv[(size_t)j * HD + d], o);
+    out[((size_t)t * NH + h) * HD + d] = o;
+  }
+}
+
+// out[t][i] = silu(gu[t][i]) * gu[t][I + i], silu(x) = x * (1 / (1 + exp(-x)))
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gu, float* __restrict__ out, int I) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= I) return;
+  const float g = gu[(size_t)t * 2 * I + i], u = gu[(size_t)t * 2 * I + I + i];
+  out[(size_t)t * I + i] = (g * (1.f / (1.f + expf(-g)))) * u;
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float* __restrict__ h, const float* __restrict__ y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) h[i] += y[i];
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi) || (bv != bv && v == v);  // NaN never wins
+}
+
+// Greedy pick: argmax (first index on ties) over V logits with kArgmaxWGs workgroups; the
+// last to arrive combines the partials in workgroup order, writes the token id (to ids[0], to
+// the history at state[1] and to state[3]), advances the position by `advance` and re-arms
+// the counter.
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int V, int32_t* __restrict__ ids,
+                                                     int32_t* __restrict__ history, int hist_len,
+                                                     int32_t* __restrict__ state, int advance) {
+  __shared__ float bv_s[4];
+  __shared__ int bi_s[4];
+  __shared__ int is_last;
+  const int chunk = (V + gridDim.x - 1) / gridDim.x;
+  const int b0 = blockIdx.x * chunk, b1 = min(V, b0 + chunk);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = b0 + threadIdx.x; i < b1; i += 256) {
+    const float v = logits[i];
+    if (better(v, i, bv, bi)) { bv = v; bi = i; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if ((threadIdx.x & 63) == 0) { bv_s[threadIdx.x >> 6] = bv; bi_s[threadIdx.x >> 6] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (better(bv_s[w], bi_s[w], bv, bi)) { bv = bv_s[w]; bi = bi_s[w]; }
+    int32_t* part = state + 4 + 2 * blockIdx.x;
+    __hip_atomic_store(part, __float_as_int(bv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(part + 1, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    is_last = __hip_atomic_fetch_add(state + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+    if (is_last) {
+      float fv = -INFINITY;
+      int fi = 0x7fffffff;
+      for (int g = 0; g < (int)gridDim.x; ++g) {
+        const float v = __int_as_float(__hip_atomic_load(state + 4 + 2 * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const int i = __hip_atomic_load(state + 5 + 2 * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (better(v, i, fv, fi)) { fv = v; fi = i; }
+      }
+      if (fi >= V) fi = 0;  // all logits NaN
+      ids[0] = fi;
+      const int step = state[1];
+      if (step < hist_len) history[step] = fi;
+      state[1] = step + 1;
+      state[3] = fi;
+      state[0] += advance;
+      __hip_atomic_store(state + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace miq
+
+using namespace miq;
+
+extern "C" int miq_decode_state_words(void) { return 4 + 2 * kArgmaxWGs; }
+
+extern "C" int miq_embed(const int32_t* ids, const void* embed, float* out, int T, int H, int V, void* stream) {
+  MIQ_REQUIRE(T >= 0 && H > 0 && V > 0, MIQ_ERR_INVALID, "embed: T=%d H=%d V=%d", T, H, V);
+  if (T == 0) return MIQ_OK;
+  MIQ_REQUIRE(ids && embed && out, MIQ_ERR_INVALID, "embed: null pointer");
+  hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256, T), dim3(256), 0, static_cast<hipStream_t>(stream), ids,
+                     static_cast<const __half*>(embed), out, H, V);
+  return check_launch("embed");
+}
+
+extern "C" int miq_rmsnorm(const float* x, const float* w, float* out, int T, int H, float eps, void* stream) {
+  MIQ_REQUIRE(T >= 0 && H > 0, MIQ_ERR_INVALID, "rmsnorm: T=%d H=%d", T, H);
+  if (T == 0) return MIQ_OK;
+  MIQ_REQUIRE(x && w && out, MIQ_ERR_INVALID, "rmsnorm: null pointer");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, static_cast<hipStream_t>(stream), x, w, out, H, eps);
+  return check_launch("rmsnorm");
+}
+
+extern "C" int miq_rope_kv(const float* qkv, const int32_t* state, float* q_out, float* kcache, float* vcache, int T,
+                           int NH, int NKV, int HD, int LMAX, double theta, void* stream) {
+  MIQ_REQUIRE(T >= 0 && NH > 0 && NKV > 0 && NH % NKV == 0 && HD > 0 && HD % 2 == 0 && LMAX > 0, MIQ_ERR_INVALID,
+              "rope_kv: T=%d NH=%d NKV=%d HD=%d LMAX=%d", T, NH, NKV, HD, LMAX);
+  if (T == 0) return MIQ_OK;
+  MIQ_REQUIRE(qkv && state && q_out && kcache && vcache, MIQ_ERR_INVALID, "rope_kv: null pointer");
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(1, T), dim3(256), 0, static_cast<hipStream_t>(stream), qkv, state, q_out,
+                     kcache, vcache, NH, NKV, HD, LMAX, theta);
+  return check_launch("rope_kv");
+}
+
+extern "C" int miq_attention(const float* q, const float* kcache, const float* vcache, const int32_t* state, float* out,
+                             int T, int NH, int NKV, int HD, int LMAX, float scale, void* stream) {
+  MIQ_REQUIRE(T >= 0 && NH > 0 && NKV > 0 && NH % NKV == 0 && HD > 0 && HD <= 256 && HD % 4 == 0 && LMAX > 0,
+              MIQ_ERR_INVALID, "attention: T=%d NH=%d NKV=%d HD=%d LMAX=%d", T, NH, NKV, HD, LMAX);
+  if (T == 0) return MIQ_OK;
+  MIQ_REQUIRE((size_t)LMAX * 4 <= 64 * 1024, MIQ_ERR_UNSUPPORTED, "attention: LMAX=%d above 16384", LMAX);
+  MIQ_REQUIRE(q && kcache && vcache && state && out, MIQ_ERR_INVALID, "attention: null pointer");
+  MIQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), MIQ_ERR_ALIGN, "attention: caches must be 16-byte aligned");
+  hipLaunchKernelGGL(attention_kernel, dim3(NH, T), dim3(64), (size_t)LMAX * 4, static_cast<hipStream_t>(stream), q,
+                     kcache, vcache, state, out, NH, NKV, HD, LMAX, scale);
+  return check_launch("attention");
+}
+
+extern "C" int miq_silu_mul(const float* gu, float* out, int T, int I, void* stream) {
+  MIQ_REQUIRE(T >= 0 && I > 0, MIQ_ERR_INVALID, "silu_mul: T=%d I=%d", T, I);
+  if (T == 0) return MIQ_OK;
+  MIQ_REQUIRE(gu && out, MIQ_ERR_INVALID, "silu_mul: null pointer");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((I + 255) / 256, T), dim3(256), 0, static_cast<hipStream_t>(stream), gu,
+                     out, I);
+  return check_launch("silu_mul");
+}
+
+extern "C" int miq_add(float* h, const float* y, int64_t n, void* stream) {
+  MIQ_REQUIRE(n >= 0, MIQ_ERR_INVALID, "add: n=%lld", (long long)n);
+  if (n == 0) return MIQ_OK;
+  MIQ_REQUIRE(h && y, MIQ_ERR_INVALID, "add: null pointer");
+  hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream), h,
+                     y, (size_t)n);
+  return check_launch("add");
+}
+
+extern "C" int miq_argmax_advance(const float* logits, int V, int32_t* ids, int32_t* history, int hist_len,
+                                  int32_t* state, int advance, void* stream) {
+  MIQ_REQUIRE(V > 0 && hist_len >= 0, MIQ_ERR_INVALID, "argmax: V=%d", V);
+  MIQ_REQUIRE(logits && ids && state && (history || hist_len == 0), MIQ_ERR_INVALID, "argmax: null pointer");
+  const int wgs = V < 256 * kArgmaxWGs ? (V + 255) / 256 : kArgmaxWGs;
+  hipLaunchKernelGGL(argmax_kernel, dim3(wgs), dim3(256), 0, static_cast<hipStream_t>(stream), logits, V, ids, history,
+                     hist_len, state, advance);
+  return check_launch("argmax");
+}

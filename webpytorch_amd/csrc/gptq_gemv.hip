@@ -143,9 +143,9 @@ template <int RPW> struct GemvBatch {
 template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT>
 __global__ __launch_bounds__(256) void gptq_gemv_kernel(
     const XT* __restrict__ x, const int32_t* __restrict__ perm, const uint32_t* __restrict__ qw,
-    const uint32_t* __restrict__ qz, const ST* __restrict__ sc, const float* __restrict__ bias,
-    OT* __restrict__ out, float* __restrict__ ws, int* __restrict__ counters, int M, int K, int N,
-    int gs, float zoff, int rows_per_wg, int ksplit) {
+    const uint32_t* __restrict__ qz, const ST* __restrict__ sc, const float* bias, OT* out,
+    float* __restrict__ ws, int* __restrict__ counters, int M, int K, int N, int gs, float zoff, int rows_per_wg,
+    int ksplit) {
   using C = Codes<BITS>;
   constexpr int PER = C::PER, PAIRS = C::PAIRS;
   constexpr int BK = RPW * PER;

@@ -1,0 +1,215 @@
+"""GPTQ int4 decoder (Qwen2 family) on MI355X with a captured decode step: the drop-in
+counterpart of the reference's `CausalLM` decode path (`webtorch/llm.py:506-647, 1258-1336,
+1465-1489, 1558-1636, 1716-1817`) for GPTQ checkpoints.
+
+Host code only plans and launches; every operator is a HIP kernel from libmiq.so. The
+activations stay fp32, as in the reference's numpy decode. One decode step runs embedding ->
+24 x (RMSNorm, fused q|k|v GEMV + bias, RoPE + KV write, causal GQA attention, o GEMV +
+residual, RMSNorm, fused gate|up GEMV, SwiGLU, down GEMV + residual) -> final RMSNorm -> head
+GEMV -> device argmax. The position and the token ids live in a device "decode state", so the
+step is recorded once as a HIP graph and replayed per token with no host work in between (the
+reference re-uploads inputs and reads the logits back to the host every token,
+`webtorch/llm.py:1582-1589, 1808-1814`).
+
+Layout choices: q, k and v (and gate and up) share their input, so their GPTQ tensors are
+concatenated along the output dimension at load time and run as one GEMV (per-column groups
+make this identical to separate layers). The tied head is re-quantized from the fp16
+embedding on the device, bit-exact with `_gptq_quantize` (`webtorch/_core.py:3782-3824`;
+per-column quantization makes the reference's 4096-row blocks, `llm.py:594-602`, one matrix).
+"""
+import math
+import time
+
+import numpy as np
+import torch
+
+from . import _lib, core
+from .core import ptr, stream_handle
+
+
+class GenResult:
+    """Result of `generate` (`webtorch/llm.py:273-279`)."""
+
+    def __init__(self, text, tokens, ttft_s, decode_tok_s):
+        self.text = text
+        self.tokens = tokens
+        self.ttft_s = ttft_s
+        self.decode_tok_s = decode_tok_s
+
+    def __repr__(self):
+        return "GenResult(ttft=%.4fs, %.1f tok/s, %d tokens)" % (self.ttft_s, self.decode_tok_s, len(self.tokens))
+
+
+def _cat_layers(parts, gs, bits):
+    """Concatenate AutoGPTQ layers that share K along the output dimension."""
+    qw = np.concatenate([np.asarray(p["qweight"]) for p in parts], axis=1)
+    qz = np.concatenate([np.asarray(p["qzeros"]) for p in parts], axis=1)
+    sc = np.concatenate([np.asarray(p["scales"]) for p in parts], axis=1)
+    bias = None
+    if any(p.get("bias") is not None for p in parts):
+        bias = np.concatenate([np.asarray(p["bias"], np.float32) if p.get("bias") is not None
+                               else np.zeros(np.asarray(p["qweight"]).shape[1], np.float32) for p in parts])
+    return {"qweight": qw, "qzeros": qz, "scales": sc, "bias": bias}
+
+
+class _Lin:
+    """Device tensors of one (possibly fused) GPTQ linear."""
+
+    def __init__(self, d, K, gs, bits, zoff):
+        self.qweight = core.to_device(d["qweight"], torch.int32)
+        self.qzeros = core.to_device(d["qzeros"], torch.int32)
+        self.scales = core.to_device(d["scales"])
+        self.bias = None if d.get("bias") is None else core.to_device(np.asarray(d["bias"], np.float32))
+        self.K, self.N = K, int(self.qweight.shape[1])
+        self.gs, self.bits, self.zoff = gs, bits, zoff
+
+
+class CausalLM:
+    """Qwen2-shaped GPTQ decoder with device-resident decode (see module docstring).
+
+    Build with `CausalLM.from_weights(weights, lmax)` where `weights` holds AutoGPTQ tensors per
+    layer ({"q","k","v","o","gate","up","down"} dicts with qweight/qzeros/scales[/bias],
+    "in_ln", "post_ln"), the fp16 "embed" table (tied head), "final_norm" and "cfg"
+    (L, H, NH, NKV, HD, I, V, gs, bits[, eps, theta])."""
+
+    def __init__(self, weights, lmax=256):
+        c = weights["cfg"]
+        self.L, self.H, self.NH, self.NKV, self.HD = c["L"], c["H"], c["NH"], c["NKV"], c["HD"]
+        self.I, self.V, self.gs, self.bits = c["I"], c["V"], c["gs"], c["bits"]
+        self.eps = float(c.get("eps", 1e-6))
+        self.theta = float(c.get("theta", 1e6))
+        self.lmax = int(lmax)
+        core.device()
+        self.layers = []
+        for lay in weights["layers"]:
+            self.layers.append({
+                "qkv": _Lin(_cat_layers([lay["q"], lay["k"], lay["v"]], self.gs, self.bits), self.H, self.gs, self.bits, 1.0),
+                "o": _Lin(lay["o"], self.NH * self.HD, self.gs, self.bits, 1.0),
+                "gate_up": _Lin(_cat_layers([lay["gate"], lay["up"]], self.gs, self.bits), self.H, self.gs, self.bits, 1.0),
+                "down": _Lin(lay["down"], self.I, self.gs, self.bits, 1.0),
+                "in_ln": core.to_device(np.asarray(lay["in_ln"], np.float32)),
+                "post_ln": core.to_device(np.asarray(lay["post_ln"], np.float32)),
+            })
+        self.embed = core.to_device(np.asarray(weights["embed"], np.float16))
+        self.final_norm = core.to_device(np.asarray(weights["final_norm"], np.float32))
+        self.head = self._quantize_head()
+        self._alloc()
+        self._graph = None
+
+    @classmethod
+    def from_weights(cls, weights, lmax=256):
+        return cls(weights, lmax)
+
+    # ---- load-time ----
+    def _quantize_head(self):
+        """Tied head: the fp16 embedding (V, H) quantized on the device to int4 GPTQ with fp32
+        scales and zero offset 0, as `_quantize_head` does (`webtorch/llm.py:594-602`)."""
+        qw, qz, sc, K, N = core.gptq_quantize(self.embed, self.gs, self.bits, from_out_in=True)
+        return _Lin({"qweight": qw, "qzeros": qz, "scales": sc}, K, self.gs, self.bits, 0.0)
+
+    def _alloc(self):
+        dev, f32, T = core.device(), torch.float32, self.lmax
+        z = lambda *s: torch.zeros(s, dtype=f32, device=dev)  # noqa: E731
+        qkvd = (self.NH + 2 * self.NKV) * self.HD
+        self.buf = {"h": z(T, self.H), "xn": z(T, self.H), "qkv": z(T, qkvd), "q": z(T, self.NH * self.HD),
+                    "att": z(T, self.NH * self.HD), "gu": z(T, 2 * self.I), "act": z(T, self.I), "tmp": z(T, self.H),
+                    "hl": z(1, self.H), "logits": z(1, self.V)}
+        self.kc = torch.zeros((self.L, self.NKV, self.lmax, self.HD), dtype=f32, device=dev)
+        self.vc = torch.zeros_like(self.kc)
+        self.ids = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.history = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.state = torch.zeros(_lib.lib().miq_decode_state_words(), dtype=torch.int32, device=dev)
+        # one split-K workspace sized for every projection at T = 1 and at the largest prefill
+        need = core.gemv_workspace_bytes(1, self.head.K, self.head.N, self.gs, self.bits, _lib.MIQ_F32)
+        for M in (1, T):  # the head only ever sees the last token
+            for lin in [self.layers[0][k] for k in ("qkv", "o", "gate_up", "down")]:
+                need = max(need, core.gemv_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits, _lib.MIQ_F32))
+        self.ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+
+    # ---- one forward over T tokens at the device position ----
+    def _linear(self, lin, x, out, bias=None):
+        core._gptq_matmul(x, lin.qweight, lin.qzeros, lin.scales, lin.K, lin.N, lin.gs, lin.bits, lin.zoff,
+                          bias=lin.bias if bias is None else bias, out=out, ws=self.ws)
+
+    def _step(self, T):
+        """T tokens (ids[:T]) at positions state[0].. -> next token on the device
+        (`_kv_forward`, `webtorch/llm.py:1619-1636`)."""
+        b, st = self.buf, stream_handle()
+        H, NH, NKV, HD, I = self.H, self.NH, self.NKV, self.HD, self.I
+        h, xn = b["h"][:T], b["xn"][:T]
+        _lib.call("miq_embed", ptr(self.ids), ptr(self.embed), ptr(h), T, H, self.V, st)
+        scale = 1.0 / math.sqrt(HD)
+        for i, lay in enumerate(self.layers):
+            _lib.call("miq_rmsnorm", ptr(h), ptr(lay["in_ln"]), ptr(xn), T, H, self.eps, st)
+            self._linear(lay["qkv"], xn, b["qkv"][:T])
+            _lib.call("miq_rope_kv", ptr(b["qkv"]), ptr(self.state), ptr(b["q"]), ptr(self.kc[i]), ptr(self.vc[i]), T,
+                      NH, NKV, HD, self.lmax, self.theta, st)
+            _lib.call("miq_attention", ptr(b["q"]), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.state), ptr(b["att"]), T,
+                      NH, NKV, HD, self.lmax, scale, st)
+            self._residual(lay["o"], b["att"][:T], h, T)
+            _lib.call("miq_rmsnorm", ptr(h), ptr(lay["post_ln"]), ptr(xn), T, H, self.eps, st)
+            self._linear(lay["gate_up"], xn, b["gu"][:T])
+            _lib.call("miq_silu_mul", ptr(b["gu"]), ptr(b["act"]), T, I, st)
+            self._residual(lay["down"], b["act"][:T], h, T)
+        _lib.call("miq_rmsnorm", ptr(h[T - 1:T]), ptr(self.final_norm), ptr(b["hl"]), 1, H, self.eps, st)
+        self._linear(self.head, b["hl"], b["logits"])
+        _lib.call("miq_argmax_advance", ptr(b["logits"]), self.V, ptr(self.ids), ptr(self.history), self.lmax,
+                  ptr(self.state), T, st)
+
+    def _residual(self, lin, x, h, T):
+        """h += x @ W: fused into the GEMV (bias = out = h) for one token, an add otherwise."""
+        if T == 1 and lin.bias is None:
+            self._linear(lin, x, h, bias=h)
+        else:
+            tmp = self.buf["tmp"][:T]
+            self._linear(lin, x, tmp)
+            _lib.call("miq_add", ptr(h), ptr(tmp), T * self.H, stream_handle())
+
+    # ---- capture-replay ----
+    def capture(self):
+        """Record one decode step (T = 1) as a HIP graph (`beginCapture`/`endCapture`,
+        `webgpu/wgpy_backends/webgpu/platform.py:45-56`). Nothing in it depends on the host."""
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._step(1)
+        self._graph = g
+        return g
+
+    def reset(self):
+        self.state.zero_()
+        self.history.zero_()
+
+    def _plan_length(self, n_prompt, max_new):
+        """Refuse sequences that do not fit the KV cache (`webtorch/llm.py:1397-1429`)."""
+        if n_prompt < 1 or max_new < 1:
+            raise ValueError("need at least one prompt token and one new token")
+        if n_prompt + max_new > self.lmax:
+            raise ValueError("prompt (%d) + max_new (%d) exceeds lmax %d" % (n_prompt, max_new, self.lmax))
+
+    def generate(self, ids, max_new, use_graph=True):
+        """Greedy decode with no end token (`webtorch/llm.py:1716-1817` with do_sample off):
+        prefill the prompt, then max_new - 1 decode steps. Returns a GenResult whose `tokens`
+        are the max_new generated ids."""
+        ids = [int(i) for i in ids]
+        self._plan_length(len(ids), max_new)
+        self.reset()
+        self.ids[:len(ids)].copy_(torch.tensor(ids, dtype=torch.int32))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self._step(len(ids))
+        torch.cuda.synchronize()
+        ttft = time.perf_counter() - t0
+        if use_graph and self._graph is None and max_new > 1:
+            self.capture()
+        t1 = time.perf_counter()
+        for _ in range(max_new - 1):
+            if use_graph:
+                self._graph.replay()
+            else:
+                self._step(1)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t1
+        toks = [int(t) for t in self.history[:max_new].cpu().numpy()]
+        rate = (max_new - 1) / dt if max_new > 1 and dt > 0 else 0.0
+        return GenResult("", toks, ttft, rate)
