@@ -3,21 +3,19 @@
 
     python bench.py [--steps K] [--warmup W] [--no-cpu]
 
-Workload (one "step"): every int4 GPTQ GEMV of one decode token of a Qwen2-0.5B-shaped model
-(hidden 896, 14/2 heads of 64, intermediate 4864, vocab 151936, group size 128), M = 1,
-fp16 activations:
-  24 layers x {qkv 896->1152 (+ fp32 bias), o 896->896, gate_up 896->9728, down 4864->896}
-  + the tied head 896->151936 (fp32 scales, zero offset 0, as the head re-quantization makes it).
-q/k/v and gate/up share their input, so each pair or triple runs as one GEMV over the
-concatenated columns (per-column groups make that identical to separate layers). The weights
-(random bits, synthetic) sit in HBM before timing; two distinct copies of the whole set
-(~522 MB, more than the 256 MB Infinity Cache) alternate between steps so every step
-streams from HBM. Each step is one HIP graph replay on the current stream.
+Workload: greedy decode of a random-init Qwen2-0.5B-shaped int4 GPTQ model (24 layers, hidden
+896, 14/2 heads of 64, intermediate 4864, vocab 151936, group size 128, tied head re-quantized
+on the device) with the library's decode engine. A "step" is one decode token: one replay of
+the captured graph (embedding, 24 layers, head GEMV, device argmax), after a 64-token prefill.
+The weights (synthetic, seeded) are in HBM before timing.
 
-The JSON line reports `value` = algorithmic bytes of the step's GEMVs / step time (GB/s);
-`roofline` for the GEMV kernel (the only kernel of the step); per-shape timings; the GGUF
-Q4_K GEMV at the Llama-3-8B up_proj shape; and `cpu_baseline`: the reference's numpy
-fallback (restated in `oracle/`) timed on this host on a bounded sample of the same GEMVs.
+The JSON line reports `value` = algorithmic bytes of the step's int4 GEMVs (every weight of the
+model once per token) / step time, in GB/s, plus decode tokens/s; `roofline` for the GEMV kernel
+measured on the same 97 GEMVs per token replayed alone over two alternating weight copies
+(522 MB, above the 256 MB Infinity Cache, so from HBM); per-shape GEMV timings; the GGUF Q4_K
+GEMV (Llama-3-8B up_proj), the act-order prefill GEMM (K = N = 4096) and the Qwen3-MoE expert
+block; and `cpu_baseline`: the reference's numpy fallback (restated in `oracle/`) timed on
+this host on a bounded sample of the same GEMVs.
 """
 import argparse
 import json
@@ -131,6 +129,29 @@ def gemm_bench(torch, core, Ms=(16, 128, 512), copies=32, reps=32):
     return res
 
 
+def moe_bench(torch, core, reps=8):
+    """Qwen3-MoE block: T=256 tokens of hidden 2048, 128 experts (gate/up 2048->768, down
+    768->2048, int4 gs=128), top-8; routing + grouped GEMMs + combine on the device."""
+    from webpytorch_amd import synth
+    w = synth.moe_workload(3)
+    ex = core.MoEExperts(w["experts"])
+    x = torch.from_numpy(w["x"]).cuda()
+    lg = torch.from_numpy(w["logits"]).cuda()
+
+    def run():
+        for _ in range(reps):
+            ex(x, lg, 8)
+    run()
+    torch.cuda.synchronize()
+    g = capture(torch, run)
+    t = timed(torch, g.replay, 5) / reps
+    nbytes = 128 * 3 * gemv_bytes(2048, 768, "f16", False)
+    flops = 256 * 8 * 2 * (2 * 2048 * 768 + 768 * 2048)
+    del g
+    return {"us": round(t * 1e6, 2), "weight_GBs": round(nbytes / t / 1e9, 1),
+            "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "TFLOPs": round(flops / t / 1e12, 1)}
+
+
 def cpu_baseline(seconds=10.0):
     """The reference's numpy-fallback GEMV path (`_gptq_matmul_np`, restated in oracle/) on a
     bounded sample: one decoder layer's seven linears (q, k, v, o, gate, up, down as separate
@@ -174,32 +195,17 @@ def cpu_baseline(seconds=10.0):
                           len(times), t * 1e3, nbytes)}
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    a = ap.parse_args()
-    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the quantized-linear path has no multi-GPU mode here "
-              "(column/expert sharding is a design note only); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-    from webpytorch_amd import core
-    torch.cuda.set_device(0)
-    torch.manual_seed(0)
-
+def gemv_only(torch, core, steps):
+    """The step's 97 int4 GEMVs alone (no other kernels), over two alternating weight copies:
+    the roofline measurement of the GEMV kernel, and per-shape timings."""
     copies = []
     for c in range(2):
         layers = [{k: make_layer(torch, K, N, sdt, b) for k, (K, N, sdt, _, b) in SHAPES.items() if k != "head"}
                   for _ in range(LAYERS)]
         K, N, sdt, _, b = SHAPES["head"]
         copies.append((layers, make_layer(torch, K, N, sdt, b)))
-    xs = {k: torch.randn((1, K), device="cuda").half() for k, (K, *_r) in SHAPES.items()}
-    ys = {k: torch.empty((1, N), device="cuda", dtype=torch.float16) for k, (K, N, *_r) in SHAPES.items()}
+    xs = {k: torch.randn((1, K), device="cuda") for k, (K, *_r) in SHAPES.items()}
+    ys = {k: torch.empty((1, N), device="cuda") for k, (K, N, *_r) in SHAPES.items()}
 
     def gemv(name, w):
         K, N, sdt, zoff, _ = SHAPES[name]
@@ -212,31 +218,21 @@ def main():
             for name in ("qkv", "o", "gate_up", "down"):
                 gemv(name, lay[name])
         gemv("head", head)
-
-    launches = LAYERS * 4 + 1
-    step_bytes = sum(LAYERS * gemv_bytes(K, N, sdt, b) for k, (K, N, sdt, _, b) in SHAPES.items() if k != "head")
-    step_bytes += gemv_bytes(*[SHAPES["head"][i] for i in (0, 1, 2, 4)])
     for c in range(2):
         step(c)
     torch.cuda.synchronize()
     graphs = [capture(torch, lambda c=c: step(c)) for c in range(2)]
-
-    for i in range(a.warmup):
+    for i in range(4):
         graphs[i % 2].replay()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for i in range(a.steps):
+    ev0.record()
+    for i in range(steps):
         graphs[i % 2].replay()
-    ev1.record(stream)
+    ev1.record()
     ev1.synchronize()
-    torch.cuda.synchronize()
-    t_step = ev0.elapsed_time(ev1) * 1e-3 / a.steps
-    value = step_bytes / t_step / 1e9
-    per_launch = t_step / launches
-
-    # per-shape sustained time: graphs of back-to-back launches of one shape over 48 copies
+    t = ev0.elapsed_time(ev1) * 1e-3 / steps
+    del graphs
     kernels = {}
     for name, (K, N, sdt, zoff, b) in SHAPES.items():
         ws = [copies[c][0][l][name] for c in range(2) for l in range(LAYERS)] if name != "head" else \
@@ -247,30 +243,80 @@ def main():
             for i in range(reps):
                 gemv(name, ws[i % len(ws)])
         g = capture(torch, run)
-        t = timed(torch, g.replay, 5) / reps
+        tt = timed(torch, g.replay, 5) / reps
         nb = gemv_bytes(K, N, sdt, b)
-        kernels[name] = {"K": K, "N": N, "bytes": nb, "us": round(t * 1e6, 3), "GBs": round(nb / t / 1e9, 1)}
+        kernels[name] = {"K": K, "N": N, "bytes": nb, "us": round(tt * 1e6, 3), "GBs": round(nb / tt / 1e9, 1)}
         del g
-    q4k = q4k_bench(torch, core)
-    gemm = gemm_bench(torch, core)
+    return t, kernels
 
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extras", action="store_true", help="only the decode step and its roofline")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the quantized-linear path has no multi-GPU mode here "
+              "(column/expert sharding is a design note only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from webpytorch_amd import core, llm, synth
+    torch.cuda.set_device(0)
+    torch.manual_seed(0)
+
+    prompt = 64
+    lmax = max(256, prompt + a.warmup + a.steps + 2)
+    m = llm.CausalLM.from_weights(synth.decoder_weights(5, **synth.QWEN2_05B), lmax=lmax)
+    ids = synth.prompt_ids(5, prompt, synth.QWEN2_05B["V"])
+    r = m.generate(ids, 2)  # prefill + one step; captures the decode graph
+    g = m._graph
+    for _ in range(a.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(a.steps):
+        g.replay()
+    ev1.record(stream)
+    ev1.synchronize()
+    torch.cuda.synchronize()
+    t_step = ev0.elapsed_time(ev1) * 1e-3 / a.steps
+    launches = LAYERS * 4 + 1
+    step_bytes = sum(LAYERS * gemv_bytes(K, N, sdt, b) for k, (K, N, sdt, _, b) in SHAPES.items() if k != "head")
+    step_bytes += gemv_bytes(*[SHAPES["head"][i] for i in (0, 1, 2, 4)])
+    value = step_bytes / t_step / 1e9
+
+    t_gemv, kernels = gemv_only(torch, core, a.steps)
+    achieved = step_bytes / t_gemv / 1e9
     res = {
         "metric": "int4 GEMV achieved HBM GB/s (% of peak) + decode tokens/s, Qwen2-0.5B shape",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(t_step * 1e3, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int4 weights, fp16 activations, fp32 accumulate", "data": "synthetic",
-        "config": {"workload": "Qwen2-0.5B int4 GPTQ decode-step GEMVs, M=1: 24 x {qkv 896->1152, "
-                               "o 896->896, gate_up 896->9728, down 4864->896} + head 896->151936; gs=128; "
-                               "2 alternating weight copies (522 MB)",
-                   "launches_per_step": launches, "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "miq::gptq_gemv_kernel", "avg_launch_us": round(per_launch * 1e6, 3),
+        "vs_baseline": None, "dtype": "int4 weights, fp32 activations, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "greedy decode, random-init Qwen2-0.5B-shaped int4 GPTQ model (24 layers, "
+                               "hidden 896, 14/2 heads, intermediate 4864, vocab 151936, gs=128), 64-token "
+                               "prompt; one step = one decode token (captured graph replay)",
+                   "gemv_bytes_per_token": step_bytes, "gemv_launches_per_token": launches},
+        "decode_tokens_per_s": round(1.0 / t_step, 1),
+        "ttft_ms": round(r.ttft_s * 1e3, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "miq::gptq_gemv_kernel",
+                     "measured_on": "the 97 GEMVs of a token alone, 2 alternating weight copies (522 MB)",
+                     "avg_launch_us": round(t_gemv / launches * 1e6, 3),
                      "avg_bytes_per_launch": step_bytes // launches},
         "gemv_shapes": kernels,
-        "q4k_gemv_llama3_8b_up": q4k,
-        "gptq_gemm_act_order_4096": gemm,
     }
+    if not a.no_extras:
+        res["q4k_gemv_llama3_8b_up"] = q4k_bench(torch, core)
+        res["gptq_gemm_act_order_4096"] = gemm_bench(torch, core)
+        res["moe_qwen3_t256"] = moe_bench(torch, core)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
     print(json.dumps(res), flush=True)
