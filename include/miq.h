@@ -84,6 +84,22 @@ int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, const int32_t
                   void* out, int out_dtype, int M, int K, int N, int gs, int bits,
                   float zero_offset, void* workspace, size_t workspace_bytes, void* stream);
 
+/* input transforms of miq_gptq_gemv_fused */
+#define MIQ_X_PLAIN 0   /* x as given */
+#define MIQ_X_RMSNORM 1 /* x[m] / sqrt(mean(x[m]^2) + eps) * norm_w, over the full K */
+#define MIQ_X_SWIGLU 2  /* x rows hold [gate | up] (2K values): silu(gate) * up */
+
+/* Decode GEMV with the preceding elementwise step fused into the activation staging:
+ * out[M][N] = T(x) @ W + bias for fp32 x and out (M == 1 for the fused modes, int4), with T the
+ * x_mode transform. Same weight, workspace and bias rules as miq_gptq_gemv (bias may alias out).
+ * Replaces: `_rms` + `_qkv` / `_mlp` of the decode step (webtorch/llm.py:1259-1268, 1489-1519),
+ * each an RMSNorm or SwiGLU dispatch followed by a `_gptq_matmul`. */
+int miq_gptq_gemv_fused(const float* x, int x_mode, const float* norm_w, float eps, const int32_t* perm,
+                        const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                        int scales_dtype, const float* bias, float* out, int M, int K, int N, int gs,
+                        int bits, float zero_offset, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 /* Bytes of workspace miq_gptq_gemm needs (0 if none); same contract as
  * miq_gptq_gemv_workspace (zeroed counters first, not shared by concurrent calls). */
 int miq_gptq_gemm_workspace(int M, int K, int N, int gs, int bits, size_t* bytes);
@@ -179,14 +195,24 @@ int miq_embed(const int32_t* ids, const void* embed, float* out, int T, int H, i
  * Replaces: `CausalLM._rms` (webtorch/llm.py:1259-1268) and `rmsnorm` (webtorch/_core.py:2234-2263). */
 int miq_rmsnorm(const float* x, const float* w, float* out, int T, int H, float eps, void* stream);
 
-/* Rotate-half RoPE (theta, float64 angles rounded to fp32) at positions state[0] + t of the
- * fused q|k|v rows qkv [T][(NH + 2 NKV) HD]; q to q_out [T][NH][HD]; k, v written into the
- * caches [NKV][LMAX][HD] at their positions (positions >= LMAX are dropped).
+/* Rotate-half RoPE at positions state[0] + t of the fused q|k|v rows qkv [T][(NH + 2 NKV) HD]
+ * with the fp32 tables cos_tab / sin_tab [LMAX][HD/2] (cos/sin of pos * theta^(-2i/HD) in
+ * float64, rounded once); q to q_out [T][NH][HD]; k, v written into the caches
+ * [NKV][LMAX][HD] at their positions (positions >= LMAX are dropped).
  * Replaces: `_rope_np`, `_rot` and the rope step of `_kv_forward` (webtorch/llm.py:1270-1304,
  * 1626-1627), `rope_decode` (webtorch/_core.py:2302-2330) and `kv_write`
  * (webtorch/_core.py:1504-1540). */
-int miq_rope_kv(const float* qkv, const int32_t* state, float* q_out, float* kcache, float* vcache,
-                int T, int NH, int NKV, int HD, int LMAX, double theta, void* stream);
+int miq_rope_kv(const float* qkv, const int32_t* state, const float* cos_tab, const float* sin_tab,
+                float* q_out, float* kcache, float* vcache, int T, int NH, int NKV, int HD, int LMAX,
+                void* stream);
+
+/* One decode token (T = 1): RoPE of q and of the new k from the fused row qkv, the new k and v
+ * written into the caches at state[0], and attention over positions 0..state[0]; out [NH][HD].
+ * Replaces: the per-token `_rope1` x2 + `kv_write` x2 + `gqa_attention` of `_decode_fwd`
+ * (webtorch/llm.py:1591-1616; webtorch/_core.py:1319-1340, 1504-1540, 2302-2330). */
+int miq_attention_decode(const float* qkv, const int32_t* state, const float* cos_tab,
+                         const float* sin_tab, float* kcache, float* vcache, float* out, int NH,
+                         int NKV, int HD, int LMAX, float scale, void* stream);
 
 /* Causal GQA attention: token t (position state[0] + t) of head h attends to cache positions
  * 0..state[0] + t of kv head h / (NH / NKV); out [T][NH][HD] fp32.

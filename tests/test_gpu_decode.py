@@ -41,7 +41,11 @@ def test_rmsnorm_rope_silu_match_oracle(gpu):
     kc = torch.zeros((NKV, LMAX, HD), device="cuda")
     vc = torch.zeros_like(kc)
     qkvd, st = torch.from_numpy(qkv).cuda(), _state(torch, pos)
-    _lib.call("miq_rope_kv", ptr(qkvd), ptr(st), ptr(q), ptr(kc), ptr(vc), T, NH, NKV, HD, LMAX, 1e6, None)
+    ct, stab = o.rope_tables(0, LMAX)
+    cos_t = torch.from_numpy(np.ascontiguousarray(ct[:, :HD // 2])).cuda()
+    sin_t = torch.from_numpy(np.ascontiguousarray(stab[:, :HD // 2])).cuda()
+    _lib.call("miq_rope_kv", ptr(qkvd), ptr(st), ptr(cos_t), ptr(sin_t), ptr(q), ptr(kc), ptr(vc), T, NH, NKV, HD,
+              LMAX, None)
     cos, sin = o.rope_tables(pos, T)
     qr = qkv[:, :NH * HD].reshape(T, NH, HD).transpose(1, 0, 2)
     kr = qkv[:, NH * HD:(NH + NKV) * HD].reshape(T, NKV, HD).transpose(1, 0, 2)
@@ -84,6 +88,41 @@ def test_attention_matches_oracle(gpu, pos, T):
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("pos", [0, 5, 37])
+def test_attention_decode_fused_rope_kv(gpu, pos):
+    """The one-token attention (RoPE + KV write + attention in one launch) against the oracle's
+    rope, cache append and attention."""
+    import torch
+    from webpytorch_amd import _lib
+    from webpytorch_amd.core import ptr
+    NH, NKV, HD, LMAX = 14, 2, 64, 64
+    o = decode.Qwen2Oracle(synth.decoder_weights(1, L=1, H=128, NH=2, NKV=1, HD=64, I=128, V=64, gs=64), lmax=LMAX)
+    rng = np.random.default_rng(pos)
+    kc = rng.standard_normal((NKV, LMAX, HD)).astype(np.float32)
+    vc = rng.standard_normal((NKV, LMAX, HD)).astype(np.float32)
+    qkv = rng.standard_normal((1, (NH + 2 * NKV) * HD)).astype(np.float32)
+    ct, stab = o.rope_tables(0, LMAX)
+    cos_t = torch.from_numpy(np.ascontiguousarray(ct[:, :HD // 2])).cuda()
+    sin_t = torch.from_numpy(np.ascontiguousarray(stab[:, :HD // 2])).cuda()
+    kd, vd, qd, st = (torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda(), torch.from_numpy(qkv).cuda(),
+                      _state(torch, pos))
+    out = torch.empty((1, NH * HD), device="cuda")
+    scale = 1.0 / math.sqrt(HD)
+    _lib.call("miq_attention_decode", ptr(qd), ptr(st), ptr(cos_t), ptr(sin_t), ptr(kd), ptr(vd), ptr(out), NH, NKV, HD,
+              LMAX, scale, None)
+    cos, sin = o.rope_tables(pos, 1)
+    q = qkv[:, :NH * HD].reshape(1, NH, HD).transpose(1, 0, 2)
+    k = qkv[:, NH * HD:(NH + NKV) * HD].reshape(1, NKV, HD).transpose(1, 0, 2)
+    v = qkv[:, (NH + NKV) * HD:].reshape(1, NKV, HD).transpose(1, 0, 2)
+    q = q * cos + o.rot(q) * sin
+    k = k * cos + o.rot(k) * sin
+    kref, vref = kc.copy(), vc.copy()
+    kref[:, pos:pos + 1], vref[:, pos:pos + 1] = k, v
+    assert np.array_equal(kd.cpu().numpy(), kref) and np.array_equal(vd.cpu().numpy(), vref)
+    ref = o.attend(q, kref[:, :pos + 1], vref[:, :pos + 1], None, scale).transpose(1, 0, 2).reshape(1, NH * HD)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+
+
 def test_argmax_first_index_and_state(gpu):
     import torch
     from webpytorch_amd import _lib
@@ -116,6 +155,9 @@ def test_decode_matches_reference_golden_small(gpu):
     m, ids, _ = _engine(g, int(g["lmax"]))
     want = [int(t) for t in g["tokens"]]
     assert m.generate(ids, int(g["max_new"]), use_graph=False).tokens == want
+    m.fused = False  # the unfused one-token path (separate RMSNorm / RoPE / SwiGLU launches)
+    assert m.generate(ids, int(g["max_new"]), use_graph=False).tokens == want
+    m.fused = True
     assert m.generate(ids, int(g["max_new"]), use_graph=True).tokens == want
     assert m.generate(ids, int(g["max_new"]), use_graph=True).tokens == want  # graph reused
 

@@ -11,6 +11,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmiq.so")
 
 MIQ_F32, MIQ_F16 = 0, 1
+MIQ_X_PLAIN, MIQ_X_RMSNORM, MIQ_X_SWIGLU = 0, 1, 2
 ERRORS = {-1: ValueError, -2: ValueError, -3: NotImplementedError, -4: RuntimeError}
 
 _p, _i, _f, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_size_t
@@ -22,6 +23,7 @@ SIGNATURES = {
     "miq_gptq_repack_rows": [_p, _p, _p, _i, _i, _i, _p],
     "miq_gptq_gemv_workspace": [_i, _i, _i, _i, _i, _i, _p],
     "miq_gptq_gemv": [_p, _i, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
+    "miq_gptq_gemv_fused": [_p, _i, _p, _f, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
     "miq_gptq_gemm_workspace": [_i, _i, _i, _i, _i, _p],
     "miq_gptq_gemm": [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
     "miq_gptq_quantize": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p],
@@ -32,7 +34,8 @@ SIGNATURES = {
     "miq_moe_combine": [_p, _p, _i, _i, _i, _p, _i, _p],
     "miq_embed": [_p, _p, _p, _i, _i, _i, _p],
     "miq_rmsnorm": [_p, _p, _p, _i, _i, _f, _p],
-    "miq_rope_kv": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _d, _p],
+    "miq_rope_kv": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "miq_attention_decode": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _p],
     "miq_attention": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _p],
     "miq_silu_mul": [_p, _p, _i, _i, _p],
     "miq_add": [_p, _p, _i64, _p],

@@ -7,6 +7,9 @@
 // work between tokens: the argmax writes the next token id, appends it to the history and
 // advances the position.
 //
+// RoPE uses a cos/sin table [LMAX][HD/2] that the host builds once exactly as the reference
+// does (float64 angles, rounded once to fp32), so both sides rotate with identical numbers.
+//
 // Decode state (int32 words): [0] position of the next token, [1] tokens generated,
 // [2] argmax arrival counter (zero between calls), [3] last token id, then per argmax
 // workgroup its (value bits, index) partial.
@@ -49,39 +52,109 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   for (int c = threadIdx.x; c < H; c += 256) o[c] = (xr[c] / r) * w[c];
 }
 
-// Rotate-half RoPE at positions pos0 + t (pos0 read from the device), float64 angles rounded to
-// fp32 cos/sin, then x*cos + rot(x)*sin with separate fp32 roundings. q goes to q_out
-// [T][NH][HD]; k and v go into the caches [NKV][LMAX][HD] at their positions (positions past
-// LMAX are not written).
+// Rotate-half RoPE at positions pos0 + t (pos0 read from the device) with the fp32 cos/sin
+// table [LMAX][HD/2] (float64 angles rounded once, as the reference builds it), then
+// x*cos + rot(x)*sin rounded like the numpy expression. q goes to q_out [T][NH][HD]; k and v
+// go into the caches [NKV][LMAX][HD] at their positions (positions past LMAX are not written).
+__device__ __forceinline__ float rope1(const float* row, int d, int half, float c, float s) {
+  const float rv = d < half ? -row[d + half] : row[d - half];
+  return row[d] * c + rv * s;
+}
+
 __global__ __launch_bounds__(256) void rope_kv_kernel(const float* __restrict__ qkv, const int32_t* __restrict__ state,
+                                                      const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                                                       float* __restrict__ q_out, float* __restrict__ kc,
-                                                      float* __restrict__ vc, int NH, int NKV, int HD, int LMAX,
-                                                      double theta) {
+                                                      float* __restrict__ vc, int NH, int NKV, int HD, int LMAX) {
   const int t = blockIdx.y;
   const int pos = state[0] + t;
+  if (pos >= LMAX) return;
   const int W = (NH + 2 * NKV) * HD;
   const float* row = qkv + (size_t)t * W;
   const int half = HD / 2;
   for (int i = threadIdx.x; i < W; i += 256) {
     const int head = i / HD, d = i - head * HD;
     if (head >= NH + NKV) {  // v: copied into the cache
-      const int kv = head - NH - NKV;
-      if (pos < LMAX) vc[((size_t)kv * LMAX + pos) * HD + d] = row[i];
+      vc[((size_t)(head - NH - NKV) * LMAX + pos) * HD + d] = row[i];
       continue;
     }
     const int j = d < half ? d : d - half;
-    const double inv = 1.0 / pow(theta, (double)(2 * j) / (double)HD);
-    const double ang = (double)pos * inv;
-    const float c = (float)cos(ang), s = (float)sin(ang);
-    const float xv = row[i];
-    const float rv = d < half ? -row[i + half] : row[i - half];
-    const float y = xv * c + rv * s;
-    if (head < NH) {
-      q_out[((size_t)t * NH + head) * HD + d] = y;
-    } else if (pos < LMAX) {
-      kc[((size_t)(head - NH) * LMAX + pos) * HD + d] = y;
+    const float y = rope1(row + head * HD, d, half, cos_t[(size_t)pos * half + j], sin_t[(size_t)pos * half + j]);
+    if (head < NH) q_out[((size_t)t * NH + head) * HD + d] = y;
+    else kc[((size_t)(head - NH) * LMAX + pos) * HD + d] = y;
+  }
+}
+
+// One decode token: RoPE of its q head and of the kv head's new k, the new k and v written
+// into the caches (by the first query head of each kv group), then attention over positions
+// 0..pos with the new position's k and v taken from LDS (the other workgroups of the group
+// may not have written them yet). A workgroup of 256 threads per query head: a thread per
+// position for the scores, then 4 waves over positions x 64 lanes over the head dimension
+// for the weighted sum, combined in wave order.
+__global__ __launch_bounds__(256) void attention_decode_kernel(
+    const float* __restrict__ qkv, const int32_t* __restrict__ state, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, float* __restrict__ kc, float* __restrict__ vc, float* __restrict__ out, int NH,
+    int NKV, int HD, int LMAX, float scale) {
+  extern __shared__ float sp[];  // [LMAX] scores -> probabilities
+  __shared__ float qs[256], kn[256], vn[256], red[4][256], wred[8];
+  const int h = blockIdx.x;
+  const int rep = NH / NKV, kv = h / rep;
+  const int pos = state[0];
+  const int half = HD / 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (pos >= LMAX) return;  // uniform: the caller never runs past its cache
+  const int S = pos + 1;
+  for (int d = tid; d < HD; d += 256) {
+    const int j = d < half ? d : d - half;
+    const float c = cos_t[(size_t)pos * half + j], s = sin_t[(size_t)pos * half + j];
+    qs[d] = rope1(qkv + h * HD, d, half, c, s);
+    kn[d] = rope1(qkv + (NH + kv) * HD, d, half, c, s);
+    vn[d] = qkv[(NH + NKV + kv) * HD + d];
+    if (h % rep == 0) {
+      kc[((size_t)kv * LMAX + pos) * HD + d] = kn[d];
+      vc[((size_t)kv * LMAX + pos) * HD + d] = vn[d];
     }
   }
+  __syncthreads();
+  const float* K = kc + (size_t)kv * LMAX * HD;
+  const float* Vv = vc + (size_t)kv * LMAX * HD;
+  float mx = -INFINITY;
+  for (int j = tid; j < S; j += 256) {
+    const float* kr = j == pos ? kn : K + (size_t)j * HD;
+    float a = 0.f;
+    for (int d = 0; d < HD; d += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+      a = fmaf(qs[d], k4.x, a);
+      a = fmaf(qs[d + 1], k4.y, a);
+      a = fmaf(qs[d + 2], k4.z, a);
+      a = fmaf(qs[d + 3], k4.w, a);
+    }
+    a *= scale;
+    sp[j] = a;
+    mx = fmaxf(mx, a);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) wred[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float sum = 0.f;
+  for (int j = tid; j < S; j += 256) {
+    const float e = expf(sp[j] - mx);
+    sp[j] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) wred[4 + wave] = sum;
+  __syncthreads();
+  sum = (wred[4] + wred[5]) + (wred[6] + wred[7]);
+  for (int j = tid; j < S; j += 256) sp[j] = sp[j] / sum;
+  __syncthreads();
+  for (int d = lane; d < HD; d += 64) {
+    float o = 0.f;
+    for (int j = wave; j < S; j += 4) o = fmaf(sp[j], j == pos ? vn[d] : Vv[(size_t)j * HD + d], o);
+    red[wave][d] = o;
+  }
+  __syncthreads();
+  for (int d = tid; d < HD; d += 256) out[(size_t)h * HD + d] = ((red[0][d] + red[1][d]) + red[2][d]) + red[3][d];
 }
 
 // Causal grouped-query attention: token t (position pos0 + t) of query head h attends to
@@ -187,14 +260,24 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ l
     __hip_atomic_store(part + 1, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
     is_last = __hip_atomic_fetch_add(state + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
-    if (is_last) {
-      float fv = -INFINITY;
-      int fi = 0x7fffffff;
-      for (int g = 0; g < (int)gridDim.x; ++g) {
-        const float v = __int_as_float(__hip_atomic_load(state + 4 + 2 * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        const int i = __hip_atomic_load(state + 5 + 2 * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (better(v, i, fv, fi)) { fv = v; fi = i; }
-      }
+  }
+  __syncthreads();
+  if (is_last && threadIdx.x < 64) {
+    // lane g loads workgroup g's partial (at most 64 workgroups), then a wave arg-max
+    float fv = -INFINITY;
+    int fi = 0x7fffffff;
+    const int g = threadIdx.x;
+    if (g < (int)gridDim.x) {
+      fv = __int_as_float(__hip_atomic_load(state + 4 + 2 * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      fi = __hip_atomic_load(state + 5 + 2 * g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(fv, o, 64);
+      const int oi = __shfl_xor(fi, o, 64);
+      if (better(ov, oi, fv, fi)) { fv = ov; fi = oi; }
+    }
+    if (threadIdx.x == 0) {
       if (fi >= V) fi = 0;  // all logits NaN
       ids[0] = fi;
       const int step = state[1];
@@ -230,15 +313,30 @@ extern "C" int miq_rmsnorm(const float* x, const float* w, float* out, int T, in
   return check_launch("rmsnorm");
 }
 
-extern "C" int miq_rope_kv(const float* qkv, const int32_t* state, float* q_out, float* kcache, float* vcache, int T,
-                           int NH, int NKV, int HD, int LMAX, double theta, void* stream) {
+extern "C" int miq_rope_kv(const float* qkv, const int32_t* state, const float* cos_tab, const float* sin_tab,
+                           float* q_out, float* kcache, float* vcache, int T, int NH, int NKV, int HD, int LMAX,
+                           void* stream) {
   MIQ_REQUIRE(T >= 0 && NH > 0 && NKV > 0 && NH % NKV == 0 && HD > 0 && HD % 2 == 0 && LMAX > 0, MIQ_ERR_INVALID,
               "rope_kv: T=%d NH=%d NKV=%d HD=%d LMAX=%d", T, NH, NKV, HD, LMAX);
   if (T == 0) return MIQ_OK;
-  MIQ_REQUIRE(qkv && state && q_out && kcache && vcache, MIQ_ERR_INVALID, "rope_kv: null pointer");
-  hipLaunchKernelGGL(rope_kv_kernel, dim3(1, T), dim3(256), 0, static_cast<hipStream_t>(stream), qkv, state, q_out,
-                     kcache, vcache, NH, NKV, HD, LMAX, theta);
+  MIQ_REQUIRE(qkv && state && cos_tab && sin_tab && q_out && kcache && vcache, MIQ_ERR_INVALID, "rope_kv: null pointer");
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(1, T), dim3(256), 0, static_cast<hipStream_t>(stream), qkv, state, cos_tab,
+                     sin_tab, q_out, kcache, vcache, NH, NKV, HD, LMAX);
   return check_launch("rope_kv");
+}
+
+extern "C" int miq_attention_decode(const float* qkv, const int32_t* state, const float* cos_tab, const float* sin_tab,
+                                    float* kcache, float* vcache, float* out, int NH, int NKV, int HD, int LMAX,
+                                    float scale, void* stream) {
+  MIQ_REQUIRE(NH > 0 && NKV > 0 && NH % NKV == 0 && HD > 0 && HD <= 256 && HD % 4 == 0 && LMAX > 0, MIQ_ERR_INVALID,
+              "attention_decode: NH=%d NKV=%d HD=%d LMAX=%d", NH, NKV, HD, LMAX);
+  MIQ_REQUIRE((size_t)LMAX * 4 <= 64 * 1024, MIQ_ERR_UNSUPPORTED, "attention_decode: LMAX=%d above 16384", LMAX);
+  MIQ_REQUIRE(qkv && state && cos_tab && sin_tab && kcache && vcache && out, MIQ_ERR_INVALID,
+              "attention_decode: null pointer");
+  MIQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), MIQ_ERR_ALIGN, "attention_decode: caches must be 16-byte aligned");
+  hipLaunchKernelGGL(attention_decode_kernel, dim3(NH), dim3(256), (size_t)LMAX * 4, static_cast<hipStream_t>(stream),
+                     qkv, state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV, HD, LMAX, scale);
+  return check_launch("attention_decode");
 }
 
 extern "C" int miq_attention(const float* q, const float* kcache, const float* vcache, const int32_t* state, float* out,

@@ -140,12 +140,15 @@ template <int RPW> struct GemvBatch {
   uint32_t z;  // raw packed zero word (shifted to this lane's columns when used)
 };
 
-template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT>
+// Input transforms applied while staging x (XMODE): none; RMSNorm of each row of x with
+// weight norm_w (x / sqrt(mean(x^2) + eps) * w, every workgroup recomputes the row's mean
+// square); SwiGLU of a [gate | up] row of 2K values (silu(gate) * up).
+template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT, int XMODE>
 __global__ __launch_bounds__(256) void gptq_gemv_kernel(
     const XT* __restrict__ x, const int32_t* __restrict__ perm, const uint32_t* __restrict__ qw,
     const uint32_t* __restrict__ qz, const ST* __restrict__ sc, const float* bias, OT* out,
     float* __restrict__ ws, int* __restrict__ counters, int M, int K, int N, int gs, float zoff, int rows_per_wg,
-    int ksplit) {
+    int ksplit, const float* __restrict__ norm_w, float eps) {
   using C = Codes<BITS>;
   constexpr int PER = C::PER, PAIRS = C::PAIRS;
   constexpr int BK = RPW * PER;
@@ -154,6 +157,7 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __shared__ int is_last;
+  __shared__ float ss_red[4][MR];
 
   const int W = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -183,7 +187,31 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
   int b = wave;
   if (colok && b < nb) load_batch(b, B);
 
-  // ---- stage x (through perm) in LDS and the per-batch sums of x ----
+  // ---- RMSNorm: mean square of every row of x over the full K ----
+  const int xstride = XMODE == 2 ? 2 * K : K;
+  float inv_r[MR];
+  if constexpr (XMODE == 1) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float ss = 0.f;
+      if (m0 + m < M)
+        for (int i = threadIdx.x; i < K; i += blockDim.x) {
+          const float v = to_f32(x[(size_t)(m0 + m) * K + i]);
+          ss += v * v;
+        }
+      ss = wave_sum(ss);
+      if (lane == 0) ss_red[wave][m] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float t = 0.f;
+      for (int w = 0; w < W; ++w) t += ss_red[w][m];
+      inv_r[m] = sqrtf(t / (float)K + eps);
+    }
+  }
+
+  // ---- stage x (through perm and the input transform) in LDS and the per-batch sums of x ----
   _Float16* xs_h = reinterpret_cast<_Float16*>(lds_raw);
   float* xs_f = reinterpret_cast<float*>(lds_raw);
   const size_t xs_bytes = ((size_t)MR * L * XB + 15) & ~(size_t)15;
@@ -196,12 +224,29 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
     const int k = r0 * PER + kk;
     float v[8];
     if (m0 + m < M) {
-      const XT* xr = x + (size_t)(m0 + m) * K;
+      const XT* xr = x + (size_t)(m0 + m) * xstride;
+      int idx[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) idx[j] = perm ? perm[k + j] : k + j;
       if (perm) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = to_f32(xr[perm[k + j]]);
+        for (int j = 0; j < 8; ++j) v[j] = to_f32(xr[idx[j]]);
       } else {
         load8(xr + k, v);
+      }
+      if constexpr (XMODE == 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (v[j] / inv_r[m]) * norm_w[idx[j]];
+      } else if constexpr (XMODE == 2) {
+        float u[8];
+        if (perm) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) u[j] = to_f32(xr[K + idx[j]]);
+        } else {
+          load8(xr + K + k, u);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (v[j] * (1.f / (1.f + expf(-v[j])))) * u[j];
       }
     } else {
 #pragma unroll
@@ -402,11 +447,11 @@ static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool ha
   return MIQ_OK;
 }
 
-template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT>
+template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT, int XMODE>
 static int launch_gemv(const GemvPlan& p, const void* x, const int32_t* perm, const int32_t* qw,
                        const int32_t* qz, const void* sc, const float* bias, void* out, void* ws,
-                       int M, int K, int N, int gs, float zoff, hipStream_t st) {
-  auto kern = gptq_gemv_kernel<BITS, MR, RPW, XT, ST, OT>;
+                       int M, int K, int N, int gs, float zoff, const float* norm_w, float eps, hipStream_t st) {
+  auto kern = gptq_gemv_kernel<BITS, MR, RPW, XT, ST, OT, XMODE>;
   int* counters = p.ksplit > 1 ? static_cast<int*>(ws) : nullptr;
   float* partials = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes) : nullptr;
   if (p.lds > 64 * 1024) {
@@ -422,7 +467,7 @@ static int launch_gemv(const GemvPlan& p, const void* x, const int32_t* perm, co
   hipLaunchKernelGGL(kern, grid, dim3(64 * p.waves), p.lds, st, static_cast<const XT*>(x), perm,
                      reinterpret_cast<const uint32_t*>(qw), reinterpret_cast<const uint32_t*>(qz),
                      static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, M, K, N,
-                     gs, zoff, p.rows_per_wg, p.ksplit);
+                     gs, zoff, p.rows_per_wg, p.ksplit, norm_w, eps);
   return check_launch("gptq_gemv");
 }
 
@@ -431,7 +476,7 @@ static int gemv_types(const GemvPlan& p, const void* x, int xd, const int32_t* p
                       const int32_t* qz, const void* sc, int sd, const float* bias, void* out, int od,
                       void* ws, int M, int K, int N, int gs, float zoff, hipStream_t st) {
 #define MIQ_GEMV_CASE(XT, ST, OT) \
-  return launch_gemv<BITS, MR, RPW, XT, ST, OT>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st)
+  return launch_gemv<BITS, MR, RPW, XT, ST, OT, 0>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, nullptr, 0.f, st)
   if (xd == MIQ_F16) {
     if (sd == MIQ_F16) { if (od == MIQ_F16) MIQ_GEMV_CASE(__half, __half, __half); MIQ_GEMV_CASE(__half, __half, float); }
     if (od == MIQ_F16) MIQ_GEMV_CASE(__half, float, __half);
@@ -454,6 +499,23 @@ static int gemv_dispatch(const GemvPlan& p, const void* x, int xd, const int32_t
   MIQ_GEMV_MR(1, 4); MIQ_GEMV_MR(4, 4); MIQ_GEMV_MR(8, 4);
 #undef MIQ_GEMV_MR
   return fail(MIQ_ERR_UNSUPPORTED, "gptq_gemv: no kernel for mr=%d rpw=%d", p.mr, p.rpw);
+}
+
+// Fused-input decode GEMV: one row of fp32 activations, fp32 output, int4, RMSNorm (XMODE 1) or
+// SwiGLU (XMODE 2) applied while staging.
+template <int XMODE>
+static int gemv_fused_dispatch(const GemvPlan& p, const void* x, const int32_t* perm, const int32_t* qw,
+                               const int32_t* qz, const void* sc, int sd, const float* bias, void* out, void* ws,
+                               int M, int K, int N, int gs, int bits, float zoff, const float* norm_w, float eps,
+                               hipStream_t st) {
+  MIQ_REQUIRE(p.mr == 1 && bits == 4, MIQ_ERR_UNSUPPORTED, "gptq_gemv_fused: one row of int4 only (M=%d bits=%d)",
+              M, bits);
+#define MIQ_GEMV_FUSED(RPW, ST) \
+  return launch_gemv<4, 1, RPW, float, ST, float, XMODE>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, norm_w, eps, st)
+  if (p.rpw == 8) { if (sd == MIQ_F16) MIQ_GEMV_FUSED(8, __half); MIQ_GEMV_FUSED(8, float); }
+  if (sd == MIQ_F16) MIQ_GEMV_FUSED(4, __half);
+  MIQ_GEMV_FUSED(4, float);
+#undef MIQ_GEMV_FUSED
 }
 
 int check_gptq_dims(const char* who, int K, int N, int gs, int bits) {
@@ -566,4 +628,33 @@ extern "C" int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, co
                             workspace, M, K, N, gs, zero_offset, st);
   return gemv_dispatch<8>(p, x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype,
                           workspace, M, K, N, gs, zero_offset, st);
+}
+
+extern "C" int miq_gptq_gemv_fused(const float* x, int x_mode, const float* norm_w, float eps, const int32_t* perm,
+                                   const int32_t* qweight, const int32_t* qzeros, const void* scales, int scales_dtype,
+                                   const float* bias, float* out, int M, int K, int N, int gs, int bits,
+                                   float zero_offset, void* workspace, size_t workspace_bytes, void* stream) {
+  if (x_mode == MIQ_X_PLAIN)
+    return miq_gptq_gemv(x, MIQ_F32, perm, qweight, qzeros, scales, scales_dtype, bias, out, MIQ_F32, M, K, N, gs,
+                         bits, zero_offset, workspace, workspace_bytes, stream);
+  MIQ_REQUIRE(x_mode == MIQ_X_RMSNORM || x_mode == MIQ_X_SWIGLU, MIQ_ERR_UNSUPPORTED, "gptq_gemv_fused: x_mode %d",
+              x_mode);
+  MIQ_REQUIRE(x_mode != MIQ_X_RMSNORM || norm_w, MIQ_ERR_INVALID, "gptq_gemv_fused: RMSNorm needs its weight");
+  int rc = gemv_check("gptq_gemv_fused", x, MIQ_F32, qweight, qzeros, scales, scales_dtype, out, MIQ_F32, M, K, N, gs,
+                      bits);
+  if (rc || M == 0) return rc;
+  GemvPlan p;
+  rc = gemv_plan(M, K, N, gs, bits, MIQ_F32, workspace != nullptr, &p);
+  if (rc) return rc;
+  if (p.ksplit > 1) {
+    MIQ_REQUIRE(workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
+                "gptq_gemv_fused: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes,
+                workspace_bytes);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (x_mode == MIQ_X_RMSNORM)
+    return gemv_fused_dispatch<1>(p, x, perm, qweight, qzeros, scales, scales_dtype, bias, out, workspace, M, K, N, gs,
+                                  bits, zero_offset, norm_w, eps, st);
+  return gemv_fused_dispatch<2>(p, x, perm, qweight, qzeros, scales, scales_dtype, bias, out, workspace, M, K, N, gs,
+                                bits, zero_offset, nullptr, 0.f, st);
 }

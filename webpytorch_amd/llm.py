@@ -72,8 +72,9 @@ class CausalLM:
     "in_ln", "post_ln"), the fp16 "embed" table (tied head), "final_norm" and "cfg"
     (L, H, NH, NKV, HD, I, V, gs, bits[, eps, theta])."""
 
-    def __init__(self, weights, lmax=256):
+    def __init__(self, weights, lmax=256, fused=True):
         c = weights["cfg"]
+        self.fused = bool(fused)  # one-token steps use the fused launches (else the prefill path)
         self.L, self.H, self.NH, self.NKV, self.HD = c["L"], c["H"], c["NH"], c["NKV"], c["HD"]
         self.I, self.V, self.gs, self.bits = c["I"], c["V"], c["gs"], c["bits"]
         self.eps = float(c.get("eps", 1e-6))
@@ -97,8 +98,8 @@ class CausalLM:
         self._graph = None
 
     @classmethod
-    def from_weights(cls, weights, lmax=256):
-        return cls(weights, lmax)
+    def from_weights(cls, weights, lmax=256, fused=True):
+        return cls(weights, lmax, fused)
 
     # ---- load-time ----
     def _quantize_head(self):
@@ -116,6 +117,11 @@ class CausalLM:
                     "hl": z(1, self.H), "logits": z(1, self.V)}
         self.kc = torch.zeros((self.L, self.NKV, self.lmax, self.HD), dtype=f32, device=dev)
         self.vc = torch.zeros_like(self.kc)
+        # RoPE tables exactly as `_rope_np` builds them (float64 angles, rounded once to fp32)
+        inv = 1.0 / (self.theta ** (np.arange(0, self.HD, 2, dtype=np.float64) / self.HD))
+        ang = np.arange(0, T, dtype=np.float64)[:, None] * inv[None, :]
+        self.cos_t = core.to_device(np.cos(ang).astype(np.float32))
+        self.sin_t = core.to_device(np.sin(ang).astype(np.float32))
         self.ids = torch.zeros(T, dtype=torch.int32, device=dev)
         self.history = torch.zeros(T, dtype=torch.int32, device=dev)
         self.state = torch.zeros(_lib.lib().miq_decode_state_words(), dtype=torch.int32, device=dev)
@@ -131,9 +137,37 @@ class CausalLM:
         core._gptq_matmul(x, lin.qweight, lin.qzeros, lin.scales, lin.K, lin.N, lin.gs, lin.bits, lin.zoff,
                           bias=lin.bias if bias is None else bias, out=out, ws=self.ws)
 
+    def _fused(self, lin, x, mode, norm_w, out, bias=None):
+        """One-token GEMV with RMSNorm (mode 1) or SwiGLU (mode 2) applied to x while staging."""
+        _lib.call("miq_gptq_gemv_fused", ptr(x), mode, ptr(norm_w), self.eps, None, ptr(lin.qweight),
+                  ptr(lin.qzeros), ptr(lin.scales), core.dtype_code(lin.scales), ptr(lin.bias if bias is None else bias),
+                  ptr(out), 1, lin.K, lin.N, lin.gs, lin.bits, float(lin.zoff), ptr(self.ws), self.ws.numel(),
+                  stream_handle())
+
+    def _decode_step(self):
+        """One token at position state[0] (`_decode_fwd`, `webtorch/llm.py:1591-1616`): five
+        launches per layer -- RMSNorm+qkv, RoPE+KV write+attention, o+residual, RMSNorm+gate|up,
+        SwiGLU+down+residual -- then RMSNorm+head and the device argmax."""
+        b, st = self.buf, stream_handle()
+        h = b["h"][:1]
+        _lib.call("miq_embed", ptr(self.ids), ptr(self.embed), ptr(h), 1, self.H, self.V, st)
+        scale = 1.0 / math.sqrt(self.HD)
+        for i, lay in enumerate(self.layers):
+            self._fused(lay["qkv"], h, _lib.MIQ_X_RMSNORM, lay["in_ln"], b["qkv"])
+            _lib.call("miq_attention_decode", ptr(b["qkv"]), ptr(self.state), ptr(self.cos_t), ptr(self.sin_t),
+                      ptr(self.kc[i]), ptr(self.vc[i]), ptr(b["att"]), self.NH, self.NKV, self.HD, self.lmax, scale, st)
+            self._linear(lay["o"], b["att"][:1], h, bias=h)
+            self._fused(lay["gate_up"], h, _lib.MIQ_X_RMSNORM, lay["post_ln"], b["gu"])
+            self._fused(lay["down"], b["gu"][:1], _lib.MIQ_X_SWIGLU, None, h, bias=h)
+        self._fused(self.head, h, _lib.MIQ_X_RMSNORM, self.final_norm, b["logits"])
+        _lib.call("miq_argmax_advance", ptr(b["logits"]), self.V, ptr(self.ids), ptr(self.history), self.lmax,
+                  ptr(self.state), 1, st)
+
     def _step(self, T):
         """T tokens (ids[:T]) at positions state[0].. -> next token on the device
         (`_kv_forward`, `webtorch/llm.py:1619-1636`)."""
+        if T == 1 and self.fused:
+            return self._decode_step()
         b, st = self.buf, stream_handle()
         H, NH, NKV, HD, I = self.H, self.NH, self.NKV, self.HD, self.I
         h, xn = b["h"][:T], b["xn"][:T]
@@ -142,8 +176,8 @@ class CausalLM:
         for i, lay in enumerate(self.layers):
             _lib.call("miq_rmsnorm", ptr(h), ptr(lay["in_ln"]), ptr(xn), T, H, self.eps, st)
             self._linear(lay["qkv"], xn, b["qkv"][:T])
-            _lib.call("miq_rope_kv", ptr(b["qkv"]), ptr(self.state), ptr(b["q"]), ptr(self.kc[i]), ptr(self.vc[i]), T,
-                      NH, NKV, HD, self.lmax, self.theta, st)
+            _lib.call("miq_rope_kv", ptr(b["qkv"]), ptr(self.state), ptr(self.cos_t), ptr(self.sin_t), ptr(b["q"]),
+                      ptr(self.kc[i]), ptr(self.vc[i]), T, NH, NKV, HD, self.lmax, st)
             _lib.call("miq_attention", ptr(b["q"]), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.state), ptr(b["att"]), T,
                       NH, NKV, HD, self.lmax, scale, st)
             self._residual(lay["o"], b["att"][:T], h, T)
