@@ -85,7 +85,10 @@ __global__ __launch_bounds__(256) void gptq_repack_kernel(const uint32_t* __rest
 #define MIQ_GEMV_MIN_WGS 1  // split K further while fewer workgroups than this would run
 #endif
 #ifndef MIQ_GEMV_MAX_WAVES
-#define MIQ_GEMV_MAX_WAVES 4  // waves per workgroup (256 threads)
+#define MIQ_GEMV_MAX_WAVES 16  // waves per workgroup (1024 threads)
+#endif
+#ifndef MIQ_GEMV_SPLIT_WAVES
+#define MIQ_GEMV_SPLIT_WAVES 4  // waves per workgroup when K is split across workgroups
 #endif
 constexpr int kGemvStageBytes = 64 * 1024;  // LDS for the staged activations (no workspace)
 
@@ -144,7 +147,7 @@ template <int RPW> struct GemvBatch {
 // weight norm_w (x / sqrt(mean(x^2) + eps) * w, every workgroup recomputes the row's mean
 // square); SwiGLU of a [gate | up] row of 2K values (silu(gate) * up).
 template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT, int XMODE>
-__global__ __launch_bounds__(256) void gptq_gemv_kernel(
+__global__ __launch_bounds__(64 * MIQ_GEMV_MAX_WAVES) void gptq_gemv_kernel(
     const XT* __restrict__ x, const int32_t* __restrict__ perm, const uint32_t* __restrict__ qw,
     const uint32_t* __restrict__ qz, const ST* __restrict__ sc, const float* bias, OT* out,
     float* __restrict__ ws, int* __restrict__ counters, int M, int K, int N, int gs, float zoff, int rows_per_wg,
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __shared__ int is_last;
-  __shared__ float ss_red[4][MR];
+  __shared__ float ss_red[MIQ_GEMV_MAX_WAVES][MR];
 
   const int W = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -182,10 +185,12 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
     B.z = qz[(size_t)g * NZ + n0 / PER];
   };
 
-  // ---- first batch of weights, issued before the activations are staged ----
-  GemvBatch<RPW> B;
-  int b = wave;
-  if (colok && b < nb) load_batch(b, B);
+  // ---- a wave's first two batches of weights, issued before the activations are staged ----
+  GemvBatch<RPW> B, B2;
+  const int b = wave;
+  const bool has1 = colok && b < nb, has2 = colok && b + W < nb;
+  if (has1) load_batch(b, B);
+  if (has2) load_batch(b + W, B2);
 
   // ---- RMSNorm: mean square of every row of x over the full K ----
   const int xstride = XMODE == 2 ? 2 * K : K;
@@ -273,7 +278,7 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.f;
 
-  auto compute = [&](int bb) {
+  auto compute = [&](int bb, const GemvBatch<RPW>& B) {
     float part[MR][4];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
@@ -331,12 +336,13 @@ __global__ __launch_bounds__(256) void gptq_gemv_kernel(
     }
   };
 
-  if (colok) {
-    while (b < nb) {
-      compute(b);
-      b += W;
-      if (b < nb) load_batch(b, B);
-    }
+  // straight-line code keeps both batches in flight (a loop makes the compiler wait on the
+  // prefetched one); further batches, if any, go one at a time
+  if (has1) compute(b, B);
+  if (has2) compute(b + W, B2);
+  for (int bb = b + 2 * W; colok && bb < nb; bb += W) {
+    load_batch(bb, B);
+    compute(bb, B);
   }
 
   // ---- fixed-order reduction of the W waves ----
@@ -418,10 +424,12 @@ static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool ha
   p->mblocks = (M + p->mr - 1) / p->mr;
   const int xb = x_dtype == MIQ_F16 ? 2 : 4;
   const int nbt = K / per / rpw;  // batches per column tile
-  const int wmax = MIQ_GEMV_MAX_WAVES;
+  const int wmax = MIQ_GEMV_SPLIT_WAVES;
   const int base = p->tiles * p->mblocks;
   int waves, ksplit;
-  if (have_ws && base <= kMaxCounters) {
+  // wide layers fill the chip by columns alone: no K split, each wave streams several batches
+  const bool wide = base >= 2 * kCUs && (size_t)p->mr * K * xb <= (size_t)kGemvStageBytes;
+  if (have_ws && base <= kMaxCounters && !wide) {
     // one batch per wave; fewer waves per workgroup while too few workgroups would run
     waves = nbt < wmax ? nbt : wmax;
     ksplit = (nbt + waves - 1) / waves;
@@ -430,7 +438,9 @@ static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool ha
       ksplit = (nbt + waves - 1) / waves;
     }
   } else {
-    waves = nbt < wmax ? nbt : wmax;
+    // every wave takes two batches (both in flight at once): ceil(batches / 2) waves
+    waves = (nbt + 1) / 2;
+    waves = waves > MIQ_GEMV_MAX_WAVES ? MIQ_GEMV_MAX_WAVES : waves;
     ksplit = 1;
     MIQ_REQUIRE((size_t)p->mr * K * xb <= (size_t)kGemvStageBytes, MIQ_ERR_INVALID,
                 "gptq_gemv: K=%d needs a workspace (see miq_gptq_gemv_workspace)", K);
