@@ -190,3 +190,46 @@ def test_generate_refuses_overlong(gpu):
     m, ids, _ = _engine(g, 20)
     with pytest.raises(ValueError, match="lmax"):
         m.generate(ids, 10)
+
+
+def test_decode_varied_tokens_vs_oracle(gpu):
+    """A model quantized from Gaussian weights, whose greedy tokens vary (the uniform-code
+    models settle on one token): 32 greedy ids identical to the oracle's (itself pinned to the
+    reference's CPU decode), eager fused, eager unfused and graph-replayed. Seed chosen so that
+    every step's top-1/top-2 logit gap is above 1% of the logits' spread."""
+    from webpytorch_amd import llm
+    sh = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+    w = synth.decoder_weights(14, gaussian=True, **sh)
+    ids = synth.prompt_ids(14, 16, sh["V"])
+    want, _ = decode.Qwen2Oracle(w, lmax=64).generate(ids, 32)
+    assert len(set(want)) >= 10
+    m = llm.CausalLM.from_weights(w, lmax=64)
+    assert m.generate(ids, 32, use_graph=False).tokens == want
+    m.fused = False
+    assert m.generate(ids, 32, use_graph=False).tokens == want
+    m.fused = True
+    assert m.generate(ids, 32).tokens == want
+
+
+def test_decode_full_shape_logits_vs_oracle(gpu):
+    """End-to-end config weights (Qwen2-0.5B shape, uniform codes): the logits after the 64-token
+    prefill and after one decode step against the oracle's, elementwise."""
+    import torch
+    from webpytorch_amd import llm
+    w = synth.decoder_weights(5, **synth.QWEN2_05B)
+    ids = synth.prompt_ids(5, 64, synth.QWEN2_05B["V"])
+    o = decode.Qwen2Oracle(w, lmax=128)
+    cache = [None] * o.L
+    n1, l1 = o.forward(list(ids), 0, cache)
+    n2, l2 = o.forward([n1], 64, cache)
+    m = llm.CausalLM.from_weights(w, lmax=128)
+    r = m.generate(ids, 1, use_graph=False)
+    g1 = m.buf["logits"][0].cpu().numpy()
+    m._step(1)
+    torch.cuda.synchronize()
+    g2 = m.buf["logits"][0].cpu().numpy()
+    assert r.tokens == [n1] and int(m.history[1]) == n2
+    for got, ref in ((g1, l1), (g2, l2)):
+        bad = np.abs(got - ref) > 1e-3 + 1e-2 * np.abs(ref)
+        assert not bad.any(), np.abs(got - ref).max()
+        assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-4

@@ -126,8 +126,9 @@ class CausalLM:
         self.history = torch.zeros(T, dtype=torch.int32, device=dev)
         self.state = torch.zeros(_lib.lib().miq_decode_state_words(), dtype=torch.int32, device=dev)
         # one split-K workspace sized for every projection at T = 1 and at the largest prefill
+        # (the need is not monotonic in the row count: wide enough layers stop splitting K)
         need = core.gemv_workspace_bytes(1, self.head.K, self.head.N, self.gs, self.bits, _lib.MIQ_F32)
-        for M in (1, T):  # the head only ever sees the last token
+        for M in range(1, T + 1):  # the head only ever sees the last token
             for lin in [self.layers[0][k] for k in ("qkv", "o", "gate_up", "down")]:
                 need = max(need, core.gemv_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits, _lib.MIQ_F32))
         self.ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)

@@ -133,26 +133,50 @@ def moe_workload(seed, T=256, H=2048, E=128, I=768, top_k=8, gs=128, experts=Tru
             "E": E, "I": I, "gs": gs}
 
 
+def quantized_gaussian_layer(seed, K, N, gs=128, bits=4, name="w"):
+    """AutoGPTQ layer quantized from Gaussian weights ~N(0, 1/K) with the asymmetric min-max
+    rule (per group and column: scale = (max - min) / qmax, zero = round(-min / scale)), stored
+    as AutoGPTQ does (zero - 1, fp16 scales). Unlike uniform random codes, these weights have
+    no common offset, so a model built from them produces varied greedy tokens."""
+    per, qmax = 32 // bits, (1 << bits) - 1
+    W = rng(seed, name + ".w").standard_normal((K, N)) / np.sqrt(K)
+    Wg = W.reshape(K // gs, gs, N)
+    lo, hi = Wg.min(1), Wg.max(1)
+    sc = ((hi - lo) / qmax).astype(np.float16)
+    s32 = sc.astype(np.float64)
+    zp = np.clip(np.round(-lo / s32), 1, qmax).astype(np.int64)   # AutoGPTQ cannot store zero 0
+    q = np.clip(np.round(Wg / s32[:, None, :]) + zp[:, None, :], 0, qmax).astype(np.int64).reshape(K, N)
+    qweight = np.zeros((K // per, N), np.uint32)
+    for j in range(per):
+        qweight |= q[j::per].astype(np.uint32) << np.uint32(j * bits)
+    zs = ((zp - 1) & qmax).astype(np.uint32)
+    qzeros = np.zeros((K // gs, N // per), np.uint32)
+    for j in range(per):
+        qzeros |= zs[:, j::per] << np.uint32(j * bits)
+    return {"qweight": qweight.view(np.int32), "qzeros": qzeros.view(np.int32), "scales": sc,
+            "g_idx": (np.arange(K) // gs).astype(np.int32), "K": K, "N": N, "gs": gs, "bits": bits}
+
+
 def decoder_weights(seed, L=24, H=896, NH=14, NKV=2, HD=64, I=4864, V=151936, gs=128,
-                    bits=4, **_):
+                    bits=4, embed_scale=0.02, gaussian=False, **_):
     """Random-init Qwen2-shaped int4 decoder: AutoGPTQ int4 linears (q/k/v with fp16 bias),
-    RMSNorm weights near 1, fp16 embeddings ~N(0, 0.02) (the head is tied to them)."""
+    RMSNorm weights near 1, fp16 embeddings ~N(0, embed_scale**2) (the head is tied to them).
+    The linears hold uniform random codes, zeros and |N|*0.01+1e-3 scales, or, with
+    `gaussian`, codes quantized from Gaussian weights (`quantized_gaussian_layer`)."""
+    make = (lambda K, N, name: quantized_gaussian_layer(seed, K, N, gs, bits, name=name)) if gaussian else \
+        (lambda K, N, name: gptq_layer(seed, K, N, gs, bits, name=name))
     layers = []
     for i in range(L):
         p = "l%d." % i
-        lay = {"q": gptq_layer(seed, H, NH * HD, gs, bits, name=p + "q"),
-               "k": gptq_layer(seed, H, NKV * HD, gs, bits, name=p + "k"),
-               "v": gptq_layer(seed, H, NKV * HD, gs, bits, name=p + "v"),
-               "o": gptq_layer(seed, NH * HD, H, gs, bits, name=p + "o"),
-               "gate": gptq_layer(seed, H, I, gs, bits, name=p + "gate"),
-               "up": gptq_layer(seed, H, I, gs, bits, name=p + "up"),
-               "down": gptq_layer(seed, I, H, gs, bits, name=p + "down")}
+        lay = {"q": make(H, NH * HD, p + "q"), "k": make(H, NKV * HD, p + "k"),
+               "v": make(H, NKV * HD, p + "v"), "o": make(NH * HD, H, p + "o"),
+               "gate": make(H, I, p + "gate"), "up": make(H, I, p + "up"), "down": make(I, H, p + "down")}
         for nm, n in (("q", NH * HD), ("k", NKV * HD), ("v", NKV * HD)):
             lay[nm]["bias"] = (rng(seed, p + nm + ".bias").standard_normal(n) * 0.02).astype(np.float16)
         lay["in_ln"] = (1.0 + 0.02 * rng(seed, p + "in_ln").standard_normal(H)).astype(np.float16)
         lay["post_ln"] = (1.0 + 0.02 * rng(seed, p + "post_ln").standard_normal(H)).astype(np.float16)
         layers.append(lay)
-    embed = (rng(seed, "embed").standard_normal((V, H)) * 0.02).astype(np.float16)
+    embed = (rng(seed, "embed").standard_normal((V, H)) * embed_scale).astype(np.float16)
     final_norm = (1.0 + 0.02 * rng(seed, "final_norm").standard_normal(H)).astype(np.float16)
     return {"layers": layers, "embed": embed, "final_norm": final_norm,
             "cfg": dict(L=L, H=H, NH=NH, NKV=NKV, HD=HD, I=I, V=V, gs=gs, bits=bits)}
