@@ -33,9 +33,14 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=" + ARCH, "-munsafe-fp-at
          "-Wno-unused-result", "-I" + INCLUDE, "-I" + CSRC]
 
 
+# per-source flags: the matrix-core kernels keep their MFMA accumulators in ordinary VGPRs, so
+# the per-group scale fold reads them without a copy out of the accumulation registers
+FILE_FLAGS = {"gptq_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc()] + FLAGS + ["-c", src, "-o", obj]
+    cmd = [hipcc()] + FLAGS + FILE_FLAGS.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed for %s:\n%s" % (src, r.stderr[-4000:]))

@@ -332,7 +332,7 @@ class GGMLLinear:
         if isinstance(raw, torch.Tensor):
             b = raw.reshape(-1).view(torch.uint8)
         else:
-            b = torch.from_numpy(np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray))
+            b = torch.from_numpy(np.frombuffer(bytearray(raw), np.uint8) if isinstance(raw, (bytes, bytearray))
                                  else np.ascontiguousarray(raw).reshape(-1).view(np.uint8))
         if b.numel() < nbytes:
             raise ValueError("raw holds %d bytes, %s (%d x %d) needs %d" % (b.numel(), type_name, N, K, nbytes))

@@ -1,21 +1,38 @@
 // GPTQ int4/int8 prefill GEMM on the gfx950 matrix cores (v_mfma_f32_16x16x32_f16).
 //
-// out[M][N] = x[M][K] (fp16, gathered through perm for act-order) @ W + bias, W in the
-// AutoGPTQ layout (see gptq_gemv.hip). Dequantization stays exact: each packed word becomes
-// the 8 integers q - (z + zoff) in fp16 (exact: |q - z - zoff| <= 256), the matrix cores
-// accumulate x * (q - z) in fp32 (fp16 products are exact in fp32), and the fp32 group scale
-// is applied to each chunk's partial sums: acc += s[g][n] * sum_{k in chunk} x[k] (q - z).
+// out[M][N] = x[M][K] (fp16) @ W + bias, W in the AutoGPTQ layout (see gptq_gemv.hip).
+// Dequantization stays exact: each packed word becomes the 8 integers q - (z + zoff) in fp16
+// (exact: |q - z - zoff| <= 263), the matrix cores accumulate x * (q - z) in fp32 (fp16
+// products are exact in fp32), and the fp32 group scale multiplies each stage's partial sums:
+// acc += s[g][n] * sum_{k in stage} x[k] (q - z).
 //
-// Mapping. A workgroup is 4 waves side by side along N; a wave owns 64 columns as 4 MFMA
-// column blocks, lane (p, kb) = (lane % 16, lane / 16) holding columns ncol + s = n_wave +
-// 4 p + s (s = 0..3, one 16-byte load covers all four) and the k-block kb of each 32-wide
-// step. The B operand of an MFMA is one packed word per lane (int4: 8 consecutive k of one
-// column; int8: two words); its 8 values come out of the unpack in the order c0 c4 c1 c5 c2
-// c6 c3 c7 (int8: c0 c2 c1 c3 c4 c6 c5 c7), so the activations are staged in LDS in that same
-// order within each 8-wide k block, which leaves every dot product unchanged. A workgroup
-// covers BM = 16 * TM rows of x; the K range is cut into chunks of KC (<= 128, inside one
-// group) and, for parallelism, into ksplit slices combined deterministically through the
-// workspace exactly as the GEMV does (last-arriving workgroup sums the slices in order).
+// Activations. A first pass copies x into the workspace (gathered through perm for act-order)
+// with each 8-wide k block reordered the way the code unpack produces the weights: int4
+// c0 c4 c1 c5 c2 c6 c3 c7, int8 c0 c2 c1 c3 c4 c6 c5 c7. Every dot product is unchanged, the
+// MFMA A operand is then a plain 16-byte read, and the B operand needs no byte shuffling.
+//
+// Mapping. A workgroup is 4 waves side by side along N; a wave owns 16 TM rows x 16 CB columns
+// as TM x CB MFMA tiles (BM = 16 TM, BN = 64 CB). Lane (p, kb) = (lane % 16, lane / 16) holds
+// columns ncol + s = n_wave + CB p + s (s < CB; one LDS read gives the CB packed words of a k
+// row) and the 8-wide k block kb of each 32-wide MFMA step. Each wave dequantizes its own
+// columns, so the unpack is spread over the 16 TM rows it feeds.
+//
+// Pipeline. K is walked in stages of KC (<= 128, inside one group). A stage's activation rows,
+// packed weight rows, scales and zero points are copied global -> LDS by the DMA path of the
+// vector memory unit (global_load_lds), NBUF - 1 stages ahead of the stage being multiplied, so
+// the loads of several stages are in flight while the matrix cores work and no register holds
+// data on its way to LDS. One barrier per stage both publishes the stage that landed and frees
+// the buffer that the next copy overwrites. Activation rows sit in LDS with their 16-byte
+// chunks XOR-swizzled by row (chunk c of row r at slot c ^ (r mod chunks-per-row)), so the 16
+// rows that one operand read touches fall in different banks.
+//
+// K may also be split over workgroups (ksplit) when the tile grid alone is too small for the
+// chip; slices are combined deterministically through the workspace, the last workgroup to
+// arrive summing them in slice order, as the GEMV does.
+//
+// Placement. Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2; the
+// tile order is remapped so that the workgroups on one XCD share weight columns (same column
+// tile and K slice, different row tiles).
 #include <type_traits>
 
 #include "miq_common.h"
@@ -26,123 +43,273 @@ namespace miq {
 #define MIQ_GEMM_TARGET_WGS 256
 #endif
 
-template <int BITS, int TM, int KC, typename ST, typename OT>
-__global__ __launch_bounds__(256) void gptq_gemm_kernel(
-    const __half* __restrict__ x, const int32_t* __restrict__ perm, const uint32_t* __restrict__ qw,
-    const uint32_t* __restrict__ qz, const ST* __restrict__ sc, const float* __restrict__ bias,
-    OT* __restrict__ out, float* __restrict__ ws, int* __restrict__ counters, int M, int K, int N, int gs,
-    float zoff, int chunks_per_wg, int ksplit) {
-  constexpr int PER = 32 / BITS;
-  constexpr int BM = 16 * TM;
-  constexpr int STEPS = KC / 32;
-  constexpr int RB = BITS == 4 ? 1 : 2;  // 16-byte weight loads per lane and step
-  __shared__ __align__(16) _Float16 xs[BM * KC];  // activation chunk [BM][KC], pair order
+#ifndef MIQ_GEMM_SCHED_PATTERN
+#define MIQ_GEMM_SCHED_PATTERN 0
+#endif
+
+constexpr int kXCDs = 8;
+constexpr int kLdsBytes = 160 * 1024;
+
+// 16 bytes stored with device scope (sc1: written through the XCD's L2, so that workgroups on
+// other XCDs read it). Not counted by the compiler's wait counters: the caller waits with
+// s_waitcnt before publishing.
+__device__ __forceinline__ void store_agent16(float* p, float4v v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ uint64_t pack_f2(float a, float b) {
+  return (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+}
+
+// 8 fp16 in k order (16 bytes: words (h0,h1) (h2,h3) (h4,h5) (h6,h7)) into the unpack's order
+template <int BITS> __device__ __forceinline__ uint4 pair_order8(uint4 v) {
+  if constexpr (BITS == 4)  // (h0,h4) (h1,h5) (h2,h6) (h3,h7)
+    return make_uint4((v.x & 0xFFFFu) | (v.z << 16), (v.x >> 16) | (v.z & 0xFFFF0000u),
+                      (v.y & 0xFFFFu) | (v.w << 16), (v.y >> 16) | (v.w & 0xFFFF0000u));
+  else  // (h0,h2) (h1,h3) (h4,h6) (h5,h7)
+    return make_uint4((v.x & 0xFFFFu) | (v.y << 16), (v.x >> 16) | (v.y & 0xFFFF0000u),
+                      (v.z & 0xFFFFu) | (v.w << 16), (v.z >> 16) | (v.w & 0xFFFF0000u));
+}
+
+// xp = x with each 8-wide k block in pair order, stored stage-major: xp[k / KC][m][k % KC]. A
+// stage of a row tile is then one contiguous block, which spreads its reads over all L2
+// channels (rows of x are 2 K bytes apart, a power of two for the usual K, and would all land
+// in the same few channels). Grid (K/8/256 rounded up, M).
+template <int BITS>
+__global__ __launch_bounds__(256) void stage_x_kernel(const __half* __restrict__ x, __half* __restrict__ xp, int M,
+                                                      int K, int KC) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= K / 8) return;
+  const int m = blockIdx.y, k = i * 8;
+  *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC) =
+      pair_order8<BITS>(*reinterpret_cast<const uint4*>(x + (size_t)m * K + k));
+}
+
+// the same with the columns gathered through perm: one workgroup per row, the row staged in
+// LDS (2 K bytes of dynamic LDS, K <= 32768)
+template <int BITS>
+__global__ __launch_bounds__(256) void gather_x_kernel(const __half* __restrict__ x, const int32_t* __restrict__ perm,
+                                                       __half* __restrict__ xp, int M, int K, int KC) {
+  extern __shared__ __align__(16) unsigned short row[];
+  const int m = blockIdx.x;
+  const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)m * K);
+  for (int i = threadIdx.x; i < K / 8; i += 256) reinterpret_cast<uint4*>(row)[i] = src[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < K / 8; i += 256) {
+    const int4 pa = reinterpret_cast<const int4*>(perm)[2 * i];
+    const int4 pb = reinterpret_cast<const int4*>(perm)[2 * i + 1];
+    const uint4 v = make_uint4(row[pa.x] | ((uint32_t)row[pa.y] << 16), row[pa.z] | ((uint32_t)row[pa.w] << 16),
+                               row[pb.x] | ((uint32_t)row[pb.y] << 16), row[pb.z] | ((uint32_t)row[pb.w] << 16));
+    const int k = i * 8;
+    *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC) = pair_order8<BITS>(v);
+  }
+}
+
+template <int BITS, int TM, int CB, int KC, typename ST> struct GemmShape {
+  static constexpr int PER = 32 / BITS;
+  static constexpr int BM = 16 * TM, BN = 64 * CB;
+  static constexpr int STEPS = KC / 32;
+  static constexpr int RB = BITS == 4 ? 1 : 2;    // packed rows per lane and MFMA step
+  static constexpr int AROW = KC * 2;             // bytes of one activation row of a stage
+  static constexpr int CPR = AROW / 16;           // 16-byte chunks per row
+  static constexpr int RPI = 1024 / AROW;         // rows per activation DMA (64 lanes x 16 B)
+  static constexpr int NA = BM / RPI;             // activation DMAs per stage
+  static constexpr int BROWS = KC / PER;          // packed weight rows per stage
+  static constexpr int BROWB = BN * 4;            // bytes per packed row of the tile
+  static constexpr int NB = BROWS * BROWB / 1024; // weight DMAs per stage (16-byte lanes)
+  static constexpr int SB = BN * (int)sizeof(ST); // scale bytes per stage
+  static constexpr int NS = SB / 256;             // scale DMAs (4-byte lanes)
+  static constexpr int NI = NA + NB + NS + 1;     // + one zero-point DMA
+  static constexpr int NIW = (NI + 3) / 4;        // per wave (the last ones repeat the zero DMA)
+  static constexpr int A_OFF = 0, B_OFF = BM * AROW, S_OFF = B_OFF + BROWS * BROWB, Z_OFF = S_OFF + SB;
+  static constexpr int STAGE = Z_OFF + 256;
+  static constexpr int NBUF = 4 * STAGE + 64 <= kLdsBytes ? 4 : (3 * STAGE + 64 <= kLdsBytes ? 3 : 2);
+  static constexpr int P = NBUF - 1;              // stages in flight ahead of the one multiplied
+  static_assert(BM % RPI == 0 && (BROWS * BROWB) % 1024 == 0 && SB % 256 == 0, "whole DMAs");
+  static_assert(BN / PER <= 64, "zero points of a tile fit one DMA");
+  static_assert((P - 1) * NIW < 64, "vmcnt range");
+};
+
+// 8 waves: 4 multiply (one per SIMD), 4 only issue the stage copies. A copy instruction that
+// finds the memory pipeline full stalls the wave that issues it; kept on their own waves, those
+// stalls never hold back an MFMA.
+template <int BITS, int TM, int CB, int KC, typename ST, typename OT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gptq_gemm_kernel(
+    const __half* __restrict__ xp, const uint32_t* __restrict__ qw, const uint32_t* __restrict__ qz,
+    const ST* __restrict__ sc, const float* __restrict__ bias, OT* __restrict__ out, float* __restrict__ ws,
+    int* __restrict__ counters, int M, int K, int N, int gs, float zoff, int stages_per_wg, int ksplit, int ntiles,
+    int mtiles) {
+  using G = GemmShape<BITS, TM, CB, KC, ST>;
+  constexpr int PER = G::PER, STEPS = G::STEPS, RB = G::RB, NBUF = G::NBUF, P = G::P, NIW = G::NIW;
+  __shared__ __align__(16) char lds[NBUF * G::STAGE];
   __shared__ int is_last;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = uniform(threadIdx.x >> 6);
-  const int p = lane & 15, kb = lane >> 4;
-  const int ncol = blockIdx.x * 256 + wave * 64 + 4 * p;
-  const bool colok = ncol < N;
-  const bool wave_active = blockIdx.x * 256 + wave * 64 < N;
-  const int m0 = blockIdx.y * BM;
-  const int ks = blockIdx.z;
-  const int nchunks = K / KC;
-  const int c0 = ks * chunks_per_wg;
-  const int c1 = min(nchunks, c0 + chunks_per_wg);
-  const int NZ = N / PER;
-  const int zshift = (ncol % PER) * BITS;
+  // ---- tile of this workgroup: XCD-major order, row tiles fastest ----
+  const int T = (int)gridDim.x, L = (int)blockIdx.x;
+  const int Lp = T % kXCDs == 0 ? (L % kXCDs) * (T / kXCDs) + L / kXCDs : L;
+  const int mtile = Lp % mtiles;
+  const int rest = Lp / mtiles;
+  const int ks = rest % ksplit;
+  const int ntile = rest / ksplit;
 
-  float4v acc[TM][4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const bool producer = uniform(tid >> 6) >= 4;  // waves 4..7 issue the copies
+  const int wave = uniform(tid >> 6) & 3;  // (the range lets each copy's kind fold at compile time)
+  const int p = lane & 15, kb = lane >> 4;
+  const int n0 = ntile * G::BN;
+  const int cl = wave * 16 * CB + CB * p;  // the lane's first column within the tile
+  const int ncol = n0 + cl;
+  const bool colok = ncol < N;
+  const int m0 = mtile * G::BM;
+  const int nst = K / KC;
+  const int st0 = ks * stages_per_wg;
+  const int st1 = min(nst, st0 + stages_per_wg);
+  const int last = st1 - 1;
+  const int NZ = N / PER;
+  const uint32_t lds0 = lds_addr(lds);
+
+  // ---- copy j of one stage into LDS buffer buf: instruction i = wave + 4 j of the stage.
+  // Rows past M and columns past N re-read the last valid row / column (in bounds; they only
+  // feed outputs that are never stored).
+  auto issue_one = [&](int s, int buf, int j) __attribute__((always_inline)) {
+    const uint32_t base = lds0 + buf * G::STAGE;
+    const int g = s * KC / gs;
+    const int i = wave + 4 * j;  // wave-uniform
+    if (i < G::NA) {
+      const int rloc = i * G::RPI + lane / G::CPR, slot = lane % G::CPR;
+      const int chunk = slot ^ (rloc % G::CPR);
+      const int row = min(m0 + rloc, M - 1);
+      dma16(xp + ((size_t)s * M + row) * KC + chunk * 8, uniform(base + G::A_OFF + i * 1024));
+    } else if (i < G::NA + G::NB) {
+      const int b = i - G::NA;
+      const int r = b * (1024 / G::BROWB) + lane / (G::BROWB / 16), c4 = lane % (G::BROWB / 16);
+      dma16(qw + (size_t)(s * G::BROWS + r) * N + min(n0 + 4 * c4, N - 4), uniform(base + G::B_OFF + b * 1024));
+    } else if (i < G::NA + G::NB + G::NS) {
+      const int h = i - G::NA - G::NB;
+      constexpr int E = 4 / (int)sizeof(ST);  // scales per lane
+      dma4(sc + (size_t)g * N + min(n0 + 64 * E * h + E * lane, N - E), uniform(base + G::S_OFF + 256 * h));
+    } else {
+      dma4(qz + (size_t)g * NZ + min(n0 / PER + lane, NZ - 1), uniform(base + G::Z_OFF));
+    }
+  };
+  auto issue = [&](int s, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NIW; ++j) issue_one(s, buf, j);
+  };
+
+  float4v acc[TM][CB];
 #pragma unroll
   for (int t = 0; t < TM; ++t)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc[t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < CB; ++s) acc[t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-  for (int c = c0; c < c1; ++c) {
-    const int kc0 = c * KC;
-    // ---- weights, scales and zeros of the chunk (issued before the activations are staged) ----
-    // lanes past N hold zero weights: the matrix cores read every lane's operands, so no lane
-    // of a wave may skip the MFMA (their outputs are dropped at the end)
+  // One stage of matrix work. Every LDS read of the stage is issued first, then the weights
+  // are unpacked step by step while the MFMAs run.
+  auto compute = [&](int buf) __attribute__((always_inline)) {
+    const char* stg = lds + buf * G::STAGE;
     uint4 bw[STEPS][RB];
+    half8v af[STEPS][TM];
 #pragma unroll
     for (int st = 0; st < STEPS; ++st)
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) bw[st][rb] = make_uint4(0u, 0u, 0u, 0u);
-    uint4 sraw = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t zraw = 0;
-    if (colok) {
-#pragma unroll
-      for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const int row = (kc0 + st * 32) / PER + kb * RB + rb;
-          bw[st][rb] = *reinterpret_cast<const uint4*>(qw + (size_t)row * N + ncol);
-        }
-      const int g = kc0 / gs;
-      sraw = load_scales4<ST>(sc + (size_t)g * N + ncol);
-      zraw = qz[(size_t)g * NZ + ncol / PER];
-    }
-    // ---- stage the activation chunk ----
-    __syncthreads();  // the previous chunk's reads are done
-    for (int ci = threadIdx.x; ci < BM * KC / 8; ci += 256) {
-      const int r = ci / (KC / 8), kk = (ci - r * (KC / 8)) * 8;
-      const int k = kc0 + kk;
-      float v[8];
-      if (m0 + r < M) {
-        const __half* xr = x + (size_t)(m0 + r) * K;
-        if (perm) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = __half2float(xr[perm[k + j]]);
+      for (int rb = 0; rb < RB; ++rb) {
+        const char* src = stg + G::B_OFF + ((st * 32) / PER + kb * RB + rb) * G::BROWB + cl * 4;
+        if constexpr (CB == 4) {
+          bw[st][rb] = *reinterpret_cast<const uint4*>(src);
         } else {
-          load8(xr + k, v);
+          const uint2 t2 = *reinterpret_cast<const uint2*>(src);
+          bw[st][rb] = make_uint4(t2.x, t2.y, 0u, 0u);
         }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = 0.f;
       }
-      *reinterpret_cast<uint4*>(xs + r * KC + kk) = pack8_pairs<BITS>(v);
-    }
-    __syncthreads();
-    if (!wave_active) continue;  // wave-uniform: the whole wave is past N
-
-    // ---- zero points folded into the fp16 conversion: (1024 + q) - (1024 + z + zoff) ----
-    half2v zl[4], zh[4];
-    zero_pairs<BITS>(zraw >> zshift, zoff, zl, zh);
-    float4v part[TM][4];
+    const uint32_t zw = *reinterpret_cast<const uint32_t*>(stg + G::Z_OFF + (cl / PER) * 4) >> ((cl % PER) * BITS);
 #pragma unroll
-    for (int t = 0; t < TM; ++t)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) part[t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < STEPS; ++st) {
-      half8v bf[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) bf[s] = b_fragment<BITS>(bw[st], s, zl[s], zh[s]);
+    for (int st = 0; st < STEPS; ++st)
 #pragma unroll
       for (int t = 0; t < TM; ++t) {
-        const half8v af = *reinterpret_cast<const half8v*>(xs + (16 * t + p) * KC + st * 32 + 8 * kb);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) part[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[s], part[t][s], 0, 0, 0);
+        const int r = 16 * t + p, chunk = st * 4 + kb;
+        af[st][t] = *reinterpret_cast<const half8v*>(stg + G::A_OFF + r * G::AROW + ((chunk ^ (r % G::CPR)) * 16));
       }
-    }
     float sf[4];
-    scales4<ST>(sraw, sf);
+    if constexpr (CB == 4) {
+      scales4<ST>(load_scales4<ST>(reinterpret_cast<const ST*>(stg + G::S_OFF) + cl), sf);
+    } else {
+      const ST* sp = reinterpret_cast<const ST*>(stg + G::S_OFF) + cl;
+      sf[0] = to_f32(sp[0]);
+      sf[1] = to_f32(sp[1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    half2v zl[4], zh[4];
+    zero_pairs<BITS>(zw, zoff, zl, zh);
+    float4v part[TM][CB];
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < CB; ++s) part[t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
+    // the unpack runs one step ahead of the MFMAs, and the scheduling pattern below puts a few
+    // unpack instructions behind each MFMA: the SIMD issues them while the matrix core works
+    half8v bf[CB], bn[CB];
+#pragma unroll
+    for (int s = 0; s < CB; ++s) bn[s] = b_fragment<BITS>(bw[0], s, zl[s], zh[s]);
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+#pragma unroll
+      for (int s = 0; s < CB; ++s) bf[s] = bn[s];
+      if (st + 1 < STEPS) {
+#pragma unroll
+        for (int s = 0; s < CB; ++s) bn[s] = b_fragment<BITS>(bw[st + 1], s, zl[s], zh[s]);
+      }
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int s = 0; s < CB; ++s)
+          part[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[st][t], bf[s], part[t][s], 0, 0, 0);
+    }
+#if MIQ_GEMM_SCHED_PATTERN
+    constexpr int kValuPerMfma = (CB * (BITS == 4 ? 9 : 8) + TM * CB - 1) / (TM * CB) + 1;
+    __builtin_amdgcn_sched_group_barrier(0x002, CB * (BITS == 4 ? 9 : 8) + 16, 0);  // zero points, first unpack
+#pragma unroll
+    for (int i = 0; i < STEPS * TM * CB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // then a few VALU
+    }
+#endif
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+      for (int s = 0; s < CB; ++s)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][s][r] = fmaf(sf[s], part[t][s][r], acc[t][s][r]);
+  };
+
+  // ---- pipeline: stages st0 .. last, P of them in flight ----
+  if (producer) {
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+      if (st0 + q <= last) issue(st0 + q, q);
+  }
+  for (int s = st0; s <= last; ++s) {
+    // a producer's copies of stage s are done once at most min(P - 1, last - s) later stages
+    // remain in flight; the barrier makes every copy of stage s visible and tells the producers
+    // that stage s - 1, whose buffer the next copy reuses, has been multiplied
+    if (producer) {
+      const int ahead = min(P - 1, last - s);
+      if (ahead >= 2) wait_vmcnt<(P - 1 >= 2 ? 2 * NIW : 0)>();
+      else if (ahead == 1) wait_vmcnt<NIW>();
+      else wait_vmcnt<0>();
+    }
+    __syncthreads();
+    if (producer) {
+      if (s + P <= last) issue(s + P, (s - st0 + P) % NBUF);
+    } else {
+      compute((s - st0) % NBUF);
+    }
   }
 
-  // ---- epilogue: D[row = 16 t + 4 kb + r][col = ncol + s] = acc[t][s][r] ----
+  // ---- epilogue: D[row = m0 + 16 t + 4 kb + r][col = ncol + s] = acc[t][s][r] ----
   if (ksplit == 1) {
-    if (!colok) return;
-    float b4[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias)
+    if (producer || !colok) return;
+    float bv[CB];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) b4[s] = bias[ncol + s];
+    for (int s = 0; s < CB; ++s) bv[s] = bias ? bias[ncol + s] : 0.f;
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -151,12 +318,13 @@ __global__ __launch_bounds__(256) void gptq_gemm_kernel(
         if (row >= M) continue;
         OT* o = out + (size_t)row * N + ncol;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) o[s] = from_f32<OT>(acc[t][s][r] + b4[s]);
+        for (int s = 0; s < CB; ++s) o[s] = from_f32<OT>(acc[t][s][r] + bv[s]);
       }
     return;
   }
   // split K: device-scope stores of the slice, count in, the last workgroup sums the slices
-  if (colok) {
+  // (the producer waves take part in the barriers only)
+  if (!producer && colok) {
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -164,107 +332,171 @@ __global__ __launch_bounds__(256) void gptq_gemm_kernel(
         const int row = m0 + 16 * t + 4 * kb + r;
         if (row >= M) continue;
         float* d = ws + ((size_t)ks * M + row) * N + ncol;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) __hip_atomic_store(d + s, acc[t][s][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (CB == 4) {
+          store_agent16(d, (float4v){acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]});
+        } else {
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(d), pack_f2(acc[t][0][r], acc[t][1][r]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  int* ctr = counters + (size_t)blockIdx.y * gridDim.x + blockIdx.x;
-  if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ksplit - 1;
+  int* ctr = counters + (size_t)ntile * mtiles + mtile;
+  if (tid == 0) is_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ksplit - 1;
   __syncthreads();
-  if (!is_last) return;
-  if (colok) {
-    const size_t stride = (size_t)M * N;
+  if (!is_last || producer) return;
+  // the slices are summed in slice order (this workgroup's own slice is still in acc); KU slices
+  // per trip keep up to 64 loads in flight per lane. Rows past M and columns past N read row
+  // M - 1 / column N - CB (in bounds) and are not stored.
+  {
+    constexpr int KU = 16 / (TM * CB) > 0 ? 16 / (TM * CB) : 1;
+    const int ccol = min(ncol, N - CB);
+    float4v sum[TM][CB];
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + 16 * t + 4 * kb + r;
-        if (row >= M) continue;
-        const float* pp = ws + (size_t)row * N + ncol;
-        float sum[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int k2 = 0; k2 < ksplit; ++k2) {
-          float v[4];
+      for (int s = 0; s < CB; ++s) sum[t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < ksplit; k0 += KU) {
+      float v[KU][TM][4][CB];
 #pragma unroll
-          for (int s = 0; s < 4; ++s) v[s] = __hip_atomic_load(pp + k2 * stride + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int u = 0; u < KU; ++u) {
+        const int kk = min(k0 + u, ksplit - 1);
 #pragma unroll
-          for (int s = 0; s < 4; ++s) sum[s] += v[s];
-        }
-        OT* o = out + (size_t)row * N + ncol;
+        for (int t = 0; t < TM; ++t)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) o[s] = from_f32<OT>(sum[s] + (bias ? bias[ncol + s] : 0.f));
+          for (int r = 0; r < 4; ++r) {
+            const uint64_t* pp =
+                reinterpret_cast<const uint64_t*>(ws + ((size_t)kk * M + min(m0 + 16 * t + 4 * kb + r, M - 1)) * N + ccol);
+#pragma unroll
+            for (int s = 0; s < CB; s += 2) {
+              const uint64_t w = __hip_atomic_load(pp + s / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              v[u][t][r][s] = __uint_as_float((uint32_t)w);
+              v[u][t][r][s + 1] = __uint_as_float((uint32_t)(w >> 32));
+            }
+          }
       }
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        if (k0 + u >= ksplit) break;
+        const bool own = k0 + u == ks;
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+          for (int s = 0; s < CB; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sum[t][s][r] += own ? acc[t][s][r] : v[u][t][r][s];
+      }
+    }
+    if (colok) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + 16 * t + 4 * kb + r;
+          if (row >= M) continue;
+          OT* o = out + (size_t)row * N + ncol;
+#pragma unroll
+          for (int s = 0; s < CB; ++s) o[s] = from_f32<OT>(sum[t][s][r] + (bias ? bias[ncol + s] : 0.f));
+        }
+    }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed
+  if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // re-armed
 }
 
+// wave tiles (TM x CB MFMA tiles per wave) the planner chooses from, largest first
+struct WaveTile {
+  int tm, cb;
+};
+constexpr WaveTile kWaveTiles[] = {{4, 4}, {4, 2}, {2, 4}, {1, 4}};
+
 struct GemmPlan {
-  int tm, kc, tiles, mtiles, ksplit, chunks_per_wg;
-  size_t counter_bytes, ws_bytes;
+  int tm, cb, kc, ntiles, mtiles, ksplit, stages_per_wg;
+  size_t partial_bytes, xp_bytes, ws_bytes;
 };
 
-static int gemm_plan(int M, int K, int N, int gs, bool have_ws, GemmPlan* p) {
+static int gemm_plan(int M, int K, int N, int gs, GemmPlan* p) {
   int kc = 0;
   if (gs % 128 == 0) kc = 128;
-  else if (gs == 64) kc = 64;
-  else if (gs == 32) kc = 32;
-  MIQ_REQUIRE(kc, MIQ_ERR_UNSUPPORTED, "gptq_gemm: group size %d (32, 64 or a multiple of 128)", gs);
+  else if (gs % 64 == 0) kc = 64;
+  else if (gs % 32 == 0) kc = 32;
+  MIQ_REQUIRE(kc, MIQ_ERR_UNSUPPORTED, "gptq_gemm: group size %d (a multiple of 32)", gs);
   p->kc = kc;
-  p->tm = M >= 64 ? 4 : (M >= 32 ? 2 : 1);
-  p->tiles = (N + 255) / 256;
+  // the largest wave tile whose grid covers the chip; failing that, the smallest that the rows
+  // fill, with K split to make up the rest
+  int pick = -1;
+#if defined(MIQ_GEMM_TM) && defined(MIQ_GEMM_CB)
+  for (int i = 0; i < 4; ++i)
+    if (kWaveTiles[i].tm == MIQ_GEMM_TM && kWaveTiles[i].cb == MIQ_GEMM_CB) pick = i;
+#else
+  for (int i = 0; i < 4 && pick < 0; ++i) {
+    const long tiles = (long)((M + 16 * kWaveTiles[i].tm - 1) / (16 * kWaveTiles[i].tm)) *
+                       ((N + 64 * kWaveTiles[i].cb - 1) / (64 * kWaveTiles[i].cb));
+    if (tiles >= MIQ_GEMM_TARGET_WGS) pick = i;
+  }
+  if (pick < 0) pick = 1;
+#endif
+  p->tm = kWaveTiles[pick].tm;
+  p->cb = kWaveTiles[pick].cb;
+  p->ntiles = (N + 64 * p->cb - 1) / (64 * p->cb);
   p->mtiles = (M + 16 * p->tm - 1) / (16 * p->tm);
-  const int nchunks = K / kc;
-  const int base = p->tiles * p->mtiles;
-  int ksplit = have_ws && base <= kMaxCounters ? (MIQ_GEMM_TARGET_WGS + base - 1) / base : 1;
-  if (ksplit > nchunks) ksplit = nchunks;
+  const int nst = K / kc;
+  const int base = p->ntiles * p->mtiles;
+  int ksplit = base <= kMaxCounters ? (MIQ_GEMM_TARGET_WGS + base - 1) / base : 1;
+  if (ksplit > nst) ksplit = nst;
   if (ksplit < 1) ksplit = 1;
-  p->chunks_per_wg = (nchunks + ksplit - 1) / ksplit;
-  p->ksplit = (nchunks + p->chunks_per_wg - 1) / p->chunks_per_wg;
-  p->counter_bytes = p->ksplit > 1 ? kCounterBytes : 0;
-  p->ws_bytes = p->ksplit > 1 ? p->counter_bytes + (size_t)p->ksplit * M * N * 4 : 0;
+  p->stages_per_wg = (nst + ksplit - 1) / ksplit;
+  p->ksplit = (nst + p->stages_per_wg - 1) / p->stages_per_wg;
+  p->partial_bytes = p->ksplit > 1 ? (size_t)p->ksplit * M * N * 4 : 0;
+  p->xp_bytes = ((size_t)M * K * 2 + 255) & ~(size_t)255;
+  p->ws_bytes = kCounterBytes + p->partial_bytes + p->xp_bytes;
   return MIQ_OK;
 }
 
-template <int BITS, int TM, int KC, typename ST, typename OT>
-static int launch_gemm(const GemmPlan& p, const void* x, const int32_t* perm, const int32_t* qw, const int32_t* qz,
-                       const void* sc, const float* bias, void* out, void* ws, int M, int K, int N, int gs,
-                       float zoff, hipStream_t st) {
-  int* counters = p.ksplit > 1 ? static_cast<int*>(ws) : nullptr;
-  float* partials = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes) : nullptr;
-  dim3 grid(p.tiles, p.mtiles, p.ksplit);
-  hipLaunchKernelGGL((gptq_gemm_kernel<BITS, TM, KC, ST, OT>), grid, dim3(256), 0, st,
-                     static_cast<const __half*>(x), perm, reinterpret_cast<const uint32_t*>(qw),
-                     reinterpret_cast<const uint32_t*>(qz), static_cast<const ST*>(sc), bias, static_cast<OT*>(out),
-                     partials, counters, M, K, N, gs, zoff, p.chunks_per_wg, p.ksplit);
+template <int BITS, int TM, int CB, int KC, typename ST, typename OT>
+static int launch_gemm(const GemmPlan& p, const __half* xp, const int32_t* qw, const int32_t* qz, const void* sc,
+                       const float* bias, void* out, void* ws, int M, int K, int N, int gs, float zoff, hipStream_t st) {
+  int* counters = static_cast<int*>(ws);
+  float* partials = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+  const int grid = p.ntiles * p.mtiles * p.ksplit;
+  hipLaunchKernelGGL((gptq_gemm_kernel<BITS, TM, CB, KC, ST, OT>), dim3(grid), dim3(512), 0, st, xp,
+                     reinterpret_cast<const uint32_t*>(qw), reinterpret_cast<const uint32_t*>(qz),
+                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, M, K, N, gs, zoff,
+                     p.stages_per_wg, p.ksplit, p.ntiles, p.mtiles);
   return check_launch("gptq_gemm");
 }
 
-template <int BITS, int TM, int KC>
-static int gemm_types(const GemmPlan& p, const void* x, const int32_t* perm, const int32_t* qw, const int32_t* qz,
-                      const void* sc, int sd, const float* bias, void* out, int od, void* ws, int M, int K, int N,
-                      int gs, float zoff, hipStream_t st) {
+template <int BITS, int TM, int CB, int KC>
+static int gemm_types(const GemmPlan& p, const __half* xp, const int32_t* qw, const int32_t* qz, const void* sc,
+                      int sd, const float* bias, void* out, int od, void* ws, int M, int K, int N, int gs, float zoff,
+                      hipStream_t st) {
   if (sd == MIQ_F16) {
-    if (od == MIQ_F16) return launch_gemm<BITS, TM, KC, __half, __half>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
-    return launch_gemm<BITS, TM, KC, __half, float>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
+    if (od == MIQ_F16)
+      return launch_gemm<BITS, TM, CB, KC, __half, __half>(p, xp, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
+    return launch_gemm<BITS, TM, CB, KC, __half, float>(p, xp, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
   }
-  if (od == MIQ_F16) return launch_gemm<BITS, TM, KC, float, __half>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
-  return launch_gemm<BITS, TM, KC, float, float>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
+  if (od == MIQ_F16)
+    return launch_gemm<BITS, TM, CB, KC, float, __half>(p, xp, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
+  return launch_gemm<BITS, TM, CB, KC, float, float>(p, xp, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, st);
+}
+
+template <int BITS, int KC>
+static int gemm_tiles(const GemmPlan& p, const __half* xp, const int32_t* qw, const int32_t* qz, const void* sc,
+                      int sd, const float* bias, void* out, int od, void* ws, int M, int K, int N, int gs, float zoff,
+                      hipStream_t st) {
+  if (p.tm == 4 && p.cb == 4) return gemm_types<BITS, 4, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  if (p.tm == 4 && p.cb == 2) return gemm_types<BITS, 4, 2, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  if (p.tm == 2 && p.cb == 4) return gemm_types<BITS, 2, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  return gemm_types<BITS, 1, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
 }
 
 template <int BITS>
-static int gemm_dispatch(const GemmPlan& p, const void* x, const int32_t* perm, const int32_t* qw, const int32_t* qz,
-                         const void* sc, int sd, const float* bias, void* out, int od, void* ws, int M, int K, int N,
-                         int gs, float zoff, hipStream_t st) {
-#define MIQ_GEMM_CASE(TM, KC) \
-  if (p.tm == TM && p.kc == KC) \
-    return gemm_types<BITS, TM, KC>(p, x, perm, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st)
-  MIQ_GEMM_CASE(1, 128); MIQ_GEMM_CASE(2, 128); MIQ_GEMM_CASE(4, 128);
-  MIQ_GEMM_CASE(1, 64); MIQ_GEMM_CASE(2, 64); MIQ_GEMM_CASE(4, 64);
-  MIQ_GEMM_CASE(1, 32); MIQ_GEMM_CASE(2, 32); MIQ_GEMM_CASE(4, 32);
-#undef MIQ_GEMM_CASE
-  return fail(MIQ_ERR_UNSUPPORTED, "gptq_gemm: no kernel for tm=%d kc=%d", p.tm, p.kc);
+static int gemm_dispatch(const GemmPlan& p, const __half* xp, const int32_t* qw, const int32_t* qz, const void* sc,
+                         int sd, const float* bias, void* out, int od, void* ws, int M, int K, int N, int gs,
+                         float zoff, hipStream_t st) {
+  if (p.kc == 128) return gemm_tiles<BITS, 128>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  if (p.kc == 64) return gemm_tiles<BITS, 64>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  return gemm_tiles<BITS, 32>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
 }
 
 int check_gptq_dims(const char* who, int K, int N, int gs, int bits);
@@ -281,7 +513,7 @@ extern "C" int miq_gptq_gemm_workspace(int M, int K, int N, int gs, int bits, si
   MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "gptq_gemm_workspace: M=%d", M);
   if (M == 0) return MIQ_OK;
   GemmPlan p;
-  rc = gemm_plan(M, K, N, gs, true, &p);
+  rc = gemm_plan(M, K, N, gs, &p);
   if (rc) return rc;
   *bytes = p.ws_bytes;
   return MIQ_OK;
@@ -296,24 +528,35 @@ extern "C" int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* 
   MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "gptq_gemm: M=%d", M);
   if (M == 0) return MIQ_OK;
   MIQ_REQUIRE(x && qweight && qzeros && scales && out, MIQ_ERR_INVALID, "gptq_gemm: null pointer");
-  MIQ_REQUIRE(N % 4 == 0 && K % 32 == 0 && aligned(qweight, 16) && aligned(x, 16) &&
-                  aligned(scales, scales_dtype == MIQ_F16 ? 8 : 16),
-              MIQ_ERR_ALIGN, "gptq_gemm: x and qweight must be 16-byte aligned, N %% 4 == 0, K %% 32 == 0");
+  MIQ_REQUIRE(N % 4 == 0 && K % 32 == 0 && aligned(qweight, 16) && aligned(x, 16) && aligned(scales, 4) &&
+                  (!perm || aligned(perm, 16)),
+              MIQ_ERR_ALIGN, "gptq_gemm: x, qweight and perm must be 16-byte aligned, N %% 4 == 0, K %% 32 == 0");
   MIQ_REQUIRE(scales_dtype == MIQ_F16 || scales_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "gptq_gemm: scales dtype");
   MIQ_REQUIRE(out_dtype == MIQ_F16 || out_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "gptq_gemm: out dtype");
   MIQ_REQUIRE(zero_offset == (float)(int)zero_offset && zero_offset >= 0.f && zero_offset <= 8.f, MIQ_ERR_UNSUPPORTED,
               "gptq_gemm: zero_offset %g (the exact fp16 path takes a small integer)", zero_offset);
+  MIQ_REQUIRE(!perm || K <= 32768, MIQ_ERR_UNSUPPORTED, "gptq_gemm: act-order with K=%d > 32768", K);
   GemmPlan p;
-  rc = gemm_plan(M, K, N, gs, workspace != nullptr, &p);
+  rc = gemm_plan(M, K, N, gs, &p);
   if (rc) return rc;
-  if (p.ksplit > 1) {
-    MIQ_REQUIRE(workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
-                "gptq_gemm: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes, workspace_bytes);
-  }
+  MIQ_REQUIRE(workspace && workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
+              "gptq_gemm: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  __half* xp = reinterpret_cast<__half*>(static_cast<char*>(workspace) + kCounterBytes + p.partial_bytes);
+  const __half* xin = static_cast<const __half*>(x);
+  if (perm) {
+    if (bits == 4) hipLaunchKernelGGL(gather_x_kernel<4>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xp, M, K, p.kc);
+    else hipLaunchKernelGGL(gather_x_kernel<8>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xp, M, K, p.kc);
+  } else {
+    const dim3 g((K / 8 + 255) / 256, M);
+    if (bits == 4) hipLaunchKernelGGL(stage_x_kernel<4>, g, dim3(256), 0, st, xin, xp, M, K, p.kc);
+    else hipLaunchKernelGGL(stage_x_kernel<8>, g, dim3(256), 0, st, xin, xp, M, K, p.kc);
+  }
+  rc = check_launch("gptq_gemm staging");
+  if (rc) return rc;
   if (bits == 4)
-    return gemm_dispatch<4>(p, x, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, workspace, M, K,
-                            N, gs, zero_offset, st);
-  return gemm_dispatch<8>(p, x, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, workspace, M, K, N,
-                          gs, zero_offset, st);
+    return gemm_dispatch<4>(p, xp, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, workspace, M, K, N, gs,
+                            zero_offset, st);
+  return gemm_dispatch<8>(p, xp, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, workspace, M, K, N, gs,
+                          zero_offset, st);
 }

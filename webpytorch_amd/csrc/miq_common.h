@@ -163,6 +163,55 @@ __device__ __forceinline__ half8v b_fragment(const uint4* w, int s, half2v zl, h
   }
 }
 
+// The same operand with the 8 values in k order (c0 c1 ... c7), for activations kept in memory
+// order. v_perm copies byte i of the word into bytes 0 and 2; its low nibble (c_2i) and high
+// nibble (c_2i+1, times 16) then sit in the low mantissa bits of the two halves, and one packed
+// fma with per-half factors (1, 1/16) and offsets zc = (-(1024 + z'), -(64 + z')) leaves the two
+// exact integers c - z'. int8: bytes 0 and 1 (then 2 and 3) of a word become the pair directly.
+template <int BITS> __device__ __forceinline__ half2v zero_consts_nat(uint32_t code, float zoff) {
+  const float zf = (float)code + zoff;
+  if constexpr (BITS == 4) return (half2v){(_Float16)(-(1024.f + zf)), (_Float16)(-(64.f + zf))};
+  else return (half2v){(_Float16)(-(1024.f + zf)), (_Float16)(-(1024.f + zf))};
+}
+template <int BITS>
+__device__ __forceinline__ half8v b_fragment_nat(const uint4* w, int s, half2v zc) {
+  const uint32_t w0 = (&w[0].x)[s];
+  if constexpr (BITS == 4) {
+    const half2v f = (half2v){(_Float16)1.0f, (_Float16)0.0625f};
+    half2v h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = __builtin_amdgcn_perm(w0, w0, (uint32_t)i | 0x0C00u | ((uint32_t)i << 16) | 0x0C000000u);
+      h[i] = __builtin_elementwise_fma(as_h2(and_or(t, 0x00F0000Fu, 0x64006400u)), f, zc);
+    }
+    return cat4(h[0], h[1], h[2], h[3]);
+  } else {
+    const uint32_t w1 = (&w[1].x)[s];
+    const uint32_t lo = 0x0C010C00u, hi = 0x0C030C02u;  // bytes (0, 1) and (2, 3) into the halves
+    return cat4(as_h2(__builtin_amdgcn_perm(w0, w0, lo) | 0x64006400u) + zc,
+                as_h2(__builtin_amdgcn_perm(w0, w0, hi) | 0x64006400u) + zc,
+                as_h2(__builtin_amdgcn_perm(w1, w1, lo) | 0x64006400u) + zc,
+                as_h2(__builtin_amdgcn_perm(w1, w1, hi) | 0x64006400u) + zc);
+  }
+}
+
+// ---- LDS DMA: each of the 64 lanes copies 16 (or 4) bytes from its own global address to LDS
+// at m0 + 16 * lane (4 * lane). Written as inline asm so that the compiler does not track it:
+// the caller waits for these loads itself (s_waitcnt vmcnt) and orders them with a barrier.
+typedef __attribute__((address_space(3))) const char lds_cchar;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_cchar*)p; }
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // Uniform (scalar) copy of a value that is the same in every lane.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
