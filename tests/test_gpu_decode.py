@@ -88,14 +88,15 @@ def test_attention_matches_oracle(gpu, pos, T):
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("pos", [0, 5, 37])
-def test_attention_decode_fused_rope_kv(gpu, pos):
+@pytest.mark.parametrize("pos,LMAX", [(0, 64), (5, 64), (37, 64), (255, 256), (37, 300), (290, 300)])
+def test_attention_decode_fused_rope_kv(gpu, pos, LMAX):
     """The one-token attention (RoPE + KV write + attention in one launch) against the oracle's
-    rope, cache append and attention."""
+    rope, cache append and attention; caches of up to 256 positions take the prefetching kernel,
+    longer ones the looping one."""
     import torch
     from webpytorch_amd import _lib
     from webpytorch_amd.core import ptr
-    NH, NKV, HD, LMAX = 14, 2, 64, 64
+    NH, NKV, HD = 14, 2, 64
     o = decode.Qwen2Oracle(synth.decoder_weights(1, L=1, H=128, NH=2, NKV=1, HD=64, I=128, V=64, gs=64), lmax=LMAX)
     rng = np.random.default_rng(pos)
     kc = rng.standard_normal((NKV, LMAX, HD)).astype(np.float32)

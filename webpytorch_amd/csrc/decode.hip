@@ -157,6 +157,87 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(
   for (int d = tid; d < HD; d += 256) out[(size_t)h * HD + d] = ((red[0][d] + red[1][d]) + red[2][d]) + red[3][d];
 }
 
+// The same for head dimension 64 and caches of at most 256 positions, with every load that does
+// not depend on the position issued at entry: the key row of position tid, the value column of
+// lane for positions wave + 4 i, and the new q/k/v. The kernel then waits for memory about twice
+// (position, then its RoPE row) instead of once per phase. Cache rows past the position are
+// read (in bounds) and masked: their scores are -inf and their values never enter the sum. The
+// arithmetic and its order are those of attention_decode_kernel.
+__global__ __launch_bounds__(256) void attention_decode_small_kernel(
+    const float* __restrict__ qkv, const int32_t* __restrict__ state, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, float* __restrict__ kc, float* __restrict__ vc, float* __restrict__ out, int NH,
+    int NKV, int LMAX, float scale) {
+  constexpr int HD = 64, HALF = 32;
+  __shared__ float qs[HD], kn[HD], vn[HD], red[4][HD], wred[8], sp[256];
+  const int h = blockIdx.x;
+  const int rep = NH / NKV, kv = h / rep;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* K = kc + (size_t)kv * LMAX * HD;
+  const float* Vv = vc + (size_t)kv * LMAX * HD;
+  float4 kr[HD / 4];
+  const float* krow = K + (size_t)min(tid, LMAX - 1) * HD;
+#pragma unroll
+  for (int i = 0; i < HD / 4; ++i) kr[i] = *reinterpret_cast<const float4*>(krow + 4 * i);
+  float vr[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) vr[i] = Vv[(size_t)min(wave + 4 * i, LMAX - 1) * HD + lane];
+  const int pos = state[0];
+  if (pos >= LMAX) return;  // uniform: the caller never runs past its cache
+  const int S = pos + 1;
+  if (tid < HD) {
+    const int d = tid, j = d < HALF ? d : d - HALF;
+    const float c = cos_t[(size_t)pos * HALF + j], s = sin_t[(size_t)pos * HALF + j];
+    qs[d] = rope1(qkv + h * HD, d, HALF, c, s);
+    kn[d] = rope1(qkv + (NH + kv) * HD, d, HALF, c, s);
+    vn[d] = qkv[(NH + NKV + kv) * HD + d];
+    if (h % rep == 0) {
+      kc[((size_t)kv * LMAX + pos) * HD + d] = kn[d];
+      vc[((size_t)kv * LMAX + pos) * HD + d] = vn[d];
+    }
+  }
+  __syncthreads();
+  float mx = -INFINITY;
+  if (tid < S) {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < HD / 4; ++i) {
+      const float4 k4 = tid == pos ? *reinterpret_cast<const float4*>(kn + 4 * i) : kr[i];
+      a = fmaf(qs[4 * i], k4.x, a);
+      a = fmaf(qs[4 * i + 1], k4.y, a);
+      a = fmaf(qs[4 * i + 2], k4.z, a);
+      a = fmaf(qs[4 * i + 3], k4.w, a);
+    }
+    a *= scale;
+    sp[tid] = a;
+    mx = a;
+  }
+  mx = wave_max(mx);
+  if (lane == 0) wred[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+  float sum = 0.f;
+  if (tid < S) {
+    const float e = expf(sp[tid] - mx);
+    sp[tid] = e;
+    sum = e;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) wred[4 + wave] = sum;
+  __syncthreads();
+  sum = (wred[4] + wred[5]) + (wred[6] + wred[7]);
+  if (tid < S) sp[tid] = sp[tid] / sum;
+  __syncthreads();
+  float o = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const int j = wave + 4 * i;
+    if (j < S) o = fmaf(sp[j], j == pos ? vn[lane] : vr[i], o);
+  }
+  red[wave][lane] = o;
+  __syncthreads();
+  if (tid < HD) out[(size_t)h * HD + tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+}
+
 // Causal grouped-query attention: token t (position pos0 + t) of query head h attends to
 // cache positions 0 .. pos0 + t of kv head h / (NH / NKV). One wave per (head, token):
 // lanes over positions for the scores, lanes over the head dimension for the output.
@@ -334,8 +415,12 @@ extern "C" int miq_attention_decode(const float* qkv, const int32_t* state, cons
   MIQ_REQUIRE(qkv && state && cos_tab && sin_tab && kcache && vcache && out, MIQ_ERR_INVALID,
               "attention_decode: null pointer");
   MIQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), MIQ_ERR_ALIGN, "attention_decode: caches must be 16-byte aligned");
-  hipLaunchKernelGGL(attention_decode_kernel, dim3(NH), dim3(256), (size_t)LMAX * 4, static_cast<hipStream_t>(stream),
-                     qkv, state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV, HD, LMAX, scale);
+  if (HD == 64 && LMAX <= 256)
+    hipLaunchKernelGGL(attention_decode_small_kernel, dim3(NH), dim3(256), 0, static_cast<hipStream_t>(stream), qkv,
+                       state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV, LMAX, scale);
+  else
+    hipLaunchKernelGGL(attention_decode_kernel, dim3(NH), dim3(256), (size_t)LMAX * 4, static_cast<hipStream_t>(stream),
+                       qkv, state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV, HD, LMAX, scale);
   return check_launch("attention_decode");
 }
 
