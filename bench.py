@@ -250,6 +250,33 @@ def gemv_only(torch, core, steps):
     return t, kernels
 
 
+def copy_calibration(torch, nbytes=512 << 20, reps=4):
+    """A plain device copy of `nbytes` (fp32 elementwise copy kernel), `reps` times: reads and
+    writes exactly `nbytes` each, the scale for the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.rand(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return nbytes
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gptq_gemv_hbm_traffic_qwen2_05b_int4.md")
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch of the decode token, from the committed FETCH_SIZE / WRITE_SIZE
+    counter summary (its `traffic_bytes_per_launch:` line), or None if that summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":")[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +285,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extras", action="store_true", help="only the decode step and its roofline")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the roofline workload (the token's GEMVs alone) and a plain 512 MiB copy, "
+                         "for hardware-counter runs")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized-linear path has no multi-GPU mode here "
@@ -268,6 +298,12 @@ def main():
     from webpytorch_amd import core, llm, synth
     torch.cuda.set_device(0)
     torch.manual_seed(0)
+    if a.gemv_only:
+        t_gemv, kernels = gemv_only(torch, core, a.steps)
+        copy_bytes = copy_calibration(torch)
+        print(json.dumps({"gemv_step_us": round(t_gemv * 1e6, 2), "gemv_shapes": kernels,
+                          "copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes}), flush=True)
+        return
 
     prompt = 64
     lmax = max(256, prompt + a.warmup + a.steps + 2)
@@ -306,7 +342,9 @@ def main():
         "decode_tokens_per_s": round(1.0 / t_step, 1),
         "ttft_ms": round(r.ttft_s * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_note": "HBM bytes per launch (FETCH_SIZE + WRITE_SIZE over the same GEMVs, "
+                                     "scaled by the counters' reading for a plain copy of known size)",
                      "kernel": "miq::gptq_gemv_kernel",
                      "measured_on": "the 97 GEMVs of a token alone, 2 alternating weight copies (522 MB)",
                      "avg_launch_us": round(t_gemv / launches * 1e6, 3),
