@@ -236,6 +236,42 @@ int miq_add(float* h, const float* y, int64_t n, void* stream);
 int miq_argmax_advance(const float* logits, int V, int32_t* ids, int32_t* history, int hist_len,
                        int32_t* state, int advance, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Persistent decode step: the whole one-token step of an int4 GPTQ Qwen2-style decoder
+ * (embedding, L x [RMSNorm, q|k|v + bias, RoPE + KV write + GQA attention, o + residual,
+ * RMSNorm, gate|up, SwiGLU, down + residual], final RMSNorm, tied int4 head, greedy argmax
+ * and the state advance of miq_argmax_advance) in ONE launch of one 1024-thread workgroup per
+ * CU. Workgroups pass activations through tagged device-scope words in the workspace instead
+ * of kernel boundaries, and every projection's weights are loaded a layer ahead.
+ * Replaces: the captured one-token step `_decode_fwd` (webtorch/llm.py:1591-1616) replayed by
+ * capture-replay (webtorch/llm.py:19-20), i.e. the same work as the launch sequence
+ * miq_embed, L x (miq_gptq_gemv_fused, miq_attention_decode, miq_gptq_gemv,
+ * miq_gptq_gemv_fused x2), miq_gptq_gemv_fused, miq_argmax_advance.
+ *
+ * miq_decode_persistent_plan: MIQ_OK and the grid (= CU count) and workspace bytes if the
+ * shape is supported (bits 4, HD 64, H, (NH + 2 NKV) HD and 2I multiples of 64, H / 8 and
+ * NH HD / 8 packed rows within 16 x min(16, gs / 8), LMAX <= 8192, the role workgroups
+ * fitting the CU count), else MIQ_ERR_UNSUPPORTED (use the launch sequence above).
+ *
+ * layer_table: device array [L][20] of uint64 addresses per layer, in this order: q|k|v
+ * qweight, qzeros, fp16 scales, fp32 bias (0 if none); o qweight, qzeros, scales; gate|up
+ * qweight, qzeros, scales; down qweight, qzeros, scales; input RMSNorm weight, post-attention
+ * RMSNorm weight (fp32 [H]); k cache, v cache (fp32 [NKV][LMAX][64]); 3 unused slots.
+ * Layers use zero offset zoff, the head (int4, fp32 scales [H/gs][V]) head_zoff; embed is
+ * fp16 [V][H]. logits [V] receives the head output. ws: 256-byte aligned, zeroed before the
+ * first step and again after any error; uint32 word 0 counts finished steps and word 1 holds
+ * error bits (1: a workgroup waited more than 100 ms -- not all workgroups were resident --
+ * 2: state[0] >= LMAX), read by the caller after the step. Steps on one workspace must not
+ * overlap, and the step must not share the GPU with other kernels. */
+int miq_decode_persistent_plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs,
+                               int bits, int* grid, size_t* ws_bytes);
+int miq_decode_persistent(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
+                          const int32_t* head_qzeros, const float* head_scales, const float* final_norm,
+                          const float* cos_tab, const float* sin_tab, int32_t* ids, int32_t* history,
+                          int hist_len, int32_t* state, float* logits, void* ws, size_t ws_bytes, int L,
+                          int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits,
+                          float eps, float zoff, float head_zoff, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

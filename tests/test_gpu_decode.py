@@ -234,3 +234,61 @@ def test_decode_full_shape_logits_vs_oracle(gpu):
         bad = np.abs(got - ref) > 1e-3 + 1e-2 * np.abs(ref)
         assert not bad.any(), np.abs(got - ref).max()
         assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-4
+
+
+def _persistent_pair(sh, seed, lmax, prompt):
+    from webpytorch_amd import llm
+    w = synth.decoder_weights(seed, gaussian=True, **sh)
+    ids = synth.prompt_ids(seed, prompt, sh["V"])
+    a = llm.CausalLM.from_weights(w, lmax=lmax, persistent=True)
+    b = llm.CausalLM.from_weights(w, lmax=lmax, persistent=False)
+    assert a.pws is not None and b.pws is None
+    return a, b, ids
+
+
+@pytest.mark.parametrize("prompt,steps,lmax", [(16, 24, 64), (270, 40, 320)])
+def test_persistent_step_matches_launch_sequence(gpu, prompt, steps, lmax):
+    """The one-launch persistent step against the launch sequence (5 launches per layer) on the
+    same model after the same prefill: identical greedy ids and per-step logits within 1e-4
+    relative; the second case runs past 256 cached positions (the attention's second chunk)."""
+    import torch
+    sh = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+    a, b, ids = _persistent_pair(sh, 14, lmax, prompt)
+    for m in (a, b):
+        m.generate(ids, 1, use_graph=False)
+    for step in range(steps):
+        for m in (a, b):
+            m._step(1)
+        torch.cuda.synchronize()
+        la, lb = a.buf["logits"][0].cpu().numpy(), b.buf["logits"][0].cpu().numpy()
+        assert int(a.history[step + 1]) == int(b.history[step + 1]), step
+        np.testing.assert_allclose(la, lb, rtol=1e-4, atol=1e-4 * np.abs(lb).max())
+    assert a.persistent_error() == 0
+    assert np.array_equal(a.state[:4].cpu().numpy(), b.state[:4].cpu().numpy())
+    # the caches the persistent step wrote are the ones the launch sequence wrote (both fp32
+    # accumulations; the persistent step's bf16-split matrix-core products carry a 128-bias
+    # that cancels to ~1e-6 of the values' scale)
+    n = prompt + steps
+    for ca, cb in ((a.kc, b.kc), (a.vc, b.vc)):
+        ga, gb = ca[:, :, :n].cpu().numpy(), cb[:, :, :n].cpu().numpy()
+        np.testing.assert_allclose(ga, gb, rtol=1e-4, atol=1e-4 * np.abs(gb).max())
+
+
+def test_persistent_step_graph_replay_and_position_guard(gpu):
+    """Graph-replayed persistent steps give the eager ids; a step at position LMAX does no work
+    and reports error bit 2 (every workgroup leaves at entry), and reset() clears it."""
+    import torch
+    sh = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+    a, b, ids = _persistent_pair(sh, 14, 64, 16)
+    want = b.generate(ids, 20).tokens
+    assert a.generate(ids, 20).tokens == want
+    assert a.generate(ids, 20, use_graph=False).tokens == want
+    a.state[0] = a.lmax
+    hist = a.history.clone()
+    a._step(1)
+    torch.cuda.synchronize()
+    assert a.persistent_error() == 2
+    assert torch.equal(a.history, hist) and int(a.state[0]) == a.lmax
+    a.reset()
+    assert a.persistent_error() == 0
+    assert a.generate(ids, 20).tokens == want

@@ -1,0 +1,906 @@
+// Persistent decode step for gfx950: one launch per token for a Qwen2-style int4 GPTQ decoder
+// (the captured one-token step of `webtorch/llm.py:1591-1616`), with no grid-wide barrier.
+//
+// Every workgroup (1024 threads, one per CU) has a role for all layers: a 64-column tile of
+// the q|k|v, o or gate|up projection, a query head of the attention, or a (64-column tile,
+// K-slice) of the down projection. Workgroups hand results to each other through small
+// exchange buffers of tagged 64-bit words -- (tag << 32) | fp32 bits -- written and read at
+// device scope (they bypass the per-XCD L2). A consumer polls the words it needs until every
+// one carries the tag of the current (token, layer, phase); a tag never repeats between
+// consecutive tokens, so no flag, counter or reset is needed. A role's weights for layer l are
+// issued as soon as its layer l-1 work is stored, a whole layer ahead of their use, so the
+// critical path per projection is one hop (store -> poll) plus its arithmetic; the HBM
+// traffic of the weights overlaps the chain of dependent steps.
+//
+// After the last layer every workgroup takes 64-column tiles of the tied head, keeps a
+// running arg-max, and publishes it; workgroup 0 combines the partials in workgroup order,
+// writes the token id, appends it to the history and advances the position, exactly as
+// argmax_kernel does.
+//
+// Waits are bounded: a workgroup that is still waiting `spin_limit` wall-clock ticks after it
+// started sets an error bit and leaves, so every wait chain ends and the grid drains (the
+// host reads the bit). All workgroups must be resident at once; the host sizes the grid to
+// the CU count and checks occupancy, and the step must not share the GPU with other work.
+//
+// Control words at the start of the workspace (uint32): [0] epoch of the last token done,
+// [1] error bits (1: wait timed out, 2: position past the cache).
+#include <math.h>
+
+#include <algorithm>
+
+#include "miq_common.h"
+
+// The elementwise steps (RMSNorm, RoPE, SiLU, softmax) round every product and sum separately,
+// as the reference's numpy expressions do; explicit fmaf() calls are unaffected.
+#pragma clang fp contract(off)
+
+namespace miq {
+namespace pd {
+
+constexpr int kThreads = 1024, kWaves = 16, kTile = 64, kMaxSPQ = 16, kSlots = 20;
+enum Slot { QKV_QW, QKV_QZ, QKV_SC, QKV_B, O_QW, O_QZ, O_SC, GU_QW, GU_QZ, GU_SC, D_QW, D_QZ, D_SC, IN_LN, POST_LN, KC, VC };
+enum Phase { P_QKV = 0, P_ATT = 1, P_HMID = 2, P_GU = 3, P_DOWN = 4, P_AMAX = 5 };
+
+struct Params {
+  const uint64_t* layers;  // [L][kSlots] device addresses, indexed by Slot
+  const __half* embed;
+  const uint32_t* head_qw;
+  const uint32_t* head_qz;
+  const float* head_sc;
+  const float* final_norm;
+  const float* cos_t;
+  const float* sin_t;
+  int32_t* ids;
+  int32_t* history;
+  int32_t* state;
+  float* logits;
+  uint32_t* ctl;
+  uint64_t *tq, *tatt, *thmid, *tgu, *tdown, *tamax;
+  int L, H, NH, NKV, I, V, LMAX, gs, lgs, hist_len, ksd;  // lgs = log2(gs)
+  int nq, na, no, ngu, nd;  // workgroups per role (nd = no * ksd)
+  int lds_a, lds_x;         // LDS regions (floats): exchange/staging, activations
+  float eps, scale, zoff, head_zoff;
+  long long spin_limit;
+#ifdef MIQ_PD_TRACE
+  unsigned long long* trace;  // [G][L + 2][8] wall-clock stamps of the phase marks below
+#endif
+};
+
+// Phase marks (stage k of layer l of this workgroup); empty unless built with MIQ_PD_TRACE.
+#ifdef MIQ_PD_TRACE
+#define PD_MARK(l, k)                                                                          \
+  do {                                                                                         \
+    if (threadIdx.x == 0) p.trace[((size_t)blockIdx.x * (p.L + 2) + (l)) * 8 + (k)] = wall_clock64(); \
+  } while (0)
+#else
+#define PD_MARK(l, k) \
+  do {                \
+  } while (0)
+#endif
+
+__device__ __forceinline__ void tput(uint64_t* p, uint32_t tag, float v) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t tget(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The thread index as a value the compiler cannot see through: index math derived from it is
+// recomputed where it is used (a few instructions per layer) instead of being hoisted out of
+// the layer loop and held in registers for the whole token.
+__device__ __forceinline__ int opaque_tid() {
+  int v = threadIdx.x;
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+struct Ctx {
+  long long deadline;
+  uint32_t ep;
+  int L;
+  __device__ uint32_t tag(int l, int ph) const { return ep * (uint32_t)(8 * (L + 1)) + 8u * (uint32_t)l + (uint32_t)ph; }
+};
+
+// Polls n tagged words (word i at addr(i)) until word i carries tagf(i), leaving their values
+// in dst[0..n) (LDS). Called by the whole workgroup with the same arguments; n <= NPL * 1024.
+// Returns false (uniformly) once the workgroup's deadline has passed.
+template <int NPL, typename F, typename T>
+__device__ bool wait_tagged(int n, const Ctx& c, F addr, T tagf, float* dst) {
+  const int tid = opaque_tid();
+  for (;;) {
+    uint64_t v[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) v[j] = tget(addr(min(tid + j * kThreads, n - 1)));
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int i = tid + j * kThreads;
+      if (i < n) {
+        ok &= (uint32_t)(v[j] >> 32) == tagf(i);
+        dst[i] = __uint_as_float((uint32_t)v[j]);
+      }
+    }
+    if (__syncthreads_and(ok)) return true;
+    if (__syncthreads_or(wall_clock64() > c.deadline)) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// Sum over the workgroup, combined in wave order (every thread gets the total).
+__device__ __forceinline__ float block_sum(float v, float* red16) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red16[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) t += red16[w];
+  return t;
+}
+__device__ __forceinline__ float block_max(float v, float* red16) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red16[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = red16[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) t = fmaxf(t, red16[w]);
+  return t;
+}
+
+// ---- 64-column int4 tile on the matrix cores ----------------------------------------------
+// The activations x (fp32) are split exactly into three bf16 terms, x = b1 + b2 + b3 (b1 =
+// bf16(x), b2 = bf16(x - b1), b3 = x - b1 - b2, which fits bf16), which become rows 0-2 of the
+// A operand of v_mfma_f32_16x16x32_bf16; the codes become the B operand with no conversion
+// instruction per value: OR-ing a code c into mantissa bits 0-3 of 128.0 (bf16 0x4300, whose
+// mantissa step is 1) gives 128 + c; a code of the upper nibble of a byte, shifted down one bit
+// into mantissa bits 3-6 (bf16 has 7 mantissa bits, so bit 7 is the exponent's), gives
+// 128 + 8c, matched by x / 8 in A. Products of bf16 values are exact in fp32, so rows 0-2 of D
+// sum to sum_k x_k (128 + c_k) or (x_k / 8)(128 + 8 c_k) in fp32; the per-step bias sums (128
+// or 16 times the x of each kind) and x sums are subtracted per quantization group with the
+// zero point: acc += s_g * (p - (bias + z_g * sum x)).
+//
+// A 32-k step of A is staged in LDS as 4 k-blocks (one per 16 lanes) x 4 slots (the three
+// bf16 terms and a zero slot for lanes whose A row is 3..15) x 8 values, 256 bytes.
+// Wave w of the 16 takes the 16 columns (w & 3) of the 64-column tile and the k-quarter
+// (w >> 2) of the steps; lane l loads packed row (l >> 4) of each step for column l & 15, which
+// is exactly its B fragment (column l & 15, k 8 (l >> 4) .. + 7).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kStepBytes = 256;
+
+template <typename ST, int SPQ>
+struct Tile {
+  uint32_t w[SPQ];
+  uint32_t z[SPQ];
+  float s[SPQ];
+  int st0, ns;  // first step and step count of this wave
+};
+
+// Issues this wave's loads for the tile of columns [c0, c0 + 64) (clamped to N - 1) over the
+// nsteps 32-k steps starting at packed row rb (absolute, for the group index; groups are
+// 2^lgs values, 2^(lgs - 3) packed rows).
+template <typename ST, int SPQ>
+__device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw, const uint32_t* qz, const ST* sc,
+                                           int N, int c0, int rb, int nsteps, int lgs) {
+  const int tid = opaque_tid();
+  const int wave = uniform(tid >> 6), lane = tid & 63;
+  const int spq = (nsteps + 3) >> 2;
+  t.st0 = (wave >> 2) * spq;
+  t.ns = max(0, min(spq, nsteps - t.st0));
+  const int c = min(c0 + (wave & 3) * 16 + (lane & 15), N - 1);
+  const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
+  const uint32_t* wp = qw + (uint32_t)((r0 + (lane >> 4)) * N + c);
+#pragma unroll
+  for (int i = 0; i < SPQ; ++i) {
+    if (i < t.ns) {
+      const int g = (r0 + 4 * i) >> gsh;
+      t.w[i] = wp[(uint32_t)(4 * i * N)];
+      t.s[i] = to_f32(sc[(uint32_t)(g * N + c)]);
+      t.z[i] = qz[(uint32_t)(g * (N >> 3) + (c >> 3))];
+    }
+  }
+}
+
+// This wave's share of sum_k x_k W[k][c] (valid in lanes 0..15, column c0 + 16 (w & 3) + lane).
+template <typename ST, int SPQ>
+__device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float* corr,
+                                          const float* xsum, int rb, int c0, int lgs, float zoff) {
+  const int tid = opaque_tid();
+  const int wave = uniform(tid >> 6), lane = tid & 63;
+  const int sh = ((c0 + (wave & 3) * 16 + (lane & 15)) & 7) * 4;
+  const unsigned char* ap = xa + t.st0 * kStepBytes + (lane >> 4) * 64 + min(lane & 15, 3) * 16;
+  const float* cp = corr + t.st0;
+  const float* xp = xsum + t.st0;
+  const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
+  floatx4 d = {0.f, 0.f, 0.f, 0.f};
+  float acc = 0.f, cs = 0.f, xs = 0.f;
+#pragma unroll
+  for (int i = 0; i < SPQ; ++i) {
+    if (i < t.ns) {
+      const bf16x8 av = *reinterpret_cast<const bf16x8*>(ap + i * kStepBytes);
+      // halves (c0, c4) (8 c1, 8 c5) (c2, c6) (8 c3, 8 c7) over 128
+      const uint32_t w = t.w[i];
+      const u32x4 bw = {and_or(w, 0x000F000Fu, 0x43004300u), and_or(w >> 1, 0x00780078u, 0x43004300u),
+                        and_or(w >> 8, 0x000F000Fu, 0x43004300u), and_or(w >> 9, 0x00780078u, 0x43004300u)};
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
+      cs += cp[i];
+      xs += xp[i];
+      const int r = r0 + 4 * i;
+      if (i + 1 == t.ns || ((r + 4) >> gsh) != (r >> gsh)) {  // last step of this group
+        const float pv = (d[0] + d[1]) + d[2];
+        const float zc = (float)((t.z[i] >> sh) & 15u) + zoff;
+        acc = fmaf(t.s[i], pv - fmaf(zc, xs, cs), acc);
+        d = (floatx4){0.f, 0.f, 0.f, 0.f};
+        cs = 0.f;
+        xs = 0.f;
+      }
+    }
+  }
+  return acc;
+}
+
+// Sums the four k-quarters of each column in quarter order; valid in threads 0..63 (column
+// c0 + thread).
+__device__ __forceinline__ float tile_sum(float acc, float* red) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane < 16) red[(wave >> 2) * 64 + (wave & 3) * 16 + lane] = acc;
+  __syncthreads();
+  float y = 0.f;
+  if (threadIdx.x < 64) {
+    const int t = threadIdx.x;
+    y = ((red[t] + red[64 + t]) + red[128 + t]) + red[192 + t];
+  }
+  return y;
+}
+
+// Stages K fp32 activations (LDS) as the A operand of K / 32 steps, with each step's bias sum
+// (128 x the x of codes in bits 0-3 of a byte, 16 x the others) and x sum.
+__device__ __forceinline__ void stage_a(const float* x, int K, unsigned char* xa, float* corr, float* xsum) {
+  const int nch = K / 8;  // 8-value k-blocks, 4 per step
+  const int tid = opaque_tid();
+  for (int ch0 = 0; ch0 < nch; ch0 += kThreads) {
+    const int ch = ch0 + tid;
+    if (ch < nch) {  // all four blocks of a step are present together (K % 32 == 0)
+      const float4 va = *reinterpret_cast<const float4*>(x + ch * 8);
+      const float4 vb = *reinterpret_cast<const float4*>(x + ch * 8 + 4);
+      const float o[8] = {va.x, vb.x, va.y * 0.125f, vb.y * 0.125f, va.z, vb.z, va.w * 0.125f, vb.w * 0.125f};
+      bf16x8 t1, t2, t3;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const __bf16 b1 = (__bf16)o[j];
+        const float r1 = o[j] - (float)b1;
+        const __bf16 b2 = (__bf16)r1;
+        t1[j] = b1;
+        t2[j] = b2;
+        t3[j] = (__bf16)(r1 - (float)b2);
+      }
+      unsigned char* dst = xa + (ch >> 2) * kStepBytes + (ch & 3) * 64;
+      *reinterpret_cast<bf16x8*>(dst) = t1;
+      *reinterpret_cast<bf16x8*>(dst + 16) = t2;
+      *reinterpret_cast<bf16x8*>(dst + 32) = t3;
+      *reinterpret_cast<u32x4*>(dst + 48) = (u32x4){0u, 0u, 0u, 0u};
+      const float lo = (va.x + va.z) + (vb.x + vb.z), hi = (va.y + va.w) + (vb.y + vb.w);
+      float cb = 128.f * lo + 16.f * hi, sm = lo + hi;
+      cb += __shfl_xor(cb, 1, 64);
+      cb += __shfl_xor(cb, 2, 64);
+      sm += __shfl_xor(sm, 1, 64);
+      sm += __shfl_xor(sm, 2, 64);
+      if ((ch & 3) == 0) {
+        corr[ch >> 2] = cb;
+        xsum[ch >> 2] = sm;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// RMSNorm weights of the H <= 2048 columns this thread normalizes, loaded ahead of the wait.
+struct NormW {
+  float v[2];
+};
+__device__ __forceinline__ void norm_prefetch(NormW& nw, const float* w, int H) {
+  nw.v[0] = (int)threadIdx.x < H ? w[threadIdx.x] : 0.f;
+  nw.v[1] = (int)threadIdx.x + kThreads < H ? w[threadIdx.x + kThreads] : 0.f;
+}
+
+// h = h / sqrt(mean(h^2) + eps) * w in place (h in LDS, H <= 2048).
+__device__ __forceinline__ void rmsnorm_inplace(float* h, const NormW& nw, int H, float eps, float* red16) {
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += kThreads) ss = ss + h[i] * h[i];
+  const float r = sqrtf(block_sum(ss, red16) / (float)H + eps);
+  if ((int)threadIdx.x < H) h[threadIdx.x] = (h[threadIdx.x] / r) * nw.v[0];
+  if ((int)threadIdx.x + kThreads < H) h[threadIdx.x + kThreads] = (h[threadIdx.x + kThreads] / r) * nw.v[1];
+  __syncthreads();
+}
+
+__device__ __forceinline__ float rope1(const float* row, int d, int half, float c, float s) {
+  const float rv = d < half ? -row[d + half] : row[d - half];
+  return row[d] * c + rv * s;
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// LDS carve-up: hin (exchange words and scratch), xs (fp32 activations), xa (A operand steps),
+// corr / xsum (per step), red (4 quarters x 64 columns), red16 (wave scalars), qkv (rotated q, k
+// and the new v).
+struct Lds {
+  float *hin, *xs;
+  unsigned char* xa;
+  float *corr, *xsum, *red, *red16, *qkv;
+};
+
+#define MIQ_PD_INLINE __device__ __attribute__((always_inline)) inline
+
+// h(l) of the H columns into dst: layer 0 is the current token's embedding row; later layers
+// sum the down projection's K-slices in slice order and then add the residual hmid(l - 1),
+// as the split-K GEMV with the residual as its bias does.
+MIQ_PD_INLINE bool load_h_full(const Params& p, const Ctx& c, int l, int tok, float* dst, float* raw) {
+  const int H = p.H, ks = p.ksd;
+  if (l == 0) {
+    for (int i = threadIdx.x; i < H; i += kThreads)
+      dst[i] = (tok >= 0 && tok < p.V) ? __half2float(p.embed[(size_t)tok * H + i]) : 0.f;
+    __syncthreads();
+    return true;
+  }
+  const uint32_t td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
+  const bool ok = wait_tagged<8>(
+      (ks + 1) * H, c,
+      [&](int j) -> const uint64_t* { return j < ks * H ? p.tdown + j : p.thmid + (j - ks * H); },
+      [&](int j) { return j < ks * H ? td : th; }, raw);
+  if (!ok) return false;
+  for (int i = threadIdx.x; i < H; i += kThreads) {
+    float h = raw[i];
+    for (int sl = 1; sl < ks; ++sl) h += raw[sl * H + i];
+    dst[i] = h + raw[ks * H + i];
+  }
+  __syncthreads();
+  return true;
+}
+
+// q|k|v projection, columns [64 t, 64 t + 64): RMSNorm(h(l)) @ Wqkv + bias.
+template <int SA>
+MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
+  const int H = p.H, NQ = (p.NH + 2 * p.NKV) * 64, c0 = t * kTile;
+  for (int l = 0; l < p.L; ++l) {
+    const uint64_t* lt = p.layers + (size_t)l * kSlots;
+    Tile<__half, SA> w;
+    tile_issue(w, (const uint32_t*)lt[QKV_QW], (const uint32_t*)lt[QKV_QZ], (const __half*)lt[QKV_SC], NQ, c0, 0,
+               H / 32, p.lgs);
+    NormW nw;
+    norm_prefetch(nw, (const float*)lt[IN_LN], H);
+    const float* bias = (const float*)lt[QKV_B];
+    const float bv = (bias && threadIdx.x < 64) ? bias[min(c0 + (int)threadIdx.x, NQ - 1)] : 0.f;
+    PD_MARK(l, 0);
+    if (!load_h_full(p, c, l, tok, s.xs, s.hin)) return false;
+    PD_MARK(l, 1);
+    rmsnorm_inplace(s.xs, nw, H, p.eps, s.red16);
+    stage_a(s.xs, H, s.xa, s.corr, s.xsum);
+    PD_MARK(l, 3);
+    float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.zoff), s.red);
+    PD_MARK(l, 4);
+    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < NQ) {
+      if (bias) y += bv;
+      tput(p.tq + c0 + threadIdx.x, c.tag(l, P_QKV), y);
+    }
+    PD_MARK(l, 2);
+    __syncthreads();
+  }
+  return true;
+}
+
+// Attention of query head hq at position pos over positions 0..pos: RoPE of q and of the kv
+// head's new k (the first query head of each group writes k and v into the caches), scores
+// (q . k) * scale, softmax, sum p v. Four threads per position for the scores, a wave per
+// residue of the position mod 16 and a lane per dimension for the weighted sum. The cache
+// rows of the first 256 positions and the RoPE row are loaded before q/k/v are waited for.
+MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq, int pos) {
+  const int NH = p.NH, NKV = p.NKV, LMAX = p.LMAX, rep = NH / NKV, g = hq / rep, S = pos + 1;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qq = tid & 3, jq = tid >> 2;
+  float* sp = s.hin + 256;  // scores -> probabilities [S]
+  float* qs = s.qkv;
+  float* kn = s.qkv + 64;
+  float* vn = s.qkv + 128;
+  const int jr = (tid & 63) < 32 ? (tid & 63) : (tid & 63) - 32;
+  const float cs = p.cos_t[(size_t)pos * 32 + jr], sn = p.sin_t[(size_t)pos * 32 + jr];
+  for (int l = 0; l < p.L; ++l) {
+    const uint64_t* lt = p.layers + (size_t)l * kSlots;
+    float* kc = (float*)lt[KC] + (size_t)g * LMAX * 64;
+    float* vc = (float*)lt[VC] + (size_t)g * LMAX * 64;
+    float4 kr[4];
+    {
+      const float* kp = kc + (size_t)min(jq, LMAX - 1) * 64 + qq * 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const float4*>(kp + 4 * i);
+    }
+    float vr[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) vr[i] = vc[(size_t)min(wave + 16 * i, LMAX - 1) * 64 + lane];
+    const uint32_t tg = c.tag(l, P_QKV);
+    PD_MARK(l, 0);
+    const bool ok = wait_tagged<1>(
+        192, c,
+        [&](int i) -> const uint64_t* {
+          return p.tq + (i < 64 ? hq * 64 + i : i < 128 ? (NH + g) * 64 + (i - 64) : (NH + NKV + g) * 64 + (i - 128));
+        },
+        [&](int) { return tg; }, s.hin);
+    if (!ok) return false;
+    PD_MARK(l, 1);
+    if (tid < 64) {
+      const int d = tid;
+      qs[d] = rope1(s.hin, d, 32, cs, sn);
+      kn[d] = rope1(s.hin + 64, d, 32, cs, sn);
+      vn[d] = s.hin[128 + d];
+      if (hq % rep == 0) {
+        kc[(size_t)pos * 64 + d] = kn[d];
+        vc[(size_t)pos * 64 + d] = vn[d];
+      }
+    }
+    __syncthreads();
+    for (int cb = 0; cb < S; cb += 256) {
+      const int j = cb + jq;
+      float4 k4[4];
+      if (cb == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) k4[i] = kr[i];
+      } else {
+        const float* kp = kc + (size_t)min(j, LMAX - 1) * 64 + qq * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kp + 4 * i);
+      }
+      if (j == pos) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kn + qq * 16 + 4 * i);
+      }
+      const float* qp = qs + qq * 16;
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a = fmaf(qp[4 * i], k4[i].x, a);
+        a = fmaf(qp[4 * i + 1], k4[i].y, a);
+        a = fmaf(qp[4 * i + 2], k4[i].z, a);
+        a = fmaf(qp[4 * i + 3], k4[i].w, a);
+      }
+      a = a + __shfl_xor(a, 1, 64);
+      a = a + __shfl_xor(a, 2, 64);
+      if (qq == 0 && j < S) sp[j] = a * p.scale;
+    }
+    __syncthreads();
+    PD_MARK(l, 3);
+    float mx = -INFINITY;
+    for (int j = tid; j < S; j += kThreads) mx = fmaxf(mx, sp[j]);
+    mx = block_max(mx, s.red16);
+    float sum = 0.f;
+    for (int j = tid; j < S; j += kThreads) {
+      const float e = expf(sp[j] - mx);
+      sp[j] = e;
+      sum += e;
+    }
+    sum = block_sum(sum, s.red16 + 16);
+    for (int j = tid; j < S; j += kThreads) sp[j] = sp[j] / sum;
+    __syncthreads();
+    PD_MARK(l, 4);
+    float o = 0.f;
+    for (int cb = 0; cb < S; cb += 256) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int j = cb + wave + 16 * i;
+        if (j < S) {
+          const float v = j == pos ? vn[lane] : cb == 0 ? vr[i] : vc[(size_t)j * 64 + lane];
+          o = fmaf(sp[j], v, o);
+        }
+      }
+    }
+    // 16 waves' partial sums, combined in wave order (over the scores, once all are read)
+    __syncthreads();
+    s.hin[wave * 64 + lane] = o;
+    __syncthreads();
+    if (tid < 64) {
+      float y = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) y += s.hin[w * 64 + tid];
+      tput(p.tatt + hq * 64 + tid, c.tag(l, P_ATT), y);
+    }
+    PD_MARK(l, 2);
+    __syncthreads();
+  }
+  return true;
+}
+
+// o projection, columns [64 t, 64 t + 64) of H: h(l) + att(l) @ Wo.
+template <int SA>
+MIQ_PD_INLINE bool role_o(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
+  const int H = p.H, NHD = p.NH * 64, ks = p.ksd, c0 = t * kTile;
+  const int lane = threadIdx.x & 63;
+  for (int l = 0; l < p.L; ++l) {
+    const uint64_t* lt = p.layers + (size_t)l * kSlots;
+    Tile<__half, SA> w;
+    tile_issue(w, (const uint32_t*)lt[O_QW], (const uint32_t*)lt[O_QZ], (const __half*)lt[O_SC], H, c0, 0, NHD / 32,
+               p.lgs);
+    // words: att (NHD), then for l > 0 the residual h(l) of these columns: ks slices + hmid
+    const int nres = l == 0 ? 0 : (ks + 1) * kTile;
+    const uint32_t ta = c.tag(l, P_ATT), td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
+    PD_MARK(l, 0);
+    const bool ok = wait_tagged<4>(
+        NHD + nres, c,
+        [&](int i) -> const uint64_t* {
+          if (i < NHD) return p.tatt + i;
+          const int j = i - NHD, sl = j / kTile, cc = c0 + (j - sl * kTile);
+          return sl < ks ? p.tdown + (size_t)sl * H + cc : p.thmid + cc;
+        },
+        [&](int i) { return i < NHD ? ta : ((i - NHD) / kTile < ks ? td : th); }, s.hin);
+    if (!ok) return false;
+    PD_MARK(l, 1);
+    float hres = 0.f;
+    if (threadIdx.x < 64) {
+      if (l == 0) {
+        hres = (tok >= 0 && tok < p.V) ? __half2float(p.embed[(size_t)tok * H + min(c0 + lane, H - 1)]) : 0.f;
+      } else {
+        const float* r = s.hin + NHD;
+        hres = r[lane];
+        for (int sl = 1; sl < ks; ++sl) hres += r[sl * kTile + lane];
+        hres = hres + r[ks * kTile + lane];
+      }
+    }
+    stage_a(s.hin, NHD, s.xa, s.corr, s.xsum);
+    PD_MARK(l, 3);
+    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.zoff), s.red);
+    PD_MARK(l, 4);
+    if (threadIdx.x < 64 && c0 + lane < H) tput(p.thmid + c0 + lane, c.tag(l, P_HMID), y + hres);
+    PD_MARK(l, 2);
+    __syncthreads();
+  }
+  return true;
+}
+
+// gate|up projection, columns [64 t, 64 t + 64) of 2I: RMSNorm(hmid(l)) @ Wgu.
+template <int SA>
+MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
+  const int H = p.H, N = 2 * p.I, c0 = t * kTile;
+  for (int l = 0; l < p.L; ++l) {
+    const uint64_t* lt = p.layers + (size_t)l * kSlots;
+    Tile<__half, SA> w;
+    tile_issue(w, (const uint32_t*)lt[GU_QW], (const uint32_t*)lt[GU_QZ], (const __half*)lt[GU_SC], N, c0, 0, H / 32,
+               p.lgs);
+    NormW nw;
+    norm_prefetch(nw, (const float*)lt[POST_LN], H);
+    const uint32_t th = c.tag(l, P_HMID);
+    PD_MARK(l, 0);
+    if (!wait_tagged<2>(
+            H, c, [&](int i) -> const uint64_t* { return p.thmid + i; }, [&](int) { return th; }, s.xs))
+      return false;
+    PD_MARK(l, 1);
+    rmsnorm_inplace(s.xs, nw, H, p.eps, s.red16);
+    stage_a(s.xs, H, s.xa, s.corr, s.xsum);
+    PD_MARK(l, 3);
+    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.zoff), s.red);
+    PD_MARK(l, 4);
+    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < N) tput(p.tgu + c0 + threadIdx.x, c.tag(l, P_GU), y);
+    PD_MARK(l, 2);
+    __syncthreads();
+  }
+  return true;
+}
+
+// down projection, columns [64 t, 64 t + 64) of H over K-slice sl of I: the slice's share of
+// silu(gate) * up @ Wd.
+template <int SD>
+MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t, int sl) {
+  const int H = p.H, I = p.I, KS = I / p.ksd, rb = sl * (KS / 8), c0 = t * kTile;
+  for (int l = 0; l < p.L; ++l) {
+    const uint64_t* lt = p.layers + (size_t)l * kSlots;
+    Tile<__half, SD> w;
+    tile_issue(w, (const uint32_t*)lt[D_QW], (const uint32_t*)lt[D_QZ], (const __half*)lt[D_SC], H, c0, rb, KS / 32,
+               p.lgs);
+    const uint32_t tg = c.tag(l, P_GU);
+    PD_MARK(l, 0);
+    if (!wait_tagged<4>(
+            2 * KS, c,
+            [&](int i) -> const uint64_t* { return p.tgu + (i < KS ? sl * KS + i : I + sl * KS + (i - KS)); },
+            [&](int) { return tg; }, s.hin))
+      return false;
+    PD_MARK(l, 1);
+    for (int i = threadIdx.x; i < KS; i += kThreads) {
+      const float gv = s.hin[i], u = s.hin[KS + i];
+      s.xs[i] = (gv * (1.f / (1.f + expf(-gv)))) * u;
+    }
+    __syncthreads();
+    stage_a(s.xs, KS, s.xa, s.corr, s.xsum);
+    PD_MARK(l, 3);
+    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, rb, c0, p.lgs, p.zoff), s.red);
+    PD_MARK(l, 4);
+    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < H)
+      tput(p.tdown + (size_t)sl * H + c0 + threadIdx.x, c.tag(l, P_DOWN), y);
+    PD_MARK(l, 2);
+    __syncthreads();
+  }
+  return true;
+}
+
+// Tied head over 64-column tiles b, b + G, ... (the next tile's loads issued before the current
+// one is computed) with a running arg-max, published as tagged (value, index) words.
+template <int SA>
+MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int tok) {
+  const int H = p.H, V = p.V, G = gridDim.x, b = blockIdx.x;
+  const int ntile = (V + kTile - 1) / kTile;
+  Tile<float, SA> w, wn;
+  if (b < ntile) tile_issue(w, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
+  NormW nw;
+  norm_prefetch(nw, p.final_norm, H);
+  PD_MARK(p.L, 0);
+  if (!load_h_full(p, c, p.L, tok, s.xs, s.hin)) return false;
+  PD_MARK(p.L, 1);
+  rmsnorm_inplace(s.xs, nw, H, p.eps, s.red16);
+  stage_a(s.xs, H, s.xa, s.corr, s.xsum);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int t = b; t < ntile; t += G) {
+    const int c0 = t * kTile, n = c0 + (int)threadIdx.x;
+    if (t + G < ntile) tile_issue(wn, p.head_qw, p.head_qz, p.head_sc, V, c0 + G * kTile, 0, H / 32, p.lgs);
+    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.head_zoff), s.red);
+    if (threadIdx.x < 64 && n < V) {
+      p.logits[n] = y;
+      if (better(y, n, bv, bi) || (bv != bv && y == y)) { bv = y; bi = n; }
+    }
+    __syncthreads();
+    w = wn;
+  }
+  if (threadIdx.x < 64) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (better(ov, oi, bv, bi) || (bv != bv && ov == ov)) { bv = ov; bi = oi; }
+    }
+    if (threadIdx.x == 0) {
+      tput(p.tamax + b, c.tag(p.L, P_AMAX), bv);
+      tput(p.tamax + G + b, c.tag(p.L, P_AMAX), __int_as_float(bi));
+    }
+  }
+  PD_MARK(p.L, 2);
+  return true;
+}
+
+// Workgroup 0: combine the G arg-max partials, emit the token and advance the decode state.
+MIQ_PD_INLINE bool finish_token(const Params& p, const Ctx& c, const Lds& s, int pos) {
+  const int G = gridDim.x;
+  const uint32_t tg = c.tag(p.L, P_AMAX);
+  if (!wait_tagged<1>(
+          2 * G, c, [&](int i) -> const uint64_t* { return p.tamax + i; }, [&](int) { return tg; }, s.hin))
+    return false;
+  if (threadIdx.x < 64) {
+    float fv = -INFINITY;
+    int fi = 0x7fffffff;
+    for (int gi = threadIdx.x; gi < G; gi += 64) {
+      const float v = s.hin[gi];
+      const int i = __float_as_int(s.hin[G + gi]);
+      if (better(v, i, fv, fi) || (fv != fv && v == v)) { fv = v; fi = i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(fv, o, 64);
+      const int oi = __shfl_xor(fi, o, 64);
+      if (better(ov, oi, fv, fi) || (fv != fv && ov == ov)) { fv = ov; fi = oi; }
+    }
+    if (threadIdx.x == 0) {
+      if (fi >= p.V) fi = 0;  // all logits NaN
+      p.ids[0] = fi;
+      const int step = p.state[1];
+      if (step < p.hist_len) p.history[step] = fi;
+      p.state[1] = step + 1;
+      p.state[3] = fi;
+      p.state[0] = pos + 1;
+      p.ctl[0] = c.ep;
+    }
+  }
+  return true;
+}
+
+template <int SA, int SD>
+__global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
+  extern __shared__ __align__(16) float lds[];
+  Lds s;
+  s.hin = lds;
+  s.xs = s.hin + p.lds_a;
+  s.xa = reinterpret_cast<unsigned char*>(s.xs + p.lds_x);
+  s.corr = reinterpret_cast<float*>(s.xa + (size_t)(p.lds_x / 32) * kStepBytes);
+  s.xsum = s.corr + p.lds_x / 32;
+  s.red = s.xsum + p.lds_x / 32;
+  s.red16 = s.red + 4 * 64;
+  s.qkv = s.red16 + 32;
+  Ctx c;
+  c.deadline = wall_clock64() + p.spin_limit;
+  PD_MARK(p.L + 1, 0);
+  c.ep = p.ctl[0] + 1u;
+  c.L = p.L;
+  const int pos = p.state[0];
+  const int tok = p.ids[0];
+  if (pos < 0 || pos >= p.LMAX) {  // uniform over the grid: every workgroup leaves at once
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(p.ctl + 1, 2u);
+    return;
+  }
+  int r = blockIdx.x;
+  bool ok = true;
+  if (r < p.nq) {
+    ok = role_qkv<SA>(p, c, s, r, tok);
+  } else if ((r -= p.nq) < p.na) {
+    ok = role_attn(p, c, s, r, pos);
+  } else if ((r -= p.na) < p.no) {
+    ok = role_o<SA>(p, c, s, r, tok);
+  } else if ((r -= p.no) < p.ngu) {
+    ok = role_gu<SA>(p, c, s, r);
+  } else if ((r -= p.ngu) < p.nd) {
+    ok = role_down<SD>(p, c, s, r % p.no, r / p.no);
+  }
+  ok = ok && role_head<SA>(p, c, s, tok);
+  if (ok && blockIdx.x == 0) ok = finish_token(p, c, s, pos);
+  if (!ok && threadIdx.x == 0) atomicOr(p.ctl + 1, 1u);
+  PD_MARK(p.L + 1, 1);
+}
+
+// Role counts, K-slices of the down projection and LDS regions for a model shape.
+struct Plan {
+  int G, nq, na, no, ngu, ksd, nd, lds_a, lds_x, spa, spd;
+  size_t lds_bytes, ws_bytes;
+  size_t off_tq, off_tatt, off_thmid, off_tgu, off_tdown, off_tamax;
+};
+
+static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits, Plan* pl) {
+  MIQ_REQUIRE(L > 0 && H > 0 && NH > 0 && NKV > 0 && NH % NKV == 0 && I > 0 && V > 0 && LMAX > 0 && gs > 0,
+              MIQ_ERR_INVALID, "decode_persistent: L=%d H=%d NH=%d NKV=%d I=%d V=%d LMAX=%d gs=%d", L, H, NH, NKV, I, V,
+              LMAX, gs);
+  MIQ_REQUIRE(bits == 4 && HD == 64, MIQ_ERR_UNSUPPORTED, "decode_persistent: needs int4 and head dim 64 (bits=%d HD=%d)",
+              bits, HD);
+  const int NQ = (NH + 2 * NKV) * HD, NHD = NH * HD;
+  MIQ_REQUIRE(H % kTile == 0 && NQ % kTile == 0 && (2 * I) % kTile == 0 && gs >= 32 && (gs & (gs - 1)) == 0 &&
+                  V % 8 == 0,
+              MIQ_ERR_UNSUPPORTED,
+              "decode_persistent: H, q|k|v width and 2I must be multiples of 64, gs a power of two >= 32, V of 8");
+  MIQ_REQUIRE(H % gs == 0 && NHD % gs == 0 && I % gs == 0, MIQ_ERR_UNSUPPORTED,
+              "decode_persistent: H, NH*HD and I must be multiples of the group size %d", gs);
+  // K in 32-value steps, at most 16 per k-quarter of a tile
+  auto rows_ok = [&](int K) { return K % 32 == 0 && K <= 32 * 4 * kMaxSPQ; };
+  MIQ_REQUIRE(rows_ok(H) && rows_ok(NHD) && LMAX <= 8192 && NHD <= 4096 - 9 * kTile, MIQ_ERR_UNSUPPORTED,
+              "decode_persistent: H=%d / NH*HD=%d / LMAX=%d out of range for gs=%d", H, NHD, LMAX, gs);
+  int cus = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return fail(MIQ_ERR_HIP, "decode_persistent: cannot query the CU count");
+  Plan q{};
+  q.G = cus;
+  q.nq = NQ / kTile;
+  q.na = NH;
+  q.no = H / kTile;
+  q.ngu = 2 * I / kTile;
+  q.ksd = 0;
+  for (int k = 8; k >= 1; k >>= 1) {
+    if (I % (8 * k) || !rows_ok(I / k) || 2 * (I / k) > 4 * kThreads || (k + 1) * H > 8 * kThreads) continue;
+    if (q.nq + q.na + q.no + q.ngu + q.no * k > q.G) continue;
+    q.ksd = k;
+    break;
+  }
+  MIQ_REQUIRE(q.ksd > 0 && 2 * q.G <= kThreads, MIQ_ERR_UNSUPPORTED,
+              "decode_persistent: the roles of this shape do not fit %d workgroups", q.G);
+  q.nd = q.no * q.ksd;
+  const int KS = I / q.ksd;
+  q.spa = (std::max(H, NHD) / 32 + 3) / 4;
+  q.spd = (KS / 32 + 3) / 4;
+  q.lds_a = std::max(std::max((q.ksd + 1) * H, NHD + (q.ksd + 1) * kTile), std::max(std::max(2 * KS, kWaves * 64), std::max(256 + LMAX, 2 * q.G)));
+  q.lds_a = (q.lds_a + 3) & ~3;
+  q.lds_x = (std::max(H, std::max(NHD, KS)) + 31) & ~31;
+  q.lds_bytes = (size_t)(q.lds_a + q.lds_x) * 4 + (size_t)(q.lds_x / 32) * kStepBytes +
+                (size_t)(2 * (q.lds_x / 32) + 4 * 64 + 32 + 192) * 4;
+  size_t off = 256;  // control words
+  auto take = [&](size_t words) {
+    const size_t o = off;
+    off += (words * 8 + 255) & ~(size_t)255;
+    return o;
+  };
+  q.off_tq = take(NQ);
+  q.off_tatt = take(NHD);
+  q.off_thmid = take(H);
+  q.off_tgu = take(2 * (size_t)I);
+  q.off_tdown = take((size_t)q.ksd * H);
+  q.off_tamax = take(2 * (size_t)q.G);
+  q.ws_bytes = off;
+  *pl = q;
+  return MIQ_OK;
+}
+
+}  // namespace pd
+}  // namespace miq
+
+using namespace miq;
+
+extern "C" int miq_decode_persistent_plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs,
+                                          int bits, int* grid, size_t* ws_bytes) {
+  pd::Plan pl;
+  const int rc = pd::plan(L, H, NH, NKV, HD, I, V, LMAX, gs, bits, &pl);
+  if (rc != MIQ_OK) return rc;
+  if (grid) *grid = pl.G;
+  if (ws_bytes) *ws_bytes = pl.ws_bytes;
+  return MIQ_OK;
+}
+
+extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
+                                     const int32_t* head_qzeros, const float* head_scales, const float* final_norm,
+                                     const float* cos_tab, const float* sin_tab, int32_t* ids, int32_t* history,
+                                     int hist_len, int32_t* state, float* logits, void* ws, size_t ws_bytes, int L,
+                                     int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits, float eps,
+                                     float zoff, float head_zoff, void* stream) {
+  pd::Plan pl;
+  const int rc = pd::plan(L, H, NH, NKV, HD, I, V, LMAX, gs, bits, &pl);
+  if (rc != MIQ_OK) return rc;
+  MIQ_REQUIRE(layer_table && embed && head_qweight && head_qzeros && head_scales && final_norm && cos_tab && sin_tab &&
+                  ids && state && logits && ws && (history || hist_len == 0) && hist_len >= 0,
+              MIQ_ERR_INVALID, "decode_persistent: null pointer");
+  MIQ_REQUIRE(ws_bytes >= pl.ws_bytes, MIQ_ERR_INVALID, "decode_persistent: workspace %zu bytes, need %zu", ws_bytes,
+              pl.ws_bytes);
+  MIQ_REQUIRE(aligned(ws, 256) && aligned(layer_table, 8), MIQ_ERR_ALIGN,
+              "decode_persistent: workspace must be 256-byte aligned");
+  int dev = 0, per_cu = 0, khz = 0;
+  // 32-k steps per k-quarter of the K = H projections and of a down K-slice, rounded up to the
+  // instantiated register capacities
+  void (*kfn)(pd::Params) = nullptr;
+  if (pl.spa <= 8 && pl.spd <= 12) kfn = pd::decode_persistent_kernel<8, 12>;
+  else if (pl.spa <= 8) kfn = pd::decode_persistent_kernel<8, 16>;
+  else if (pl.spd <= 12) kfn = pd::decode_persistent_kernel<16, 12>;
+  else kfn = pd::decode_persistent_kernel<16, 16>;
+  auto kern = reinterpret_cast<const void*>(kfn);
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, pd::kThreads, pl.lds_bytes) != hipSuccess)
+    return fail(MIQ_ERR_HIP, "decode_persistent: occupancy query failed");
+  MIQ_REQUIRE(per_cu >= 1, MIQ_ERR_UNSUPPORTED, "decode_persistent: a workgroup does not fit a CU");
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) khz = 100000;
+  pd::Params p{};
+  unsigned char* w = static_cast<unsigned char*>(ws);
+  p.layers = layer_table;
+  p.embed = static_cast<const __half*>(embed);
+  p.head_qw = reinterpret_cast<const uint32_t*>(head_qweight);
+  p.head_qz = reinterpret_cast<const uint32_t*>(head_qzeros);
+  p.head_sc = head_scales;
+  p.final_norm = final_norm;
+  p.cos_t = cos_tab;
+  p.sin_t = sin_tab;
+  p.ids = ids;
+  p.history = history;
+  p.state = state;
+  p.logits = logits;
+  p.ctl = reinterpret_cast<uint32_t*>(w);
+  p.tq = reinterpret_cast<uint64_t*>(w + pl.off_tq);
+  p.tatt = reinterpret_cast<uint64_t*>(w + pl.off_tatt);
+  p.thmid = reinterpret_cast<uint64_t*>(w + pl.off_thmid);
+  p.tgu = reinterpret_cast<uint64_t*>(w + pl.off_tgu);
+  p.tdown = reinterpret_cast<uint64_t*>(w + pl.off_tdown);
+  p.tamax = reinterpret_cast<uint64_t*>(w + pl.off_tamax);
+  p.L = L;
+  p.H = H;
+  p.NH = NH;
+  p.NKV = NKV;
+  p.I = I;
+  p.V = V;
+  p.LMAX = LMAX;
+  p.gs = gs;
+  p.lgs = 0;
+  while ((1 << p.lgs) < gs) ++p.lgs;
+  p.hist_len = hist_len;
+  p.ksd = pl.ksd;
+  p.nq = pl.nq;
+  p.na = pl.na;
+  p.no = pl.no;
+  p.ngu = pl.ngu;
+  p.nd = pl.nd;
+  p.lds_a = pl.lds_a;
+  p.lds_x = pl.lds_x;
+  p.eps = eps;
+  p.scale = 1.0f / sqrtf((float)HD);
+  p.zoff = zoff;
+  p.head_zoff = head_zoff;
+  p.spin_limit = (long long)khz * 100;  // 100 ms
+  hipLaunchKernelGGL(kfn, dim3(pl.G), dim3(pd::kThreads), pl.lds_bytes,
+                     static_cast<hipStream_t>(stream), p);
+  return check_launch("decode_persistent");
+}

@@ -11,12 +11,20 @@ step is recorded once as a HIP graph and replayed per token with no host work in
 reference re-uploads inputs and reads the logits back to the host every token,
 `webtorch/llm.py:1582-1589, 1808-1814`).
 
+Where the shape allows it (`miq_decode_persistent_plan`), the one-token step is a single
+persistent launch instead of 5 launches per layer: one workgroup per CU with a fixed role
+(a 64-column tile of a projection, a query head, or a tile and K-slice of the down
+projection); the workgroups exchange activations through tagged device-scope words, so the
+step has no kernel boundary and each projection's weights are fetched a layer ahead.
+`persistent=False` keeps the launch sequence; prefill always uses it.
+
 Layout choices: q, k and v (and gate and up) share their input, so their GPTQ tensors are
 concatenated along the output dimension at load time and run as one GEMV (per-column groups
 make this identical to separate layers). The tied head is re-quantized from the fp16
 embedding on the device, bit-exact with `_gptq_quantize` (`webtorch/_core.py:3782-3824`;
 per-column quantization makes the reference's 4096-row blocks, `llm.py:594-602`, one matrix).
 """
+import ctypes
 import math
 import time
 
@@ -72,9 +80,10 @@ class CausalLM:
     "in_ln", "post_ln"), the fp16 "embed" table (tied head), "final_norm" and "cfg"
     (L, H, NH, NKV, HD, I, V, gs, bits[, eps, theta])."""
 
-    def __init__(self, weights, lmax=256, fused=True):
+    def __init__(self, weights, lmax=256, fused=True, persistent=None):
         c = weights["cfg"]
         self.fused = bool(fused)  # one-token steps use the fused launches (else the prefill path)
+        self.persistent = persistent  # None: the persistent step where the shape allows it
         self.L, self.H, self.NH, self.NKV, self.HD = c["L"], c["H"], c["NH"], c["NKV"], c["HD"]
         self.I, self.V, self.gs, self.bits = c["I"], c["V"], c["gs"], c["bits"]
         self.eps = float(c.get("eps", 1e-6))
@@ -98,8 +107,8 @@ class CausalLM:
         self._graph = None
 
     @classmethod
-    def from_weights(cls, weights, lmax=256, fused=True):
-        return cls(weights, lmax, fused)
+    def from_weights(cls, weights, lmax=256, fused=True, persistent=None):
+        return cls(weights, lmax, fused, persistent)
 
     # ---- load-time ----
     def _quantize_head(self):
@@ -132,6 +141,48 @@ class CausalLM:
             for lin in [self.layers[0][k] for k in ("qkv", "o", "gate_up", "down")]:
                 need = max(need, core.gemv_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits, _lib.MIQ_F32))
         self.ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+        self._alloc_persistent()
+
+    def _alloc_persistent(self):
+        """Layer address table and exchange workspace of the persistent one-token step, if the
+        shape is supported and the layers carry fp16 scales (else the launch sequence runs)."""
+        self.pws = None
+        if self.persistent is False or not self.fused:
+            return
+        lays = self.layers
+        fp16 = all(lay[k].scales.dtype == torch.float16 for lay in lays for k in ("qkv", "o", "gate_up", "down"))
+        if not fp16 or self.head.scales.dtype != torch.float32:
+            if self.persistent:
+                raise ValueError("persistent decode needs fp16 layer scales and an fp32-scaled head")
+            return
+        grid, wsb = ctypes.c_int(0), ctypes.c_size_t(0)
+        rc = _lib.lib().miq_decode_persistent_plan(self.L, self.H, self.NH, self.NKV, self.HD, self.I, self.V,
+                                                   self.lmax, self.gs, self.bits, ctypes.byref(grid),
+                                                   ctypes.byref(wsb))
+        if rc != 0:
+            if self.persistent:
+                raise _lib.ERRORS.get(rc, _lib.MiqError)(
+                    "persistent decode: %s" % _lib.lib().miq_last_error().decode(errors="replace"))
+            return
+        def a(t):
+            return 0 if t is None else int(t.data_ptr())
+        table = []
+        for i, lay in enumerate(lays):
+            qkv, o, gu, dn = lay["qkv"], lay["o"], lay["gate_up"], lay["down"]
+            table.append([a(qkv.qweight), a(qkv.qzeros), a(qkv.scales), a(qkv.bias),
+                          a(o.qweight), a(o.qzeros), a(o.scales),
+                          a(gu.qweight), a(gu.qzeros), a(gu.scales),
+                          a(dn.qweight), a(dn.qzeros), a(dn.scales),
+                          a(lay["in_ln"]), a(lay["post_ln"]), a(self.kc[i]), a(self.vc[i]), 0, 0, 0])
+        self.layer_table = torch.tensor(table, dtype=torch.int64, device=core.device())
+        self.pws = torch.zeros(int(wsb.value), dtype=torch.uint8, device=core.device())
+        self.persistent_grid = int(grid.value)
+
+    def persistent_error(self):
+        """Error bits of the persistent step's last runs (0 if none; see miq.h)."""
+        if self.pws is None:
+            return 0
+        return int(self.pws[4:8].view(torch.int32).item())
 
     # ---- one forward over T tokens at the device position ----
     def _linear(self, lin, x, out, bias=None):
@@ -146,10 +197,19 @@ class CausalLM:
                   stream_handle())
 
     def _decode_step(self):
-        """One token at position state[0] (`_decode_fwd`, `webtorch/llm.py:1591-1616`): five
-        launches per layer -- RMSNorm+qkv, RoPE+KV write+attention, o+residual, RMSNorm+gate|up,
-        SwiGLU+down+residual -- then RMSNorm+head and the device argmax."""
+        """One token at position state[0] (`_decode_fwd`, `webtorch/llm.py:1591-1616`): one
+        persistent launch, or five launches per layer -- RMSNorm+qkv, RoPE+KV write+attention,
+        o+residual, RMSNorm+gate|up, SwiGLU+down+residual -- then RMSNorm+head and the device
+        argmax."""
         b, st = self.buf, stream_handle()
+        if self.pws is not None:
+            _lib.call("miq_decode_persistent", ptr(self.layer_table), ptr(self.embed), ptr(self.head.qweight),
+                      ptr(self.head.qzeros), ptr(self.head.scales), ptr(self.final_norm), ptr(self.cos_t),
+                      ptr(self.sin_t), ptr(self.ids), ptr(self.history), self.lmax, ptr(self.state),
+                      ptr(b["logits"]), ptr(self.pws), self.pws.numel(), self.L, self.H, self.NH, self.NKV, self.HD,
+                      self.I, self.V, self.lmax, self.gs, self.bits, self.eps, float(self.layers[0]["qkv"].zoff),
+                      float(self.head.zoff), st)
+            return
         h = b["h"][:1]
         _lib.call("miq_embed", ptr(self.ids), ptr(self.embed), ptr(h), 1, self.H, self.V, st)
         scale = 1.0 / math.sqrt(self.HD)
@@ -214,6 +274,8 @@ class CausalLM:
     def reset(self):
         self.state.zero_()
         self.history.zero_()
+        if self.pws is not None:
+            self.pws.zero_()  # epoch and every exchange tag back to zero (never a valid tag)
 
     def _plan_length(self, n_prompt, max_new):
         """Refuse sequences that do not fit the KV cache (`webtorch/llm.py:1397-1429`)."""
@@ -245,6 +307,10 @@ class CausalLM:
                 self._step(1)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t1
+        err = self.persistent_error()
+        if err:
+            raise _lib.MiqError("persistent decode step failed (error bits %d): %s" % (
+                err, "a workgroup timed out waiting" if err & 1 else "position past the KV cache"))
         toks = [int(t) for t in self.history[:max_new].cpu().numpy()]
         rate = (max_new - 1) / dt if max_new > 1 and dt > 0 else 0.0
         return GenResult("", toks, ttft, rate)
