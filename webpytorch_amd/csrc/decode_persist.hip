@@ -101,29 +101,36 @@ struct Ctx {
   __device__ uint32_t tag(int l, int ph) const { return ep * (uint32_t)(8 * (L + 1)) + 8u * (uint32_t)l + (uint32_t)ph; }
 };
 
-// Polls n tagged words (word i at addr(i)) until word i carries tagf(i), leaving their values
+// Polls n tagged words (word i at base + off(i)) until word i carries tagf(i), leaving their values
 // in dst[0..n) (LDS). Called by the whole workgroup with the same arguments; n <= NPL * 1024.
-// Returns false (uniformly) once the workgroup's deadline has passed.
+// Each wave polls its own words until they are all current (no barrier per round), then the
+// workgroup meets once. Returns false (uniformly) once a wave has passed the deadline.
 template <int NPL, typename F, typename T>
-__device__ bool wait_tagged(int n, const Ctx& c, F addr, T tagf, float* dst) {
+__device__ bool wait_tagged(int n, const Ctx& c, const uint64_t* base, F off, T tagf, float* dst) {
   const int tid = opaque_tid();
+  bool late = false;
   for (;;) {
     uint64_t v[NPL];
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) v[j] = tget(addr(min(tid + j * kThreads, n - 1)));
+    for (int j = 0; j < NPL; ++j)
+      if (j * kThreads < n) v[j] = tget(base + (uint32_t)off(min(tid + j * kThreads, n - 1)));
     bool ok = true;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       const int i = tid + j * kThreads;
-      if (i < n) {
+      if (j * kThreads < n && i < n) {
         ok &= (uint32_t)(v[j] >> 32) == tagf(i);
         dst[i] = __uint_as_float((uint32_t)v[j]);
       }
     }
-    if (__syncthreads_and(ok)) return true;
-    if (__syncthreads_or(wall_clock64() > c.deadline)) return false;
-    __builtin_amdgcn_s_sleep(2);
+    if (__all(ok)) break;
+    if (wall_clock64() > c.deadline) {  // wave-uniform (scalar clock)
+      late = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
   }
+  return !__syncthreads_or(late);
 }
 
 // Sum over the workgroup, combined in wave order (every thread gets the total).
@@ -174,9 +181,33 @@ template <typename ST, int SPQ>
 struct Tile {
   uint32_t w[SPQ];
   uint32_t z[SPQ];
-  float s[SPQ];
-  int st0, ns;  // first step and step count of this wave
+  uint32_t s[SPQ];  // raw scale bits (fp16 in the low half, or fp32)
+  int st0, ns;      // first step and step count of this wave
 };
+
+__device__ __forceinline__ uint32_t scale_bits(const __half* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ __forceinline__ uint32_t scale_bits(const float* p) { return *reinterpret_cast<const uint32_t*>(p); }
+template <typename ST> __device__ __forceinline__ float scale_f32(uint32_t b);
+template <> __device__ __forceinline__ float scale_f32<__half>(uint32_t b) {
+  return __half2float(__ushort_as_half((unsigned short)b));
+}
+template <> __device__ __forceinline__ float scale_f32<float>(uint32_t b) { return __uint_as_float(b); }
+
+// Holds loaded values in registers from here on. Without it the compiler sinks loads issued
+// ahead of a wait down to their first use after the wait, which puts a memory round trip back
+// on the critical path; the empty asm makes the values used (so loaded) at this point.
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+template <typename ST, int SPQ>
+__device__ __forceinline__ void pin(Tile<ST, SPQ>& t) {
+#pragma unroll
+  for (int i = 0; i < SPQ; ++i) {
+    pin(t.w[i]);
+    pin(t.z[i]);
+    pin(t.s[i]);
+  }
+}
 
 // Issues this wave's loads for the tile of columns [c0, c0 + 64) (clamped to N - 1) over the
 // nsteps 32-k steps starting at packed row rb (absolute, for the group index; groups are
@@ -192,51 +223,65 @@ __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw,
   const int c = min(c0 + (wave & 3) * 16 + (lane & 15), N - 1);
   const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
   const uint32_t* wp = qw + (uint32_t)((r0 + (lane >> 4)) * N + c);
+  if (t.ns > 0) {
+    // unguarded loads (steps past the wave's last repeat it) issue back to back
 #pragma unroll
-  for (int i = 0; i < SPQ; ++i) {
-    if (i < t.ns) {
-      const int g = (r0 + 4 * i) >> gsh;
-      t.w[i] = wp[(uint32_t)(4 * i * N)];
-      t.s[i] = to_f32(sc[(uint32_t)(g * N + c)]);
+    for (int i = 0; i < SPQ; ++i) {
+      const int ii = min(i, t.ns - 1);
+      const int g = (r0 + 4 * ii) >> gsh;
+      t.w[i] = wp[(uint32_t)(4 * ii * N)];
+      t.s[i] = scale_bits(sc + (uint32_t)(g * N + c));
       t.z[i] = qz[(uint32_t)(g * (N >> 3) + (c >> 3))];
     }
+    pin(t);
   }
 }
 
 // This wave's share of sum_k x_k W[k][c] (valid in lanes 0..15, column c0 + 16 (w & 3) + lane).
+// The A fragment and step sums of step i + 2 are read from LDS while step i computes (reads
+// clamped to the wave's last step, so they need no guard); the MFMAs of a quantization group
+// chain, and each group is folded into acc with its scale and zero point.
 template <typename ST, int SPQ>
-__device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float* corr,
-                                          const float* xsum, int rb, int c0, int lgs, float zoff) {
+__device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float2* cx, int rb,
+                                          int c0, int lgs, float zoff) {
+  if (t.ns == 0) return 0.f;  // wave-uniform: a k-quarter past the end of K
   const int tid = opaque_tid();
   const int wave = uniform(tid >> 6), lane = tid & 63;
   const int sh = ((c0 + (wave & 3) * 16 + (lane & 15)) & 7) * 4;
   const unsigned char* ap = xa + t.st0 * kStepBytes + (lane >> 4) * 64 + min(lane & 15, 3) * 16;
-  const float* cp = corr + t.st0;
-  const float* xp = xsum + t.st0;
+  const float2* cp = cx + t.st0;
+  const int last = t.ns - 1;
+  bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ap), a1 = *reinterpret_cast<const bf16x8*>(ap + min(1, last) * kStepBytes);
+  float2 x0 = cp[0], x1 = cp[min(1, last)];
   const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
   floatx4 d = {0.f, 0.f, 0.f, 0.f};
   float acc = 0.f, cs = 0.f, xs = 0.f;
 #pragma unroll
   for (int i = 0; i < SPQ; ++i) {
+    const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(ap + min(i + 2, last) * kStepBytes);
+    const float2 x2 = cp[min(i + 2, last)];
     if (i < t.ns) {
-      const bf16x8 av = *reinterpret_cast<const bf16x8*>(ap + i * kStepBytes);
       // halves (c0, c4) (8 c1, 8 c5) (c2, c6) (8 c3, 8 c7) over 128
       const uint32_t w = t.w[i];
       const u32x4 bw = {and_or(w, 0x000F000Fu, 0x43004300u), and_or(w >> 1, 0x00780078u, 0x43004300u),
                         and_or(w >> 8, 0x000F000Fu, 0x43004300u), and_or(w >> 9, 0x00780078u, 0x43004300u)};
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
-      cs += cp[i];
-      xs += xp[i];
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
+      cs += x0.x;
+      xs += x0.y;
       const int r = r0 + 4 * i;
       if (i + 1 == t.ns || ((r + 4) >> gsh) != (r >> gsh)) {  // last step of this group
         const float pv = (d[0] + d[1]) + d[2];
         const float zc = (float)((t.z[i] >> sh) & 15u) + zoff;
-        acc = fmaf(t.s[i], pv - fmaf(zc, xs, cs), acc);
+        acc = fmaf(scale_f32<ST>(t.s[i]), pv - fmaf(zc, xs, cs), acc);
         d = (floatx4){0.f, 0.f, 0.f, 0.f};
         cs = 0.f;
         xs = 0.f;
       }
     }
+    a0 = a1;
+    a1 = a2;
+    x0 = x1;
+    x1 = x2;
   }
   return acc;
 }
@@ -255,64 +300,64 @@ __device__ __forceinline__ float tile_sum(float acc, float* red) {
   return y;
 }
 
-// Stages K fp32 activations (LDS) as the A operand of K / 32 steps, with each step's bias sum
-// (128 x the x of codes in bits 0-3 of a byte, 16 x the others) and x sum.
-__device__ __forceinline__ void stage_a(const float* x, int K, unsigned char* xa, float* corr, float* xsum) {
-  const int nch = K / 8;  // 8-value k-blocks, 4 per step
-  const int tid = opaque_tid();
-  for (int ch0 = 0; ch0 < nch; ch0 += kThreads) {
-    const int ch = ch0 + tid;
-    if (ch < nch) {  // all four blocks of a step are present together (K % 32 == 0)
-      const float4 va = *reinterpret_cast<const float4*>(x + ch * 8);
-      const float4 vb = *reinterpret_cast<const float4*>(x + ch * 8 + 4);
-      const float o[8] = {va.x, vb.x, va.y * 0.125f, vb.y * 0.125f, va.z, vb.z, va.w * 0.125f, vb.w * 0.125f};
-      bf16x8 t1, t2, t3;
+// Stages one 8-value k-block (chunk ch of K / 8) of the A operand: the three bf16 terms of x in
+// the codes' order (x0, x4, x1 / 8, x5 / 8, x2, x6, x3 / 8, x7 / 8) and a zero slot; the four
+// chunks of a step (consecutive threads, all present since K % 32 == 0) combine their bias
+// sums (128 x the x of low nibbles, 16 x the others) and x sums into cx[step].
+__device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned char* xa, float2* cx) {
+  const float o[8] = {v[0], v[4], v[1] * 0.125f, v[5] * 0.125f, v[2], v[6], v[3] * 0.125f, v[7] * 0.125f};
+  bf16x8 t1, t2, t3;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const __bf16 b1 = (__bf16)o[j];
-        const float r1 = o[j] - (float)b1;
-        const __bf16 b2 = (__bf16)r1;
-        t1[j] = b1;
-        t2[j] = b2;
-        t3[j] = (__bf16)(r1 - (float)b2);
-      }
-      unsigned char* dst = xa + (ch >> 2) * kStepBytes + (ch & 3) * 64;
-      *reinterpret_cast<bf16x8*>(dst) = t1;
-      *reinterpret_cast<bf16x8*>(dst + 16) = t2;
-      *reinterpret_cast<bf16x8*>(dst + 32) = t3;
-      *reinterpret_cast<u32x4*>(dst + 48) = (u32x4){0u, 0u, 0u, 0u};
-      const float lo = (va.x + va.z) + (vb.x + vb.z), hi = (va.y + va.w) + (vb.y + vb.w);
-      float cb = 128.f * lo + 16.f * hi, sm = lo + hi;
-      cb += __shfl_xor(cb, 1, 64);
-      cb += __shfl_xor(cb, 2, 64);
-      sm += __shfl_xor(sm, 1, 64);
-      sm += __shfl_xor(sm, 2, 64);
-      if ((ch & 3) == 0) {
-        corr[ch >> 2] = cb;
-        xsum[ch >> 2] = sm;
-      }
-    }
+  for (int j = 0; j < 8; ++j) {
+    const __bf16 b1 = (__bf16)o[j];
+    const float r1 = o[j] - (float)b1;
+    const __bf16 b2 = (__bf16)r1;
+    t1[j] = b1;
+    t2[j] = b2;
+    t3[j] = (__bf16)(r1 - (float)b2);
   }
-  __syncthreads();
+  unsigned char* dst = xa + (ch >> 2) * kStepBytes + (ch & 3) * 64;
+  *reinterpret_cast<bf16x8*>(dst) = t1;
+  *reinterpret_cast<bf16x8*>(dst + 16) = t2;
+  *reinterpret_cast<bf16x8*>(dst + 32) = t3;
+  *reinterpret_cast<u32x4*>(dst + 48) = (u32x4){0u, 0u, 0u, 0u};
+  const float lo = (v[0] + v[2]) + (v[4] + v[6]), hi = (v[1] + v[3]) + (v[5] + v[7]);
+  float cb = 128.f * lo + 16.f * hi, sm = lo + hi;
+  cb += __shfl_xor(cb, 1, 64);
+  cb += __shfl_xor(cb, 2, 64);
+  sm += __shfl_xor(sm, 1, 64);
+  sm += __shfl_xor(sm, 2, 64);
+  if ((ch & 3) == 0) cx[ch >> 2] = make_float2(cb, sm);
 }
 
-// RMSNorm weights of the H <= 2048 columns this thread normalizes, loaded ahead of the wait.
-struct NormW {
-  float v[2];
-};
-__device__ __forceinline__ void norm_prefetch(NormW& nw, const float* w, int H) {
-  nw.v[0] = (int)threadIdx.x < H ? w[threadIdx.x] : 0.f;
-  nw.v[1] = (int)threadIdx.x + kThreads < H ? w[threadIdx.x + kThreads] : 0.f;
-}
-
-// h = h / sqrt(mean(h^2) + eps) * w in place (h in LDS, H <= 2048).
-__device__ __forceinline__ void rmsnorm_inplace(float* h, const NormW& nw, int H, float eps, float* red16) {
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < H; i += kThreads) ss = ss + h[i] * h[i];
+// RMSNorm of a chunk's 8 values, v = v / sqrt(sum(all h^2) / H + eps) * w, where ss is this
+// thread's sum of squares (0 for threads without a chunk); block-wide (all threads call it).
+__device__ __forceinline__ void rmsnorm_chunk(float* v, float ss, const float4* w, int H, float eps, float* red16) {
   const float r = sqrtf(block_sum(ss, red16) / (float)H + eps);
-  if ((int)threadIdx.x < H) h[threadIdx.x] = (h[threadIdx.x] / r) * nw.v[0];
-  if ((int)threadIdx.x + kThreads < H) h[threadIdx.x + kThreads] = (h[threadIdx.x + kThreads] / r) * nw.v[1];
-  __syncthreads();
+  v[0] = (v[0] / r) * w[0].x;
+  v[1] = (v[1] / r) * w[0].y;
+  v[2] = (v[2] / r) * w[0].z;
+  v[3] = (v[3] / r) * w[0].w;
+  v[4] = (v[4] / r) * w[1].x;
+  v[5] = (v[5] / r) * w[1].y;
+  v[6] = (v[6] / r) * w[1].z;
+  v[7] = (v[7] / r) * w[1].w;
+}
+
+__device__ __forceinline__ float sumsq8(const float* v) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss = ss + v[j] * v[j];
+  return ss;
+}
+
+// This thread's chunk (8 values) of an RMSNorm weight vector of H values, loaded ahead.
+__device__ __forceinline__ void norm_prefetch(float4* w, const float* nw, int H) {
+  const int ch = min((int)threadIdx.x, H / 8 - 1);
+  w[0] = *reinterpret_cast<const float4*>(nw + ch * 8);
+  w[1] = *reinterpret_cast<const float4*>(nw + ch * 8 + 4);
+  pin(w[0]);
+  pin(w[1]);
 }
 
 __device__ __forceinline__ float rope1(const float* row, int d, int half, float c, float s) {
@@ -325,39 +370,46 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 }
 
 // LDS carve-up: hin (exchange words and scratch), xs (fp32 activations), xa (A operand steps),
-// corr / xsum (per step), red (4 quarters x 64 columns), red16 (wave scalars), qkv (rotated q, k
-// and the new v).
+// cx (bias and x sums per step), red (4 quarters x 64 columns), red16 (wave scalars), qkv
+// (rotated q, k and the new v).
 struct Lds {
   float *hin, *xs;
   unsigned char* xa;
-  float *corr, *xsum, *red, *red16, *qkv;
+  float2* cx;
+  float *red, *red16, *qkv;
 };
 
 #define MIQ_PD_INLINE __device__ __attribute__((always_inline)) inline
 
-// h(l) of the H columns into dst: layer 0 is the current token's embedding row; later layers
-// sum the down projection's K-slices in slice order and then add the residual hmid(l - 1),
-// as the split-K GEMV with the residual as its bias does.
-MIQ_PD_INLINE bool load_h_full(const Params& p, const Ctx& c, int l, int tok, float* dst, float* raw) {
-  const int H = p.H, ks = p.ksd;
-  if (l == 0) {
-    for (int i = threadIdx.x; i < H; i += kThreads)
-      dst[i] = (tok >= 0 && tok < p.V) ? __half2float(p.embed[(size_t)tok * H + i]) : 0.f;
-    __syncthreads();
-    return true;
+// h(l) for this thread's 8-value chunk (threads < H / 8; the others get zeros): layer 0 is the
+// current token's embedding row; later layers sum the down projection's K-slices in slice order
+// and then add the residual hmid(l - 1), as the split-K GEMV with the residual as its bias does.
+MIQ_PD_INLINE bool gather_h(const Params& p, const Ctx& c, int l, int tok, float* raw, float* v) {
+  const int H = p.H, ks = p.ksd, ch = threadIdx.x;
+  if (l > 0) {
+    const uint32_t td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
+    if (!wait_tagged<8>(  // the ks down slices and hmid are consecutive H-word rows
+            (ks + 1) * H, c, p.tdown, [&](int j) { return j; }, [=](int j) { return j < ks * H ? td : th; }, raw))
+      return false;
   }
-  const uint32_t td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
-  const bool ok = wait_tagged<8>(
-      (ks + 1) * H, c,
-      [&](int j) -> const uint64_t* { return j < ks * H ? p.tdown + j : p.thmid + (j - ks * H); },
-      [&](int j) { return j < ks * H ? td : th; }, raw);
-  if (!ok) return false;
-  for (int i = threadIdx.x; i < H; i += kThreads) {
-    float h = raw[i];
-    for (int sl = 1; sl < ks; ++sl) h += raw[sl * H + i];
-    dst[i] = h + raw[ks * H + i];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = 0.f;
+  if (ch < H / 8) {
+    if (l == 0) {
+      if (tok >= 0 && tok < p.V) {
+        const __half* e = p.embed + (size_t)tok * H + ch * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __half2float(e[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float h = raw[ch * 8 + j];
+        for (int sl = 1; sl < ks; ++sl) h += raw[sl * H + ch * 8 + j];
+        v[j] = h + raw[ks * H + ch * 8 + j];
+      }
+    }
   }
-  __syncthreads();
   return true;
 }
 
@@ -370,17 +422,21 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
     Tile<__half, SA> w;
     tile_issue(w, (const uint32_t*)lt[QKV_QW], (const uint32_t*)lt[QKV_QZ], (const __half*)lt[QKV_SC], NQ, c0, 0,
                H / 32, p.lgs);
-    NormW nw;
+    float4 nw[2];
     norm_prefetch(nw, (const float*)lt[IN_LN], H);
     const float* bias = (const float*)lt[QKV_B];
-    const float bv = (bias && threadIdx.x < 64) ? bias[min(c0 + (int)threadIdx.x, NQ - 1)] : 0.f;
+    float bv = (bias && threadIdx.x < 64) ? bias[min(c0 + (int)threadIdx.x, NQ - 1)] : 0.f;
+    pin(bv);
     PD_MARK(l, 0);
-    if (!load_h_full(p, c, l, tok, s.xs, s.hin)) return false;
+    float v[8];
+    if (!gather_h(p, c, l, tok, s.hin, v)) return false;
     PD_MARK(l, 1);
-    rmsnorm_inplace(s.xs, nw, H, p.eps, s.red16);
-    stage_a(s.xs, H, s.xa, s.corr, s.xsum);
+    const int ch = threadIdx.x;
+    rmsnorm_chunk(v, ch < H / 8 ? sumsq8(v) : 0.f, nw, H, p.eps, s.red16);
+    if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
+    __syncthreads();
     PD_MARK(l, 3);
-    float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.zoff), s.red);
+    float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.zoff), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < NQ) {
       if (bias) y += bv;
@@ -419,14 +475,16 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
     float vr[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) vr[i] = vc[(size_t)min(wave + 16 * i, LMAX - 1) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pin(kr[i]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pin(vr[i]);
     const uint32_t tg = c.tag(l, P_QKV);
     PD_MARK(l, 0);
     const bool ok = wait_tagged<1>(
-        192, c,
-        [&](int i) -> const uint64_t* {
-          return p.tq + (i < 64 ? hq * 64 + i : i < 128 ? (NH + g) * 64 + (i - 64) : (NH + NKV + g) * 64 + (i - 128));
-        },
-        [&](int) { return tg; }, s.hin);
+        192, c, p.tq,
+        [&](int i) { return i < 64 ? hq * 64 + i : i < 128 ? (NH + g) * 64 + (i - 64) : (NH + NKV + g) * 64 + (i - 128); },
+        [=](int) { return tg; }, s.hin);
     if (!ok) return false;
     PD_MARK(l, 1);
     if (tid < 64) {
@@ -524,14 +582,13 @@ MIQ_PD_INLINE bool role_o(const Params& p, const Ctx& c, const Lds& s, int t, in
     const int nres = l == 0 ? 0 : (ks + 1) * kTile;
     const uint32_t ta = c.tag(l, P_ATT), td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
     PD_MARK(l, 0);
-    const bool ok = wait_tagged<4>(
-        NHD + nres, c,
-        [&](int i) -> const uint64_t* {
-          if (i < NHD) return p.tatt + i;
-          const int j = i - NHD, sl = j / kTile, cc = c0 + (j - sl * kTile);
-          return sl < ks ? p.tdown + (size_t)sl * H + cc : p.thmid + cc;
+    const bool ok = wait_tagged<2>(  // att is followed by the down slices and hmid
+        NHD + nres, c, p.tatt,
+        [&](int i) {
+          const int j = i - NHD, sl = j >> 6;
+          return i < NHD ? i : NHD + sl * H + c0 + (j & 63);
         },
-        [&](int i) { return i < NHD ? ta : ((i - NHD) / kTile < ks ? td : th); }, s.hin);
+        [=](int i) { return i < NHD ? ta : ((i - NHD) >> 6 < ks ? td : th); }, s.hin);
     if (!ok) return false;
     PD_MARK(l, 1);
     float hres = 0.f;
@@ -545,9 +602,10 @@ MIQ_PD_INLINE bool role_o(const Params& p, const Ctx& c, const Lds& s, int t, in
         hres = hres + r[ks * kTile + lane];
       }
     }
-    stage_a(s.hin, NHD, s.xa, s.corr, s.xsum);
+    if ((int)threadIdx.x < NHD / 8) stage_chunk(threadIdx.x, s.hin + threadIdx.x * 8, s.xa, s.cx);
+    __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.zoff), s.red);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.zoff), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + lane < H) tput(p.thmid + c0 + lane, c.tag(l, P_HMID), y + hres);
     PD_MARK(l, 2);
@@ -565,18 +623,23 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
     Tile<__half, SA> w;
     tile_issue(w, (const uint32_t*)lt[GU_QW], (const uint32_t*)lt[GU_QZ], (const __half*)lt[GU_SC], N, c0, 0, H / 32,
                p.lgs);
-    NormW nw;
+    float4 nw[2];
     norm_prefetch(nw, (const float*)lt[POST_LN], H);
     const uint32_t th = c.tag(l, P_HMID);
     PD_MARK(l, 0);
     if (!wait_tagged<2>(
-            H, c, [&](int i) -> const uint64_t* { return p.thmid + i; }, [&](int) { return th; }, s.xs))
+            H, c, p.thmid, [&](int i) { return i; }, [=](int) { return th; }, s.xs))
       return false;
     PD_MARK(l, 1);
-    rmsnorm_inplace(s.xs, nw, H, p.eps, s.red16);
-    stage_a(s.xs, H, s.xa, s.corr, s.xsum);
+    const int ch = threadIdx.x;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = ch < H / 8 ? s.xs[ch * 8 + j] : 0.f;
+    rmsnorm_chunk(v, sumsq8(v), nw, H, p.eps, s.red16);
+    if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
+    __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.zoff), s.red);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.zoff), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < N) tput(p.tgu + c0 + threadIdx.x, c.tag(l, P_GU), y);
     PD_MARK(l, 2);
@@ -598,19 +661,23 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
     const uint32_t tg = c.tag(l, P_GU);
     PD_MARK(l, 0);
     if (!wait_tagged<4>(
-            2 * KS, c,
-            [&](int i) -> const uint64_t* { return p.tgu + (i < KS ? sl * KS + i : I + sl * KS + (i - KS)); },
-            [&](int) { return tg; }, s.hin))
+            2 * KS, c, p.tgu, [&](int i) { return i < KS ? sl * KS + i : I + sl * KS + (i - KS); },
+            [=](int) { return tg; }, s.hin))
       return false;
     PD_MARK(l, 1);
-    for (int i = threadIdx.x; i < KS; i += kThreads) {
-      const float gv = s.hin[i], u = s.hin[KS + i];
-      s.xs[i] = (gv * (1.f / (1.f + expf(-gv)))) * u;
+    const int ch = threadIdx.x;
+    if (ch < KS / 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float gv = s.hin[ch * 8 + j], u = s.hin[KS + ch * 8 + j];
+        v[j] = (gv * (1.f / (1.f + expf(-gv)))) * u;
+      }
+      stage_chunk(ch, v, s.xa, s.cx);
     }
     __syncthreads();
-    stage_a(s.xs, KS, s.xa, s.corr, s.xsum);
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, rb, c0, p.lgs, p.zoff), s.red);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, rb, c0, p.lgs, p.zoff), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < H)
       tput(p.tdown + (size_t)sl * H + c0 + threadIdx.x, c.tag(l, P_DOWN), y);
@@ -628,19 +695,22 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   const int ntile = (V + kTile - 1) / kTile;
   Tile<float, SA> w, wn;
   if (b < ntile) tile_issue(w, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
-  NormW nw;
+  float4 nw[2];
   norm_prefetch(nw, p.final_norm, H);
   PD_MARK(p.L, 0);
-  if (!load_h_full(p, c, p.L, tok, s.xs, s.hin)) return false;
+  float v[8];
+  if (!gather_h(p, c, p.L, tok, s.hin, v)) return false;
   PD_MARK(p.L, 1);
-  rmsnorm_inplace(s.xs, nw, H, p.eps, s.red16);
-  stage_a(s.xs, H, s.xa, s.corr, s.xsum);
+  const int ch = threadIdx.x;
+  rmsnorm_chunk(v, ch < H / 8 ? sumsq8(v) : 0.f, nw, H, p.eps, s.red16);
+  if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
+  __syncthreads();
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int t = b; t < ntile; t += G) {
     const int c0 = t * kTile, n = c0 + (int)threadIdx.x;
     if (t + G < ntile) tile_issue(wn, p.head_qw, p.head_qz, p.head_sc, V, c0 + G * kTile, 0, H / 32, p.lgs);
-    const float y = tile_sum(tile_mma(w, s.xa, s.corr, s.xsum, 0, c0, p.lgs, p.head_zoff), s.red);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.head_zoff), s.red);
     if (threadIdx.x < 64 && n < V) {
       p.logits[n] = y;
       if (better(y, n, bv, bi) || (bv != bv && y == y)) { bv = y; bi = n; }
@@ -669,7 +739,7 @@ MIQ_PD_INLINE bool finish_token(const Params& p, const Ctx& c, const Lds& s, int
   const int G = gridDim.x;
   const uint32_t tg = c.tag(p.L, P_AMAX);
   if (!wait_tagged<1>(
-          2 * G, c, [&](int i) -> const uint64_t* { return p.tamax + i; }, [&](int) { return tg; }, s.hin))
+          2 * G, c, p.tamax, [&](int i) { return i; }, [=](int) { return tg; }, s.hin))
     return false;
   if (threadIdx.x < 64) {
     float fv = -INFINITY;
@@ -706,9 +776,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   s.hin = lds;
   s.xs = s.hin + p.lds_a;
   s.xa = reinterpret_cast<unsigned char*>(s.xs + p.lds_x);
-  s.corr = reinterpret_cast<float*>(s.xa + (size_t)(p.lds_x / 32) * kStepBytes);
-  s.xsum = s.corr + p.lds_x / 32;
-  s.red = s.xsum + p.lds_x / 32;
+  s.cx = reinterpret_cast<float2*>(s.xa + (size_t)(p.lds_x / 32) * kStepBytes);
+  s.red = reinterpret_cast<float*>(s.cx + p.lds_x / 32);
   s.red16 = s.red + 4 * 64;
   s.qkv = s.red16 + 32;
   Ctx c;
@@ -763,7 +832,7 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
               "decode_persistent: H, NH*HD and I must be multiples of the group size %d", gs);
   // K in 32-value steps, at most 16 per k-quarter of a tile
   auto rows_ok = [&](int K) { return K % 32 == 0 && K <= 32 * 4 * kMaxSPQ; };
-  MIQ_REQUIRE(rows_ok(H) && rows_ok(NHD) && LMAX <= 8192 && NHD <= 4096 - 9 * kTile, MIQ_ERR_UNSUPPORTED,
+  MIQ_REQUIRE(rows_ok(H) && rows_ok(NHD) && LMAX <= 8192 && NHD <= 2 * kThreads - 9 * kTile, MIQ_ERR_UNSUPPORTED,
               "decode_persistent: H=%d / NH*HD=%d / LMAX=%d out of range for gs=%d", H, NHD, LMAX, gs);
   int cus = 0, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -800,10 +869,11 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
     return o;
   };
   q.off_tq = take(NQ);
-  q.off_tatt = take(NHD);
-  q.off_thmid = take(H);
+  // att, the down projection's K-slices and hmid back to back: one base for the o role's poll
+  q.off_tatt = take(NHD + (size_t)(q.ksd + 1) * H);
+  q.off_tdown = q.off_tatt + (size_t)NHD * 8;
+  q.off_thmid = q.off_tdown + (size_t)q.ksd * H * 8;
   q.off_tgu = take(2 * (size_t)I);
-  q.off_tdown = take((size_t)q.ksd * H);
   q.off_tamax = take(2 * (size_t)q.G);
   q.ws_bytes = off;
   *pl = q;
