@@ -167,8 +167,8 @@ __device__ __forceinline__ float block_max(float v, float* red16) {
 // or 16 times the x of each kind) and x sums are subtracted per quantization group with the
 // zero point: acc += s_g * (p - (bias + z_g * sum x)).
 //
-// A 32-k step of A is staged in LDS as 4 k-blocks (one per 16 lanes) x 4 slots (the three
-// bf16 terms and a zero slot for lanes whose A row is 3..15) x 8 values, 256 bytes.
+// A 32-k step of A is staged in LDS as 4 k-blocks (one per 16 lanes) x 4 slots of 8 values
+// (the three bf16 terms; the fourth slot is unused), 256 bytes.
 // Wave w of the 16 takes the 16 columns (w & 3) of the 64-column tile and the k-quarter
 // (w >> 2) of the steps; lane l loads packed row (l >> 4) of each step for column l & 15, which
 // is exactly its B fragment (column l & 15, k 8 (l >> 4) .. + 7).
@@ -212,7 +212,7 @@ __device__ __forceinline__ void pin(Tile<ST, SPQ>& t) {
 // Issues this wave's loads for the tile of columns [c0, c0 + 64) (clamped to N - 1) over the
 // nsteps 32-k steps starting at packed row rb (absolute, for the group index; groups are
 // 2^lgs values, 2^(lgs - 3) packed rows).
-template <typename ST, int SPQ>
+template <typename ST, int SPQ, bool PIN = true>
 __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw, const uint32_t* qz, const ST* sc,
                                            int N, int c0, int rb, int nsteps, int lgs) {
   const int tid = opaque_tid();
@@ -233,7 +233,7 @@ __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw,
       t.s[i] = scale_bits(sc + (uint32_t)(g * N + c));
       t.z[i] = qz[(uint32_t)(g * (N >> 3) + (c >> 3))];
     }
-    pin(t);
+    if (PIN) pin(t);
   }
 }
 
@@ -248,17 +248,25 @@ __device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned
   const int tid = opaque_tid();
   const int wave = uniform(tid >> 6), lane = tid & 63;
   const int sh = ((c0 + (wave & 3) * 16 + (lane & 15)) & 7) * 4;
-  const unsigned char* ap = xa + t.st0 * kStepBytes + (lane >> 4) * 64 + min(lane & 15, 3) * 16;
+  // Only A rows 0-2 (lanes with lane % 16 < 3) carry data: D rows 3-15 are never read, so the
+  // other lanes skip the LDS read and feed whatever their registers hold.
+  const bool arow = (lane & 15) < 3;
+  const unsigned char* ap = xa + t.st0 * kStepBytes + (lane >> 4) * 64 + (lane & 15) * 16;
   const float2* cp = cx + t.st0;
   const int last = t.ns - 1;
-  bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ap), a1 = *reinterpret_cast<const bf16x8*>(ap + min(1, last) * kStepBytes);
+  bf16x8 a0, a1;
+  if (arow) {
+    a0 = *reinterpret_cast<const bf16x8*>(ap);
+    a1 = *reinterpret_cast<const bf16x8*>(ap + min(1, last) * kStepBytes);
+  }
   float2 x0 = cp[0], x1 = cp[min(1, last)];
   const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
   floatx4 d = {0.f, 0.f, 0.f, 0.f};
   float acc = 0.f, cs = 0.f, xs = 0.f;
 #pragma unroll
   for (int i = 0; i < SPQ; ++i) {
-    const bf16x8 a2 = *reinterpret_cast<const bf16x8*>(ap + min(i + 2, last) * kStepBytes);
+    bf16x8 a2;
+    if (arow) a2 = *reinterpret_cast<const bf16x8*>(ap + min(i + 2, last) * kStepBytes);
     const float2 x2 = cp[min(i + 2, last)];
     if (i < t.ns) {
       // halves (c0, c4) (8 c1, 8 c5) (c2, c6) (8 c3, 8 c7) over 128
@@ -301,7 +309,7 @@ __device__ __forceinline__ float tile_sum(float acc, float* red) {
 }
 
 // Stages one 8-value k-block (chunk ch of K / 8) of the A operand: the three bf16 terms of x in
-// the codes' order (x0, x4, x1 / 8, x5 / 8, x2, x6, x3 / 8, x7 / 8) and a zero slot; the four
+// the codes' order (x0, x4, x1 / 8, x5 / 8, x2, x6, x3 / 8, x7 / 8), rows 0-2; the four
 // chunks of a step (consecutive threads, all present since K % 32 == 0) combine their bias
 // sums (128 x the x of low nibbles, 16 x the others) and x sums into cx[step].
 __device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned char* xa, float2* cx) {
@@ -320,7 +328,6 @@ __device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned cha
   *reinterpret_cast<bf16x8*>(dst) = t1;
   *reinterpret_cast<bf16x8*>(dst + 16) = t2;
   *reinterpret_cast<bf16x8*>(dst + 32) = t3;
-  *reinterpret_cast<u32x4*>(dst + 48) = (u32x4){0u, 0u, 0u, 0u};
   const float lo = (v[0] + v[2]) + (v[4] + v[6]), hi = (v[1] + v[3]) + (v[5] + v[7]);
   float cb = 128.f * lo + 16.f * hi, sm = lo + hi;
   cb += __shfl_xor(cb, 1, 64);
@@ -330,18 +337,31 @@ __device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned cha
   if ((ch & 3) == 0) cx[ch >> 2] = make_float2(cb, sm);
 }
 
-// RMSNorm of a chunk's 8 values, v = v / sqrt(sum(all h^2) / H + eps) * w, where ss is this
-// thread's sum of squares (0 for threads without a chunk); block-wide (all threads call it).
-__device__ __forceinline__ void rmsnorm_chunk(float* v, float ss, const float4* w, int H, float eps, float* red16) {
-  const float r = sqrtf(block_sum(ss, red16) / (float)H + eps);
-  v[0] = (v[0] / r) * w[0].x;
-  v[1] = (v[1] / r) * w[0].y;
-  v[2] = (v[2] / r) * w[0].z;
-  v[3] = (v[3] / r) * w[0].w;
-  v[4] = (v[4] / r) * w[1].x;
-  v[5] = (v[5] / r) * w[1].y;
-  v[6] = (v[6] / r) * w[1].z;
-  v[7] = (v[7] / r) * w[1].w;
+// RMSNorm applied after the projection, which is linear: RMSNorm(h) @ W = ((h * w) @ W) / r with
+// r = sqrt(mean(h^2) + eps) one scalar per token, so the block reduction for r overlaps the
+// matrix work instead of preceding it. norm_stage scales this thread's chunk by the norm weight
+// and leaves the wave's sum of squares in red16[wave] (visible after the next barrier);
+// norm_r combines them in wave order.
+__device__ __forceinline__ void norm_stage(float* v, const float4* w, float* red16) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss = ss + v[j] * v[j];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red16[threadIdx.x >> 6] = ss;
+  v[0] = v[0] * w[0].x;
+  v[1] = v[1] * w[0].y;
+  v[2] = v[2] * w[0].z;
+  v[3] = v[3] * w[0].w;
+  v[4] = v[4] * w[1].x;
+  v[5] = v[5] * w[1].y;
+  v[6] = v[6] * w[1].z;
+  v[7] = v[7] * w[1].w;
+}
+__device__ __forceinline__ float norm_r(const float* red16, int H, float eps) {
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) t += red16[w];
+  return sqrtf(t / (float)H + eps);
 }
 
 __device__ __forceinline__ float sumsq8(const float* v) {
@@ -416,6 +436,8 @@ MIQ_PD_INLINE bool gather_h(const Params& p, const Ctx& c, int l, int tok, float
 // q|k|v projection, columns [64 t, 64 t + 64): RMSNorm(h(l)) @ Wqkv + bias.
 template <int SA>
 MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
+  float zo = p.zoff;
+  pin(zo);
   const int H = p.H, NQ = (p.NH + 2 * p.NKV) * 64, c0 = t * kTile;
   for (int l = 0; l < p.L; ++l) {
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
@@ -432,13 +454,14 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
     if (!gather_h(p, c, l, tok, s.hin, v)) return false;
     PD_MARK(l, 1);
     const int ch = threadIdx.x;
-    rmsnorm_chunk(v, ch < H / 8 ? sumsq8(v) : 0.f, nw, H, p.eps, s.red16);
+    norm_stage(v, nw, s.red16);
     if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
     __syncthreads();
     PD_MARK(l, 3);
-    float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.zoff), s.red);
+    float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < NQ) {
+      y = y / norm_r(s.red16, H, p.eps);
       if (bias) y += bv;
       tput(p.tq + c0 + threadIdx.x, c.tag(l, P_QKV), y);
     }
@@ -571,6 +594,8 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
 // o projection, columns [64 t, 64 t + 64) of H: h(l) + att(l) @ Wo.
 template <int SA>
 MIQ_PD_INLINE bool role_o(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
+  float zo = p.zoff;
+  pin(zo);
   const int H = p.H, NHD = p.NH * 64, ks = p.ksd, c0 = t * kTile;
   const int lane = threadIdx.x & 63;
   for (int l = 0; l < p.L; ++l) {
@@ -605,7 +630,7 @@ MIQ_PD_INLINE bool role_o(const Params& p, const Ctx& c, const Lds& s, int t, in
     if ((int)threadIdx.x < NHD / 8) stage_chunk(threadIdx.x, s.hin + threadIdx.x * 8, s.xa, s.cx);
     __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.zoff), s.red);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + lane < H) tput(p.thmid + c0 + lane, c.tag(l, P_HMID), y + hres);
     PD_MARK(l, 2);
@@ -617,6 +642,8 @@ MIQ_PD_INLINE bool role_o(const Params& p, const Ctx& c, const Lds& s, int t, in
 // gate|up projection, columns [64 t, 64 t + 64) of 2I: RMSNorm(hmid(l)) @ Wgu.
 template <int SA>
 MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
+  float zo = p.zoff;
+  pin(zo);
   const int H = p.H, N = 2 * p.I, c0 = t * kTile;
   for (int l = 0; l < p.L; ++l) {
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
@@ -635,13 +662,14 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
     float v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = ch < H / 8 ? s.xs[ch * 8 + j] : 0.f;
-    rmsnorm_chunk(v, sumsq8(v), nw, H, p.eps, s.red16);
+    norm_stage(v, nw, s.red16);
     if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
     __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.zoff), s.red);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
-    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < N) tput(p.tgu + c0 + threadIdx.x, c.tag(l, P_GU), y);
+    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < N)
+      tput(p.tgu + c0 + threadIdx.x, c.tag(l, P_GU), y / norm_r(s.red16, H, p.eps));
     PD_MARK(l, 2);
     __syncthreads();
   }
@@ -652,6 +680,8 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
 // silu(gate) * up @ Wd.
 template <int SD>
 MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t, int sl) {
+  float zo = p.zoff;
+  pin(zo);
   const int H = p.H, I = p.I, KS = I / p.ksd, rb = sl * (KS / 8), c0 = t * kTile;
   for (int l = 0; l < p.L; ++l) {
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
@@ -677,7 +707,7 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
     }
     __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, rb, c0, p.lgs, p.zoff), s.red);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, rb, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < H)
       tput(p.tdown + (size_t)sl * H + c0 + threadIdx.x, c.tag(l, P_DOWN), y);
@@ -693,8 +723,13 @@ template <int SA>
 MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int tok) {
   const int H = p.H, V = p.V, G = gridDim.x, b = blockIdx.x;
   const int ntile = (V + kTile - 1) / kTile;
-  Tile<float, SA> w, wn;
-  if (b < ntile) tile_issue(w, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
+  float zo = p.head_zoff;
+  pin(zo);
+  // three tiles in flight: b and b + G are loaded before the wait for h; then each step issues
+  // the tile two steps ahead and holds (pins) the next one once the current one is computed
+  Tile<float, SA> t0, t1, t2;
+  if (b < ntile) tile_issue(t0, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
+  if (b + G < ntile) tile_issue(t1, p.head_qw, p.head_qz, p.head_sc, V, (b + G) * kTile, 0, H / 32, p.lgs);
   float4 nw[2];
   norm_prefetch(nw, p.final_norm, H);
   PD_MARK(p.L, 0);
@@ -702,21 +737,30 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   if (!gather_h(p, c, p.L, tok, s.hin, v)) return false;
   PD_MARK(p.L, 1);
   const int ch = threadIdx.x;
-  rmsnorm_chunk(v, ch < H / 8 ? sumsq8(v) : 0.f, nw, H, p.eps, s.red16);
+  norm_stage(v, nw, s.red16);
   if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
   __syncthreads();
+  const float rn = norm_r(s.red16, H, p.eps);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int t = b; t < ntile; t += G) {
-    const int c0 = t * kTile, n = c0 + (int)threadIdx.x;
-    if (t + G < ntile) tile_issue(wn, p.head_qw, p.head_qz, p.head_sc, V, c0 + G * kTile, 0, H / 32, p.lgs);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, p.head_zoff), s.red);
+  auto step = [&](Tile<float, SA>& cur, Tile<float, SA>& nxt, Tile<float, SA>& ahead, int t)
+                  __attribute__((always_inline)) {
+    if (t >= ntile) return;  // uniform
+    if (t + 2 * G < ntile)
+      tile_issue<float, SA, false>(ahead, p.head_qw, p.head_qz, p.head_sc, V, (t + 2 * G) * kTile, 0, H / 32, p.lgs);
+    const int n = t * kTile + (int)threadIdx.x;
+    const float y = tile_sum(tile_mma(cur, s.xa, s.cx, 0, t * kTile, p.lgs, zo), s.red) / rn;
     if (threadIdx.x < 64 && n < V) {
       p.logits[n] = y;
       if (better(y, n, bv, bi) || (bv != bv && y == y)) { bv = y; bi = n; }
     }
     __syncthreads();
-    w = wn;
+    if (t + G < ntile) pin(nxt);  // issued a step ago, computed next
+  };
+  for (int t = b; t < ntile; t += 3 * G) {
+    step(t0, t1, t2, t);
+    step(t1, t2, t0, t + G);
+    step(t2, t0, t1, t + 2 * G);
   }
   if (threadIdx.x < 64) {
 #pragma unroll
