@@ -9,13 +9,16 @@ on the device) with the library's decode engine. A "step" is one decode token: o
 the captured graph (embedding, 24 layers, head GEMV, device argmax), after a 64-token prefill.
 The weights (synthetic, seeded) are in HBM before timing.
 
-The JSON line reports `value` = algorithmic bytes of the step's int4 GEMVs (every weight of the
-model once per token) / step time, in GB/s, plus decode tokens/s; `roofline` for the GEMV kernel
-measured on the same 97 GEMVs per token replayed alone over two alternating weight copies
-(522 MB, above the 256 MB Infinity Cache, so from HBM); per-shape GEMV timings; the GGUF Q4_K
-GEMV (Llama-3-8B up_proj), the act-order prefill GEMM (K = N = 4096) and the Qwen3-MoE expert
-block; and `cpu_baseline`: the reference's numpy fallback (restated in `oracle/`) timed on
-this host on a bounded sample of the same GEMVs.
+The step is one launch of the persistent decode kernel (the engine's default where the shape
+allows it). The JSON line reports `value` = algorithmic bytes of the step's int4 GEMVs (every
+weight of the model once per token) / step time, in GB/s, plus decode tokens/s and the same
+step as a launch sequence; `roofline` for the persistent kernel (its algorithmic bytes: weights,
+activations, KV rows, over its launch time); the drop-in GEMV kernel on the token's 97 GEMVs
+replayed alone over two alternating weight copies (522 MB, above the 256 MB Infinity Cache, so
+from HBM), with per-shape timings; the GGUF Q4_K GEMV (Llama-3-8B up_proj), the act-order
+prefill GEMM (K = N = 4096) and the Qwen3-MoE expert block; and `cpu_baseline`: the
+reference's numpy fallback (restated in `oracle/`) timed on this host on a bounded sample of
+the same GEMVs.
 """
 import argparse
 import json
@@ -28,7 +31,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-H, NH, NKV, HD, I, V, LAYERS, GS = 896, 14, 2, 64, 4864, 151936, 24, 128
+H, NH, NKV, HD, I, V, LAYERS, GS = 896, 14, 2, 64, 4864, 151936, 24, 128  # Qwen2-0.5B
 SHAPES = {  # name: (K, N, scales dtype, zero offset, bias)
     "qkv": (H, (NH + 2 * NKV) * HD, "f16", 1.0, True),
     "o": (NH * HD, H, "f16", 1.0, False),
@@ -250,23 +253,49 @@ def gemv_only(torch, core, steps):
     return t, kernels
 
 
-def copy_calibration(torch, nbytes=512 << 20, reps=4):
-    """A plain device copy of `nbytes` (fp32 elementwise copy kernel), `reps` times: reads and
-    writes exactly `nbytes` each, the scale for the FETCH_SIZE / WRITE_SIZE counters."""
+def decode_step_time(torch, m, ids, warmup, steps):
+    """Prefill + one step (which captures the decode graph), `warmup` untimed replays, then the
+    mean time of `steps` replays between events on the replay stream."""
+    r = m.generate(ids, 2)
+    pos0 = int(m.state[0])
+    g = m._graph
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        g.replay()
+    ev1.record(stream)
+    ev1.synchronize()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) * 1e-3 / steps, r, pos0
+
+
+def copy_calibration(torch, nbytes=1 << 30, reps=2):
+    """A plain streaming kernel over `nbytes` (torch's fp32 elementwise add, ordinary cached
+    loads and stores), `reps` times, from a source that a 1 GiB write has pushed out of the 256 MB
+    Infinity Cache: reads and writes exactly `nbytes` from and to HBM each time, the scale for the
+    FETCH_SIZE / WRITE_SIZE counters. (The runtime's own copy kernel reads in a way these
+    counters do not see.)"""
     src = torch.rand(nbytes // 4, device="cuda")
     dst = torch.empty_like(src)
+    evict = torch.empty(1 << 28, device="cuda")
     for _ in range(reps):
-        dst.copy_(src)
+        evict.fill_(1.0)
+        torch.add(src, 1.0, out=dst)
     torch.cuda.synchronize()
+    del evict
     return nbytes
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gptq_gemv_hbm_traffic_qwen2_05b_int4.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_persistent_hbm_traffic_qwen2_05b_int4.md")
 
 
 def measured_traffic():
-    """HBM bytes per GEMV launch of the decode token, from the committed FETCH_SIZE / WRITE_SIZE
-    counter summary (its `traffic_bytes_per_launch:` line), or None if that summary is absent."""
+    """HBM bytes per launch of the persistent decode kernel, from the committed FETCH_SIZE /
+    WRITE_SIZE counter summary (its `traffic_bytes_per_launch:` line), or None if it is absent."""
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
@@ -286,8 +315,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extras", action="store_true", help="only the decode step and its roofline")
     ap.add_argument("--gemv-only", action="store_true",
-                    help="only the roofline workload (the token's GEMVs alone) and a plain 512 MiB copy, "
-                         "for hardware-counter runs")
+                    help="only the token's GEMVs alone and a plain 1 GiB copy, for hardware-counter runs")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the persistent decode step and a plain 1 GiB copy, for hardware-counter runs")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized-linear path has no multi-GPU mode here "
@@ -298,6 +328,13 @@ def main():
     from webpytorch_amd import core, llm, synth
     torch.cuda.set_device(0)
     torch.manual_seed(0)
+    if a.decode_only:
+        m = llm.CausalLM.from_weights(synth.decoder_weights(5, **synth.QWEN2_05B), lmax=256)
+        t, _, _ = decode_step_time(torch, m, synth.prompt_ids(5, 64, synth.QWEN2_05B["V"]), 2, a.steps)
+        copy_bytes = copy_calibration(torch)
+        print(json.dumps({"decode_step_us": round(t * 1e6, 2), "copy_bytes_read": copy_bytes,
+                          "copy_bytes_written": copy_bytes, "error_bits": m.persistent_error()}), flush=True)
+        return
     if a.gemv_only:
         t_gemv, kernels = gemv_only(torch, core, a.steps)
         copy_bytes = copy_calibration(torch)
@@ -307,29 +344,34 @@ def main():
 
     prompt = 64
     lmax = max(256, prompt + a.warmup + a.steps + 2)
-    m = llm.CausalLM.from_weights(synth.decoder_weights(5, **synth.QWEN2_05B), lmax=lmax)
+    w = synth.decoder_weights(5, **synth.QWEN2_05B)
     ids = synth.prompt_ids(5, prompt, synth.QWEN2_05B["V"])
-    r = m.generate(ids, 2)  # prefill + one step; captures the decode graph
-    g = m._graph
-    for _ in range(a.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(a.steps):
-        g.replay()
-    ev1.record(stream)
-    ev1.synchronize()
-    torch.cuda.synchronize()
-    t_step = ev0.elapsed_time(ev1) * 1e-3 / a.steps
-    launches = LAYERS * 4 + 1
+    m = llm.CausalLM.from_weights(w, lmax=lmax)
+    if m.pws is None:
+        raise SystemExit("the persistent decode step is not available for this shape")
+    t_step, r, pos0 = decode_step_time(torch, m, ids, a.warmup, a.steps)
+    if m.persistent_error():
+        raise SystemExit("persistent decode step reported error bits %d" % m.persistent_error())
     step_bytes = sum(LAYERS * gemv_bytes(K, N, sdt, b) for k, (K, N, sdt, _, b) in SHAPES.items() if k != "head")
     step_bytes += gemv_bytes(*[SHAPES["head"][i] for i in (0, 1, 2, 4)])
     value = step_bytes / t_step / 1e9
+    # the kernel's algorithmic bytes: weights, activations, the KV rows of positions 0..pos (read)
+    # and pos (written) over 24 layers x 2 kv heads x (k, v), the embedding row
+    pos_mid = pos0 + (a.warmup + a.steps) / 2.0
+    kv_bytes = int(LAYERS * NKV * 2 * HD * 4 * (pos_mid + 2))
+    kernel_bytes = step_bytes + kv_bytes + H * 2
+    achieved = kernel_bytes / t_step / 1e9
+
+    # the same step as a launch sequence (5 launches per layer + head + argmax), for comparison
+    del m
+    torch.cuda.empty_cache()
+    ms = llm.CausalLM.from_weights(w, lmax=lmax, persistent=False)
+    t_seq, _, _ = decode_step_time(torch, ms, ids, a.warmup, a.steps)
+    del ms
+    torch.cuda.empty_cache()
 
     t_gemv, kernels = gemv_only(torch, core, a.steps)
-    achieved = step_bytes / t_gemv / 1e9
+    launches = LAYERS * 4 + 1
     res = {
         "metric": "int4 GEMV achieved HBM GB/s (% of peak) + decode tokens/s, Qwen2-0.5B shape",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -337,19 +379,25 @@ def main():
         "vs_baseline": None, "dtype": "int4 weights, fp32 activations, fp32 accumulate", "data": "synthetic",
         "config": {"workload": "greedy decode, random-init Qwen2-0.5B-shaped int4 GPTQ model (24 layers, "
                                "hidden 896, 14/2 heads, intermediate 4864, vocab 151936, gs=128), 64-token "
-                               "prompt; one step = one decode token (captured graph replay)",
-                   "gemv_bytes_per_token": step_bytes, "gemv_launches_per_token": launches},
+                               "prompt; one step = one decode token = one launch of the persistent decode "
+                               "kernel (captured graph replay)",
+                   "gemv_bytes_per_token": step_bytes, "kernel_bytes_per_token": kernel_bytes,
+                   "launches_per_token": 1},
         "decode_tokens_per_s": round(1.0 / t_step, 1),
+        "decode_tokens_per_s_launch_sequence": round(1.0 / t_seq, 1),
         "ttft_ms": round(r.ttft_s * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "traffic_note": "HBM bytes per launch (FETCH_SIZE + WRITE_SIZE over the same GEMVs, "
-                                     "scaled by the counters' reading for a plain copy of known size)",
-                     "kernel": "miq::gptq_gemv_kernel",
-                     "measured_on": "the 97 GEMVs of a token alone, 2 alternating weight copies (522 MB)",
-                     "avg_launch_us": round(t_gemv / launches * 1e6, 3),
-                     "avg_bytes_per_launch": step_bytes // launches},
-        "gemv_shapes": kernels,
+                     "traffic_note": "HBM bytes per launch (FETCH_SIZE + WRITE_SIZE of the kernel, scaled by "
+                                     "the counters' reading for a plain copy of known size)",
+                     "kernel": "miq::pd::decode_persistent_kernel",
+                     "measured_on": "the timed graph replays (one launch per token)",
+                     "avg_launch_us": round(t_step * 1e6, 2), "algorithmic_bytes_per_launch": kernel_bytes},
+        "gemv_kernel": {"kernel": "miq::gptq_gemv_kernel (the drop-in operator)",
+                        "measured_on": "the token's 97 GEMVs alone, 2 alternating weight copies (522 MB)",
+                        "avg_launch_us": round(t_gemv / launches * 1e6, 3),
+                        "achieved_GBs": round(step_bytes / t_gemv / 1e9, 2),
+                        "frac": round(step_bytes / t_gemv / 1e9 / HBM_PEAK_GBS, 4), "shapes": kernels},
     }
     if not a.no_extras:
         res["q4k_gemv_llama3_8b_up"] = q4k_bench(torch, core)
