@@ -155,6 +155,35 @@ def moe_bench(torch, core, reps=8):
             "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4), "TFLOPs": round(flops / t / 1e12, 1)}
 
 
+def gemv_large(torch, core, reps=24):
+    """The GEMV operator on bandwidth-bound 7B-class shapes (int4, gs 128, fp16 scales, 1 row of
+    fp16 or fp32 activations), over enough distinct weight copies (>= 600 MB) that every launch
+    reads HBM: GB/s of algorithmic bytes and the fraction of the 8 TB/s peak."""
+    res = {}
+    for name, K, N, xdt in (("llama7b_up_4096x11008_f16x", 4096, 11008, torch.float16),
+                            ("llama7b_down_11008x4096_f16x", 11008, 4096, torch.float16),
+                            ("llama7b_up_4096x11008_f32x", 4096, 11008, torch.float32)):
+        nb = gemv_bytes(K, N, "f16", False) + (K * 2 if xdt == torch.float32 else 0)
+        copies = max(2, int(600e6 // nb) + 1)
+        ws = [make_layer(torch, K, N, "f16", False) for _ in range(copies)]
+        x = torch.randn((1, K), device="cuda").to(xdt)
+        y = torch.empty((1, N), device="cuda", dtype=torch.float16)
+
+        def run(ws=ws, x=x, y=y, K=K, N=N):
+            for i in range(reps):
+                qw, qz, sc, _ = ws[i % len(ws)]
+                core._gptq_matmul(x, qw, qz, sc, K, N, GS, 4, 1.0, out=y)
+        run()
+        torch.cuda.synchronize()
+        g = capture(torch, run)
+        t = timed(torch, g.replay, 5) / reps
+        res[name] = {"bytes": nb, "us": round(t * 1e6, 3), "GBs": round(nb / t / 1e9, 1),
+                     "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4)}
+        del g, ws
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(seconds=10.0):
     """The reference's numpy-fallback GEMV path (`_gptq_matmul_np`, restated in oracle/) on a
     bounded sample: one decoder layer's seven linears (q, k, v, o, gate, up, down as separate
@@ -316,6 +345,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="only the decode step and its roofline")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the token's GEMVs alone and a plain 1 GiB copy, for hardware-counter runs")
+    ap.add_argument("--gemv-large", action="store_true", help="only the GEMV operator on 7B-class shapes")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the persistent decode step and a plain 1 GiB copy, for hardware-counter runs")
     a = ap.parse_args()
@@ -328,6 +358,9 @@ def main():
     from webpytorch_amd import core, llm, synth
     torch.cuda.set_device(0)
     torch.manual_seed(0)
+    if a.gemv_large:
+        print(json.dumps(gemv_large(torch, core)), flush=True)
+        return
     if a.decode_only:
         m = llm.CausalLM.from_weights(synth.decoder_weights(5, **synth.QWEN2_05B), lmax=256)
         t, _, _ = decode_step_time(torch, m, synth.prompt_ids(5, 64, synth.QWEN2_05B["V"]), 2, a.steps)
@@ -400,6 +433,7 @@ def main():
                         "frac": round(step_bytes / t_gemv / 1e9 / HBM_PEAK_GBS, 4), "shapes": kernels},
     }
     if not a.no_extras:
+        res["gemv_large"] = gemv_large(torch, core)
         res["q4k_gemv_llama3_8b_up"] = q4k_bench(torch, core)
         res["gptq_gemm_act_order_4096"] = gemm_bench(torch, core)
         res["moe_qwen3_t256"] = moe_bench(torch, core)

@@ -118,6 +118,34 @@ def test_act_order_gemv(gpu, M):
                                                       g_idx=L["g_idx"]))
 
 
+@pytest.mark.parametrize("K,N,xdt,sdt,zoff,bias", [
+    (4096, 11008, np.float16, "f16", 1.0, False),   # 6 K-slices
+    (11008, 4096, np.float32, "f16", 1.0, True),    # 16 K-slices of 22 steps
+    (896, 65536, np.float32, "f32", 0.0, False),    # one K-slice (a tied-head shape)
+    (2048, 4096, np.float16, "f32", 1.0, True),
+])
+def test_large_gemv_matrix_core_path(gpu, K, N, xdt, sdt, zoff, bias):
+    """One row against a layer of >= 4 MiB of int4 codes: the matrix-core GEMV (exact bf16
+    splits of x, fp32 accumulation) against the numpy-fallback oracle, deterministic."""
+    import torch
+    from webpytorch_amd import core
+    L = synth.gptq_layer(40 + K % 7, K, N, 128, 4)
+    sc = L["scales"] if sdt == "f16" else L["scales"].astype(np.float32) * np.float32(1.37)
+    x = synth.activations(41, 1, K, np.float16).astype(xdt)
+    b = (np.random.default_rng(3).standard_normal(N) * 0.1).astype(np.float32) if bias else None
+    out = torch.empty((1, N), dtype=torch.float32, device="cuda")
+    args = (torch.from_numpy(x).cuda(), core.to_device(L["qweight"]), core.to_device(L["qzeros"]), core.to_device(sc),
+            K, N, 128, 4, zoff)
+    got = core._gptq_matmul(*args, bias=None if b is None else core.to_device(b), out=out).cpu().numpy()
+    ref = gptq.gptq_matmul_np(x.astype(np.float32), L["qweight"], L["qzeros"], sc, K, N, 128, 4, zoff)
+    if b is not None:
+        ref = ref + b
+    _close(got, ref)
+    assert _rel(got, ref) < 1e-5
+    again = core._gptq_matmul(*args, bias=None if b is None else core.to_device(b), out=out).cpu().numpy()
+    assert np.array_equal(got, again)
+
+
 def test_int8_per_channel_gemv(gpu):
     import torch
     from webpytorch_amd import core

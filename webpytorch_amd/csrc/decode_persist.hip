@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include "miq_common.h"
+#include "mma_tile.h"
 
 // The elementwise steps (RMSNorm, RoPE, SiLU, softmax) round every product and sum separately,
 // as the reference's numpy expressions do; explicit fmaf() calls are unaffected.
@@ -36,6 +37,8 @@
 
 namespace miq {
 namespace pd {
+
+using namespace mt;
 
 constexpr int kThreads = 1024, kWaves = 16, kTile = 64, kMaxSPQ = 16, kSlots = 20;
 enum Slot { QKV_QW, QKV_QZ, QKV_SC, QKV_B, O_QW, O_QZ, O_SC, GU_QW, GU_QZ, GU_SC, D_QW, D_QZ, D_SC, IN_LN, POST_LN, KC, VC };
@@ -83,15 +86,6 @@ __device__ __forceinline__ void tput(uint64_t* p, uint32_t tag, float v) {
 }
 __device__ __forceinline__ uint64_t tget(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The thread index as a value the compiler cannot see through: index math derived from it is
-// recomputed where it is used (a few instructions per layer) instead of being hoisted out of
-// the layer loop and held in registers for the whole token.
-__device__ __forceinline__ int opaque_tid() {
-  int v = threadIdx.x;
-  asm volatile("" : "+v"(v));
-  return v;
 }
 
 struct Ctx {
@@ -153,188 +147,6 @@ __device__ __forceinline__ float block_max(float v, float* red16) {
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) t = fmaxf(t, red16[w]);
   return t;
-}
-
-// ---- 64-column int4 tile on the matrix cores ----------------------------------------------
-// The activations x (fp32) are split exactly into three bf16 terms, x = b1 + b2 + b3 (b1 =
-// bf16(x), b2 = bf16(x - b1), b3 = x - b1 - b2, which fits bf16), which become rows 0-2 of the
-// A operand of v_mfma_f32_16x16x32_bf16; the codes become the B operand with no conversion
-// instruction per value: OR-ing a code c into mantissa bits 0-3 of 128.0 (bf16 0x4300, whose
-// mantissa step is 1) gives 128 + c; a code of the upper nibble of a byte, shifted down one bit
-// into mantissa bits 3-6 (bf16 has 7 mantissa bits, so bit 7 is the exponent's), gives
-// 128 + 8c, matched by x / 8 in A. Products of bf16 values are exact in fp32, so rows 0-2 of D
-// sum to sum_k x_k (128 + c_k) or (x_k / 8)(128 + 8 c_k) in fp32; the per-step bias sums (128
-// or 16 times the x of each kind) and x sums are subtracted per quantization group with the
-// zero point: acc += s_g * (p - (bias + z_g * sum x)).
-//
-// A 32-k step of A is staged in LDS as 4 k-blocks (one per 16 lanes) x 4 slots of 8 values
-// (the three bf16 terms; the fourth slot is unused), 256 bytes.
-// Wave w of the 16 takes the 16 columns (w & 3) of the 64-column tile and the k-quarter
-// (w >> 2) of the steps; lane l loads packed row (l >> 4) of each step for column l & 15, which
-// is exactly its B fragment (column l & 15, k 8 (l >> 4) .. + 7).
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kStepBytes = 256;
-
-template <typename ST, int SPQ>
-struct Tile {
-  uint32_t w[SPQ];
-  uint32_t z[SPQ];
-  uint32_t s[SPQ];  // raw scale bits (fp16 in the low half, or fp32)
-  int st0, ns;      // first step and step count of this wave
-};
-
-__device__ __forceinline__ uint32_t scale_bits(const __half* p) { return *reinterpret_cast<const uint16_t*>(p); }
-__device__ __forceinline__ uint32_t scale_bits(const float* p) { return *reinterpret_cast<const uint32_t*>(p); }
-template <typename ST> __device__ __forceinline__ float scale_f32(uint32_t b);
-template <> __device__ __forceinline__ float scale_f32<__half>(uint32_t b) {
-  return __half2float(__ushort_as_half((unsigned short)b));
-}
-template <> __device__ __forceinline__ float scale_f32<float>(uint32_t b) { return __uint_as_float(b); }
-
-// Holds loaded values in registers from here on. Without it the compiler sinks loads issued
-// ahead of a wait down to their first use after the wait, which puts a memory round trip back
-// on the critical path; the empty asm makes the values used (so loaded) at this point.
-__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void pin(float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
-template <typename ST, int SPQ>
-__device__ __forceinline__ void pin(Tile<ST, SPQ>& t) {
-#pragma unroll
-  for (int i = 0; i < SPQ; ++i) {
-    pin(t.w[i]);
-    pin(t.z[i]);
-    pin(t.s[i]);
-  }
-}
-
-// Issues this wave's loads for the tile of columns [c0, c0 + 64) (clamped to N - 1) over the
-// nsteps 32-k steps starting at packed row rb (absolute, for the group index; groups are
-// 2^lgs values, 2^(lgs - 3) packed rows).
-template <typename ST, int SPQ, bool PIN = true>
-__device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw, const uint32_t* qz, const ST* sc,
-                                           int N, int c0, int rb, int nsteps, int lgs) {
-  const int tid = opaque_tid();
-  const int wave = uniform(tid >> 6), lane = tid & 63;
-  const int spq = (nsteps + 3) >> 2;
-  t.st0 = (wave >> 2) * spq;
-  t.ns = max(0, min(spq, nsteps - t.st0));
-  const int c = min(c0 + (wave & 3) * 16 + (lane & 15), N - 1);
-  const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
-  const uint32_t* wp = qw + (uint32_t)((r0 + (lane >> 4)) * N + c);
-  if (t.ns > 0) {
-    // unguarded loads (steps past the wave's last repeat it) issue back to back
-#pragma unroll
-    for (int i = 0; i < SPQ; ++i) {
-      const int ii = min(i, t.ns - 1);
-      const int g = (r0 + 4 * ii) >> gsh;
-      t.w[i] = wp[(uint32_t)(4 * ii * N)];
-      t.s[i] = scale_bits(sc + (uint32_t)(g * N + c));
-      t.z[i] = qz[(uint32_t)(g * (N >> 3) + (c >> 3))];
-    }
-    if (PIN) pin(t);
-  }
-}
-
-// This wave's share of sum_k x_k W[k][c] (valid in lanes 0..15, column c0 + 16 (w & 3) + lane).
-// The A fragment and step sums of step i + 2 are read from LDS while step i computes (reads
-// clamped to the wave's last step, so they need no guard); the MFMAs of a quantization group
-// chain, and each group is folded into acc with its scale and zero point.
-template <typename ST, int SPQ>
-__device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float2* cx, int rb,
-                                          int c0, int lgs, float zoff) {
-  if (t.ns == 0) return 0.f;  // wave-uniform: a k-quarter past the end of K
-  const int tid = opaque_tid();
-  const int wave = uniform(tid >> 6), lane = tid & 63;
-  const int sh = ((c0 + (wave & 3) * 16 + (lane & 15)) & 7) * 4;
-  // Only A rows 0-2 (lanes with lane % 16 < 3) carry data: D rows 3-15 are never read, so the
-  // other lanes skip the LDS read and feed whatever their registers hold.
-  const bool arow = (lane & 15) < 3;
-  const unsigned char* ap = xa + t.st0 * kStepBytes + (lane >> 4) * 64 + (lane & 15) * 16;
-  const float2* cp = cx + t.st0;
-  const int last = t.ns - 1;
-  bf16x8 a0, a1;
-  if (arow) {
-    a0 = *reinterpret_cast<const bf16x8*>(ap);
-    a1 = *reinterpret_cast<const bf16x8*>(ap + min(1, last) * kStepBytes);
-  }
-  float2 x0 = cp[0], x1 = cp[min(1, last)];
-  const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
-  floatx4 d = {0.f, 0.f, 0.f, 0.f};
-  float acc = 0.f, cs = 0.f, xs = 0.f;
-#pragma unroll
-  for (int i = 0; i < SPQ; ++i) {
-    bf16x8 a2;
-    if (arow) a2 = *reinterpret_cast<const bf16x8*>(ap + min(i + 2, last) * kStepBytes);
-    const float2 x2 = cp[min(i + 2, last)];
-    if (i < t.ns) {
-      // halves (c0, c4) (8 c1, 8 c5) (c2, c6) (8 c3, 8 c7) over 128
-      const uint32_t w = t.w[i];
-      const u32x4 bw = {and_or(w, 0x000F000Fu, 0x43004300u), and_or(w >> 1, 0x00780078u, 0x43004300u),
-                        and_or(w >> 8, 0x000F000Fu, 0x43004300u), and_or(w >> 9, 0x00780078u, 0x43004300u)};
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
-      cs += x0.x;
-      xs += x0.y;
-      const int r = r0 + 4 * i;
-      if (i + 1 == t.ns || ((r + 4) >> gsh) != (r >> gsh)) {  // last step of this group
-        const float pv = (d[0] + d[1]) + d[2];
-        const float zc = (float)((t.z[i] >> sh) & 15u) + zoff;
-        acc = fmaf(scale_f32<ST>(t.s[i]), pv - fmaf(zc, xs, cs), acc);
-        d = (floatx4){0.f, 0.f, 0.f, 0.f};
-        cs = 0.f;
-        xs = 0.f;
-      }
-    }
-    a0 = a1;
-    a1 = a2;
-    x0 = x1;
-    x1 = x2;
-  }
-  return acc;
-}
-
-// Sums the four k-quarters of each column in quarter order; valid in threads 0..63 (column
-// c0 + thread).
-__device__ __forceinline__ float tile_sum(float acc, float* red) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane < 16) red[(wave >> 2) * 64 + (wave & 3) * 16 + lane] = acc;
-  __syncthreads();
-  float y = 0.f;
-  if (threadIdx.x < 64) {
-    const int t = threadIdx.x;
-    y = ((red[t] + red[64 + t]) + red[128 + t]) + red[192 + t];
-  }
-  return y;
-}
-
-// Stages one 8-value k-block (chunk ch of K / 8) of the A operand: the three bf16 terms of x in
-// the codes' order (x0, x4, x1 / 8, x5 / 8, x2, x6, x3 / 8, x7 / 8), rows 0-2; the four
-// chunks of a step (consecutive threads, all present since K % 32 == 0) combine their bias
-// sums (128 x the x of low nibbles, 16 x the others) and x sums into cx[step].
-__device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned char* xa, float2* cx) {
-  const float o[8] = {v[0], v[4], v[1] * 0.125f, v[5] * 0.125f, v[2], v[6], v[3] * 0.125f, v[7] * 0.125f};
-  bf16x8 t1, t2, t3;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const __bf16 b1 = (__bf16)o[j];
-    const float r1 = o[j] - (float)b1;
-    const __bf16 b2 = (__bf16)r1;
-    t1[j] = b1;
-    t2[j] = b2;
-    t3[j] = (__bf16)(r1 - (float)b2);
-  }
-  unsigned char* dst = xa + (ch >> 2) * kStepBytes + (ch & 3) * 64;
-  *reinterpret_cast<bf16x8*>(dst) = t1;
-  *reinterpret_cast<bf16x8*>(dst + 16) = t2;
-  *reinterpret_cast<bf16x8*>(dst + 32) = t3;
-  const float lo = (v[0] + v[2]) + (v[4] + v[6]), hi = (v[1] + v[3]) + (v[5] + v[7]);
-  float cb = 128.f * lo + 16.f * hi, sm = lo + hi;
-  cb += __shfl_xor(cb, 1, 64);
-  cb += __shfl_xor(cb, 2, 64);
-  sm += __shfl_xor(sm, 1, 64);
-  sm += __shfl_xor(sm, 2, 64);
-  if ((ch & 3) == 0) cx[ch >> 2] = make_float2(cb, sm);
 }
 
 // RMSNorm applied after the projection, which is linear: RMSNorm(h) @ W = ((h * w) @ W) / r with
@@ -551,17 +363,19 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
     }
     __syncthreads();
     PD_MARK(l, 3);
-    float mx = -INFINITY;
-    for (int j = tid; j < S; j += kThreads) mx = fmaxf(mx, sp[j]);
-    mx = block_max(mx, s.red16);
-    float sum = 0.f;
-    for (int j = tid; j < S; j += kThreads) {
-      const float e = expf(sp[j] - mx);
-      sp[j] = e;
-      sum += e;
+    if (wave == 0) {  // softmax in one wave: reductions by shuffles, one barrier after it
+      float mx = -INFINITY;
+      for (int j = lane; j < S; j += 64) mx = fmaxf(mx, sp[j]);
+      mx = wave_max(mx);
+      float sum = 0.f;
+      for (int j = lane; j < S; j += 64) {
+        const float e = expf(sp[j] - mx);
+        sp[j] = e;
+        sum += e;
+      }
+      sum = wave_sum(sum);
+      for (int j = lane; j < S; j += 64) sp[j] = sp[j] / sum;
     }
-    sum = block_sum(sum, s.red16 + 16);
-    for (int j = tid; j < S; j += kThreads) sp[j] = sp[j] / sum;
     __syncthreads();
     PD_MARK(l, 4);
     float o = 0.f;
@@ -747,7 +561,7 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
                   __attribute__((always_inline)) {
     if (t >= ntile) return;  // uniform
     if (t + 2 * G < ntile)
-      tile_issue<float, SA, false>(ahead, p.head_qw, p.head_qz, p.head_sc, V, (t + 2 * G) * kTile, 0, H / 32, p.lgs);
+      tile_issue<float, SA, 4, false>(ahead, p.head_qw, p.head_qz, p.head_sc, V, (t + 2 * G) * kTile, 0, H / 32, p.lgs);
     const int n = t * kTile + (int)threadIdx.x;
     const float y = tile_sum(tile_mma(cur, s.xa, s.cx, 0, t * kTile, p.lgs, zo), s.red) / rn;
     if (threadIdx.x < 64 && n < V) {

@@ -1,0 +1,265 @@
+// One-row int4 GPTQ GEMV on the gfx950 matrix cores, for layers large enough to be bound by
+// HBM bandwidth (the decode projections of 1B+ models, tied heads).
+//
+// y[n] = sum_k x[k] W[k][n] (+ bias), W[k][n] = s[g][n] (q[k][n] - (z[g][n] + zoff)).
+//
+// Grid (tiles of 256 columns, K-slices); a 256-thread workgroup holds 4 waves, one per 64
+// columns, each taking every 32-k step of its K-slice. A wave issues the loads of all its steps
+// (16 bytes of codes per lane per step, scales and zeros per group) at entry, then the
+// workgroup stages its slice of x in LDS as exact three-term bf16 splits (the A operand of the
+// shared tile code, mma_tile.h) and the waves run four MFMA chains that share each step's A
+// fragment. With one K-slice the workgroup writes y; with several, each writes fp32
+// partials in the workspace at device scope and the last to arrive (agent-scope counter) sums
+// them in slice order, adds the bias, writes y and re-arms the counter, so results are
+// deterministic. Several workgroups per CU keep ~50-100 KB of weights in flight per CU.
+#include <algorithm>
+
+#include "miq_common.h"
+#include "mma_tile.h"
+
+namespace miq {
+namespace gm {
+
+using namespace mt;
+
+constexpr int kThreadsG = 256;
+constexpr int kMaxSlices = 32;
+
+template <typename ST> struct Scales4;
+template <> struct Scales4<__half> {  // four fp16 scales of adjacent columns
+  using T = uint2;
+  static __device__ __forceinline__ T load(const __half* p) { return *reinterpret_cast<const uint2*>(p); }
+  static __device__ __forceinline__ float get(const T& v, int t) {
+    const uint32_t w = t < 2 ? v.x : v.y;
+    return __half2float(__ushort_as_half((unsigned short)((t & 1) ? w >> 16 : w & 0xFFFFu)));
+  }
+};
+template <> struct Scales4<float> {
+  using T = uint4;
+  static __device__ __forceinline__ T load(const float* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ float get(const T& v, int t) {
+    return __uint_as_float(t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w);
+  }
+};
+
+// Groups of 128 values (4 steps of 32). A 256-thread workgroup covers 256 columns; wave w takes
+// the 64 columns [64 w, 64 w + 64) and every step of the workgroup's K-slice. Lane l loads 16
+// bytes -- the codes of 4 adjacent columns 4 (l & 15) .. + 3 -- of packed row (l >> 4) of each
+// step (a wave load covers 4 rows x 256 contiguous bytes), and feeds them to four MFMAs that
+// share the step's A fragment: MFMA t's column l & 15 is the lane's column 4 (l & 15) + t. Each
+// lane thus holds whole column results for 4 columns; no reduction across waves is needed.
+template <typename XT, typename ST, typename OT, int SPQ, bool PERM>
+__global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restrict__ x, const int32_t* __restrict__ perm,
+                                                             const uint32_t* __restrict__ qw,
+                                                             const uint32_t* __restrict__ qz, const ST* __restrict__ sc,
+                                                             const float* __restrict__ bias, OT* __restrict__ out,
+                                                             float* __restrict__ partials, int* __restrict__ counters,
+                                                             int K, int N, float zoff, int slice_steps) {
+  constexpr int NG = SPQ / 4;  // groups per slice
+  using SV = typename Scales4<ST>::T;
+  __shared__ __align__(16) unsigned char xa[SPQ * kStepBytes];
+  __shared__ float2 cx[SPQ];
+  __shared__ int is_last;
+  const int tile = blockIdx.x, sl = blockIdx.y, kslices = gridDim.y;
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int st0 = sl * slice_steps;
+  const int ns = min(slice_steps, K / 32 - st0);  // a multiple of 4, > 0 by the planner
+  const int rb = st0 * 4;                          // first packed row of the slice
+  const int c = tile * 256 + wave * 64 + (lane & 15) * 4;
+  const int cl = min(c, N - 4);                    // loads stay in bounds past N
+  // this thread's 8 activations of the slice (or their permutation indices) as raw 16-byte
+  // loads, issued before the weights; gathering and converting wait until the weight loads are
+  // in flight, so the activation round trip overlaps them. Threads past the slice's chunks
+  // stage one of the first four steps' chunks again (same values to the same LDS words): with
+  // no branch around them, the compiler keeps the loads ahead of the weight loads.
+  const int ch = (int)threadIdx.x < ns * 4 ? (int)threadIdx.x : (int)(threadIdx.x & 15);
+  const int k0 = st0 * 32 + ch * 8;
+  const uint4* src = PERM ? reinterpret_cast<const uint4*>(perm + k0) : reinterpret_cast<const uint4*>(x + k0);
+  const uint4 xr0 = src[0];
+  const uint4 xr1 = src[(PERM || sizeof(XT) == 4) ? 1 : 0];
+  // every step's codes and every group's scales and zeros of this wave, issued up front
+  uint4 w[SPQ];
+  SV sv[NG];
+  uint32_t zw[NG];
+  const uint32_t* wp = qw + (size_t)(rb + (lane >> 4)) * N + cl;
+  // steps past the slice's end reload its last step (a select, not a branch: a branch around a
+  // load makes the compiler's wait counts conservative at the join)
+#pragma unroll
+  for (int i = 0; i < SPQ; ++i) w[i] = *reinterpret_cast<const uint4*>(wp + (size_t)(4 * min(i, ns - 1)) * N);
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const int g = (rb >> 4) + min(gi, (ns >> 2) - 1);  // 16 packed rows per group
+    sv[gi] = Scales4<ST>::load(sc + (size_t)g * N + cl);
+    zw[gi] = qz[(size_t)g * (N >> 3) + (cl >> 3)];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the scheduler keeps every load above the conversions
+  float v[8];
+  const uint32_t r[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
+  if (PERM) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = to_f32(x[r[j]]);  // indices are non-negative
+  } else if (sizeof(XT) == 2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = __half2float(__ushort_as_half((unsigned short)(r[j] & 0xFFFFu)));
+      v[2 * j + 1] = __half2float(__ushort_as_half((unsigned short)(r[j] >> 16)));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(r[j]);
+  }
+  stage_chunk(ch, v, xa, cx);
+  __syncthreads();
+  // A rows 0-2 are read by lanes 0-2 of each 16; the other rows of D are never used
+  const bool arow = (lane & 15) < 3;
+  const unsigned char* ap = xa + (lane >> 4) * 64 + (lane & 15) * 16;
+  const int zsh = (cl & 7) * 4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    if (4 * gi < ns) {
+      floatx4 d[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) d[t] = (floatx4){0.f, 0.f, 0.f, 0.f};
+      float cs = 0.f, xs = 0.f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int i = 4 * gi + s4;
+        bf16x8 av;
+        if (arow) av = *reinterpret_cast<const bf16x8*>(ap + i * kStepBytes);
+        const float2 cxi = cx[i];
+        cs += cxi.x;
+        xs += cxi.y;
+        const uint32_t wt[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 bw = b_bf16(wt[t]);
+          d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), d[t], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float pv = (d[t][0] + d[t][1]) + d[t][2];
+        const float zc = (float)((zw[gi] >> (zsh + 4 * t)) & 15u) + zoff;
+        acc[t] = fmaf(Scales4<ST>::get(sv[gi], t), pv - fmaf(zc, xs, cs), acc[t]);
+      }
+    }
+  }
+  const bool mine = lane < 16 && c < N;
+  if (kslices == 1) {
+    if (mine)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) out[c + t] = from_f32<OT>(bias ? acc[t] + bias[c + t] : acc[t]);
+    return;
+  }
+  // split K: partials at device scope, the last workgroup of the tile sums them in slice order
+  if (mine)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      __hip_atomic_store(partials + (size_t)sl * N + c + t, acc[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kslices - 1;
+  __syncthreads();
+  if (!is_last) return;
+  const int n = tile * 256 + (int)threadIdx.x;
+  if (n < N) {
+    float pp[kMaxSlices];
+#pragma unroll
+    for (int i = 0; i < kMaxSlices; ++i)  // all loads in flight at once
+      pp[i] = i < kslices ? __hip_atomic_load(partials + (size_t)i * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : 0.f;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxSlices; ++i)
+      if (i < kslices) s += pp[i];
+    out[n] = from_f32<OT>(bias ? s + bias[n] : s);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Launch shape: ~4 workgroups per CU, K-slices of a multiple of 4 steps (whole groups), at most
+// 16 steps and 32 slices; SPQ is the slice length rounded up to an instantiated capacity.
+struct Plan {
+  int tiles, kslices, slice_steps, spq;
+  size_t ws_bytes;
+};
+
+static bool plan(int K, int N, Plan* p) {
+  const int steps = K / 32;
+  p->tiles = (N + 255) / 256;
+  int ks = (4 * kCUs + p->tiles - 1) / p->tiles;
+  ks = std::max(ks, (steps + 15) / 16);
+  ks = std::min(ks, std::min(kMaxSlices, steps / 4));
+  int ss = (steps + ks - 1) / ks;
+  ss = (ss + 3) & ~3;
+  if (ss > 16) return false;
+  p->slice_steps = ss;
+  p->kslices = (steps + ss - 1) / ss;
+  if (p->kslices > kMaxSlices || (p->kslices > 1 && p->tiles > kMaxCounters)) return false;
+  p->spq = ss <= 4 ? 4 : ss <= 8 ? 8 : ss <= 12 ? 12 : 16;
+  p->ws_bytes = p->kslices > 1 ? kCounterBytes + (size_t)p->kslices * N * 4 : 0;
+  return true;
+}
+
+template <typename XT, typename ST, typename OT>
+static int launch(const Plan& pl, const void* x, const int32_t* perm, const int32_t* qw, const int32_t* qz,
+                  const void* sc, const float* bias, void* out, void* ws, int K, int N, float zoff, hipStream_t st) {
+  int* counters = pl.kslices > 1 ? static_cast<int*>(ws) : nullptr;
+  float* partials = pl.kslices > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
+  dim3 grid(pl.tiles, pl.kslices);
+#define MIQ_GM_LAUNCH(S, P)                                                                                        \
+  hipLaunchKernelGGL((gemv_mma_kernel<XT, ST, OT, S, P>), grid, dim3(kThreadsG), 0, st, static_cast<const XT*>(x), \
+                     perm, reinterpret_cast<const uint32_t*>(qw), reinterpret_cast<const uint32_t*>(qz),           \
+                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, K, N, zoff,      \
+                     pl.slice_steps)
+#define MIQ_GM_SPQ(S)          \
+  {                            \
+    if (perm)                  \
+      MIQ_GM_LAUNCH(S, true);  \
+    else                       \
+      MIQ_GM_LAUNCH(S, false); \
+  }
+  if (pl.spq == 4) MIQ_GM_SPQ(4)
+  else if (pl.spq == 8) MIQ_GM_SPQ(8)
+  else if (pl.spq == 12) MIQ_GM_SPQ(12)
+  else MIQ_GM_SPQ(16)
+#undef MIQ_GM_SPQ
+#undef MIQ_GM_LAUNCH
+  return check_launch("gemv_mma");
+}
+
+}  // namespace gm
+
+// Entry used by miq_gptq_gemv for one row of int4 codes (see there for the argument contract).
+// Returns MIQ_ERR_UNSUPPORTED (before launching anything) for shapes it does not cover.
+int gemv_mma(const void* x, int xd, const int32_t* perm, const int32_t* qw, const int32_t* qz, const void* sc,
+             int sd, const float* bias, void* out, int od, int K, int N, int gs, float zoff, void* ws,
+             size_t ws_bytes, hipStream_t st) {
+  if (gs != 128 || K % 128 || N % 8 || !aligned(qw, 16) || !aligned(sc, 16) || !aligned(x, 16) ||
+      (perm && !aligned(perm, 16)))
+    return MIQ_ERR_UNSUPPORTED;
+  gm::Plan pl;
+  if (!gm::plan(K, N, &pl)) return MIQ_ERR_UNSUPPORTED;
+  if (pl.kslices > 1 && (!ws || ws_bytes < pl.ws_bytes)) return MIQ_ERR_UNSUPPORTED;
+#define MIQ_GM_TYPES(XT, ST, OT) return gm::launch<XT, ST, OT>(pl, x, perm, qw, qz, sc, bias, out, ws, K, N, zoff, st)
+  if (xd == MIQ_F16) {
+    if (sd == MIQ_F16) { if (od == MIQ_F16) MIQ_GM_TYPES(__half, __half, __half); MIQ_GM_TYPES(__half, __half, float); }
+    if (od == MIQ_F16) MIQ_GM_TYPES(__half, float, __half);
+    MIQ_GM_TYPES(__half, float, float);
+  }
+  if (sd == MIQ_F16) { if (od == MIQ_F16) MIQ_GM_TYPES(float, __half, __half); MIQ_GM_TYPES(float, __half, float); }
+  if (od == MIQ_F16) MIQ_GM_TYPES(float, float, __half);
+  MIQ_GM_TYPES(float, float, float);
+#undef MIQ_GM_TYPES
+}
+
+// Workspace bytes gemv_mma needs for this shape (0 if it needs none or does not cover it).
+size_t gemv_mma_workspace(int K, int N) {
+  gm::Plan pl;
+  if (K % 128 || !gm::plan(K, N, &pl)) return 0;
+  return pl.ws_bytes;
+}
+
+}  // namespace miq

@@ -11,6 +11,7 @@
 // through an act-order permutation) are staged once per workgroup in LDS as fp32, with
 // per-chunk sums so the zero point is applied once per chunk: sum x*(q - z) is computed as
 // sum x*q - z * sum x.
+#include <algorithm>
 #include <type_traits>
 
 #include "miq_common.h"
@@ -81,6 +82,9 @@ __global__ __launch_bounds__(256) void gptq_repack_kernel(const uint32_t* __rest
 // the last to arrive (device-scope atomic counter) sums them in ksplit order, adds the bias,
 // writes the output and re-arms the counter to zero, so results are deterministic.
 
+#ifndef MIQ_GEMV_MMA_MIN_BYTES
+#define MIQ_GEMV_MMA_MIN_BYTES (4u << 20)  // int4 codes of a layer from which one row takes gemv_mma
+#endif
 #ifndef MIQ_GEMV_MIN_WGS
 #define MIQ_GEMV_MIN_WGS 1  // split K further while fewer workgroups than this would run
 #endif
@@ -614,6 +618,8 @@ extern "C" int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, in
   rc = gemv_plan(M, K, N, gs, bits, x_dtype, true, &p);
   if (rc) return rc;
   *bytes = p.ws_bytes;
+  if (M == 1 && bits == 4 && (size_t)K * N / 2 >= MIQ_GEMV_MMA_MIN_BYTES)
+    *bytes = std::max(*bytes, gemv_mma_workspace(K, N));
   return MIQ_OK;
 }
 
@@ -624,6 +630,13 @@ extern "C" int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, co
   int rc = gemv_check("gptq_gemv", x, x_dtype, qweight, qzeros, scales, scales_dtype, out, out_dtype, M, K, N,
                       gs, bits);
   if (rc || M == 0) return rc;
+  // one row of a large int4 layer: the matrix-core GEMV (it declines shapes it does not cover)
+  if (M == 1 && bits == 4 && (size_t)K * N / 2 >= MIQ_GEMV_MMA_MIN_BYTES &&
+      (workspace == nullptr || aligned(workspace, 256))) {
+    rc = gemv_mma(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, K, N, gs,
+                  zero_offset, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+    if (rc != MIQ_ERR_UNSUPPORTED) return rc;
+  }
   GemvPlan p;
   rc = gemv_plan(M, K, N, gs, bits, x_dtype, workspace != nullptr, &p);
   if (rc) return rc;

@@ -20,6 +20,13 @@ int check_launch(const char* what);
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// One-row int4 GEMV on the matrix cores (gemv_mma.hip), used by miq_gptq_gemv for large layers;
+// returns MIQ_ERR_UNSUPPORTED without launching for shapes it does not cover.
+int gemv_mma(const void* x, int xd, const int32_t* perm, const int32_t* qw, const int32_t* qz, const void* sc,
+             int sd, const float* bias, void* out, int od, int K, int N, int gs, float zoff, void* ws,
+             size_t ws_bytes, hipStream_t st);
+size_t gemv_mma_workspace(int K, int N);
+
 // ---- element loads / stores for the activation / output dtypes ---------------------
 template <typename T> __device__ __forceinline__ float to_f32(T v);
 template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
