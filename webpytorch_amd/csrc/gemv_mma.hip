@@ -8,10 +8,15 @@
 // (16 bytes of codes per lane per step, scales and zeros per group) at entry, then the
 // workgroup stages its slice of x in LDS as exact three-term bf16 splits (the A operand of the
 // shared tile code, mma_tile.h) and the waves run four MFMA chains that share each step's A
-// fragment. With one K-slice the workgroup writes y; with several, each writes fp32
-// partials in the workspace at device scope and the last to arrive (agent-scope counter) sums
-// them in slice order, adds the bias, writes y and re-arms the counter, so results are
-// deterministic. Several workgroups per CU keep ~50-100 KB of weights in flight per CU.
+// fragment. With one K-slice the workgroup writes y. With several, the slices of a column meet
+// in one 64-bit word of the workspace's zeroed counter region: each adds its partial as a
+// fixed-point integer (2^-24 resolution, offset to stay non-negative) together with a count in
+// the top bits, by one agent-scope atomic whose return value tells the last slice that it is
+// last and holds the whole sum; that slice writes y (+ bias) and re-zeroes the word. Integer
+// sums do not depend on the order of arrival, so results are deterministic, and the reduction
+// costs one round trip to the coherence point. Columns past the counter region (N > 32768)
+// use fp32 partials and a per-tile arrival counter instead (three round trips). Several
+// workgroups per CU keep ~50-100 KB of weights in flight per CU.
 #include <algorithm>
 
 #include "miq_common.h"
@@ -24,6 +29,14 @@ using namespace mt;
 
 constexpr int kThreadsG = 256;
 constexpr int kMaxSlices = 32;
+// fixed-point slice sums: a partial p becomes round(p * 2^24) + 2^51, in [0, 2^52) for
+// |p| < 2^27 (partials beyond saturate, NaN to -2^27); 32 of them stay below 2^57, and the
+// arrival count sits in bits 58-63
+constexpr float kFixScale = 16777216.f;
+constexpr float kFixSat = 134217720.f;  // the largest float below 2^27
+constexpr unsigned long long kFixBias = 1ull << 51;
+constexpr int kCountShift = 58;
+constexpr size_t kMaxFixCols = kCounterBytes / 8;
 
 template <typename ST> struct Scales4;
 template <> struct Scales4<__half> {  // four fp16 scales of adjacent columns
@@ -54,7 +67,8 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
                                                              const uint32_t* __restrict__ qz, const ST* __restrict__ sc,
                                                              const float* __restrict__ bias, OT* __restrict__ out,
                                                              float* __restrict__ partials, int* __restrict__ counters,
-                                                             int K, int N, float zoff, int slice_steps) {
+                                                             unsigned long long* __restrict__ fixacc, int K, int N,
+                                                             float zoff, int slice_steps) {
   constexpr int NG = SPQ / 4;  // groups per slice
   using SV = typename Scales4<ST>::T;
   __shared__ __align__(16) unsigned char xa[SPQ * kStepBytes];
@@ -152,6 +166,28 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
       for (int t = 0; t < 4; ++t) out[c + t] = from_f32<OT>(bias ? acc[t] + bias[c + t] : acc[t]);
     return;
   }
+  if (fixacc) {
+    // split K over fixed-point words: lane l takes column 4 (l & 15) + (l >> 4) of the wave's 64
+    const int t = lane >> 4;
+    const float a0 = __shfl(acc[0], lane & 15, 64), a1 = __shfl(acc[1], lane & 15, 64);
+    const float a2 = __shfl(acc[2], lane & 15, 64), a3 = __shfl(acc[3], lane & 15, 64);
+    const float p = t == 0 ? a0 : t == 1 ? a1 : t == 2 ? a2 : a3;
+    const int n = tile * 256 + wave * 64 + (lane & 15) * 4 + t;
+    if (n < N) {
+      const float pc = fminf(fmaxf(p, -kFixSat), kFixSat);
+      const unsigned long long add =
+          (1ull << kCountShift) + (unsigned long long)(__float2ll_rn(pc * kFixScale) + (long long)kFixBias);
+      const unsigned long long old =
+          __hip_atomic_fetch_add(fixacc + n, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((int)(old >> kCountShift) == kslices - 1) {
+        const long long tot = (long long)((old + add) & ((1ull << kCountShift) - 1)) - (long long)kslices * (long long)kFixBias;
+        const float y = (float)tot * (1.f / kFixScale);
+        out[n] = from_f32<OT>(bias ? y + bias[n] : y);
+        __hip_atomic_store(fixacc + n, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    return;
+  }
   // split K: partials at device scope, the last workgroup of the tile sums them in slice order
   if (mine)
 #pragma unroll
@@ -183,6 +219,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
 // 16 steps and 32 slices; SPQ is the slice length rounded up to an instantiated capacity.
 struct Plan {
   int tiles, kslices, slice_steps, spq;
+  bool fixed;  // split K reduced in fixed-point words of the counter region
   size_t ws_bytes;
 };
 
@@ -199,20 +236,23 @@ static bool plan(int K, int N, Plan* p) {
   p->kslices = (steps + ss - 1) / ss;
   if (p->kslices > kMaxSlices || (p->kslices > 1 && p->tiles > kMaxCounters)) return false;
   p->spq = ss <= 4 ? 4 : ss <= 8 ? 8 : ss <= 12 ? 12 : 16;
-  p->ws_bytes = p->kslices > 1 ? kCounterBytes + (size_t)p->kslices * N * 4 : 0;
+  p->fixed = p->kslices > 1 && (size_t)N <= kMaxFixCols;
+  p->ws_bytes = p->kslices == 1 ? 0 : p->fixed ? kCounterBytes : kCounterBytes + (size_t)p->kslices * N * 4;
   return true;
 }
 
 template <typename XT, typename ST, typename OT>
 static int launch(const Plan& pl, const void* x, const int32_t* perm, const int32_t* qw, const int32_t* qz,
                   const void* sc, const float* bias, void* out, void* ws, int K, int N, float zoff, hipStream_t st) {
-  int* counters = pl.kslices > 1 ? static_cast<int*>(ws) : nullptr;
-  float* partials = pl.kslices > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
+  const bool slow = pl.kslices > 1 && !pl.fixed;
+  int* counters = slow ? static_cast<int*>(ws) : nullptr;
+  float* partials = slow ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
+  unsigned long long* fixacc = pl.fixed ? static_cast<unsigned long long*>(ws) : nullptr;
   dim3 grid(pl.tiles, pl.kslices);
 #define MIQ_GM_LAUNCH(S, P)                                                                                        \
   hipLaunchKernelGGL((gemv_mma_kernel<XT, ST, OT, S, P>), grid, dim3(kThreadsG), 0, st, static_cast<const XT*>(x), \
                      perm, reinterpret_cast<const uint32_t*>(qw), reinterpret_cast<const uint32_t*>(qz),           \
-                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, K, N, zoff,      \
+                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, fixacc, K, N, zoff, \
                      pl.slice_steps)
 #define MIQ_GM_SPQ(S)          \
   {                            \
