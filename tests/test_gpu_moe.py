@@ -113,6 +113,51 @@ def test_moe_graph_capture_routes_live(gpu):
         _check(got, ref, rel=1e-5)
 
 
+@pytest.mark.parametrize("T,E,k", [(37, 40, 3), (64, 200, 6), (20, 300, 4), (9, 700, 8), (256, 128, 8),
+                                   (3, 1024, 32), (1, 5, 5)])
+def test_route_layout(gpu, T, E, k):
+    """The whole route buffer against a float64 softmax with top-k by (probability, lowest
+    index): picks ascending per token, their renormalised weights, each expert's slots in
+    ascending token order, the expert offsets and the 32-row tiles. Row 0 has tied logits."""
+    import torch
+    from webpytorch_amd import core
+    rng = np.random.default_rng(T * 1000 + E)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[0, :E // 2] = lg[0, E // 2]
+    nbytes = core.moe_route_bytes(T, E, k)
+    route = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    lgd = torch.from_numpy(lg).cuda()
+    core._lib.call("miq_moe_route", core.ptr(lgd), T, E, k, 1, core.ptr(route), route.numel(),
+                   core.stream_handle())
+    r = route.cpu().numpy().view(np.int32)
+    tk = T * k
+    p = moe.softmax_rows(lg)
+    order = np.lexsort((np.broadcast_to(np.arange(E), p.shape), -p), axis=1)[:, :k]
+    exp_e = np.sort(order, axis=1)
+    pw = np.take_along_axis(p, exp_e, 1)
+    exp_w = (pw / pw.sum(1, keepdims=True)).astype(np.float32)
+    got_e = r[:tk].reshape(T, k)
+    got_w = r[tk:2 * tk].view(np.float32).reshape(T, k)
+    assert np.array_equal(got_e, exp_e)
+    np.testing.assert_allclose(got_w, exp_w, rtol=1e-6, atol=0)
+    slot_of, sorted_tok = r[2 * tk:3 * tk], r[3 * tk:4 * tk]
+    sorted_w = r[4 * tk:5 * tk].view(np.float32)
+    off = r[5 * tk:5 * tk + E + 1]
+    cnt = np.bincount(exp_e.ravel(), minlength=E)
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(cnt)]))
+    for e in range(E):
+        toks = np.nonzero((exp_e == e).any(1))[0]
+        assert np.array_equal(sorted_tok[off[e]:off[e + 1]], toks), e
+    for i in range(tk):
+        s = slot_of[i]
+        assert sorted_tok[s] == i // k and sorted_w[s] == got_w.ravel()[i]
+    ntiles = r[5 * tk + E + 1]
+    t0 = (5 * tk + E + 1 + 1 + 3) & ~3
+    tiles = r[t0:t0 + 4 * ntiles].reshape(-1, 4)
+    want = [(e, off[e] + r0, min(32, cnt[e] - r0), 0) for e in range(E) for r0 in range(0, cnt[e], 32)]
+    assert [tuple(t) for t in tiles] == want
+
+
 def test_moe_rejects_bad_sizes(gpu):
     from webpytorch_amd import core
     with pytest.raises(NotImplementedError, match="T\\*k"):

@@ -16,6 +16,7 @@
 // expert (up to kMoeBM rows) and 256 output columns. The intermediate h keeps fp32 accuracy
 // through the fp16 matrix cores as two fp16 halves, hi = fp16(h) and lo = fp16(h - hi)
 // (together exact to about 22 bits); the down GEMM multiplies both by the same weights.
+#include <algorithm>
 #include <type_traits>
 
 #include "miq_common.h"
@@ -48,16 +49,88 @@ __host__ __device__ inline RouteLayout route_layout(int T, int E, int k) {
 }
 
 // ------------------------------------------------------------------------------------
-// Router: one workgroup of 1024 threads. Phase 1, a wave per token: float64 softmax over the E
-// logits, k rounds of arg-max (lowest index on ties), renormalisation over the picks, then the
-// picks sorted by expert. Phase 2: per-expert counts, offsets and row tiles. Phase 3: a thread
-// per expert walks the tokens in order and assigns slots, so each expert's rows are in ascending
-// token order.
-__global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int k,
-                                                         int norm_topk, int* __restrict__ route) {
+// Router, two kernels. Top-k: a wave per token (four per workgroup): float64 softmax over the E
+// logits (each lane keeps the probabilities of experts lane, lane + 64, ... in registers), k
+// rounds of arg-max over them (lowest index on ties; a pick is set to -1 so it cannot win
+// again; lane j keeps pick j), renormalisation over the picks, and the picks stored in
+// ascending expert order. Slots: one workgroup of 1024 threads with the picks in LDS counts
+// each expert's picks (LDS atomics: sums do not depend on order), turns the counts into offsets
+// and row tiles (prefix sums over the experts), and then one wave walks the picks in order and
+// hands out each expert's slots, so each expert's rows are in ascending token order.
+template <int EPL>  // experts per lane: E <= 64 * EPL
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                       int norm_topk, int* __restrict__ route) {
   const RouteLayout L = route_layout(T, E, k);
   int* topk_e = route + L.topk_e;
   float* topk_w = reinterpret_cast<float*>(route + L.topk_w);
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves
+  {
+    const float* lt = logits + (size_t)t * E;
+    double pv[EPL];
+    double mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      pv[i] = e < E ? (double)lt[e] : -INFINITY;
+      mx = fmax(mx, pv[i]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+    double sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i < E) {
+        pv[i] = exp(pv[i] - mx);
+        sum += pv[i];
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) pv[i] = lane + 64 * i < E ? pv[i] / sum : -1.0;
+    // lane j keeps pick j (k <= 32), so no per-lane array is indexed at run time
+    int my_e = E;
+    double my_p = 0.0;
+    double psum = 0.0;
+    for (int j = 0; j < k; ++j) {
+      double best = -1.0;
+      int be = E;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (pv[i] > best) {  // ascending e within the lane: the first of equals stays
+          best = pv[i];
+          be = lane + 64 * i;
+        }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const double ob = __shfl_xor(best, o, 64);
+        const int oe = __shfl_xor(be, o, 64);
+        if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; }
+      }
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (lane + 64 * i == be) pv[i] = -1.0;
+      if (lane == j) {
+        my_e = be;
+        my_p = best;
+      }
+      psum += best;
+    }
+    // ascending expert order: a pick's rank is the number of picks with a smaller expert
+    int rank = 0;
+    for (int i = 0; i < k; ++i) rank += __shfl(my_e, i, 64) < my_e;
+    if (lane < k) {
+      topk_e[t * k + rank] = my_e;
+      topk_w[t * k + rank] = (float)(norm_topk ? my_p / psum : my_p);
+    }
+  }
+}
+
+__global__ __launch_bounds__(1024) void moe_slots_kernel(int T, int E, int k, int* __restrict__ route) {
+  const RouteLayout L = route_layout(T, E, k);
+  const int* topk_e = route + L.topk_e;
+  const float* topk_w = reinterpret_cast<const float*>(route + L.topk_w);
   int* slot_of = route + L.slot_of;
   int* sorted_tok = route + L.sorted_tok;
   float* sorted_w = reinterpret_cast<float*>(route + L.sorted_w);
@@ -65,91 +138,88 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float* __restrict
   int* ntiles = route + L.ntiles;
   int4* tiles = reinterpret_cast<int4*>(route + L.tiles);
 
-  // everything phases 2 and 3 read lives in LDS
   extern __shared__ int lds_i[];
-  int* se = lds_i;                                         // [T*k] chosen experts, ascending per token
-  float* sw = reinterpret_cast<float*>(lds_i + T * k);     // [T*k] their weights
-  int* cnt = lds_i + 2 * T * k;                            // [E]
-  int* off = cnt + E;                                      // [E + 1]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-
-  for (int t = wave; t < T; t += nw) {
-    const float* lt = logits + (size_t)t * E;
-    double mx = -INFINITY;
-    for (int e = lane; e < E; e += 64) mx = fmax(mx, (double)lt[e]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
-    double sum = 0.0;
-    for (int e = lane; e < E; e += 64) sum += exp((double)lt[e] - mx);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    // k rounds of arg-max over p = exp(l - max) / sum; a picked expert is excluded afterwards
-    int pick_e[32];
-    double pick_p[32];
-    double psum = 0.0;
-    for (int j = 0; j < k; ++j) {
-      double best = -1.0;
-      int be = E;
-      for (int e = lane; e < E; e += 64) {
-        bool taken = false;
-        for (int i = 0; i < j; ++i) taken |= (pick_e[i] == e);
-        if (taken) continue;
-        const double pe = exp((double)lt[e] - mx) / sum;
-        if (pe > best || (pe == best && e < be)) { best = pe; be = e; }
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const double ob = __shfl_xor(best, o, 64);
-        const int oe = __shfl_xor(be, o, 64);
-        if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; }
-      }
-      pick_e[j] = be;
-      pick_p[j] = best;
-      psum += best;
-    }
-    if (lane == 0) {
-      // ascending expert order (insertion sort of k <= 32 picks)
-      for (int a = 1; a < k; ++a)
-        for (int b = a; b > 0 && pick_e[b - 1] > pick_e[b]; --b) {
-          const int te = pick_e[b]; pick_e[b] = pick_e[b - 1]; pick_e[b - 1] = te;
-          const double tp = pick_p[b]; pick_p[b] = pick_p[b - 1]; pick_p[b - 1] = tp;
-        }
-      for (int j = 0; j < k; ++j) {
-        const float w = (float)(norm_topk ? pick_p[j] / psum : pick_p[j]);
-        se[t * k + j] = pick_e[j];
-        sw[t * k + j] = w;
-        topk_e[t * k + j] = pick_e[j];
-        topk_w[t * k + j] = w;
-      }
-    }
+  const int TK = T * k;
+  int* se = lds_i;                                   // [TK] chosen experts, ascending per token
+  float* sw = reinterpret_cast<float*>(lds_i + TK);  // [TK] their weights
+  int* cnt = lds_i + 2 * TK;                         // [E + 1] picks per expert
+  int* off = cnt + E + 1;                            // [E + 1] first slot per expert
+  int* run = off + E + 1;                            // [E + 1] slots assigned so far
+  int* wsum = run + E + 1;                           // [2][16] wave totals of the scans
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    cnt[e] = 0;
+    run[e] = 0;
   }
-  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < T * k; i += blockDim.x) atomicAdd(&cnt[se[i]], 1);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int o = 0, nt = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = o;
-      expert_off[e] = o;
-      for (int r0 = 0; r0 < cnt[e]; r0 += kMoeBM) tiles[nt++] = make_int4(e, o + r0, min(kMoeBM, cnt[e] - r0), 0);
-      o += cnt[e];
-    }
-    off[E] = o;
-    expert_off[E] = o;
-    *ntiles = nt;
+  for (int i = threadIdx.x; i < TK; i += blockDim.x) {
+    se[i] = topk_e[i];
+    sw[i] = topk_w[i];
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int s = off[e];
-    for (int t = 0; t < T; ++t)
-      for (int j = 0; j < k; ++j)
-        if (se[t * k + j] == e) {
-          slot_of[t * k + j] = s;
-          sorted_tok[s] = t;
-          sorted_w[s] = sw[t * k + j];
-          ++s;
-        }
+  for (int i = threadIdx.x; i < TK; i += blockDim.x) atomicAdd(&cnt[se[i]], 1);  // sums: order-free
+  __syncthreads();
+  // expert e's rows and row tiles, exclusive prefix sums over e (one expert per thread,
+  // E <= 1024): wave scans, then the wave totals
+  int c = 0, ntl = 0;
+  if ((int)threadIdx.x < E) {
+    c = cnt[threadIdx.x];
+    ntl = (c + kMoeBM - 1) / kMoeBM;
+  }
+  int pc = c, pt = ntl;  // inclusive scans within the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int uc = __shfl_up(pc, o, 64), ut = __shfl_up(pt, o, 64);
+    if (lane >= o) {
+      pc += uc;
+      pt += ut;
+    }
+  }
+  if (lane == 63) {
+    wsum[wave] = pc;
+    wsum[16 + wave] = pt;
+  }
+  __syncthreads();
+  int bc = 0, bt = 0;
+  for (int w = 0; w < wave; ++w) {
+    bc += wsum[w];
+    bt += wsum[16 + w];
+  }
+  if ((int)threadIdx.x < E) {
+    const int e = threadIdx.x, o = bc + pc - c, t0 = bt + pt - ntl;
+    off[e] = o;
+    expert_off[e] = o;
+    for (int i = 0; i < ntl; ++i) tiles[t0 + i] = make_int4(e, o + i * kMoeBM, min(kMoeBM, c - i * kMoeBM), 0);
+    if (e == E - 1) {
+      off[E] = o + c;
+      expert_off[E] = o + c;
+      *ntiles = t0 + ntl;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // one wave walks the picks in order, 64 at a time: a pick's slot is its expert's offset, plus
+  // the slots that expert already gave out, plus the earlier lanes with the same expert (the
+  // lanes that match it, from ballots over the bits of the expert index)
+  for (int i0 = 0; i0 < TK; i0 += 64) {
+    const int i = i0 + lane;
+    const bool valid = i < TK;
+    const int e = valid ? se[i] : E;  // E: a sentinel with its own (unused) counter
+    uint64_t m = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 11; ++b) {  // E <= 1024 < 2^11
+      const bool bit = (e >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      m &= bit ? bb : ~bb;
+    }
+    const int rank = __popcll(m & ((1ull << lane) - 1));
+    const int base = run[e];
+    if (valid) {
+      const int sl = off[e] + base + rank;
+      slot_of[i] = sl;
+      sorted_tok[sl] = i / k;
+      sorted_w[sl] = sw[i];
+    }
+    if (rank == 0) run[e] = base + __popcll(m);
   }
 }
 
@@ -168,7 +238,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   constexpr int TM = kMoeBM / 16;
   constexpr int STEPS = KC / 32;
   constexpr int RB = BITS == 4 ? 1 : 2;
-  constexpr int NSET = GATE_UP ? 2 : 1;
+  constexpr int NSET = 1;  // weight sets per wave (gate_up: waves 0-1 gate, 2-3 up)
+  constexpr int WCOLS = GATE_UP ? 128 : 256;  // columns per workgroup
   constexpr int NA = GATE_UP ? 1 : 2;  // activation planes (down: hi and lo)
   __shared__ __align__(16) _Float16 xs[NA][kMoeBM * KC];
 
@@ -183,14 +254,15 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int p = lane & 15, kb = lane >> 4;
-  const int ncol = blockIdx.x * 256 + wave * 64 + 4 * p;
+  const int cw = GATE_UP ? (wave & 1) : wave, set = GATE_UP ? (wave >> 1) : 0;
+  const int ncol = blockIdx.x * WCOLS + cw * 64 + 4 * p;
   const bool colok = ncol < N;
-  const bool wave_active = blockIdx.x * 256 + wave * 64 < N;
+  const bool wave_active = blockIdx.x * WCOLS + cw * 64 < N;
   const int NZ = N / PER;
   const int zshift = (ncol % PER) * BITS;
-  const uint32_t* qw[2] = {qw0 + e * qw_stride, GATE_UP ? qw1 + e * qw_stride : nullptr};
-  const uint32_t* qz[2] = {qz0 + e * qz_stride, GATE_UP ? qz1 + e * qz_stride : nullptr};
-  const ST* sc[2] = {sc0 + e * sc_stride, GATE_UP ? sc1 + e * sc_stride : nullptr};
+  const uint32_t* qw[1] = {(set ? qw1 : qw0) + e * qw_stride};
+  const uint32_t* qz[1] = {(set ? qz1 : qz0) + e * qz_stride};
+  const ST* sc[1] = {(set ? sc1 : sc0) + e * sc_stride};
 
   float4v acc[NSET][TM][4];
 #pragma unroll
@@ -200,51 +272,73 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 #pragma unroll
       for (int s = 0; s < 4; ++s) acc[q][t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-  for (int kc0 = 0; kc0 < K; kc0 += KC) {
+  // Register double buffer: while one K chunk is multiplied, the next chunk's codes, scales,
+  // zero points and activation rows are in flight. Loads use addresses clamped into the
+  // matrices (columns past N, the chunk after the last), so no branch surrounds them and the
+  // compiler's wait counts stay exact; such values are never used.
+  constexpr int XCN = NA * kMoeBM * KC / 8;           // 16-byte activation pieces per chunk
+  constexpr int XCH = (XCN + 255) / 256;              // per thread
+  const int ncl = min(ncol, N - 4);
+  size_t xsrc[XCH];                                   // element offset of each piece's row
+  int xdst[XCH];                                      // its LDS offset (plane, row, k), -1: none
+  bool xz[XCH];                                       // a row past the tile: zeros
+#pragma unroll
+  for (int j = 0; j < XCH; ++j) {
+    const int ci = threadIdx.x + 256 * j;
+    const int cc = min(ci, XCN - 1);
+    const int pl = cc / (kMoeBM * KC / 8), cr = cc - pl * (kMoeBM * KC / 8);
+    const int r = cr / (KC / 8), kk = (cr - r * (KC / 8)) * 8;
+    const int rr = min(r, nrows - 1);
+    const size_t row = GATE_UP ? (size_t)sorted_tok[slot0 + rr] : (size_t)(slot0 + rr);
+    xsrc[j] = (size_t)pl * a_plane + row * K + kk;
+    xdst[j] = ci < XCN ? pl * kMoeBM * KC + r * KC + kk : -1;
+    xz[j] = r >= nrows;
+  }
+  struct Chunk {
     uint4 bw[NSET][STEPS][RB];
     uint4 sraw[NSET];
     uint32_t zraw[NSET];
+    uint4 xv[XCH];
+  };
+  auto load_chunk = [&](int kc0, Chunk& c) {
+#pragma unroll
+    for (int j = 0; j < XCH; ++j) c.xv[j] = *reinterpret_cast<const uint4*>(a + xsrc[j] + kc0);
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
-      sraw[q] = make_uint4(0u, 0u, 0u, 0u);
-      zraw[q] = 0;
 #pragma unroll
       for (int st = 0; st < STEPS; ++st)
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) bw[q][st][rb] = make_uint4(0u, 0u, 0u, 0u);
-      if (colok) {
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb) {
-            const int row = (kc0 + st * 32) / PER + kb * RB + rb;
-            bw[q][st][rb] = *reinterpret_cast<const uint4*>(qw[q] + (size_t)row * N + ncol);
-          }
-        const int g = kc0 / gs;
-        sraw[q] = load_scales4<ST>(sc[q] + (size_t)g * N + ncol);
-        zraw[q] = qz[q][(size_t)g * NZ + ncol / PER];
-      }
+        for (int rb = 0; rb < RB; ++rb) {
+          const int row = (kc0 + st * 32) / PER + kb * RB + rb;
+          c.bw[q][st][rb] = *reinterpret_cast<const uint4*>(qw[q] + (size_t)row * N + ncl);
+        }
+      const int g = kc0 / gs;
+      c.sraw[q] = load_scales4<ST>(sc[q] + (size_t)g * N + ncl);
+      c.zraw[q] = qz[q][(size_t)g * NZ + ncl / PER];
     }
-    __syncthreads();
-    for (int ci = threadIdx.x; ci < NA * kMoeBM * KC / 8; ci += 256) {
-      const int pl = ci / (kMoeBM * KC / 8), cr = ci - pl * (kMoeBM * KC / 8);
-      const int r = cr / (KC / 8), kk = (cr - r * (KC / 8)) * 8;
-      float v[8];
-      if (r < nrows) {
-        const size_t src = GATE_UP ? (size_t)sorted_tok[slot0 + r] : (size_t)(slot0 + r);
-        load8(a + (size_t)pl * a_plane + src * K + kc0 + kk, v);
-      } else {
+  };
+  // the activation pieces in the order the code unpack produces (int4: (x0,x4) (x1,x5) (x2,x6)
+  // (x3,x7); int8: (x0,x2) (x1,x3) (x4,x6) (x5,x7)), moved as 16-bit halves
+  auto stage = [&](const Chunk& c) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = 0.f;
-      }
-      *reinterpret_cast<uint4*>(xs[pl] + r * KC + kk) = pack8_pairs<BITS>(v);
+    for (int j = 0; j < XCH; ++j) {
+      if (xdst[j] < 0) continue;
+      const uint4 w = xz[j] ? make_uint4(0u, 0u, 0u, 0u) : c.xv[j];
+      uint4 o;
+      if constexpr (BITS == 4)
+        o = make_uint4((w.x & 0xFFFFu) | (w.z << 16), (w.x >> 16) | (w.z & 0xFFFF0000u),
+                       (w.y & 0xFFFFu) | (w.w << 16), (w.y >> 16) | (w.w & 0xFFFF0000u));
+      else
+        o = make_uint4((w.x & 0xFFFFu) | (w.y << 16), (w.x >> 16) | (w.y & 0xFFFF0000u),
+                       (w.z & 0xFFFFu) | (w.w << 16), (w.z >> 16) | (w.w & 0xFFFF0000u));
+      *reinterpret_cast<uint4*>(&xs[0][0] + xdst[j]) = o;
     }
-    __syncthreads();
-    if (!wave_active) continue;
+  };
+  auto multiply = [&](const Chunk& c) {
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
       half2v zl[4], zh[4];
-      zero_pairs<BITS>(zraw[q] >> zshift, zoff, zl, zh);
+      zero_pairs<BITS>(c.zraw[q] >> zshift, zoff, zl, zh);
       float4v part[TM][4];
 #pragma unroll
       for (int t = 0; t < TM; ++t)
@@ -254,7 +348,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
       for (int st = 0; st < STEPS; ++st) {
         half8v bf[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bf[s] = b_fragment<BITS>(bw[q][st], s, zl[s], zh[s]);
+        for (int s = 0; s < 4; ++s) bf[s] = b_fragment<BITS>(c.bw[q][st], s, zl[s], zh[s]);
 #pragma unroll
         for (int pl = 0; pl < NA; ++pl)
 #pragma unroll
@@ -265,7 +359,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
           }
       }
       float sf[4];
-      scales4<ST>(sraw[q], sf);
+      scales4<ST>(c.sraw[q], sf);
 #pragma unroll
       for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -273,34 +367,64 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[q][t][s][r] = fmaf(sf[s], part[t][s][r], acc[q][t][s][r]);
     }
+  };
+  auto iter = [&](int kc0, Chunk& cur, Chunk& nxt) {
+    __syncthreads();  // the previous chunk's activation reads are done
+    stage(cur);
+    __syncthreads();
+    load_chunk(min(kc0 + KC, K - KC), nxt);
+    if (wave_active) multiply(cur);
+  };
+  Chunk c0, c1;
+  load_chunk(0, c0);
+  for (int kc0 = 0; kc0 < K; kc0 += 2 * KC) {
+    iter(kc0, c0, c1);
+    if (kc0 + KC < K) iter(kc0 + KC, c1, c0);
   }
 
-  if (!colok) return;
+  if constexpr (GATE_UP) {
+    // the up waves hand their sums to the gate waves of the same columns through LDS
+    __shared__ float4v ux[2][TM][4][64];
+    if (set == 1)
 #pragma unroll
-  for (int t = 0; t < TM; ++t)
+      for (int t = 0; t < TM; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * t + 4 * kb + r;
-      if (row >= nrows) continue;
-      const size_t slot = (size_t)slot0 + row;
-      if constexpr (GATE_UP) {
+        for (int s = 0; s < 4; ++s) ux[cw][t][s][lane] = acc[0][t][s];
+    __syncthreads();
+    if (set == 1 || !colok) return;
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * t + 4 * kb + r;
+        if (row >= nrows) continue;
+        const size_t slot = (size_t)slot0 + row;
         __half* hi = static_cast<__half*>(out) + slot * N + ncol;
         __half* lo = hi + out_plane;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const float g = acc[0][t][s][r], u = acc[1][t][s][r];
+          const float g = acc[0][t][s][r], u = ux[cw][t][s][lane][r];
           const float h = g * (1.f / (1.f + expf(-g))) * u;
           const __half hh = __float2half_rn(h);
           hi[s] = hh;
           lo[s] = __float2half_rn(h - __half2float(hh));
         }
-      } else {
+      }
+  } else {
+    if (!colok) return;
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * t + 4 * kb + r;
+        if (row >= nrows) continue;
+        const size_t slot = (size_t)slot0 + row;
         float* y = static_cast<float*>(out) + slot * N + ncol;
         const float w = sorted_w[slot];
 #pragma unroll
         for (int s = 0; s < 4; ++s) y[s] = acc[0][t][s][r] * w;
       }
-    }
+  }
 }
 
 // out[t][c] = sum over token t's experts, ascending, of y[slot][c] (starting from zero).
@@ -326,7 +450,7 @@ static int launch_moe_gemm(const void* a, const int* route, int T, int E, int k,
   const RouteLayout L = route_layout(T, E, k);
   const int per = 32 / BITS;
   const size_t qws = (size_t)(K / per) * N, qzs = (size_t)(K / gs) * (N / per), scs = (size_t)(K / gs) * N;
-  dim3 grid((N + 255) / 256, L.max_tiles);
+  dim3 grid(GATE_UP ? (N + 127) / 128 : (N + 255) / 256, L.max_tiles);
   // gate_up writes h as two planes of T*k x N halves; down reads them (a_plane = T*k x K)
   const size_t a_plane = GATE_UP ? 0 : (size_t)T * k * K;
   const size_t out_plane = GATE_UP ? (size_t)T * k * N : 0;
@@ -389,9 +513,17 @@ extern "C" int miq_moe_route(const float* logits, int T, int E, int k, int norm_
   MIQ_REQUIRE(logits && route, MIQ_ERR_INVALID, "moe_route: null pointer");
   MIQ_REQUIRE(route_bytes >= route_layout(T, E, k).words * 4 && aligned(route, 16), MIQ_ERR_INVALID,
               "moe_route: route buffer of %zu bytes (16-byte aligned) needed", route_layout(T, E, k).words * 4);
-  const size_t lds = (2 * (size_t)T * k + 2 * (size_t)E + 1) * 4;
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), lds, static_cast<hipStream_t>(stream), logits, T, E, k,
-                     norm_topk, static_cast<int*>(route));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int* r = static_cast<int*>(route);
+  const dim3 g((T + 3) / 4);
+  if (E <= 64) hipLaunchKernelGGL(moe_topk_kernel<1>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
+  else if (E <= 128) hipLaunchKernelGGL(moe_topk_kernel<2>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
+  else if (E <= 256) hipLaunchKernelGGL(moe_topk_kernel<4>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
+  else if (E <= 512) hipLaunchKernelGGL(moe_topk_kernel<8>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
+  else hipLaunchKernelGGL(moe_topk_kernel<16>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
+  // se, sw [T*k]; cnt, off, run [E+1]; wave sums [32]
+  const size_t lds = (2 * (size_t)T * k + 3 * ((size_t)E + 1) + 32) * 4;
+  hipLaunchKernelGGL(moe_slots_kernel, dim3(1), dim3(1024), lds, st, T, E, k, r);
   return check_launch("moe_route");
 }
 
