@@ -78,3 +78,44 @@ def test_gemm_repeated_calls_are_deterministic(gpu):
     a = ql.forward(x, out_dtype=torch.float32).cpu().numpy()
     for _ in range(3):
         assert np.array_equal(a, ql.forward(x, out_dtype=torch.float32).cpu().numpy())
+
+
+@pytest.mark.parametrize("K,N,M,sdt,zoff,bias,act", [
+    (896, 968, 12, "f32", 0.0, True, False),     # N not a multiple of 64, K of 28 steps
+    (4864, 896, 9, "f16", 1.0, False, False),    # two A blocks, ragged last K-slice
+    (1024, 200, 16, "f16", 1.0, True, True),     # act-order through the gathered copy
+    (4096, 4096, 3, "f16", 1.0, False, False),   # one A block (through the C entry: M <= 8)
+    (2048, 1024, 8, "f32", 1.0, True, True),
+    (2048, 3080, 16, "f32", 1.0, True, True),    # 16 waves per workgroup over all of K, ragged N
+])
+def test_few_row_gemm(gpu, K, N, M, sdt, zoff, bias, act):
+    """The few-row matrix-core product (M <= 16, gs = 128): exact bf16 halves of the fp16 rows,
+    per-group folds, a fixed-point split-K; called through miq_gptq_gemm."""
+    import torch
+    from webpytorch_amd import core
+    L = synth.gptq_layer(60 + M, K, N, 128, 4, act_order=act)
+    sc = L["scales"] if sdt == "f16" else L["scales"].astype(np.float32) * np.float32(0.71)
+    rng = np.random.default_rng(K + N + M)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    x = synth.activations(61 + M, M, K, np.float16)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], sc, b, 128, 4,
+                                            g_idx=L["g_idx"] if act else None)
+    ql.zero_offset = zoff
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ws = core.workspace(core.gemm_workspace_bytes(M, K, N, 128, 4))
+    core._lib.call("miq_gptq_gemm", core.ptr(xd), core.ptr(ql.perm), core.ptr(ql.qweight), core.ptr(ql.qzeros),
+                   core.ptr(ql.scales), core.dtype_code(ql.scales), core.ptr(ql.bias), core.ptr(out),
+                   core.dtype_code(out), M, K, N, 128, 4, float(zoff), core.ptr(ws), ws.numel(),
+                   core.stream_handle())
+    got = out.cpu().numpy()
+    ref = gptq.linear_forward(x, dict(L, scales=sc), zoff=zoff, g_idx=L["g_idx"] if act else None)
+    if b is not None:
+        ref = ref + b
+    _check(got, ref, rel=1e-5)
+    for _ in range(2):  # the fixed-point words re-zero: repeated calls agree bit for bit
+        core._lib.call("miq_gptq_gemm", core.ptr(xd), core.ptr(ql.perm), core.ptr(ql.qweight),
+                       core.ptr(ql.qzeros), core.ptr(ql.scales), core.dtype_code(ql.scales), core.ptr(ql.bias),
+                       core.ptr(out), core.dtype_code(out), M, K, N, 128, 4, float(zoff), core.ptr(ws), ws.numel(),
+                       core.stream_handle())
+        assert np.array_equal(got, out.cpu().numpy())

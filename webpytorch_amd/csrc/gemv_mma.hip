@@ -14,8 +14,8 @@
 // the top bits, by one agent-scope atomic whose return value tells the last slice that it is
 // last and holds the whole sum; that slice writes y (+ bias) and re-zeroes the word. Integer
 // sums do not depend on the order of arrival, so results are deterministic, and the reduction
-// costs one round trip to the coherence point. Columns past the counter region (N > 32768)
-// use fp32 partials and a per-tile arrival counter instead (three round trips). Several
+// costs one round trip to the coherence point. Layers with more columns than the counter region
+// has words use fp32 partials and a per-tile arrival counter instead (three round trips). Several
 // workgroups per CU keep ~50-100 KB of weights in flight per CU.
 #include <algorithm>
 
@@ -28,14 +28,7 @@ namespace gm {
 using namespace mt;
 
 constexpr int kThreadsG = 256;
-constexpr int kMaxSlices = 32;
-// fixed-point slice sums: a partial p becomes round(p * 2^24) + 2^51, in [0, 2^52) for
-// |p| < 2^27 (partials beyond saturate, NaN to -2^27); 32 of them stay below 2^57, and the
-// arrival count sits in bits 58-63
-constexpr float kFixScale = 16777216.f;
-constexpr float kFixSat = 134217720.f;  // the largest float below 2^27
-constexpr unsigned long long kFixBias = 1ull << 51;
-constexpr int kCountShift = 58;
+constexpr int kMaxSlices = kFixMaxSlices;
 constexpr size_t kMaxFixCols = kCounterBytes / 8;
 
 template <typename ST> struct Scales4;
@@ -173,19 +166,8 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
     const float a2 = __shfl(acc[2], lane & 15, 64), a3 = __shfl(acc[3], lane & 15, 64);
     const float p = t == 0 ? a0 : t == 1 ? a1 : t == 2 ? a2 : a3;
     const int n = tile * 256 + wave * 64 + (lane & 15) * 4 + t;
-    if (n < N) {
-      const float pc = fminf(fmaxf(p, -kFixSat), kFixSat);
-      const unsigned long long add =
-          (1ull << kCountShift) + (unsigned long long)(__float2ll_rn(pc * kFixScale) + (long long)kFixBias);
-      const unsigned long long old =
-          __hip_atomic_fetch_add(fixacc + n, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((int)(old >> kCountShift) == kslices - 1) {
-        const long long tot = (long long)((old + add) & ((1ull << kCountShift) - 1)) - (long long)kslices * (long long)kFixBias;
-        const float y = (float)tot * (1.f / kFixScale);
-        out[n] = from_f32<OT>(bias ? y + bias[n] : y);
-        __hip_atomic_store(fixacc + n, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    float y;
+    if (n < N && fix_add(fixacc + n, p, kslices, &y)) out[n] = from_f32<OT>(bias ? y + bias[n] : y);
     return;
   }
   // split K: partials at device scope, the last workgroup of the tile sums them in slice order

@@ -33,6 +33,7 @@
 // Placement. Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2; the
 // tile order is remapped so that the workgroups on one XCD share weight columns (same column
 // tile and K slice, different row tiles).
+#include <algorithm>
 #include <type_traits>
 
 #include "miq_common.h"
@@ -85,23 +86,37 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const __half* __restrict__
 }
 
 // the same with the columns gathered through perm: one workgroup per row, the row staged in
-// LDS (2 K bytes of dynamic LDS, K <= 32768)
+// LDS (2 K bytes of dynamic LDS, K <= 32768). The permutation indices of a thread's first
+// chunks do not depend on the row, so they are loaded while the row is on its way.
 template <int BITS>
 __global__ __launch_bounds__(256) void gather_x_kernel(const __half* __restrict__ x, const int32_t* __restrict__ perm,
                                                        __half* __restrict__ xp, int M, int K, int KC) {
   extern __shared__ __align__(16) unsigned short row[];
-  const int m = blockIdx.x;
+  constexpr int PRE = 4;  // chunks per thread whose indices are loaded early (K <= 8192: all)
+  const int m = blockIdx.x, nc = K / 8;
+  const int4* pp = reinterpret_cast<const int4*>(perm);
+  int4 pa[PRE], pb[PRE];
+#pragma unroll
+  for (int j = 0; j < PRE; ++j) {
+    const int i = min((int)threadIdx.x + 256 * j, nc - 1);
+    pa[j] = pp[2 * i];
+    pb[j] = pp[2 * i + 1];
+  }
   const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)m * K);
-  for (int i = threadIdx.x; i < K / 8; i += 256) reinterpret_cast<uint4*>(row)[i] = src[i];
+  for (int i = threadIdx.x; i < nc; i += 256) reinterpret_cast<uint4*>(row)[i] = src[i];
   __syncthreads();
-  for (int i = threadIdx.x; i < K / 8; i += 256) {
-    const int4 pa = reinterpret_cast<const int4*>(perm)[2 * i];
-    const int4 pb = reinterpret_cast<const int4*>(perm)[2 * i + 1];
-    const uint4 v = make_uint4(row[pa.x] | ((uint32_t)row[pa.y] << 16), row[pa.z] | ((uint32_t)row[pa.w] << 16),
-                               row[pb.x] | ((uint32_t)row[pb.y] << 16), row[pb.z] | ((uint32_t)row[pb.w] << 16));
+  auto put = [&](int i, int4 a, int4 b) {
+    const uint4 v = make_uint4(row[a.x] | ((uint32_t)row[a.y] << 16), row[a.z] | ((uint32_t)row[a.w] << 16),
+                               row[b.x] | ((uint32_t)row[b.y] << 16), row[b.z] | ((uint32_t)row[b.w] << 16));
     const int k = i * 8;
     *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC) = pair_order8<BITS>(v);
+  };
+#pragma unroll
+  for (int j = 0; j < PRE; ++j) {
+    const int i = threadIdx.x + 256 * j;
+    if (i < nc) put(i, pa[j], pb[j]);
   }
+  for (int i = threadIdx.x + 256 * PRE; i < nc; i += 256) put(i, pp[2 * i], pp[2 * i + 1]);
 }
 
 template <int BITS, int TM, int CB, int KC, typename ST> struct GemmShape {
@@ -516,6 +531,10 @@ extern "C" int miq_gptq_gemm_workspace(int M, int K, int N, int gs, int bits, si
   rc = gemm_plan(M, K, N, gs, &p);
   if (rc) return rc;
   *bytes = p.ws_bytes;
+  // the few-row kernel's needs, with or without act-order (the caller may pass either)
+  const size_t s0 = gemm_small_workspace(M, K, N, gs, bits, false), s1 = gemm_small_workspace(M, K, N, gs, bits, true);
+  if (s0 != SIZE_MAX) *bytes = std::max(*bytes, s0);
+  if (s1 != SIZE_MAX) *bytes = std::max(*bytes, s1);
   return MIQ_OK;
 }
 
@@ -536,14 +555,29 @@ extern "C" int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* 
   MIQ_REQUIRE(zero_offset == (float)(int)zero_offset && zero_offset >= 0.f && zero_offset <= 8.f, MIQ_ERR_UNSUPPORTED,
               "gptq_gemm: zero_offset %g (the exact fp16 path takes a small integer)", zero_offset);
   MIQ_REQUIRE(!perm || K <= 32768, MIQ_ERR_UNSUPPORTED, "gptq_gemm: act-order with K=%d > 32768", K);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const __half* xin = static_cast<const __half*>(x);
+  // a few rows: the matrix-core kernel that streams the weights like the GEMV
+  const size_t need_small = gemm_small_workspace(M, K, N, gs, bits, perm != nullptr);
+  if (need_small != SIZE_MAX &&
+      (need_small == 0 || (workspace && workspace_bytes >= need_small && aligned(workspace, 256)))) {
+    __half* xg = nullptr;
+    if (perm) {
+      xg = reinterpret_cast<__half*>(static_cast<char*>(workspace) + kCounterBytes);
+      hipLaunchKernelGGL(gather_x_kernel<4>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xg, M, K, 128);
+      rc = check_launch("gptq_gemm gather");
+      if (rc) return rc;
+    }
+    rc = gemm_small(xin, xg, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs, bits,
+                    zero_offset, workspace, workspace_bytes, st);
+    if (rc != MIQ_ERR_UNSUPPORTED) return rc;
+  }
   GemmPlan p;
   rc = gemm_plan(M, K, N, gs, &p);
   if (rc) return rc;
   MIQ_REQUIRE(workspace && workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
               "gptq_gemm: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes, workspace_bytes);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   __half* xp = reinterpret_cast<__half*>(static_cast<char*>(workspace) + kCounterBytes + p.partial_bytes);
-  const __half* xin = static_cast<const __half*>(x);
   if (perm) {
     if (bits == 4) hipLaunchKernelGGL(gather_x_kernel<4>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xp, M, K, p.kc);
     else hipLaunchKernelGGL(gather_x_kernel<8>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xp, M, K, p.kc);

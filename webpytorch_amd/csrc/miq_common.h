@@ -26,6 +26,12 @@ int gemv_mma(const void* x, int xd, const int32_t* perm, const int32_t* qw, cons
              int sd, const float* bias, void* out, int od, int K, int N, int gs, float zoff, void* ws,
              size_t ws_bytes, hipStream_t st);
 size_t gemv_mma_workspace(int K, int N);
+// Few-row (M <= 16) int4 product on the matrix cores (gemm_small.hip), used by miq_gptq_gemm;
+// MIQ_ERR_UNSUPPORTED for shapes it does not cover. xg: gathered copy of x (act-order) or null.
+int gemm_small(const __half* x, const __half* xg, const int32_t* qw, const int32_t* qz, const void* sc, int sd,
+               const float* bias, void* out, int od, int M, int K, int N, int gs, int bits, float zoff, void* ws,
+               size_t ws_bytes, hipStream_t st);
+size_t gemm_small_workspace(int M, int K, int N, int gs, int bits, bool perm);  // SIZE_MAX: not covered
 
 // ---- element loads / stores for the activation / output dtypes ---------------------
 template <typename T> __device__ __forceinline__ float to_f32(T v);
@@ -228,7 +234,7 @@ constexpr int kCUs = 256;
 // Split-K workspaces: every kernel keeps its arrival counters in the same fixed region at the
 // start of the workspace (so one call's partial sums can never land on another call's
 // counters) and its partials after it.
-constexpr size_t kCounterBytes = 256 * 1024;
+constexpr size_t kCounterBytes = 2 << 20;
 constexpr int kMaxCounters = (int)(kCounterBytes / 4);
 
 }  // namespace miq

@@ -220,5 +220,43 @@ __device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned cha
   if ((ch & 3) == 0) cx[ch >> 2] = make_float2(cb, sm);
 }
 
+// ---- deterministic split-K sums in fixed point ------------------------------------------
+// The K-slices of one output meet in a zeroed 64-bit word: each adds its partial p as
+// round(p * 2^24) + 2^51 (in [0, 2^52) for |p| < 2^27; larger partials saturate, NaN becomes
+// -2^27) together with 1 in bits 58-63, by one agent-scope atomic. Integer sums do not depend on
+// the order of arrival, so results are deterministic; up to 32 slices stay below 2^57. The
+// atomic's return value tells the last slice that it is last and holds the whole sum; that slice
+// re-zeroes the word. One round trip to the coherence point per slice.
+constexpr float kFixScale = 16777216.f;
+constexpr float kFixSat = 134217720.f;  // the largest float below 2^27
+constexpr unsigned long long kFixBias = 1ull << 51;
+constexpr int kFixCountShift = 58;
+constexpr int kFixMaxSlices = 32;
+
+// The word a slice adds for its partial p.
+__device__ __forceinline__ unsigned long long fix_word(float p) {
+  const float pc = fminf(fmaxf(p, -kFixSat), kFixSat);
+  return (1ull << kFixCountShift) + (unsigned long long)(__float2ll_rn(pc * kFixScale) + (long long)kFixBias);
+}
+__device__ __forceinline__ unsigned long long fix_issue(unsigned long long* w, unsigned long long add) {
+  return __hip_atomic_fetch_add(w, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// After the atomic returned `old`: true in the last slice, with the whole sum in *sum, and the
+// word re-zeroed. Issue every atomic of a lane before finishing any, so their round trips
+// overlap.
+__device__ __forceinline__ bool fix_finish(unsigned long long* w, unsigned long long old, unsigned long long add,
+                                           int slices, float* sum) {
+  if ((int)(old >> kFixCountShift) != slices - 1) return false;
+  const long long tot =
+      (long long)((old + add) & ((1ull << kFixCountShift) - 1)) - (long long)slices * (long long)kFixBias;
+  *sum = (float)tot * (1.f / kFixScale);
+  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+__device__ __forceinline__ bool fix_add(unsigned long long* w, float p, int slices, float* sum) {
+  const unsigned long long add = fix_word(p);
+  return fix_finish(w, fix_issue(w, add), add, slices, sum);
+}
+
 }  // namespace mt
 }  // namespace miq
