@@ -57,10 +57,25 @@ def make_layer(torch, K, N, sdt, bias):
     return qw, qz, sc, b
 
 
-def timed(torch, fn, reps, warm=1):
-    for _ in range(warm):
-        fn()
+def timed(torch, fn, reps, warm=1, min_warm_s=0.03, min_timed_s=0.02):
+    """Seconds per call of fn (GPU time between events). The GPU is first kept busy for at
+    least min_warm_s (its clocks ramp up under load; a cold first measurement reads slow), and
+    the timed window is stretched to at least min_timed_s."""
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0, n = time.perf_counter(), 0
+    while n < warm or time.perf_counter() - t0 < min_warm_s:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    s.record()
+    fn()
+    e.record()
+    e.synchronize()
+    per = max(s.elapsed_time(e) * 1e-3, 1e-7)
+    reps = max(reps, int(min_timed_s / per) + 1)
     torch.cuda.synchronize()
     s.record()
     for _ in range(reps):

@@ -85,38 +85,25 @@ __global__ __launch_bounds__(256) void stage_x_kernel(const __half* __restrict__
       pair_order8<BITS>(*reinterpret_cast<const uint4*>(x + (size_t)m * K + k));
 }
 
-// the same with the columns gathered through perm: one workgroup per row, the row staged in
-// LDS (2 K bytes of dynamic LDS, K <= 32768). The permutation indices of a thread's first
-// chunks do not depend on the row, so they are loaded while the row is on its way.
+// the same with the columns gathered through perm: a thread per 8-wide output chunk reads its 8
+// permutation indices (shared by every row, so they stay in cache) and gathers the 8 values
+// straight from the row; no staging, no barrier: two dependent reads per thread.
+// Grid (K/8/256 rounded up, M).
 template <int BITS>
 __global__ __launch_bounds__(256) void gather_x_kernel(const __half* __restrict__ x, const int32_t* __restrict__ perm,
                                                        __half* __restrict__ xp, int M, int K, int KC) {
-  extern __shared__ __align__(16) unsigned short row[];
-  constexpr int PRE = 4;  // chunks per thread whose indices are loaded early (K <= 8192: all)
-  const int m = blockIdx.x, nc = K / 8;
-  const int4* pp = reinterpret_cast<const int4*>(perm);
-  int4 pa[PRE], pb[PRE];
-#pragma unroll
-  for (int j = 0; j < PRE; ++j) {
-    const int i = min((int)threadIdx.x + 256 * j, nc - 1);
-    pa[j] = pp[2 * i];
-    pb[j] = pp[2 * i + 1];
-  }
-  const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)m * K);
-  for (int i = threadIdx.x; i < nc; i += 256) reinterpret_cast<uint4*>(row)[i] = src[i];
-  __syncthreads();
-  auto put = [&](int i, int4 a, int4 b) {
-    const uint4 v = make_uint4(row[a.x] | ((uint32_t)row[a.y] << 16), row[a.z] | ((uint32_t)row[a.w] << 16),
-                               row[b.x] | ((uint32_t)row[b.y] << 16), row[b.z] | ((uint32_t)row[b.w] << 16));
-    const int k = i * 8;
-    *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC) = pair_order8<BITS>(v);
-  };
-#pragma unroll
-  for (int j = 0; j < PRE; ++j) {
-    const int i = threadIdx.x + 256 * j;
-    if (i < nc) put(i, pa[j], pb[j]);
-  }
-  for (int i = threadIdx.x + 256 * PRE; i < nc; i += 256) put(i, pp[2 * i], pp[2 * i + 1]);
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= K / 8) return;
+  const int m = blockIdx.y;
+  const int4 pa = reinterpret_cast<const int4*>(perm)[2 * i];
+  const int4 pb = reinterpret_cast<const int4*>(perm)[2 * i + 1];
+  const unsigned short* row = reinterpret_cast<const unsigned short*>(x + (size_t)m * K);
+  const uint4 v = make_uint4(row[(unsigned)pa.x] | ((uint32_t)row[(unsigned)pa.y] << 16),
+                             row[(unsigned)pa.z] | ((uint32_t)row[(unsigned)pa.w] << 16),
+                             row[(unsigned)pb.x] | ((uint32_t)row[(unsigned)pb.y] << 16),
+                             row[(unsigned)pb.z] | ((uint32_t)row[(unsigned)pb.w] << 16));
+  const int k = i * 8;
+  *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC) = pair_order8<BITS>(v);
 }
 
 template <int BITS, int TM, int CB, int KC, typename ST> struct GemmShape {
@@ -564,7 +551,8 @@ extern "C" int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* 
     __half* xg = nullptr;
     if (perm) {
       xg = reinterpret_cast<__half*>(static_cast<char*>(workspace) + kCounterBytes);
-      hipLaunchKernelGGL(gather_x_kernel<4>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xg, M, K, 128);
+      hipLaunchKernelGGL(gather_x_kernel<4>, dim3((K / 8 + 255) / 256, M), dim3(256), 0, st, xin, perm, xg, M, K,
+                         128);
       rc = check_launch("gptq_gemm gather");
       if (rc) return rc;
     }
@@ -579,8 +567,9 @@ extern "C" int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* 
               "gptq_gemm: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes, workspace_bytes);
   __half* xp = reinterpret_cast<__half*>(static_cast<char*>(workspace) + kCounterBytes + p.partial_bytes);
   if (perm) {
-    if (bits == 4) hipLaunchKernelGGL(gather_x_kernel<4>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xp, M, K, p.kc);
-    else hipLaunchKernelGGL(gather_x_kernel<8>, dim3(M), dim3(256), (size_t)K * 2, st, xin, perm, xp, M, K, p.kc);
+    const dim3 g((K / 8 + 255) / 256, M);
+    if (bits == 4) hipLaunchKernelGGL(gather_x_kernel<4>, g, dim3(256), 0, st, xin, perm, xp, M, K, p.kc);
+    else hipLaunchKernelGGL(gather_x_kernel<8>, g, dim3(256), 0, st, xin, perm, xp, M, K, p.kc);
   } else {
     const dim3 g((K / 8 + 255) / 256, M);
     if (bits == 4) hipLaunchKernelGGL(stage_x_kernel<4>, g, dim3(256), 0, st, xin, xp, M, K, p.kc);
