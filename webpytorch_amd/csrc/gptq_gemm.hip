@@ -410,7 +410,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 struct WaveTile {
   int tm, cb;
 };
-constexpr WaveTile kWaveTiles[] = {{4, 4}, {4, 2}, {2, 4}, {1, 4}};
+constexpr WaveTile kWaveTiles[] = {{4, 4}, {4, 2}, {2, 4}, {2, 2}, {1, 4}, {1, 2}};
+constexpr int kNumWaveTiles = 6;
 
 struct GemmPlan {
   int tm, cb, kc, ntiles, mtiles, ksplit, stages_per_wg;
@@ -424,19 +425,25 @@ static int gemm_plan(int M, int K, int N, int gs, GemmPlan* p) {
   else if (gs % 32 == 0) kc = 32;
   MIQ_REQUIRE(kc, MIQ_ERR_UNSUPPORTED, "gptq_gemm: group size %d (a multiple of 32)", gs);
   p->kc = kc;
-  // the largest wave tile whose grid covers the chip; failing that, the smallest that the rows
-  // fill, with K split to make up the rest
+  // the largest wave tile whose grid covers the chip (no K split); failing that, the one with
+  // the most tiles, with K split to make up the rest
   int pick = -1;
 #if defined(MIQ_GEMM_TM) && defined(MIQ_GEMM_CB)
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kNumWaveTiles; ++i)
     if (kWaveTiles[i].tm == MIQ_GEMM_TM && kWaveTiles[i].cb == MIQ_GEMM_CB) pick = i;
 #else
-  for (int i = 0; i < 4 && pick < 0; ++i) {
+  long most = 0;
+  int pick_most = 0;
+  for (int i = 0; i < kNumWaveTiles; ++i) {
     const long tiles = (long)((M + 16 * kWaveTiles[i].tm - 1) / (16 * kWaveTiles[i].tm)) *
                        ((N + 64 * kWaveTiles[i].cb - 1) / (64 * kWaveTiles[i].cb));
-    if (tiles >= MIQ_GEMM_TARGET_WGS) pick = i;
+    if (tiles >= MIQ_GEMM_TARGET_WGS && pick < 0) pick = i;
+    if (tiles > most) {
+      most = tiles;
+      pick_most = i;
+    }
   }
-  if (pick < 0) pick = 1;
+  if (pick < 0) pick = pick_most;  // no tile fills the chip alone: the most tiles, K split for the rest
 #endif
   p->tm = kWaveTiles[pick].tm;
   p->cb = kWaveTiles[pick].cb;
@@ -489,6 +496,8 @@ static int gemm_tiles(const GemmPlan& p, const __half* xp, const int32_t* qw, co
   if (p.tm == 4 && p.cb == 4) return gemm_types<BITS, 4, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
   if (p.tm == 4 && p.cb == 2) return gemm_types<BITS, 4, 2, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
   if (p.tm == 2 && p.cb == 4) return gemm_types<BITS, 2, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  if (p.tm == 2 && p.cb == 2) return gemm_types<BITS, 2, 2, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  if (p.tm == 1 && p.cb == 2) return gemm_types<BITS, 1, 2, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
   return gemm_types<BITS, 1, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
 }
 
