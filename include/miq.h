@@ -62,10 +62,11 @@ int miq_gptq_dequant_f32(const int32_t* qweight, const int32_t* qzeros, const vo
 int miq_gptq_repack_rows(const int32_t* qweight, const int32_t* perm, int32_t* out, int K, int N,
                          int bits, void* stream);
 
-/* Bytes of workspace miq_gptq_gemv needs for this problem (0 if none). The first 256 KiB of a
- * workspace hold arrival counters, shared by every split-K entry point, that must be zero
- * before the first call on it; every call leaves them zero again. Partial sums follow them.
- * One workspace must not serve two calls that run concurrently. */
+/* Bytes of workspace miq_gptq_gemv needs for this problem (0 if none). The first 2 MiB of a
+ * workspace (the counter region) hold arrival counters and fixed-point split-K sums, shared by
+ * every split-K entry point, that must be zero before the first call on it; every call leaves
+ * them zero again. Partial sums and staged activations follow them. One workspace must not
+ * serve two calls that run concurrently. */
 int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, int x_dtype, size_t* bytes);
 
 /* Decode GEMV / skinny GEMM: out[M][N] = x[M][K] (gathered through perm if non-NULL)
@@ -109,7 +110,10 @@ int miq_gptq_gemm_workspace(int M, int K, int N, int gs, int bits, size_t* bytes
  * q - (z + zero_offset) in fp16 (zero_offset must be a small non-negative integer), fp16 x
  * fp16 products accumulate in fp32 and the fp32 group scale multiplies each chunk's sums.
  * scales fp16|fp32, out fp16|fp32. Requires x and qweight 16-byte aligned, N % 4 == 0 and
- * gs in {32, 64} or a multiple of 128. workspace as for miq_gptq_gemv.
+ * gs in {32, 64} or a multiple of 128. workspace as for miq_gptq_gemv. Up to 16 rows of int4
+ * with gs 128 run a kernel that streams the weights like the GEMV (all loads issued up front,
+ * K split over waves and workgroups, deterministic fixed-point slice sums); more rows run the
+ * tiled LDS-pipelined kernel.
  * Replaces: `_gptq_matmul` M > 1 dispatch to the tiled `_GPTQ_WGSL` kernel
  * (webtorch/_core.py:3833-3888, 3995-4027) and the bias add of `QuantizedLinear.forward`
  * (webtorch/_core.py:4446-4456). */
