@@ -40,7 +40,7 @@ namespace pd {
 
 using namespace mt;
 
-constexpr int kThreads = 1024, kWaves = 16, kTile = 64, kMaxSPQ = 16, kSlots = 20;
+constexpr int kThreads = 1024, kWaves = 16, kTile = 64, kMaxSPQ = 8, kSlots = 20;
 enum Slot { QKV_QW, QKV_QZ, QKV_SC, QKV_B, O_QW, O_QZ, O_SC, GU_QW, GU_QZ, GU_SC, D_QW, D_QZ, D_SC, IN_LN, POST_LN, KC, VC };
 enum Phase { P_QKV = 0, P_ATT = 1, P_HMID = 2, P_GU = 3, P_DOWN = 4, P_AMAX = 5 };
 
@@ -561,7 +561,7 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
                   __attribute__((always_inline)) {
     if (t >= ntile) return;  // uniform
     if (t + 2 * G < ntile)
-      tile_issue<float, SA, 4, false>(ahead, p.head_qw, p.head_qz, p.head_sc, V, (t + 2 * G) * kTile, 0, H / 32, p.lgs);
+      tile_issue<float, SA, false>(ahead, p.head_qw, p.head_qz, p.head_sc, V, (t + 2 * G) * kTile, 0, H / 32, p.lgs);
     const int n = t * kTile + (int)threadIdx.x;
     const float y = tile_sum(tile_mma(cur, s.xa, s.cx, 0, t * kTile, p.lgs, zo), s.red) / rn;
     if (threadIdx.x < 64 && n < V) {
@@ -636,7 +636,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   s.xa = reinterpret_cast<unsigned char*>(s.xs + p.lds_x);
   s.cx = reinterpret_cast<float2*>(s.xa + (size_t)(p.lds_x / 32) * kStepBytes);
   s.red = reinterpret_cast<float*>(s.cx + p.lds_x / 32);
-  s.red16 = s.red + 4 * 64;
+  s.red16 = s.red + kKParts * 64;
   s.qkv = s.red16 + 32;
   Ctx c;
   c.deadline = wall_clock64() + p.spin_limit;
@@ -688,8 +688,8 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
               "decode_persistent: H, q|k|v width and 2I must be multiples of 64, gs a power of two >= 32, V of 8");
   MIQ_REQUIRE(H % gs == 0 && NHD % gs == 0 && I % gs == 0, MIQ_ERR_UNSUPPORTED,
               "decode_persistent: H, NH*HD and I must be multiples of the group size %d", gs);
-  // K in 32-value steps, at most 16 per k-quarter of a tile
-  auto rows_ok = [&](int K) { return K % 32 == 0 && K <= 32 * 4 * kMaxSPQ; };
+  // K in 32-value steps, at most kMaxSPQ per k-part of a tile
+  auto rows_ok = [&](int K) { return K % 32 == 0 && K <= 32 * kKParts * kMaxSPQ; };
   MIQ_REQUIRE(rows_ok(H) && rows_ok(NHD) && LMAX <= 8192 && NHD <= 2 * kThreads - 9 * kTile, MIQ_ERR_UNSUPPORTED,
               "decode_persistent: H=%d / NH*HD=%d / LMAX=%d out of range for gs=%d", H, NHD, LMAX, gs);
   int cus = 0, dev = 0;
@@ -713,13 +713,13 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
               "decode_persistent: the roles of this shape do not fit %d workgroups", q.G);
   q.nd = q.no * q.ksd;
   const int KS = I / q.ksd;
-  q.spa = (std::max(H, NHD) / 32 + 3) / 4;
-  q.spd = (KS / 32 + 3) / 4;
+  q.spa = (std::max(H, NHD) / 32 + kKParts - 1) / kKParts;
+  q.spd = (KS / 32 + kKParts - 1) / kKParts;
   q.lds_a = std::max(std::max((q.ksd + 1) * H, NHD + (q.ksd + 1) * kTile), std::max(std::max(2 * KS, kWaves * 64), std::max(256 + LMAX, 2 * q.G)));
   q.lds_a = (q.lds_a + 3) & ~3;
-  q.lds_x = (std::max(H, std::max(NHD, KS)) + 31) & ~31;
+  q.lds_x = (std::max(H, std::max(NHD, KS)) + 63) & ~63;  // even step count: red 16-byte aligned
   q.lds_bytes = (size_t)(q.lds_a + q.lds_x) * 4 + (size_t)(q.lds_x / 32) * kStepBytes +
-                (size_t)(2 * (q.lds_x / 32) + 4 * 64 + 32 + 192) * 4;
+                (size_t)(2 * (q.lds_x / 32) + kKParts * 64 + 32 + 192) * 4;
   size_t off = 256;  // control words
   auto take = [&](size_t words) {
     const size_t o = off;
@@ -770,13 +770,13 @@ extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* em
   MIQ_REQUIRE(aligned(ws, 256) && aligned(layer_table, 8), MIQ_ERR_ALIGN,
               "decode_persistent: workspace must be 256-byte aligned");
   int dev = 0, per_cu = 0, khz = 0;
-  // 32-k steps per k-quarter of the K = H projections and of a down K-slice, rounded up to the
+  // 32-k steps per k-part (wave) of the K = H projections and of a down K-slice, rounded up to the
   // instantiated register capacities
   void (*kfn)(pd::Params) = nullptr;
-  if (pl.spa <= 8 && pl.spd <= 12) kfn = pd::decode_persistent_kernel<8, 12>;
-  else if (pl.spa <= 8) kfn = pd::decode_persistent_kernel<8, 16>;
-  else if (pl.spd <= 12) kfn = pd::decode_persistent_kernel<16, 12>;
-  else kfn = pd::decode_persistent_kernel<16, 16>;
+  if (pl.spa <= 2 && pl.spd <= 4) kfn = pd::decode_persistent_kernel<2, 4>;
+  else if (pl.spa <= 4 && pl.spd <= 4) kfn = pd::decode_persistent_kernel<4, 4>;
+  else if (pl.spa <= 4) kfn = pd::decode_persistent_kernel<4, 8>;
+  else kfn = pd::decode_persistent_kernel<8, 8>;
   auto kern = reinterpret_cast<const void*>(kfn);
   if (hipGetDevice(&dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, pd::kThreads, pl.lds_bytes) != hipSuccess)

@@ -45,23 +45,6 @@ using namespace mt;
 
 constexpr int kXkc = 128;  // stage width of the gathered copy
 
-template <typename ST> struct Scales4;
-template <> struct Scales4<__half> {  // four fp16 scales of adjacent columns
-  using T = uint2;
-  static __device__ __forceinline__ T load(const __half* p) { return *reinterpret_cast<const uint2*>(p); }
-  static __device__ __forceinline__ float get(const T& v, int t) {
-    const uint32_t w = t < 2 ? v.x : v.y;
-    return __half2float(__ushort_as_half((unsigned short)((t & 1) ? w >> 16 : w & 0xFFFFu)));
-  }
-};
-template <> struct Scales4<float> {
-  using T = uint4;
-  static __device__ __forceinline__ T load(const float* p) { return *reinterpret_cast<const uint4*>(p); }
-  static __device__ __forceinline__ float get(const T& v, int t) {
-    return __uint_as_float(t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w);
-  }
-};
-
 // 8 fp16 in k order (words (h0,h1) (h2,h3) (h4,h5) (h6,h7)) into pair order (h0,h4) (h1,h5)
 // (h2,h6) (h3,h7): k 0, 4, 1, 5, 2, 6, 3, 7, the order of the B halves
 __device__ __forceinline__ uint4 pair_order(uint4 v) {

@@ -31,23 +31,6 @@ constexpr int kThreadsG = 256;
 constexpr int kMaxSlices = kFixMaxSlices;
 constexpr size_t kMaxFixCols = kCounterBytes / 8;
 
-template <typename ST> struct Scales4;
-template <> struct Scales4<__half> {  // four fp16 scales of adjacent columns
-  using T = uint2;
-  static __device__ __forceinline__ T load(const __half* p) { return *reinterpret_cast<const uint2*>(p); }
-  static __device__ __forceinline__ float get(const T& v, int t) {
-    const uint32_t w = t < 2 ? v.x : v.y;
-    return __half2float(__ushort_as_half((unsigned short)((t & 1) ? w >> 16 : w & 0xFFFFu)));
-  }
-};
-template <> struct Scales4<float> {
-  using T = uint4;
-  static __device__ __forceinline__ T load(const float* p) { return *reinterpret_cast<const uint4*>(p); }
-  static __device__ __forceinline__ float get(const T& v, int t) {
-    return __uint_as_float(t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w);
-  }
-};
-
 // Groups of 128 values (4 steps of 32). A 256-thread workgroup covers 256 columns; wave w takes
 // the 64 columns [64 w, 64 w + 64) and every step of the workgroup's K-slice. Lane l loads 16
 // bytes -- the codes of 4 adjacent columns 4 (l & 15) .. + 3 -- of packed row (l >> 4) of each
@@ -119,6 +102,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   __syncthreads();
   // A rows 0-2 are read by lanes 0-2 of each 16; the other rows of D are never used
   const bool arow = (lane & 15) < 3;
+  const BMasks bm = b_masks();
   const unsigned char* ap = xa + (lane >> 4) * 64 + (lane & 15) * 16;
   const int zsh = (cl & 7) * 4;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -140,7 +124,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
         const uint32_t wt[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const u32x4 bw = b_bf16(wt[t]);
+          const u32x4 bw = b_bf16(wt[t], bm);
           d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), d[t], 0, 0, 0);
         }
       }

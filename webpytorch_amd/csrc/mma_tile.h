@@ -29,49 +29,62 @@ __device__ __forceinline__ int opaque_tid() {
 //
 // A 32-k step of A is staged in LDS as 4 k-blocks (one per 16 lanes) x 4 slots of 8 values
 // (the three bf16 terms; the fourth slot is unused), 256 bytes.
-// A tile of 64 columns is computed by 4 x KQ waves: wave w takes the 16 columns (w & 3) and the
-// k-part (w >> 2) of the steps; lane l loads packed row (l >> 4) of each step for column
-// l & 15, which is exactly its B fragment (column l & 15, k 8 (l >> 4) .. + 7).
+// A tile of 64 columns is computed by the 16 waves of a workgroup, each taking all 64 columns
+// and one k-part (a sixteenth) of the steps: lane l loads 16 bytes of packed row (l >> 4) of
+// each step -- columns 4 (l & 15) .. + 3 -- and feeds MFMA t the word of column 4 (l & 15) + t,
+// which is exactly its B fragment (column l & 15 of MFMA t, k 8 (l >> 4) .. + 7). The four
+// MFMAs of a step share the A fragment, so the per-step work (A read, sums, addresses) is paid
+// once per four MFMAs.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kStepBytes = 256;
 
 // The B fragment of one packed word: halves (c0, c4) (8 c1, 8 c5) (c2, c6) (8 c3, 8 c7) over 128,
-// three shifts and four v_and_or_b32 in one asm block. The compiler's hazard tracking does not
-// see into inline asm, so an asm write followed closely by an MFMA that reads the register is
-// not padded (the MFMA then reads the stale value); the block ends with the wait states a VALU
-// write needs before an MFMA source read.
-__device__ __forceinline__ u32x4 b_bf16(uint32_t q) {
-  uint32_t b0, b1, b2, b3, t;
-  asm("v_lshrrev_b32 %4, 1, %5\n\t"
-      "v_and_or_b32 %1, %4, %7, %8\n\t"
-      "v_lshrrev_b32 %4, 8, %5\n\t"
-      "v_and_or_b32 %2, %4, %6, %8\n\t"
-      "v_lshrrev_b32 %4, 9, %5\n\t"
-      "v_and_or_b32 %3, %4, %7, %8\n\t"
-      "v_and_or_b32 %0, %5, %6, %8\n\t"
-      "s_nop 2"
-      : "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3), "=&v"(t)
-      : "v"(q), "v"(0x000F000Fu), "v"(0x00780078u), "v"(0x43004300u));
-  return (u32x4){b0, b1, b2, b3};
+// three shifts and four v_and_or_b32. Written in C++ so that the compiler's hazard tracking
+// covers the conversion (an inline-asm version once read stale operands: the compiler neither
+// pads an asm VALU write before the MFMA that reads it nor delays the next asm write of a
+// register an issued MFMA is still reading). The masks and the 128.0 pattern are held in
+// registers (opaque to the compiler), so each pair is one v_and_or_b32 with no literals.
+struct BMasks {
+  uint32_t lo, hi, mg;
+};
+__device__ __forceinline__ BMasks b_masks() {
+  uint32_t lo = 0x000F000Fu, hi = 0x00780078u, mg = 0x43004300u;
+  asm volatile("" : "+v"(lo), "+v"(hi), "+v"(mg));
+  return {lo, hi, mg};
 }
+__device__ __forceinline__ u32x4 b_bf16(uint32_t q, const BMasks& k) {
+  return (u32x4){(q & k.lo) | k.mg, ((q >> 1) & k.hi) | k.mg, ((q >> 8) & k.lo) | k.mg, ((q >> 9) & k.hi) | k.mg};
+}
+
+// Raw scale bits of 4 adjacent columns (fp16: 8 bytes, fp32: 16 bytes), converted when used.
+template <typename ST> struct Scales4;
+template <> struct Scales4<__half> {
+  using T = uint2;
+  static __device__ __forceinline__ T load(const __half* p) { return *reinterpret_cast<const uint2*>(p); }
+  static __device__ __forceinline__ float get(const T& v, int t) {
+    const uint32_t w = t < 2 ? v.x : v.y;
+    return __half2float(__ushort_as_half((unsigned short)((t & 1) ? w >> 16 : w & 0xFFFFu)));
+  }
+};
+template <> struct Scales4<float> {
+  using T = uint4;
+  static __device__ __forceinline__ T load(const float* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ float get(const T& v, int t) {
+    return __uint_as_float(t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w);
+  }
+};
+
+constexpr int kKParts = 16;  // k-parts of a tile: the waves of a 1024-thread workgroup
 
 template <typename ST, int SPQ>
 struct Tile {
-  uint32_t w[SPQ];
-  uint32_t z[SPQ];
-  uint32_t s[SPQ];  // raw scale bits (fp16 in the low half, or fp32)
-  int st0, ns;      // first step and step count of this wave
+  uint4 w[SPQ];                    // codes of 4 adjacent columns, one packed row per step
+  uint32_t z[SPQ];                 // zero-point word of those columns' group
+  typename Scales4<ST>::T s[SPQ];  // raw scale bits of the 4 columns
+  int st0, ns;                     // first step and step count of this wave
 };
-
-__device__ __forceinline__ uint32_t scale_bits(const __half* p) { return *reinterpret_cast<const uint16_t*>(p); }
-__device__ __forceinline__ uint32_t scale_bits(const float* p) { return *reinterpret_cast<const uint32_t*>(p); }
-template <typename ST> __device__ __forceinline__ float scale_f32(uint32_t b);
-template <> __device__ __forceinline__ float scale_f32<__half>(uint32_t b) {
-  return __half2float(__ushort_as_half((unsigned short)b));
-}
-template <> __device__ __forceinline__ float scale_f32<float>(uint32_t b) { return __uint_as_float(b); }
 
 // Holds loaded values in registers from here on. Without it the compiler sinks loads issued
 // ahead of a wait down to their first use after the wait, which puts a memory round trip back
@@ -79,6 +92,8 @@ template <> __device__ __forceinline__ float scale_f32<float>(uint32_t b) { retu
 __device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+__device__ __forceinline__ void pin(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+__device__ __forceinline__ void pin(uint2& v) { asm volatile("" : "+v"(v.x), "+v"(v.y)); }
 template <typename ST, int SPQ>
 __device__ __forceinline__ void pin(Tile<ST, SPQ>& t) {
 #pragma unroll
@@ -89,18 +104,18 @@ __device__ __forceinline__ void pin(Tile<ST, SPQ>& t) {
   }
 }
 
-// Issues this wave's loads for the tile of columns [c0, c0 + 64) (clamped to N - 1) over the
-// nsteps 32-k steps starting at packed row rb (absolute, for the group index; groups are
-// 2^lgs values, 2^(lgs - 3) packed rows).
-template <typename ST, int SPQ, int KQ = 4, bool PIN = true>
+// Issues this wave's loads for the tile of columns [c0, c0 + 64) (clamped to N - 4; N a
+// multiple of 4) over the nsteps 32-k steps starting at packed row rb (absolute, for the group
+// index; groups are 2^lgs values, 2^(lgs - 3) packed rows). nsteps <= kKParts * SPQ.
+template <typename ST, int SPQ, bool PIN = true>
 __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw, const uint32_t* qz, const ST* sc,
                                            int N, int c0, int rb, int nsteps, int lgs) {
   const int tid = opaque_tid();
   const int wave = uniform(tid >> 6), lane = tid & 63;
-  const int spq = (nsteps + KQ - 1) / KQ;
-  t.st0 = (wave >> 2) * spq;
+  const int spq = (nsteps + kKParts - 1) / kKParts;
+  t.st0 = wave * spq;
   t.ns = max(0, min(spq, nsteps - t.st0));
-  const int c = min(c0 + (wave & 3) * 16 + (lane & 15), N - 1);
+  const int c = min(c0 + 4 * (lane & 15), N - 4);
   const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
   const uint32_t* wp = qw + (uint32_t)((r0 + (lane >> 4)) * N + c);
   if (t.ns > 0) {
@@ -109,31 +124,34 @@ __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw,
     for (int i = 0; i < SPQ; ++i) {
       const int ii = min(i, t.ns - 1);
       const int g = (r0 + 4 * ii) >> gsh;
-      t.w[i] = wp[(uint32_t)(4 * ii * N)];
-      t.s[i] = scale_bits(sc + (uint32_t)(g * N + c));
+      t.w[i] = *reinterpret_cast<const uint4*>(wp + (uint32_t)(4 * ii * N));
+      t.s[i] = Scales4<ST>::load(sc + (uint32_t)(g * N + c));
       t.z[i] = qz[(uint32_t)(g * (N >> 3) + (c >> 3))];
     }
     if (PIN) pin(t);
   }
 }
 
-// This wave's share of sum_k x_k W[k][c] (valid in lanes 0..15, column c0 + 16 (w & 3) + lane).
-// The A fragment and step sums of step i + 2 are read from LDS while step i computes (reads
-// clamped to the wave's last step, so they need no guard); the MFMAs of a quantization group
-// chain, and each group is folded into acc with its scale and zero point.
+// This wave's share of sum_k x_k W[k][c] for its 4 columns (valid in lanes 0..15: columns
+// c0 + 4 lane + t). The A fragment and step sums of step i + 2 are read from LDS while step i
+// computes (reads clamped to the wave's last step, so they need no guard); the four MFMA chains
+// of a quantization group share each step's A fragment, and each group is folded into acc with
+// its scales and zero points.
 template <typename ST, int SPQ>
-__device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float2* cx, int rb,
-                                          int c0, int lgs, float zoff) {
-  if (t.ns == 0) return 0.f;  // wave-uniform: a k-quarter past the end of K
+__device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float2* cx, int rb,
+                                           int c0, int lgs, float zoff) {
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (t.ns == 0) return make_float4(0.f, 0.f, 0.f, 0.f);  // wave-uniform: a k-part past the end of K
   const int tid = opaque_tid();
-  const int wave = uniform(tid >> 6), lane = tid & 63;
-  const int sh = ((c0 + (wave & 3) * 16 + (lane & 15)) & 7) * 4;
+  const int lane = tid & 63;
+  const int sh = ((c0 + 4 * (lane & 15)) & 7) * 4;
   // Only A rows 0-2 (lanes with lane % 16 < 3) carry data: D rows 3-15 are never read, so the
   // other lanes skip the LDS read and feed whatever their registers hold.
   const bool arow = (lane & 15) < 3;
   const unsigned char* ap = xa + t.st0 * kStepBytes + (lane >> 4) * 64 + (lane & 15) * 16;
   const float2* cp = cx + t.st0;
   const int last = t.ns - 1;
+  const BMasks bm = b_masks();
   bf16x8 a0, a1;
   if (arow) {
     a0 = *reinterpret_cast<const bf16x8*>(ap);
@@ -141,24 +159,33 @@ __device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned
   }
   float2 x0 = cp[0], x1 = cp[min(1, last)];
   const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
-  floatx4 d = {0.f, 0.f, 0.f, 0.f};
-  float acc = 0.f, cs = 0.f, xs = 0.f;
+  floatx4 d[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) d[q] = (floatx4){0.f, 0.f, 0.f, 0.f};
+  float cs = 0.f, xs = 0.f;
 #pragma unroll
   for (int i = 0; i < SPQ; ++i) {
     bf16x8 a2;
     if (arow) a2 = *reinterpret_cast<const bf16x8*>(ap + min(i + 2, last) * kStepBytes);
     const float2 x2 = cp[min(i + 2, last)];
     if (i < t.ns) {
-      const u32x4 bw = b_bf16(t.w[i]);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
+      const uint32_t wt[4] = {t.w[i].x, t.w[i].y, t.w[i].z, t.w[i].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 bw = b_bf16(wt[q], bm);
+        d[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, bw), d[q], 0, 0, 0);
+      }
       cs += x0.x;
       xs += x0.y;
       const int r = r0 + 4 * i;
       if (i + 1 == t.ns || ((r + 4) >> gsh) != (r >> gsh)) {  // last step of this group
-        const float pv = (d[0] + d[1]) + d[2];
-        const float zc = (float)((t.z[i] >> sh) & 15u) + zoff;
-        acc = fmaf(scale_f32<ST>(t.s[i]), pv - fmaf(zc, xs, cs), acc);
-        d = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float pv = (d[q][0] + d[q][1]) + d[q][2];
+          const float zc = (float)((t.z[i] >> (sh + 4 * q)) & 15u) + zoff;
+          acc[q] = fmaf(Scales4<ST>::get(t.s[i], q), pv - fmaf(zc, xs, cs), acc[q]);
+          d[q] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        }
         cs = 0.f;
         xs = 0.f;
       }
@@ -168,25 +195,19 @@ __device__ __forceinline__ float tile_mma(const Tile<ST, SPQ>& t, const unsigned
     x0 = x1;
     x1 = x2;
   }
-  return acc;
+  return make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
 
-// Sums the KQ k-parts of each column in order; valid in threads 0..63 (column c0 + thread).
-// red holds KQ x 64 floats.
-template <int KQ = 4>
-__device__ __forceinline__ float tile_sum(float acc, float* red) {
+// Sums the kKParts k-parts of each column in wave order; valid in threads 0..63 (column
+// c0 + thread). red holds kKParts x 64 floats, 16-byte aligned.
+__device__ __forceinline__ float tile_sum(float4 acc, float* red) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (KQ == 1) {  // one wave per 16 columns: the sums are already whole
-    if (lane < 16) red[(wave & 3) * 16 + lane] = acc;
-  } else if (lane < 16) {
-    red[(wave >> 2) * 64 + (wave & 3) * 16 + lane] = acc;
-  }
+  if (lane < 16) *reinterpret_cast<float4*>(red + wave * 64 + 4 * lane) = acc;
   __syncthreads();
   float y = 0.f;
   if (threadIdx.x < 64) {
-    const int t = threadIdx.x;
 #pragma unroll
-    for (int q = 0; q < KQ; ++q) y += red[q * 64 + t];
+    for (int q = 0; q < kKParts; ++q) y += red[q * 64 + threadIdx.x];
   }
   return y;
 }
