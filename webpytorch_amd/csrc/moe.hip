@@ -272,8 +272,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 #pragma unroll
       for (int s = 0; s < 4; ++s) acc[q][t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-  // Register double buffer: while one K chunk is multiplied, the next chunk's codes, scales,
-  // zero points and activation rows are in flight. Loads use addresses clamped into the
+  // Register triple buffer: while one K chunk is multiplied, the next two chunks' codes,
+  // scales, zero points and activation rows are in flight. Loads use addresses clamped into the
   // matrices (columns past N, the chunk after the last), so no branch surrounds them and the
   // compiler's wait counts stay exact; such values are never used.
   constexpr int XCN = NA * kMoeBM * KC / 8;           // 16-byte activation pieces per chunk
@@ -368,18 +368,21 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
           for (int r = 0; r < 4; ++r) acc[q][t][s][r] = fmaf(sf[s], part[t][s][r], acc[q][t][s][r]);
     }
   };
-  auto iter = [&](int kc0, Chunk& cur, Chunk& nxt) {
+  // chunk i is multiplied while chunks i + 1 and i + 2 are in flight (three register sets)
+  auto iter = [&](int kc0, Chunk& cur, Chunk& ahead2) {
     __syncthreads();  // the previous chunk's activation reads are done
     stage(cur);
     __syncthreads();
-    load_chunk(min(kc0 + KC, K - KC), nxt);
+    load_chunk(min(kc0 + 2 * KC, K - KC), ahead2);
     if (wave_active) multiply(cur);
   };
-  Chunk c0, c1;
+  Chunk c0, c1, c2;
   load_chunk(0, c0);
-  for (int kc0 = 0; kc0 < K; kc0 += 2 * KC) {
-    iter(kc0, c0, c1);
+  load_chunk(min(KC, K - KC), c1);
+  for (int kc0 = 0; kc0 < K; kc0 += 3 * KC) {
+    iter(kc0, c0, c2);
     if (kc0 + KC < K) iter(kc0 + KC, c1, c0);
+    if (kc0 + 2 * KC < K) iter(kc0 + 2 * KC, c2, c1);
   }
 
   if constexpr (GATE_UP) {
