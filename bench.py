@@ -441,7 +441,7 @@ def main():
                      "kernel": "miq::pd::decode_persistent_kernel",
                      "measured_on": "the timed graph replays (one launch per token)",
                      "avg_launch_us": round(t_step * 1e6, 2), "algorithmic_bytes_per_launch": kernel_bytes},
-        "gemv_kernel": {"kernel": "the drop-in GEMV operator (miq::gptq_gemv_kernel; miq::gm::gemv_mma_kernel for layers of >= 4 MiB of codes)",
+        "gemv_kernel": {"kernel": "the drop-in GEMV operator (one row of int4 codes: miq::gm::gemv_mma_kernel)",
                         "measured_on": "the token's 97 GEMVs alone, 2 alternating weight copies (522 MB)",
                         "avg_launch_us": round(t_gemv / launches * 1e6, 3),
                         "achieved_GBs": round(step_bytes / t_gemv / 1e9, 2),

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void gptq_repack_kernel(const uint32_t* __rest
 // writes the output and re-arms the counter to zero, so results are deterministic.
 
 #ifndef MIQ_GEMV_MMA_MIN_BYTES
-#define MIQ_GEMV_MMA_MIN_BYTES (4u << 20)  // int4 codes of a layer from which one row takes gemv_mma
+#define MIQ_GEMV_MMA_MIN_BYTES 0u  // int4 codes of a layer from which one row takes gemv_mma (every size)
 #endif
 #ifndef MIQ_GEMV_MIN_WGS
 #define MIQ_GEMV_MIN_WGS 1  // split K further while fewer workgroups than this would run
@@ -630,7 +630,7 @@ extern "C" int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, co
   int rc = gemv_check("gptq_gemv", x, x_dtype, qweight, qzeros, scales, scales_dtype, out, out_dtype, M, K, N,
                       gs, bits);
   if (rc || M == 0) return rc;
-  // one row of a large int4 layer: the matrix-core GEMV (it declines shapes it does not cover)
+  // one row of an int4 layer: the matrix-core GEMV (it declines shapes it does not cover)
   if (M == 1 && bits == 4 && (size_t)K * N / 2 >= MIQ_GEMV_MMA_MIN_BYTES &&
       (workspace == nullptr || aligned(workspace, 256))) {
     rc = gemv_mma(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, K, N, gs,
