@@ -19,12 +19,18 @@
 //
 // Pipeline. K is walked in stages of KC (<= 128, inside one group). A stage's activation rows,
 // packed weight rows, scales and zero points are copied global -> LDS by the DMA path of the
-// vector memory unit (global_load_lds), NBUF - 1 stages ahead of the stage being multiplied, so
-// the loads of several stages are in flight while the matrix cores work and no register holds
-// data on its way to LDS. One barrier per stage both publishes the stage that landed and frees
-// the buffer that the next copy overwrites. Activation rows sit in LDS with their 16-byte
-// chunks XOR-swizzled by row (chunk c of row r at slot c ^ (r mod chunks-per-row)), so the 16
-// rows that one operand read touches fall in different banks.
+// vector memory unit (global_load_lds), so no register holds data on its way to LDS. The
+// workgroup's multiplying waves are two halves of 4 (one wave of each half per SIMD, on the same
+// columns): stages go in pairs, and half h multiplies stage 2j + h of pair j into accumulators of
+// its own. Wave tiles of up to 4 MFMA tiles get 4 more waves that only issue the copies, P2
+// pairs ahead (a copy instruction that finds the memory pipeline full stalls the wave that
+// issues it; kept on their own waves, those stalls never hold back an MFMA); with larger tiles
+// each multiplying wave copies its own stages (measured faster there: three waves per SIMD cap
+// the registers at 168, and the copies are then the bound either way). One barrier per pair both publishes the pair that landed and frees the buffers that
+// the next copies overwrite; while one multiplying wave of a SIMD waits on LDS, the other keeps
+// the matrix core busy. The halves' sums are added at the end (half 0 + half 1, a fixed order). Activation rows sit in LDS with their 16-byte chunks
+// XOR-swizzled by row (chunk c of row r at slot c ^ (r mod chunks-per-row)), so the 16 rows that
+// one operand read touches fall in different banks.
 //
 // K may also be split over workgroups (ksplit) when the tile grid alone is too small for the
 // chip; slices are combined deterministically through the workspace, the last workgroup to
@@ -124,25 +130,30 @@ template <int BITS, int TM, int CB, int KC, typename ST> struct GemmShape {
   static constexpr int NIW = (NI + 3) / 4;        // per wave (the last ones repeat the zero DMA)
   static constexpr int A_OFF = 0, B_OFF = BM * AROW, S_OFF = B_OFF + BROWS * BROWB, Z_OFF = S_OFF + SB;
   static constexpr int STAGE = Z_OFF + 256;
-  static constexpr int NBUF = 4 * STAGE + 64 <= kLdsBytes ? 4 : (3 * STAGE + 64 <= kLdsBytes ? 3 : 2);
-  static constexpr int P = NBUF - 1;              // stages in flight ahead of the one multiplied
+  static constexpr int NB2 = 6 * STAGE + 64 <= kLdsBytes ? 3 : 2;  // buffered stage pairs
+  static constexpr int NBUF = 2 * NB2;
+  static constexpr int P2 = NB2 - 1;              // pairs in flight ahead of the one multiplied
+  static constexpr int RED = 4 * TM * CB * 4 * 64 * 4;  // one half's accumulators, for the final sum
   static_assert(BM % RPI == 0 && (BROWS * BROWB) % 1024 == 0 && SB % 256 == 0, "whole DMAs");
   static_assert(BN / PER <= 64, "zero points of a tile fit one DMA");
-  static_assert((P - 1) * NIW < 64, "vmcnt range");
+  static constexpr int LDS = NBUF * STAGE > RED ? NBUF * STAGE : RED;
+  static constexpr bool COPIERS = TM * CB <= 4;   // 4 waves that only copy
+  static constexpr int THREADS = COPIERS ? 768 : 512;
+  static_assert(4 * STAGE + 64 <= kLdsBytes && LDS + 64 <= kLdsBytes, "LDS");
+  static_assert(4 * NIW < 64, "vmcnt range");
 };
 
-// 8 waves: 4 multiply (one per SIMD), 4 only issue the stage copies. A copy instruction that
-// finds the memory pipeline full stalls the wave that issues it; kept on their own waves, those
-// stalls never hold back an MFMA.
+// Waves w and w + 4 own the same columns and take alternate stages; wave w + 8, if any, copies.
 template <int BITS, int TM, int CB, int KC, typename ST, typename OT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gptq_gemm_kernel(
+__global__ __attribute__((amdgpu_flat_work_group_size(1, TM * CB <= 4 ? 768 : 512),
+                          amdgpu_waves_per_eu(TM * CB <= 4 ? 3 : 2, TM * CB <= 4 ? 3 : 2))) void gptq_gemm_kernel(
     const __half* __restrict__ xp, const uint32_t* __restrict__ qw, const uint32_t* __restrict__ qz,
     const ST* __restrict__ sc, const float* __restrict__ bias, OT* __restrict__ out, float* __restrict__ ws,
     int* __restrict__ counters, int M, int K, int N, int gs, float zoff, int stages_per_wg, int ksplit, int ntiles,
     int mtiles) {
   using G = GemmShape<BITS, TM, CB, KC, ST>;
-  constexpr int PER = G::PER, STEPS = G::STEPS, RB = G::RB, NBUF = G::NBUF, P = G::P, NIW = G::NIW;
-  __shared__ __align__(16) char lds[NBUF * G::STAGE];
+  constexpr int PER = G::PER, STEPS = G::STEPS, RB = G::RB, NBUF = G::NBUF, NB2 = G::NB2, P2 = G::P2, NIW = G::NIW;
+  __shared__ __align__(16) char lds[G::LDS];
   __shared__ int is_last;
 
   // ---- tile of this workgroup: XCD-major order, row tiles fastest ----
@@ -154,8 +165,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ntile = rest / ksplit;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const bool producer = uniform(tid >> 6) >= 4;  // waves 4..7 issue the copies
-  const int wave = uniform(tid >> 6) & 3;  // (the range lets each copy's kind fold at compile time)
+  const bool copier = G::COPIERS && uniform(tid >> 6) >= 8;  // waves 8..11 issue the copies
+  const int half = (uniform(tid >> 6) >> 2) & 1;  // which stage of each pair this wave multiplies
+  const int wave = uniform(tid >> 6) & 3;  // column group / copy slot (the range lets each copy's kind fold)
   const int p = lane & 15, kb = lane >> 4;
   const int n0 = ntile * G::BN;
   const int cl = wave * 16 * CB + CB * p;  // the lane's first column within the tile
@@ -282,29 +294,80 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int r = 0; r < 4; ++r) acc[t][s][r] = fmaf(sf[s], part[t][s][r], acc[t][s][r]);
   };
 
-  // ---- pipeline: stages st0 .. last, P of them in flight ----
-  if (producer) {
+  // ---- pipeline: pairs of stages, half h owning stage st0 + 2 j + h of pair j (buffer
+  // 2 (j mod NB2) + h); the copying waves run P2 pairs ahead ----
+  const int nst_wg = st1 - st0;
+  const int nmine = (nst_wg - half + 1) / 2;  // stages of this half (pairs 0 .. nmine - 1)
+  const int npairs = (nst_wg + 1) / 2;
+  auto issue_pair = [&](int q) __attribute__((always_inline)) {
+    const int b = 2 * (q % NB2);
+    issue(st0 + 2 * q, b);
+    if (2 * q + 1 < nst_wg) issue(st0 + 2 * q + 1, b + 1);
+  };
+  if constexpr (G::COPIERS) {
+    if (copier) {
 #pragma unroll
-    for (int q = 0; q < P; ++q)
-      if (st0 + q <= last) issue(st0 + q, q);
-  }
-  for (int s = st0; s <= last; ++s) {
-    // a producer's copies of stage s are done once at most min(P - 1, last - s) later stages
-    // remain in flight; the barrier makes every copy of stage s visible and tells the producers
-    // that stage s - 1, whose buffer the next copy reuses, has been multiplied
-    if (producer) {
-      const int ahead = min(P - 1, last - s);
-      if (ahead >= 2) wait_vmcnt<(P - 1 >= 2 ? 2 * NIW : 0)>();
-      else if (ahead == 1) wait_vmcnt<NIW>();
+      for (int q = 0; q < P2; ++q)
+        if (q < npairs) issue_pair(q);
+    }
+    for (int j = 0; j < npairs; ++j) {
+      // a copying wave's copies of pair j are done once only those of its later pairs (at most
+      // P2 - 1 <= 1, issued after them) remain; the barrier makes every copy of pair j visible
+      // and tells the copying waves that pair j - 1, whose buffers the next copies reuse, has
+      // been multiplied
+      if (copier) {
+        const int nxt = j + 1 < npairs && P2 >= 2 ? (2 * (j + 1) + 1 < nst_wg ? 2 : 1) : 0;  // stages of pair j + 1
+        if (nxt == 2) wait_vmcnt<2 * NIW>();
+        else if (nxt == 1) wait_vmcnt<NIW>();
+        else wait_vmcnt<0>();
+      }
+      __syncthreads();
+      if (copier) {
+        if (j + P2 < npairs) issue_pair(j + P2);
+      } else if (j < nmine) {
+        compute(2 * (j % NB2) + half);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < P2; ++q)
+      if (q < nmine) issue(st0 + 2 * q + half, 2 * q + half);
+    for (int j = 0; j < npairs; ++j) {
+      // this wave's copies of pair j are done once only those of its later pairs (at most
+      // P2 - 1 <= 1, issued after them) remain
+      const int later = min(P2 - 1, max(0, nmine - 1 - j));
+      if (P2 >= 2 && later >= 1) wait_vmcnt<NIW>();
       else wait_vmcnt<0>();
+      __syncthreads();
+      if (j + P2 < nmine) issue(st0 + 2 * (j + P2) + half, 2 * ((j + P2) % NB2) + half);
+      if (j < nmine) compute(2 * (j % NB2) + half);
+    }
+  }
+
+  // ---- the two halves' sums: half 1 through LDS (the stage buffers are free once every wave
+  // has passed the barrier), half 0 adds them ----
+  __syncthreads();
+  {
+    float* red = reinterpret_cast<float*>(lds) + (size_t)wave * (TM * CB * 4 * 64) + lane;
+    if (half == 1 && !copier) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int s = 0; s < CB; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[((t * CB + s) * 4 + r) * 64] = acc[t][s][r];
     }
     __syncthreads();
-    if (producer) {
-      if (s + P <= last) issue(s + P, (s - st0 + P) % NBUF);
-    } else {
-      compute((s - st0) % NBUF);
+    if (half == 0 && !copier) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int s = 0; s < CB; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[t][s][r] += red[((t * CB + s) * 4 + r) * 64];
     }
   }
+  const bool producer = copier || half == 1;  // from here on, only the barriers
 
   // ---- epilogue: D[row = m0 + 16 t + 4 kb + r][col = ncol + s] = acc[t][s][r] ----
   if (ksplit == 1) {
@@ -418,7 +481,7 @@ struct GemmPlan {
   size_t partial_bytes, xp_bytes, ws_bytes;
 };
 
-static int gemm_plan(int M, int K, int N, int gs, GemmPlan* p) {
+static int gemm_plan(int M, int K, int N, int gs, int bits, GemmPlan* p) {
   int kc = 0;
   if (gs % 128 == 0) kc = 128;
   else if (gs % 64 == 0) kc = 64;
@@ -447,9 +510,10 @@ static int gemm_plan(int M, int K, int N, int gs, GemmPlan* p) {
 #endif
   p->tm = kWaveTiles[pick].tm;
   p->cb = kWaveTiles[pick].cb;
+  if (bits == 8 && p->cb == 4 && p->kc == 128) p->kc = 64;  // two stage pairs of LDS
   p->ntiles = (N + 64 * p->cb - 1) / (64 * p->cb);
   p->mtiles = (M + 16 * p->tm - 1) / (16 * p->tm);
-  const int nst = K / kc;
+  const int nst = K / p->kc;
   const int base = p->ntiles * p->mtiles;
   int ksplit = base <= kMaxCounters ? (MIQ_GEMM_TARGET_WGS + base - 1) / base : 1;
   if (ksplit > nst) ksplit = nst;
@@ -468,7 +532,7 @@ static int launch_gemm(const GemmPlan& p, const __half* xp, const int32_t* qw, c
   int* counters = static_cast<int*>(ws);
   float* partials = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
   const int grid = p.ntiles * p.mtiles * p.ksplit;
-  hipLaunchKernelGGL((gptq_gemm_kernel<BITS, TM, CB, KC, ST, OT>), dim3(grid), dim3(512), 0, st, xp,
+  hipLaunchKernelGGL((gptq_gemm_kernel<BITS, TM, CB, KC, ST, OT>), dim3(grid), dim3(GemmShape<BITS, TM, CB, KC, ST>::THREADS), 0, st, xp,
                      reinterpret_cast<const uint32_t*>(qw), reinterpret_cast<const uint32_t*>(qz),
                      static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, M, K, N, gs, zoff,
                      p.stages_per_wg, p.ksplit, p.ntiles, p.mtiles);
@@ -493,12 +557,15 @@ template <int BITS, int KC>
 static int gemm_tiles(const GemmPlan& p, const __half* xp, const int32_t* qw, const int32_t* qz, const void* sc,
                       int sd, const float* bias, void* out, int od, void* ws, int M, int K, int N, int gs, float zoff,
                       hipStream_t st) {
-  if (p.tm == 4 && p.cb == 4) return gemm_types<BITS, 4, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
   if (p.tm == 4 && p.cb == 2) return gemm_types<BITS, 4, 2, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
-  if (p.tm == 2 && p.cb == 4) return gemm_types<BITS, 2, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
   if (p.tm == 2 && p.cb == 2) return gemm_types<BITS, 2, 2, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
   if (p.tm == 1 && p.cb == 2) return gemm_types<BITS, 1, 2, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
-  return gemm_types<BITS, 1, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  if constexpr (BITS == 4 || KC < 128) {  // int8 weights with 4 columns a lane take 64-wide stages
+    if (p.tm == 4 && p.cb == 4) return gemm_types<BITS, 4, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+    if (p.tm == 2 && p.cb == 4) return gemm_types<BITS, 2, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+    if (p.tm == 1 && p.cb == 4) return gemm_types<BITS, 1, 4, KC>(p, xp, qw, qz, sc, sd, bias, out, od, ws, M, K, N, gs, zoff, st);
+  }
+  return ::miq::fail(MIQ_ERR_UNSUPPORTED, "gptq_gemm: no kernel for tile %dx%d, stage %d", p.tm, p.cb, KC);
 }
 
 template <int BITS>
@@ -524,7 +591,7 @@ extern "C" int miq_gptq_gemm_workspace(int M, int K, int N, int gs, int bits, si
   MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "gptq_gemm_workspace: M=%d", M);
   if (M == 0) return MIQ_OK;
   GemmPlan p;
-  rc = gemm_plan(M, K, N, gs, &p);
+  rc = gemm_plan(M, K, N, gs, bits, &p);
   if (rc) return rc;
   *bytes = p.ws_bytes;
   // the few-row kernel's needs, with or without act-order (the caller may pass either)
@@ -570,7 +637,7 @@ extern "C" int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* 
     if (rc != MIQ_ERR_UNSUPPORTED) return rc;
   }
   GemmPlan p;
-  rc = gemm_plan(M, K, N, gs, &p);
+  rc = gemm_plan(M, K, N, gs, bits, &p);
   if (rc) return rc;
   MIQ_REQUIRE(workspace && workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
               "gptq_gemm: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes, workspace_bytes);
