@@ -31,7 +31,9 @@ class Qwen2Oracle:
         self.layers = weights["layers"]
         self.embed = weights["embed"]                      # (V, H) fp16
         self.final_norm = np.asarray(weights["final_norm"], np.float32)
-        self.head = self.quantize_head(self.embed, head_block)
+        # an untied model quantizes its own fp16 lm_head the same way (`webtorch/llm.py:604-612`)
+        head = weights.get("head")
+        self.head = self.quantize_head(self.embed if head is None else np.asarray(head, np.float16), head_block)
 
     def quantize_head(self, emb, blk):
         out = []

@@ -1,0 +1,341 @@
+"""On-disk checkpoints for the quantized-linear path: AutoGPTQ safetensors directories and the
+GGUF container with native Q4_K upload.
+
+* `SafetensorsDir` reads a HuggingFace model directory (`model.safetensors.index.json` and its
+  shards, or a single `model.safetensors`) by byte ranges, as the reference's `_hdr` / `_np` /
+  `_f16_chunked` do (`webtorch/llm.py:541-592`): an 8-byte little-endian header length, a
+  JSON header (`__metadata__` dropped), tensors at `data_offsets` past the header. BF16 and
+  F16 become fp32 and I32 stays int32 on `array`; `rows_f16` streams a 2-D table in row blocks
+  straight to fp16, never holding the fp32 copy.
+* `gptq_weights(path)` builds the weights dictionary of `llm.CausalLM` from an AutoGPTQ
+  directory (`webtorch/llm.py:418-475, 506-539, 569-573, 614-647` -- `from_gptq`): the shape from
+  `config.json`, AutoGPTQ tensors per projection, norms, the fp16 embedding and, for an untied
+  model, the fp16 `lm_head.weight` (quantized on the device like the tied head). Scales stay in
+  their fp16 file encoding (the reference widens them to fp32 on the host, an exact
+  conversion); `g_idx` is not read, as in the reference (`_qlin` passes no g_idx).
+* `parse_header` / `GGUFFile` read the GGUF container (`webtorch/ggufload.py:16-112`): magic,
+  version, typed metadata, tensor infos (ggml dimension order, innermost first), data section
+  aligned to `general.alignment`. `GGUFFile.linear` uploads a 2-D tensor unchanged as a
+  `GGMLLinear` when a native kernel decodes its type (`_gload_native`,
+  `webtorch/llm.py:762-783`) and returns None otherwise, for the caller to convert.
+
+File formats are kept exactly (they are formats); the code is this package's own.
+"""
+import json
+import os
+import struct
+
+import numpy as np
+
+from . import core
+
+# ---------------------------------------------------------------------------------------------
+# safetensors
+
+
+class SafetensorsDir:
+    """Tensors of a HuggingFace safetensors model directory, read by byte range."""
+
+    def __init__(self, path):
+        self.base = str(path)
+        self._hdrs = {}
+        idx = os.path.join(self.base, "model.safetensors.index.json")
+        if os.path.exists(idx):
+            with open(idx) as f:
+                self.index = dict(json.load(f)["weight_map"])
+        else:
+            h, _ = self.header("model.safetensors")
+            self.index = {k: "model.safetensors" for k in h}
+
+    def header(self, shard):
+        """(tensor table, byte offset of the data section) of one shard file."""
+        if shard not in self._hdrs:
+            with open(os.path.join(self.base, shard), "rb") as f:
+                n = int.from_bytes(f.read(8), "little")
+                raw = f.read(n)
+            if len(raw) != n:
+                raise ValueError("%s: truncated safetensors header" % shard)
+            h = json.loads(raw.decode("utf-8"))
+            h.pop("__metadata__", None)
+            self._hdrs[shard] = (h, 8 + n)
+        return self._hdrs[shard]
+
+    def __contains__(self, name):
+        return name in self.index
+
+    def names(self):
+        return list(self.index)
+
+    def info(self, name):
+        if name not in self.index:
+            raise KeyError("tensor %r not in %s" % (name, self.base))
+        h, base = self.header(self.index[name])
+        return h[name], base
+
+    def _read(self, name, a, b):
+        """Bytes [a, b) of a tensor's data."""
+        info, base = self.info(name)
+        with open(os.path.join(self.base, self.index[name]), "rb") as f:
+            f.seek(base + info["data_offsets"][0] + a)
+            raw = f.read(b - a)
+        if len(raw) != b - a:
+            raise ValueError("%s: tensor %r truncated" % (self.base, name))
+        return raw
+
+    @staticmethod
+    def _decode(raw, dt, to_f16=False):
+        if dt == "BF16":
+            a = (np.frombuffer(raw, np.uint16).astype(np.uint32) << 16).view(np.float32)
+        elif dt == "F16":
+            a = np.frombuffer(raw, np.float16)
+            return a.copy() if to_f16 else a.astype(np.float32)
+        elif dt == "F32":
+            a = np.frombuffer(raw, np.float32)
+        elif dt == "I32":
+            if to_f16:
+                raise ValueError("an I32 tensor has no fp16 form")
+            return np.frombuffer(raw, np.int32).copy()
+        else:
+            raise ValueError("safetensors dtype %s is not read by this loader" % dt)
+        return a.astype(np.float16) if to_f16 else a.copy()
+
+    def array(self, name, keep_f16=False):
+        """The tensor as numpy: BF16/F16/F32 -> fp32 (F16 kept with `keep_f16`), I32 -> int32."""
+        info, _ = self.info(name)
+        a, z = info["data_offsets"]
+        raw = self._read(name, 0, z - a)
+        dt = info["dtype"]
+        arr = self._decode(raw, dt, to_f16=keep_f16 and dt == "F16")
+        return arr.reshape(info["shape"])
+
+    def rows_f16(self, name, chunk_bytes=64 << 20):
+        """A 2-D F16/BF16/F32 table as fp16 (rows, cols), read in row blocks of about
+        `chunk_bytes` so no fp32 copy of the whole table exists."""
+        info, _ = self.info(name)
+        rows, cols = info["shape"]
+        dt = info["dtype"]
+        esz = {"F16": 2, "BF16": 2, "F32": 4}.get(dt)
+        if esz is None:
+            raise ValueError("%r: dtype %s is not a float table" % (name, dt))
+        row = cols * esz
+        rpc = max(1, chunk_bytes // row)
+        out = np.empty((rows, cols), np.float16)
+        for r0 in range(0, rows, rpc):
+            r1 = min(rows, r0 + rpc)
+            out[r0:r1] = self._decode(self._read(name, r0 * row, r1 * row), dt, to_f16=True).reshape(r1 - r0, cols)
+        return out
+
+
+def _text_config(cfg):
+    """Composite configs nest the decoder under `text_config` (`webtorch/llm.py:428-432`)."""
+    t = cfg.get("text_config") or {}
+    return dict(t) if "hidden_size" in t else cfg
+
+
+KV_BUDGET = 2 << 30  # bytes of fp32 K and V cache the automatic context length may take
+
+
+def auto_lmax(requested, declared, L, NKV, HD):
+    """Context length to load with (`webtorch/llm.py:1381-1395`): an explicit request, else what
+    the model declares (2048 if nothing), capped by the KV-cache budget, at least 512."""
+    if requested:
+        return int(requested)
+    per_tok = 2 * L * NKV * HD * 4
+    cap = max(512, KV_BUDGET // per_tok)
+    want = int(declared) if declared else 2048
+    return max(512, min(want, cap))
+
+
+def gptq_config(path):
+    """Shape, quantization and context fields of an AutoGPTQ directory's config.json."""
+    with open(os.path.join(str(path), "config.json")) as f:
+        full = json.load(f)
+    cfg = _text_config(full)
+    q = full.get("quantization_config") or cfg.get("quantization_config")
+    if not q:
+        raise ValueError("%s: config.json has no quantization_config (not an AutoGPTQ directory)" % path)
+    H, NH = int(cfg["hidden_size"]), int(cfg["num_attention_heads"])
+    out = dict(L=int(cfg["num_hidden_layers"]), H=H, NH=NH, NKV=int(cfg.get("num_key_value_heads", NH)),
+               HD=int(cfg.get("head_dim") or H // NH), I=int(cfg["intermediate_size"]),
+               V=int(cfg["vocab_size"]), eps=float(cfg.get("rms_norm_eps", 1e-6)),
+               theta=float(cfg.get("rope_theta", 10000.0)), gs=int(q["group_size"]), bits=int(q["bits"]))
+    if int(cfg.get("num_experts", cfg.get("num_local_experts", 0)) or 0):
+        raise NotImplementedError("sparse-MoE decoders are run through moe_mlp, not CausalLM")
+    types = cfg.get("layer_types") or []
+    if any(t != "full_attention" for t in types) or int(cfg.get("full_attention_interval", 0) or 0) > 1:
+        raise NotImplementedError("hybrid linear-attention decoders are not part of this path")
+    return out, bool(cfg.get("tie_word_embeddings", False)), cfg.get("max_position_embeddings")
+
+
+def gptq_weights(path):
+    """`llm.CausalLM` weights from an AutoGPTQ safetensors directory, plus the model's
+    declared context length: (weights, declared_lmax)."""
+    cfg, tie, declared = gptq_config(path)
+    st = SafetensorsDir(path)
+
+    def lin(prefix):
+        d = {"qweight": st.array(prefix + ".qweight"), "qzeros": st.array(prefix + ".qzeros"),
+             "scales": st.array(prefix + ".scales", keep_f16=True)}
+        if prefix + ".bias" in st:
+            d["bias"] = st.array(prefix + ".bias")
+        return d
+
+    if "model.layers.0.self_attn.q_norm.weight" in st:
+        raise NotImplementedError("QK-norm decoders (Qwen3) are not part of this path")
+    layers = []
+    for i in range(cfg["L"]):
+        p = "model.layers.%d." % i
+        lay = {"q": lin(p + "self_attn.q_proj"), "k": lin(p + "self_attn.k_proj"),
+               "v": lin(p + "self_attn.v_proj"), "o": lin(p + "self_attn.o_proj"),
+               "gate": lin(p + "mlp.gate_proj"), "up": lin(p + "mlp.up_proj"),
+               "down": lin(p + "mlp.down_proj"),
+               "in_ln": st.array(p + "input_layernorm.weight"),
+               "post_ln": st.array(p + "post_attention_layernorm.weight")}
+        layers.append(lay)
+    w = {"layers": layers, "embed": st.rows_f16("model.embed_tokens.weight"),
+         "final_norm": st.array("model.norm.weight"), "cfg": cfg}
+    if not tie:
+        w["head"] = st.rows_f16("lm_head.weight")
+    return w, declared
+
+
+# ---------------------------------------------------------------------------------------------
+# GGUF
+
+GGUF_MAGIC = 0x46554747  # "GGUF", little-endian
+# metadata value types
+(GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32, GGUF_BOOL, GGUF_STRING, GGUF_ARRAY,
+ GGUF_U64, GGUF_I64, GGUF_F64) = range(13)
+_SCALAR = {GGUF_U8: "<B", GGUF_I8: "<b", GGUF_U16: "<H", GGUF_I16: "<h", GGUF_U32: "<I", GGUF_I32: "<i",
+           GGUF_F32: "<f", GGUF_U64: "<Q", GGUF_I64: "<q", GGUF_F64: "<d"}
+
+# ggml tensor type ids and (values per block, bytes per block) of the types this package knows
+GGML_TYPES = {0: ("F32", 1, 4), 1: ("F16", 1, 2), 2: ("Q4_0", 32, 18), 3: ("Q4_1", 32, 20),
+              6: ("Q5_0", 32, 22), 7: ("Q5_1", 32, 24), 8: ("Q8_0", 32, 34), 10: ("Q2_K", 256, 84),
+              11: ("Q3_K", 256, 110), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176),
+              14: ("Q6_K", 256, 210), 30: ("BF16", 1, 2)}
+GGML_NAMES = {k: v[0] for k, v in GGML_TYPES.items()}
+GGML_IDS = {v[0]: k for k, v in GGML_TYPES.items()}
+
+
+def tensor_nbytes(ttype, n):
+    """Bytes of n values of ggml type `ttype` (id or name); n must fill whole blocks."""
+    tid = GGML_IDS[ttype] if isinstance(ttype, str) else int(ttype)
+    if tid not in GGML_TYPES:
+        raise NotImplementedError("ggml type %s" % ttype)
+    _, vals, blk = GGML_TYPES[tid]
+    if n % vals:
+        raise ValueError("%d values do not fill whole %s blocks of %d" % (n, GGML_NAMES[tid], vals))
+    return n // vals * blk
+
+
+class _Cursor:
+    """Little-endian reads over a byte buffer; EOFError past its end (the caller reads more)."""
+
+    def __init__(self, buf):
+        self.b = memoryview(buf)
+        self.p = 0
+
+    def take(self, n):
+        if self.p + n > len(self.b):
+            raise EOFError("GGUF header needs more than %d bytes" % len(self.b))
+        v = self.b[self.p:self.p + n]
+        self.p += n
+        return v
+
+    def scalar(self, fmt):
+        return struct.unpack(fmt, self.take(struct.calcsize(fmt)))[0]
+
+    def string(self):
+        return bytes(self.take(self.scalar("<Q"))).decode("utf-8", "replace")
+
+    def value(self, t):
+        if t in _SCALAR:
+            return self.scalar(_SCALAR[t])
+        if t == GGUF_BOOL:
+            return self.take(1)[0] != 0
+        if t == GGUF_STRING:
+            return self.string()
+        if t == GGUF_ARRAY:
+            at, n = self.scalar("<I"), self.scalar("<Q")
+            return [self.value(at) for _ in range(n)]
+        raise ValueError("bad GGUF metadata value type %d" % t)
+
+
+def parse_header(buf):
+    """(version, metadata, tensor_infos, data_start) of a GGUF file from a prefix `buf` of it
+    (`webtorch/ggufload.py:92-112`). Tensor infos are dicts name / dims (ggml order, innermost
+    first) / type / offset (from data_start). Raises EOFError when `buf` ends inside the
+    header."""
+    r = _Cursor(buf)
+    if r.scalar("<I") != GGUF_MAGIC:
+        raise ValueError("not a GGUF file")
+    version = r.scalar("<I")
+    if version < 2:
+        raise NotImplementedError("GGUF version %d (64-bit counts need version >= 2)" % version)
+    n_tensors, n_kv = r.scalar("<Q"), r.scalar("<Q")
+    meta = {}
+    for _ in range(n_kv):
+        k = r.string()
+        meta[k] = r.value(r.scalar("<I"))
+    infos = []
+    for _ in range(n_tensors):
+        name = r.string()
+        nd = r.scalar("<I")
+        dims = [r.scalar("<Q") for _ in range(nd)]
+        infos.append({"name": name, "dims": dims, "type": r.scalar("<I"), "offset": r.scalar("<Q")})
+    align = int(meta.get("general.alignment", 32))
+    return version, meta, infos, (r.p + align - 1) // align * align
+
+
+class GGUFFile:
+    """A GGUF file on disk: header parsed from a growing prefix, tensors read by byte range."""
+
+    def __init__(self, path, first_read=1 << 20, max_header=128 << 20):
+        self.path = str(path)
+        size = first_read
+        with open(self.path, "rb") as f:
+            while True:
+                f.seek(0)
+                buf = f.read(size)
+                try:
+                    self.version, self.meta, infos, self.data_start = parse_header(buf)
+                    break
+                except EOFError:
+                    if len(buf) < size or size >= max_header:
+                        raise
+                    size *= 2
+        self.infos = {t["name"]: t for t in infos}
+
+    def shape(self, name):
+        """numpy order (outermost first), e.g. (out, in) for a 2-D weight."""
+        return tuple(int(d) for d in reversed(self.infos[name]["dims"]))
+
+    def type_name(self, name):
+        t = self.infos[name]["type"]
+        return GGML_NAMES.get(t, "type%d" % t)
+
+    def raw(self, name):
+        t = self.infos[name]
+        n = int(np.prod([int(d) for d in t["dims"]], dtype=np.int64))
+        nb = tensor_nbytes(t["type"], n)
+        with open(self.path, "rb") as f:
+            f.seek(self.data_start + int(t["offset"]))
+            b = f.read(nb)
+        if len(b) != nb:
+            raise ValueError("%s: tensor %r truncated" % (self.path, name))
+        return b
+
+    def linear(self, name, bias=None):
+        """The 2-D weight uploaded unchanged as a GGMLLinear (K = innermost dimension), or None
+        when no native kernel decodes its type or K is not a whole number of blocks."""
+        t = self.infos[name]
+        if len(t["dims"]) != 2:
+            return None
+        nm = GGML_NAMES.get(t["type"])
+        if not core.ggml_native_supported(nm):
+            return None
+        N, K = self.shape(name)
+        if K % GGML_TYPES[t["type"]][1]:
+            return None
+        return core.GGMLLinear(self.raw(name), nm, K, N, bias)

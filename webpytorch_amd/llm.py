@@ -77,8 +77,10 @@ class CausalLM:
 
     Build with `CausalLM.from_weights(weights, lmax)` where `weights` holds AutoGPTQ tensors per
     layer ({"q","k","v","o","gate","up","down"} dicts with qweight/qzeros/scales[/bias],
-    "in_ln", "post_ln"), the fp16 "embed" table (tied head), "final_norm" and "cfg"
-    (L, H, NH, NKV, HD, I, V, gs, bits[, eps, theta])."""
+    "in_ln", "post_ln"), the fp16 "embed" table, optionally an fp16 "head" (V, H) for an untied
+    model (else the head is tied to the embedding), "final_norm" and "cfg"
+    (L, H, NH, NKV, HD, I, V, gs, bits[, eps, theta]); or with `CausalLM.from_gptq(path)` from an
+    AutoGPTQ safetensors directory."""
 
     def __init__(self, weights, lmax=256, fused=True, persistent=None):
         c = weights["cfg"]
@@ -102,7 +104,10 @@ class CausalLM:
             })
         self.embed = core.to_device(np.asarray(weights["embed"], np.float16))
         self.final_norm = core.to_device(np.asarray(weights["final_norm"], np.float32))
-        self.head = self._quantize_head()
+        head = weights.get("head")
+        if head is not None and tuple(np.shape(head)) != (self.V, self.H):
+            raise ValueError("head must be (V, H) = (%d, %d), got %s" % (self.V, self.H, np.shape(head)))
+        self.head = self._quantize_head(None if head is None else core.to_device(np.asarray(head, np.float16)))
         self._alloc()
         self._graph = None
 
@@ -110,11 +115,23 @@ class CausalLM:
     def from_weights(cls, weights, lmax=256, fused=True, persistent=None):
         return cls(weights, lmax, fused, persistent)
 
+    @classmethod
+    def from_gptq(cls, path, lmax=None, fused=True, persistent=None):
+        """Load an AutoGPTQ safetensors directory (config.json + model.safetensors or an index
+        and shards), as the reference's `from_gptq` does (`webtorch/llm.py:614-647`). `lmax=None`
+        takes the model's declared context, capped by a 2 GiB KV-cache budget."""
+        from . import checkpoint
+        w, declared = checkpoint.gptq_weights(path)
+        c = w["cfg"]
+        return cls(w, checkpoint.auto_lmax(lmax, declared, c["L"], c["NKV"], c["HD"]), fused, persistent)
+
     # ---- load-time ----
-    def _quantize_head(self):
-        """Tied head: the fp16 embedding (V, H) quantized on the device to int4 GPTQ with fp32
-        scales and zero offset 0, as `_quantize_head` does (`webtorch/llm.py:594-602`)."""
-        qw, qz, sc, K, N = core.gptq_quantize(self.embed, self.gs, self.bits, from_out_in=True)
+    def _quantize_head(self, head=None):
+        """The head (the fp16 embedding when tied, else the model's fp16 (V, H) head) quantized
+        on the device to int4 GPTQ with fp32 scales and zero offset 0, as `_quantize_head` does
+        (`webtorch/llm.py:594-612`)."""
+        qw, qz, sc, K, N = core.gptq_quantize(self.embed if head is None else head, self.gs, self.bits,
+                                              from_out_in=True)
         return _Lin({"qweight": qw, "qzeros": qz, "scales": sc}, K, self.gs, self.bits, 0.0)
 
     def _alloc(self):
