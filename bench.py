@@ -116,6 +116,31 @@ def q4k_bench(torch, core, copies=16, reps=32):
             "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def ggml_bench(torch, core, type_name, copies=12, reps=24):
+    """GGUF Q8_0 / Q6_K GEMV at the Llama-3-8B up_proj shape: x fp16 (1, 4096) -> y fp32
+    (1, 14336), over `copies` distinct weight copies (above the 256 MB Infinity Cache)."""
+    K, N = 4096, 14336
+    vals, blk = {"Q8_0": (32, 34), "Q6_K": (256, 210)}[type_name]
+    nb = N * K // vals
+    w = torch.randint(0, 256, (copies, nb, blk), dtype=torch.uint8, device="cuda")
+    d = 0 if type_name == "Q8_0" else 208
+    w[:, :, d + 1] &= 0x3B  # finite fp16 d
+    w = w.reshape(copies, N, -1)
+    x = torch.randn((1, K), device="cuda").half()
+    out = torch.empty((1, N), device="cuda")
+
+    def run():
+        for i in range(reps):
+            core.ggml_matmul(x, w[i % copies], type_name, K, N, out=out)
+    run()
+    torch.cuda.synchronize()
+    g = capture(torch, run)
+    t = timed(torch, g.replay, 5) / reps
+    nbytes = nb * blk + K * 2 + N * 4
+    return {"K": K, "N": N, "bytes": nbytes, "us": round(t * 1e6, 3), "GBs": round(nbytes / t / 1e9, 1),
+            "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
 
 
@@ -450,6 +475,8 @@ def main():
     if not a.no_extras:
         res["gemv_large"] = gemv_large(torch, core)
         res["q4k_gemv_llama3_8b_up"] = q4k_bench(torch, core)
+        res["q6k_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q6_K")
+        res["q8_0_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q8_0")
         res["gptq_gemm_act_order_4096"] = gemm_bench(torch, core)
         res["moe_qwen3_t256"] = moe_bench(torch, core)
     if not a.no_cpu:

@@ -146,6 +146,16 @@ int miq_q4k_dequant_f32(const uint8_t* blocks, float* out, int64_t n_blocks, voi
 int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out,
                  int out_dtype, int M, int K, int N, void* stream);
 
+/* out[M][N] = x[M][K] @ W^T + bias for the other native GGUF types a Q4_K_M file holds:
+ * ggml_type 8 (Q8_0: 34-byte blocks of 32 weights, fp16 d + int8 codes) or 14 (Q6_K: 210-byte
+ * super-blocks of 256 weights). W = N rows of K/32 (Q8_0) or K/256 (Q6_K) blocks as the file
+ * stores them; w and x 16-byte aligned; M <= 65535. Other types: MIQ_ERR_UNSUPPORTED.
+ * Replaces: `ggml_matmul` / `_ggml_run` for Q8_0 and Q6_K (webtorch/_core.py:3720-3779) with
+ * the decode kernel `_GGML_GEMV_*` and `_Q8_0_DEC` / `_Q6K_DEC` (webtorch/_core.py:2985-3044,
+ * 3071-3077, 3158-3176). */
+int miq_ggml_gemv(const void* x, int x_dtype, const uint8_t* w, int ggml_type, const float* bias,
+                  void* out, int out_dtype, int M, int K, int N, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Sparse MoE MLP (router + experts), all on the device
  *   route buffer: opaque int32 words laid out by (T, E, k), miq_moe_route_bytes long.

@@ -4,10 +4,10 @@ Follows `ggufload.dequant` for Q4_K (`webtorch/ggufload.py:116-130, 188-202`) an
 `UnquantizedLinear` float32 matmul (`webtorch/_core.py:4462-4481`) that the reference uses for
 a dequantized GGUF weight on the CPU.
 
-Pins: llama.cpp's `block_q4_K` / `dequantize_row_q4_K` semantics (the same formula),
-special cases (d = dmin = 0 gives zeros; all sub-scales 0 gives -dmin*m; a block with one
-nonzero code), the packer round trip (`webpytorch_amd.synth.pack_q4k_scales`), and golden
-vectors written by the reference's own `dequant` (`tests/golden/`).
+Pins (tests/test_oracle_q4k.py): a scalar restatement of llama.cpp's published
+`dequantize_row_q4_K` loop (the same formula, independent index arithmetic), special cases
+(d = dmin = 0 gives zeros; all sub-scales 0 gives -dmin*m; a block with one nonzero code), the
+packer round trip (`webpytorch_amd.synth.pack_q4k_scales`) and a brute-force matmul.
 """
 import numpy as np
 

@@ -64,6 +64,48 @@ def test_gemv_ragged_shapes_and_bias(gpu, K, N):
 
 def test_unsupported_type_raises(gpu):
     from webpytorch_amd import core
-    assert core.ggml_native_supported("Q4_K") and not core.ggml_native_supported("Q6_K")
+    assert core.ggml_native_supported("Q4_K") and not core.ggml_native_supported("Q5_K")
     with pytest.raises(NotImplementedError):
-        core.GGMLLinear(b"\0" * 210, "Q6_K", 256, 1)
+        core.GGMLLinear(b"\0" * 176, "Q5_K", 256, 1)
+
+
+# ---- Q8_0 and Q6_K (the other types of a Q4_K_M file) ------------------------------------
+
+def _ggml_case(type_name, K, N, seed):
+    from oracle import ggml
+    W = (synth.q8_0_layer if type_name == "Q8_0" else synth.q6k_layer)(seed, K, N)
+    return W, lambda x: ggml.ggml_matmul(x, W, type_name, K, N)
+
+
+@pytest.mark.parametrize("type_name", ["Q8_0", "Q6_K"])
+@pytest.mark.parametrize("M", [1, 3])
+def test_q8_0_q6k_gemv_llama3_up_shape(gpu, type_name, M):
+    import torch
+    from webpytorch_amd import core
+    K, N = 4096, 14336
+    W, ref_fn = _ggml_case(type_name, K, N, 3)
+    x = synth.activations(3, M, K, np.float16)
+    got = core.GGMLLinear(W, type_name, K, N)(torch.from_numpy(x)).cpu().numpy()
+    ref = ref_fn(x)
+    assert got.shape == (M, N) and _rel(got, ref) < 1e-5
+    assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+
+
+@pytest.mark.parametrize("type_name,K,N", [("Q8_0", 32, 2), ("Q8_0", 96, 33), ("Q8_0", 8192, 70),
+                                           ("Q6_K", 256, 2), ("Q6_K", 768, 33), ("Q6_K", 8192, 70)])
+def test_q8_0_q6k_ragged_rows_bias_dtypes(gpu, type_name, K, N):
+    """Odd block counts per row put every other row at a 2-byte offset; fp32 and fp16
+    activations, fp16 output, bias."""
+    import torch
+    from webpytorch_amd import core
+    W, ref_fn = _ggml_case(type_name, K, N, K + N)
+    b = np.linspace(-1, 1, N).astype(np.float32)
+    lin = core.GGMLLinear(W, type_name, K, N, bias=b)
+    for xdt in (np.float32, np.float16):
+        x = synth.activations(K, 2, K, xdt)
+        ref = ref_fn(x) + b
+        got = lin(torch.from_numpy(x)).cpu().numpy()
+        assert _rel(got, ref) < 1e-5
+        got16 = lin.forward(torch.from_numpy(x), out_dtype=torch.float16).cpu().numpy()
+        assert got16.dtype == np.float16
+        assert np.all(np.abs(got16.astype(np.float32) - ref) <= 1e-3 + 1e-2 * np.abs(ref))

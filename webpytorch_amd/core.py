@@ -286,12 +286,14 @@ class QuantizedLinear:
 
 
 # ---- GGUF native ---------------------------------------------------------------------
-_NATIVE_TYPES = {"Q4_K": (256, 144)}
+# (values per block, bytes per block, ggml type id) of the types a native kernel decodes
+_NATIVE_TYPES = {"Q4_K": (256, 144, 12), "Q6_K": (256, 210, 14), "Q8_0": (32, 34, 8)}
 
 
 def ggml_native_supported(type_name):
     """Can this ggml type be multiplied straight from the file's bytes
-    (`webtorch/_core.py:3644-3646`)? Q4_K is; the other ggml types are not built yet."""
+    (`webtorch/_core.py:3644-3646`)? Q4_K, Q6_K and Q8_0 are (the types of a Q4_K_M file);
+    the other ggml types are not built."""
     return type_name in _NATIVE_TYPES
 
 
@@ -303,16 +305,20 @@ def q4k_dequant(blocks, n_blocks):
 
 def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32, out=None):
     """xf (M, K) @ W.T -> (M, N), decoding ggml blocks in the kernel
-    (`webtorch/_core.py:3720-3734`). `packed` is the file's row layout (N rows of K/256
-    super-blocks), uint8 on the GPU."""
-    if type_name != "Q4_K":
+    (`webtorch/_core.py:3720-3734`). `packed` is the file's row layout (N rows of K / block
+    values blocks), uint8 on the GPU."""
+    if type_name not in _NATIVE_TYPES:
         raise NotImplementedError("native ggml type %s" % type_name)
     xf = aligned16(as_activation(xf).contiguous())
     M = int(xf.shape[0])
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=xf.device)
-    _lib.call("miq_q4k_gemv", ptr(xf), dtype_code(xf), ptr(packed), ptr(bias), ptr(out), dtype_code(out),
-              M, int(K), int(N), stream_handle())
+    if type_name == "Q4_K":
+        _lib.call("miq_q4k_gemv", ptr(xf), dtype_code(xf), ptr(packed), ptr(bias), ptr(out), dtype_code(out),
+                  M, int(K), int(N), stream_handle())
+    else:
+        _lib.call("miq_ggml_gemv", ptr(xf), dtype_code(xf), ptr(packed), _NATIVE_TYPES[type_name][2], ptr(bias),
+                  ptr(out), dtype_code(out), M, int(K), int(N), stream_handle())
     return out
 
 
@@ -325,7 +331,7 @@ class GGMLLinear:
     def __init__(self, raw, type_name, K, N, bias=None):
         if type_name not in _NATIVE_TYPES:
             raise NotImplementedError("native ggml type %s" % type_name)
-        vals, blk = _NATIVE_TYPES[type_name]
+        vals, blk, _ = _NATIVE_TYPES[type_name]
         self.type_name = type_name
         self.Kt, self.Nt = int(K), int(N)
         nbytes = self.Nt * (self.Kt // vals) * blk

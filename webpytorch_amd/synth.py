@@ -110,6 +110,29 @@ def q4k_layer(seed, K, N, name="q4k"):
     return q4k_blocks(seed, N * (K // 256), name).reshape(N, (K // 256) * 144)
 
 
+def q8_0_layer(seed, K, N, name="q8_0"):
+    """N rows of K/32 GGUF Q8_0 blocks (34 bytes: fp16 d = |N(0,1)| * 0.01, 32 uniform int8
+    codes), as a (N, K/32 * 34) uint8 array."""
+    g = rng(seed, name)
+    nb = N * (K // 32)
+    b = np.empty((nb, 34), np.uint8)
+    b[:, 0:2] = (np.abs(g.standard_normal(nb)) * 0.01).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    b[:, 2:] = g.integers(0, 256, (nb, 32), dtype=np.uint8)
+    return b.reshape(N, (K // 32) * 34)
+
+
+def q6k_layer(seed, K, N, name="q6k"):
+    """N rows of K/256 GGUF Q6_K super-blocks (210 bytes: uniform ql and qh bytes, 16 int8
+    scales uniform in [-64, 63], fp16 d = |N(0,1)| * 0.001), as a (N, K/256 * 210) uint8 array."""
+    g = rng(seed, name)
+    nb = N * (K // 256)
+    b = np.empty((nb, 210), np.uint8)
+    b[:, 0:192] = g.integers(0, 256, (nb, 192), dtype=np.uint8)
+    b[:, 192:208] = g.integers(-64, 64, (nb, 16)).astype(np.int8).view(np.uint8)
+    b[:, 208:210] = (np.abs(g.standard_normal(nb)) * 0.001).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(N, (K // 256) * 210)
+
+
 def activations(seed, M, K, dtype=np.float16, name="x"):
     return rng(seed, name).standard_normal((M, K)).astype(dtype)
 
