@@ -73,15 +73,29 @@ template <int BITS> __device__ __forceinline__ uint4 pack8_pairs(const float* v)
 }
 
 // ---- wavefront (64 lanes) reductions --------------------------------------------------
+// Within each row of 16 lanes by DPP moves (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror: every lane ends with its row's total), then the four row totals by v_readlane,
+// summed in a fixed order. No LDS round trip (a shuffle across rows is a ds_bpermute each).
+// Call with all 64 lanes active; every lane gets the same result.
+template <int CTRL> __device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_at(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_move<0xB1>(v);
+  v += dpp_move<0x4E>(v);
+  v += dpp_move<0x141>(v);
+  v += dpp_move<0x140>(v);
+  return (lane_at(v, 0) + lane_at(v, 16)) + (lane_at(v, 32) + lane_at(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  v = fmaxf(v, dpp_move<0x140>(v));
+  return fmaxf(fmaxf(lane_at(v, 0), lane_at(v, 16)), fmaxf(lane_at(v, 32), lane_at(v, 48)));
 }
 
 // ---- fp16 pairs: 4-bit codes to exact fp16 without a conversion per value ---------------
