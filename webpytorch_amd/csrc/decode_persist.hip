@@ -200,6 +200,36 @@ __device__ __forceinline__ float rope1(const float* row, int d, int half, float 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
+// (value, index) arg-max over a wave with all 64 lanes active, NaN losing to any number: DPP
+// moves within each row of 16, then the four row winners by v_readlane. The order (larger value,
+// then smaller index) is total, so every lane ends with the same winner whatever the pairing.
+template <int CTRL> __device__ __forceinline__ void amax_step(float& v, int& i) {
+  const float ov = dpp_move<CTRL>(v);
+  const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
+  if (better(ov, oi, v, i) || (v != v && ov == ov)) {
+    v = ov;
+    i = oi;
+  }
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  amax_step<0xB1>(v, i);
+  amax_step<0x4E>(v, i);
+  amax_step<0x141>(v, i);
+  amax_step<0x140>(v, i);
+  float bv = lane_at(v, 0);
+  int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+  for (int r = 16; r < 64; r += 16) {
+    const float ov = lane_at(v, r);
+    const int oi = __builtin_amdgcn_readlane(i, r);
+    if (better(ov, oi, bv, bi) || (bv != bv && ov == ov)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  v = bv;
+  i = bi;
+}
 
 // LDS carve-up: hin (exchange words and scratch), xs (fp32 activations), xa (A operand steps),
 // cx (bias and x sums per step), red (4 quarters x 64 columns), red16 (wave scalars), qkv
@@ -357,8 +387,7 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
         a = fmaf(qp[4 * i + 2], k4[i].z, a);
         a = fmaf(qp[4 * i + 3], k4[i].w, a);
       }
-      a = a + __shfl_xor(a, 1, 64);
-      a = a + __shfl_xor(a, 2, 64);
+      a = quad_sum(a);
       if (qq == 0 && j < S) sp[j] = a * p.scale;
     }
     __syncthreads();
@@ -577,12 +606,7 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
     step(t2, t0, t1, t + 2 * G);
   }
   if (threadIdx.x < 64) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (better(ov, oi, bv, bi) || (bv != bv && ov == ov)) { bv = ov; bi = oi; }
-    }
+    wave_argmax(bv, bi);
     if (threadIdx.x == 0) {
       tput(p.tamax + b, c.tag(p.L, P_AMAX), bv);
       tput(p.tamax + G + b, c.tag(p.L, P_AMAX), __int_as_float(bi));
@@ -607,12 +631,7 @@ MIQ_PD_INLINE bool finish_token(const Params& p, const Ctx& c, const Lds& s, int
       const int i = __float_as_int(s.hin[G + gi]);
       if (better(v, i, fv, fi) || (fv != fv && v == v)) { fv = v; fi = i; }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(fv, o, 64);
-      const int oi = __shfl_xor(fi, o, 64);
-      if (better(ov, oi, fv, fi) || (fv != fv && ov == ov)) { fv = ov; fi = oi; }
-    }
+    wave_argmax(fv, fi);
     if (threadIdx.x == 0) {
       if (fi >= p.V) fi = 0;  // all logits NaN
       p.ids[0] = fi;

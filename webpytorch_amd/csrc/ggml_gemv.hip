@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void ggml_gemv_kernel(const XT* __restrict__ x
     if constexpr (VPL == 8) {
       xg[i] = sum;
     } else {
-      sum += __shfl_xor(sum, 1, 64);  // i and i ^ 1 are neighbouring lanes (K / 8 is even)
+      sum += dpp_move<0xB1>(sum);  // i and i ^ 1 are neighbouring lanes (K / 8 is even)
       if ((i & 1) == 0) xg[i >> 1] = sum;
     }
   }

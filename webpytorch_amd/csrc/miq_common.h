@@ -83,6 +83,11 @@ template <int CTRL> __device__ __forceinline__ float dpp_move(float v) {
 __device__ __forceinline__ float lane_at(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
+// Sum over each quad of 4 consecutive lanes (all four active): the pairing of xor 1 then xor 2.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp_move<0xB1>(v);
+  return v + dpp_move<0x4E>(v);
+}
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_move<0xB1>(v);
   v += dpp_move<0x4E>(v);

@@ -234,10 +234,8 @@ __device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned cha
   *reinterpret_cast<bf16x8*>(dst + 32) = t3;
   const float lo = (v[0] + v[2]) + (v[4] + v[6]), hi = (v[1] + v[3]) + (v[5] + v[7]);
   float cb = 128.f * lo + 16.f * hi, sm = lo + hi;
-  cb += __shfl_xor(cb, 1, 64);
-  cb += __shfl_xor(cb, 2, 64);
-  sm += __shfl_xor(sm, 1, 64);
-  sm += __shfl_xor(sm, 2, 64);
+  cb = quad_sum(cb);
+  sm = quad_sum(sm);
   if ((ch & 3) == 0) cx[ch >> 2] = make_float2(cb, sm);
 }
 

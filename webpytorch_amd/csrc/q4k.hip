@@ -129,8 +129,7 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
       for (int j = 0; j < 8; ++j) v[j] = 0.f;
     }
     float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
+    sum = quad_sum(sum);
     if ((lane & 3) == 0) xsum[m * (K / 32) + k / 32] = sum;
     if constexpr (kHalf) {
       // activations c0..c0+7 of a 64-wide group land in code words wq and wq+1 (wq = (c0 % 32) / 4)
