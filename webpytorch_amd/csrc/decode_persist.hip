@@ -124,7 +124,20 @@ __device__ bool wait_tagged(int n, const Ctx& c, const uint64_t* base, F off, T 
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  return !__syncthreads_or(late);
+  // late is wave-uniform (a vote and the scalar clock decide it): one flag per wave and one
+  // barrier (__syncthreads_or costs three). Every caller passes another barrier before its next
+  // wait, so no wave rewrites its flag while another still reads it.
+  __shared__ __align__(16) int wt_late[kWaves];
+  if ((threadIdx.x & 63) == 0) wt_late[threadIdx.x >> 6] = late ? 1 : 0;
+  __syncthreads();
+  const int4* f = reinterpret_cast<const int4*>(wt_late);
+  int any = 0;
+#pragma unroll
+  for (int q = 0; q < kWaves / 4; ++q) {
+    const int4 t = f[q];
+    any |= t.x | t.y | t.z | t.w;
+  }
+  return any == 0;
 }
 
 // Sum over the workgroup, combined in wave order (every thread gets the total).
