@@ -275,7 +275,9 @@ int miq_argmax_advance(const float* logits, int V, int32_t* ids, int32_t* histor
  * fp16 [V][H]. logits [V] receives the head output. ws: 256-byte aligned, zeroed before the
  * first step and again after any error; uint32 word 0 counts finished steps and word 1 holds
  * error bits (1: a workgroup waited more than 100 ms -- not all workgroups were resident --
- * 2: state[0] >= LMAX), read by the caller after the step. Steps on one workspace must not
+ * 2: state[0] >= LMAX), read by the caller after the step. The environment variable
+ * MIQ_PD_SPIN_TICKS (wall-clock ticks, read at each call) shortens the 100 ms bound, so that
+ * tests can drive the timeout path; after such a step the workspace must be zeroed again. Steps on one workspace must not
  * overlap, and the step must not share the GPU with other kernels. */
 int miq_decode_persistent_plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs,
                                int bits, int* grid, size_t* ws_bytes);

@@ -274,6 +274,27 @@ def test_persistent_step_matches_launch_sequence(gpu, prompt, steps, lmax):
         np.testing.assert_allclose(ga, gb, rtol=1e-4, atol=1e-4 * np.abs(gb).max())
 
 
+def test_persistent_step_wait_timeout_drains(gpu, monkeypatch):
+    """A spin bound of one wall-clock tick makes every waiting workgroup give up: the step ends
+    (the grid drains), reports error bit 1 and leaves the decode state alone; after reset() the
+    same model decodes the launch sequence's ids."""
+    import torch
+    sh = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+    a, b, ids = _persistent_pair(sh, 14, 64, 16)
+    want = b.generate(ids, 8).tokens
+    a.generate(ids, 1, use_graph=False)
+    state = a.state.clone()
+    monkeypatch.setenv("MIQ_PD_SPIN_TICKS", "1")
+    a._step(1)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("MIQ_PD_SPIN_TICKS")
+    assert a.persistent_error() & 1
+    assert torch.equal(a.state[:4], state[:4])
+    a.reset()
+    assert a.persistent_error() == 0
+    assert a.generate(ids, 8, use_graph=False).tokens == want
+
+
 def test_persistent_step_graph_replay_and_position_guard(gpu):
     """Graph-replayed persistent steps give the eager ids; a step at position LMAX does no work
     and reports error bit 2 (every workgroup leaves at entry), and reset() clears it."""

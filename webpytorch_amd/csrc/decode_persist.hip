@@ -26,6 +26,8 @@
 // [1] error bits (1: wait timed out, 2: position past the cache).
 #include <math.h>
 
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "miq_common.h"
@@ -860,6 +862,10 @@ extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* em
   p.zoff = zoff;
   p.head_zoff = head_zoff;
   p.spin_limit = (long long)khz * 100;  // 100 ms
+  if (const char* e = getenv("MIQ_PD_SPIN_TICKS")) {  // a shorter bound, for tests of the error path
+    const long long t = atoll(e);
+    if (t > 0 && t < p.spin_limit) p.spin_limit = t;
+  }
   hipLaunchKernelGGL(kfn, dim3(pl.G), dim3(pd::kThreads), pl.lds_bytes,
                      static_cast<hipStream_t>(stream), p);
   return check_launch("decode_persistent");
