@@ -127,8 +127,9 @@ __device__ bool wait_tagged(int n, const Ctx& c, const uint64_t* base, F off, T 
     __builtin_amdgcn_s_sleep(1);
   }
   // late is wave-uniform (a vote and the scalar clock decide it): one flag per wave and one
-  // barrier (__syncthreads_or costs three). Every caller passes another barrier before its next
-  // wait, so no wave rewrites its flag while another still reads it.
+  // barrier (__syncthreads_or costs three). The flags are per instantiation, i.e. per call site
+  // (each passes its own lambdas), and every call site passes another barrier before it waits
+  // again, so no wave rewrites a flag while another still reads it.
   __shared__ __align__(16) int wt_late[kWaves];
   if ((threadIdx.x & 63) == 0) wt_late[threadIdx.x >> 6] = late ? 1 : 0;
   __syncthreads();
@@ -264,10 +265,13 @@ struct Lds {
 MIQ_PD_INLINE bool gather_h(const Params& p, const Ctx& c, int l, int tok, float* raw, float* v) {
   const int H = p.H, ks = p.ksd, ch = threadIdx.x;
   if (l > 0) {
+    // the ks down slices and hmid are consecutive H-word rows; hmid (written a whole step
+    // earlier) is waited for on its own, so the rounds that wait for the slices carry only them
     const uint32_t td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
-    if (!wait_tagged<8>(  // the ks down slices and hmid are consecutive H-word rows
-            (ks + 1) * H, c, p.tdown, [&](int j) { return j; }, [=](int j) { return j < ks * H ? td : th; }, raw))
+    if (!wait_tagged<8>(
+            H, c, p.tdown + (size_t)ks * H, [&](int j) { return j; }, [=](int) { return th; }, raw + ks * H))
       return false;
+    if (!wait_tagged<8>(ks * H, c, p.tdown, [&](int j) { return j; }, [=](int) { return td; }, raw)) return false;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = 0.f;
