@@ -411,7 +411,7 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
     }
     __syncthreads();
     PD_MARK(l, 3);
-    if (wave == 0) {  // softmax in one wave: reductions by shuffles, one barrier after it
+    if (wave == 0) {  // softmax in one wave: DPP reductions, one barrier after it
       float mx = -INFINITY;
       for (int j = lane; j < S; j += 64) mx = fmaxf(mx, sp[j]);
       mx = wave_max(mx);
@@ -422,7 +422,7 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
         sum += e;
       }
       sum = wave_sum(sum);
-      for (int j = lane; j < S; j += 64) sp[j] = sp[j] / sum;
+      if (lane == 0) s.red16[16] = sum;  // the division waits until the weighted sum
     }
     __syncthreads();
     PD_MARK(l, 4);
@@ -437,15 +437,15 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
         }
       }
     }
-    // 16 waves' partial sums, combined in wave order (over the scores, once all are read)
-    __syncthreads();
-    s.hin[wave * 64 + lane] = o;
+    // 16 waves' partial sums (in red, which the attention does not otherwise use), combined in
+    // wave order, then divided by the softmax denominator
+    s.red[wave * 64 + lane] = o;
     __syncthreads();
     if (tid < 64) {
       float y = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) y += s.hin[w * 64 + tid];
-      tput(p.tatt + hq * 64 + tid, c.tag(l, P_ATT), y);
+      for (int w = 0; w < kWaves; ++w) y += s.red[w * 64 + tid];
+      tput(p.tatt + hq * 64 + tid, c.tag(l, P_ATT), y / s.red16[16]);
     }
     PD_MARK(l, 2);
     __syncthreads();
