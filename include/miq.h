@@ -62,11 +62,16 @@ int miq_gptq_dequant_f32(const int32_t* qweight, const int32_t* qzeros, const vo
 int miq_gptq_repack_rows(const int32_t* qweight, const int32_t* perm, int32_t* out, int K, int N,
                          int bits, void* stream);
 
-/* Bytes of workspace miq_gptq_gemv needs for this problem (0 if none). The first 2 MiB of a
- * workspace (the counter region) hold arrival counters and fixed-point split-K sums, shared by
- * every split-K entry point, that must be zero before the first call on it; every call leaves
- * them zero again. Partial sums and staged activations follow them. One workspace must not
- * serve two calls that run concurrently. */
+/* Bytes of workspace miq_gptq_gemv needs for this problem (0 if none). The first 4 MiB of a
+ * workspace (the counter region) hold arrival counters, fixed-point split-K sums and their
+ * escape masks, shared by every split-K entry point, that must be zero before the first call
+ * on it; every call leaves them zero again. Partial sums, escape slots and staged activations
+ * follow them. One workspace must not serve two calls that run concurrently.
+ * Split-K sums are exact for every input: a K-slice partial that is NaN, infinite or of
+ * magnitude >= 2^22 (beyond the fixed-point words) reaches the final sum as an fp32 value, so
+ * NaN and infinities propagate as in an fp32 sum. (The one-row int4 kernel computes with exact
+ * bf16 splits of x against biased codes, in which an infinite activation meets itself with the
+ * opposite sign: an infinite x gives NaN, not +-Inf, in the outputs it reaches.) */
 int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, int x_dtype, size_t* bytes);
 
 /* Decode GEMV / skinny GEMM: out[M][N] = x[M][K] (gathered through perm if non-NULL)
@@ -155,6 +160,12 @@ int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const float* bias
  * 3071-3077, 3158-3176). */
 int miq_ggml_gemv(const void* x, int x_dtype, const uint8_t* w, int ggml_type, const float* bias,
                   void* out, int out_dtype, int M, int K, int N, void* stream);
+
+/* Dequant n_blocks blocks of ggml_type 12 (Q4_K), 8 (Q8_0) or 14 (Q6_K) to fp32 (256, 32 or
+ * 256 values each), bit-exact (every product is exact in fp32). blocks 2-byte aligned (16 for
+ * Q4_K). Other types: MIQ_ERR_UNSUPPORTED.
+ * Replaces: `ggufload.dequant` for Q4_K, Q8_0 and Q6_K (webtorch/ggufload.py:133-145, 188-222). */
+int miq_ggml_dequant_f32(const uint8_t* blocks, int ggml_type, float* out, int64_t n_blocks, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Sparse MoE MLP (router + experts), all on the device

@@ -33,8 +33,9 @@ def test_prefill_gemm_config2(gpu, M, act):
     ref = gptq.linear_forward(x, L, zoff=1.0, g_idx=L["g_idx"] if act else None)
     _check(got, ref)
     # fp16 output rounds the same sums once
-    y16 = ql(torch.from_numpy(x))
+    y16 = ql.forward(torch.from_numpy(x), out_dtype=torch.float16)
     assert y16.dtype == torch.float16
+    assert ql(torch.from_numpy(x)).dtype == torch.float32  # the reference's forward returns fp32
     _check(y16.float().cpu().numpy(), ref, rel=2e-3)
 
 

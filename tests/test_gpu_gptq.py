@@ -91,7 +91,7 @@ def test_config0_gemv_fp16(gpu):
     L = synth.gptq_layer(0, 896, 4864, 128, 4)
     x = synth.activations(0, 1, 896, np.float16)
     ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 128, 4)
-    y = ql(torch.from_numpy(x))
+    y = ql.forward(torch.from_numpy(x), out_dtype=torch.float16)
     assert y.dtype == torch.float16 and tuple(y.shape) == (1, 4864)
     ref = gptq.gptq_matmul_np(x, L["qweight"], L["qzeros"], L["scales"], 896, 4864, 128, 4, 1.0)
     _close(y.float().cpu().numpy(), ref)

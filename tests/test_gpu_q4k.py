@@ -109,3 +109,40 @@ def test_q8_0_q6k_ragged_rows_bias_dtypes(gpu, type_name, K, N):
         got16 = lin.forward(torch.from_numpy(x), out_dtype=torch.float16).cpu().numpy()
         assert got16.dtype == np.float16
         assert np.all(np.abs(got16.astype(np.float32) - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+
+
+@pytest.mark.parametrize("type_name,K,N", [("Q8_0", 96, 33), ("Q6_K", 768, 33), ("Q4_K", 768, 33)])
+def test_dequantize_every_native_type_bit_exact(gpu, type_name, K, N):
+    """GGMLLinear.dequantize decodes the layer's own type (the reference's `ggufload.dequant`),
+    including rows at 2-byte offsets."""
+    from oracle import ggml
+    from webpytorch_amd import core
+    W = {"Q8_0": synth.q8_0_layer, "Q6_K": synth.q6k_layer, "Q4_K": synth.q4k_layer}[type_name](7, K, N)
+    got = core.GGMLLinear(W, type_name, K, N).dequantize().cpu().numpy()
+    if type_name == "Q4_K":
+        ref = q4k.q4k_dequant(W.reshape(-1), N * K).reshape(N, K)
+    else:
+        ref = ggml.DEQUANT[type_name][0](W.reshape(-1), N * K).reshape(N, K)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_name,K,N", [("Q4_K", 1024, 40), ("Q6_K", 512, 33), ("Q8_0", 128, 17)])
+def test_ggml_matmul_accepts_the_reference_transposed_layout(gpu, type_name, K, N):
+    """`ggml_matmul` given the reference's (word, row) u32 layout (`ggml_transpose`,
+    `webtorch/_core.py:4315-4344`: word w of row r at w * N + r, the row's tail bytes
+    zero-padded to a word) gives the same result as the native rows."""
+    import torch
+    from webpytorch_amd import core
+    W = {"Q8_0": synth.q8_0_layer, "Q6_K": synth.q6k_layer, "Q4_K": synth.q4k_layer}[type_name](9, K, N)
+    rows = np.asarray(W, np.uint8).reshape(N, -1)
+    rowb = rows.shape[1]
+    nw = (rowb + 3) // 4
+    padded = np.zeros((N, nw * 4), np.uint8)
+    padded[:, :rowb] = rows
+    transposed = np.ascontiguousarray(padded.view(np.uint32).reshape(N, nw).T).reshape(-1)
+    x = torch.from_numpy(synth.activations(9, 2, K, np.float32)).cuda()
+    a = core.ggml_matmul(x, core.ggml_transpose(rows, N, rowb), type_name, K, N).cpu().numpy()
+    b = core.ggml_matmul(x, torch.from_numpy(transposed.view(np.int32)).cuda(), type_name, K, N).cpu().numpy()
+    assert np.array_equal(a, b)
+    with pytest.raises(ValueError):
+        core.ggml_matmul(x, torch.from_numpy(transposed.view(np.int32)[:-1]).cuda(), type_name, K, N)

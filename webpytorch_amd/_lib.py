@@ -45,6 +45,7 @@ SIGNATURES = {
     "miq_decode_persistent": [_p] * 10 + [_i, _p, _p, _p, _sz] + [_i] * 10 + [_f] * 3 + [_p],
     "miq_q4k_gemv": [_p, _i, _p, _p, _p, _i, _i, _i, _i, _p],
     "miq_ggml_gemv": [_p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _p],
+    "miq_ggml_dequant_f32": [_p, _i, _p, _i64, _p],
 }
 
 _lib = None

@@ -69,7 +69,7 @@ def as_activation(x):
 
 
 _WORKSPACE = {}
-_RETIRED = []
+_RETIRED = {}
 _WS_BYTES = {}
 
 
@@ -96,19 +96,23 @@ def gemm_workspace_bytes(M, K, N, gs, bits):
 
 
 def workspace(nbytes):
-    """The current device's GEMV workspace, grown on demand and zeroed when allocated (the
-    kernels leave its arrival counters zero). Calls that share it must not run concurrently:
-    calls issued on one stream are ordered, which is how every operator here uses it."""
+    """The split-K workspace of the current (device, stream), grown on demand and zeroed when
+    allocated (the kernels leave its counter region zero). One workspace per stream: calls on
+    one stream are ordered, so they never share it concurrently, and calls on two streams get
+    two workspaces. A grown workspace keeps the old one alive (a captured graph may still point
+    at it); growth at least doubles, so a stream retires O(log size) buffers."""
     if nbytes == 0:
         return None
     dev = torch.cuda.current_device()
-    t = _WORKSPACE.get(dev)
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    t = _WORKSPACE.get(key)
     if t is None or t.numel() < nbytes:
+        size = max(nbytes, 8 << 20)
         if t is not None:
-            # a captured graph may still point at the old buffer: keep it alive
-            _RETIRED.append(t)
-        t = torch.zeros(max(nbytes, 4 << 20), dtype=torch.uint8, device=device())
-        _WORKSPACE[dev] = t
+            _RETIRED.setdefault(key, []).append(t)
+            size = max(size, 2 * t.numel())
+        t = torch.zeros(size, dtype=torch.uint8, device=device())
+        _WORKSPACE[key] = t
     return t
 
 
@@ -138,7 +142,7 @@ def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=
     of fp16 activations run the matrix-core GEMM (fp32 activations stay on the GEMV, which
     keeps them in fp32)."""
     M = int(xf.shape[0])
-    od = out_dtype or xf.dtype
+    od = out_dtype or torch.float32
     if out is None:
         out = torch.empty((M, N), dtype=od, device=xf.device)
     if M == 0:
@@ -253,7 +257,10 @@ class QuantizedLinear:
         qw, qz, sc, _, _ = gptq_quantize(W, group_size, bits)
         return QuantizedLinear(qw, qz, sc, b, K, N, Kp, Np, group_size, bits)
 
-    def forward(self, x, out_dtype=None):
+    def forward(self, x, out_dtype=torch.float32):
+        """x (..., Kt) -> (..., Nt), float32 like the reference's `forward` (its
+        `_gptq_matmul` accumulates and returns fp32); `out_dtype=torch.float16` writes fp16
+        from the kernel instead."""
         xt = as_activation(x)
         lead = xt.shape[:-1]
         xf = xt.reshape(-1, self.Kt)
@@ -303,12 +310,71 @@ def q4k_dequant(blocks, n_blocks):
     return out
 
 
-def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32, out=None):
-    """xf (M, K) @ W.T -> (M, N), decoding ggml blocks in the kernel
-    (`webtorch/_core.py:3720-3734`). `packed` is the file's row layout (N rows of K / block
-    values blocks), uint8 on the GPU."""
+def ggml_dequant(blocks, type_name, n_blocks):
+    """fp32 values of n_blocks blocks of a native type, bit-exact with `ggufload.dequant`
+    (`webtorch/ggufload.py:133-222`)."""
     if type_name not in _NATIVE_TYPES:
         raise NotImplementedError("native ggml type %s" % type_name)
+    vals, _, tid = _NATIVE_TYPES[type_name]
+    out = torch.empty(int(n_blocks) * vals, dtype=torch.float32, device=blocks.device)
+    _lib.call("miq_ggml_dequant_f32", ptr(blocks), tid, ptr(out), int(n_blocks), stream_handle())
+    return out
+
+
+def _row_bytes(type_name, K):
+    vals, blk, _ = _NATIVE_TYPES[type_name]
+    if K % vals:
+        raise ValueError("K=%d is not a multiple of the %s block (%d values)" % (K, type_name, vals))
+    return K // vals * blk
+
+
+def ggml_transpose(src, n, rowb):
+    """Load-time layout step, same name and arguments as the reference's (`(n, rowb bytes)` in,
+    `webtorch/_core.py:4315-4344`), returning the layout the kernels here read: the n rows of
+    rowb bytes unchanged, as a uint8 (n, rowb) device tensor. The reference transposes to
+    (word, row) u32 so that WebGPU threads read adjacent words; on MI355X a wave's 16-byte loads
+    of the native rows already coalesce, so the bytes stay as the file holds them."""
+    t = src if isinstance(src, torch.Tensor) else torch.from_numpy(
+        np.frombuffer(bytearray(src), np.uint8) if isinstance(src, (bytes, bytearray))
+        else np.ascontiguousarray(src).reshape(-1).view(np.uint8))
+    b = t.reshape(-1).view(torch.uint8)
+    if b.numel() < n * rowb:
+        raise ValueError("%d bytes given, (%d, %d) needs %d" % (b.numel(), n, rowb, n * rowb))
+    return b[:n * rowb].to(device()).contiguous().reshape(n, rowb)
+
+
+def rows_from_transposed(words, n, rowb):
+    """The reference's (word, row) u32 layout (`ggml_transpose` output: word w of row r at
+    index w * n + r) back to n rows of rowb bytes, on the device."""
+    nw = (rowb + 3) // 4
+    w = words.reshape(-1)
+    if w.numel() != nw * n:
+        raise ValueError("transposed layout holds %d words, (%d rows x %d words) expected" % (w.numel(), n, nw))
+    rows = w.view(torch.int32).reshape(nw, n).t().contiguous().view(torch.uint8).reshape(n, nw * 4)
+    return rows[:, :rowb].contiguous()
+
+
+def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32, out=None):
+    """xf (M, K) @ W.T -> (M, N), decoding ggml blocks in the kernel
+    (`webtorch/_core.py:3720-3734`).
+
+    `packed` is either the layout `ggml_transpose` here returns (uint8 bytes: N rows of
+    K / block-values blocks, as the file stores them) or the reference's own transposed
+    (word, row) layout as int32/uint32 words, which is converted to rows on the device on every
+    call (a copy of the weight: build a `GGMLLinear`, or pass rows, to avoid it). The dtype
+    tells the two apart: bytes are rows, 32-bit words are the reference's transposed layout."""
+    if type_name not in _NATIVE_TYPES:
+        raise NotImplementedError("native ggml type %s" % type_name)
+    rowb = _row_bytes(type_name, int(K))
+    if not isinstance(packed, torch.Tensor):
+        packed = to_device(packed)
+    if packed.dtype in (torch.int32, torch.uint32):
+        packed = rows_from_transposed(packed.to(device()), int(N), rowb)
+    elif packed.dtype != torch.uint8:
+        raise TypeError("packed must be uint8 rows or int32 transposed words, got %s" % packed.dtype)
+    elif packed.numel() != int(N) * rowb:
+        raise ValueError("packed holds %d bytes, %s (%d x %d) needs %d" % (packed.numel(), type_name, N, K,
+                                                                           int(N) * rowb))
     xf = aligned16(as_activation(xf).contiguous())
     M = int(xf.shape[0])
     if out is None:
@@ -331,18 +397,9 @@ class GGMLLinear:
     def __init__(self, raw, type_name, K, N, bias=None):
         if type_name not in _NATIVE_TYPES:
             raise NotImplementedError("native ggml type %s" % type_name)
-        vals, blk, _ = _NATIVE_TYPES[type_name]
         self.type_name = type_name
         self.Kt, self.Nt = int(K), int(N)
-        nbytes = self.Nt * (self.Kt // vals) * blk
-        if isinstance(raw, torch.Tensor):
-            b = raw.reshape(-1).view(torch.uint8)
-        else:
-            b = torch.from_numpy(np.frombuffer(bytearray(raw), np.uint8) if isinstance(raw, (bytes, bytearray))
-                                 else np.ascontiguousarray(raw).reshape(-1).view(np.uint8))
-        if b.numel() < nbytes:
-            raise ValueError("raw holds %d bytes, %s (%d x %d) needs %d" % (b.numel(), type_name, N, K, nbytes))
-        self.packed = b[:nbytes].to(device()).contiguous().reshape(self.Nt, -1)
+        self.packed = ggml_transpose(raw, self.Nt, _row_bytes(type_name, self.Kt))
         self.bias = None if bias is None else to_device(np.asarray(bias, np.float32))
 
     def forward(self, x, out_dtype=torch.float32):
@@ -355,9 +412,9 @@ class GGMLLinear:
     __call__ = forward
 
     def dequantize(self):
-        """fp32 (N, K) weight."""
-        nb = self.Nt * (self.Kt // 256)
-        return q4k_dequant(self.packed, nb).reshape(self.Nt, self.Kt)
+        """fp32 (N, K) weight, bit-exact with `ggufload.dequant` of the same bytes."""
+        nb = self.Nt * (self.Kt // _NATIVE_TYPES[self.type_name][0])
+        return ggml_dequant(self.packed, self.type_name, nb).reshape(self.Nt, self.Kt)
 
     def nbytes(self):
         return int(self.packed.numel() + (0 if self.bias is None else self.bias.numel() * 4))

@@ -58,8 +58,9 @@ __global__ __launch_bounds__(NWV * 64) void gemm_small_kernel(const __half* __re
                                                               const uint32_t* __restrict__ qz,
                                                               const ST* __restrict__ sc,
                                                               const float* __restrict__ bias, OT* __restrict__ out,
-                                                              unsigned long long* __restrict__ fixacc, int M, int K,
-                                                              int N, float zoff) {
+                                                              unsigned long long* __restrict__ fixacc,
+                                                              float* __restrict__ side, int M, int K, int N,
+                                                              float zoff) {
   using SV = typename Scales4<ST>::T;
   constexpr int NT = NWV * 64;         // threads
   constexpr int NG = SPQ / 4;          // groups per wave
@@ -181,20 +182,22 @@ __global__ __launch_bounds__(NWV * 64) void gemm_small_kernel(const __half* __re
   }
   // every atomic first, then the checks: the round trips overlap. The words of a tile are laid
   // out [v][lane], so one atomic instruction covers 512 contiguous bytes.
-  unsigned long long* wt = fixacc + (size_t)tile * NV * 64 + lane;
+  const size_t w0 = (size_t)tile * NV * 64 + lane, nwords = (size_t)gridDim.x * NV * 64;
   unsigned long long add[NW], old[NW];
 #pragma unroll
   for (int u = 0; u < NW; ++u) {
     const int v = wave * NW + u, m = row_of(v), n = col_of(v);
     add[u] = fix_word(ys[u]);
     old[u] = 0;
-    if (m < M && n < N) old[u] = fix_issue(wt + v * 64, add[u]);
+    if (m < M && n < N)
+      old[u] = fix_issue(fixacc + w0 + v * 64, add[u], ys[u], fix_esc(fixacc, w0 + v * 64, side, nwords), sl);
   }
 #pragma unroll
   for (int u = 0; u < NW; ++u) {
     const int v = wave * NW + u, m = row_of(v), n = col_of(v);
     float r;
-    if (m < M && n < N && fix_finish(wt + v * 64, old[u], add[u], kslices, &r))
+    if (m < M && n < N &&
+        fix_finish(fixacc + w0 + v * 64, old[u], add[u], kslices, fix_esc(fixacc, w0 + v * 64, side, nwords), &r))
       out[(size_t)m * N + n] = from_f32<OT>(bias ? r + bias[n] : r);
   }
 }
@@ -229,20 +232,20 @@ static bool plan(int M, int K, int N, Plan* p) {
   }
   p->kslices = (steps + 4 * p->spq - 1) / (4 * p->spq);
   if (p->kslices > kFixMaxSlices) return false;
-  if (p->kslices > 1 && (size_t)p->tiles * 16 * 64 > kCounterBytes / 8) return false;
+  if (p->kslices > 1 && (size_t)p->tiles * 16 * 64 > kFixMaxWords) return false;
   return true;
 }
 
 template <int NWV, int SPQ, bool XP>
 static void launch3(const Plan& pl, const __half* x, const int32_t* qw, const int32_t* qz, const void* sc, int sd,
-                    const float* bias, void* out, int od, unsigned long long* fixacc, int M, int K, int N, float zoff,
-                    hipStream_t st) {
+                    const float* bias, void* out, int od, unsigned long long* fixacc, float* side, int M, int K, int N,
+                    float zoff, hipStream_t st) {
   const dim3 grid(pl.tiles, pl.kslices);
   const uint32_t* w = reinterpret_cast<const uint32_t*>(qw);
   const uint32_t* z = reinterpret_cast<const uint32_t*>(qz);
 #define MIQ_GS_LAUNCH(ST, OT)                                                                                      \
   hipLaunchKernelGGL((gemm_small_kernel<NWV, SPQ, XP, ST, OT>), grid, dim3(NWV * 64), 0, st, x, w, z,            \
-                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), fixacc, M, K, N, zoff)
+                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), fixacc, side, M, K, N, zoff)
   if (sd == MIQ_F16) {
     if (od == MIQ_F16) MIQ_GS_LAUNCH(__half, __half);
     else MIQ_GS_LAUNCH(__half, float);
@@ -255,13 +258,18 @@ static void launch3(const Plan& pl, const __half* x, const int32_t* qw, const in
 
 }  // namespace gs
 
-// Bytes of workspace gemm_small needs (0: none; SIZE_MAX: the shape is not covered). With perm
-// the gathered copy of x follows the counter region.
+// Bytes of the gathered copy of x (act-order) that follows the counter region.
+static size_t xg_bytes(int M, int K) { return ((size_t)M * K * 2 + 255) & ~(size_t)255; }
+
+// Bytes of workspace gemm_small needs (0: none; SIZE_MAX: the shape is not covered): the counter
+// region, with perm the gathered copy of x, and with several K-slices the escape slots of the
+// fixed-point words ([kslices][words] floats).
 size_t gemm_small_workspace(int M, int K, int N, int gs_, int bits, bool perm) {
   gs::Plan pl;
   if (bits != 4 || gs_ != 128 || !gs::plan(M, K, N, &pl)) return SIZE_MAX;
-  if (!perm) return pl.kslices > 1 ? kCounterBytes : 0;
-  return kCounterBytes + (((size_t)M * K * 2 + 255) & ~(size_t)255);
+  const size_t esc = pl.kslices > 1 ? (size_t)pl.kslices * pl.tiles * 16 * 64 * 4 : 0;
+  if (!perm) return pl.kslices > 1 ? kCounterBytes + esc : 0;
+  return kCounterBytes + xg_bytes(M, K) + esc;
 }
 
 // Launches the few-row product when it covers the shape; MIQ_ERR_UNSUPPORTED (before launching
@@ -273,13 +281,17 @@ int gemm_small(const __half* x, const __half* xg, const int32_t* qw, const int32
   if (bits != 4 || gs_ != 128 || !gs::plan(M, K, N, &pl) || !aligned(qw, 16) || !aligned(sc, 16) ||
       !aligned(x, 16))
     return MIQ_ERR_UNSUPPORTED;
-  if (pl.kslices > 1 && (!ws || ws_bytes < kCounterBytes)) return MIQ_ERR_UNSUPPORTED;
+  if (pl.kslices > 1 && (!ws || ws_bytes < gemm_small_workspace(M, K, N, gs_, bits, xg != nullptr)))
+    return MIQ_ERR_UNSUPPORTED;
   unsigned long long* fixacc = pl.kslices > 1 ? static_cast<unsigned long long*>(ws) : nullptr;
+  float* side = pl.kslices > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes +
+                                                          (xg ? xg_bytes(M, K) : 0))
+                               : nullptr;
   const __half* src = xg ? xg : x;
 #define MIQ_GS_CASE(NWV, SPQ)                                                                                      \
   if (pl.nwv == NWV && pl.spq == SPQ) {                                                                            \
-    if (xg) gs::launch3<NWV, SPQ, true>(pl, src, qw, qz, sc, sd, bias, out, od, fixacc, M, K, N, zoff, st);       \
-    else gs::launch3<NWV, SPQ, false>(pl, src, qw, qz, sc, sd, bias, out, od, fixacc, M, K, N, zoff, st);         \
+    if (xg) gs::launch3<NWV, SPQ, true>(pl, src, qw, qz, sc, sd, bias, out, od, fixacc, side, M, K, N, zoff, st); \
+    else gs::launch3<NWV, SPQ, false>(pl, src, qw, qz, sc, sd, bias, out, od, fixacc, side, M, K, N, zoff, st);   \
     return check_launch("gemm_small");                                                                             \
   }
   MIQ_GS_CASE(4, 16) MIQ_GS_CASE(4, 8) MIQ_GS_CASE(4, 4) MIQ_GS_CASE(16, 8) MIQ_GS_CASE(16, 4)

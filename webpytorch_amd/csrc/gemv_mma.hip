@@ -14,7 +14,8 @@
 // the top bits, by one agent-scope atomic whose return value tells the last slice that it is
 // last and holds the whole sum; that slice writes y (+ bias) and re-zeroes the word. Integer
 // sums do not depend on the order of arrival, so results are deterministic, and the reduction
-// costs one round trip to the coherence point. Layers with more columns than the counter region
+// costs one round trip to the coherence point. Partials the fixed point cannot hold (NaN, Inf,
+// |p| >= 2^22) reach the last slice exactly through escape slots (mma_tile.h). Layers with more columns than the counter region
 // has words use fp32 partials and a per-tile arrival counter instead (three round trips). Several
 // workgroups per CU keep ~50-100 KB of weights in flight per CU.
 #include <algorithm>
@@ -29,7 +30,7 @@ using namespace mt;
 
 constexpr int kThreadsG = 256;
 constexpr int kMaxSlices = kFixMaxSlices;
-constexpr size_t kMaxFixCols = kCounterBytes / 8;
+constexpr size_t kMaxFixCols = kFixMaxWords;
 
 // Groups of 128 values (4 steps of 32). A 256-thread workgroup covers 256 columns; wave w takes
 // the 64 columns [64 w, 64 w + 64) and every step of the workgroup's K-slice. Lane l loads 16
@@ -151,7 +152,8 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
     const float p = t == 0 ? a0 : t == 1 ? a1 : t == 2 ? a2 : a3;
     const int n = tile * 256 + wave * 64 + (lane & 15) * 4 + t;
     float y;
-    if (n < N && fix_add(fixacc + n, p, kslices, &y)) out[n] = from_f32<OT>(bias ? y + bias[n] : y);
+    if (n < N && fix_add(fixacc + n, p, kslices, sl, fix_esc(fixacc, n, partials, N), &y))
+      out[n] = from_f32<OT>(bias ? y + bias[n] : y);
     return;
   }
   // split K: partials at device scope, the last workgroup of the tile sums them in slice order
@@ -203,7 +205,9 @@ static bool plan(int K, int N, Plan* p) {
   if (p->kslices > kMaxSlices || (p->kslices > 1 && p->tiles > kMaxCounters)) return false;
   p->spq = ss <= 4 ? 4 : ss <= 8 ? 8 : ss <= 12 ? 12 : 16;
   p->fixed = p->kslices > 1 && (size_t)N <= kMaxFixCols;
-  p->ws_bytes = p->kslices == 1 ? 0 : p->fixed ? kCounterBytes : kCounterBytes + (size_t)p->kslices * N * 4;
+  // after the counter region: fp32 partials [kslices][N] (slow path) or the fixed-point
+  // words' escape slots, same shape
+  p->ws_bytes = p->kslices == 1 ? 0 : kCounterBytes + (size_t)p->kslices * N * 4;
   return true;
 }
 
@@ -212,7 +216,7 @@ static int launch(const Plan& pl, const void* x, const int32_t* perm, const int3
                   const void* sc, const float* bias, void* out, void* ws, int K, int N, float zoff, hipStream_t st) {
   const bool slow = pl.kslices > 1 && !pl.fixed;
   int* counters = slow ? static_cast<int*>(ws) : nullptr;
-  float* partials = slow ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
+  float* partials = pl.kslices > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
   unsigned long long* fixacc = pl.fixed ? static_cast<unsigned long long*>(ws) : nullptr;
   dim3 grid(pl.tiles, pl.kslices);
 #define MIQ_GM_LAUNCH(S, P)                                                                                        \

@@ -213,10 +213,50 @@ static int types(const void* x, int xd, const uint8_t* w, const float* bias, voi
   return launch<T, float, float>(x, w, bias, out, M, K, N, st);
 }
 
+// Full fp32 dequant of n_blocks blocks, one thread per weight. Every product is exact in fp32
+// (fp16 d x int8 code; fp16 d x int8 scale x 6-bit code), so the order of the factors does
+// not change a bit.
+template <int T>
+__global__ __launch_bounds__(256) void ggml_dequant_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                                           int64_t nvals) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nvals) return;
+  const int64_t blk = i / Blk<T>::VALS;
+  const int j = (int)(i - blk * Blk<T>::VALS);
+  const size_t bs = (size_t)blk * Blk<T>::BYTES;
+  if constexpr (T == kQ8_0) {
+    out[i] = f16_at(w, bs) * (float)(int8_t)w[bs + 2 + j];
+  } else {
+    const int h = j >> 7, r = j & 127, q = r >> 5, l = r & 31;
+    const uint32_t lo = w[bs + 64 * h + l + 32 * (q & 1)];
+    const uint32_t nib = (q >> 1) ? (lo >> 4) : (lo & 15u);
+    const uint32_t c = nib | (((uint32_t)(w[bs + 128 + 32 * h + l] >> (2 * q)) & 3u) << 4);
+    const float sc = (float)(int8_t)w[bs + 192 + 8 * h + (l >> 4) + 2 * q];
+    out[i] = (f16_at(w, bs + 208) * sc) * (float)((int)c - 32);
+  }
+}
+
 }  // namespace gg
 }  // namespace miq
 
 using namespace miq;
+
+extern "C" int miq_ggml_dequant_f32(const uint8_t* blocks, int ggml_type, float* out, int64_t n_blocks,
+                                    void* stream) {
+  if (ggml_type == 12) return miq_q4k_dequant_f32(blocks, out, n_blocks, stream);
+  MIQ_REQUIRE(ggml_type == gg::kQ8_0 || ggml_type == gg::kQ6_K, MIQ_ERR_UNSUPPORTED,
+              "ggml_dequant: ggml type %d (Q4_K = 12, Q8_0 = 8 and Q6_K = 14 are decoded here)", ggml_type);
+  MIQ_REQUIRE(n_blocks >= 0, MIQ_ERR_INVALID, "ggml_dequant: n_blocks=%lld", (long long)n_blocks);
+  if (n_blocks == 0) return MIQ_OK;
+  MIQ_REQUIRE(blocks && out, MIQ_ERR_INVALID, "ggml_dequant: null pointer");
+  MIQ_REQUIRE(aligned(blocks, 2), MIQ_ERR_ALIGN, "ggml_dequant: blocks must be 2-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t vals = n_blocks * (ggml_type == gg::kQ8_0 ? 32 : 256);
+  const dim3 grid((unsigned)((vals + 255) / 256));
+  if (ggml_type == gg::kQ8_0) hipLaunchKernelGGL(gg::ggml_dequant_kernel<gg::kQ8_0>, grid, dim3(256), 0, st, blocks, out, vals);
+  else hipLaunchKernelGGL(gg::ggml_dequant_kernel<gg::kQ6_K>, grid, dim3(256), 0, st, blocks, out, vals);
+  return check_launch("ggml_dequant");
+}
 
 extern "C" int miq_ggml_gemv(const void* x, int x_dtype, const uint8_t* w, int ggml_type, const float* bias,
                              void* out, int out_dtype, int M, int K, int N, void* stream) {

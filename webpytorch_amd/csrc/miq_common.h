@@ -110,13 +110,19 @@ __device__ __forceinline__ float wave_max(float v) {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
-// (a & m) | o in one VALU instruction (the compiler otherwise splits it in two, each with a
-// literal); m and o stay in registers across the loop.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-  uint32_t d;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(m), "v"(o));
-  return d;
+// A constant as a register value the compiler cannot see through. The empty asm emits no
+// instruction and has no side effects, so the compiler still hoists and shares it like any
+// other value; the constant then stays in a register across a loop.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
 }
+// (a & m) | o as one v_and_or_b32 with register operands (with literal m and o the compiler
+// splits it in two instructions, each carrying a literal). Plain C++, so that the compiler's
+// hazard tracking covers the result where it feeds a matrix-core instruction: it neither pads
+// an inline-asm VALU write before an MFMA that reads it nor delays an inline-asm write of a
+// register that an issued MFMA is still reading.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & opaque(m)) | opaque(o); }
 // codes in bits 0-3 and 16-19 of w
 __device__ __forceinline__ half2v nib_lo(uint32_t w) {
   return as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) - (half2v){(_Float16)1024, (_Float16)1024};
@@ -195,38 +201,6 @@ __device__ __forceinline__ half8v b_fragment(const uint4* w, int s, half2v zl, h
   }
 }
 
-// The same operand with the 8 values in k order (c0 c1 ... c7), for activations kept in memory
-// order. v_perm copies byte i of the word into bytes 0 and 2; its low nibble (c_2i) and high
-// nibble (c_2i+1, times 16) then sit in the low mantissa bits of the two halves, and one packed
-// fma with per-half factors (1, 1/16) and offsets zc = (-(1024 + z'), -(64 + z')) leaves the two
-// exact integers c - z'. int8: bytes 0 and 1 (then 2 and 3) of a word become the pair directly.
-template <int BITS> __device__ __forceinline__ half2v zero_consts_nat(uint32_t code, float zoff) {
-  const float zf = (float)code + zoff;
-  if constexpr (BITS == 4) return (half2v){(_Float16)(-(1024.f + zf)), (_Float16)(-(64.f + zf))};
-  else return (half2v){(_Float16)(-(1024.f + zf)), (_Float16)(-(1024.f + zf))};
-}
-template <int BITS>
-__device__ __forceinline__ half8v b_fragment_nat(const uint4* w, int s, half2v zc) {
-  const uint32_t w0 = (&w[0].x)[s];
-  if constexpr (BITS == 4) {
-    const half2v f = (half2v){(_Float16)1.0f, (_Float16)0.0625f};
-    half2v h[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t t = __builtin_amdgcn_perm(w0, w0, (uint32_t)i | 0x0C00u | ((uint32_t)i << 16) | 0x0C000000u);
-      h[i] = __builtin_elementwise_fma(as_h2(and_or(t, 0x00F0000Fu, 0x64006400u)), f, zc);
-    }
-    return cat4(h[0], h[1], h[2], h[3]);
-  } else {
-    const uint32_t w1 = (&w[1].x)[s];
-    const uint32_t lo = 0x0C010C00u, hi = 0x0C030C02u;  // bytes (0, 1) and (2, 3) into the halves
-    return cat4(as_h2(__builtin_amdgcn_perm(w0, w0, lo) | 0x64006400u) + zc,
-                as_h2(__builtin_amdgcn_perm(w0, w0, hi) | 0x64006400u) + zc,
-                as_h2(__builtin_amdgcn_perm(w1, w1, lo) | 0x64006400u) + zc,
-                as_h2(__builtin_amdgcn_perm(w1, w1, hi) | 0x64006400u) + zc);
-  }
-}
-
 // ---- LDS DMA: each of the 64 lanes copies 16 (or 4) bytes from its own global address to LDS
 // at m0 + 16 * lane (4 * lane). Written as inline asm so that the compiler does not track it:
 // the caller waits for these loads itself (s_waitcnt vmcnt) and orders them with a barrier.
@@ -252,8 +226,10 @@ constexpr int kCUs = 256;
 
 // Split-K workspaces: every kernel keeps its arrival counters in the same fixed region at the
 // start of the workspace (so one call's partial sums can never land on another call's
-// counters) and its partials after it.
-constexpr size_t kCounterBytes = 2 << 20;
-constexpr int kMaxCounters = (int)(kCounterBytes / 4);
+// counters) and its partials after it. The region is 4 MiB: 64-bit fixed-point words (or int
+// counters) in the first 2 MiB, the words' 32-bit escape masks in the next 1 MiB
+// (mma_tile.h), 1 MiB unused.
+constexpr size_t kCounterBytes = 4 << 20;
+constexpr int kMaxCounters = (int)((2 << 20) / 4);
 
 }  // namespace miq

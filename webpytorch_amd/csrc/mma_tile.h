@@ -241,40 +241,80 @@ __device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned cha
 
 // ---- deterministic split-K sums in fixed point ------------------------------------------
 // The K-slices of one output meet in a zeroed 64-bit word: each adds its partial p as
-// round(p * 2^24) + 2^51 (in [0, 2^52) for |p| < 2^27; larger partials saturate, NaN becomes
-// -2^27) together with 1 in bits 58-63, by one agent-scope atomic. Integer sums do not depend on
-// the order of arrival, so results are deterministic; up to 32 slices stay below 2^57. The
-// atomic's return value tells the last slice that it is last and holds the whole sum; that slice
-// re-zeroes the word. One round trip to the coherence point per slice.
+// round(p * 2^24) + 2^46 (in [0, 2^47) for |p| < 2^22) together with 1 in the count field
+// (bits 58-63), by one agent-scope atomic. Integer sums do not depend on the order of arrival,
+// so results are deterministic; 32 slices stay below 2^52. The atomic's return value tells the
+// last slice that it is last and holds the whole sum; that slice re-zeroes the word. One round
+// trip to the coherence point per slice.
+//
+// A partial the fixed point cannot hold (NaN, +-Inf or |p| >= 2^22) takes an exact escape: its
+// slice stores p as fp32 in the slice's side slot of the output, sets the slice's bit in the
+// output's mask word (a zeroed 32-bit word) and adds 0 to the sum with 1 in the escape field
+// (bits 52-57), releasing the two stores with the add. The last slice, seeing a non-zero escape
+// field, acquires them and adds the escaped partials to the fixed-point sum in slice order, so
+// NaN and infinities propagate as in an fp32 sum and large values keep fp32 accuracy; it
+// re-zeroes the mask. Outputs without an escape pay nothing for it.
 constexpr float kFixScale = 16777216.f;
-constexpr float kFixSat = 134217720.f;  // the largest float below 2^27
-constexpr unsigned long long kFixBias = 1ull << 51;
+constexpr float kFixLimit = 4194304.f;  // 2^22: partials at or above it (and NaN) escape
+constexpr unsigned long long kFixBias = 1ull << 46;
+constexpr int kFixEscShift = 52;
 constexpr int kFixCountShift = 58;
 constexpr int kFixMaxSlices = 32;
+// The counter region holds the 64-bit words in its first kFixWordBytes and a 32-bit mask word
+// per 64-bit word after them (mask i at byte kFixWordBytes + 4 i).
+constexpr size_t kFixWordBytes = 2 << 20;
+constexpr size_t kFixMaxWords = kFixWordBytes / 8;
+
+// Where one output's escape goes: its mask word and its slot for slice 0 (slice s at
+// side + s * stride).
+struct FixEsc {
+  uint32_t* mask;
+  float* side;
+  size_t stride;
+};
+__device__ __forceinline__ FixEsc fix_esc(unsigned long long* words, size_t i, float* side_base, size_t stride) {
+  return {reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(words) + kFixWordBytes) + i, side_base + i, stride};
+}
+
+__device__ __forceinline__ bool fix_fits(float p) { return fabsf(p) < kFixLimit; }  // false for NaN
 
 // The word a slice adds for its partial p.
 __device__ __forceinline__ unsigned long long fix_word(float p) {
-  const float pc = fminf(fmaxf(p, -kFixSat), kFixSat);
-  return (1ull << kFixCountShift) + (unsigned long long)(__float2ll_rn(pc * kFixScale) + (long long)kFixBias);
+  return fix_fits(p) ? (1ull << kFixCountShift) + (unsigned long long)(__float2ll_rn(p * kFixScale) + (long long)kFixBias)
+                     : (1ull << kFixCountShift) + (1ull << kFixEscShift) + kFixBias;
 }
-__device__ __forceinline__ unsigned long long fix_issue(unsigned long long* w, unsigned long long add) {
-  return __hip_atomic_fetch_add(w, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Slice `slice` adds `add` (= fix_word(p)) to word w; returns the word's previous value.
+__device__ __forceinline__ unsigned long long fix_issue(unsigned long long* w, unsigned long long add, float p,
+                                                        const FixEsc& e, int slice) {
+  if (fix_fits(p)) return __hip_atomic_fetch_add(w, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(e.side + (size_t)slice * e.stride, p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_or(e.mask, 1u << slice, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(w, add, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 // After the atomic returned `old`: true in the last slice, with the whole sum in *sum, and the
-// word re-zeroed. Issue every atomic of a lane before finishing any, so their round trips
-// overlap.
+// word (and mask) re-zeroed. Issue every atomic of a lane before finishing any, so their round
+// trips overlap.
 __device__ __forceinline__ bool fix_finish(unsigned long long* w, unsigned long long old, unsigned long long add,
-                                           int slices, float* sum) {
+                                           int slices, const FixEsc& e, float* sum) {
   if ((int)(old >> kFixCountShift) != slices - 1) return false;
-  const long long tot =
-      (long long)((old + add) & ((1ull << kFixCountShift) - 1)) - (long long)slices * (long long)kFixBias;
-  *sum = (float)tot * (1.f / kFixScale);
+  const unsigned long long tot = old + add;
+  const long long v = (long long)(tot & ((1ull << kFixEscShift) - 1)) - (long long)slices * (long long)kFixBias;
+  float s = (float)v * (1.f / kFixScale);
+  if ((tot >> kFixEscShift) & 63ull) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const uint32_t m = __hip_atomic_load(e.mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < slices; ++i)
+      if ((m >> i) & 1u) s += __hip_atomic_load(e.side + (size_t)i * e.stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(e.mask, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  *sum = s;
   __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
 }
-__device__ __forceinline__ bool fix_add(unsigned long long* w, float p, int slices, float* sum) {
+__device__ __forceinline__ bool fix_add(unsigned long long* w, float p, int slices, int slice, const FixEsc& e,
+                                        float* sum) {
   const unsigned long long add = fix_word(p);
-  return fix_finish(w, fix_issue(w, add), add, slices, sum);
+  return fix_finish(w, fix_issue(w, add, p, e, slice), add, slices, e, sum);
 }
 
 }  // namespace mt
