@@ -90,6 +90,23 @@ int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, const int32_t
                   void* out, int out_dtype, int M, int K, int N, int gs, int bits,
                   float zero_offset, void* workspace, size_t workspace_bytes, void* stream);
 
+/* miq_gptq_gemv without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has
+ * no counterpart in the reference. The split-K workspace is a fixed array in the library's
+ * device memory, miq_gptq_gemv_noalloc_max_bytes() (16 MiB) on each GPU the library runs on,
+ * held until the process ends; the first call on a GPU looks its address up and clears its
+ * counter region (a fill kernel on `stream`). The call itself allocates nothing. A problem
+ * whose workspace (miq_gptq_gemv_workspace) exceeds the array fails with MIQ_ERR_INVALID
+ * before launching anything. Every call on a GPU shares that GPU's array: calls that overlap
+ * on one GPU (two streams, two threads) race and may give wrong results; calls issued on one
+ * stream are ordered and safe. Arguments and results otherwise as miq_gptq_gemv. */
+int miq_gptq_gemv_noalloc(const void* x, int x_dtype, const int32_t* perm, const int32_t* qweight,
+                          const int32_t* qzeros, const void* scales, int scales_dtype, const float* bias,
+                          void* out, int out_dtype, int M, int K, int N, int gs, int bits, float zero_offset,
+                          void* stream);
+/* Bytes of the fixed workspace array miq_gptq_gemv_noalloc uses. */
+size_t miq_gptq_gemv_noalloc_max_bytes(void);
+
 /* input transforms of miq_gptq_gemv_fused */
 #define MIQ_X_PLAIN 0   /* x as given */
 #define MIQ_X_RMSNORM 1 /* x[m] / sqrt(mean(x[m]^2) + eps) * norm_w, over the full K */

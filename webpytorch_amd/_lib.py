@@ -23,6 +23,7 @@ SIGNATURES = {
     "miq_gptq_repack_rows": [_p, _p, _p, _i, _i, _i, _p],
     "miq_gptq_gemv_workspace": [_i, _i, _i, _i, _i, _i, _p],
     "miq_gptq_gemv": [_p, _i, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
+    "miq_gptq_gemv_noalloc": [_p, _i, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p],
     "miq_gptq_gemv_fused": [_p, _i, _p, _f, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
     "miq_gptq_gemm_workspace": [_i, _i, _i, _i, _i, _p],
     "miq_gptq_gemm": [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
@@ -68,6 +69,8 @@ def lib():
         L.miq_version.restype = ctypes.c_int
         L.miq_decode_state_words.restype = ctypes.c_int
         L.miq_decode_state_words.argtypes = []
+        L.miq_gptq_gemv_noalloc_max_bytes.restype = ctypes.c_size_t
+        L.miq_gptq_gemv_noalloc_max_bytes.argtypes = []
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args

@@ -12,6 +12,7 @@
 // per-chunk sums so the zero point is applied once per chunk: sum x*(q - z) is computed as
 // sum x*q - z * sum x.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "miq_common.h"
@@ -680,4 +681,78 @@ extern "C" int miq_gptq_gemv_fused(const float* x, int x_mode, const float* norm
                                   bits, zero_offset, norm_w, eps, st);
   return gemv_fused_dispatch<2>(p, x, perm, qweight, qzeros, scales, scales_dtype, bias, out, workspace, M, K, N, gs,
                                 bits, zero_offset, nullptr, 0.f, st);
+}
+
+// ------------------------------------------------------------------------------------
+// The GEMV with no workspace argument and no allocation: its split-K workspace is a fixed
+// device array of this file. HIP gives every device its own copy of the array; host code
+// reaches a device's copy only through the address hipGetSymbolAddress returns while that
+// device is current (the array's name in host code is a host-side stand-in, not a device
+// address). Each device's address is looked up once, on the first call made on it, which also
+// clears the array's counter region with a fill kernel on the caller's stream (the kernels
+// leave it zero after every call).
+namespace miq {
+namespace na {
+
+constexpr size_t kScratchBytes = 16u << 20;  // counter region (4 MiB) + 12 MiB of partials
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint4* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+std::mutex g_lock;
+void* g_ptr[kMaxDevices];
+
+// The current device's copy of the scratch array (set up on its first use), or null with the
+// error recorded.
+void* device_scratch(hipStream_t st) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(MIQ_ERR_HIP, "gptq_gemv_noalloc: hipGetDevice: %s (device %d)", hipGetErrorString(e), dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(g_lock);
+  if (!g_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(MIQ_ERR_HIP, "gptq_gemv_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, st, static_cast<uint4*>(p), kCounterBytes / 16);
+    if (check_launch("gptq_gemv_noalloc scratch clear")) return nullptr;
+    g_ptr[dev] = p;
+  }
+  return g_ptr[dev];
+}
+
+}  // namespace na
+}  // namespace miq
+
+extern "C" size_t miq_gptq_gemv_noalloc_max_bytes(void) { return miq::na::kScratchBytes; }
+
+extern "C" int miq_gptq_gemv_noalloc(const void* x, int x_dtype, const int32_t* perm, const int32_t* qweight,
+                                     const int32_t* qzeros, const void* scales, int scales_dtype, const float* bias,
+                                     void* out, int out_dtype, int M, int K, int N, int gs, int bits,
+                                     float zero_offset, void* stream) {
+  int rc = gemv_check("gptq_gemv_noalloc", x, x_dtype, qweight, qzeros, scales, scales_dtype, out, out_dtype, M, K,
+                      N, gs, bits);
+  if (rc || M == 0) return rc;
+  size_t need = 0;
+  rc = miq_gptq_gemv_workspace(M, K, N, gs, bits, x_dtype, &need);
+  if (rc) return rc;
+  MIQ_REQUIRE(need <= na::kScratchBytes, MIQ_ERR_INVALID,
+              "gptq_gemv_noalloc: M=%d K=%d N=%d needs %zu bytes of split-K workspace, the fixed scratch holds %zu "
+              "(use miq_gptq_gemv with a workspace)",
+              M, K, N, need, na::kScratchBytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = na::device_scratch(st);
+  if (!ws) return MIQ_ERR_HIP;
+  return miq_gptq_gemv(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs,
+                       bits, zero_offset, ws, na::kScratchBytes, stream);
 }
