@@ -113,7 +113,7 @@ size_t miq_gptq_gemv_noalloc_max_bytes(void);
 #define MIQ_X_SWIGLU 2  /* x rows hold [gate | up] (2K values): silu(gate) * up */
 
 /* Decode GEMV with the preceding elementwise step fused into the activation staging:
- * out[M][N] = T(x) @ W + bias for fp32 x and out (M == 1 for the fused modes, int4), with T the
+ * out[M][N] = T(x) @ W + bias for fp32 x and out (M == 1 for the fused modes), with T the
  * x_mode transform. Same weight, workspace and bias rules as miq_gptq_gemv (bias may alias out).
  * Replaces: `_rms` + `_qkv` / `_mlp` of the decode step (webtorch/llm.py:1259-1268, 1489-1519),
  * each an RMSNorm or SwiGLU dispatch followed by a `_gptq_matmul`. */

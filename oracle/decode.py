@@ -50,7 +50,11 @@ class Qwen2Oracle:
         return (x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + self.eps)) * \
             np.asarray(w, np.float32)
 
-    def lin(self, d, x, zoff=1.0):
+    def lin(self, d, x, zoff=None):
+        """AutoGPTQ layers use zero offset 1 (`from_autogptq`); layers quantized on load carry
+        their own (0, `_gquant`)."""
+        if zoff is None:
+            zoff = d.get("zoff", 1.0)
         y = gptq.gptq_matmul_np(x, d["qweight"], d["qzeros"], d["scales"], d["K"], d["N"],
                                 d["gs"], d["bits"], zoff)
         b = d.get("bias")
@@ -128,3 +132,36 @@ class Qwen2Oracle:
             if keep_logits:
                 logs.append(lg)
         return out, logs
+
+
+HF_PROJ = (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
+           ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
+           ("down", "mlp.down_proj"))
+
+
+def fp16q_weights(tensors, config, bits, gs=128):
+    """Oracle weights of a plain fp16 HF model quantized on load, as the reference's
+    `from_fp16(quantize=bits)` does (`webtorch/llm.py:1211-1257`): each (out, in) projection read
+    as fp32 and quantized by `_gquant` (`webtorch/llm.py:835-853`: `_gptq_quantize` with
+    from_out_in, zero offset 0, fp32 scales); the tied head re-quantized from the embedding."""
+    c = config
+    H, L = c["hidden_size"], c["num_hidden_layers"]
+    layers = []
+    for i in range(L):
+        p = "model.layers.%d." % i
+        lay = {"in_ln": tensors[p + "input_layernorm.weight"].astype(np.float32),
+               "post_ln": tensors[p + "post_attention_layernorm.weight"].astype(np.float32)}
+        for nm, hf in HF_PROJ:
+            W = tensors[p + hf + ".weight"].astype(np.float32)
+            N, K = W.shape
+            qw, qz, sc, _, _ = gptq.gptq_quantize(W, gs, bits, from_out_in=True)
+            b = tensors.get(p + hf + ".bias")
+            lay[nm] = {"qweight": qw, "qzeros": qz, "scales": sc, "K": K, "N": N, "gs": gs, "bits": bits,
+                       "zoff": 0.0, "bias": None if b is None else b.astype(np.float32)}
+        layers.append(lay)
+    NH = c["num_attention_heads"]
+    cfg = dict(L=L, H=H, NH=NH, NKV=c.get("num_key_value_heads", NH), HD=c.get("head_dim") or H // NH,
+               I=c["intermediate_size"], V=c["vocab_size"], gs=gs, bits=bits, eps=c.get("rms_norm_eps", 1e-6),
+               theta=c.get("rope_theta", 10000.0))
+    return {"layers": layers, "embed": tensors["model.embed_tokens.weight"],
+            "final_norm": tensors["model.norm.weight"].astype(np.float32), "cfg": cfg}

@@ -6,10 +6,13 @@ Only functions that no closed form pins are recorded here:
     from_out_in) -- `webtorch/_core.py:3782-3824`
   * `lm_engine.moe_mlp` output on a small seeded instance -- `webtorch/lm_engine.py:294-333`
   * `CausalLM.generate` greedy token ids on the CPU growing-cache path, at a reduced shape and
-    at the full Qwen2-0.5B shape -- `webtorch/llm.py:1716-1787`
+    at the full Qwen2-0.5B shape, for uniform-code and Gaussian-quantized AutoGPTQ models, with
+    each step's top-1/top-2 logit gap -- `webtorch/llm.py:1716-1787`
+  * the same for a plain fp16 model quantized on load to int4 and int8 (`from_fp16(quantize=)`,
+    `webtorch/llm.py:1211-1257, 835-853`)
 
 Inputs are regenerated from seeds by `webpytorch_amd.synth`; the fixtures hold the seeds,
-the shapes and the reference's outputs. Usage: python tests/golden/make_golden.py [--full]
+the shapes and the reference's outputs. Usage: python tests/golden/make_golden.py [--full] [--only name,...]
 """
 import argparse
 import os
@@ -131,17 +134,84 @@ def build_reference_lm(wt, llm, wts, lmax):
     return m
 
 
-def make_decode(wt, llm, out, seed, shape, prompt_len, max_new, lmax):
-    wts = synth.decoder_weights(seed, **shape)
-    ids = synth.prompt_ids(seed, prompt_len, shape["V"])
-    m = build_reference_lm(wt, llm, wts, lmax)
+def _generate_with_margins(m, ids, max_new):
+    """The reference's greedy generate, recording each step's top-1 minus top-2 logit and the
+    logits' spread (max - min) as `_pick` sees them."""
+    margins, spreads = [], []
+    pick = m._pick
+
+    def recording_pick(logits):
+        lg = np.asarray(logits, np.float32)
+        top = np.partition(lg, -2)[-2:]
+        margins.append(float(top[1] - top[0]))
+        spreads.append(float(lg.max() - lg.min()))
+        return pick(logits)
+    m._pick = recording_pick
     t0 = time.time()
     res = m.generate(ids=[int(i) for i in ids], max_new=max_new)
-    dt = time.time() - t0
-    print("%s: %d tokens in %.1fs" % (os.path.basename(out), len(res.tokens), dt))
+    return res.tokens, np.asarray(margins, np.float32), np.asarray(spreads, np.float32), time.time() - t0
+
+
+SHAPE_KEYS = ("L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits")
+
+
+def make_decode(wt, llm, out, seed, shape, prompt_len, max_new, lmax, gaussian=False):
+    wts = synth.decoder_weights(seed, gaussian=gaussian, **shape)
+    ids = synth.prompt_ids(seed, prompt_len, shape["V"])
+    m = build_reference_lm(wt, llm, wts, lmax)
+    toks, margins, spreads, dt = _generate_with_margins(m, ids, max_new)
+    print("%s: %d tokens (%d distinct) in %.1fs, min margin %.3g" % (os.path.basename(out), len(toks),
+                                                                     len(set(toks)), dt, margins.min()))
     np.savez_compressed(out, seed=seed, prompt_len=prompt_len, max_new=max_new, lmax=lmax,
-                        shape=np.array([shape[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits")]),
-                        tokens=np.asarray(res.tokens, np.int64))
+                        gaussian=int(gaussian), shape=np.array([shape[k] for k in SHAPE_KEYS]),
+                        tokens=np.asarray(toks, np.int64), margins=margins, spreads=spreads)
+
+
+def build_reference_fp16q(wt, llm, model, bits, lmax, gs=128):
+    """The reference's `CausalLM.from_fp16(quantize=bits)` composition (`webtorch/llm.py:1211-1257`,
+    `_gquant` 835-853, `_quantize_head` 594-602) on the tensors of `synth.fp16_decoder`: every
+    (out, in) projection read as fp32 from its fp16 bytes and quantized on load."""
+    c, t = model["config"], model["tensors"]
+    m = llm.CausalLM("")
+    m._apply_cfg(dict(c))
+    m.gs, m.bits, m._qbits, m.lmax = gs, bits, bits, lmax
+    m.tok = _Tok()
+    m.gen_defaults = {}
+    m._gpu = False
+    m.embed = t["model.embed_tokens.weight"]
+    m.head = m._quantize_head(m.embed)
+
+    def lin(prefix):
+        b = t.get(prefix + ".bias")
+        return m._mklin(t[prefix + ".weight"].astype(np.float32), None if b is None else b.astype(np.float32))
+    m.layers = []
+    for i in range(c["num_hidden_layers"]):
+        p = "model.layers.%d." % i
+        m.layers.append({"in_ln": wt.Tensor(t[p + "input_layernorm.weight"].astype(np.float32)),
+                         "post_ln": wt.Tensor(t[p + "post_attention_layernorm.weight"].astype(np.float32)),
+                         "q": lin(p + "self_attn.q_proj"), "k": lin(p + "self_attn.k_proj"),
+                         "v": lin(p + "self_attn.v_proj"), "o": lin(p + "self_attn.o_proj"), "qn": None,
+                         "kn": None, "gate": lin(p + "mlp.gate_proj"), "up": lin(p + "mlp.up_proj"),
+                         "down": lin(p + "mlp.down_proj")})
+    m.final_norm = wt.Tensor(t["model.norm.weight"].astype(np.float32))
+    m._init_state()
+    return m
+
+
+def make_fp16q(wt, llm, out, seed, shape, prompt_len, max_new, lmax):
+    """Greedy ids of a plain fp16 model loaded with quantize-on-load to int4 and to int8."""
+    model = synth.fp16_decoder(seed, **shape)
+    ids = synth.prompt_ids(seed, prompt_len, shape["V"])
+    d = {}
+    for bits in (4, 8):
+        m = build_reference_fp16q(wt, llm, model, bits, lmax)
+        toks, margins, spreads, dt = _generate_with_margins(m, ids, max_new)
+        print("%s int%d: %d tokens (%d distinct) in %.1fs, min margin %.3g" % (
+            os.path.basename(out), bits, len(toks), len(set(toks)), dt, margins.min()))
+        d["tokens_int%d" % bits] = np.asarray(toks, np.int64)
+        d["margins_int%d" % bits] = margins
+    np.savez_compressed(out, seed=seed, prompt_len=prompt_len, max_new=max_new, lmax=lmax,
+                        shape=np.array([shape[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V")]), **d)
 
 
 SMALL = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
@@ -151,15 +221,31 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--full", action="store_true", help="also the full Qwen2-0.5B-shaped decode")
     ap.add_argument("--full-only", action="store_true", help="only the full Qwen2-0.5B-shaped decode")
+    ap.add_argument("--only", default="", help="comma-separated fixture names to (re)write")
     a = ap.parse_args()
     wt, lm_engine, llm = import_reference()
-    if not a.full_only:
+    only = set(filter(None, a.only.split(",")))
+
+    def want(name, default):
+        return name in only if only else default
+    if want("gptq_quantize", not a.full_only):
         make_quantize(wt, os.path.join(HERE, "gptq_quantize.npz"))
+    if want("moe_small", not a.full_only):
         make_moe(wt, lm_engine, os.path.join(HERE, "moe_small.npz"))
+    if want("decode_small", not a.full_only):
         make_decode(wt, llm, os.path.join(HERE, "decode_small.npz"), 11, SMALL, 16, 24, 64)
-    if a.full or a.full_only:
+    # Gaussian-quantized models: varied greedy tokens; seed 14 (reduced shape) and seed 6 (full
+    # shape) were chosen for their smallest per-step top-1/top-2 logit gap (recorded in the file)
+    if want("decode_gauss_small", not a.full_only):
+        make_decode(wt, llm, os.path.join(HERE, "decode_gauss_small.npz"), 14, SMALL, 16, 32, 64, gaussian=True)
+    if want("decode_fp16q_small", not a.full_only):
+        make_fp16q(wt, llm, os.path.join(HERE, "decode_fp16q_small.npz"), 21, SMALL, 16, 32, 64)
+    if want("decode_qwen2_05b", a.full or a.full_only):
         make_decode(wt, llm, os.path.join(HERE, "decode_qwen2_05b.npz"), 5, dict(synth.QWEN2_05B),
                     64, 128, 256)
+    if want("decode_gauss_qwen2_05b", a.full or a.full_only):
+        make_decode(wt, llm, os.path.join(HERE, "decode_gauss_qwen2_05b.npz"), 6, dict(synth.QWEN2_05B),
+                    64, 128, 256, gaussian=True)
 
 
 if __name__ == "__main__":

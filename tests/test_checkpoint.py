@@ -300,3 +300,80 @@ def test_gguf_q4k_linear_vs_oracle(gpu, tmp_path):
     ref = q4k.q4k_matmul(x, W, K, N)
     assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
     assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5
+
+
+# ---- plain fp16 directories: quantize-on-load and the from_pretrained dispatch ----------------
+
+def write_fp16_dir(path, model):
+    """A plain fp16 HuggingFace directory of a `synth.fp16_decoder` model."""
+    from safetensors.numpy import save_file
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump(model["config"], f)
+    save_file(model["tensors"], os.path.join(path, "model.safetensors"))
+
+
+def test_fp16_dir_config_dispatch(tmp_path):
+    """A plain directory is not an AutoGPTQ one, so `from_pretrained` takes the quantize-on-load
+    branch (`webtorch/_sdk.py:108-113`); the AutoGPTQ directory takes `from_gptq`."""
+    m = synth.fp16_decoder(21, **{k: SMALL[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V")})
+    write_fp16_dir(str(tmp_path / "fp16"), m)
+    write_gptq_dir(str(tmp_path / "gptq"), synth.decoder_weights(3, **SMALL))
+    assert not checkpoint.is_quantized_dir(str(tmp_path / "fp16"))
+    assert checkpoint.is_quantized_dir(str(tmp_path / "gptq"))
+    with pytest.raises(ValueError, match="already-quantized"):
+        checkpoint.fp16_weights(str(tmp_path / "gptq"), 4)
+    with pytest.raises(NotImplementedError):
+        checkpoint.fp16_weights(str(tmp_path / "fp16"), 3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits", [4, 8])
+def test_from_pretrained_quantizes_fp16_dir_like_the_reference(gpu, tmp_path, bits):
+    """`AutoModelForCausalLM.from_pretrained(dir, dtype="int4"|"int8")` on a plain fp16
+    directory: every linear quantized on the device on load (gs 128, zero offset 0, fp32 scales;
+    int8 group-128 asymmetric), bit-exact with the oracle's `_gptq_quantize`, then greedy ids
+    identical to the reference's `from_fp16(quantize=bits)` CPU decode (fixture), eager, unfused
+    and graph-replayed."""
+    import torch
+    from webpytorch_amd import llm
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "decode_fp16q_small.npz"))
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V"], [int(v) for v in g["shape"]]))
+    model = synth.fp16_decoder(int(g["seed"]), **sh)
+    write_fp16_dir(str(tmp_path), model)
+    m = llm.AutoModelForCausalLM.from_pretrained(str(tmp_path), dtype="int%d" % bits, lmax=int(g["lmax"]))
+    assert m.bits == bits and m.gs == 128 and m.layers[0]["qkv"].zoff == 0.0
+    assert m.layers[0]["o"].scales.dtype == torch.float32
+    # the device quantizer's output equals the oracle's for a loaded projection
+    ow = decode.fp16q_weights(model["tensors"], model["config"], bits)
+    assert np.array_equal(m.layers[1]["down"].qweight.cpu().numpy(), ow["layers"][1]["down"]["qweight"])
+    assert np.array_equal(m.layers[1]["down"].scales.cpu().numpy().view(np.uint32),
+                          ow["layers"][1]["down"]["scales"].view(np.uint32))
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    want = [int(t) for t in g["tokens_int%d" % bits]]
+    n = int(g["max_new"])
+    assert m.generate(ids, n, use_graph=False).tokens == want
+    m.fused = False
+    assert m.generate(ids, n, use_graph=False).tokens == want
+    m.fused = True
+    assert m.generate(ids, n).tokens == want
+
+
+@pytest.mark.gpu
+def test_from_pretrained_dispatch_and_refusals(gpu, tmp_path):
+    from webpytorch_amd import llm
+    w = synth.decoder_weights(14, gaussian=True, **SMALL)
+    write_gptq_dir(str(tmp_path / "gptq"), w)
+    ids = synth.prompt_ids(14, 16, SMALL["V"])
+    # an AutoGPTQ directory loads at its stored bits whatever dtype asks for
+    for dt in ("auto", "int8"):
+        m = llm.AutoModelForCausalLM.from_pretrained(str(tmp_path / "gptq"), dtype=dt, lmax=64)
+        assert m.bits == 4 and m.layers[0]["qkv"].zoff == 1.0
+    assert m.generate(ids, 8).tokens == llm.CausalLM.from_weights(w, lmax=64).generate(ids, 8).tokens
+    model = synth.fp16_decoder(2, **{k: SMALL[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V")})
+    write_fp16_dir(str(tmp_path / "fp16"), model)
+    for dt in ("auto", "fp16"):  # unquantized execution is outside the quantized path
+        with pytest.raises(NotImplementedError, match="fp16"):
+            llm.AutoModelForCausalLM.from_pretrained(str(tmp_path / "fp16"), dtype=dt, lmax=64)
+    with pytest.raises(ValueError, match="dtype"):
+        llm.AutoModelForCausalLM.from_pretrained(str(tmp_path / "fp16"), dtype="int3")

@@ -186,6 +186,44 @@ def test_decode_matches_reference_golden_qwen2_05b(gpu):
     assert res.tokens == [int(t) for t in g["tokens"]]
 
 
+def _gauss_engine(g, lmax, persistent=None):
+    from webpytorch_amd import llm
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits"], [int(v) for v in g["shape"]]))
+    w = synth.decoder_weights(int(g["seed"]), gaussian=True, **sh)
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    return llm.CausalLM.from_weights(w, lmax=lmax, persistent=persistent), ids
+
+
+def test_decode_matches_reference_golden_gaussian_small(gpu):
+    """Gaussian-quantized weights (varied tokens, every step's top-1/top-2 gap recorded in the
+    fixture): the reference's greedy ids, persistent step and launch sequence, eager and
+    graph-replayed."""
+    g = np.load(os.path.join(GOLDEN, "decode_gauss_small.npz"))
+    want = [int(t) for t in g["tokens"]]
+    assert len(set(want)) >= 16 and float(g["margins"].min()) > 1e-3
+    for persistent in (True, False):
+        m, ids = _gauss_engine(g, int(g["lmax"]), persistent)
+        assert (m.pws is not None) == persistent
+        assert m.generate(ids, int(g["max_new"]), use_graph=False).tokens == want
+        assert m.generate(ids, int(g["max_new"])).tokens == want
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(GOLDEN, "decode_gauss_qwen2_05b.npz")),
+                    reason="full-shape Gaussian fixture not generated")
+def test_decode_matches_reference_golden_gaussian_qwen2_05b(gpu):
+    """End-to-end config with varied tokens: Qwen2-0.5B shape, Gaussian-quantized int4 weights,
+    64-token prompt, 128 greedy ids identical to the reference's CPU decode, for the persistent
+    step and the launch sequence (graph-replayed). The fixture records each step's top-1/top-2
+    logit gap; the smallest is far above the engines' logit error (~1e-6 relative)."""
+    g = np.load(os.path.join(GOLDEN, "decode_gauss_qwen2_05b.npz"))
+    want = [int(t) for t in g["tokens"]]
+    assert len(want) == 128 and len(set(want)) >= 30 and float(g["margins"].min()) > 1e-3
+    for persistent in (True, False):
+        m, ids = _gauss_engine(g, int(g["lmax"]), persistent)
+        assert (m.pws is not None) == persistent
+        assert m.generate(ids, int(g["max_new"])).tokens == want
+
+
 def test_generate_refuses_overlong(gpu):
     g = np.load(os.path.join(GOLDEN, "decode_small.npz"))
     m, ids, _ = _engine(g, 20)
@@ -246,14 +284,17 @@ def _persistent_pair(sh, seed, lmax, prompt):
     return a, b, ids
 
 
-@pytest.mark.parametrize("prompt,steps,lmax", [(16, 24, 64), (270, 40, 320)])
-def test_persistent_step_matches_launch_sequence(gpu, prompt, steps, lmax):
+@pytest.mark.parametrize("sh,prompt,steps,lmax", [
+    (dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4), 16, 24, 64),
+    (dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4), 270, 40, 320),
+    (dict(synth.QWEN2_05B), 240, 24, 288)])
+def test_persistent_step_matches_launch_sequence(gpu, sh, prompt, steps, lmax):
     """The one-launch persistent step against the launch sequence (5 launches per layer) on the
     same model after the same prefill: identical greedy ids and per-step logits within 1e-4
-    relative; the second case runs past 256 cached positions (the attention's second chunk)."""
+    relative; the second and third cases run past 256 cached positions (the attention's second
+    chunk), the third at the full Qwen2-0.5B shape (its role counts, K-slices and GQA grouping)."""
     import torch
-    sh = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
-    a, b, ids = _persistent_pair(sh, 14, lmax, prompt)
+    a, b, ids = _persistent_pair(sh, 6 if sh["L"] == 24 else 14, lmax, prompt)
     for m in (a, b):
         m.generate(ids, 1, use_graph=False)
     for step in range(steps):

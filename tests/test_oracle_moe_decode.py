@@ -2,6 +2,7 @@
 import os
 
 import numpy as np
+import pytest
 
 from oracle import decode, moe
 from webpytorch_amd import synth
@@ -94,3 +95,32 @@ def test_prefill_equals_stepwise_decode():
     for p, t in enumerate(ids):
         _, l2 = o.forward([t], p, c2)
     assert np.allclose(l1, l2, rtol=1e-4, atol=1e-5)
+
+
+def test_decode_matches_reference_golden_gaussian_small():
+    """Gaussian-quantized weights: varied greedy ids of the reference's CPU decode (fixture)."""
+    g = np.load(os.path.join(GOLDEN, "decode_gauss_small.npz"))
+    assert int(g["gaussian"]) == 1
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits"], [int(v) for v in g["shape"]]))
+    o = decode.Qwen2Oracle(synth.decoder_weights(int(g["seed"]), gaussian=True, **sh), lmax=int(g["lmax"]))
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    toks, logs = o.generate(ids, int(g["max_new"]), keep_logits=True)
+    want = [int(t) for t in g["tokens"]]
+    assert toks == want and len(set(want)) >= 16
+    # the oracle's logits carry the reference's top-1/top-2 gaps
+    gaps = [float(np.diff(np.partition(lg, -2)[-2:])[0]) for lg in logs]
+    np.testing.assert_allclose(gaps, g["margins"], rtol=1e-3, atol=1e-5)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_fp16_quantize_on_load_matches_reference_golden(bits):
+    """A plain fp16 model quantized on load (`from_fp16(quantize=bits)`: gs 128, zero offset 0,
+    fp32 scales; int8 is group-128 asymmetric): the reference's greedy ids."""
+    g = np.load(os.path.join(GOLDEN, "decode_fp16q_small.npz"))
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V"], [int(v) for v in g["shape"]]))
+    model = synth.fp16_decoder(int(g["seed"]), **sh)
+    o = decode.Qwen2Oracle(decode.fp16q_weights(model["tensors"], model["config"], bits), lmax=int(g["lmax"]))
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    toks, _ = o.generate(ids, int(g["max_new"]))
+    want = [int(t) for t in g["tokens_int%d" % bits]]
+    assert toks == want and len(set(want)) >= 16

@@ -7,6 +7,8 @@ GGUF container with native Q4_K upload.
   JSON header (`__metadata__` dropped), tensors at `data_offsets` past the header. BF16 and
   F16 become fp32 and I32 stays int32 on `array`; `rows_f16` streams a 2-D table in row blocks
   straight to fp16, never holding the fp32 copy.
+* `fp16_weights(path, bits)` builds it from a plain fp16/bf16 directory, quantizing every
+  projection on the device on load (`from_fp16(quantize=4|8)`, `webtorch/llm.py:1211-1257`).
 * `gptq_weights(path)` builds the weights dictionary of `llm.CausalLM` from an AutoGPTQ
   directory (`webtorch/llm.py:418-475, 506-539, 569-573, 614-647` -- `from_gptq`): the shape from
   `config.json`, AutoGPTQ tensors per projection, norms, the fp16 embedding and, for an untied
@@ -146,24 +148,41 @@ def auto_lmax(requested, declared, L, NKV, HD):
     return max(512, min(want, cap))
 
 
-def gptq_config(path):
-    """Shape, quantization and context fields of an AutoGPTQ directory's config.json."""
+def read_config(path):
+    """config.json of a HuggingFace model directory, as a dict."""
     with open(os.path.join(str(path), "config.json")) as f:
-        full = json.load(f)
-    cfg = _text_config(full)
-    q = full.get("quantization_config") or cfg.get("quantization_config")
-    if not q:
-        raise ValueError("%s: config.json has no quantization_config (not an AutoGPTQ directory)" % path)
+        return json.load(f)
+
+
+def is_quantized_dir(path):
+    """Does the directory hold an already-quantized (AutoGPTQ) model (`quantization_config`),
+    the test `from_pretrained` dispatches on (`webtorch/_sdk.py:108-113`)?"""
+    full = read_config(path)
+    return bool(full.get("quantization_config") or _text_config(full).get("quantization_config"))
+
+
+def _shape_config(cfg, gs, bits):
     H, NH = int(cfg["hidden_size"]), int(cfg["num_attention_heads"])
     out = dict(L=int(cfg["num_hidden_layers"]), H=H, NH=NH, NKV=int(cfg.get("num_key_value_heads", NH)),
                HD=int(cfg.get("head_dim") or H // NH), I=int(cfg["intermediate_size"]),
                V=int(cfg["vocab_size"]), eps=float(cfg.get("rms_norm_eps", 1e-6)),
-               theta=float(cfg.get("rope_theta", 10000.0)), gs=int(q["group_size"]), bits=int(q["bits"]))
+               theta=float(cfg.get("rope_theta", 10000.0)), gs=int(gs), bits=int(bits))
     if int(cfg.get("num_experts", cfg.get("num_local_experts", 0)) or 0):
         raise NotImplementedError("sparse-MoE decoders are run through moe_mlp, not CausalLM")
     types = cfg.get("layer_types") or []
     if any(t != "full_attention" for t in types) or int(cfg.get("full_attention_interval", 0) or 0) > 1:
         raise NotImplementedError("hybrid linear-attention decoders are not part of this path")
+    return out
+
+
+def gptq_config(path):
+    """Shape, quantization and context fields of an AutoGPTQ directory's config.json."""
+    full = read_config(path)
+    cfg = _text_config(full)
+    q = full.get("quantization_config") or cfg.get("quantization_config")
+    if not q:
+        raise ValueError("%s: config.json has no quantization_config (not an AutoGPTQ directory)" % path)
+    out = _shape_config(cfg, q["group_size"], q["bits"])
     return out, bool(cfg.get("tie_word_embeddings", False)), cfg.get("max_position_embeddings")
 
 
@@ -339,3 +358,54 @@ class GGUFFile:
         if K % GGML_TYPES[t["type"]][1]:
             return None
         return core.GGMLLinear(self.raw(name), nm, K, N, bias)
+
+
+PROJECTIONS = (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
+               ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
+               ("down", "mlp.down_proj"))
+
+
+def fp16_weights(path, bits, gs=128):
+    """`llm.CausalLM` weights of a plain fp16/bf16 HuggingFace directory quantized on load to
+    int`bits` (`from_fp16(quantize=bits)`, `webtorch/llm.py:1211-1257`): every (out, in)
+    projection goes to the device in its file encoding and is quantized there by
+    `core.gptq_quantize` -- the reference's `_gquant` (`webtorch/llm.py:835-853`): group size
+    128, asymmetric min-max, zero offset 0, fp32 scales; int8 is the same rule with 8-bit codes.
+    Returns (weights, declared context length)."""
+    import torch
+    full = read_config(path)
+    cfg = _text_config(full)
+    if full.get("quantization_config") or cfg.get("quantization_config"):
+        raise ValueError("%s holds an already-quantized model; load it with from_gptq" % path)
+    if int(bits) not in (4, 8):
+        raise NotImplementedError("quantize-on-load to %s bits (4 or 8)" % bits)
+    shape = _shape_config(cfg, gs, bits)
+    st = SafetensorsDir(path)
+    if "model.layers.0.self_attn.q_norm.weight" in st:
+        raise NotImplementedError("QK-norm decoders (Qwen3) are not part of this path")
+    per = 32 // int(bits)
+
+    def lin(prefix):
+        info, _ = st.info(prefix + ".weight")
+        N, K = (int(d) for d in info["shape"])
+        if K % gs or N % per:
+            raise NotImplementedError("%s: (%d, %d) needs padding to the group / pack size" % (prefix, N, K))
+        W = torch.from_numpy(st.array(prefix + ".weight", keep_f16=True))
+        qw, qz, sc, _, _ = core.gptq_quantize(W, gs, int(bits), from_out_in=True)
+        d = {"qweight": qw, "qzeros": qz, "scales": sc, "zoff": 0.0}
+        if prefix + ".bias" in st:
+            d["bias"] = st.array(prefix + ".bias")
+        return d
+
+    layers = []
+    for i in range(shape["L"]):
+        p = "model.layers.%d." % i
+        lay = {nm: lin(p + hf) for nm, hf in PROJECTIONS}
+        lay["in_ln"] = st.array(p + "input_layernorm.weight")
+        lay["post_ln"] = st.array(p + "post_attention_layernorm.weight")
+        layers.append(lay)
+    w = {"layers": layers, "embed": st.rows_f16("model.embed_tokens.weight"),
+         "final_norm": st.array("model.norm.weight"), "cfg": shape}
+    if not cfg.get("tie_word_embeddings", False):
+        w["head"] = st.rows_f16("lm_head.weight")
+    return w, cfg.get("max_position_embeddings")

@@ -29,6 +29,24 @@ int check_launch(const char* what) {
   return MIQ_OK;
 }
 
+int require_lds(const char* what, size_t bytes) {
+  // A launch may ask for dynamic LDS up to the device's per-workgroup limit (160 KB on gfx950)
+  // with no opt-in call; the limit is read once per device.
+  static int limit[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(MIQ_ERR_HIP, "%s: cannot query the current device", what);
+  if (limit[dev] <= 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+      return fail(MIQ_ERR_HIP, "%s: cannot query the LDS limit", what);
+    limit[dev] = v;
+  }
+  if (bytes > (size_t)limit[dev])
+    return fail(MIQ_ERR_UNSUPPORTED, "%s: %zu bytes of LDS exceed the device's %d", what, bytes, limit[dev]);
+  return MIQ_OK;
+}
+
 }  // namespace miq
 
 extern "C" const char* miq_last_error(void) { return miq::g_err; }

@@ -186,13 +186,8 @@ static int launch(const void* x, const uint8_t* w, const float* bias, void* out,
   const size_t lds = (size_t)K * 4 + (size_t)(K / Blk<T>::VPL) * 4;
   MIQ_REQUIRE(lds <= 160 * 1024, MIQ_ERR_UNSUPPORTED, "ggml_gemv: K=%d too large to stage", K);
   if (lds > 64 * 1024) {
-    static bool raised = false;  // once per instantiation
-    if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      MIQ_REQUIRE(e == hipSuccess, MIQ_ERR_HIP, "ggml_gemv: LDS attribute: %s", hipGetErrorString(e));
-      raised = true;
-    }
+    const int rc = require_lds("ggml_gemv", lds);
+    if (rc) return rc;
   }
   const int groups = (N + 3) / 4;
   int wgs = (groups + 3) / 4;

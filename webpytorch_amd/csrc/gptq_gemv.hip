@@ -470,13 +470,8 @@ static int launch_gemv(const GemvPlan& p, const void* x, const int32_t* perm, co
   int* counters = p.ksplit > 1 ? static_cast<int*>(ws) : nullptr;
   float* partials = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes) : nullptr;
   if (p.lds > 64 * 1024) {
-    static bool raised = false;  // once per instantiation
-    if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      MIQ_REQUIRE(e == hipSuccess, MIQ_ERR_HIP, "gptq_gemv: LDS attribute: %s", hipGetErrorString(e));
-      raised = true;
-    }
+    const int rc = require_lds("gptq_gemv", p.lds);
+    if (rc) return rc;
   }
   dim3 grid(p.tiles, p.ksplit, p.mblocks);
   hipLaunchKernelGGL(kern, grid, dim3(64 * p.waves), p.lds, st, static_cast<const XT*>(x), perm,
@@ -523,13 +518,17 @@ static int gemv_fused_dispatch(const GemvPlan& p, const void* x, const int32_t* 
                                const int32_t* qz, const void* sc, int sd, const float* bias, void* out, void* ws,
                                int M, int K, int N, int gs, int bits, float zoff, const float* norm_w, float eps,
                                hipStream_t st) {
-  MIQ_REQUIRE(p.mr == 1 && bits == 4, MIQ_ERR_UNSUPPORTED, "gptq_gemv_fused: one row of int4 only (M=%d bits=%d)",
-              M, bits);
-#define MIQ_GEMV_FUSED(RPW, ST) \
-  return launch_gemv<4, 1, RPW, float, ST, float, XMODE>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, norm_w, eps, st)
-  if (p.rpw == 8) { if (sd == MIQ_F16) MIQ_GEMV_FUSED(8, __half); MIQ_GEMV_FUSED(8, float); }
-  if (sd == MIQ_F16) MIQ_GEMV_FUSED(4, __half);
-  MIQ_GEMV_FUSED(4, float);
+  MIQ_REQUIRE(p.mr == 1, MIQ_ERR_UNSUPPORTED, "gptq_gemv_fused: one row only (M=%d)", M);
+#define MIQ_GEMV_FUSED(B, RPW, ST) \
+  return launch_gemv<B, 1, RPW, float, ST, float, XMODE>(p, x, perm, qw, qz, sc, bias, out, ws, M, K, N, gs, zoff, norm_w, eps, st)
+  if (bits == 4) {
+    if (p.rpw == 8) { if (sd == MIQ_F16) MIQ_GEMV_FUSED(4, 8, __half); MIQ_GEMV_FUSED(4, 8, float); }
+    if (sd == MIQ_F16) MIQ_GEMV_FUSED(4, 4, __half);
+    MIQ_GEMV_FUSED(4, 4, float);
+  }
+  if (p.rpw == 8) { if (sd == MIQ_F16) MIQ_GEMV_FUSED(8, 8, __half); MIQ_GEMV_FUSED(8, 8, float); }
+  if (sd == MIQ_F16) MIQ_GEMV_FUSED(8, 4, __half);
+  MIQ_GEMV_FUSED(8, 4, float);
 #undef MIQ_GEMV_FUSED
 }
 

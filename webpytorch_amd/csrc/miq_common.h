@@ -12,6 +12,8 @@ namespace miq {
 void set_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// MIQ_OK if `bytes` of dynamic LDS fit one workgroup on the current device, else an error.
+int require_lds(const char* what, size_t bytes);
 
 #define MIQ_REQUIRE(cond, code, ...)              \
   do {                                            \

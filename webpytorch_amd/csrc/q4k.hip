@@ -261,13 +261,8 @@ static int launch_q4k(const void* x, const uint8_t* w, const float* bias, void* 
   const size_t lds = (size_t)MR * K * sizeof(XT) + (size_t)MR * (K / 32) * 4;
   MIQ_REQUIRE(lds <= 160 * 1024, MIQ_ERR_UNSUPPORTED, "q4k_gemv: K=%d too large to stage", K);
   if (lds > 64 * 1024) {
-    static bool raised = false;  // once per instantiation
-    if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      MIQ_REQUIRE(e == hipSuccess, MIQ_ERR_HIP, "q4k_gemv: LDS attribute: %s", hipGetErrorString(e));
-      raised = true;
-    }
+    const int rc = require_lds("q4k_gemv", lds);
+    if (rc) return rc;
   }
   const int groups = (N + R - 1) / R;
   int wgs = (groups + 3) / 4;

@@ -49,27 +49,34 @@ class GenResult:
 
 
 def _cat_layers(parts, gs, bits):
-    """Concatenate AutoGPTQ layers that share K along the output dimension."""
-    qw = np.concatenate([np.asarray(p["qweight"]) for p in parts], axis=1)
-    qz = np.concatenate([np.asarray(p["qzeros"]) for p in parts], axis=1)
-    sc = np.concatenate([np.asarray(p["scales"]) for p in parts], axis=1)
-    bias = None
+    """Concatenate GPTQ layers that share K along the output dimension, on the device."""
+    zoffs = {float(p.get("zoff", 1.0)) for p in parts}
+    if len(zoffs) != 1:
+        raise ValueError("fused projections must share their zero offset")
+    cat = lambda key, dt=None: torch.cat([core.to_device(p[key], dt) for p in parts], dim=1)  # noqa: E731
+    out = {"qweight": cat("qweight", torch.int32), "qzeros": cat("qzeros", torch.int32), "zoff": zoffs.pop()}
+    sdt = {core.to_device(p["scales"]).dtype for p in parts}
+    out["scales"] = cat("scales", torch.float32 if torch.float32 in sdt else None)
     if any(p.get("bias") is not None for p in parts):
-        bias = np.concatenate([np.asarray(p["bias"], np.float32) if p.get("bias") is not None
-                               else np.zeros(np.asarray(p["qweight"]).shape[1], np.float32) for p in parts])
-    return {"qweight": qw, "qzeros": qz, "scales": sc, "bias": bias}
+        out["bias"] = torch.cat([core.to_device(p["bias"], torch.float32) if p.get("bias") is not None
+                                 else torch.zeros(int(np.shape(p["qweight"])[1]), dtype=torch.float32,
+                                                  device=core.device()) for p in parts])
+    return out
 
 
 class _Lin:
-    """Device tensors of one (possibly fused) GPTQ linear."""
+    """Device tensors of one (possibly fused) GPTQ linear. The zero offset is the layer's own:
+    1 for AutoGPTQ tensors (stored zero - 1), 0 for layers quantized on load."""
 
-    def __init__(self, d, K, gs, bits, zoff):
+    def __init__(self, d, K, gs, bits, zoff=None):
         self.qweight = core.to_device(d["qweight"], torch.int32)
         self.qzeros = core.to_device(d["qzeros"], torch.int32)
         self.scales = core.to_device(d["scales"])
-        self.bias = None if d.get("bias") is None else core.to_device(np.asarray(d["bias"], np.float32))
+        b = d.get("bias")
+        self.bias = None if b is None else core.to_device(b, torch.float32)
         self.K, self.N = K, int(self.qweight.shape[1])
-        self.gs, self.bits, self.zoff = gs, bits, zoff
+        self.gs, self.bits = gs, bits
+        self.zoff = float(d.get("zoff", 1.0) if zoff is None else zoff)
 
 
 class CausalLM:
@@ -95,10 +102,10 @@ class CausalLM:
         self.layers = []
         for lay in weights["layers"]:
             self.layers.append({
-                "qkv": _Lin(_cat_layers([lay["q"], lay["k"], lay["v"]], self.gs, self.bits), self.H, self.gs, self.bits, 1.0),
-                "o": _Lin(lay["o"], self.NH * self.HD, self.gs, self.bits, 1.0),
-                "gate_up": _Lin(_cat_layers([lay["gate"], lay["up"]], self.gs, self.bits), self.H, self.gs, self.bits, 1.0),
-                "down": _Lin(lay["down"], self.I, self.gs, self.bits, 1.0),
+                "qkv": _Lin(_cat_layers([lay["q"], lay["k"], lay["v"]], self.gs, self.bits), self.H, self.gs, self.bits),
+                "o": _Lin(lay["o"], self.NH * self.HD, self.gs, self.bits),
+                "gate_up": _Lin(_cat_layers([lay["gate"], lay["up"]], self.gs, self.bits), self.H, self.gs, self.bits),
+                "down": _Lin(lay["down"], self.I, self.gs, self.bits),
                 "in_ln": core.to_device(np.asarray(lay["in_ln"], np.float32)),
                 "post_ln": core.to_device(np.asarray(lay["post_ln"], np.float32)),
             })
@@ -122,6 +129,20 @@ class CausalLM:
         takes the model's declared context, capped by a 2 GiB KV-cache budget."""
         from . import checkpoint
         w, declared = checkpoint.gptq_weights(path)
+        c = w["cfg"]
+        return cls(w, checkpoint.auto_lmax(lmax, declared, c["L"], c["NKV"], c["HD"]), fused, persistent)
+
+    @classmethod
+    def from_fp16(cls, path, lmax=None, quantize=None, fused=True, persistent=None):
+        """Load a plain fp16/bf16 HuggingFace safetensors directory, quantizing every linear to
+        int`quantize` (4 or 8) on the device as it loads (`webtorch/llm.py:1221-1257`: group
+        size 128, zero offset 0, fp32 scales; the tied head as `_quantize_head`). Unquantized
+        fp16 execution (`quantize=None` in the reference) is not part of this library."""
+        if quantize is None:
+            raise NotImplementedError("unquantized fp16 execution is not part of this library: "
+                                      "pass quantize=4 or quantize=8 (dtype='int4' / 'int8')")
+        from . import checkpoint
+        w, declared = checkpoint.fp16_weights(path, int(quantize))
         c = w["cfg"]
         return cls(w, checkpoint.auto_lmax(lmax, declared, c["L"], c["NKV"], c["HD"]), fused, persistent)
 
@@ -167,10 +188,12 @@ class CausalLM:
         if self.persistent is False or not self.fused:
             return
         lays = self.layers
-        fp16 = all(lay[k].scales.dtype == torch.float16 for lay in lays for k in ("qkv", "o", "gate_up", "down"))
-        if not fp16 or self.head.scales.dtype != torch.float32:
+        lins = [lay[k] for lay in lays for k in ("qkv", "o", "gate_up", "down")]
+        fp16 = all(q.scales.dtype == torch.float16 for q in lins)
+        one_zoff = len({q.zoff for q in lins}) == 1
+        if not fp16 or not one_zoff or self.head.scales.dtype != torch.float32:
             if self.persistent:
-                raise ValueError("persistent decode needs fp16 layer scales and an fp32-scaled head")
+                raise ValueError("persistent decode needs fp16 layer scales, one zero offset and an fp32-scaled head")
             return
         grid, wsb = ctypes.c_int(0), ctypes.c_size_t(0)
         rc = _lib.lib().miq_decode_persistent_plan(self.L, self.H, self.NH, self.NKV, self.HD, self.I, self.V,
@@ -331,3 +354,36 @@ class CausalLM:
         toks = [int(t) for t in self.history[:max_new].cpu().numpy()]
         rate = (max_new - 1) / dt if max_new > 1 and dt > 0 else 0.0
         return GenResult("", toks, ttft, rate)
+
+
+class AutoModelForCausalLM:
+    """Entry point with the reference SDK's signature (`webtorch/_sdk.py:72-115`)."""
+
+    @staticmethod
+    def from_pretrained(path, dtype="auto", bits=None, lmax=None, weights="native"):
+        """Load a decoder for the quantized engine, dispatching on `dtype` as the reference does
+        (`AutoModelForCausalLM._load_raw`, `webtorch/_sdk.py:98-115`):
+
+        * a directory whose config.json has `quantization_config` (AutoGPTQ int4/int8) loads at
+          its own stored bits whatever `dtype` says (`from_gptq`);
+        * a plain fp16/bf16 directory with dtype "int4" / "int8" is quantized on load
+          (`from_fp16(quantize=4|8)`: group size 128, asymmetric, zero offset 0);
+        * a `.gguf` file loads through `from_gguf` ("auto" keeps the width the file stores,
+          "int4" / "int8" requantize, `bits` overrides, `weights` as in the reference).
+
+        Unquantized execution ("fp16", or "auto" on a plain fp16 directory) is not part of this
+        library and raises NotImplementedError. Unlike the reference this call is synchronous
+        and does not cache loaded models."""
+        p = str(path).rstrip("/")
+        if dtype not in ("auto", "fp16", "int4", "int8"):
+            raise ValueError("dtype must be 'auto', 'fp16', 'int4' or 'int8', got %r" % (dtype,))
+        if p.endswith(".gguf"):
+            if dtype == "fp16":
+                raise NotImplementedError("unquantized fp16 execution is not part of this library")
+            gb = 8 if dtype == "int8" else (4 if dtype == "int4" else bits)
+            return CausalLM.from_gguf(p, lmax=lmax, bits=gb, weights=weights)
+        from . import checkpoint
+        if checkpoint.is_quantized_dir(p):
+            return CausalLM.from_gptq(p, lmax=lmax)
+        q = {"int4": 4, "int8": 8}.get(dtype)
+        return CausalLM.from_fp16(p, lmax=lmax, quantize=q)

@@ -207,3 +207,31 @@ def decoder_weights(seed, L=24, H=896, NH=14, NKV=2, HD=64, I=4864, V=151936, gs
 
 def prompt_ids(seed, T=64, V=151936):
     return rng(seed, "prompt").integers(0, V, size=T).astype(np.int64)
+
+
+def fp16_decoder(seed, L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, eps=1e-6, theta=1e6, max_pos=4096,
+                 **_):
+    """A plain (unquantized) fp16 Qwen2-shaped model as a HuggingFace directory holds it: the
+    tensors by their HF names, (out, in) projection weights ~N(0, 1/in), q/k/v biases, RMSNorm
+    weights near 1, embeddings ~N(0, 0.02**2) with the head tied to them, and the config.json
+    fields. Returns {"tensors": {name: fp16 array}, "config": dict}."""
+    t = {"model.embed_tokens.weight": (rng(seed, "embed").standard_normal((V, H)) * 0.02).astype(np.float16),
+         "model.norm.weight": (1.0 + 0.02 * rng(seed, "final_norm").standard_normal(H)).astype(np.float16)}
+    projs = (("self_attn.q_proj", NH * HD, H, True), ("self_attn.k_proj", NKV * HD, H, True),
+             ("self_attn.v_proj", NKV * HD, H, True), ("self_attn.o_proj", H, NH * HD, False),
+             ("mlp.gate_proj", I, H, False), ("mlp.up_proj", I, H, False), ("mlp.down_proj", H, I, False))
+    for i in range(L):
+        p = "model.layers.%d." % i
+        for nm, n_out, n_in, bias in projs:
+            t[p + nm + ".weight"] = (rng(seed, p + nm).standard_normal((n_out, n_in)) / np.sqrt(n_in)).astype(np.float16)
+            if bias:
+                t[p + nm + ".bias"] = (rng(seed, p + nm + ".bias").standard_normal(n_out) * 0.02).astype(np.float16)
+        t[p + "input_layernorm.weight"] = (1.0 + 0.02 * rng(seed, p + "in_ln").standard_normal(H)).astype(np.float16)
+        t[p + "post_attention_layernorm.weight"] = (
+            1.0 + 0.02 * rng(seed, p + "post_ln").standard_normal(H)).astype(np.float16)
+    cfg = {"architectures": ["Qwen2ForCausalLM"], "model_type": "qwen2", "hidden_size": H,
+           "intermediate_size": I, "num_hidden_layers": L, "num_attention_heads": NH,
+           "num_key_value_heads": NKV, "head_dim": HD, "vocab_size": V, "rms_norm_eps": eps,
+           "rope_theta": theta, "tie_word_embeddings": True, "max_position_embeddings": max_pos,
+           "torch_dtype": "float16"}
+    return {"tensors": t, "config": cfg}
