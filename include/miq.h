@@ -200,21 +200,30 @@ int miq_moe_route_bytes(int T, int E, int k, size_t* bytes);
 int miq_moe_route(const float* logits, int T, int E, int k, int norm_topk, void* route,
                   size_t route_bytes, void* stream);
 
-/* h = silu(x @ Wgate[e]) * (x @ Wup[e]) for each sorted slot's token and expert, x fp16 [T][H];
- * h is fp32-accurate, stored as two fp16 planes [2][T*k][I]: hi = fp16(h), lo = fp16(h - hi).
+/* h[T*k][I] fp32 = silu(x @ Wgate[e]) * (x @ Wup[e]) for each sorted slot's token and expert;
+ * x [T][H] fp16 (x_dtype MIQ_F16) or fp32 (MIQ_F32). fp32 x enters the fp16 matrix cores as two
+ * fp16 planes of each row scaled by a power of two (hi = fp16(x 2^s), lo = fp16(x 2^s - hi): about
+ * 22 significant bits relative to the row's largest value, no fp16 range limit). Also records
+ * each slot row's max |h| in the route buffer for miq_moe_down (route must come from
+ * miq_moe_route of the same call sequence).
  * Replaces: the per-expert `silu(exp["gate"](xe)) * exp["up"](xe)` of `moe_mlp`
  * (webtorch/lm_engine.py:310-316). */
-int miq_moe_gate_up(const void* x, const void* route, int T, int E, int k, const int32_t* qw_gate,
-                    const int32_t* qz_gate, const void* sc_gate, const int32_t* qw_up,
-                    const int32_t* qz_up, const void* sc_up, int scales_dtype, void* h, int H, int I,
-                    int gs, int bits, float zero_offset, void* stream);
+int miq_moe_gate_up(const void* x, int x_dtype, void* route, int T, int E, int k, const int32_t* qw_gate,
+                    const int32_t* qz_gate, const void* sc_gate, const int32_t* qw_up, const int32_t* qz_up,
+                    const void* sc_up, int scales_dtype, float* h, int H, int I, int gs, int bits,
+                    float zero_offset, void* stream);
 
-/* y[T*k][H] fp32 = routing weight * ((hi + lo) @ Wdown[e]) per sorted slot, h as written by
- * miq_moe_gate_up.
+/* y[T*k][H] fp32 = routing weight * (h @ Wdown[e]) per sorted slot, h as written by
+ * miq_moe_gate_up (fp32, entering the matrix cores as row-scaled fp16 hi and lo planes).
  * Replaces: `exp["down"](...)` and `ye * w` of `moe_mlp` (webtorch/lm_engine.py:316-318). */
-int miq_moe_down(const void* h, const void* route, int T, int E, int k, const int32_t* qw,
+int miq_moe_down(const float* h, void* route, int T, int E, int k, const int32_t* qw,
                  const int32_t* qz, const void* sc, int scales_dtype, float* y, int I, int H, int gs,
                  int bits, float zero_offset, void* stream);
+
+/* out[T][H] += ys * sigmoid(gate_logits[t]) (gate_logits fp32 [T], or NULL: out += ys), the
+ * shared expert's contribution.
+ * Replaces: the shared-expert tail of `moe_mlp` (webtorch/lm_engine.py:322-328). */
+int miq_moe_shared_add(float* out, const float* ys, const float* gate_logits, int T, int H, void* stream);
 
 /* out[T][H] fp32 = sum of each token's k slot outputs in ascending expert order, from zero.
  * Replaces: the scatter-add `acc[rows] = acc[rows] + ye` of `moe_mlp`

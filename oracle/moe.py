@@ -34,9 +34,10 @@ def silu(x):
     return x * (1.0 / (1.0 + np.exp(-x)))
 
 
-def moe_mlp_np(x, logits, experts, top_k, norm_topk_prob=True):
+def moe_mlp_np(x, logits, experts, top_k, norm_topk_prob=True, shared=None, shared_gate=None):
     """x (T, H); logits (T, E); experts: list of {gate, up, down} callables (T', K) -> (T', N)
-    float32. Returns (T, H) float32."""
+    float32; shared: {gate, up, down} callables or None; shared_gate: callable (T, H) -> (T, 1)
+    or None (`webtorch/lm_engine.py:322-328`). Returns (T, H) float32."""
     x = np.asarray(x, np.float32)
     idx, w = route(logits, top_k, norm_topk_prob)
     out = np.zeros((x.shape[0], x.shape[1]), np.float32)
@@ -49,13 +50,27 @@ def moe_mlp_np(x, logits, experts, top_k, norm_topk_prob=True):
         ye = ex["down"](silu(ex["gate"](xe)) * ex["up"](xe))
         ye = ye * w[rows, slot].astype(np.float32).reshape(-1, 1)
         out[rows] = out[rows] + ye
+    if shared is not None:
+        ys = shared["down"](silu(shared["gate"](x)) * shared["up"](x))
+        if shared_gate is not None:
+            g = 1.0 / (1.0 + np.exp(-np.asarray(shared_gate(x), np.float32)))
+            ys = ys * g
+        out = out + ys
     return out
+
+
+def gptq_linear(d, zoff=1.0, n_out=None):
+    """A GPTQ layer dict as a CPU callable x -> x @ W (+ bias), the first n_out columns."""
+    def f(t):
+        y = gptq.gptq_matmul_np(t, d["qweight"], d["qzeros"], d["scales"], d["K"], d["N"], d["gs"],
+                                d["bits"], zoff)
+        if d.get("bias") is not None:
+            y = y + np.asarray(d["bias"], np.float32)
+        return y if n_out is None else y[:, :n_out]
+    return f
 
 
 def gptq_expert(layer_dicts):
     """Wrap AutoGPTQ expert layer dicts as CPU callables (QuantizedLinear with zero bias,
     zero_offset 1, as `QuantizedLinear.from_autogptq` builds them)."""
-    def lin(d):
-        return lambda t: gptq.gptq_matmul_np(t, d["qweight"], d["qzeros"], d["scales"], d["K"],
-                                             d["N"], d["gs"], d["bits"], 1.0)
-    return {k: lin(v) for k, v in layer_dicts.items()}
+    return {k: gptq_linear(v) for k, v in layer_dicts.items()}

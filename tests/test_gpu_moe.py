@@ -164,3 +164,84 @@ def test_moe_rejects_bad_sizes(gpu):
         core.moe_route_bytes(1024, 128, 8)
     with pytest.raises(ValueError, match="k="):
         core.moe_route_bytes(4, 8, 9)
+
+
+# ---- fp32 activations, the shared expert, long batches, non-finite rows ----------------------
+
+@pytest.fixture(scope="module")
+def small_moe():
+    return synth.moe_workload(12, T=48, H=512, E=16, I=256, top_k=4, gs=128)
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e-6, 3e5])
+def test_moe_fp32_activations(gpu, small_moe, scale):
+    """fp32 x (not fp16-representable) against the reference's fp32 multiply: the row-scaled
+    hi/lo planes keep fp32 accuracy, also for magnitudes past fp16's range (3e5 * N(0,1)) and
+    tiny ones (1e-6, fp16 subnormal)."""
+    import torch
+    from webpytorch_amd import core
+    w = small_moe
+    x = (np.random.default_rng(5).standard_normal((48, 512)) * scale).astype(np.float32)
+    ref = moe.moe_mlp_np(x, w["logits"], [moe.gptq_expert(e) for e in w["experts"]], 4)
+    got = core.MoEExperts(w["experts"])(torch.from_numpy(x).cuda(), torch.from_numpy(w["logits"]).cuda(), 4)
+    _check(got.cpu().numpy(), ref, rel=2e-5)
+
+
+def test_moe_shared_expert_fp32(gpu, small_moe):
+    """The shared expert with its sigmoid gate (Qwen-style), fp32 throughout, against the
+    oracle's `moe_mlp` tail (`webtorch/lm_engine.py:322-328`); the one-output gate linear is
+    quantized from a float weight with padding (from_linear)."""
+    import torch
+    from webpytorch_amd import core
+    w = small_moe
+    H = 512
+    shared = {n: synth.gptq_layer(13, *(kn if n != "down" else kn[::-1]), 128, 4, name="sh." + n)
+              for n, kn in (("gate", (H, 384)), ("up", (H, 384)), ("down", (H, 384)))}
+
+    class Lin:
+        pass
+    sg = Lin()
+    sg.weight = (np.random.default_rng(7).standard_normal((H, 1)) * 0.05).astype(np.float32)
+    sg.bias = np.array([0.1], np.float32)
+    sgq = core.QuantizedLinear.from_linear(sg, group_size=128, bits=4)
+    x = np.random.default_rng(6).standard_normal((48, H)).astype(np.float32)
+    lay = {"moe": {"gate": lambda t: torch.from_numpy(w["logits"]).cuda(), "experts": w["experts"], "top_k": 4,
+                   "norm_topk_prob": True, "shared": shared, "shared_gate": sgq}}
+    got = core.moe_mlp(None, lay, torch.from_numpy(x).cuda()).cpu().numpy()
+    from oracle import gptq
+    qw, qz, sc, _, _ = gptq.gptq_quantize(np.pad(sg.weight, ((0, 0), (0, 7))), 128, 4)
+    gate_fn = moe.gptq_linear({"qweight": qw, "qzeros": qz, "scales": sc, "K": H, "N": 8, "gs": 128, "bits": 4,
+                               "bias": np.pad(sg.bias, (0, 7))}, zoff=0.0, n_out=1)
+    ref = moe.moe_mlp_np(x, w["logits"], [moe.gptq_expert(e) for e in w["experts"]], 4,
+                         shared=moe.gptq_expert(shared), shared_gate=gate_fn)
+    _check(got, ref, rel=2e-5)
+    # the gate matters: without it the result differs
+    lay2 = dict(lay["moe"], shared_gate=None)
+    lay2.pop("_shared", None)
+    lay2.pop("_grouped", None)
+    nog = core.moe_mlp(None, {"moe": lay2}, torch.from_numpy(x).cuda()).cpu().numpy()
+    assert np.abs(nog - got).max() > 1e-3
+
+
+def test_moe_more_picks_than_one_routing_pass(gpu):
+    """T * k = 4800 > 4096: routed in blocks of tokens, identical to the oracle."""
+    import torch
+    from webpytorch_amd import core
+    w = synth.moe_workload(14, T=600, H=256, E=16, I=128, top_k=8, gs=128)
+    ref = moe.moe_mlp_np(w["x"], w["logits"], [moe.gptq_expert(e) for e in w["experts"]], 8)
+    got = core.MoEExperts(w["experts"])(torch.from_numpy(w["x"]).cuda(), torch.from_numpy(w["logits"]).cuda(), 8)
+    _check(got.cpu().numpy(), ref, rel=1e-5)
+
+
+def test_moe_nan_row_stays_in_its_token(gpu, small_moe):
+    import torch
+    from webpytorch_amd import core
+    w = small_moe
+    x = np.random.default_rng(8).standard_normal((48, 512)).astype(np.float32)
+    x[3, 100] = np.nan
+    ref = moe.moe_mlp_np(x, w["logits"], [moe.gptq_expert(e) for e in w["experts"]], 4)
+    got = core.MoEExperts(w["experts"])(torch.from_numpy(x).cuda(), torch.from_numpy(w["logits"]).cuda(),
+                                        4).cpu().numpy()
+    assert np.isnan(ref[3]).all() and np.isnan(got[3]).all()
+    keep = np.arange(48) != 3
+    _check(got[keep], ref[keep], rel=2e-5)

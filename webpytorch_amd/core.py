@@ -126,6 +126,63 @@ def _scales(s):
     return t if t.dtype in (torch.float16, torch.float32) else t.float()
 
 
+# ---- first-use known-answer checks ---------------------------------------------------
+# The reference multiplies one random block per (ggml type, kernel mode) the first time that
+# kernel runs and raises if it disagrees with the dequantizer (`_ggml_selfcheck`,
+# `webtorch/_core.py:3684-3717`), so that a broken build raises instead of producing plausible
+# numbers. The same is done here for every product path, on the device: the kernel's result for
+# a small random problem against the exact fp32 dequant (its own kernel, bit-exact) times x,
+# accumulated in float64. Each (path, device) is checked once, outside graph capture.
+_CHECKED = set()
+SELFCHECK_RTOL = 1e-4
+
+
+def _first_use(key):
+    """True (and the key recorded) if `key` has not been checked on this device yet and the
+    current stream is not capturing a graph (a check reads its result back to the host)."""
+    k = key + (torch.cuda.current_device(),)
+    if k in _CHECKED or torch.cuda.is_current_stream_capturing():
+        return False
+    _CHECKED.add(k)
+    return True
+
+
+def _reference_product(x, W):
+    """x (M, K) @ W (K, N) in float64 on the device."""
+    return x.double() @ W.double()
+
+
+def _check_close(what, got, want):
+    err = float((got.double() - want).abs().max() / (want.abs().max() + 1e-30))
+    if not err < SELFCHECK_RTOL:
+        raise RuntimeError("%s is wrong on this device (rel err %.3g against the exact dequant)" % (what, err))
+
+
+def _selfcheck_gptq(M, xdt, bits, gs):
+    """Known-answer check of the kernel `_gptq_matmul` picks for M rows of `xdt` activations."""
+    g = np.random.default_rng(0x5e1f + M + 31 * bits)
+    K, N = 256, 256
+    per = 32 // bits
+    qw = torch.from_numpy(g.integers(0, 1 << 32, (K // per, N), dtype=np.uint64).astype(np.uint32).view(np.int32))
+    qz = torch.from_numpy(g.integers(0, 1 << 32, (K // gs, N // per), dtype=np.uint64).astype(np.uint32).view(np.int32))
+    sc = torch.from_numpy((np.abs(g.standard_normal((K // gs, N))) * 0.01 + 1e-3).astype(np.float16))
+    x = torch.from_numpy(g.standard_normal((M, K)).astype(np.float32)).to(device(), xdt)
+    qw, qz, sc = qw.to(device()), qz.to(device()), sc.to(device())
+    got = _gptq_matmul(x, qw, qz, sc, K, N, gs, bits, 1.0, out_dtype=torch.float32, _check=False)
+    want = _reference_product(x, gptq_dequant(qw, qz, sc, K, N, gs, bits, 1.0))
+    _check_close("the GPTQ int%d product kernel for %d rows of %s" % (bits, M, str(xdt).replace("torch.", "")),
+                 got, want)
+
+
+def _gptq_path(M, xdt):
+    """The product kernel class `_gptq_matmul` runs for M rows (one check per class)."""
+    if M == 1:
+        return 1
+    if M <= GEMV_MAX_M or xdt != torch.float16:
+        return 4
+    return 12 if M <= 16 else 40
+
+
 # ---- GPTQ ----------------------------------------------------------------------------
 def gptq_dequant(qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, g_idx=None):
     """Full fp32 weight (K, N); bit-exact with the reference's dequant for integer zoff."""
@@ -136,12 +193,15 @@ def gptq_dequant(qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, g_idx=None):
 
 
 def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=None, perm=None,
-                 out_dtype=None, out=None, ws=None):
+                 out_dtype=None, out=None, ws=None, _check=True):
     """xf (M, K) @ dequant(W) (+ bias) -> (M, N) on the current stream
     (`webtorch/_core.py:4008-4043`). Up to GEMV_MAX_M rows run the split-K GEMV; more rows
     of fp16 activations run the matrix-core GEMM (fp32 activations stay on the GEMV, which
-    keeps them in fp32)."""
+    keeps them in fp32). The first call of each kernel class on a device runs its
+    known-answer check (RuntimeError if it fails)."""
     M = int(xf.shape[0])
+    if _check and M and 256 % gs == 0 and _first_use(("gptq", bits, gs, _gptq_path(M, xf.dtype), xf.dtype)):
+        _selfcheck_gptq(_gptq_path(M, xf.dtype), xf.dtype, bits, gs)
     od = out_dtype or torch.float32
     if out is None:
         out = torch.empty((M, N), dtype=od, device=xf.device)
@@ -354,7 +414,29 @@ def rows_from_transposed(words, n, rowb):
     return rows[:, :rowb].contiguous()
 
 
-def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32, out=None):
+def _ggml_selfcheck(type_name, mode):
+    """Multiply two random blocks of `type_name` with the kernel of `mode` (rows 1, 2, or 0 for
+    3 and more) and compare against the device's exact dequant of the same bytes times x in
+    float64; RuntimeError on a mismatch (`_ggml_selfcheck`, `webtorch/_core.py:3684-3717`).
+    Random bytes are legal blocks of every type; draws whose fp16 fields decode to Inf/NaN or
+    huge values are skipped, as the reference does."""
+    vals, blk, _ = _NATIVE_TYPES[type_name]
+    for seed in range(32):
+        g = np.random.default_rng(seed)
+        raw = torch.from_numpy(g.integers(0, 256, (2, blk), dtype=np.uint8)).to(device())
+        W = ggml_dequant(raw.reshape(-1), type_name, 2).reshape(2, vals)
+        if bool(torch.isfinite(W).all()) and float(W.abs().max()) < 1e4:
+            break
+    else:
+        raise RuntimeError("could not draw a finite %s block to self-check against" % type_name)
+    M = mode if mode else 3
+    x = torch.from_numpy(g.standard_normal((M, vals)).astype(np.float32)).to(device())
+    got = ggml_matmul(x, raw, type_name, vals, 2, _check=False)
+    _check_close("the native ggml %s kernel for %s" % ("gemv" if mode else "gemm", type_name), got,
+                 _reference_product(x, W.t()))
+
+
+def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32, out=None, _check=True):
     """xf (M, K) @ W.T -> (M, N), decoding ggml blocks in the kernel
     (`webtorch/_core.py:3720-3734`).
 
@@ -377,6 +459,9 @@ def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32,
                                                                            int(N) * rowb))
     xf = aligned16(as_activation(xf).contiguous())
     M = int(xf.shape[0])
+    mode = M if M <= 2 else 0
+    if _check and M and _first_use(("ggml", type_name, mode)):
+        _ggml_selfcheck(type_name, mode)
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=xf.device)
     if type_name == "Q4_K":
@@ -437,12 +522,7 @@ class MoEExperts:
     stream with no host synchronisation."""
 
     def __init__(self, experts):
-        def as_ql(d):
-            if isinstance(d, QuantizedLinear):
-                return d
-            return QuantizedLinear.from_autogptq(d["qweight"], d["qzeros"], d["scales"], d.get("bias"),
-                                                 d["gs"], d["bits"])
-        exps = [{k: as_ql(e[k]) for k in ("gate", "up", "down")} for e in experts]
+        exps = [{k: _as_linear(e[k]) for k in ("gate", "up", "down")} for e in experts]
         g0 = exps[0]["gate"]
         self.E = len(exps)
         self.H, self.I = g0.Kp, g0.Np
@@ -463,38 +543,87 @@ class MoEExperts:
                                               for e in exps]).contiguous()
                                  for a in ("qweight", "qzeros", "scales"))
 
+    # tokens per routing pass: the router handles T * k <= MAX_ROUTED picks at a time
+    MAX_ROUTED = 4096
+
     def __call__(self, x, logits, top_k, norm_topk_prob=True):
-        """x (T, H) -> (T, H) float32; logits (T, E) router outputs."""
+        """x (T, H) fp16 or fp32 -> (T, H) float32; logits (T, E) router outputs. fp32 x stays
+        fp32 (it enters the matrix cores as row-scaled fp16 hi/lo planes); longer batches are
+        routed in blocks of MAX_ROUTED // top_k tokens (tokens are independent)."""
         xt = as_activation(x)
         T = int(xt.shape[0])
-        xh = aligned16(xt.reshape(T, self.H).to(torch.float16).contiguous())
+        xt = aligned16(xt.reshape(T, self.H).contiguous())
         lg = as_activation(logits).float().reshape(T, self.E).contiguous()
-        out = torch.empty((T, self.H), dtype=torch.float32, device=xh.device)
-        if T == 0:
-            return out
+        out = torch.empty((T, self.H), dtype=torch.float32, device=xt.device)
         k = int(top_k)
-        route = torch.empty(moe_route_bytes(T, self.E, k), dtype=torch.uint8, device=xh.device)
-        h = torch.empty((2, T * k, self.I), dtype=torch.float16, device=xh.device)  # hi, lo planes
-        y = torch.empty((T * k, self.H), dtype=torch.float32, device=xh.device)
+        step = max(1, self.MAX_ROUTED // k)
+        for t0 in range(0, T, step):
+            t1 = min(T, t0 + step)
+            self._block(xt[t0:t1], lg[t0:t1], k, norm_topk_prob, out[t0:t1])
+        return out
+
+    def _block(self, xt, lg, k, norm_topk_prob, out):
+        T = int(xt.shape[0])
+        route = torch.empty(moe_route_bytes(T, self.E, k), dtype=torch.uint8, device=xt.device)
+        h = torch.empty((T * k, self.I), dtype=torch.float32, device=xt.device)
+        y = torch.empty((T * k, self.H), dtype=torch.float32, device=xt.device)
         st = stream_handle()
         sd = dtype_code(self.w["gate"][2])
+        xt = aligned16(xt)
         _lib.call("miq_moe_route", ptr(lg), T, self.E, k, int(bool(norm_topk_prob)), ptr(route), route.numel(), st)
         g, u, d = self.w["gate"], self.w["up"], self.w["down"]
-        _lib.call("miq_moe_gate_up", ptr(xh), ptr(route), T, self.E, k, ptr(g[0]), ptr(g[1]), ptr(g[2]), ptr(u[0]),
-                  ptr(u[1]), ptr(u[2]), sd, ptr(h), self.H, self.I, self.gs, self.bits, float(self.zoff), st)
+        _lib.call("miq_moe_gate_up", ptr(xt), dtype_code(xt), ptr(route), T, self.E, k, ptr(g[0]), ptr(g[1]), ptr(g[2]),
+                  ptr(u[0]), ptr(u[1]), ptr(u[2]), sd, ptr(h), self.H, self.I, self.gs, self.bits, float(self.zoff), st)
         _lib.call("miq_moe_down", ptr(h), ptr(route), T, self.E, k, ptr(d[0]), ptr(d[1]), ptr(d[2]), sd, ptr(y),
                   self.I, self.H, self.gs, self.bits, float(self.zoff), st)
         _lib.call("miq_moe_combine", ptr(y), ptr(route), T, self.E, k, ptr(out), self.H, st)
         self.last_route = route
+
+
+class SharedExpert:
+    """The optional always-on expert of a Qwen-style MoE layer with its sigmoid gate
+    (`webtorch/lm_engine.py:322-328`): ys = down(silu(gate(x)) * up(x)) in fp32, times
+    sigmoid(shared_gate(x)) if present, added to the routed output. gate and up run as one fused
+    GEMM (their columns concatenated), SwiGLU and the gated add are kernels."""
+
+    def __init__(self, shared, shared_gate=None):
+        g, u, dn = (_as_linear(shared[n]) for n in ("gate", "up", "down"))
+        if (g.Kp, g.Np, g.gs, g.bits, g.zero_offset) != (u.Kp, u.Np, u.gs, u.bits, u.zero_offset) or g.perm is not None:
+            raise ValueError("shared gate and up must share shape, group size, bits and zero offset")
+        sdt = torch.float32 if torch.float32 in (g.scales.dtype, u.scales.dtype) else g.scales.dtype
+        self.gate_up = QuantizedLinear(torch.cat([g.qweight, u.qweight], 1), torch.cat([g.qzeros, u.qzeros], 1),
+                                       torch.cat([g.scales.to(sdt), u.scales.to(sdt)], 1),
+                                       torch.cat([g.bias, u.bias]), g.Kt, g.Nt + u.Nt, g.Kp, g.Np + u.Np, g.gs, g.bits,
+                                       g.zero_offset)
+        self.I = g.Np
+        self.down = dn
+        self.gate = None if shared_gate is None else _as_linear(shared_gate)
+
+    def add_to(self, out, x):
+        """out (T, H) fp32 += the gated shared-expert output for x (T, H)."""
+        T = int(x.shape[0])
+        gu = self.gate_up(x)                                   # (T, 2I) fp32
+        act = torch.empty((T, self.I), dtype=torch.float32, device=gu.device)
+        st = stream_handle()
+        _lib.call("miq_silu_mul", ptr(gu), ptr(act), T, self.I, st)
+        ys = self.down(act).contiguous()                       # (T, H) fp32
+        gl = None if self.gate is None else self.gate(x).reshape(T).contiguous()
+        _lib.call("miq_moe_shared_add", ptr(out), ptr(ys), ptr(gl), T, int(out.shape[1]), st)
         return out
+
+
+def _as_linear(d):
+    if isinstance(d, QuantizedLinear):
+        return d
+    return QuantizedLinear.from_autogptq(d["qweight"], d["qzeros"], d["scales"], d.get("bias"), d["gs"], d["bits"])
 
 
 def moe_mlp(lm, lay, x):
     """Sparse MoE MLP, drop-in for `moe_mlp(lm, lay, x)` (`webtorch/lm_engine.py:294-329`) with
     the same `lay["moe"]` schema: gate (router linear), experts [{gate, up, down}], top_k,
     norm_topk_prob, shared {gate, up, down} | None, shared_gate | None. Routing runs on the
-    device (the reference reads the router logits back to the host); the stacked experts are
-    cached in the dict under "_grouped". The activations enter the expert GEMMs as fp16."""
+    device (the reference reads the router logits back to the host); the stacked experts (and
+    the fused shared expert) are cached in the dict. fp32 activations stay fp32 throughout."""
     m = lay["moe"]
     xt = as_activation(x)
     T = int(xt.shape[0])
@@ -503,11 +632,9 @@ def moe_mlp(lm, lay, x):
     if ex is None:
         ex = m["_grouped"] = MoEExperts(m["experts"])
     out = ex(xt, logits, m["top_k"], m.get("norm_topk_prob", True))
-    s = m.get("shared")
-    if s:
-        g = s["gate"](xt).float()
-        ys = s["down"]((g * torch.sigmoid(g) * s["up"](xt).float()).to(xt.dtype)).float()
-        if m.get("shared_gate") is not None:
-            ys = ys * torch.sigmoid(m["shared_gate"](xt).float())
-        out = out + ys.reshape(T, -1)
+    if m.get("shared"):
+        se = m.get("_shared")
+        if se is None:
+            se = m["_shared"] = SharedExpert(m["shared"], m.get("shared_gate"))
+        se.add_to(out, xt.reshape(T, -1))
     return out

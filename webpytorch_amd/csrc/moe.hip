@@ -6,16 +6,23 @@
 //            per token its k experts in ascending order with fp32 weights; per expert the list
 //            of its (token, weight) slots in ascending token order ("sorted slots"); and a
 //            table of row tiles (expert, first slot, rows) that the GEMMs walk.
-//   gate_up  h[slot] = silu(x[token] @ Wg[e]) * (x[token] @ Wu[e])   (fp32, stored as fp16 hi + lo)
+//   gate_up  h[slot] = silu(x[token] @ Wg[e]) * (x[token] @ Wu[e])   (fp32)
 //   down     y[slot] = w[slot] * (h[slot] @ Wd[e])                    (fp32)
 //   combine  out[t] = sum over t's experts in ascending order of y[slot]  (fp32)
 //
 // The combine order (experts ascending, starting from zero) and the fp32 weight multiply are the
 // reference's (`webtorch/lm_engine.py:294-333`). The GEMMs use the prefill GEMM's exact
 // dequantization and MFMA mapping (see gptq_gemm.hip); a workgroup takes one row tile of one
-// expert (up to kMoeBM rows) and 256 output columns. The intermediate h keeps fp32 accuracy
-// through the fp16 matrix cores as two fp16 halves, hi = fp16(h) and lo = fp16(h - hi)
-// (together exact to about 22 bits); the down GEMM multiplies both by the same weights.
+// expert (up to kMoeBM rows) and 256 (down) or 128 (gate_up) output columns.
+//
+// fp32 activations (the intermediate h always; x when the caller's is fp32) go through the fp16
+// matrix cores as two fp16 planes of a row scaled by a power of two: v = a * 2^s with s chosen so
+// the row's largest |a| is just below 2^15, hi = fp16(v), lo = fp16(v - hi), both multiplied by
+// the same weight fragments and the sum scaled back by 2^-s (exact). That keeps about 22
+// significant bits relative to the row's largest value with no fp16 range limit. The row scale
+// of x comes from a small pass over x; that of h from the maxima the gate_up epilogue takes
+// (an atomic max per row and workgroup into a per-slot word the router zeroed). NaN and
+// infinite rows keep scale 1, so they propagate.
 #include <algorithm>
 #include <type_traits>
 
@@ -28,7 +35,7 @@ constexpr int kMoeMaxTK = 4096;  // T * k handled by the single-workgroup router
 
 // Offsets (in 4-byte words) of the route buffer's arrays.
 struct RouteLayout {
-  size_t topk_e, topk_w, slot_of, sorted_tok, sorted_w, expert_off, ntiles, tiles, words;
+  size_t topk_e, topk_w, slot_of, sorted_tok, sorted_w, expert_off, ntiles, tiles, slot_max, x_scale, words;
   int max_tiles;
 };
 
@@ -44,8 +51,39 @@ __host__ __device__ inline RouteLayout route_layout(int T, int E, int k) {
   L.expert_off = L.sorted_w + tk;
   L.ntiles = L.expert_off + E + 1;
   L.tiles = (L.ntiles + 1 + 3) & ~(size_t)3;  // 16-byte aligned int4 entries
-  L.words = L.tiles + 4 * (size_t)L.max_tiles;
+  L.slot_max = L.tiles + 4 * (size_t)L.max_tiles;  // [T*k] max |h| of each slot's row (fp32 bits)
+  L.x_scale = L.slot_max + tk;                        // [T] row scale of fp32 x
+  L.words = L.x_scale + (size_t)T;
   return L;
+}
+
+// 2^s with s making m * 2^s just below 2^15 (1 for zero, NaN or infinite m): the row scale of
+// the fp16 hi/lo planes. Its inverse is row_unscale(m), also exact.
+__device__ __forceinline__ int row_scale_exp(float m) {
+  if (!(m > 0.f) || !(m <= 3.4e38f)) return 0;
+  int ex;
+  frexpf(m, &ex);  // m < 2^ex
+  return min(max(15 - ex, -100), 100);
+}
+__device__ __forceinline__ float row_scale(float m) { return ldexpf(1.f, row_scale_exp(m)); }
+__device__ __forceinline__ float row_unscale(float m) { return ldexpf(1.f, -row_scale_exp(m)); }
+
+// fp32 x rows: the largest |x| of each token, stored as the value row_scale reads.
+__global__ __launch_bounds__(256) void moe_xmax_kernel(const float* __restrict__ x, int T, int H, int E, int k,
+                                                       int* __restrict__ route) {
+  const RouteLayout L = route_layout(T, E, k);
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;  // whole waves
+  float m = 0.f;
+  for (int c = lane * 4; c < H; c += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(x + (size_t)t * H + c);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    // fmaxf drops NaN: carry it explicitly
+    if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = __int_as_float(0x7FC00000);
+  }
+  const bool nan = __ballot(m != m) != 0ull;
+  m = wave_max(m != m ? 0.f : m);
+  if (lane == 0) reinterpret_cast<float*>(route + L.x_scale)[t] = nan ? __int_as_float(0x7FC00000) : m;
 }
 
 // ------------------------------------------------------------------------------------
@@ -151,6 +189,7 @@ __global__ __launch_bounds__(1024) void moe_slots_kernel(int T, int E, int k, in
     cnt[e] = 0;
     run[e] = 0;
   }
+  for (int i = threadIdx.x; i < TK; i += blockDim.x) route[L.slot_max + i] = 0;  // gate_up's row maxima
   for (int i = threadIdx.x; i < TK; i += blockDim.x) {
     se[i] = topk_e[i];
     sw[i] = topk_w[i];
@@ -224,23 +263,27 @@ __global__ __launch_bounds__(1024) void moe_slots_kernel(int T, int E, int k, in
 }
 
 // ------------------------------------------------------------------------------------
-// Grouped GEMM over row tiles. GATE_UP: two weight sets sharing the activations, epilogue
-// h = silu(g) * u stored as fp16 hi and lo planes. Otherwise (down): one set whose activations
-// are those two planes (two MFMAs per weight fragment), epilogue y = w[slot] * acc in fp32.
-template <int BITS, int KC, bool GATE_UP, typename ST>
+// Grouped GEMM over row tiles. GATE_UP: two weight sets sharing the activations (x rows,
+// gathered through the sorted slots), epilogue h = silu(g) * u in fp32 plus each row's max |h|.
+// Otherwise (down): one set over h, epilogue y = w[slot] * acc in fp32. XF32: the activations
+// are fp32 and are staged as the row-scaled fp16 hi and lo planes (two MFMAs per weight
+// fragment); else (gate_up with fp16 x) they are staged as they are.
+template <int BITS, int KC, bool GATE_UP, bool XF32, typename ST>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(
-    const __half* __restrict__ a, const int* __restrict__ route, int T, int E, int k,
+    const void* __restrict__ a_in, int* __restrict__ route, int T, int E, int k,
     const uint32_t* __restrict__ qw0, const uint32_t* __restrict__ qz0, const ST* __restrict__ sc0,
     const uint32_t* __restrict__ qw1, const uint32_t* __restrict__ qz1, const ST* __restrict__ sc1,
-    size_t qw_stride, size_t qz_stride, size_t sc_stride, size_t a_plane, void* __restrict__ out,
-    size_t out_plane, int K, int N, int gs, float zoff) {
+    size_t qw_stride, size_t qz_stride, size_t sc_stride, float* __restrict__ out, int K, int N, int gs,
+    float zoff) {
   constexpr int PER = 32 / BITS;
   constexpr int TM = kMoeBM / 16;
   constexpr int STEPS = KC / 32;
   constexpr int RB = BITS == 4 ? 1 : 2;
   constexpr int NSET = 1;  // weight sets per wave (gate_up: waves 0-1 gate, 2-3 up)
   constexpr int WCOLS = GATE_UP ? 128 : 256;  // columns per workgroup
-  constexpr int NA = GATE_UP ? 1 : 2;  // activation planes (down: hi and lo)
+  constexpr int NA = XF32 ? 2 : 1;            // activation planes (hi and lo)
+  constexpr int XW = XF32 ? 2 : 1;            // 16-byte words per 8-value piece
+  static_assert(GATE_UP || XF32, "the down projection reads fp32 h");
   __shared__ __align__(16) _Float16 xs[NA][kMoeBM * KC];
 
   const RouteLayout L = route_layout(T, E, k);
@@ -250,6 +293,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   const int e = td.x, slot0 = td.y, nrows = td.z;
   const int* sorted_tok = route + L.sorted_tok;
   const float* sorted_w = reinterpret_cast<const float*>(route + L.sorted_w);
+  // the maxima the row scales come from: x's per token (gate_up), h's per slot (down)
+  const float* row_max = reinterpret_cast<const float*>(route + (GATE_UP ? L.x_scale : L.slot_max));
+  auto row_id = [&](int row) { return GATE_UP ? sorted_tok[slot0 + row] : slot0 + row; };
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -270,39 +316,44 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc[q][t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
+      for (int s4 = 0; s4 < 4; ++s4) acc[q][t][s4] = (float4v){0.f, 0.f, 0.f, 0.f};
 
   // Register triple buffer: while one K chunk is multiplied, the next two chunks' codes,
   // scales, zero points and activation rows are in flight. Loads use addresses clamped into the
   // matrices (columns past N, the chunk after the last), so no branch surrounds them and the
   // compiler's wait counts stay exact; such values are never used.
-  constexpr int XCN = NA * kMoeBM * KC / 8;           // 16-byte activation pieces per chunk
-  constexpr int XCH = (XCN + 255) / 256;              // per thread
+  constexpr int XCN = kMoeBM * KC / 8;  // 8-value activation pieces per chunk
+  constexpr int XCH = (XCN + 255) / 256;  // per thread
   const int ncl = min(ncol, N - 4);
-  size_t xsrc[XCH];                                   // element offset of each piece's row
-  int xdst[XCH];                                      // its LDS offset (plane, row, k), -1: none
-  bool xz[XCH];                                       // a row past the tile: zeros
+  size_t xsrc[XCH];  // element offset of each piece's row
+  int xdst[XCH];     // its LDS offset (row, k) in each plane, -1: none
+  bool xz[XCH];      // a row past the tile: zeros
+  float xrs[XCH];    // its row scale (fp32 activations)
 #pragma unroll
   for (int j = 0; j < XCH; ++j) {
     const int ci = threadIdx.x + 256 * j;
     const int cc = min(ci, XCN - 1);
-    const int pl = cc / (kMoeBM * KC / 8), cr = cc - pl * (kMoeBM * KC / 8);
-    const int r = cr / (KC / 8), kk = (cr - r * (KC / 8)) * 8;
+    const int r = cc / (KC / 8), kk = (cc - r * (KC / 8)) * 8;
     const int rr = min(r, nrows - 1);
-    const size_t row = GATE_UP ? (size_t)sorted_tok[slot0 + rr] : (size_t)(slot0 + rr);
-    xsrc[j] = (size_t)pl * a_plane + row * K + kk;
-    xdst[j] = ci < XCN ? pl * kMoeBM * KC + r * KC + kk : -1;
+    const size_t row = (size_t)row_id(rr);
+    xsrc[j] = row * K + kk;
+    xdst[j] = ci < XCN ? r * KC + kk : -1;
     xz[j] = r >= nrows;
+    xrs[j] = XF32 ? row_scale(row_max[row]) : 1.f;
   }
   struct Chunk {
     uint4 bw[NSET][STEPS][RB];
     uint4 sraw[NSET];
     uint32_t zraw[NSET];
-    uint4 xv[XCH];
+    uint4 xv[XCH][XW];
   };
   auto load_chunk = [&](int kc0, Chunk& c) {
 #pragma unroll
-    for (int j = 0; j < XCH; ++j) c.xv[j] = *reinterpret_cast<const uint4*>(a + xsrc[j] + kc0);
+    for (int j = 0; j < XCH; ++j)
+#pragma unroll
+      for (int w = 0; w < XW; ++w)
+        c.xv[j][w] = XF32 ? *reinterpret_cast<const uint4*>(static_cast<const float*>(a_in) + xsrc[j] + kc0 + 4 * w)
+                          : *reinterpret_cast<const uint4*>(static_cast<const __half*>(a_in) + xsrc[j] + kc0);
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
 #pragma unroll
@@ -317,21 +368,39 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
       c.zraw[q] = qz[q][(size_t)g * NZ + ncl / PER];
     }
   };
-  // the activation pieces in the order the code unpack produces (int4: (x0,x4) (x1,x5) (x2,x6)
-  // (x3,x7); int8: (x0,x2) (x1,x3) (x4,x6) (x5,x7)), moved as 16-bit halves
+  // 8 halves in k order (words (h0,h1) (h2,h3) (h4,h5) (h6,h7)) into the order the code unpack
+  // produces (int4: (x0,x4) (x1,x5) (x2,x6) (x3,x7); int8: (x0,x2) (x1,x3) (x4,x6) (x5,x7))
+  auto pair_order = [](uint4 w) {
+    if constexpr (BITS == 4)
+      return make_uint4((w.x & 0xFFFFu) | (w.z << 16), (w.x >> 16) | (w.z & 0xFFFF0000u),
+                        (w.y & 0xFFFFu) | (w.w << 16), (w.y >> 16) | (w.w & 0xFFFF0000u));
+    else
+      return make_uint4((w.x & 0xFFFFu) | (w.y << 16), (w.x >> 16) | (w.y & 0xFFFF0000u),
+                        (w.z & 0xFFFFu) | (w.w << 16), (w.z >> 16) | (w.w & 0xFFFF0000u));
+  };
   auto stage = [&](const Chunk& c) {
 #pragma unroll
     for (int j = 0; j < XCH; ++j) {
       if (xdst[j] < 0) continue;
-      const uint4 w = xz[j] ? make_uint4(0u, 0u, 0u, 0u) : c.xv[j];
-      uint4 o;
-      if constexpr (BITS == 4)
-        o = make_uint4((w.x & 0xFFFFu) | (w.z << 16), (w.x >> 16) | (w.z & 0xFFFF0000u),
-                       (w.y & 0xFFFFu) | (w.w << 16), (w.y >> 16) | (w.w & 0xFFFF0000u));
-      else
-        o = make_uint4((w.x & 0xFFFFu) | (w.y << 16), (w.x >> 16) | (w.y & 0xFFFF0000u),
-                       (w.z & 0xFFFFu) | (w.w << 16), (w.z >> 16) | (w.w & 0xFFFF0000u));
-      *reinterpret_cast<uint4*>(&xs[0][0] + xdst[j]) = o;
+      if constexpr (XF32) {
+        const uint32_t raw[8] = {c.xv[j][0].x, c.xv[j][0].y, c.xv[j][0].z, c.xv[j][0].w,
+                                 c.xv[j][1].x, c.xv[j][1].y, c.xv[j][1].z, c.xv[j][1].w};
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v0 = xz[j] ? 0.f : __uint_as_float(raw[2 * i]) * xrs[j];
+          const float v1 = xz[j] ? 0.f : __uint_as_float(raw[2 * i + 1]) * xrs[j];
+          const __half h0 = __float2half_rn(v0), h1 = __float2half_rn(v1);
+          hi[i] = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
+          lo[i] = (uint32_t)__half_as_ushort(__float2half_rn(v0 - __half2float(h0))) |
+                  ((uint32_t)__half_as_ushort(__float2half_rn(v1 - __half2float(h1))) << 16);
+        }
+        *reinterpret_cast<uint4*>(&xs[0][0] + xdst[j]) = pair_order(make_uint4(hi[0], hi[1], hi[2], hi[3]));
+        *reinterpret_cast<uint4*>(&xs[NA - 1][0] + xdst[j]) = pair_order(make_uint4(lo[0], lo[1], lo[2], lo[3]));
+      } else {
+        *reinterpret_cast<uint4*>(&xs[0][0] + xdst[j]) =
+            pair_order(xz[j] ? make_uint4(0u, 0u, 0u, 0u) : c.xv[j][0]);
+      }
     }
   };
   auto multiply = [&](const Chunk& c) {
@@ -343,19 +412,20 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 #pragma unroll
       for (int t = 0; t < TM; ++t)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) part[t][s] = (float4v){0.f, 0.f, 0.f, 0.f};
+        for (int s4 = 0; s4 < 4; ++s4) part[t][s4] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < STEPS; ++st) {
         half8v bf[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bf[s] = b_fragment<BITS>(c.bw[q][st], s, zl[s], zh[s]);
+        for (int s4 = 0; s4 < 4; ++s4) bf[s4] = b_fragment<BITS>(c.bw[q][st], s4, zl[s4], zh[s4]);
 #pragma unroll
         for (int pl = 0; pl < NA; ++pl)
 #pragma unroll
           for (int t = 0; t < TM; ++t) {
             const half8v af = *reinterpret_cast<const half8v*>(xs[pl] + (16 * t + p) * KC + st * 32 + 8 * kb);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) part[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[s], part[t][s], 0, 0, 0);
+            for (int s4 = 0; s4 < 4; ++s4)
+              part[t][s4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[s4], part[t][s4], 0, 0, 0);
           }
       }
       float sf[4];
@@ -363,9 +433,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 #pragma unroll
       for (int t = 0; t < TM; ++t)
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[q][t][s][r] = fmaf(sf[s], part[t][s][r], acc[q][t][s][r]);
+          for (int r = 0; r < 4; ++r) acc[q][t][s4][r] = fmaf(sf[s4], part[t][s4][r], acc[q][t][s4][r]);
     }
   };
   // chunk i is multiplied while chunks i + 1 and i + 2 are in flight (three register sets)
@@ -392,26 +462,35 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 #pragma unroll
       for (int t = 0; t < TM; ++t)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) ux[cw][t][s][lane] = acc[0][t][s];
+        for (int s4 = 0; s4 < 4; ++s4) ux[cw][t][s4][lane] = acc[0][t][s4];
     __syncthreads();
-    if (set == 1 || !colok) return;
+    if (set == 1 || !wave_active) return;  // wave-uniform
+    unsigned* slot_max = reinterpret_cast<unsigned*>(route + L.slot_max);
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * t + 4 * kb + r;
-        if (row >= nrows) continue;
-        const size_t slot = (size_t)slot0 + row;
-        __half* hi = static_cast<__half*>(out) + slot * N + ncol;
-        __half* lo = hi + out_plane;
+        const int row = 16 * t + 4 * kb + r;  // the same in the 16 lanes of a row of D
+        const bool live = row < nrows && colok;
+        const float un = XF32 ? row_unscale(row_max[row_id(min(row, nrows - 1))]) : 1.f;
+        float m = 0.f;
+        float hv[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float g = acc[0][t][s][r], u = ux[cw][t][s][lane][r];
-          const float h = g * (1.f / (1.f + expf(-g))) * u;
-          const __half hh = __float2half_rn(h);
-          hi[s] = hh;
-          lo[s] = __float2half_rn(h - __half2float(hh));
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const float g = acc[0][t][s4][r] * un, u = ux[cw][t][s4][lane][r] * un;
+          hv[s4] = g * (1.f / (1.f + expf(-g))) * u;
+          m = fmaxf(m, fabsf(hv[s4]));  // NaN: the word check below
+          if (hv[s4] != hv[s4]) m = __int_as_float(0x7FC00000);
         }
+        if (live) *reinterpret_cast<float4*>(out + (size_t)(slot0 + row) * N + ncol) =
+            make_float4(hv[0], hv[1], hv[2], hv[3]);
+        // the row's max over this wave's 64 columns: the 16 lanes of the row, by DPP moves
+        unsigned mb = live ? __float_as_uint(m) : 0u;  // |h| bits: ordered like the values, NaN above all
+        mb = max(mb, (unsigned)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
+        mb = max(mb, (unsigned)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));
+        mb = max(mb, (unsigned)__builtin_amdgcn_update_dpp(0, (int)mb, 0x141, 0xF, 0xF, false));
+        mb = max(mb, (unsigned)__builtin_amdgcn_update_dpp(0, (int)mb, 0x140, 0xF, 0xF, false));
+        if (p == 0 && row < nrows) atomicMax(slot_max + slot0 + row, mb);
       }
   } else {
     if (!colok) return;
@@ -422,10 +501,10 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
         const int row = 16 * t + 4 * kb + r;
         if (row >= nrows) continue;
         const size_t slot = (size_t)slot0 + row;
-        float* y = static_cast<float*>(out) + slot * N + ncol;
-        const float w = sorted_w[slot];
+        const float wsc = sorted_w[slot] * row_unscale(row_max[slot]);
+        float* y = out + slot * N + ncol;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) y[s] = acc[0][t][s][r] * w;
+        for (int s4 = 0; s4 < 4; ++s4) y[s4] = acc[0][t][s4][r] * wsc;
       }
   }
 }
@@ -446,45 +525,53 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   *reinterpret_cast<float4*>(out + (size_t)t * N + c) = s;
 }
 
-template <int BITS, int KC, bool GATE_UP>
-static int launch_moe_gemm(const void* a, const int* route, int T, int E, int k, const int32_t* qw0, const int32_t* qz0,
-                           const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt, void* out,
+template <int BITS, int KC, bool GATE_UP, bool XF32>
+static int launch_moe_gemm(const void* a, int* route, int T, int E, int k, const int32_t* qw0, const int32_t* qz0,
+                           const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt, float* out,
                            int K, int N, int gs, float zoff, hipStream_t st) {
   const RouteLayout L = route_layout(T, E, k);
   const int per = 32 / BITS;
   const size_t qws = (size_t)(K / per) * N, qzs = (size_t)(K / gs) * (N / per), scs = (size_t)(K / gs) * N;
   dim3 grid(GATE_UP ? (N + 127) / 128 : (N + 255) / 256, L.max_tiles);
-  // gate_up writes h as two planes of T*k x N halves; down reads them (a_plane = T*k x K)
-  const size_t a_plane = GATE_UP ? 0 : (size_t)T * k * K;
-  const size_t out_plane = GATE_UP ? (size_t)T * k * N : 0;
+  const uint32_t *w0 = reinterpret_cast<const uint32_t*>(qw0), *z0 = reinterpret_cast<const uint32_t*>(qz0);
+  const uint32_t *w1 = reinterpret_cast<const uint32_t*>(qw1), *z1 = reinterpret_cast<const uint32_t*>(qz1);
   if (sdt == MIQ_F16)
-    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, __half>), grid, dim3(256), 0, st,
-                       static_cast<const __half*>(a), route, T, E, k, reinterpret_cast<const uint32_t*>(qw0),
-                       reinterpret_cast<const uint32_t*>(qz0), static_cast<const __half*>(sc0),
-                       reinterpret_cast<const uint32_t*>(qw1), reinterpret_cast<const uint32_t*>(qz1),
-                       static_cast<const __half*>(sc1), qws, qzs, scs, a_plane, out, out_plane, K, N, gs, zoff);
+    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, __half>), grid, dim3(256), 0, st, a, route, T, E, k,
+                       w0, z0, static_cast<const __half*>(sc0), w1, z1, static_cast<const __half*>(sc1), qws, qzs,
+                       scs, out, K, N, gs, zoff);
   else
-    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, float>), grid, dim3(256), 0, st,
-                       static_cast<const __half*>(a), route, T, E, k, reinterpret_cast<const uint32_t*>(qw0),
-                       reinterpret_cast<const uint32_t*>(qz0), static_cast<const float*>(sc0),
-                       reinterpret_cast<const uint32_t*>(qw1), reinterpret_cast<const uint32_t*>(qz1),
-                       static_cast<const float*>(sc1), qws, qzs, scs, a_plane, out, out_plane, K, N, gs, zoff);
+    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, float>), grid, dim3(256), 0, st, a, route, T, E, k,
+                       w0, z0, static_cast<const float*>(sc0), w1, z1, static_cast<const float*>(sc1), qws, qzs, scs,
+                       out, K, N, gs, zoff);
   return check_launch(GATE_UP ? "moe_gate_up" : "moe_down");
 }
 
-template <bool GATE_UP>
-static int moe_gemm(const void* a, const int* route, int T, int E, int k, const int32_t* qw0, const int32_t* qz0,
-                    const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt, void* out, int K,
+template <bool GATE_UP, bool XF32>
+static int moe_gemm(const void* a, int* route, int T, int E, int k, const int32_t* qw0, const int32_t* qz0,
+                    const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt, float* out, int K,
                     int N, int gs, int bits, float zoff, hipStream_t st) {
   const int kc = gs % 128 == 0 ? 128 : (gs == 64 ? 64 : (gs == 32 ? 32 : 0));
   MIQ_REQUIRE(kc, MIQ_ERR_UNSUPPORTED, "moe: group size %d (32, 64 or a multiple of 128)", gs);
 #define MIQ_MOE_CASE(B, C)                                                                                        \
   if (bits == B && kc == C)                                                                                       \
-  return launch_moe_gemm<B, C, GATE_UP>(a, route, T, E, k, qw0, qz0, sc0, qw1, qz1, sc1, sdt, out, K, N, gs, zoff, st)
+  return launch_moe_gemm<B, C, GATE_UP, XF32>(a, route, T, E, k, qw0, qz0, sc0, qw1, qz1, sc1, sdt, out, K, N, gs, \
+                                              zoff, st)
   MIQ_MOE_CASE(4, 128); MIQ_MOE_CASE(4, 64); MIQ_MOE_CASE(4, 32);
   MIQ_MOE_CASE(8, 128); MIQ_MOE_CASE(8, 64); MIQ_MOE_CASE(8, 32);
 #undef MIQ_MOE_CASE
   return fail(MIQ_ERR_UNSUPPORTED, "moe: bits=%d", bits);
+}
+
+// out[t][c] += ys[t][c] * sigmoid(gl[t]) (gl null: += ys), the shared expert's contribution
+// (`webtorch/lm_engine.py:322-328`: g = 1 / (1 + exp(-gl)) in fp32, ys * g, out + ys).
+__global__ __launch_bounds__(256) void moe_shared_add_kernel(float* __restrict__ out, const float* __restrict__ ys,
+                                                             const float* __restrict__ gl, int H) {
+  const int t = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= H) return;
+  float y = ys[(size_t)t * H + c];
+  if (gl) y = y * (1.f / (1.f + expf(-gl[t])));
+  out[(size_t)t * H + c] += y;
 }
 
 int check_gptq_dims(const char* who, int K, int N, int gs, int bits);
@@ -530,9 +617,9 @@ extern "C" int miq_moe_route(const float* logits, int T, int E, int k, int norm_
   return check_launch("moe_route");
 }
 
-extern "C" int miq_moe_gate_up(const void* x, const void* route, int T, int E, int k, const int32_t* qw_gate,
+extern "C" int miq_moe_gate_up(const void* x, int x_dtype, void* route, int T, int E, int k, const int32_t* qw_gate,
                                const int32_t* qz_gate, const void* sc_gate, const int32_t* qw_up, const int32_t* qz_up,
-                               const void* sc_up, int scales_dtype, void* h, int H, int I, int gs, int bits,
+                               const void* sc_up, int scales_dtype, float* h, int H, int I, int gs, int bits,
                                float zero_offset, void* stream) {
   int rc = moe_check("moe_gate_up", T, E, k);
   if (rc) return rc;
@@ -540,15 +627,26 @@ extern "C" int miq_moe_gate_up(const void* x, const void* route, int T, int E, i
   if (rc || T == 0) return rc;
   MIQ_REQUIRE(x && route && qw_gate && qz_gate && sc_gate && qw_up && qz_up && sc_up && h, MIQ_ERR_INVALID,
               "moe_gate_up: null pointer");
-  MIQ_REQUIRE(I % 4 == 0 && H % 32 == 0 && aligned(x, 16) && aligned(qw_gate, 16) && aligned(qw_up, 16) && aligned(route, 16),
-              MIQ_ERR_ALIGN, "moe_gate_up: alignment (x, weights, route 16 bytes; I %% 4, H %% 32)");
+  MIQ_REQUIRE(x_dtype == MIQ_F16 || x_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "moe_gate_up: x dtype");
+  MIQ_REQUIRE(I % 4 == 0 && H % 32 == 0 && aligned(x, 16) && aligned(h, 16) && aligned(qw_gate, 16) &&
+                  aligned(qw_up, 16) && aligned(route, 16),
+              MIQ_ERR_ALIGN, "moe_gate_up: alignment (x, h, weights, route 16 bytes; I %% 4, H %% 32)");
   MIQ_REQUIRE(zero_offset == (float)(int)zero_offset && zero_offset >= 0.f && zero_offset <= 8.f, MIQ_ERR_UNSUPPORTED,
               "moe_gate_up: zero_offset %g", zero_offset);
-  return moe_gemm<true>(x, static_cast<const int*>(route), T, E, k, qw_gate, qz_gate, sc_gate, qw_up, qz_up, sc_up,
-                        scales_dtype, h, H, I, gs, bits, zero_offset, static_cast<hipStream_t>(stream));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int* r = static_cast<int*>(route);
+  if (x_dtype == MIQ_F32) {
+    hipLaunchKernelGGL(moe_xmax_kernel, dim3((T + 3) / 4), dim3(256), 0, st, static_cast<const float*>(x), T, H, E, k, r);
+    rc = check_launch("moe_gate_up row scales");
+    if (rc) return rc;
+    return moe_gemm<true, true>(x, r, T, E, k, qw_gate, qz_gate, sc_gate, qw_up, qz_up, sc_up, scales_dtype, h, H, I, gs,
+                                bits, zero_offset, st);
+  }
+  return moe_gemm<true, false>(x, r, T, E, k, qw_gate, qz_gate, sc_gate, qw_up, qz_up, sc_up, scales_dtype, h, H, I, gs,
+                               bits, zero_offset, st);
 }
 
-extern "C" int miq_moe_down(const void* h, const void* route, int T, int E, int k, const int32_t* qw, const int32_t* qz,
+extern "C" int miq_moe_down(const float* h, void* route, int T, int E, int k, const int32_t* qw, const int32_t* qz,
                             const void* sc, int scales_dtype, float* y, int I, int H, int gs, int bits, float zero_offset,
                             void* stream) {
   int rc = moe_check("moe_down", T, E, k);
@@ -560,8 +658,17 @@ extern "C" int miq_moe_down(const void* h, const void* route, int T, int E, int 
               "moe_down: alignment (h, weights, route 16 bytes; H %% 4, I %% 32)");
   MIQ_REQUIRE(zero_offset == (float)(int)zero_offset && zero_offset >= 0.f && zero_offset <= 8.f, MIQ_ERR_UNSUPPORTED,
               "moe_down: zero_offset %g", zero_offset);
-  return moe_gemm<false>(h, static_cast<const int*>(route), T, E, k, qw, qz, sc, nullptr, nullptr, nullptr,
-                         scales_dtype, y, I, H, gs, bits, zero_offset, static_cast<hipStream_t>(stream));
+  return moe_gemm<false, true>(h, static_cast<int*>(route), T, E, k, qw, qz, sc, nullptr, nullptr, nullptr,
+                               scales_dtype, y, I, H, gs, bits, zero_offset, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int miq_moe_shared_add(float* out, const float* ys, const float* gate_logits, int T, int H, void* stream) {
+  MIQ_REQUIRE(T >= 0 && H > 0, MIQ_ERR_INVALID, "moe_shared_add: T=%d H=%d", T, H);
+  if (T == 0) return MIQ_OK;
+  MIQ_REQUIRE(out && ys, MIQ_ERR_INVALID, "moe_shared_add: null pointer");
+  hipLaunchKernelGGL(moe_shared_add_kernel, dim3((H + 255) / 256, T), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     out, ys, gate_logits, H);
+  return check_launch("moe_shared_add");
 }
 
 extern "C" int miq_moe_combine(const float* y, const void* route, int T, int E, int k, float* out, int H,
