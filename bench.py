@@ -15,10 +15,11 @@ weight of the model once per token) / step time, in GB/s, plus decode tokens/s a
 step as a launch sequence; `roofline` for the persistent kernel (its algorithmic bytes: weights,
 activations, KV rows, over its launch time); the drop-in GEMV kernel on the token's 97 GEMVs
 replayed alone over two alternating weight copies (522 MB, above the 256 MB Infinity Cache, so
-from HBM), with per-shape timings; the GGUF Q4_K GEMV (Llama-3-8B up_proj), the act-order
-prefill GEMM (K = N = 4096) and the Qwen3-MoE expert block; and `cpu_baseline`: the
-reference's numpy fallback (restated in `oracle/`) timed on this host on a bounded sample of
-the same GEMVs.
+from HBM), with per-shape timings; config 0 exactly (fp16 in and out, 256 launches over distinct
+copies, plus single-launch latency); the full 128-token decode of the end-to-end config; the GGUF
+Q4_K GEMV (Llama-3-8B up_proj), the act-order prefill GEMM (K = N = 4096) in int4 and in
+per-channel int8, and the Qwen3-MoE expert block; and `cpu_baseline`: the reference's numpy
+fallback (restated in `oracle/`) timed on this host on bounded samples of every config.
 """
 import argparse
 import json
@@ -172,6 +173,80 @@ def gemm_bench(torch, core, Ms=(16, 128, 512), copies=32, reps=32):
     return res
 
 
+def config0_bench(torch, core, reps=256):
+    """GPTQ int4 GEMV exactly as config 0: x fp16 (1, 896) -> y fp16 (1, 4864) (Qwen2-0.5B
+    gate_proj, gs 128, fp16 scales, zero offset 1), R = 256 back-to-back launches in one graph over
+    256 distinct weight copies (583 MB, above the 256 MB Infinity Cache, so every launch reads
+    HBM): per-call time = total / R. Single-launch latency: one eager call between events (launch
+    overhead included)."""
+    K, N = 896, 4864
+    ws = [make_layer(torch, K, N, "f16", False) for _ in range(reps)]
+    x = torch.randn((1, K), device="cuda").half()
+    y = torch.empty((1, N), device="cuda", dtype=torch.float16)
+
+    def one(i=0):
+        qw, qz, sc, _ = ws[i]
+        core._gptq_matmul(x, qw, qz, sc, K, N, GS, 4, 1.0, out=y)
+
+    def run():
+        for i in range(reps):
+            one(i)
+    run()
+    torch.cuda.synchronize()
+    g = capture(torch, run)
+    t = timed(torch, g.replay, 3) / reps
+    lat = timed(torch, one, 64)
+    nb = gemv_bytes(K, N, "f16", False)
+    del g, ws
+    torch.cuda.empty_cache()
+    return {"K": K, "N": N, "x": "fp16 (1, 896)", "y": "fp16 (1, 4864)", "bytes": nb, "launches": reps,
+            "us_per_call": round(t * 1e6, 3), "GBs": round(nb / t / 1e9, 1),
+            "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4), "single_launch_us": round(lat * 1e6, 3)}
+
+
+def gemm_int8_bench(torch, core, Ms=(16, 128, 512), copies=24, reps=24):
+    """The config-2 layer quantized per output channel to symmetric int8 (dtype="int8": one
+    group spanning K, stored code q + 128, zero offset 1), K = N = 4096: x fp16 (M, 4096) ->
+    y fp16, over `copies` distinct weight copies."""
+    K = N = 4096
+    ws = []
+    for _ in range(copies):
+        qw = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 4, N), dtype=torch.int32, device="cuda")
+        qz = torch.full((1, N // 4), 0x7F7F7F7F, dtype=torch.int32, device="cuda")
+        sc = (torch.rand((1, N), device="cuda") * 0.01 + 1e-3).half()
+        ws.append((qw, qz, sc))
+    res = {}
+    for M in Ms:
+        x = torch.randn((M, K), device="cuda").half()
+        y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+
+        def run(x=x, y=y):
+            for i in range(reps):
+                qw, qz, sc = ws[i % copies]
+                core._gptq_matmul(x, qw, qz, sc, K, N, K, 8, 1.0, out=y)
+        run()
+        torch.cuda.synchronize()
+        g = capture(torch, run)
+        t = timed(torch, g.replay, 5) / reps
+        flops = 2.0 * M * K * N
+        nbytes = K * N + N // 4 * 4 + N * 2 + 2 * M * K * 2
+        res["M%d" % M] = {"us": round(t * 1e6, 3), "TFLOPs": round(flops / t / 1e12, 1),
+                          "mfma_frac": round(flops / t / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                          "GBs": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+        del g
+    return res
+
+
+def decode_full(torch, m, ids, max_new=128):
+    """The end-to-end config as a whole: prefill of the 64-token prompt (TTFT) and 128 greedy
+    tokens (127 graph-replayed decode steps over positions 64..190), timed on the host around
+    the engine's `generate` (second run: the graph is already captured)."""
+    m.generate(ids, max_new)
+    r = m.generate(ids, max_new)
+    return {"tokens": max_new, "ttft_ms": round(r.ttft_s * 1e3, 3), "decode_tokens_per_s": round(r.decode_tok_s, 1),
+            "ms_per_token": round(1e3 / r.decode_tok_s, 4) if r.decode_tok_s else None}
+
+
 def moe_bench(torch, core, reps=8):
     """Qwen3-MoE block: T=256 tokens of hidden 2048, 128 experts (gate/up 2048->768, down
     768->2048, int4 gs=128), top-8; routing + grouped GEMMs + combine on the device."""
@@ -224,13 +299,46 @@ def gemv_large(torch, core, reps=24):
     return res
 
 
-def cpu_baseline(seconds=10.0):
-    """The reference's numpy-fallback GEMV path (`_gptq_matmul_np`, restated in oracle/) on a
-    bounded sample: one decoder layer's seven linears (q, k, v, o, gate, up, down as separate
-    layers, as the reference holds them) plus four 4096-row head blocks, repeated for about
-    `seconds`; throughput in the same algorithmic bytes as the GPU figure."""
+def _median_time(fn, seconds, min_reps=3):
     import numpy as np
-    from oracle import gptq
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def _blas_info():
+    """(threads the BLAS uses, its name) from threadpoolctl / numpy's build config."""
+    try:
+        from threadpoolctl import threadpool_info
+        info = [p for p in threadpool_info() if p.get("user_api") == "blas"]
+        if info:
+            return int(info[0].get("num_threads", 1)), "%s %s" % (info[0].get("internal_api", "?"),
+                                                                  info[0].get("version", ""))
+    except Exception:
+        pass
+    return len(os.sched_getaffinity(0)), "unknown"
+
+
+def cpu_baseline(seconds=10.0):
+    """The reference's numpy-fallback path (restated in oracle/) on bounded samples of each
+    workload, on this host's cores:
+
+    * value (the headline unit, GB/s of int4 GEMV bytes): `_gptq_matmul_np` over one decoder
+      layer's seven linears (q, k, v, o, gate, up, down as separate layers, as the reference
+      holds them) plus four 4096-row head blocks, all BLAS threads, and again with one thread;
+    * config 1: Q4_K dequant (`ggufload.dequant`) + x @ W.T on a 1792-row band of the
+      Llama-3-8B up_proj (1/8 of it);
+    * config 2: `_gptq_matmul_np` at M = 128, K = N = 4096 (act-order folded into the rows);
+    * config 3: `moe_mlp` at T = 32 tokens of the Qwen3-MoE block (1/8 of the 256);
+    * config 4: one greedy decode step of the Qwen2-0.5B-shaped model after a one-token prompt.
+    """
+    import numpy as np
+    from oracle import decode as odecode, gptq, moe as omoe, q4k
     from webpytorch_amd import synth
     lin = [("q", H, NH * HD, np.float16, 1.0), ("k", H, NKV * HD, np.float16, 1.0),
            ("v", H, NKV * HD, np.float16, 1.0), ("o", NH * HD, H, np.float16, 1.0),
@@ -245,26 +353,51 @@ def cpu_baseline(seconds=10.0):
         layers.append((L, x, zoff))
         nbytes += gemv_bytes(K, N, "f16" if sdt == np.float16 else "f32", name in ("q", "k", "v"))
 
-    def one():
+    def gemv_sample():
         for L, x, zoff in layers:
             gptq.gptq_matmul_np(x, L["qweight"], L["qzeros"], L["scales"], L["K"], L["N"], GS, 4, zoff)
-    one()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
+    cores, blas = _blas_info()
+    t, n = _median_time(gemv_sample, seconds)
+    one = None
     try:
-        from threadpoolctl import threadpool_info
-        cores = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+        from threadpoolctl import threadpool_limits
+        with threadpool_limits(1):
+            t1, _ = _median_time(gemv_sample, seconds / 4)
+        one = round(nbytes / t1 / 1e9, 4)
     except Exception:
-        cores = len(os.sched_getaffinity(0))
+        pass
+    cfg = {}
+    # config 1: a 1792-row band of the Q4_K up_proj
+    Kq, Nq = 4096, 1792
+    Wq = synth.q4k_layer(1, Kq, Nq)
+    xq = synth.activations(1, 1, Kq, np.float16)
+    tq, _ = _median_time(lambda: q4k.q4k_matmul(xq, Wq, Kq, Nq), seconds / 4)
+    qb = Nq * Kq // 256 * 144 + Kq * 2 + Nq * 4
+    cfg["q4k_gemv"] = {"GBs": round(qb / tq / 1e9, 4), "sample": "4096 x 1792 band (1/8 of 14336 rows)"}
+    # config 2: M = 128
+    L2 = synth.gptq_layer(2, 4096, 4096, GS, 4)
+    x2 = synth.activations(2, 128, 4096, np.float16)
+    t2, _ = _median_time(lambda: gptq.gptq_matmul_np(x2, L2["qweight"], L2["qzeros"], L2["scales"], 4096, 4096, GS, 4,
+                                                     1.0), seconds / 4)
+    cfg["gptq_gemm_m128"] = {"TFLOPs": round(2 * 128 * 4096 * 4096 / t2 / 1e12, 5), "ms": round(t2 * 1e3, 2)}
+    # config 3: 32 tokens of the MoE block
+    w3 = synth.moe_workload(3)
+    ex3 = [omoe.gptq_expert(e) for e in w3["experts"]]
+    t3, _ = _median_time(lambda: omoe.moe_mlp_np(w3["x"][:32], w3["logits"][:32], ex3, 8), seconds / 4, 2)
+    cfg["moe_t32"] = {"ms": round(t3 * 1e3, 1), "tokens_per_s": round(32 / t3, 2)}
+    # config 4: one decode step (single-token prompt, then one step)
+    w4 = synth.decoder_weights(5, **synth.QWEN2_05B)
+    o = odecode.Qwen2Oracle(w4, lmax=8)
+    cache = [None] * o.L
+    nxt, _ = o.forward([1], 0, cache)
+    t0 = time.perf_counter()
+    o.forward([nxt], 1, cache)
+    t4 = time.perf_counter() - t0
+    cfg["decode_step"] = {"s_per_token": round(t4, 2), "tokens_per_s": round(1.0 / t4, 3)}
     return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": int(cores), "kind": "port",
             "sample": "numpy restatement of _gptq_matmul_np: 1 Qwen2-0.5B layer (7 linears) + 4 head "
-                      "blocks of 4096 rows, %d reps, median %.1f ms, %d algorithmic bytes" % (
-                          len(times), t * 1e3, nbytes)}
+                      "blocks of 4096 rows, %d reps, median %.1f ms, %d algorithmic bytes" % (n, t * 1e3, nbytes),
+            "one_thread_GBs": one, "blas": blas, "host_cpus": len(os.sched_getaffinity(0)), "configs": cfg}
 
 
 def gemv_only(torch, core, steps):
@@ -323,8 +456,10 @@ def gemv_only(torch, core, steps):
 
 
 def decode_step_time(torch, m, ids, warmup, steps):
-    """Prefill + one step (which captures the decode graph), `warmup` untimed replays, then the
-    mean time of `steps` replays between events on the replay stream."""
+    """Prefill + one step (which captures the decode graph; the first call also runs the
+    kernels' first-use checks, so a second call gives the warm TTFT), `warmup` untimed replays,
+    then the mean time of `steps` replays between events on the replay stream."""
+    m.generate(ids, 2)
     r = m.generate(ids, 2)
     pos0 = int(m.state[0])
     g = m._graph
@@ -386,6 +521,8 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the token's GEMVs alone and a plain 1 GiB copy, for hardware-counter runs")
     ap.add_argument("--gemv-large", action="store_true", help="only the GEMV operator on 7B-class shapes")
+    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "moe", "config0"],
+                    help="one kernel benchmark and a plain 1 GiB copy, for profiler runs")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the persistent decode step and a plain 1 GiB copy, for hardware-counter runs")
     a = ap.parse_args()
@@ -400,6 +537,15 @@ def main():
     torch.manual_seed(0)
     if a.gemv_large:
         print(json.dumps(gemv_large(torch, core)), flush=True)
+        return
+    if a.only:
+        fn = {"gemm": lambda: gemm_bench(torch, core, Ms=(512,)), "gemm_int8": lambda: gemm_int8_bench(torch, core),
+              "q4k": lambda: q4k_bench(torch, core), "moe": lambda: moe_bench(torch, core),
+              "config0": lambda: config0_bench(torch, core)}[a.only]
+        out = {a.only: fn()}
+        copy_bytes = copy_calibration(torch)
+        out.update({"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes})
+        print(json.dumps(out), flush=True)
         return
     if a.decode_only:
         m = llm.CausalLM.from_weights(synth.decoder_weights(5, **synth.QWEN2_05B), lmax=256)
@@ -473,11 +619,17 @@ def main():
                         "frac": round(step_bytes / t_gemv / 1e9 / HBM_PEAK_GBS, 4), "shapes": kernels},
     }
     if not a.no_extras:
+        mf = llm.CausalLM.from_weights(w, lmax=256)
+        res["decode_full_128"] = decode_full(torch, mf, ids)
+        del mf
+        torch.cuda.empty_cache()
+        res["config0_gemv_fp16"] = config0_bench(torch, core)
         res["gemv_large"] = gemv_large(torch, core)
         res["q4k_gemv_llama3_8b_up"] = q4k_bench(torch, core)
         res["q6k_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q6_K")
         res["q8_0_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q8_0")
         res["gptq_gemm_act_order_4096"] = gemm_bench(torch, core)
+        res["gptq_gemm_int8_per_channel_4096"] = gemm_int8_bench(torch, core)
         res["moe_qwen3_t256"] = moe_bench(torch, core)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
