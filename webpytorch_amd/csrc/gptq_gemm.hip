@@ -80,36 +80,78 @@ template <int BITS> __device__ __forceinline__ uint4 pair_order8(uint4 v) {
 // xp = x with each 8-wide k block in pair order, stored stage-major: xp[k / KC][m][k % KC]. A
 // stage of a row tile is then one contiguous block, which spreads its reads over all L2
 // channels (rows of x are 2 K bytes apart, a power of two for the usual K, and would all land
-// in the same few channels). Grid (K/8/256 rounded up, M).
-template <int BITS>
-__global__ __launch_bounds__(256) void stage_x_kernel(const __half* __restrict__ x, __half* __restrict__ xp, int M,
-                                                      int K, int KC) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= K / 8) return;
-  const int m = blockIdx.y, k = i * 8;
-  *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC) =
-      pair_order8<BITS>(*reinterpret_cast<const uint4*>(x + (size_t)m * K + k));
+// in the same few channels).
+//
+// One workgroup per row of x; every thread issues four 16-byte loads before it stores anything.
+// With perm (act-order columns), the row goes to LDS first (coalesced) and each output chunk
+// gathers its 8 values from there through its 8 permutation indices, which are loaded while the
+// row is in flight. Grid (M), dynamic LDS 2 K bytes with perm.
+template <int BITS, bool PERM>
+__global__ __launch_bounds__(256) void stage_rows_kernel(const __half* __restrict__ x, const int32_t* __restrict__ perm,
+                                                         __half* __restrict__ xp, int M, int K, int KC) {
+  extern __shared__ __align__(16) unsigned short srow[];  // [K] (perm only)
+  constexpr int U = 4;
+  const int m = blockIdx.x, nch = K / 8;
+  const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)m * K);
+  auto dst = [&](int i) {
+    const int k = i * 8;
+    return reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC);
+  };
+  if constexpr (PERM) {
+    for (int q0 = threadIdx.x; q0 < nch; q0 += 256 * U) {
+      uint4 v[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) v[j] = src[min(q0 + 256 * j, nch - 1)];
+#pragma unroll
+      for (int j = 0; j < U; ++j)
+        if (q0 + 256 * j < nch) reinterpret_cast<uint4*>(srow)[q0 + 256 * j] = v[j];
+    }
+    __syncthreads();
+    const int4* p4 = reinterpret_cast<const int4*>(perm);
+    for (int q0 = threadIdx.x; q0 < nch; q0 += 256 * U) {
+      int4 pa[U], pb[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int i = min(q0 + 256 * j, nch - 1);
+        pa[j] = p4[2 * i];
+        pb[j] = p4[2 * i + 1];
+      }
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        if (q0 + 256 * j >= nch) break;
+        const uint4 v = make_uint4(srow[(unsigned)pa[j].x] | ((uint32_t)srow[(unsigned)pa[j].y] << 16),
+                                   srow[(unsigned)pa[j].z] | ((uint32_t)srow[(unsigned)pa[j].w] << 16),
+                                   srow[(unsigned)pb[j].x] | ((uint32_t)srow[(unsigned)pb[j].y] << 16),
+                                   srow[(unsigned)pb[j].z] | ((uint32_t)srow[(unsigned)pb[j].w] << 16));
+        *dst(q0 + 256 * j) = pair_order8<BITS>(v);
+      }
+    }
+  } else {
+    for (int q0 = threadIdx.x; q0 < nch; q0 += 256 * U) {
+      uint4 v[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) v[j] = src[min(q0 + 256 * j, nch - 1)];
+#pragma unroll
+      for (int j = 0; j < U; ++j)
+        if (q0 + 256 * j < nch) *dst(q0 + 256 * j) = pair_order8<BITS>(v[j]);
+    }
+  }
 }
 
-// the same with the columns gathered through perm: a thread per 8-wide output chunk reads its 8
-// permutation indices (shared by every row, so they stay in cache) and gathers the 8 values
-// straight from the row; no staging, no barrier: two dependent reads per thread.
-// Grid (K/8/256 rounded up, M).
+// Launches the staging of x (gathered through perm if non-null) into xp with stage width KC.
 template <int BITS>
-__global__ __launch_bounds__(256) void gather_x_kernel(const __half* __restrict__ x, const int32_t* __restrict__ perm,
-                                                       __half* __restrict__ xp, int M, int K, int KC) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= K / 8) return;
-  const int m = blockIdx.y;
-  const int4 pa = reinterpret_cast<const int4*>(perm)[2 * i];
-  const int4 pb = reinterpret_cast<const int4*>(perm)[2 * i + 1];
-  const unsigned short* row = reinterpret_cast<const unsigned short*>(x + (size_t)m * K);
-  const uint4 v = make_uint4(row[(unsigned)pa.x] | ((uint32_t)row[(unsigned)pa.y] << 16),
-                             row[(unsigned)pa.z] | ((uint32_t)row[(unsigned)pa.w] << 16),
-                             row[(unsigned)pb.x] | ((uint32_t)row[(unsigned)pb.y] << 16),
-                             row[(unsigned)pb.z] | ((uint32_t)row[(unsigned)pb.w] << 16));
-  const int k = i * 8;
-  *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC) = pair_order8<BITS>(v);
+static int stage_rows(const __half* x, const int32_t* perm, __half* xp, int M, int K, int KC, hipStream_t st) {
+  if (perm) {
+    const size_t lds = (size_t)K * 2;
+    if (lds > 64 * 1024) {
+      const int rc = require_lds("gptq_gemm gather", lds);
+      if (rc) return rc;
+    }
+    hipLaunchKernelGGL((stage_rows_kernel<BITS, true>), dim3(M), dim3(256), lds, st, x, perm, xp, M, K, KC);
+  } else {
+    hipLaunchKernelGGL((stage_rows_kernel<BITS, false>), dim3(M), dim3(256), 0, st, x, perm, xp, M, K, KC);
+  }
+  return check_launch("gptq_gemm staging");
 }
 
 template <int BITS, int TM, int CB, int KC, typename ST> struct GemmShape {
@@ -627,9 +669,7 @@ extern "C" int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* 
     __half* xg = nullptr;
     if (perm) {
       xg = reinterpret_cast<__half*>(static_cast<char*>(workspace) + kCounterBytes);
-      hipLaunchKernelGGL(gather_x_kernel<4>, dim3((K / 8 + 255) / 256, M), dim3(256), 0, st, xin, perm, xg, M, K,
-                         128);
-      rc = check_launch("gptq_gemm gather");
+      rc = stage_rows<4>(xin, perm, xg, M, K, 128, st);
       if (rc) return rc;
     }
     rc = gemm_small(xin, xg, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs, bits,
@@ -642,16 +682,7 @@ extern "C" int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* 
   MIQ_REQUIRE(workspace && workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
               "gptq_gemm: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes, workspace_bytes);
   __half* xp = reinterpret_cast<__half*>(static_cast<char*>(workspace) + kCounterBytes + p.partial_bytes);
-  if (perm) {
-    const dim3 g((K / 8 + 255) / 256, M);
-    if (bits == 4) hipLaunchKernelGGL(gather_x_kernel<4>, g, dim3(256), 0, st, xin, perm, xp, M, K, p.kc);
-    else hipLaunchKernelGGL(gather_x_kernel<8>, g, dim3(256), 0, st, xin, perm, xp, M, K, p.kc);
-  } else {
-    const dim3 g((K / 8 + 255) / 256, M);
-    if (bits == 4) hipLaunchKernelGGL(stage_x_kernel<4>, g, dim3(256), 0, st, xin, xp, M, K, p.kc);
-    else hipLaunchKernelGGL(stage_x_kernel<8>, g, dim3(256), 0, st, xin, xp, M, K, p.kc);
-  }
-  rc = check_launch("gptq_gemm staging");
+  rc = bits == 4 ? stage_rows<4>(xin, perm, xp, M, K, p.kc, st) : stage_rows<8>(xin, perm, xp, M, K, p.kc, st);
   if (rc) return rc;
   if (bits == 4)
     return gemm_dispatch<4>(p, xp, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, workspace, M, K, N, gs,
