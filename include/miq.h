@@ -144,6 +144,22 @@ int miq_gptq_gemm(const void* x, const int32_t* perm, const int32_t* qweight, co
                   int M, int K, int N, int gs, int bits, float zero_offset, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace miq_gptq_gemm_f32x needs; same contract as miq_gptq_gemv_workspace. */
+int miq_gptq_gemm_f32x_workspace(int M, int K, int N, int gs, int bits, size_t* bytes);
+
+/* miq_gptq_gemm for fp32 activations (the decoder's prefill): each row of x is scaled by a power
+ * of two and split into two fp16 rows, hi = fp16(x 2^s) and lo = fp16(x 2^s - hi) (about 22
+ * significant bits relative to the row's largest value, no fp16 range limit; NaN and infinite
+ * rows propagate), the tiled matrix-core GEMM runs on the 2M rows, and each output is the sum of
+ * its two rows scaled back by 2^-s, + bias. x fp32 16-byte aligned; K <= 32768; otherwise as
+ * miq_gptq_gemm.
+ * Replaces: `_gptq_matmul` M > 1 (webtorch/_core.py:3833-3888, 3995-4027) on the fp32
+ * activations of the prefill `_kv_forward` (webtorch/llm.py:1619-1636). */
+int miq_gptq_gemm_f32x(const float* x, const int32_t* perm, const int32_t* qweight, const int32_t* qzeros,
+                       const void* scales, int scales_dtype, const float* bias, void* out, int out_dtype,
+                       int M, int K, int N, int gs, int bits, float zero_offset, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* Asymmetric min-max quantizer to the GPTQ layout (zero_offset 0, fp32 scales), bit-exact
  * with the reference's float32 numpy arithmetic (IEEE division, round-half-even). W is
  * [K][N] or, with from_out_in = 1, [N][K]; fp16 or fp32. Outputs qweight [K/per][N],

@@ -120,3 +120,30 @@ def test_few_row_gemm(gpu, K, N, M, sdt, zoff, bias, act):
                        core.ptr(out), core.dtype_code(out), M, K, N, 128, 4, float(zoff), core.ptr(ws), ws.numel(),
                        core.stream_handle())
         assert np.array_equal(got, out.cpu().numpy())
+
+
+@pytest.mark.parametrize("M,act,scale", [(9, False, 1.0), (64, True, 1.0), (200, False, 3e5), (512, True, 1e-4)])
+def test_fp32_activation_gemm(gpu, M, act, scale):
+    """fp32 activations on the matrix cores (row-scaled fp16 hi/lo rows): the decoder's prefill.
+    Against the oracle's fp32 product and a float64 one, including magnitudes beyond fp16's
+    range and small ones; NaN in one row stays in that row."""
+    import torch
+    from webpytorch_amd import core
+    K, N = 4096, 1024
+    L = synth.gptq_layer(40 + M, K, N, 128, 4, act_order=act)
+    x = (np.random.default_rng(M).standard_normal((M, K)) * scale).astype(np.float32)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 128, 4,
+                                            g_idx=L["g_idx"] if act else None)
+    got = ql(torch.from_numpy(x)).cpu().numpy()
+    ref = gptq.linear_forward(x, L, zoff=1.0, g_idx=L["g_idx"] if act else None)
+    if scale == 1.0:
+        _check(got, ref)
+    else:  # the elementwise bar's absolute term is for unit-scale values: compare relative to the scale
+        assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5
+    W = gptq.dequant_closed_form(L["qweight"], L["qzeros"], L["scales"], 128, 4, 1.0,
+                                 g_idx=L["g_idx"] if act else None).astype(np.float64)
+    exact = x.astype(np.float64) @ W
+    assert np.abs(got - exact).max() / np.abs(exact).max() < 1e-5
+    x[1, 7] = np.nan
+    got = ql(torch.from_numpy(x)).cpu().numpy()
+    assert np.isnan(got[1]).all() and np.isfinite(np.delete(got, 1, 0)).all()

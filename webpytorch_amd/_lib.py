@@ -27,6 +27,8 @@ SIGNATURES = {
     "miq_gptq_gemv_fused": [_p, _i, _p, _f, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
     "miq_gptq_gemm_workspace": [_i, _i, _i, _i, _i, _p],
     "miq_gptq_gemm": [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
+    "miq_gptq_gemm_f32x_workspace": [_i, _i, _i, _i, _i, _p],
+    "miq_gptq_gemm_f32x": [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _sz, _p],
     "miq_gptq_quantize": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p],
     "miq_moe_route_bytes": [_i, _i, _i, _p],
     "miq_moe_route": [_p, _i, _i, _i, _i, _p, _sz, _p],

@@ -84,6 +84,17 @@ def gemv_workspace_bytes(M, K, N, gs, bits, x_dtype):
     return b
 
 
+def gemm_f32x_workspace_bytes(M, K, N, gs, bits):
+    """Bytes of workspace the fp32-activation GEMM needs (cached per shape)."""
+    key = ("gemm32", M, K, N, gs, bits)
+    b = _WS_BYTES.get(key)
+    if b is None:
+        n = ctypes.c_size_t(0)
+        _lib.call("miq_gptq_gemm_f32x_workspace", M, K, N, gs, bits, ctypes.byref(n))
+        b = _WS_BYTES[key] = int(n.value)
+    return b
+
+
 def gemm_workspace_bytes(M, K, N, gs, bits):
     """Bytes of split-K workspace the MFMA GEMM needs for this problem (cached per shape)."""
     key = ("gemm", M, K, N, gs, bits)
@@ -178,9 +189,9 @@ def _gptq_path(M, xdt):
     """The product kernel class `_gptq_matmul` runs for M rows (one check per class)."""
     if M == 1:
         return 1
-    if M <= GEMV_MAX_M or xdt != torch.float16:
+    if M <= GEMV_MAX_M:
         return 4
-    return 12 if M <= 16 else 40
+    return 12 if M <= 16 and xdt == torch.float16 else 40
 
 
 # ---- GPTQ ----------------------------------------------------------------------------
@@ -196,9 +207,9 @@ def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=
                  out_dtype=None, out=None, ws=None, _check=True):
     """xf (M, K) @ dequant(W) (+ bias) -> (M, N) on the current stream
     (`webtorch/_core.py:4008-4043`). Up to GEMV_MAX_M rows run the split-K GEMV; more rows
-    of fp16 activations run the matrix-core GEMM (fp32 activations stay on the GEMV, which
-    keeps them in fp32). The first call of each kernel class on a device runs its
-    known-answer check (RuntimeError if it fails)."""
+    run the matrix-core GEMM (fp32 activations as row-scaled fp16 hi/lo pairs of rows). The
+    first call of each kernel class on a device runs its known-answer check (RuntimeError if
+    it fails)."""
     M = int(xf.shape[0])
     if _check and M and 256 % gs == 0 and _first_use(("gptq", bits, gs, _gptq_path(M, xf.dtype), xf.dtype)):
         _selfcheck_gptq(_gptq_path(M, xf.dtype), xf.dtype, bits, gs)
@@ -215,6 +226,14 @@ def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=
         _lib.call("miq_gptq_gemm", ptr(xf), ptr(perm), ptr(qweight), ptr(qzeros), ptr(scales),
                   dtype_code(scales), ptr(bias), ptr(out), dtype_code(out), M, K, N, gs, bits,
                   float(zoff), ptr(ws), 0 if ws is None else ws.numel(), stream_handle())
+        return out
+    if M > GEMV_MAX_M and float(zoff).is_integer() and 0 <= zoff <= 8 and K <= 32768:
+        need = gemm_f32x_workspace_bytes(M, K, N, gs, bits)
+        if ws is None or ws.numel() < need:
+            ws = workspace(need)
+        _lib.call("miq_gptq_gemm_f32x", ptr(xf), ptr(perm), ptr(qweight), ptr(qzeros), ptr(scales),
+                  dtype_code(scales), ptr(bias), ptr(out), dtype_code(out), M, K, N, gs, bits,
+                  float(zoff), ptr(ws), ws.numel(), stream_handle())
         return out
     if ws is None:
         ws = workspace(gemv_workspace_bytes(M, K, N, gs, bits, xd))

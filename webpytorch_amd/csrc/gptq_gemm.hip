@@ -138,6 +138,93 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const __half* __restric
   }
 }
 
+// fp32 activations through the fp16 matrix cores: row m of x is scaled by 2^s (s making its
+// largest |x| just below 2^15) and split into hi = fp16(x 2^s) and lo = fp16(x 2^s - hi), staged
+// as rows m and M + m of a 2M-row problem (about 22 significant bits relative to the row's
+// largest value, no fp16 range limit; NaN or infinite rows keep scale 1 and propagate). The
+// GEMM's two result rows are added and scaled back by 2^-s (exact).
+__device__ __forceinline__ int f32_row_exp(float m) {
+  if (!(m > 0.f) || !(m <= 3.4e38f)) return 0;
+  int ex;
+  frexpf(m, &ex);
+  return min(max(15 - ex, -100), 100);
+}
+
+// Stage row m of fp32 x (gathered through perm if PERM) as hi (row m) and lo (row M + m) of the
+// 2M-row stage-major pair-ordered layout, and record the row's largest |x| (NaN if it holds one)
+// in rmax[m] for the combine. The row goes through LDS (its maximum sets the scale before any
+// value is split). Grid (M), dynamic LDS 4 K bytes.
+template <int BITS, bool PERM>
+__global__ __launch_bounds__(256) void stage_rows_f32_kernel(const float* __restrict__ x, const int32_t* __restrict__ perm,
+                                                             float* __restrict__ rmax, __half* __restrict__ xp, int M,
+                                                             int K, int KC) {
+  extern __shared__ __align__(16) float frow[];  // [K]
+  __shared__ float wmax[4];
+  __shared__ int wnan[4];
+  const int m = blockIdx.x, nch = K / 8, M2 = 2 * M, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float* src = x + (size_t)m * K;
+  float mx = 0.f;
+  bool nan = false;
+  for (int q = threadIdx.x; q < K / 4; q += 256) {
+    const float4 v = reinterpret_cast<const float4*>(src)[q];
+    reinterpret_cast<float4*>(frow)[q] = v;
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    nan |= v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w;
+  }
+  nan = __ballot(nan) != 0ull;
+  mx = wave_max(mx);
+  if (lane == 0) {
+    wmax[wave] = mx;
+    wnan[wave] = nan;
+  }
+  __syncthreads();
+  mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  if (wnan[0] | wnan[1] | wnan[2] | wnan[3]) mx = __int_as_float(0x7FC00000);
+  if (threadIdx.x == 0) rmax[m] = mx;
+  const float sc = ldexpf(1.f, f32_row_exp(mx));
+  for (int i = threadIdx.x; i < nch; i += 256) {
+    float v[8];
+    if constexpr (PERM) {
+      const int4 pa = reinterpret_cast<const int4*>(perm)[2 * i], pb = reinterpret_cast<const int4*>(perm)[2 * i + 1];
+      const int idx[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = frow[(unsigned)idx[j]];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = frow[8 * i + j];
+    }
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a0 = v[2 * j] * sc, a1 = v[2 * j + 1] * sc;
+      const __half h0 = __float2half_rn(a0), h1 = __float2half_rn(a1);
+      hi[j] = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
+      lo[j] = (uint32_t)__half_as_ushort(__float2half_rn(a0 - __half2float(h0))) |
+              ((uint32_t)__half_as_ushort(__float2half_rn(a1 - __half2float(h1))) << 16);
+    }
+    const int k = i * 8;
+    *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M2 + m) * KC + k % KC) =
+        pair_order8<BITS>(make_uint4(hi[0], hi[1], hi[2], hi[3]));
+    *reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M2 + M + m) * KC + k % KC) =
+        pair_order8<BITS>(make_uint4(lo[0], lo[1], lo[2], lo[3]));
+  }
+}
+
+// out[m][n] = (y2[m][n] + y2[M + m][n]) 2^-s(m) + bias[n]. Grid (N/4/256 rounded up, M).
+template <typename OT>
+__global__ __launch_bounds__(256) void combine_rows_kernel(const float* __restrict__ y2, const float* __restrict__ rmax,
+                                                           const float* __restrict__ bias, OT* __restrict__ out, int M,
+                                                           int N) {
+  const int m = blockIdx.y, n = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n >= N) return;
+  const float un = ldexpf(1.f, -f32_row_exp(rmax[m]));
+  const float4 a = *reinterpret_cast<const float4*>(y2 + (size_t)m * N + n);
+  const float4 b = *reinterpret_cast<const float4*>(y2 + (size_t)(M + m) * N + n);
+  const float r[4] = {(a.x + b.x) * un, (a.y + b.y) * un, (a.z + b.z) * un, (a.w + b.w) * un};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) out[(size_t)m * N + n + j] = from_f32<OT>(bias ? r[j] + bias[n + j] : r[j]);
+}
+
 // Launches the staging of x (gathered through perm if non-null) into xp with stage width KC.
 template <int BITS>
 static int stage_rows(const __half* x, const int32_t* perm, __half* xp, int M, int K, int KC, hipStream_t st) {
@@ -621,9 +708,90 @@ static int gemm_dispatch(const GemmPlan& p, const __half* xp, const int32_t* qw,
 
 int check_gptq_dims(const char* who, int K, int N, int gs, int bits);
 
+// Workspace layout of the fp32-activation GEMM: the 2M-row GEMM's own workspace (counters,
+// partials, staged rows), then its fp32 result [2M][N], then the row maxima [M].
+struct F32Plan {
+  GemmPlan g;
+  size_t y2_off, rmax_off, ws_bytes;
+};
+static int f32_plan(int M, int K, int N, int gs, int bits, F32Plan* p) {
+  int rc = gemm_plan(2 * M, K, N, gs, bits, &p->g);
+  if (rc) return rc;
+  p->y2_off = (p->g.ws_bytes + 255) & ~(size_t)255;
+  p->rmax_off = p->y2_off + (((size_t)2 * M * N * 4 + 255) & ~(size_t)255);
+  p->ws_bytes = p->rmax_off + (((size_t)M * 4 + 255) & ~(size_t)255);
+  return MIQ_OK;
+}
+
 }  // namespace miq
 
 using namespace miq;
+
+extern "C" int miq_gptq_gemm_f32x_workspace(int M, int K, int N, int gs, int bits, size_t* bytes) {
+  MIQ_REQUIRE(bytes, MIQ_ERR_INVALID, "gptq_gemm_f32x_workspace: null output");
+  *bytes = 0;
+  int rc = check_gptq_dims("gptq_gemm_f32x_workspace", K, N, gs, bits);
+  if (rc) return rc;
+  MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "gptq_gemm_f32x_workspace: M=%d", M);
+  if (M == 0) return MIQ_OK;
+  F32Plan p;
+  rc = f32_plan(M, K, N, gs, bits, &p);
+  if (rc) return rc;
+  *bytes = p.ws_bytes;
+  return MIQ_OK;
+}
+
+extern "C" int miq_gptq_gemm_f32x(const float* x, const int32_t* perm, const int32_t* qweight, const int32_t* qzeros,
+                                  const void* scales, int scales_dtype, const float* bias, void* out, int out_dtype,
+                                  int M, int K, int N, int gs, int bits, float zero_offset, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  int rc = check_gptq_dims("gptq_gemm_f32x", K, N, gs, bits);
+  if (rc) return rc;
+  MIQ_REQUIRE(M >= 0, MIQ_ERR_INVALID, "gptq_gemm_f32x: M=%d", M);
+  if (M == 0) return MIQ_OK;
+  MIQ_REQUIRE(x && qweight && qzeros && scales && out, MIQ_ERR_INVALID, "gptq_gemm_f32x: null pointer");
+  MIQ_REQUIRE(N % 4 == 0 && K % 32 == 0 && aligned(qweight, 16) && aligned(x, 16) && aligned(scales, 4) &&
+                  (!perm || aligned(perm, 16)),
+              MIQ_ERR_ALIGN, "gptq_gemm_f32x: x, qweight and perm must be 16-byte aligned, N %% 4 == 0, K %% 32 == 0");
+  MIQ_REQUIRE(scales_dtype == MIQ_F16 || scales_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "gptq_gemm_f32x: scales dtype");
+  MIQ_REQUIRE(out_dtype == MIQ_F16 || out_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "gptq_gemm_f32x: out dtype");
+  MIQ_REQUIRE(zero_offset == (float)(int)zero_offset && zero_offset >= 0.f && zero_offset <= 8.f, MIQ_ERR_UNSUPPORTED,
+              "gptq_gemm_f32x: zero_offset %g (the exact fp16 path takes a small integer)", zero_offset);
+  MIQ_REQUIRE(K <= 32768, MIQ_ERR_UNSUPPORTED, "gptq_gemm_f32x: K=%d > 32768 (a row is staged in LDS)", K);
+  F32Plan p;
+  rc = f32_plan(M, K, N, gs, bits, &p);
+  if (rc) return rc;
+  MIQ_REQUIRE(workspace && workspace_bytes >= p.ws_bytes && aligned(workspace, 256), MIQ_ERR_INVALID,
+              "gptq_gemm_f32x: workspace of %zu bytes (256-byte aligned) needed, %zu given", p.ws_bytes, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  __half* xp = reinterpret_cast<__half*>(ws + kCounterBytes + p.g.partial_bytes);
+  float* y2 = reinterpret_cast<float*>(ws + p.y2_off);
+  float* rmax = reinterpret_cast<float*>(ws + p.rmax_off);
+  const size_t lds = (size_t)K * 4;
+  if (lds > 64 * 1024 && (rc = require_lds("gptq_gemm_f32x staging", lds))) return rc;
+#define MIQ_F32_STAGE(B, P)                                                                                      \
+  hipLaunchKernelGGL((stage_rows_f32_kernel<B, P>), dim3(M), dim3(256), lds, st, x, perm, rmax, xp, M, K, p.g.kc)
+  if (bits == 4) {
+    if (perm) MIQ_F32_STAGE(4, true); else MIQ_F32_STAGE(4, false);
+  } else {
+    if (perm) MIQ_F32_STAGE(8, true); else MIQ_F32_STAGE(8, false);
+  }
+#undef MIQ_F32_STAGE
+  rc = check_launch("gptq_gemm_f32x staging");
+  if (rc) return rc;
+  rc = bits == 4 ? gemm_dispatch<4>(p.g, xp, qweight, qzeros, scales, scales_dtype, nullptr, y2, MIQ_F32, workspace,
+                                    2 * M, K, N, gs, zero_offset, st)
+                 : gemm_dispatch<8>(p.g, xp, qweight, qzeros, scales, scales_dtype, nullptr, y2, MIQ_F32, workspace,
+                                    2 * M, K, N, gs, zero_offset, st);
+  if (rc) return rc;
+  const dim3 g((N / 4 + 255) / 256, M);
+  if (out_dtype == MIQ_F16)
+    hipLaunchKernelGGL(combine_rows_kernel<__half>, g, dim3(256), 0, st, y2, rmax, bias, static_cast<__half*>(out), M, N);
+  else
+    hipLaunchKernelGGL(combine_rows_kernel<float>, g, dim3(256), 0, st, y2, rmax, bias, static_cast<float*>(out), M, N);
+  return check_launch("gptq_gemm_f32x combine");
+}
 
 extern "C" int miq_gptq_gemm_workspace(int M, int K, int N, int gs, int bits, size_t* bytes) {
   MIQ_REQUIRE(bytes, MIQ_ERR_INVALID, "gptq_gemm_workspace: null output");

@@ -178,6 +178,8 @@ class CausalLM:
         for M in range(1, T + 1):  # the head only ever sees the last token
             for lin in [self.layers[0][k] for k in ("qkv", "o", "gate_up", "down")]:
                 need = max(need, core.gemv_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits, _lib.MIQ_F32))
+                if M > core.GEMV_MAX_M:  # prefill rows on the matrix cores
+                    need = max(need, core.gemm_f32x_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits))
         self.ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
         self._alloc_persistent()
 
