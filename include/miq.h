@@ -262,6 +262,14 @@ int miq_embed(const int32_t* ids, const void* embed, float* out, int T, int H, i
  * Replaces: `CausalLM._rms` (webtorch/llm.py:1259-1268) and `rmsnorm` (webtorch/_core.py:2234-2263). */
 int miq_rmsnorm(const float* x, const float* w, float* out, int T, int H, float eps, void* stream);
 
+/* Per-head RMSNorm (QK-norm, Qwen3) in place on the fused q|k|v rows qkv [T][(NH + 2 NKV) HD]:
+ * each query head x / sqrt(mean(x^2) + eps) * qn (fp32 [HD]), each key head the same with kn;
+ * a null weight leaves that part alone; v is untouched. HD <= 256.
+ * Replaces: `self._rms(q, lay["qn"])` / `self._rms(k, lay["kn"])` of `CausalLM._qkv`
+ * (webtorch/llm.py:1498-1519, 1259-1268), applied before RoPE. */
+int miq_head_rmsnorm(float* qkv, const float* qn, const float* kn, int T, int NH, int NKV, int HD, float eps,
+                     void* stream);
+
 /* Rotate-half RoPE at positions state[0] + t of the fused q|k|v rows qkv [T][(NH + 2 NKV) HD]
  * with the fp32 tables cos_tab / sin_tab [LMAX][HD/2] (cos/sin of pos * theta^(-2i/HD) in
  * float64, rounded once); q to q_out [T][NH][HD]; k, v written into the caches

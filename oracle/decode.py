@@ -89,6 +89,23 @@ class Qwen2Oracle:
             a = (a.reshape(nkv, rep, T, S) + mask).reshape(nkv, rep * T, S)
         return (self.softmax(a) @ V).reshape(nh, T, hd)
 
+    def mlp(self, lay, x):
+        """Dense SwiGLU, or the sparse-MoE block through `moe_mlp` when the layer carries "moe"
+        (`CausalLM._mlp`, `webtorch/llm.py:1489-1496`). The reference's layer dict names the
+        renormalisation flag "norm_topk" while `moe_mlp` reads "norm_topk_prob"
+        (`llm.py:523-524`, `lm_engine.py:304`), so the top-k weights are always renormalised."""
+        m = lay.get("moe")
+        if m is None:
+            return self.lin(lay["down"], self.silu(self.lin(lay["gate"], x)) * self.lin(lay["up"], x))
+        from . import moe
+        experts = [{k: (lambda t, d=d: self.lin(d, t)) for k, d in e.items()} for e in m["experts"]]
+        shared = None
+        if m.get("shared"):
+            shared = {k: (lambda t, d=d: self.lin(d, t)) for k, d in m["shared"].items()}
+        sg = m.get("shared_gate")
+        return moe.moe_mlp_np(x, self.lin(m["router"], x), experts, m["top_k"], True, shared=shared,
+                              shared_gate=None if sg is None else (lambda t: self.lin(sg, t)))
+
     # ---- forward ----
     def forward(self, ids, pos, cache):
         """One `_kv_forward` call: T tokens at positions pos.. -> greedy next id, logits."""
@@ -98,8 +115,13 @@ class Qwen2Oracle:
         scale = 1.0 / math.sqrt(self.HD)
         for i, lay in enumerate(self.layers):
             x = self.rms(h, lay["in_ln"])
-            q = self.lin(lay["q"], x).reshape(T, self.NH, self.HD).transpose(1, 0, 2)
-            k = self.lin(lay["k"], x).reshape(T, self.NKV, self.HD).transpose(1, 0, 2)
+            q = self.lin(lay["q"], x).reshape(T, self.NH, self.HD)
+            k = self.lin(lay["k"], x).reshape(T, self.NKV, self.HD)
+            if lay.get("qn") is not None:  # QK-norm over each head, before RoPE (`llm.py:1516-1517`)
+                q = self.rms(q, lay["qn"])
+            if lay.get("kn") is not None:
+                k = self.rms(k, lay["kn"])
+            q, k = q.transpose(1, 0, 2), k.transpose(1, 0, 2)
             v = self.lin(lay["v"], x).reshape(T, self.NKV, self.HD).transpose(1, 0, 2)
             q = q * cos + self.rot(q) * sin
             k = k * cos + self.rot(k) * sin
@@ -115,7 +137,7 @@ class Qwen2Oracle:
             o = self.attend(q, Kc, Vc, mask, scale)
             h = h + self.lin(lay["o"], o.transpose(1, 0, 2).reshape(T, self.NH * self.HD))
             x = self.rms(h, lay["post_ln"])
-            h = h + self.lin(lay["down"], self.silu(self.lin(lay["gate"], x)) * self.lin(lay["up"], x))
+            h = h + self.mlp(lay, x)
         last = self.rms(h, self.final_norm)[-1:]
         logits = np.concatenate([self.lin(b, last, zoff=0.0) for b in self.head], axis=-1)[0]
         return int(logits.argmax()), logits

@@ -124,11 +124,18 @@ def build_reference_lm(wt, llm, wts, lmax):
                                                 d["gs"], d["bits"])
     m.layers = []
     for lay in wts["layers"]:
-        m.layers.append({"in_ln": wt.Tensor(lay["in_ln"].astype(np.float32)),
-                         "post_ln": wt.Tensor(lay["post_ln"].astype(np.float32)),
-                         "q": ql(lay["q"]), "k": ql(lay["k"]), "v": ql(lay["v"]),
-                         "o": ql(lay["o"]), "qn": None, "kn": None,
-                         "gate": ql(lay["gate"]), "up": ql(lay["up"]), "down": ql(lay["down"])})
+        d = {"in_ln": wt.Tensor(lay["in_ln"].astype(np.float32)),
+             "post_ln": wt.Tensor(lay["post_ln"].astype(np.float32)),
+             "q": ql(lay["q"]), "k": ql(lay["k"]), "v": ql(lay["v"]), "o": ql(lay["o"]),
+             "qn": None if lay.get("qn") is None else wt.Tensor(lay["qn"].astype(np.float32)),
+             "kn": None if lay.get("kn") is None else wt.Tensor(lay["kn"].astype(np.float32))}
+        if lay.get("moe"):  # the layer dict `_build_layer` makes for a sparse layer (`llm.py:522-534`)
+            mo = lay["moe"]
+            d["moe"] = {"gate": ql(mo["router"]), "top_k": mo["top_k"], "norm_topk": True,
+                        "experts": [{k: ql(e[k]) for k in ("gate", "up", "down")} for e in mo["experts"]]}
+        else:
+            d.update({"gate": ql(lay["gate"]), "up": ql(lay["up"]), "down": ql(lay["down"])})
+        m.layers.append(d)
     m.final_norm = wt.Tensor(wts["final_norm"].astype(np.float32))
     m._init_state()
     return m
@@ -155,8 +162,8 @@ def _generate_with_margins(m, ids, max_new):
 SHAPE_KEYS = ("L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits")
 
 
-def make_decode(wt, llm, out, seed, shape, prompt_len, max_new, lmax, gaussian=False):
-    wts = synth.decoder_weights(seed, gaussian=gaussian, **shape)
+def make_decode(wt, llm, out, seed, shape, prompt_len, max_new, lmax, gaussian=False, **extra):
+    wts = synth.decoder_weights(seed, gaussian=gaussian, **shape, **extra)
     ids = synth.prompt_ids(seed, prompt_len, shape["V"])
     m = build_reference_lm(wt, llm, wts, lmax)
     toks, margins, spreads, dt = _generate_with_margins(m, ids, max_new)
@@ -164,7 +171,8 @@ def make_decode(wt, llm, out, seed, shape, prompt_len, max_new, lmax, gaussian=F
                                                                      len(set(toks)), dt, margins.min()))
     np.savez_compressed(out, seed=seed, prompt_len=prompt_len, max_new=max_new, lmax=lmax,
                         gaussian=int(gaussian), shape=np.array([shape[k] for k in SHAPE_KEYS]),
-                        tokens=np.asarray(toks, np.int64), margins=margins, spreads=spreads)
+                        tokens=np.asarray(toks, np.int64), margins=margins, spreads=spreads,
+                        extra=np.array([int(extra.get(k, 0)) for k in ("n_experts", "moe_I", "top_k", "qk_norm")]))
 
 
 def build_reference_fp16q(wt, llm, model, bits, lmax, gs=128):
@@ -238,6 +246,11 @@ def main():
     # shape) were chosen for their smallest per-step top-1/top-2 logit gap (recorded in the file)
     if want("decode_gauss_small", not a.full_only):
         make_decode(wt, llm, os.path.join(HERE, "decode_gauss_small.npz"), 14, SMALL, 16, 32, 64, gaussian=True)
+    # Qwen3-MoE-style layers: sparse MoE MLPs (8 experts of 128, top-2) and per-head q/k RMSNorm;
+    # seed 33 chosen for its varied ids and smallest top-1/top-2 gap
+    if want("decode_moe_qknorm_small", not a.full_only):
+        make_decode(wt, llm, os.path.join(HERE, "decode_moe_qknorm_small.npz"), 33, SMALL, 16, 32, 64, gaussian=True,
+                    n_experts=8, moe_I=128, top_k=2, qk_norm=1)
     if want("decode_fp16q_small", not a.full_only):
         make_fp16q(wt, llm, os.path.join(HERE, "decode_fp16q_small.npz"), 21, SMALL, 16, 32, 64)
     if want("decode_qwen2_05b", a.full or a.full_only):

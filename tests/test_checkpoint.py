@@ -24,18 +24,29 @@ SMALL = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
 def _hf_tensors(w, tie):
     """AutoGPTQ / HuggingFace tensor names of a synth.decoder_weights model."""
     t = {}
+
+    def put(name, d):
+        t[name + ".qweight"] = np.asarray(d["qweight"], np.int32)
+        t[name + ".qzeros"] = np.asarray(d["qzeros"], np.int32)
+        t[name + ".scales"] = np.asarray(d["scales"], np.float16)
+        t[name + ".g_idx"] = (np.arange(d["qweight"].shape[0] * 8) // w["cfg"]["gs"]).astype(np.int32)
+        if d.get("bias") is not None:
+            t[name + ".bias"] = np.asarray(d["bias"], np.float16)
     for i, lay in enumerate(w["layers"]):
         p = "model.layers.%d." % i
         for nm, hf in (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
                        ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
                        ("down", "mlp.down_proj")):
-            d = lay[nm]
-            t[p + hf + ".qweight"] = np.asarray(d["qweight"], np.int32)
-            t[p + hf + ".qzeros"] = np.asarray(d["qzeros"], np.int32)
-            t[p + hf + ".scales"] = np.asarray(d["scales"], np.float16)
-            t[p + hf + ".g_idx"] = (np.arange(d["qweight"].shape[0] * 8) // w["cfg"]["gs"]).astype(np.int32)
-            if d.get("bias") is not None:
-                t[p + hf + ".bias"] = np.asarray(d["bias"], np.float16)
+            if nm in lay:
+                put(p + hf, lay[nm])
+        if lay.get("moe"):
+            put(p + "mlp.gate", lay["moe"]["router"])
+            for e, ex in enumerate(lay["moe"]["experts"]):
+                for nm in ("gate", "up", "down"):
+                    put(p + "mlp.experts.%d.%s_proj" % (e, nm), ex[nm])
+        for key, nm in (("qn", "self_attn.q_norm.weight"), ("kn", "self_attn.k_norm.weight")):
+            if lay.get(key) is not None:
+                t[p + nm] = np.asarray(lay[key], np.float16)
         t[p + "input_layernorm.weight"] = np.asarray(lay["in_ln"], np.float16)
         t[p + "post_attention_layernorm.weight"] = np.asarray(lay["post_ln"], np.float16)
     t["model.embed_tokens.weight"] = np.asarray(w["embed"], np.float16)
@@ -54,6 +65,8 @@ def write_gptq_dir(path, w, tie=True, shards=1, declared=4096):
            "vocab_size": c["V"], "rms_norm_eps": 1e-6, "rope_theta": 1e6, "tie_word_embeddings": tie,
            "max_position_embeddings": declared,
            "quantization_config": {"bits": c["bits"], "group_size": c["gs"], "desc_act": False}}
+    if c.get("n_experts"):
+        cfg.update(num_experts=c["n_experts"], num_experts_per_tok=c["top_k"], moe_intermediate_size=c["moe_I"])
     os.makedirs(path, exist_ok=True)
     with open(os.path.join(path, "config.json"), "w") as f:
         json.dump(cfg, f)
@@ -195,13 +208,19 @@ def test_gptq_config_contract(tmp_path):
     base = {"hidden_size": 64, "num_hidden_layers": 1, "num_attention_heads": 2, "intermediate_size": 128,
             "vocab_size": 16}
     for extra, err in (({}, ValueError),  # no quantization_config
-                       ({"quantization_config": {"bits": 4, "group_size": 64}, "num_experts": 8}, NotImplementedError),
                        ({"quantization_config": {"bits": 4, "group_size": 64},
                          "layer_types": ["linear_attention"]}, NotImplementedError)):
         with open(tmp_path / "config.json", "w") as f:
             json.dump(dict(base, **extra), f)
         with pytest.raises(err):
             checkpoint.gptq_config(str(tmp_path))
+    # sparse MoE fields (`webtorch/llm.py:440-445`)
+    with open(tmp_path / "config.json", "w") as f:
+        json.dump(dict(base, quantization_config={"bits": 4, "group_size": 64}, num_experts=8, num_experts_per_tok=2,
+                       decoder_sparse_step=2, mlp_only_layers=[3]), f)
+    c, _, _ = checkpoint.gptq_config(str(tmp_path))
+    assert (c["n_experts"], c["top_k"], c["sparse_step"], c["mlp_only"], c["shared_expert"]) == (8, 2, 2, [3], False)
+    assert [checkpoint._is_moe_layer(c, i) for i in range(6)] == [False, True, False, False, False, True]
     # nested text_config, head_dim and the defaults
     with open(tmp_path / "config.json", "w") as f:
         json.dump({"text_config": dict(base, head_dim=48), "quantization_config": {"bits": 8, "group_size": 32}}, f)
@@ -377,3 +396,19 @@ def test_from_pretrained_dispatch_and_refusals(gpu, tmp_path):
             llm.AutoModelForCausalLM.from_pretrained(str(tmp_path / "fp16"), dtype=dt, lmax=64)
     with pytest.raises(ValueError, match="dtype"):
         llm.AutoModelForCausalLM.from_pretrained(str(tmp_path / "fp16"), dtype="int3")
+
+
+@pytest.mark.gpu
+def test_from_gptq_moe_qknorm_directory(gpu, tmp_path):
+    """A Qwen3-MoE-style AutoGPTQ directory (router `mlp.gate`, experts `mlp.experts.{e}.*`,
+    `self_attn.{q,k}_norm`) loads into the engine and decodes the reference's greedy ids."""
+    from webpytorch_amd import llm
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "decode_moe_qknorm_small.npz"))
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits"], [int(v) for v in g["shape"]]))
+    ne, mi, k, qk = [int(v) for v in g["extra"]]
+    w = synth.decoder_weights(int(g["seed"]), gaussian=True, n_experts=ne, moe_I=mi, top_k=k, qk_norm=bool(qk), **sh)
+    write_gptq_dir(str(tmp_path), w, shards=2)
+    m = llm.CausalLM.from_gptq(str(tmp_path), lmax=int(g["lmax"]))
+    assert m.has_moe and m.has_qk_norm and m.pws is None
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    assert m.generate(ids, int(g["max_new"])).tokens == [int(t) for t in g["tokens"]]

@@ -224,6 +224,51 @@ def test_decode_matches_reference_golden_gaussian_qwen2_05b(gpu):
         assert m.generate(ids, int(g["max_new"])).tokens == want
 
 
+def test_decode_moe_qknorm_matches_reference_golden(gpu):
+    """Sparse-MoE layers (router GEMV, device routing, grouped expert GEMMs) and per-head q/k
+    RMSNorm inside the engine: the reference's greedy ids (its `CausalLM` CPU decode with the
+    same layer dicts), eager fused, eager unfused (prefill-style launches per token) and
+    graph-replayed with the routing live."""
+    from webpytorch_amd import llm
+    g = np.load(os.path.join(GOLDEN, "decode_moe_qknorm_small.npz"))
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits"], [int(v) for v in g["shape"]]))
+    ne, mi, k, qk = [int(v) for v in g["extra"]]
+    w = synth.decoder_weights(int(g["seed"]), gaussian=True, n_experts=ne, moe_I=mi, top_k=k, qk_norm=bool(qk), **sh)
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    want = [int(t) for t in g["tokens"]]
+    m = llm.CausalLM.from_weights(w, lmax=int(g["lmax"]))
+    assert m.pws is None  # the persistent step covers dense layers only
+    n = int(g["max_new"])
+    assert m.generate(ids, n, use_graph=False).tokens == want
+    m.fused = False
+    assert m.generate(ids, n, use_graph=False).tokens == want
+    m.fused = True
+    assert m.generate(ids, n).tokens == want
+    assert m.generate(ids, n).tokens == want  # the captured graph again, routing re-run per replay
+
+
+def test_head_rmsnorm_vs_oracle(gpu):
+    import torch
+    from webpytorch_amd import _lib, core
+    T, NH, NKV, HD = 5, 6, 2, 64
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((T, (NH + 2 * NKV) * HD)) * 3).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    qd, kd = torch.from_numpy(qn).cuda(), torch.from_numpy(kn).cuda()  # kept alive across the launch
+    _lib.call("miq_head_rmsnorm", core.ptr(xd), core.ptr(qd), core.ptr(kd), T, NH, NKV, HD, 1e-6,
+              core.stream_handle())
+    got = xd.cpu().numpy()
+    o = decode.Qwen2Oracle.__new__(decode.Qwen2Oracle)
+    o.eps = 1e-6
+    q = o.rms(x[:, :NH * HD].reshape(T, NH, HD), qn).reshape(T, -1)
+    k = o.rms(x[:, NH * HD:(NH + NKV) * HD].reshape(T, NKV, HD), kn).reshape(T, -1)
+    np.testing.assert_allclose(got[:, :NH * HD], q, rtol=2e-6, atol=1e-6)
+    np.testing.assert_allclose(got[:, NH * HD:(NH + NKV) * HD], k, rtol=2e-6, atol=1e-6)
+    assert np.array_equal(got[:, (NH + NKV) * HD:], x[:, (NH + NKV) * HD:])
+
+
 def test_generate_refuses_overlong(gpu):
     g = np.load(os.path.join(GOLDEN, "decode_small.npz"))
     m, ids, _ = _engine(g, 20)

@@ -124,3 +124,27 @@ def test_fp16_quantize_on_load_matches_reference_golden(bits):
     toks, _ = o.generate(ids, int(g["max_new"]))
     want = [int(t) for t in g["tokens_int%d" % bits]]
     assert toks == want and len(set(want)) >= 16
+
+
+def _moe_fixture():
+    g = np.load(os.path.join(GOLDEN, "decode_moe_qknorm_small.npz"))
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits"], [int(v) for v in g["shape"]]))
+    ne, mi, k, qk = [int(v) for v in g["extra"]]
+    w = synth.decoder_weights(int(g["seed"]), gaussian=True, n_experts=ne, moe_I=mi, top_k=k, qk_norm=bool(qk), **sh)
+    return g, sh, w
+
+
+def test_decode_moe_qknorm_matches_reference_golden():
+    """Sparse-MoE layers (router, 8 experts, top-2) with per-head q/k RMSNorm: the oracle's
+    greedy ids and per-step logit gaps equal those of the reference's `CausalLM` CPU decode."""
+    g, sh, w = _moe_fixture()
+    o = decode.Qwen2Oracle(w, lmax=int(g["lmax"]))
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    toks, logs = o.generate(ids, int(g["max_new"]), keep_logits=True)
+    assert toks == [int(t) for t in g["tokens"]] and len(set(toks)) >= 16
+    gaps = [float(np.diff(np.partition(lg, -2)[-2:])[0]) for lg in logs]
+    np.testing.assert_allclose(gaps, g["margins"], rtol=1e-3, atol=1e-5)
+    # the QK-norm is what the reference applied: without it the ids differ
+    for lay in w["layers"]:
+        lay.pop("qn"), lay.pop("kn")
+    assert decode.Qwen2Oracle(w, lmax=int(g["lmax"])).generate(ids, int(g["max_new"]))[0] != toks

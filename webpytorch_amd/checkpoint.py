@@ -167,8 +167,12 @@ def _shape_config(cfg, gs, bits):
                HD=int(cfg.get("head_dim") or H // NH), I=int(cfg["intermediate_size"]),
                V=int(cfg["vocab_size"]), eps=float(cfg.get("rms_norm_eps", 1e-6)),
                theta=float(cfg.get("rope_theta", 10000.0)), gs=int(gs), bits=int(bits))
-    if int(cfg.get("num_experts", cfg.get("num_local_experts", 0)) or 0):
-        raise NotImplementedError("sparse-MoE decoders are run through moe_mlp, not CausalLM")
+    ne = int(cfg.get("num_experts", cfg.get("num_local_experts", 0)) or 0)
+    if ne:  # sparse MoE (`webtorch/llm.py:440-445, 477-479`)
+        out.update(n_experts=ne, top_k=int(cfg.get("num_experts_per_tok", 0) or 0),
+                   sparse_step=int(cfg.get("decoder_sparse_step", 1) or 1),
+                   mlp_only=sorted(int(i) for i in (cfg.get("mlp_only_layers") or [])),
+                   shared_expert=bool(cfg.get("shared_expert_intermediate_size", 0)))
     types = cfg.get("layer_types") or []
     if any(t != "full_attention" for t in types) or int(cfg.get("full_attention_interval", 0) or 0) > 1:
         raise NotImplementedError("hybrid linear-attention decoders are not part of this path")
@@ -186,32 +190,72 @@ def gptq_config(path):
     return out, bool(cfg.get("tie_word_embeddings", False)), cfg.get("max_position_embeddings")
 
 
+def _is_moe_layer(cfg, i):
+    """`CausalLM._is_moe_layer` (`webtorch/llm.py:477-479`)."""
+    return (cfg.get("n_experts", 0) > 0 and i not in cfg.get("mlp_only", [])
+            and (i + 1) % cfg.get("sparse_step", 1) == 0)
+
+
+def _decoder_layers(st, cfg, lin):
+    """The layer dicts of `llm.CausalLM` read with the format's linear factory `lin(prefix)`, as
+    `_build_layer` does (`webtorch/llm.py:506-539`): attention projections, optional per-head
+    q/k RMSNorm weights (Qwen3), and either a dense SwiGLU or a sparse-MoE block (router
+    `mlp.gate`, experts `mlp.experts.{e}.*`, optional shared expert and its gate)."""
+    layers = []
+    for i in range(cfg["L"]):
+        p = "model.layers.%d." % i
+        lay = {"q": lin(p + "self_attn.q_proj"), "k": lin(p + "self_attn.k_proj"),
+               "v": lin(p + "self_attn.v_proj"), "o": lin(p + "self_attn.o_proj"),
+               "in_ln": st.array(p + "input_layernorm.weight"),
+               "post_ln": st.array(p + "post_attention_layernorm.weight")}
+        for key, nm in (("qn", "self_attn.q_norm.weight"), ("kn", "self_attn.k_norm.weight")):
+            if p + nm in st:
+                lay[key] = st.array(p + nm)
+        if _is_moe_layer(cfg, i):
+            mo = {"router": lin(p + "mlp.gate"), "top_k": cfg["top_k"],
+                  "experts": [{"gate": lin(p + "mlp.experts.%d.gate_proj" % e),
+                               "up": lin(p + "mlp.experts.%d.up_proj" % e),
+                               "down": lin(p + "mlp.experts.%d.down_proj" % e)} for e in range(cfg["n_experts"])]}
+            if cfg.get("shared_expert"):
+                mo["shared"] = {"gate": lin(p + "mlp.shared_expert.gate_proj"), "up": lin(p + "mlp.shared_expert.up_proj"),
+                                "down": lin(p + "mlp.shared_expert.down_proj")}
+                mo["shared_gate"] = _shared_gate(st, p + "mlp.shared_expert_gate", cfg)
+            lay["moe"] = mo
+        else:
+            lay.update({"gate": lin(p + "mlp.gate_proj"), "up": lin(p + "mlp.up_proj"),
+                        "down": lin(p + "mlp.down_proj")})
+        layers.append(lay)
+    return layers
+
+
+def _shared_gate(st, prefix, cfg):
+    """The shared expert's one-output gate: a linear of 1 column, quantized on load from its float
+    weight with the output padded to the pack size (`QuantizedLinear.from_linear`)."""
+    class _W:
+        pass
+    w = _W()
+    w.weight = np.ascontiguousarray(st.array(prefix + ".weight").astype(np.float32).T)  # (in, out)
+    w.bias = st.array(prefix + ".bias") if prefix + ".bias" in st else np.zeros(w.weight.shape[1], np.float32)
+    return core.QuantizedLinear.from_linear(w, group_size=cfg["gs"], bits=cfg["bits"])
+
+
 def gptq_weights(path):
     """`llm.CausalLM` weights from an AutoGPTQ safetensors directory, plus the model's
-    declared context length: (weights, declared_lmax)."""
+    declared context length: (weights, declared_lmax). A linear stored unquantized in such a
+    directory (a MoE router kept in fp16, say) is quantized on load as `from_fp16` would."""
     cfg, tie, declared = gptq_config(path)
     st = SafetensorsDir(path)
 
     def lin(prefix):
+        if prefix + ".qweight" not in st and prefix + ".weight" in st:
+            return _quantize_linear(st, prefix, cfg["gs"], cfg["bits"])
         d = {"qweight": st.array(prefix + ".qweight"), "qzeros": st.array(prefix + ".qzeros"),
              "scales": st.array(prefix + ".scales", keep_f16=True)}
         if prefix + ".bias" in st:
             d["bias"] = st.array(prefix + ".bias")
         return d
 
-    if "model.layers.0.self_attn.q_norm.weight" in st:
-        raise NotImplementedError("QK-norm decoders (Qwen3) are not part of this path")
-    layers = []
-    for i in range(cfg["L"]):
-        p = "model.layers.%d." % i
-        lay = {"q": lin(p + "self_attn.q_proj"), "k": lin(p + "self_attn.k_proj"),
-               "v": lin(p + "self_attn.v_proj"), "o": lin(p + "self_attn.o_proj"),
-               "gate": lin(p + "mlp.gate_proj"), "up": lin(p + "mlp.up_proj"),
-               "down": lin(p + "mlp.down_proj"),
-               "in_ln": st.array(p + "input_layernorm.weight"),
-               "post_ln": st.array(p + "post_attention_layernorm.weight")}
-        layers.append(lay)
-    w = {"layers": layers, "embed": st.rows_f16("model.embed_tokens.weight"),
+    w = {"layers": _decoder_layers(st, cfg, lin), "embed": st.rows_f16("model.embed_tokens.weight"),
          "final_norm": st.array("model.norm.weight"), "cfg": cfg}
     if not tie:
         w["head"] = st.rows_f16("lm_head.weight")
@@ -360,9 +404,20 @@ class GGUFFile:
         return core.GGMLLinear(self.raw(name), nm, K, N, bias)
 
 
-PROJECTIONS = (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
-               ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
-               ("down", "mlp.down_proj"))
+def _quantize_linear(st, prefix, gs, bits):
+    """One float (out, in) linear of a safetensors directory quantized on the device in its file
+    encoding (`_gquant`, `webtorch/llm.py:835-853`: gs 128, zero offset 0, fp32 scales)."""
+    import torch
+    info, _ = st.info(prefix + ".weight")
+    N, K = (int(d) for d in info["shape"])
+    if K % gs or N % (32 // bits):
+        raise NotImplementedError("%s: (%d, %d) needs padding to the group / pack size" % (prefix, N, K))
+    W = torch.from_numpy(st.array(prefix + ".weight", keep_f16=True))
+    qw, qz, sc, _, _ = core.gptq_quantize(W, gs, bits, from_out_in=True)
+    d = {"qweight": qw, "qzeros": qz, "scales": sc, "zoff": 0.0}
+    if prefix + ".bias" in st:
+        d["bias"] = st.array(prefix + ".bias")
+    return d
 
 
 def fp16_weights(path, bits, gs=128):
@@ -372,7 +427,6 @@ def fp16_weights(path, bits, gs=128):
     `core.gptq_quantize` -- the reference's `_gquant` (`webtorch/llm.py:835-853`): group size
     128, asymmetric min-max, zero offset 0, fp32 scales; int8 is the same rule with 8-bit codes.
     Returns (weights, declared context length)."""
-    import torch
     full = read_config(path)
     cfg = _text_config(full)
     if full.get("quantization_config") or cfg.get("quantization_config"):
@@ -381,31 +435,9 @@ def fp16_weights(path, bits, gs=128):
         raise NotImplementedError("quantize-on-load to %s bits (4 or 8)" % bits)
     shape = _shape_config(cfg, gs, bits)
     st = SafetensorsDir(path)
-    if "model.layers.0.self_attn.q_norm.weight" in st:
-        raise NotImplementedError("QK-norm decoders (Qwen3) are not part of this path")
-    per = 32 // int(bits)
-
-    def lin(prefix):
-        info, _ = st.info(prefix + ".weight")
-        N, K = (int(d) for d in info["shape"])
-        if K % gs or N % per:
-            raise NotImplementedError("%s: (%d, %d) needs padding to the group / pack size" % (prefix, N, K))
-        W = torch.from_numpy(st.array(prefix + ".weight", keep_f16=True))
-        qw, qz, sc, _, _ = core.gptq_quantize(W, gs, int(bits), from_out_in=True)
-        d = {"qweight": qw, "qzeros": qz, "scales": sc, "zoff": 0.0}
-        if prefix + ".bias" in st:
-            d["bias"] = st.array(prefix + ".bias")
-        return d
-
-    layers = []
-    for i in range(shape["L"]):
-        p = "model.layers.%d." % i
-        lay = {nm: lin(p + hf) for nm, hf in PROJECTIONS}
-        lay["in_ln"] = st.array(p + "input_layernorm.weight")
-        lay["post_ln"] = st.array(p + "post_attention_layernorm.weight")
-        layers.append(lay)
-    w = {"layers": layers, "embed": st.rows_f16("model.embed_tokens.weight"),
-         "final_norm": st.array("model.norm.weight"), "cfg": shape}
+    w = {"layers": _decoder_layers(st, shape, lambda prefix: _quantize_linear(st, prefix, gs, int(bits))),
+         "embed": st.rows_f16("model.embed_tokens.weight"), "final_norm": st.array("model.norm.weight"),
+         "cfg": shape}
     if not cfg.get("tie_word_embeddings", False):
         w["head"] = st.rows_f16("lm_head.weight")
     return w, cfg.get("max_position_embeddings")

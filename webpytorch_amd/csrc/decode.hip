@@ -52,6 +52,36 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   for (int c = threadIdx.x; c < H; c += 256) o[c] = (xr[c] / r) * w[c];
 }
 
+// Per-head RMSNorm (QK-norm) in place on fused q|k|v rows [T][(NH + 2 NKV) HD]: each of the NH
+// query heads by qn [HD], each of the NKV key heads by kn [HD] (null: that part untouched); the v
+// heads are left alone. One wave per (token, head), HD <= 256.
+__global__ __launch_bounds__(256) void head_rmsnorm_kernel(float* __restrict__ qkv, const float* __restrict__ qn,
+                                                           const float* __restrict__ kn, int T, int NH, int NKV,
+                                                           int HD, float eps) {
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int nh = NH + NKV;
+  if (wid >= T * nh) return;  // whole waves
+  const int t = wid / nh, h = wid % nh;
+  const float* w = h < NH ? qn : kn;
+  if (!w) return;
+  float* row = qkv + (size_t)t * (NH + 2 * NKV) * HD + (size_t)h * HD;
+  float v[4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    v[i] = d < HD ? row[d] : 0.f;
+    s = s + v[i] * v[i];
+  }
+  s = wave_sum(s);
+  const float r = sqrtf(s / (float)HD + eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    if (d < HD) row[d] = (v[i] / r) * w[d];
+  }
+}
+
 // Rotate-half RoPE at positions pos0 + t (pos0 read from the device) with the fp32 cos/sin
 // table [LMAX][HD/2] (float64 angles rounded once, as the reference builds it), then
 // x*cos + rot(x)*sin rounded like the numpy expression. q goes to q_out [T][NH][HD]; k and v
@@ -392,6 +422,18 @@ extern "C" int miq_rmsnorm(const float* x, const float* w, float* out, int T, in
   MIQ_REQUIRE(x && w && out, MIQ_ERR_INVALID, "rmsnorm: null pointer");
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, static_cast<hipStream_t>(stream), x, w, out, H, eps);
   return check_launch("rmsnorm");
+}
+
+extern "C" int miq_head_rmsnorm(float* qkv, const float* qn, const float* kn, int T, int NH, int NKV, int HD, float eps,
+                                void* stream) {
+  MIQ_REQUIRE(T >= 0 && NH > 0 && NKV > 0 && HD > 0 && HD <= 256, MIQ_ERR_INVALID,
+              "head_rmsnorm: T=%d NH=%d NKV=%d HD=%d (HD <= 256)", T, NH, NKV, HD);
+  if (T == 0 || (!qn && !kn)) return MIQ_OK;
+  MIQ_REQUIRE(qkv, MIQ_ERR_INVALID, "head_rmsnorm: null pointer");
+  const int waves = T * (NH + NKV);
+  hipLaunchKernelGGL(head_rmsnorm_kernel, dim3((waves + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream), qkv,
+                     qn, kn, T, NH, NKV, HD, eps);
+  return check_launch("head_rmsnorm");
 }
 
 extern "C" int miq_rope_kv(const float* qkv, const int32_t* state, const float* cos_tab, const float* sin_tab,

@@ -64,6 +64,14 @@ def _cat_layers(parts, gs, bits):
     return out
 
 
+def _gptq_dict(d, gs, bits):
+    """A GPTQ layer dict as a QuantizedLinear with its own zero offset (AutoGPTQ tensors: 1)."""
+    per = 32 // bits
+    K, N = int(np.shape(d["qweight"])[0]) * per, int(np.shape(d["qweight"])[1])
+    return core.QuantizedLinear(d["qweight"], d["qzeros"], d["scales"], d.get("bias"), K, N, K, N, gs, bits,
+                                zero_offset=float(d.get("zoff", 1.0)))
+
+
 class _Lin:
     """Device tensors of one (possibly fused) GPTQ linear. The zero offset is the layer's own:
     1 for AutoGPTQ tensors (stored zero - 1), 0 for layers quantized on load."""
@@ -100,15 +108,28 @@ class CausalLM:
         self.lmax = int(lmax)
         core.device()
         self.layers = []
+        vec = lambda v: None if v is None else core.to_device(v if isinstance(v, torch.Tensor) else  # noqa: E731
+                                                              np.asarray(v, np.float32), torch.float32)
         for lay in weights["layers"]:
-            self.layers.append({
-                "qkv": _Lin(_cat_layers([lay["q"], lay["k"], lay["v"]], self.gs, self.bits), self.H, self.gs, self.bits),
-                "o": _Lin(lay["o"], self.NH * self.HD, self.gs, self.bits),
-                "gate_up": _Lin(_cat_layers([lay["gate"], lay["up"]], self.gs, self.bits), self.H, self.gs, self.bits),
-                "down": _Lin(lay["down"], self.I, self.gs, self.bits),
-                "in_ln": core.to_device(np.asarray(lay["in_ln"], np.float32)),
-                "post_ln": core.to_device(np.asarray(lay["post_ln"], np.float32)),
-            })
+            d = {"qkv": _Lin(_cat_layers([lay["q"], lay["k"], lay["v"]], self.gs, self.bits), self.H, self.gs, self.bits),
+                 "o": _Lin(lay["o"], self.NH * self.HD, self.gs, self.bits),
+                 "in_ln": vec(lay["in_ln"]), "post_ln": vec(lay["post_ln"]),
+                 "qn": vec(lay.get("qn")), "kn": vec(lay.get("kn"))}
+            mo = lay.get("moe")
+            if mo:  # sparse MoE MLP (`CausalLM._mlp` -> `moe_mlp`, `webtorch/llm.py:1489-1496`)
+                lin = lambda e: _gptq_dict(e, self.gs, self.bits)  # noqa: E731
+                d["moe"] = {"router": _Lin(mo["router"], self.H, self.gs, self.bits),
+                            "experts": core.MoEExperts([{k: lin(e[k]) for k in ("gate", "up", "down")}
+                                                        for e in mo["experts"]]),
+                            "top_k": int(mo["top_k"]),
+                            "shared": core.SharedExpert({k: lin(mo["shared"][k]) for k in ("gate", "up", "down")},
+                                                        mo.get("shared_gate")) if mo.get("shared") else None}
+            else:
+                d["gate_up"] = _Lin(_cat_layers([lay["gate"], lay["up"]], self.gs, self.bits), self.H, self.gs, self.bits)
+                d["down"] = _Lin(lay["down"], self.I, self.gs, self.bits)
+            self.layers.append(d)
+        self.has_moe = any("moe" in lay for lay in self.layers)
+        self.has_qk_norm = any(lay["qn"] is not None or lay["kn"] is not None for lay in self.layers)
         self.embed = core.to_device(np.asarray(weights["embed"], np.float16))
         self.final_norm = core.to_device(np.asarray(weights["final_norm"], np.float32))
         head = weights.get("head")
@@ -160,8 +181,12 @@ class CausalLM:
         z = lambda *s: torch.zeros(s, dtype=f32, device=dev)  # noqa: E731
         qkvd = (self.NH + 2 * self.NKV) * self.HD
         self.buf = {"h": z(T, self.H), "xn": z(T, self.H), "qkv": z(T, qkvd), "q": z(T, self.NH * self.HD),
-                    "att": z(T, self.NH * self.HD), "gu": z(T, 2 * self.I), "act": z(T, self.I), "tmp": z(T, self.H),
-                    "hl": z(1, self.H), "logits": z(1, self.V)}
+                    "att": z(T, self.NH * self.HD), "tmp": z(T, self.H), "hl": z(1, self.H), "logits": z(1, self.V)}
+        if not all("moe" in lay for lay in self.layers):
+            self.buf.update(gu=z(T, 2 * self.I), act=z(T, self.I))
+        if self.has_moe:
+            E = max(int(lay["moe"]["router"].N) for lay in self.layers if "moe" in lay)
+            self.buf["rlog"] = z(T, E)
         self.kc = torch.zeros((self.L, self.NKV, self.lmax, self.HD), dtype=f32, device=dev)
         self.vc = torch.zeros_like(self.kc)
         # RoPE tables exactly as `_rope_np` builds them (float64 angles, rounded once to fp32)
@@ -175,8 +200,15 @@ class CausalLM:
         # one split-K workspace sized for every projection at T = 1 and at the largest prefill
         # (the need is not monotonic in the row count: wide enough layers stop splitting K)
         need = core.gemv_workspace_bytes(1, self.head.K, self.head.N, self.gs, self.bits, _lib.MIQ_F32)
+        lins = {}
+        for lay in self.layers:
+            for k in ("qkv", "o", "gate_up", "down"):
+                if k in lay:
+                    lins[k] = lay[k]
+            if "moe" in lay:
+                lins["router"] = lay["moe"]["router"]
         for M in range(1, T + 1):  # the head only ever sees the last token
-            for lin in [self.layers[0][k] for k in ("qkv", "o", "gate_up", "down")]:
+            for lin in lins.values():
                 need = max(need, core.gemv_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits, _lib.MIQ_F32))
                 if M > core.GEMV_MAX_M:  # prefill rows on the matrix cores
                     need = max(need, core.gemm_f32x_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits))
@@ -188,6 +220,10 @@ class CausalLM:
         shape is supported and the layers carry fp16 scales (else the launch sequence runs)."""
         self.pws = None
         if self.persistent is False or not self.fused:
+            return
+        if self.has_moe or self.has_qk_norm:
+            if self.persistent:
+                raise ValueError("the persistent decode step covers dense layers without QK-norm")
             return
         lays = self.layers
         lins = [lay[k] for lay in lays for k in ("qkv", "o", "gate_up", "down")]
@@ -257,9 +293,13 @@ class CausalLM:
         scale = 1.0 / math.sqrt(self.HD)
         for i, lay in enumerate(self.layers):
             self._fused(lay["qkv"], h, _lib.MIQ_X_RMSNORM, lay["in_ln"], b["qkv"])
+            self._qk_norm(lay, 1)
             _lib.call("miq_attention_decode", ptr(b["qkv"]), ptr(self.state), ptr(self.cos_t), ptr(self.sin_t),
                       ptr(self.kc[i]), ptr(self.vc[i]), ptr(b["att"]), self.NH, self.NKV, self.HD, self.lmax, scale, st)
             self._linear(lay["o"], b["att"][:1], h, bias=h)
+            if "moe" in lay:
+                self._moe(lay, h, 1)
+                continue
             self._fused(lay["gate_up"], h, _lib.MIQ_X_RMSNORM, lay["post_ln"], b["gu"])
             self._fused(lay["down"], b["gu"][:1], _lib.MIQ_X_SWIGLU, None, h, bias=h)
         self._fused(self.head, h, _lib.MIQ_X_RMSNORM, self.final_norm, b["logits"])
@@ -279,11 +319,15 @@ class CausalLM:
         for i, lay in enumerate(self.layers):
             _lib.call("miq_rmsnorm", ptr(h), ptr(lay["in_ln"]), ptr(xn), T, H, self.eps, st)
             self._linear(lay["qkv"], xn, b["qkv"][:T])
+            self._qk_norm(lay, T)
             _lib.call("miq_rope_kv", ptr(b["qkv"]), ptr(self.state), ptr(self.cos_t), ptr(self.sin_t), ptr(b["q"]),
                       ptr(self.kc[i]), ptr(self.vc[i]), T, NH, NKV, HD, self.lmax, st)
             _lib.call("miq_attention", ptr(b["q"]), ptr(self.kc[i]), ptr(self.vc[i]), ptr(self.state), ptr(b["att"]), T,
                       NH, NKV, HD, self.lmax, scale, st)
             self._residual(lay["o"], b["att"][:T], h, T)
+            if "moe" in lay:
+                self._moe(lay, h, T)
+                continue
             _lib.call("miq_rmsnorm", ptr(h), ptr(lay["post_ln"]), ptr(xn), T, H, self.eps, st)
             self._linear(lay["gate_up"], xn, b["gu"][:T])
             _lib.call("miq_silu_mul", ptr(b["gu"]), ptr(b["act"]), T, I, st)
@@ -292,6 +336,32 @@ class CausalLM:
         self._linear(self.head, b["hl"], b["logits"])
         _lib.call("miq_argmax_advance", ptr(b["logits"]), self.V, ptr(self.ids), ptr(self.history), self.lmax,
                   ptr(self.state), T, st)
+
+    def _qk_norm(self, lay, T):
+        """Per-head RMSNorm of q and k in the fused q|k|v rows, before RoPE (Qwen3's QK-norm,
+        `CausalLM._qkv`, `webtorch/llm.py:1498-1519`); nothing for layers without it."""
+        if lay["qn"] is None and lay["kn"] is None:
+            return
+        _lib.call("miq_head_rmsnorm", ptr(self.buf["qkv"]), ptr(lay["qn"]), ptr(lay["kn"]), T, self.NH, self.NKV,
+                  self.HD, self.eps, stream_handle())
+
+    def _moe(self, lay, h, T):
+        """h += the sparse-MoE MLP of RMSNorm(h) (`moe_mlp`, `webtorch/lm_engine.py:294-329`): router
+        GEMV, device routing, grouped expert GEMMs and combine, plus the shared expert; all on the
+        current stream, so the decode step stays capturable with live routing. The reference's
+        layer dict names the flag "norm_topk" where `moe_mlp` reads "norm_topk_prob", so its top-k
+        weights are always renormalised; so are these."""
+        b, st = self.buf, stream_handle()
+        mo = lay["moe"]
+        xn = b["xn"][:T]
+        _lib.call("miq_rmsnorm", ptr(h), ptr(lay["post_ln"]), ptr(xn), T, self.H, self.eps, st)
+        E = mo["router"].N
+        logits = b["rlog"][:T, :E] if b["rlog"].shape[1] == E else b["rlog"].view(-1)[:T * E].view(T, E)
+        self._linear(mo["router"], xn, logits)
+        out = mo["experts"](xn, logits, mo["top_k"], True)
+        if mo["shared"] is not None:
+            mo["shared"].add_to(out, xn)
+        _lib.call("miq_add", ptr(h), ptr(out), T * self.H, st)
 
     def _residual(self, lin, x, h, T):
         """h += x @ W: fused into the GEMV (bias = out = h) for one token, an add otherwise."""

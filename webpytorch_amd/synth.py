@@ -181,19 +181,34 @@ def quantized_gaussian_layer(seed, K, N, gs=128, bits=4, name="w"):
 
 
 def decoder_weights(seed, L=24, H=896, NH=14, NKV=2, HD=64, I=4864, V=151936, gs=128,
-                    bits=4, embed_scale=0.02, gaussian=False, **_):
+                    bits=4, embed_scale=0.02, gaussian=False, n_experts=0, moe_I=None, top_k=2,
+                    qk_norm=False, **_):
     """Random-init Qwen2-shaped int4 decoder: AutoGPTQ int4 linears (q/k/v with fp16 bias),
     RMSNorm weights near 1, fp16 embeddings ~N(0, embed_scale**2) (the head is tied to them).
     The linears hold uniform random codes, zeros and |N|*0.01+1e-3 scales, or, with
-    `gaussian`, codes quantized from Gaussian weights (`quantized_gaussian_layer`)."""
+    `gaussian`, codes quantized from Gaussian weights (`quantized_gaussian_layer`).
+
+    `n_experts` > 0 makes every layer's MLP a sparse MoE block (Qwen3-MoE style): a router
+    linear H -> n_experts and n_experts {gate, up, down} experts of intermediate `moe_I`, top
+    `top_k`, stored under "moe". `qk_norm` adds the per-head q/k RMSNorm weights "qn"/"kn"
+    (fp16 [HD], near 1)."""
     make = (lambda K, N, name: quantized_gaussian_layer(seed, K, N, gs, bits, name=name)) if gaussian else \
         (lambda K, N, name: gptq_layer(seed, K, N, gs, bits, name=name))
     layers = []
     for i in range(L):
         p = "l%d." % i
         lay = {"q": make(H, NH * HD, p + "q"), "k": make(H, NKV * HD, p + "k"),
-               "v": make(H, NKV * HD, p + "v"), "o": make(NH * HD, H, p + "o"),
-               "gate": make(H, I, p + "gate"), "up": make(H, I, p + "up"), "down": make(I, H, p + "down")}
+               "v": make(H, NKV * HD, p + "v"), "o": make(NH * HD, H, p + "o")}
+        if n_experts:
+            mi = moe_I or I
+            lay["moe"] = {"router": make(H, n_experts, p + "router"), "top_k": int(top_k),
+                          "experts": [{"gate": make(H, mi, p + "e%d.gate" % e), "up": make(H, mi, p + "e%d.up" % e),
+                                       "down": make(mi, H, p + "e%d.down" % e)} for e in range(n_experts)]}
+        else:
+            lay.update({"gate": make(H, I, p + "gate"), "up": make(H, I, p + "up"), "down": make(I, H, p + "down")})
+        if qk_norm:
+            lay["qn"] = (1.0 + 0.1 * rng(seed, p + "qn").standard_normal(HD)).astype(np.float16)
+            lay["kn"] = (1.0 + 0.1 * rng(seed, p + "kn").standard_normal(HD)).astype(np.float16)
         for nm, n in (("q", NH * HD), ("k", NKV * HD), ("v", NKV * HD)):
             lay[nm]["bias"] = (rng(seed, p + nm + ".bias").standard_normal(n) * 0.02).astype(np.float16)
         lay["in_ln"] = (1.0 + 0.02 * rng(seed, p + "in_ln").standard_normal(H)).astype(np.float16)
@@ -201,8 +216,10 @@ def decoder_weights(seed, L=24, H=896, NH=14, NKV=2, HD=64, I=4864, V=151936, gs
         layers.append(lay)
     embed = (rng(seed, "embed").standard_normal((V, H)) * embed_scale).astype(np.float16)
     final_norm = (1.0 + 0.02 * rng(seed, "final_norm").standard_normal(H)).astype(np.float16)
-    return {"layers": layers, "embed": embed, "final_norm": final_norm,
-            "cfg": dict(L=L, H=H, NH=NH, NKV=NKV, HD=HD, I=I, V=V, gs=gs, bits=bits)}
+    cfg = dict(L=L, H=H, NH=NH, NKV=NKV, HD=HD, I=I, V=V, gs=gs, bits=bits)
+    if n_experts:
+        cfg.update(n_experts=int(n_experts), moe_I=int(moe_I or I), top_k=int(top_k))
+    return {"layers": layers, "embed": embed, "final_norm": final_norm, "cfg": cfg}
 
 
 def prompt_ids(seed, T=64, V=151936):
