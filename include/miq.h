@@ -184,20 +184,22 @@ int miq_q4k_dequant_f32(const uint8_t* blocks, float* out, int64_t n_blocks, voi
 int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out,
                  int out_dtype, int M, int K, int N, void* stream);
 
-/* out[M][N] = x[M][K] @ W^T + bias for the other native GGUF types a Q4_K_M file holds:
- * ggml_type 8 (Q8_0: 34-byte blocks of 32 weights, fp16 d + int8 codes) or 14 (Q6_K: 210-byte
- * super-blocks of 256 weights). W = N rows of K/32 (Q8_0) or K/256 (Q6_K) blocks as the file
- * stores them; w and x 16-byte aligned; M <= 65535. Other types: MIQ_ERR_UNSUPPORTED.
- * Replaces: `ggml_matmul` / `_ggml_run` for Q8_0 and Q6_K (webtorch/_core.py:3720-3779) with
- * the decode kernel `_GGML_GEMV_*` and `_Q8_0_DEC` / `_Q6K_DEC` (webtorch/_core.py:2985-3044,
- * 3071-3077, 3158-3176). */
+/* out[M][N] = x[M][K] @ W^T + bias for the native GGUF block types beside Q4_K, by ggml type id:
+ * 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 20 IQ4_NL (32 weights per block: 18, 20, 22, 24, 34,
+ * 18 bytes) and 10 Q2_K, 11 Q3_K, 13 Q5_K, 14 Q6_K, 23 IQ4_XS (256 per super-block: 84, 110, 176,
+ * 210, 136 bytes). W = N rows of K / (weights per block) blocks as the file stores them; w and x
+ * 16-byte aligned; M <= 65535. Other types: MIQ_ERR_UNSUPPORTED.
+ * Replaces: `ggml_matmul` / `_ggml_run` for these types (webtorch/_core.py:3720-3779) with the
+ * decode kernel `_GGML_GEMV_*` (webtorch/_core.py:2985-3044) and the type's decoder
+ * (`_Q8_0_DEC` 3072, `_IQ4NL_DEC` 3080, `_IQ4XS_DEC` 3094, `_Q5K_DEC` 3137, `_Q6K_DEC` 3159,
+ * `_Q3K_DEC` 3182, `_Q2K_DEC` 3214, `_Q4_0_DEC` .. `_Q5_1_DEC` 3419-3468). */
 int miq_ggml_gemv(const void* x, int x_dtype, const uint8_t* w, int ggml_type, const float* bias,
                   void* out, int out_dtype, int M, int K, int N, void* stream);
 
-/* Dequant n_blocks blocks of ggml_type 12 (Q4_K), 8 (Q8_0) or 14 (Q6_K) to fp32 (256, 32 or
- * 256 values each), bit-exact (every product is exact in fp32). blocks 2-byte aligned (16 for
- * Q4_K). Other types: MIQ_ERR_UNSUPPORTED.
- * Replaces: `ggufload.dequant` for Q4_K, Q8_0 and Q6_K (webtorch/ggufload.py:133-145, 188-222). */
+/* Dequant n_blocks blocks of ggml_type 12 (Q4_K) or any type miq_ggml_gemv takes to fp32,
+ * bit-exact (every value is one fp32 rounding of exact products). blocks 2-byte aligned (16
+ * for Q4_K). Other types: MIQ_ERR_UNSUPPORTED.
+ * Replaces: `ggufload.dequant` for the same types (webtorch/ggufload.py:133-320). */
 int miq_ggml_dequant_f32(const uint8_t* blocks, int ggml_type, float* out, int64_t n_blocks, void* stream);
 
 /* ---------------------------------------------------------------------------------------

@@ -278,8 +278,10 @@ def test_gguf_tensor_sizes():
     assert checkpoint.tensor_nbytes("F16", 7) == 14 and checkpoint.tensor_nbytes(0, 7) == 28
     with pytest.raises(ValueError):
         checkpoint.tensor_nbytes("Q4_K", 100)
+    assert checkpoint.tensor_nbytes(23, 512) == 2 * 136          # IQ4_XS
+    assert checkpoint.tensor_nbytes("IQ4_NL", 64) == 2 * 18
     with pytest.raises(NotImplementedError):
-        checkpoint.tensor_nbytes(23, 256)                         # IQ4_XS: not known here
+        checkpoint.tensor_nbytes(16, 256)                         # IQ2_XXS: not known here
 
 
 # ---- GPU -------------------------------------------------------------------------------------

@@ -64,9 +64,10 @@ def test_gemv_ragged_shapes_and_bias(gpu, K, N):
 
 def test_unsupported_type_raises(gpu):
     from webpytorch_amd import core
-    assert core.ggml_native_supported("Q4_K") and not core.ggml_native_supported("Q5_K")
+    assert core.ggml_native_supported("Q4_K") and core.ggml_native_supported("Q5_K")
+    assert not core.ggml_native_supported("IQ2_XXS")
     with pytest.raises(NotImplementedError):
-        core.GGMLLinear(b"\0" * 176, "Q5_K", 256, 1)
+        core.GGMLLinear(b"\0" * 66, "IQ2_XXS", 256, 1)
 
 
 # ---- Q8_0 and Q6_K (the other types of a Q4_K_M file) ------------------------------------
@@ -146,3 +147,86 @@ def test_ggml_matmul_accepts_the_reference_transposed_layout(gpu, type_name, K, 
     assert np.array_equal(a, b)
     with pytest.raises(ValueError):
         core.ggml_matmul(x, torch.from_numpy(transposed.view(np.int32)[:-1]).cuda(), type_name, K, N)
+
+
+# ---- the other llama.cpp block types -------------------------------------------------------
+
+NEW_TYPES = ["Q4_0", "Q4_1", "Q5_0", "Q5_1", "IQ4_NL", "IQ4_XS", "Q5_K", "Q2_K", "Q3_K"]
+
+
+@pytest.mark.parametrize("type_name", NEW_TYPES)
+def test_new_type_dequant_bit_exact_random_blocks(gpu, type_name):
+    """Device dequant of random blocks (every code and sub-scale byte uniform, fp16 fields of
+    mixed sign and magnitude, subnormals included, kept finite) matches the oracle bit for
+    bit."""
+    import torch
+    from oracle import ggml
+    from webpytorch_amd import core
+    f, vals, nbytes = ggml.DEQUANT[type_name]
+    g = np.random.default_rng(vals * 1000 + nbytes)
+    nb = 1531
+    raw = g.integers(0, 256, (nb, nbytes), dtype=np.uint8)
+    for off in ggml.F16_FIELDS[type_name]:
+        h = (g.standard_normal(nb) * np.exp2(g.integers(-26, 6, nb))).astype(np.float16)
+        raw[:, off:off + 2] = h.view(np.uint8).reshape(nb, 2)
+    got = core.ggml_dequant(torch.from_numpy(raw.reshape(-1)).cuda(), type_name, nb).cpu().numpy()
+    ref = f(raw.reshape(-1), nb * vals)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_name", NEW_TYPES)
+@pytest.mark.parametrize("M", [1, 2, 5])
+def test_new_type_gemv_llama3_up_shape(gpu, type_name, M):
+    """The llama-3-8B up projection (4096 -> 14336) in each type against the oracle's dequant
+    times x, one to five activation rows."""
+    import torch
+    from oracle import ggml
+    from webpytorch_amd import core
+    K, N = 4096, 14336
+    W = synth.ggml_layer(type_name, 3, K, N)
+    x = synth.activations(3, M, K, np.float16)
+    got = core.GGMLLinear(W, type_name, K, N)(torch.from_numpy(x)).cpu().numpy()
+    ref = ggml.ggml_matmul(x, W, type_name, K, N)
+    assert got.shape == (M, N) and _rel(got, ref) < 1e-5
+    assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+
+
+@pytest.mark.parametrize("type_name", NEW_TYPES)
+def test_new_type_ragged_rows_bias_dtypes(gpu, type_name):
+    """Odd block counts per row (rows at 2-byte offsets), a ragged row count, bias, fp32 and
+    fp16 activations, fp16 output, and GGMLLinear.dequantize bit-exact."""
+    import torch
+    from oracle import ggml
+    from webpytorch_amd import core
+    vals = ggml.DEQUANT[type_name][1]
+    K, N = 3 * vals if vals == 256 else 7 * vals, 37
+    W = synth.ggml_layer(type_name, K + N, K, N)
+    b = np.linspace(-1, 1, N).astype(np.float32)
+    lin = core.GGMLLinear(W, type_name, K, N, bias=b)
+    for xdt in (np.float32, np.float16):
+        x = synth.activations(K, 2, K, xdt)
+        ref = ggml.ggml_matmul(x, W, type_name, K, N) + b
+        got = lin(torch.from_numpy(x)).cpu().numpy()
+        assert _rel(got, ref) < 1e-5
+        got16 = lin.forward(torch.from_numpy(x), out_dtype=torch.float16).cpu().numpy()
+        assert got16.dtype == np.float16
+        assert np.all(np.abs(got16.astype(np.float32) - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+    deq = lin.dequantize().cpu().numpy()
+    ref = ggml.DEQUANT[type_name][0](W.reshape(-1), N * K).reshape(N, K)
+    assert np.array_equal(deq.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_name", NEW_TYPES)
+def test_new_type_prefill_rows(gpu, type_name):
+    """More activation rows than the one-row kernels take (a prefill of 24 tokens) go through
+    the same layer and match the oracle."""
+    import torch
+    from oracle import ggml
+    from webpytorch_amd import core
+    K, N = 2048, 96
+    W = synth.ggml_layer(type_name, 11, K, N)
+    x = synth.activations(11, 24, K, np.float32)
+    got = core.GGMLLinear(W, type_name, K, N)(torch.from_numpy(x)).cpu().numpy()
+    ref = ggml.ggml_matmul(x, W, type_name, K, N)
+    assert _rel(got, ref) < 1e-5
+    assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))

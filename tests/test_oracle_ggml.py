@@ -111,3 +111,230 @@ def test_matmul_brute_force(type_name, K, N):
     Wd = (scalar_q8_0 if type_name == "Q8_0" else scalar_q6k)(W.tobytes(), N * K).reshape(N, K)
     ref = x.astype(np.float64) @ Wd.astype(np.float64).T
     assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+# ---- the other block types: scalar restatements of llama.cpp's dequantize_row_* loops --------
+
+KV = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]  # kvalues_iq4nl
+F = np.float32
+
+
+def _u16(b, o):
+    return int(b[o]) | (int(b[o + 1]) << 8)
+
+
+def _u32(b, o):
+    return _u16(b, o) | (_u16(b, o + 2) << 16)
+
+
+def scalar_q4_0(raw, n):
+    """y[j] = (qs[j] & 0xF) - 8, y[j + 16] = (qs[j] >> 4) - 8, each times d."""
+    out = np.zeros(n, F)
+    for i in range(n // 32):
+        b = raw[18 * i:18 * i + 18]
+        d = F(_half(b, 0))
+        for j in range(16):
+            out[32 * i + j] = F((b[2 + j] & 0xF) - 8) * d
+            out[32 * i + j + 16] = F((b[2 + j] >> 4) - 8) * d
+    return out
+
+
+def scalar_q4_1(raw, n):
+    out = np.zeros(n, F)
+    for i in range(n // 32):
+        b = raw[20 * i:20 * i + 20]
+        d, m = F(_half(b, 0)), F(_half(b, 2))
+        for j in range(16):
+            out[32 * i + j] = F(b[4 + j] & 0xF) * d + m
+            out[32 * i + j + 16] = F(b[4 + j] >> 4) * d + m
+    return out
+
+
+def scalar_q5(raw, n, with_min):
+    """q5_0 / q5_1: xh_0 = ((qh >> j) << 4) & 0x10, xh_1 = (qh >> (j + 12)) & 0x10."""
+    sz = 24 if with_min else 22
+    out = np.zeros(n, F)
+    for i in range(n // 32):
+        b = raw[sz * i:sz * i + sz]
+        d = F(_half(b, 0))
+        m = F(_half(b, 2)) if with_min else None
+        o = 4 if with_min else 2
+        qh = _u32(b, o)
+        for j in range(16):
+            xh0 = ((qh >> j) << 4) & 0x10
+            xh1 = (qh >> (j + 12)) & 0x10
+            x0 = (b[o + 4 + j] & 0x0F) | xh0
+            x1 = (b[o + 4 + j] >> 4) | xh1
+            if with_min:
+                out[32 * i + j] = F(x0) * d + m
+                out[32 * i + j + 16] = F(x1) * d + m
+            else:
+                out[32 * i + j] = F(x0 - 16) * d
+                out[32 * i + j + 16] = F(x1 - 16) * d
+    return out
+
+
+def scalar_iq4_nl(raw, n):
+    out = np.zeros(n, F)
+    for i in range(n // 32):
+        b = raw[18 * i:18 * i + 18]
+        d = F(_half(b, 0))
+        for j in range(16):
+            out[32 * i + j] = d * F(KV[b[2 + j] & 0xF])
+            out[32 * i + j + 16] = d * F(KV[b[2 + j] >> 4])
+    return out
+
+
+def scalar_iq4_xs(raw, n):
+    out = np.zeros(n, F)
+    for i in range(n // 256):
+        b = raw[136 * i:136 * i + 136]
+        d = F(_half(b, 0))
+        sh = _u16(b, 2)
+        y = 256 * i
+        for ib in range(8):
+            ls = ((b[4 + ib // 2] >> (4 * (ib % 2))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4)
+            dl = d * F(ls - 32)
+            q = 8 + 16 * ib
+            for j in range(16):
+                out[y + j] = dl * F(KV[b[q + j] & 0xF])
+                out[y + j + 16] = dl * F(KV[b[q + j] >> 4])
+            y += 32
+    return out
+
+
+def get_scale_min_k4(j, q):
+    if j < 4:
+        return q[j] & 63, q[j + 4] & 63
+    return (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4), (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
+
+
+def scalar_q5k(raw, n):
+    out = np.zeros(n, F)
+    for i in range(n // 256):
+        b = raw[176 * i:176 * i + 176]
+        d, mn = F(_half(b, 0)), F(_half(b, 2))
+        sc = b[4:16]
+        y, ql, is_, u1, u2 = 256 * i, 48, 0, 1, 2
+        for _ in range(4):
+            s1, m1 = get_scale_min_k4(is_, sc)
+            s2, m2 = get_scale_min_k4(is_ + 1, sc)
+            d1, mm1, d2, mm2 = d * F(s1), mn * F(m1), d * F(s2), mn * F(m2)
+            for l in range(32):
+                out[y + l] = d1 * F((b[ql + l] & 0xF) + (16 if b[16 + l] & u1 else 0)) - mm1
+            for l in range(32):
+                out[y + 32 + l] = d2 * F((b[ql + l] >> 4) + (16 if b[16 + l] & u2 else 0)) - mm2
+            y += 64
+            ql += 32
+            is_ += 2
+            u1 <<= 2
+            u2 <<= 2
+    return out
+
+
+def scalar_q2k(raw, n):
+    out = np.zeros(n, F)
+    for i in range(n // 256):
+        b = raw[84 * i:84 * i + 84]
+        d, mn = F(_half(b, 80)), F(_half(b, 82))
+        y, q, is_ = 256 * i, 16, 0
+        for _ in range(2):
+            shift = 0
+            for _ in range(4):
+                for half in range(2):
+                    sc = b[is_]
+                    is_ += 1
+                    dl, ml = d * F(sc & 0xF), mn * F(sc >> 4)
+                    for l in range(16):
+                        out[y] = dl * F((b[q + 16 * half + l] >> shift) & 3) - ml
+                        y += 1
+                shift += 2
+            q += 32
+    return out
+
+
+def scalar_q3k(raw, n):
+    """With the scales unpacked the way llama.cpp does it: the 12 bytes as three 32-bit words,
+    rebuilt into four words of 6-bit values by the kmask1 / kmask2 shifts."""
+    k1, k2 = 0x03030303, 0x0F0F0F0F
+    out = np.zeros(n, F)
+    for i in range(n // 256):
+        b = raw[110 * i:110 * i + 110]
+        d = F(_half(b, 108))
+        a = [_u32(b, 96), _u32(b, 100), _u32(b, 104)]
+        tmp = a[2]
+        aux = [(a[0] & k2) | (((tmp >> 0) & k1) << 4), (a[1] & k2) | (((tmp >> 2) & k1) << 4),
+               ((a[0] >> 4) & k2) | (((tmp >> 4) & k1) << 4), ((a[1] >> 4) & k2) | (((tmp >> 6) & k1) << 4)]
+        scales = [((aux[k // 4] >> (8 * (k % 4))) & 0xFF) for k in range(16)]
+        scales = [s - 256 if s >= 128 else s for s in scales]
+        y, q, m, is_ = 256 * i, 32, 1, 0
+        for _ in range(2):
+            shift = 0
+            for _ in range(4):
+                for half in range(2):
+                    dl = d * F(scales[is_] - 32)
+                    is_ += 1
+                    for l in range(16):
+                        v = ((b[q + 16 * half + l] >> shift) & 3) - (0 if b[16 * half + l] & m else 4)
+                        out[y] = dl * F(v)
+                        y += 1
+                shift += 2
+                m <<= 1
+            q += 32
+    return out
+
+
+SCALAR = {"Q4_0": scalar_q4_0, "Q4_1": scalar_q4_1, "Q5_0": lambda r, n: scalar_q5(r, n, False),
+          "Q5_1": lambda r, n: scalar_q5(r, n, True), "IQ4_NL": scalar_iq4_nl, "IQ4_XS": scalar_iq4_xs,
+          "Q5_K": scalar_q5k, "Q2_K": scalar_q2k, "Q3_K": scalar_q3k}
+
+
+def _random_blocks(type_name, nblocks, seed):
+    """Random bytes with finite fp16 fields (exponent kept below Inf/NaN)."""
+    vals, nbytes = ggml.DEQUANT[type_name][1:]
+    b = np.random.default_rng(seed).integers(0, 256, (nblocks, nbytes), dtype=np.uint8)
+    for off in ggml.F16_FIELDS[type_name]:
+        b[:, off + 1] &= 0x3B
+    return b
+
+
+@pytest.mark.parametrize("type_name", sorted(SCALAR))
+@pytest.mark.parametrize("seed", [0, 1])
+def test_block_types_match_published_loops(type_name, seed):
+    vals = ggml.DEQUANT[type_name][1]
+    raw = _random_blocks(type_name, 3, seed).reshape(-1)
+    got = ggml.DEQUANT[type_name][0](raw.tobytes(), 3 * vals)
+    want = SCALAR[type_name](raw.tobytes(), 3 * vals)  # bytes index to Python ints (no uint8 wrap)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_name", sorted(SCALAR))
+def test_block_types_special_cases(type_name):
+    """Zero fp16 fields give zeros; one changed code byte moves only the weights it feeds."""
+    vals, nbytes = ggml.DEQUANT[type_name][1:]
+    f = ggml.DEQUANT[type_name][0]
+    b = _random_blocks(type_name, 2, 7)
+    z = b.copy()
+    for off in ggml.F16_FIELDS[type_name]:
+        z[:, off:off + 2] = 0
+    assert not np.any(f(z.reshape(-1).tobytes(), 2 * vals))
+    base = f(b.reshape(-1).tobytes(), 2 * vals)
+    c = b.copy()
+    qoff = ggml.CODE_BYTES[type_name]
+    c[1, qoff] ^= 0xFF
+    moved = np.nonzero(f(c.reshape(-1).tobytes(), 2 * vals) != base)[0]
+    assert moved.size and moved.min() >= vals and moved.size <= 8  # only block 1, one byte's weights
+
+
+def test_q4_1_and_iq4_unit_scale_values():
+    """d = 1 and m = 0 give the raw codes (Q4_1) or the codebook (IQ4_NL)."""
+    one = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    b = np.zeros(20, np.uint8)
+    b[0:2] = one
+    b[4:20] = np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4)
+    got = ggml.q4_1_dequant(b.tobytes(), 32)
+    assert np.array_equal(got, np.concatenate([np.arange(16), np.arange(16)[::-1]]).astype(F))
+    b = np.zeros(18, np.uint8)
+    b[0:2] = one
+    b[2:18] = np.arange(16, dtype=np.uint8)
+    assert np.array_equal(ggml.iq4_nl_dequant(b.tobytes(), 32)[:16], np.array(KV, F))

@@ -276,7 +276,8 @@ _SCALAR = {GGUF_U8: "<B", GGUF_I8: "<b", GGUF_U16: "<H", GGUF_I16: "<h", GGUF_U3
 GGML_TYPES = {0: ("F32", 1, 4), 1: ("F16", 1, 2), 2: ("Q4_0", 32, 18), 3: ("Q4_1", 32, 20),
               6: ("Q5_0", 32, 22), 7: ("Q5_1", 32, 24), 8: ("Q8_0", 32, 34), 10: ("Q2_K", 256, 84),
               11: ("Q3_K", 256, 110), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176),
-              14: ("Q6_K", 256, 210), 30: ("BF16", 1, 2)}
+              14: ("Q6_K", 256, 210), 20: ("IQ4_NL", 32, 18), 23: ("IQ4_XS", 256, 136),
+              30: ("BF16", 1, 2)}
 GGML_NAMES = {k: v[0] for k, v in GGML_TYPES.items()}
 GGML_IDS = {v[0]: k for k, v in GGML_TYPES.items()}
 

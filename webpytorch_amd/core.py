@@ -373,13 +373,17 @@ class QuantizedLinear:
 
 # ---- GGUF native ---------------------------------------------------------------------
 # (values per block, bytes per block, ggml type id) of the types a native kernel decodes
-_NATIVE_TYPES = {"Q4_K": (256, 144, 12), "Q6_K": (256, 210, 14), "Q8_0": (32, 34, 8)}
+_NATIVE_TYPES = {"Q4_K": (256, 144, 12), "Q6_K": (256, 210, 14), "Q8_0": (32, 34, 8),
+                 "Q4_0": (32, 18, 2), "Q4_1": (32, 20, 3), "Q5_0": (32, 22, 6), "Q5_1": (32, 24, 7),
+                 "IQ4_NL": (32, 18, 20), "IQ4_XS": (256, 136, 23), "Q5_K": (256, 176, 13),
+                 "Q2_K": (256, 84, 10), "Q3_K": (256, 110, 11)}
 
 
 def ggml_native_supported(type_name):
     """Can this ggml type be multiplied straight from the file's bytes
-    (`webtorch/_core.py:3644-3646`)? Q4_K, Q6_K and Q8_0 are (the types of a Q4_K_M file);
-    the other ggml types are not built."""
+    (`webtorch/_core.py:3644-3646`)? The llama.cpp block types Q4_0, Q4_1, Q5_0, Q5_1, Q8_0,
+    IQ4_NL, IQ4_XS, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K are; the reference's codebook-grid
+    i-quants (IQ1/IQ2/IQ3), ternary (TQ) and fp4 (MXFP4/NVFP4) types are not built here."""
     return type_name in _NATIVE_TYPES
 
 
@@ -437,17 +441,13 @@ def _ggml_selfcheck(type_name, mode):
     """Multiply two random blocks of `type_name` with the kernel of `mode` (rows 1, 2, or 0 for
     3 and more) and compare against the device's exact dequant of the same bytes times x in
     float64; RuntimeError on a mismatch (`_ggml_selfcheck`, `webtorch/_core.py:3684-3717`).
-    Random bytes are legal blocks of every type; draws whose fp16 fields decode to Inf/NaN or
-    huge values are skipped, as the reference does."""
-    vals, blk, _ = _NATIVE_TYPES[type_name]
-    for seed in range(32):
-        g = np.random.default_rng(seed)
-        raw = torch.from_numpy(g.integers(0, 256, (2, blk), dtype=np.uint8)).to(device())
-        W = ggml_dequant(raw.reshape(-1), type_name, 2).reshape(2, vals)
-        if bool(torch.isfinite(W).all()) and float(W.abs().max()) < 1e4:
-            break
-    else:
-        raise RuntimeError("could not draw a finite %s block to self-check against" % type_name)
+    Code and sub-scale bytes are uniform random (every byte pattern is a legal block); the fp16
+    scale fields are drawn small and finite, where the reference redraws until they are."""
+    from . import synth
+    vals = _NATIVE_TYPES[type_name][0]
+    raw = torch.from_numpy(synth.ggml_layer(type_name, 0, vals, 2, scale=0.01)).to(device())
+    W = ggml_dequant(raw.reshape(-1), type_name, 2).reshape(2, vals)
+    g = np.random.default_rng(vals)
     M = mode if mode else 3
     x = torch.from_numpy(g.standard_normal((M, vals)).astype(np.float32)).to(device())
     got = ggml_matmul(x, raw, type_name, vals, 2, _check=False)

@@ -1,5 +1,7 @@
-// GGUF Q8_0 and Q6_K: decode GEMV over the native blocks (gfx950), the types a Q4_K_M file
-// mixes in beside Q4_K.
+// The GGUF block types beside Q4_K: decode GEMV and fp32 dequant over the blocks as the file
+// stores them (gfx950). Q8_0 and Q6_K (the rest of a Q4_K_M file) are laid out below; Q4_0,
+// Q4_1, Q5_0, Q5_1, IQ4_NL (32-value blocks), IQ4_XS, Q5_K, Q2_K and Q3_K (256-value
+// super-blocks) follow llama.cpp's published block layouts, each given beside its decoder.
 //
 // Q8_0 block (32 weights, 34 bytes): fp16 d at 0, 32 int8 codes at 2; weight i = d * q[i].
 // Q6_K super-block (256 weights, 210 bytes): ql[128] at 0 (low 4 bits), qh[64] at 128 (high 2
@@ -28,15 +30,23 @@
 namespace miq {
 namespace gg {
 
-constexpr int kQ8_0 = 8, kQ6_K = 14;  // ggml type ids
+// ggml type ids
+constexpr int kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ5_K = 13, kQ6_K = 14,
+              kIQ4_NL = 20, kIQ4_XS = 23;
 
+// Values and bytes per block; lanes per block and values per lane of the GEMV.
 template <int T> struct Blk;
-template <> struct Blk<kQ8_0> {
-  static constexpr int VALS = 32, BYTES = 34, LPB = 4, VPL = 8;
-};
-template <> struct Blk<kQ6_K> {
-  static constexpr int VALS = 256, BYTES = 210, LPB = 16, VPL = 16;
-};
+template <> struct Blk<kQ8_0> { static constexpr int VALS = 32, BYTES = 34, LPB = 4, VPL = 8; };
+template <> struct Blk<kQ6_K> { static constexpr int VALS = 256, BYTES = 210, LPB = 16, VPL = 16; };
+template <> struct Blk<kQ4_0> { static constexpr int VALS = 32, BYTES = 18, LPB = 4, VPL = 8; };
+template <> struct Blk<kQ4_1> { static constexpr int VALS = 32, BYTES = 20, LPB = 4, VPL = 8; };
+template <> struct Blk<kQ5_0> { static constexpr int VALS = 32, BYTES = 22, LPB = 4, VPL = 8; };
+template <> struct Blk<kQ5_1> { static constexpr int VALS = 32, BYTES = 24, LPB = 4, VPL = 8; };
+template <> struct Blk<kIQ4_NL> { static constexpr int VALS = 32, BYTES = 18, LPB = 4, VPL = 8; };
+template <> struct Blk<kIQ4_XS> { static constexpr int VALS = 256, BYTES = 136, LPB = 16, VPL = 16; };
+template <> struct Blk<kQ5_K> { static constexpr int VALS = 256, BYTES = 176, LPB = 16, VPL = 16; };
+template <> struct Blk<kQ2_K> { static constexpr int VALS = 256, BYTES = 84, LPB = 16, VPL = 16; };
+template <> struct Blk<kQ3_K> { static constexpr int VALS = 256, BYTES = 110, LPB = 16, VPL = 16; };
 
 __device__ __forceinline__ uint32_t ld32(const uint8_t* w, size_t a) {
   return *reinterpret_cast<const uint32_t*>(w + a);  // a % 4 == 0
@@ -55,10 +65,34 @@ __device__ __forceinline__ float dot4u(uint32_t c, const float* x, float p) {
   return fmaf(x[3], (float)(c >> 24), p);
 }
 
-// Position of lane t's first weight within its block.
+// Position of lane t's first weight within its block. 32-value types: lane t takes the low
+// (t < 2) or high nibbles of 8 code bytes, i.e. values 16 (t >> 1) + 8 (t & 1) .. + 7. Q2_K /
+// Q3_K (and Q6_K): lane t = (h, j, u) takes the 16 values 128 h + 32 j + 16 u.. of one scale.
+// Q5_K: lane t = (g, hi, part) takes values 64 g + 32 hi + 16 part... IQ4_XS: lane t = (ib, hi)
+// takes values 32 ib + 16 hi...
 template <int T> __device__ __forceinline__ int lane_k(int t) {
   if constexpr (T == kQ8_0) return 8 * t;
+  else if constexpr (Blk<T>::VALS == 32) return 16 * (t >> 1) + 8 * (t & 1);
+  else if constexpr (T == kQ5_K) return 64 * (t >> 2) + 32 * ((t >> 1) & 1) + 16 * (t & 1);
+  else if constexpr (T == kIQ4_XS) return 32 * (t >> 1) + 16 * (t & 1);
   else return 128 * (t >> 3) + 32 * ((t >> 1) & 3) + 16 * (t & 1);
+}
+
+// Four bytes at a 2-byte-aligned address (two 2-byte loads: no read leaves the block).
+__device__ __forceinline__ uint32_t u32_at2(const uint8_t* w, size_t a) { return ld16(w, a) | (ld16(w, a + 2) << 16); }
+// 4 codes of a 4-bit codebook (IQ4_NL / IQ4_XS) as unsigned bytes kv + 128, from 4 nibble bytes
+// (0..15) in c: two byte selects over the 16-entry table and a pick by bit 3.
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t c) {
+  const uint32_t sel = c & 0x07070707u;
+  const uint32_t a = __builtin_amdgcn_perm(0x766A5D4Fu, 0x3F2D1801u, sel);  // kv[0..7] + 128
+  const uint32_t b = __builtin_amdgcn_perm(0xF1D9C5B5u, 0xA6998D81u, sel);  // kv[8..15] + 128
+  const uint32_t m = ((c >> 3) & 0x01010101u) * 0xFFu;
+  return (a & ~m) | (b & m);
+}
+// bits [sh, sh + 4) of qbits as 16 in bytes 0..3 (a 5-bit code's fifth bit)
+__device__ __forceinline__ uint32_t fifth4(uint32_t qbits, int sh) {
+  const uint32_t b = qbits >> sh;
+  return (((b & 1u) | ((b & 2u) << 7) | ((b & 4u) << 14) | ((b & 8u) << 21))) << 4;
 }
 
 // Lane t's share of one block at byte offset bs: its partial of sum_k x[k] * w[k], given its
@@ -104,6 +138,124 @@ template <> __device__ __forceinline__ float lane_dot<kQ6_K>(const uint8_t* w, s
     p = dot4u(c, x + 4 * i, p);
   }
   return (d * (float)sc) * fmaf(-32.f, xs, p);
+}
+
+// The 32-value types. Q4_0 (18 bytes): fp16 d, 16 code bytes; d (q - 8). Q4_1 (20): fp16 d,
+// fp16 m, 16 code bytes; d q + m. Q5_0 (22): fp16 d, u32 fifth bits, 16 code bytes; d (q - 16).
+// Q5_1 (24): fp16 d, fp16 m, u32 fifth bits, 16 code bytes; d q + m. IQ4_NL (18): fp16 d, 16 code
+// bytes; d kv[q] over the 16-entry codebook. Value j < 16 is the low nibble of code byte j and
+// value 16 + j the high one; a 5-bit code takes bit j (or j + 16) of the fifth-bit word.
+// Lane t's 8 code bytes (nibble t >> 1) dotted with x.
+template <int T> __device__ __forceinline__ float lane_dot32(const uint8_t* w, size_t bs, int t, const float* x,
+                                                            float xs) {
+  constexpr int QS = T == kQ4_0 || T == kIQ4_NL ? 2 : T == kQ4_1 ? 4 : T == kQ5_0 ? 6 : 8;
+  const int j0 = 8 * (t & 1), hi = t >> 1;
+  const uint32_t c0 = (u32_at2(w, bs + QS + j0) >> (4 * hi)) & 0x0F0F0F0Fu;
+  const uint32_t c1 = (u32_at2(w, bs + QS + j0 + 4) >> (4 * hi)) & 0x0F0F0F0Fu;
+  const float d = f16_at(w, bs);
+  if constexpr (T == kIQ4_NL) {
+    const float p = dot4u(iq4_lookup(c1), x + 4, dot4u(iq4_lookup(c0), x, 0.f));  // sum x (kv + 128)
+    return d * fmaf(-128.f, xs, p);
+  } else if constexpr (T == kQ4_0 || T == kQ4_1) {
+    const float p = dot4u(c1, x + 4, dot4u(c0, x, 0.f));
+    if constexpr (T == kQ4_0) return d * fmaf(-8.f, xs, p);
+    else return fmaf(d, p, f16_at(w, bs + 2) * xs);
+  } else {  // Q5_0 / Q5_1: the fifth bit of value j (of 16) in nibble half hi is bit j + 16 hi of qh
+    const uint32_t qh = u32_at2(w, bs + (T == kQ5_0 ? 2 : 4));
+    const int sh = j0 + 16 * hi;
+    const float p = dot4u(c1 | fifth4(qh, sh + 4), x + 4, dot4u(c0 | fifth4(qh, sh), x, 0.f));
+    if constexpr (T == kQ5_0) return d * fmaf(-16.f, xs, p);
+    else return fmaf(d, p, f16_at(w, bs + 2) * xs);
+  }
+}
+template <> __device__ __forceinline__ float lane_dot<kQ4_0>(const uint8_t* w, size_t bs, int t, const float* x, float xs) { return lane_dot32<kQ4_0>(w, bs, t, x, xs); }
+template <> __device__ __forceinline__ float lane_dot<kQ4_1>(const uint8_t* w, size_t bs, int t, const float* x, float xs) { return lane_dot32<kQ4_1>(w, bs, t, x, xs); }
+template <> __device__ __forceinline__ float lane_dot<kQ5_0>(const uint8_t* w, size_t bs, int t, const float* x, float xs) { return lane_dot32<kQ5_0>(w, bs, t, x, xs); }
+template <> __device__ __forceinline__ float lane_dot<kQ5_1>(const uint8_t* w, size_t bs, int t, const float* x, float xs) { return lane_dot32<kQ5_1>(w, bs, t, x, xs); }
+template <> __device__ __forceinline__ float lane_dot<kIQ4_NL>(const uint8_t* w, size_t bs, int t, const float* x, float xs) { return lane_dot32<kIQ4_NL>(w, bs, t, x, xs); }
+
+// 16 code bytes at a 2-byte-aligned address, as four words.
+__device__ __forceinline__ void load16(const uint8_t* w, size_t a, uint32_t* c) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = u32_at2(w, a + 4 * i);
+}
+
+// IQ4_XS (256 values, 136 bytes): fp16 d, u16 high scale bits, 4 bytes of low scale nibbles,
+// 128 code bytes; sub-block ib (32 values, codes as IQ4_NL in bytes 8 + 16 ib..) has
+// ls = nibble ib of the low bytes | bits 2 ib, 2 ib + 1 of the u16 << 4 and value d (ls - 32) kv[q].
+template <> __device__ __forceinline__ float lane_dot<kIQ4_XS>(const uint8_t* w, size_t bs, int t, const float* x,
+                                                               float xs) {
+  const int ib = t >> 1, hi = t & 1;
+  uint32_t c[4];
+  load16(w, bs + 8 + 16 * ib, c);
+  float p = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p = dot4u(iq4_lookup((c[i] >> (4 * hi)) & 0x0F0F0F0Fu), x + 4 * i, p);
+  const int ls = ((w[bs + 4 + ib / 2] >> (4 * (ib & 1))) & 15) | (((int)(ld16(w, bs + 2) >> (2 * ib)) & 3) << 4);
+  return (f16_at(w, bs) * (float)(ls - 32)) * fmaf(-128.f, xs, p);
+}
+
+// The Q4_K / Q5_K 6-bit scale and min of sub-block j from the 12 packed bytes at a.
+__device__ __forceinline__ void scale_min_k4(const uint8_t* w, size_t a, int j, int* sc, int* mn) {
+  if (j < 4) {
+    *sc = w[a + j] & 63;
+    *mn = w[a + j + 4] & 63;
+  } else {
+    *sc = (w[a + j + 4] & 15) | ((w[a + j - 4] >> 6) << 4);
+    *mn = (w[a + j + 4] >> 4) | ((w[a + j] >> 6) << 4);
+  }
+}
+
+// Q5_K (256 values, 176 bytes): fp16 d, fp16 dmin, 12 bytes of 6-bit scales/mins, qh[32],
+// qs[128]. Sub-block 2g + hi (32 values) takes nibble hi of qs[32 g + l] plus 16 times bit
+// 2g + hi of qh[l]; value (d sc) q - dmin m.
+template <> __device__ __forceinline__ float lane_dot<kQ5_K>(const uint8_t* w, size_t bs, int t, const float* x,
+                                                             float xs) {
+  const int g = t >> 2, hi = (t >> 1) & 1, part = t & 1, sb = 2 * g + hi;
+  uint32_t c[4], h[4];
+  load16(w, bs + 48 + 32 * g + 16 * part, c);
+  load16(w, bs + 16 + 16 * part, h);
+  float p = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    p = dot4u(((c[i] >> (4 * hi)) & 0x0F0F0F0Fu) | (((h[i] >> sb) & 0x01010101u) << 4), x + 4 * i, p);
+  int sc, mn;
+  scale_min_k4(w, bs + 4, sb, &sc, &mn);
+  return (f16_at(w, bs) * (float)sc) * p - (f16_at(w, bs + 2) * (float)mn) * xs;
+}
+
+// Q2_K (256 values, 84 bytes): 16 scale bytes (low nibble scale, high nibble min), qs[64],
+// fp16 d, fp16 dmin. Value 128 h + 32 j + 16 u + l is bits 2j, 2j + 1 of qs[32 h + 16 u + l]
+// with scale byte 8 h + 2 j + u; value (d sc) q - dmin m.
+template <> __device__ __forceinline__ float lane_dot<kQ2_K>(const uint8_t* w, size_t bs, int t, const float* x,
+                                                             float xs) {
+  const int h = t >> 3, j = (t >> 1) & 3, u = t & 1;
+  uint32_t c[4];
+  load16(w, bs + 16 + 32 * h + 16 * u, c);
+  float p = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p = dot4u((c[i] >> (2 * j)) & 0x03030303u, x + 4 * i, p);
+  const int sc = w[bs + 8 * h + 2 * j + u];
+  return (f16_at(w, bs + 80) * (float)(sc & 15)) * p - (f16_at(w, bs + 82) * (float)(sc >> 4)) * xs;
+}
+
+// Q3_K (256 values, 110 bytes): hmask[32], qs[64], 12 bytes of 6-bit scales, fp16 d. Value
+// 128 h + 32 j + 16 u + l is bits 2j of qs[32 + 32 h + 16 u + l], minus 4 unless bit 4 h + j of
+// hmask[16 u + l] is set; scale i = 8 h + 2 j + u has nibble i / 8 of byte i % 8 and bit pair
+// i / 4 of byte 8 + i % 4 as its high bits, minus 32; value d scale q.
+template <> __device__ __forceinline__ float lane_dot<kQ3_K>(const uint8_t* w, size_t bs, int t, const float* x,
+                                                             float xs) {
+  const int h = t >> 3, j = (t >> 1) & 3, u = t & 1, is = 8 * h + 2 * j + u;
+  uint32_t c[4], m[4];
+  load16(w, bs + 32 + 32 * h + 16 * u, c);
+  load16(w, bs + 16 * u, m);
+  float p = 0.f;  // sum x (v + 4), v + 4 = 2-bit code + 4 * (hmask bit)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    p = dot4u(((c[i] >> (2 * j)) & 0x03030303u) | (((m[i] >> (4 * h + j)) & 0x01010101u) << 2), x + 4 * i, p);
+  const int sc = (((int)w[bs + 96 + (is & 7)] >> (4 * (is >> 3))) & 15) |
+                 ((((int)w[bs + 104 + (is & 3)] >> (2 * (is >> 2))) & 3) << 4);
+  return (f16_at(w, bs + 108) * (float)(sc - 32)) * fmaf(-4.f, xs, p);
 }
 
 // y[m][n] = sum_k x[m][k] * W[n][k] (+ bias[n]); grid (workgroups, M), 256 threads.
@@ -208,26 +360,77 @@ static int types(const void* x, int xd, const uint8_t* w, const float* bias, voi
   return launch<T, float, float>(x, w, bias, out, M, K, N, st);
 }
 
-// Full fp32 dequant of n_blocks blocks, one thread per weight. Every product is exact in fp32
-// (fp16 d x int8 code; fp16 d x int8 scale x 6-bit code), so the order of the factors does
-// not change a bit.
+// Value j of the block at bs. Every value is an exact product (fp16 scale, small integer
+// sub-scale and code fit float32's 24 bits) or such a product plus/minus another exact one, so
+// its one rounding matches the reference's numpy whatever the order of the factors.
+__device__ __constant__ float kIQ4[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                                         1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+template <int T> __device__ __forceinline__ float value_at(const uint8_t* w, size_t bs, int j) {
+  if constexpr (T == kQ8_0) {
+    return f16_at(w, bs) * (float)(int8_t)w[bs + 2 + j];
+  } else if constexpr (T == kQ6_K) {
+    const int h = j >> 7, r = j & 127, q = r >> 5, l = r & 31;
+    const uint32_t lo = w[bs + 64 * h + l + 32 * (q & 1)];
+    const uint32_t nib = (q >> 1) ? (lo >> 4) : (lo & 15u);
+    const uint32_t c = nib | (((uint32_t)(w[bs + 128 + 32 * h + l] >> (2 * q)) & 3u) << 4);
+    const float sc = (float)(int8_t)w[bs + 192 + 8 * h + (l >> 4) + 2 * q];
+    return (f16_at(w, bs + 208) * sc) * (float)((int)c - 32);
+  } else if constexpr (Blk<T>::VALS == 32) {  // value j: nibble j >> 4 of code byte j & 15
+    constexpr int QS = T == kQ4_0 || T == kIQ4_NL ? 2 : T == kQ4_1 ? 4 : T == kQ5_0 ? 6 : 8;
+    int q = (w[bs + QS + (j & 15)] >> (4 * (j >> 4))) & 15;
+    if constexpr (T == kQ5_0 || T == kQ5_1) q |= (int)((u32_at2(w, bs + QS - 4) >> j) & 1u) << 4;
+    const float d = f16_at(w, bs);
+    if constexpr (T == kQ4_0) return d * (float)(q - 8);
+    else if constexpr (T == kQ5_0) return d * (float)(q - 16);
+    else if constexpr (T == kIQ4_NL) return d * kIQ4[q];
+    else return d * (float)q + f16_at(w, bs + 2);  // Q4_1, Q5_1: d * q + m
+  } else if constexpr (T == kIQ4_XS) {
+    const int ib = j >> 5, q = (w[bs + 8 + 16 * ib + (j & 15)] >> (4 * ((j >> 4) & 1))) & 15;
+    const int ls = ((w[bs + 4 + ib / 2] >> (4 * (ib & 1))) & 15) | (((int)(ld16(w, bs + 2) >> (2 * ib)) & 3) << 4);
+    return (f16_at(w, bs) * (float)(ls - 32)) * kIQ4[q];
+  } else if constexpr (T == kQ5_K) {
+    const int sb = j >> 5, l = j & 31;
+    const int q = ((w[bs + 48 + 32 * (sb >> 1) + l] >> (4 * (sb & 1))) & 15) + 16 * ((w[bs + 16 + l] >> sb) & 1);
+    int sc, mn;
+    scale_min_k4(w, bs + 4, sb, &sc, &mn);
+    return (f16_at(w, bs) * (float)sc) * (float)q - f16_at(w, bs + 2) * (float)mn;
+  } else {  // Q2_K, Q3_K: value 128 h + 32 jj + 16 u + l
+    const int h = j >> 7, jj = (j >> 5) & 3, u = (j >> 4) & 1, l = j & 15, is = 8 * h + 2 * jj + u;
+    if constexpr (T == kQ2_K) {
+      const int q = (w[bs + 16 + 32 * h + 16 * u + l] >> (2 * jj)) & 3;
+      const int sc = w[bs + is];
+      return (f16_at(w, bs + 80) * (float)(sc & 15)) * (float)q - f16_at(w, bs + 82) * (float)(sc >> 4);
+    } else {
+      const int q = ((w[bs + 32 + 32 * h + 16 * u + l] >> (2 * jj)) & 3) - (((w[bs + 16 * u + l] >> (4 * h + jj)) & 1) ? 0 : 4);
+      const int sc = (((int)w[bs + 96 + (is & 7)] >> (4 * (is >> 3))) & 15) |
+                     ((((int)w[bs + 104 + (is & 3)] >> (2 * (is >> 2))) & 3) << 4);
+      return (f16_at(w, bs + 108) * (float)(sc - 32)) * (float)q;
+    }
+  }
+}
+
+// Full fp32 dequant of n_blocks blocks, one thread per weight.
 template <int T>
 __global__ __launch_bounds__(256) void ggml_dequant_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
                                                            int64_t nvals) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= nvals) return;
   const int64_t blk = i / Blk<T>::VALS;
-  const int j = (int)(i - blk * Blk<T>::VALS);
-  const size_t bs = (size_t)blk * Blk<T>::BYTES;
-  if constexpr (T == kQ8_0) {
-    out[i] = f16_at(w, bs) * (float)(int8_t)w[bs + 2 + j];
-  } else {
-    const int h = j >> 7, r = j & 127, q = r >> 5, l = r & 31;
-    const uint32_t lo = w[bs + 64 * h + l + 32 * (q & 1)];
-    const uint32_t nib = (q >> 1) ? (lo >> 4) : (lo & 15u);
-    const uint32_t c = nib | (((uint32_t)(w[bs + 128 + 32 * h + l] >> (2 * q)) & 3u) << 4);
-    const float sc = (float)(int8_t)w[bs + 192 + 8 * h + (l >> 4) + 2 * q];
-    out[i] = (f16_at(w, bs + 208) * sc) * (float)((int)c - 32);
+  out[i] = value_at<T>(w, (size_t)blk * Blk<T>::BYTES, (int)(i - blk * Blk<T>::VALS));
+}
+
+// Calls f(std::integral_constant<int, T>) for the native type id t; false if t is not one.
+template <typename F> static bool with_type(int t, F&& f) {
+  switch (t) {
+#define MIQ_GG_CASE(X) \
+  case X:              \
+    f(std::integral_constant<int, X>{}); \
+    return true;
+    MIQ_GG_CASE(kQ8_0) MIQ_GG_CASE(kQ6_K) MIQ_GG_CASE(kQ4_0) MIQ_GG_CASE(kQ4_1) MIQ_GG_CASE(kQ5_0)
+    MIQ_GG_CASE(kQ5_1) MIQ_GG_CASE(kIQ4_NL) MIQ_GG_CASE(kIQ4_XS) MIQ_GG_CASE(kQ5_K) MIQ_GG_CASE(kQ2_K)
+    MIQ_GG_CASE(kQ3_K)
+#undef MIQ_GG_CASE
+    default: return false;
   }
 }
 
@@ -239,26 +442,28 @@ using namespace miq;
 extern "C" int miq_ggml_dequant_f32(const uint8_t* blocks, int ggml_type, float* out, int64_t n_blocks,
                                     void* stream) {
   if (ggml_type == 12) return miq_q4k_dequant_f32(blocks, out, n_blocks, stream);
-  MIQ_REQUIRE(ggml_type == gg::kQ8_0 || ggml_type == gg::kQ6_K, MIQ_ERR_UNSUPPORTED,
-              "ggml_dequant: ggml type %d (Q4_K = 12, Q8_0 = 8 and Q6_K = 14 are decoded here)", ggml_type);
   MIQ_REQUIRE(n_blocks >= 0, MIQ_ERR_INVALID, "ggml_dequant: n_blocks=%lld", (long long)n_blocks);
+  int vals = 0;
+  const bool known = gg::with_type(ggml_type, [&](auto tag) { vals = gg::Blk<decltype(tag)::value>::VALS; });
+  MIQ_REQUIRE(known, MIQ_ERR_UNSUPPORTED, "ggml_dequant: ggml type %d has no native decoder", ggml_type);
   if (n_blocks == 0) return MIQ_OK;
   MIQ_REQUIRE(blocks && out, MIQ_ERR_INVALID, "ggml_dequant: null pointer");
   MIQ_REQUIRE(aligned(blocks, 2), MIQ_ERR_ALIGN, "ggml_dequant: blocks must be 2-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t vals = n_blocks * (ggml_type == gg::kQ8_0 ? 32 : 256);
-  const dim3 grid((unsigned)((vals + 255) / 256));
-  if (ggml_type == gg::kQ8_0) hipLaunchKernelGGL(gg::ggml_dequant_kernel<gg::kQ8_0>, grid, dim3(256), 0, st, blocks, out, vals);
-  else hipLaunchKernelGGL(gg::ggml_dequant_kernel<gg::kQ6_K>, grid, dim3(256), 0, st, blocks, out, vals);
+  const int64_t nv = n_blocks * vals;
+  gg::with_type(ggml_type, [&](auto tag) {
+    hipLaunchKernelGGL(gg::ggml_dequant_kernel<decltype(tag)::value>, dim3((unsigned)((nv + 255) / 256)), dim3(256),
+                       0, st, blocks, out, nv);
+  });
   return check_launch("ggml_dequant");
 }
 
 extern "C" int miq_ggml_gemv(const void* x, int x_dtype, const uint8_t* w, int ggml_type, const float* bias,
                              void* out, int out_dtype, int M, int K, int N, void* stream) {
-  MIQ_REQUIRE(ggml_type == gg::kQ8_0 || ggml_type == gg::kQ6_K, MIQ_ERR_UNSUPPORTED,
-              "ggml_gemv: ggml type %d (Q8_0 = 8 and Q6_K = 14 are decoded here, Q4_K by miq_q4k_gemv)",
+  int vals = 0;
+  const bool known = gg::with_type(ggml_type, [&](auto tag) { vals = gg::Blk<decltype(tag)::value>::VALS; });
+  MIQ_REQUIRE(known, MIQ_ERR_UNSUPPORTED, "ggml_gemv: ggml type %d has no kernel here (Q4_K: miq_q4k_gemv)",
               ggml_type);
-  const int vals = ggml_type == gg::kQ8_0 ? 32 : 256;
   MIQ_REQUIRE(M >= 0 && K > 0 && N > 0 && M <= 65535, MIQ_ERR_INVALID, "ggml_gemv: M=%d K=%d N=%d", M, K, N);
   MIQ_REQUIRE(K % vals == 0, MIQ_ERR_INVALID, "ggml_gemv: K=%d is not a multiple of %d", K, vals);
   if (M == 0) return MIQ_OK;
@@ -267,6 +472,9 @@ extern "C" int miq_ggml_gemv(const void* x, int x_dtype, const uint8_t* w, int g
   MIQ_REQUIRE(x_dtype == MIQ_F16 || x_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "ggml_gemv: x dtype");
   MIQ_REQUIRE(out_dtype == MIQ_F16 || out_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "ggml_gemv: out dtype");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (ggml_type == gg::kQ8_0) return gg::types<gg::kQ8_0>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
-  return gg::types<gg::kQ6_K>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
+  int rc = MIQ_OK;
+  gg::with_type(ggml_type, [&](auto tag) {
+    rc = gg::types<decltype(tag)::value>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
+  });
+  return rc;
 }

@@ -133,6 +133,28 @@ def q6k_layer(seed, K, N, name="q6k"):
     return b.reshape(N, (K // 256) * 210)
 
 
+# (values, bytes, byte offsets of the fp16 scale fields) of the GGUF block types
+GGML_BLOCKS = {"Q4_0": (32, 18, (0,)), "Q4_1": (32, 20, (0, 2)), "Q5_0": (32, 22, (0,)),
+               "Q5_1": (32, 24, (0, 2)), "Q8_0": (32, 34, (0,)), "IQ4_NL": (32, 18, (0,)),
+               "IQ4_XS": (256, 136, (0,)), "Q2_K": (256, 84, (80, 82)), "Q3_K": (256, 110, (108,)),
+               "Q4_K": (256, 144, (0, 2)), "Q5_K": (256, 176, (0, 2)), "Q6_K": (256, 210, (208,))}
+
+
+def ggml_layer(type_name, seed, K, N, scale=0.002):
+    """N rows of K / block-values blocks of a GGUF type: uniform code and sub-scale bytes, every
+    fp16 scale field |N(0,1)| * scale (finite, so the weight is too), as a uint8 (N, row bytes)
+    array."""
+    vals, nbytes, f16 = GGML_BLOCKS[type_name]
+    if K % vals:
+        raise ValueError("%s needs K %% %d == 0" % (type_name, vals))
+    g = rng(seed, "ggml-" + type_name)
+    nb = N * (K // vals)
+    b = g.integers(0, 256, (nb, nbytes), dtype=np.uint8)
+    for off in f16:
+        b[:, off:off + 2] = (np.abs(g.standard_normal(nb)) * scale).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(N, (K // vals) * nbytes)
+
+
 def activations(seed, M, K, dtype=np.float16, name="x"):
     return rng(seed, name).standard_normal((M, K)).astype(dtype)
 
