@@ -1,26 +1,41 @@
 // Persistent decode step for gfx950: one launch per token for a Qwen2-style int4 GPTQ decoder
 // (the captured one-token step of `webtorch/llm.py:1591-1616`), with no grid-wide barrier.
 //
-// Every workgroup (1024 threads, one per CU) has a role for all layers: a 64-column tile of
-// the q|k|v, o or gate|up projection, a query head of the attention, or a (64-column tile,
-// K-slice) of the down projection. Workgroups hand results to each other through small
-// exchange buffers of tagged 64-bit words -- (tag << 32) | fp32 bits -- written and read at
-// device scope (they bypass the per-XCD L2). A consumer polls the words it needs until every
-// one carries the tag of the current (token, layer, phase); a tag never repeats between
-// consecutive tokens, so no flag, counter or reset is needed. A role's weights for layer l are
-// issued as soon as its layer l-1 work is stored, a whole layer ahead of their use, so the
-// critical path per projection is one hop (store -> poll) plus its arithmetic; the HBM
-// traffic of the weights overlaps the chain of dependent steps.
+// Every workgroup (1024 threads, one per CU) has a role for all layers:
+//   * a 64-column tile of the q|k|v projection;
+//   * a query head: RoPE, attention over the cache, and the head's share of the o projection
+//     (its 64 rows of Wo, all H columns);
+//   * a 64-column chunk of hmid(l) = h(l) + the sum of the heads' o shares;
+//   * a 64-column tile of the gate|up projection;
+//   * a (64-column tile, K-slice) of the down projection.
+// A layer is five dependent hops: h(l) -> q|k|v -> heads -> hmid chunks -> gate|up -> down ->
+// h(l + 1).
 //
-// After the last layer every workgroup takes 64-column tiles of the tied head, keeps a
-// running arg-max, and publishes it; workgroup 0 combines the partials in workgroup order,
-// writes the token id, appends it to the history and advances the position, exactly as
-// argmax_kernel does.
+// Single-writer results (q|k|v, the heads' o shares, hmid, gate|up) are (tag << 32) | fp32 bits
+// words written and read at device scope (they bypass the per-XCD L2); a tag names (token,
+// layer, phase) and never repeats between consecutive tokens, so no reset is needed.
+// h(l + 1) = hmid(l) + the down projection's K-slices is summed in fixed point instead: each
+// K-slice, and the gate|up tiles for the residual hmid(l), add their term to a 64-bit word per
+// (layer, column) as round(p 2^24) + 2^46 with 1 in a count field, by one device-scope atomic,
+// and a consumer polls the words until the count is complete (one word per column instead of one
+// per K-slice and column). Integer sums do not depend on the order of arrival, so a step is
+// deterministic; a term the fixed point cannot hold (NaN, Inf, |p| >= 2^22) takes the exact
+// escape of mma_tile.h (an fp32 side slot read back in term order). The words of a token sit in
+// one of two banks (by the parity of the token's epoch); each step zeroes the other bank for the
+// next step, and the kernel boundary orders the two. (Terms that many workgroups add to the same
+// words serialize at the coherence point, so the heads' o reduction is a hop of its own.)
+// A role's weights for layer l are issued as soon as its layer l-1 work is done, a whole layer
+// ahead of their use, so the HBM traffic of the weights overlaps the chain of dependent steps.
+//
+// After the last layer every workgroup takes 64-column tiles of the tied head, keeps a running
+// arg-max, and publishes it; workgroup 0 combines the partials in workgroup order, writes the
+// token id, appends it to the history and advances the position, exactly as argmax_kernel does.
 //
 // Waits are bounded: a workgroup that is still waiting `spin_limit` wall-clock ticks after it
-// started sets an error bit and leaves, so every wait chain ends and the grid drains (the
-// host reads the bit). All workgroups must be resident at once; the host sizes the grid to
-// the CU count and checks occupancy, and the step must not share the GPU with other work.
+// started sets an error bit and leaves, so every wait chain ends and the grid drains (the host
+// reads the bit; a step that failed leaves its bank dirty, so the caller resets the workspace).
+// All workgroups must be resident at once; the host sizes the grid to the CU count and checks
+// occupancy, and the step must not share the GPU with other work.
 //
 // Control words at the start of the workspace (uint32): [0] epoch of the last token done,
 // [1] error bits (1: wait timed out, 2: position past the cache).
@@ -44,7 +59,7 @@ using namespace mt;
 
 constexpr int kThreads = 1024, kWaves = 16, kTile = 64, kMaxSPQ = 8, kSlots = 20;
 enum Slot { QKV_QW, QKV_QZ, QKV_SC, QKV_B, O_QW, O_QZ, O_SC, GU_QW, GU_QZ, GU_SC, D_QW, D_QZ, D_SC, IN_LN, POST_LN, KC, VC };
-enum Phase { P_QKV = 0, P_ATT = 1, P_HMID = 2, P_GU = 3, P_DOWN = 4, P_AMAX = 5 };
+enum Phase { P_QKV = 0, P_ATT = 1, P_HMID = 2, P_GU = 3, P_AMAX = 5 };
 
 struct Params {
   const uint64_t* layers;  // [L][kSlots] device addresses, indexed by Slot
@@ -60,10 +75,13 @@ struct Params {
   int32_t* state;
   float* logits;
   uint32_t* ctl;
-  uint64_t *tq, *tatt, *thmid, *tgu, *tdown, *tamax;
+  uint64_t *tq, *tpart, *thmid, *tgu, *tamax;  // q|k|v, heads' o shares [NH][H], hmid, gate|up, arg-max
+  unsigned long long* fx;  // bank 0 of the fixed-point words of h(l + 1) (bank 1 at fx + bank_words)
+  float* fside;            // escape slots: term s of word i at fside + s * LH + i
+  size_t bank_words;       // 64-bit words per bank: LH sums, then LH 32-bit masks
   int L, H, NH, NKV, I, V, LMAX, gs, lgs, hist_len, ksd;  // lgs = log2(gs)
-  int nq, na, no, ngu, nd;  // workgroups per role (nd = no * ksd)
-  int lds_a, lds_x;         // LDS regions (floats): exchange/staging, activations
+  int nq, na, no, ngu, nd;  // workgroups per role (nd = no * ksd, no = H / 64)
+  int lds_a, lds_x;      // LDS regions (floats): exchange/staging, activations
   float eps, scale, zoff, head_zoff;
   long long spin_limit;
 #ifdef MIQ_PD_TRACE
@@ -97,12 +115,60 @@ struct Ctx {
   __device__ uint32_t tag(int l, int ph) const { return ep * (uint32_t)(8 * (L + 1)) + 8u * (uint32_t)l + (uint32_t)ph; }
 };
 
+// Columns c0.. of h(l + 1) as fixed-point words of this token's bank, with their masks and
+// escape slots.
+struct Fx {
+  unsigned long long* w;
+  uint32_t* m;
+  float* side;
+  size_t stride;
+};
+__device__ __forceinline__ Fx fx_row(const Params& p, uint32_t ep, int l, int c0 = 0) {
+  const size_t n = (size_t)p.L * p.H, off = (size_t)l * p.H + c0;
+  unsigned long long* bank = p.fx + (ep & 1u) * p.bank_words;
+  return {bank + off, reinterpret_cast<uint32_t*>(bank + n) + off, p.fside + off, n};
+}
+// Term `term` adds v to column i (no return value is waited for).
+__device__ __forceinline__ void fx_put(const Fx& r, int i, float v, int term) {
+  const FixEsc e{r.m + i, r.side + i, r.stride};
+  (void)fix_issue(r.w + i, fix_word(v), v, e, term);
+}
+// The value of a complete word of `terms` terms (escaped terms added in term order).
+__device__ __forceinline__ float fx_value(unsigned long long w, int terms, const Fx& r, int i) {
+  const long long v = (long long)(w & ((1ull << kFixEscShift) - 1)) - (long long)terms * (long long)kFixBias;
+  float s = (float)v * (1.f / kFixScale);
+  if ((w >> kFixEscShift) & 63ull) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const uint32_t m = __hip_atomic_load(r.m + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int t = 0; t < terms; ++t)
+      if ((m >> t) & 1u) s += __hip_atomic_load(r.side + (size_t)t * r.stride + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return s;
+}
+
+// After a wave's polling: true (uniformly) unless a wave passed the deadline. late is
+// wave-uniform (a vote and the scalar clock decide it): one flag per wave and one barrier
+// (__syncthreads_or costs three). Every wait is followed by at least one more barrier before
+// the next wait writes the flags, so no wave rewrites a flag while another still reads it.
+__device__ __forceinline__ bool all_on_time(bool late, int* flags) {
+  if ((threadIdx.x & 63) == 0) flags[threadIdx.x >> 6] = late ? 1 : 0;
+  __syncthreads();
+  const int4* f = reinterpret_cast<const int4*>(flags);
+  int any = 0;
+#pragma unroll
+  for (int q = 0; q < kWaves / 4; ++q) {
+    const int4 t = f[q];
+    any |= t.x | t.y | t.z | t.w;
+  }
+  return any == 0;
+}
+
 // Polls n tagged words (word i at base + off(i)) until word i carries tagf(i), leaving their values
 // in dst[0..n) (LDS). Called by the whole workgroup with the same arguments; n <= NPL * 1024.
 // Each wave polls its own words until they are all current (no barrier per round), then the
 // workgroup meets once. Returns false (uniformly) once a wave has passed the deadline.
 template <int NPL, typename F, typename T>
-__device__ bool wait_tagged(int n, const Ctx& c, const uint64_t* base, F off, T tagf, float* dst) {
+__device__ bool wait_tagged(int n, const Ctx& c, const uint64_t* base, F off, T tagf, float* dst, int* flags) {
   const int tid = opaque_tid();
   bool late = false;
   for (;;) {
@@ -126,43 +192,40 @@ __device__ bool wait_tagged(int n, const Ctx& c, const uint64_t* base, F off, T 
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  // late is wave-uniform (a vote and the scalar clock decide it): one flag per wave and one
-  // barrier (__syncthreads_or costs three). The flags are per instantiation, i.e. per call site
-  // (each passes its own lambdas), and every call site passes another barrier before it waits
-  // again, so no wave rewrites a flag while another still reads it.
-  __shared__ __align__(16) int wt_late[kWaves];
-  if ((threadIdx.x & 63) == 0) wt_late[threadIdx.x >> 6] = late ? 1 : 0;
-  __syncthreads();
-  const int4* f = reinterpret_cast<const int4*>(wt_late);
-  int any = 0;
-#pragma unroll
-  for (int q = 0; q < kWaves / 4; ++q) {
-    const int4 t = f[q];
-    any |= t.x | t.y | t.z | t.w;
-  }
-  return any == 0;
+  return all_on_time(late, flags);
 }
 
-// Sum over the workgroup, combined in wave order (every thread gets the total).
-__device__ __forceinline__ float block_sum(float v, float* red16) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red16[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float t = 0.f;
+// Polls the n fixed-point words of row r until each holds `terms` terms, leaving their values in
+// dst[0..n) (LDS); n <= NPL * 1024. Same contract as wait_tagged.
+template <int NPL>
+__device__ bool wait_fixed(int n, const Ctx& c, const Fx& r, int terms, float* dst, int* flags) {
+  const int tid = opaque_tid();
+  bool late = false;
+  unsigned long long v[NPL];
+  for (;;) {
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) t += red16[w];
-  return t;
-}
-__device__ __forceinline__ float block_max(float v, float* red16) {
-  v = wave_max(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red16[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float t = red16[0];
+    for (int j = 0; j < NPL; ++j)
+      if (j * kThreads < n)
+        v[j] = __hip_atomic_load(r.w + min(tid + j * kThreads, n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool ok = true;
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) t = fmaxf(t, red16[w]);
-  return t;
+    for (int j = 0; j < NPL; ++j)
+      if (j * kThreads < n && tid + j * kThreads < n) ok &= (int)(v[j] >> kFixCountShift) == terms;
+    if (__all(ok)) break;
+    if (wall_clock64() > c.deadline) {
+      late = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (!late) {
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int i = tid + j * kThreads;
+      if (j * kThreads < n && i < n) dst[i] = fx_value(v[j], terms, r, i);
+    }
+  }
+  return all_on_time(late, flags);
 }
 
 // RMSNorm applied after the projection, which is linear: RMSNorm(h) @ W = ((h * w) @ W) / r with
@@ -192,18 +255,11 @@ __device__ __forceinline__ float norm_r(const float* red16, int H, float eps) {
   return sqrtf(t / (float)H + eps);
 }
 
-__device__ __forceinline__ float sumsq8(const float* v) {
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ss = ss + v[j] * v[j];
-  return ss;
-}
-
 // This thread's chunk (8 values) of an RMSNorm weight vector of H values, loaded ahead.
 __device__ __forceinline__ void norm_prefetch(float4* w, const float* nw, int H) {
   const int ch = min((int)threadIdx.x, H / 8 - 1);
-  w[0] = *reinterpret_cast<const float4*>(nw + ch * 8);
-  w[1] = *reinterpret_cast<const float4*>(nw + ch * 8 + 4);
+  w[0] = ldgf4(nw + ch * 8);
+  w[1] = ldgf4(nw + ch * 8 + 4);
   pin(w[0]);
   pin(w[1]);
 }
@@ -247,32 +303,73 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   i = bi;
 }
 
+// ---- a head's share of the o projection ---------------------------------------------------
+// Column n of Wo over the head's 64 rows: 8 packed words (rows 8i .. 8i + 7 in nibbles 0-7),
+// and the scale and zero point of the one or two quantization groups the rows span (two when
+// the group size is 32: rows 0-31 and 32-63), as raw fp16 bits and nibbles.
+struct OCol {
+  uint32_t q[8];
+  uint32_t s;  // fp16 scale of rows 0-31 | fp16 scale of rows 32-63 << 16
+  uint32_t z;  // zero nibble of rows 0-31 | zero nibble of rows 32-63 << 8
+};
+__device__ __forceinline__ void ocol_issue(OCol& o, const uint32_t* qw, const uint32_t* qz, const __half* sc, int hq,
+                                           int H, int n, int lgs) {
+  n = min(n, H - 1);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o.q[i] = ldg(qw + (uint32_t)((hq * 8 + i) * H + n));
+  const int g0 = (hq * 64) >> lgs, g1 = (hq * 64 + 32) >> lgs;
+  const unsigned short* s16 = reinterpret_cast<const unsigned short*>(sc);
+  o.s = (uint32_t)ldg(s16 + (uint32_t)(g0 * H + n)) | ((uint32_t)ldg(s16 + (uint32_t)(g1 * H + n)) << 16);
+  const int sh = 4 * (n & 7);
+  o.z = ((ldg(qz + (uint32_t)(g0 * (H >> 3) + (n >> 3))) >> sh) & 15u) |
+        (((ldg(qz + (uint32_t)(g1 * (H >> 3) + (n >> 3))) >> sh) & 15u) << 8);
+}
+// sum_k att[k] Wo[64 hq + k][n]: per half of the rows, scale * (sum att c - (z + zoff) sum att),
+// with the halves' attention sums at att[64], att[65].
+__device__ __forceinline__ float ocol_dot(const OCol& o, const float* att, float zoff) {
+  float a[2] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 x0 = *reinterpret_cast<const float4*>(att + 8 * i);
+    const float4 x1 = *reinterpret_cast<const float4*>(att + 8 * i + 4);
+    const uint32_t lo = o.q[i] & 0x0F0F0F0Fu, hi = (o.q[i] >> 4) & 0x0F0F0F0Fu;  // rows 0,2,4,6 / 1,3,5,7
+    float& r = a[i >> 2];
+    r = fmaf(x0.x, (float)(lo & 0xFFu), r);
+    r = fmaf(x0.y, (float)(hi & 0xFFu), r);
+    r = fmaf(x0.z, (float)((lo >> 8) & 0xFFu), r);
+    r = fmaf(x0.w, (float)((hi >> 8) & 0xFFu), r);
+    r = fmaf(x1.x, (float)((lo >> 16) & 0xFFu), r);
+    r = fmaf(x1.y, (float)((hi >> 16) & 0xFFu), r);
+    r = fmaf(x1.z, (float)(lo >> 24), r);
+    r = fmaf(x1.w, (float)(hi >> 24), r);
+  }
+  const float s0 = __half2float(__ushort_as_half((unsigned short)(o.s & 0xFFFFu)));
+  const float s1 = __half2float(__ushort_as_half((unsigned short)(o.s >> 16)));
+  const float z0 = (float)(o.z & 0xFFu) + zoff, z1 = (float)(o.z >> 8) + zoff;
+  return s0 * (a[0] - z0 * att[64]) + s1 * (a[1] - z1 * att[65]);
+}
+
 // LDS carve-up: hin (exchange words and scratch), xs (fp32 activations), xa (A operand steps),
-// cx (bias and x sums per step), red (4 quarters x 64 columns), red16 (wave scalars), qkv
-// (rotated q, k and the new v).
+// cx (bias and x sums per step), red (16 k-parts x 64 columns), red16 (wave scalars), qkv
+// (rotated q, k, the new v, the attention output and its half sums), flags (wait votes).
 struct Lds {
   float *hin, *xs;
   unsigned char* xa;
   float2* cx;
   float *red, *red16, *qkv;
+  int* flags;  // two sets of wait votes
 };
+constexpr int kQkvFloats = 272;
 
 #define MIQ_PD_INLINE __device__ __attribute__((always_inline)) inline
 
-// h(l) for this thread's 8-value chunk (threads < H / 8; the others get zeros): layer 0 is the
-// current token's embedding row; later layers sum the down projection's K-slices in slice order
-// and then add the residual hmid(l - 1), as the split-K GEMV with the residual as its bias does.
-MIQ_PD_INLINE bool gather_h(const Params& p, const Ctx& c, int l, int tok, float* raw, float* v) {
-  const int H = p.H, ks = p.ksd, ch = threadIdx.x;
-  if (l > 0) {
-    // the ks down slices and hmid are consecutive H-word rows; hmid (written a whole step
-    // earlier) is waited for on its own, so the rounds that wait for the slices carry only them
-    const uint32_t td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
-    if (!wait_tagged<8>(
-            H, c, p.tdown + (size_t)ks * H, [&](int j) { return j; }, [=](int) { return th; }, raw + ks * H))
-      return false;
-    if (!wait_tagged<8>(ks * H, c, p.tdown, [&](int j) { return j; }, [=](int) { return td; }, raw)) return false;
-  }
+// h(l) for this thread's 8-value chunk (threads < H / 8; the others get zeros), also left in
+// raw[0..H): layer 0 is the current token's embedding row (each thread writes its own chunk of
+// raw); later layers wait for the fixed-point words of h(l) (the down projection's K-slices plus
+// hmid(l - 1)).
+MIQ_PD_INLINE bool gather_h(const Params& p, const Ctx& c, const Lds& s, int l, int tok, float* raw, float* v) {
+  const int H = p.H, ch = threadIdx.x;
+  if (l > 0 && !wait_fixed<1>(H, c, fx_row(p, c.ep, l - 1), p.ksd + 1, raw, s.flags)) return false;
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = 0.f;
   if (ch < H / 8) {
@@ -282,13 +379,11 @@ MIQ_PD_INLINE bool gather_h(const Params& p, const Ctx& c, int l, int tok, float
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = __half2float(e[j]);
       }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) raw[ch * 8 + j] = v[j];  // the thread's own chunk, as the wait leaves it
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float h = raw[ch * 8 + j];
-        for (int sl = 1; sl < ks; ++sl) h += raw[sl * H + ch * 8 + j];
-        v[j] = h + raw[ks * H + ch * 8 + j];
-      }
+      for (int j = 0; j < 8; ++j) v[j] = raw[ch * 8 + j];
     }
   }
   return true;
@@ -308,11 +403,11 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
     float4 nw[2];
     norm_prefetch(nw, (const float*)lt[IN_LN], H);
     const float* bias = (const float*)lt[QKV_B];
-    float bv = (bias && threadIdx.x < 64) ? bias[min(c0 + (int)threadIdx.x, NQ - 1)] : 0.f;
+    float bv = (bias && threadIdx.x < 64) ? ldg(bias + min(c0 + (int)threadIdx.x, NQ - 1)) : 0.f;
     pin(bv);
     PD_MARK(l, 0);
     float v[8];
-    if (!gather_h(p, c, l, tok, s.hin, v)) return false;
+    if (!gather_h(p, c, s, l, tok, s.hin, v)) return false;
     PD_MARK(l, 1);
     const int ch = threadIdx.x;
     norm_stage(v, nw, s.red16);
@@ -332,21 +427,27 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
   return true;
 }
 
-// Attention of query head hq at position pos over positions 0..pos: RoPE of q and of the kv
+// Query head hq at position pos over positions 0..pos, all layers: RoPE of q and of the kv
 // head's new k (the first query head of each group writes k and v into the caches), scores
-// (q . k) * scale, softmax, sum p v. Four threads per position for the scores, a wave per
-// residue of the position mod 16 and a lane per dimension for the weighted sum. The cache
-// rows of the first 256 positions and the RoPE row are loaded before q/k/v are waited for.
+// (q . k) * scale, softmax, sum p v, then the head's o share (all H columns) as tagged words.
+// Four threads per position for the scores, a wave per residue of the position mod 16 and a
+// lane per dimension for the weighted sum. The cache rows of the first 256 positions, the RoPE
+// row and the head's Wo rows are loaded before q/k/v are waited for.
 MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq, int pos) {
-  const int NH = p.NH, NKV = p.NKV, LMAX = p.LMAX, rep = NH / NKV, g = hq / rep, S = pos + 1;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qq = tid & 3, jq = tid >> 2;
+  float zo = p.zoff;
+  pin(zo);
+  const int H = p.H, NH = p.NH, NKV = p.NKV, LMAX = p.LMAX, rep = NH / NKV, g = hq / rep, S = pos + 1;
   float* sp = s.hin + 256;  // scores -> probabilities [S]
   float* qs = s.qkv;
   float* kn = s.qkv + 64;
   float* vn = s.qkv + 128;
-  const int jr = (tid & 63) < 32 ? (tid & 63) : (tid & 63) - 32;
+  float* att = s.qkv + 192;  // 64 values, then the sums of its halves
+  const int jr = (threadIdx.x & 63) < 32 ? (threadIdx.x & 63) : (threadIdx.x & 63) - 32;
   const float cs = p.cos_t[(size_t)pos * 32 + jr], sn = p.sin_t[(size_t)pos * 32 + jr];
   for (int l = 0; l < p.L; ++l) {
+    // thread indices recomputed per layer (opaque_tid): address math hoisted out of the layer
+    // loop would hold registers for the whole token
+    const int tid = opaque_tid(), wave = uniform(tid >> 6), lane = tid & 63, qq = tid & 3, jq = tid >> 2;
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
     float* kc = (float*)lt[KC] + (size_t)g * LMAX * 64;
     float* vc = (float*)lt[VC] + (size_t)g * LMAX * 64;
@@ -354,21 +455,23 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
     {
       const float* kp = kc + (size_t)min(jq, LMAX - 1) * 64 + qq * 16;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const float4*>(kp + 4 * i);
+      for (int i = 0; i < 4; ++i) kr[i] = ldgf4(kp + 4 * i);
     }
     float vr[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) vr[i] = vc[(size_t)min(wave + 16 * i, LMAX - 1) * 64 + lane];
+    for (int i = 0; i < 16; ++i) vr[i] = ldg(vc + (size_t)min(wave + 16 * i, LMAX - 1) * 64 + lane);
 #pragma unroll
     for (int i = 0; i < 4; ++i) pin(kr[i]);
 #pragma unroll
     for (int i = 0; i < 16; ++i) pin(vr[i]);
+    OCol oc;  // the head's Wo rows for column tid
+    ocol_issue(oc, (const uint32_t*)lt[O_QW], (const uint32_t*)lt[O_QZ], (const __half*)lt[O_SC], hq, H, tid, p.lgs);
     const uint32_t tg = c.tag(l, P_QKV);
     PD_MARK(l, 0);
     const bool ok = wait_tagged<1>(
         192, c, p.tq,
         [&](int i) { return i < 64 ? hq * 64 + i : i < 128 ? (NH + g) * 64 + (i - 64) : (NH + NKV + g) * 64 + (i - 128); },
-        [=](int) { return tg; }, s.hin);
+        [=](int) { return tg; }, s.hin, s.flags);
     if (!ok) return false;
     PD_MARK(l, 1);
     if (tid < 64) {
@@ -377,8 +480,8 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
       kn[d] = rope1(s.hin + 64, d, 32, cs, sn);
       vn[d] = s.hin[128 + d];
       if (hq % rep == 0) {
-        kc[(size_t)pos * 64 + d] = kn[d];
-        vc[(size_t)pos * 64 + d] = vn[d];
+        stg(kc + (size_t)pos * 64 + d, kn[d]);
+        stg(vc + (size_t)pos * 64 + d, vn[d]);
       }
     }
     __syncthreads();
@@ -391,7 +494,7 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
       } else {
         const float* kp = kc + (size_t)min(j, LMAX - 1) * 64 + qq * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kp + 4 * i);
+        for (int i = 0; i < 4; ++i) k4[i] = ldgf4(kp + 4 * i);
       }
       if (j == pos) {
 #pragma unroll
@@ -432,76 +535,67 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
       for (int i = 0; i < 16; ++i) {
         const int j = cb + wave + 16 * i;
         if (j < S) {
-          const float v = j == pos ? vn[lane] : cb == 0 ? vr[i] : vc[(size_t)j * 64 + lane];
+          const float v = j == pos ? vn[lane] : cb == 0 ? vr[i] : ldg(vc + (size_t)j * 64 + lane);
           o = fmaf(sp[j], v, o);
         }
       }
     }
-    // 16 waves' partial sums (in red, which the attention does not otherwise use), combined in
-    // wave order, then divided by the softmax denominator
+    // 16 waves' partial sums, combined in wave order, then divided by the softmax denominator
     s.red[wave * 64 + lane] = o;
     __syncthreads();
     if (tid < 64) {
       float y = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) y += s.red[w * 64 + tid];
-      tput(p.tatt + hq * 64 + tid, c.tag(l, P_ATT), y / s.red16[16]);
-    }
-    PD_MARK(l, 2);
-    __syncthreads();
-  }
-  return true;
-}
-
-// o projection, columns [64 t, 64 t + 64) of H: h(l) + att(l) @ Wo.
-template <int SA>
-MIQ_PD_INLINE bool role_o(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
-  float zo = p.zoff;
-  pin(zo);
-  const int H = p.H, NHD = p.NH * 64, ks = p.ksd, c0 = t * kTile;
-  const int lane = threadIdx.x & 63;
-  for (int l = 0; l < p.L; ++l) {
-    const uint64_t* lt = p.layers + (size_t)l * kSlots;
-    Tile<__half, SA> w;
-    tile_issue(w, (const uint32_t*)lt[O_QW], (const uint32_t*)lt[O_QZ], (const __half*)lt[O_SC], H, c0, 0, NHD / 32,
-               p.lgs);
-    // words: att (NHD), then for l > 0 the residual h(l) of these columns: ks slices + hmid
-    const int nres = l == 0 ? 0 : (ks + 1) * kTile;
-    const uint32_t ta = c.tag(l, P_ATT), td = c.tag(l - 1, P_DOWN), th = c.tag(l - 1, P_HMID);
-    PD_MARK(l, 0);
-    const bool ok = wait_tagged<2>(  // att is followed by the down slices and hmid
-        NHD + nres, c, p.tatt,
-        [&](int i) {
-          const int j = i - NHD, sl = j >> 6;
-          return i < NHD ? i : NHD + sl * H + c0 + (j & 63);
-        },
-        [=](int i) { return i < NHD ? ta : ((i - NHD) >> 6 < ks ? td : th); }, s.hin);
-    if (!ok) return false;
-    PD_MARK(l, 1);
-    float hres = 0.f;
-    if (threadIdx.x < 64) {
-      if (l == 0) {
-        hres = (tok >= 0 && tok < p.V) ? __half2float(p.embed[(size_t)tok * H + min(c0 + lane, H - 1)]) : 0.f;
-      } else {
-        const float* r = s.hin + NHD;
-        hres = r[lane];
-        for (int sl = 1; sl < ks; ++sl) hres += r[sl * kTile + lane];
-        hres = hres + r[ks * kTile + lane];
+      y = y / s.red16[16];
+      att[tid] = y;
+      const float lo = wave_sum(tid < 32 ? y : 0.f), hi = wave_sum(tid < 32 ? 0.f : y);
+      if (tid == 0) {
+        att[64] = lo;
+        att[65] = hi;
       }
     }
-    if ((int)threadIdx.x < NHD / 8) stage_chunk(threadIdx.x, s.hin + threadIdx.x * 8, s.xa, s.cx);
     __syncthreads();
-    PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
-    PD_MARK(l, 4);
-    if (threadIdx.x < 64 && c0 + lane < H) tput(p.thmid + c0 + lane, c.tag(l, P_HMID), y + hres);
+    PD_MARK(l, 5);
+    if (tid < H) tput(p.tpart + (size_t)hq * H + tid, c.tag(l, P_ATT), ocol_dot(oc, att, zo));
+    PD_MARK(l, 2);
+  }
+  return true;
+}
+
+// hmid(l) of columns [64 t, 64 t + 64): h(l) plus the heads' o shares, summed in head order.
+// h(l) of the chunk is waited for first (it is ready a whole head step earlier).
+MIQ_PD_INLINE bool role_ored(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
+  const int H = p.H, NH = p.NH, c0 = t * kTile;
+  for (int l = 0; l < p.L; ++l) {
+    float hres = 0.f;
+    PD_MARK(l, 0);
+    if (l == 0) {
+      if (threadIdx.x < 64 && tok >= 0 && tok < p.V) hres = __half2float(p.embed[(size_t)tok * H + c0 + threadIdx.x]);
+    } else {
+      if (!wait_fixed<1>(kTile, c, fx_row(p, c.ep, l - 1, c0), p.ksd + 1, s.hin, s.flags)) return false;
+      if (threadIdx.x < 64) hres = s.hin[threadIdx.x];
+    }
+    const uint32_t ta = c.tag(l, P_ATT);
+    // (its own vote flags: the flags above may still be read by a slower wave)
+    if (!wait_tagged<2>(
+            NH * kTile, c, p.tpart, [&](int i) { return (i >> 6) * H + c0 + (i & 63); }, [=](int) { return ta; },
+            s.hin + kTile, s.flags + kWaves))
+      return false;
+    PD_MARK(l, 1);
+    if (threadIdx.x < 64) {
+      float y = hres;
+      for (int h = 0; h < NH; ++h) y += s.hin[kTile + h * kTile + threadIdx.x];
+      tput(p.thmid + c0 + threadIdx.x, c.tag(l, P_HMID), y);
+    }
     PD_MARK(l, 2);
     __syncthreads();
   }
   return true;
 }
 
-// gate|up projection, columns [64 t, 64 t + 64) of 2I: RMSNorm(hmid(l)) @ Wgu.
+// gate|up projection, columns [64 t, 64 t + 64) of 2I: RMSNorm(hmid(l)) @ Wgu. The tile also
+// adds the residual hmid(l) of column chunks t, t + ngu, ... to h(l + 1) (term ksd).
 template <int SA>
 MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
   float zo = p.zoff;
@@ -516,10 +610,14 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
     norm_prefetch(nw, (const float*)lt[POST_LN], H);
     const uint32_t th = c.tag(l, P_HMID);
     PD_MARK(l, 0);
-    if (!wait_tagged<2>(
-            H, c, p.thmid, [&](int i) { return i; }, [=](int) { return th; }, s.xs))
+    if (!wait_tagged<1>(
+            H, c, p.thmid, [&](int i) { return i; }, [=](int) { return th; }, s.xs, s.flags))
       return false;
     PD_MARK(l, 1);
+    if (threadIdx.x < 64) {  // the residual hmid(l), term ksd of h(l + 1)
+      const Fx hn = fx_row(p, c.ep, l);
+      for (int k = t; k < H / kTile; k += p.ngu) fx_put(hn, k * kTile + threadIdx.x, s.xs[k * kTile + threadIdx.x], p.ksd);
+    }
     const int ch = threadIdx.x;
     float v[8];
 #pragma unroll
@@ -539,7 +637,7 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
 }
 
 // down projection, columns [64 t, 64 t + 64) of H over K-slice sl of I: the slice's share of
-// silu(gate) * up @ Wd.
+// silu(gate) * up @ Wd, term sl of h(l + 1).
 template <int SD>
 MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t, int sl) {
   float zo = p.zoff;
@@ -554,7 +652,7 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
     PD_MARK(l, 0);
     if (!wait_tagged<4>(
             2 * KS, c, p.tgu, [&](int i) { return i < KS ? sl * KS + i : I + sl * KS + (i - KS); },
-            [=](int) { return tg; }, s.hin))
+            [=](int) { return tg; }, s.hin, s.flags))
       return false;
     PD_MARK(l, 1);
     const int ch = threadIdx.x;
@@ -571,8 +669,7 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
     PD_MARK(l, 3);
     const float y = tile_sum(tile_mma(w, s.xa, s.cx, rb, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
-    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < H)
-      tput(p.tdown + (size_t)sl * H + c0 + threadIdx.x, c.tag(l, P_DOWN), y);
+    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < H) fx_put(fx_row(p, c.ep, l), c0 + threadIdx.x, y, sl);
     PD_MARK(l, 2);
     __syncthreads();
   }
@@ -596,7 +693,7 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   norm_prefetch(nw, p.final_norm, H);
   PD_MARK(p.L, 0);
   float v[8];
-  if (!gather_h(p, c, p.L, tok, s.hin, v)) return false;
+  if (!gather_h(p, c, s, p.L, tok, s.hin, v)) return false;
   PD_MARK(p.L, 1);
   const int ch = threadIdx.x;
   norm_stage(v, nw, s.red16);
@@ -640,7 +737,7 @@ MIQ_PD_INLINE bool finish_token(const Params& p, const Ctx& c, const Lds& s, int
   const int G = gridDim.x;
   const uint32_t tg = c.tag(p.L, P_AMAX);
   if (!wait_tagged<1>(
-          2 * G, c, p.tamax, [&](int i) { return i; }, [=](int) { return tg; }, s.hin))
+          2 * G, c, p.tamax, [&](int i) { return i; }, [=](int) { return tg; }, s.hin, s.flags))
     return false;
   if (threadIdx.x < 64) {
     float fv = -INFINITY;
@@ -676,6 +773,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   s.red = reinterpret_cast<float*>(s.cx + p.lds_x / 32);
   s.red16 = s.red + kKParts * 64;
   s.qkv = s.red16 + 32;
+  s.flags = reinterpret_cast<int*>(s.qkv + kQkvFloats);
   Ctx c;
   c.deadline = wall_clock64() + p.spin_limit;
   PD_MARK(p.L + 1, 0);
@@ -687,6 +785,11 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(p.ctl + 1, 2u);
     return;
   }
+  {  // the next token's bank back to zero (this token's was zeroed by the previous step)
+    unsigned long long* z = p.fx + ((c.ep + 1u) & 1u) * p.bank_words;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < p.bank_words; i += (size_t)gridDim.x * kThreads)
+      __hip_atomic_store(z + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   int r = blockIdx.x;
   bool ok = true;
   if (r < p.nq) {
@@ -694,7 +797,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   } else if ((r -= p.nq) < p.na) {
     ok = role_attn(p, c, s, r, pos);
   } else if ((r -= p.na) < p.no) {
-    ok = role_o<SA>(p, c, s, r, tok);
+    ok = role_ored(p, c, s, r, tok);
   } else if ((r -= p.no) < p.ngu) {
     ok = role_gu<SA>(p, c, s, r);
   } else if ((r -= p.ngu) < p.nd) {
@@ -709,8 +812,8 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
 // Role counts, K-slices of the down projection and LDS regions for a model shape.
 struct Plan {
   int G, nq, na, no, ngu, ksd, nd, lds_a, lds_x, spa, spd;
-  size_t lds_bytes, ws_bytes;
-  size_t off_tq, off_tatt, off_thmid, off_tgu, off_tdown, off_tamax;
+  size_t lds_bytes, ws_bytes, bank_words;
+  size_t off_tq, off_tpart, off_thmid, off_tgu, off_tamax, off_fx, off_side;
 };
 
 static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits, Plan* pl) {
@@ -728,8 +831,8 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
               "decode_persistent: H, NH*HD and I must be multiples of the group size %d", gs);
   // K in 32-value steps, at most kMaxSPQ per k-part of a tile
   auto rows_ok = [&](int K) { return K % 32 == 0 && K <= 32 * kKParts * kMaxSPQ; };
-  MIQ_REQUIRE(rows_ok(H) && rows_ok(NHD) && LMAX <= 8192 && NHD <= 2 * kThreads - 9 * kTile, MIQ_ERR_UNSUPPORTED,
-              "decode_persistent: H=%d / NH*HD=%d / LMAX=%d out of range for gs=%d", H, NHD, LMAX, gs);
+  MIQ_REQUIRE(rows_ok(H) && H <= kThreads && LMAX <= 8192, MIQ_ERR_UNSUPPORTED,
+              "decode_persistent: H=%d / NH=%d / LMAX=%d out of range", H, NH, LMAX);
   int cus = 0, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
@@ -742,35 +845,42 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
   q.ngu = 2 * I / kTile;
   q.ksd = 0;
   for (int k = 8; k >= 1; k >>= 1) {
-    if (I % (8 * k) || !rows_ok(I / k) || 2 * (I / k) > 4 * kThreads || (k + 1) * H > 8 * kThreads) continue;
+    if (I % (8 * k) || !rows_ok(I / k) || 2 * (I / k) > 4 * kThreads) continue;
     if (q.nq + q.na + q.no + q.ngu + q.no * k > q.G) continue;
     q.ksd = k;
     break;
   }
-  MIQ_REQUIRE(q.ksd > 0 && 2 * q.G <= kThreads, MIQ_ERR_UNSUPPORTED,
+  MIQ_REQUIRE(q.ksd > 0 && 2 * q.G <= kThreads && NH * kTile <= 2 * kThreads, MIQ_ERR_UNSUPPORTED,
               "decode_persistent: the roles of this shape do not fit %d workgroups", q.G);
   q.nd = q.no * q.ksd;
   const int KS = I / q.ksd;
-  q.spa = (std::max(H, NHD) / 32 + kKParts - 1) / kKParts;
+  q.spa = (H / 32 + kKParts - 1) / kKParts;
   q.spd = (KS / 32 + kKParts - 1) / kKParts;
-  q.lds_a = std::max(std::max((q.ksd + 1) * H, NHD + (q.ksd + 1) * kTile), std::max(std::max(2 * KS, kWaves * 64), std::max(256 + LMAX, 2 * q.G)));
+  q.lds_a = std::max(std::max(std::max(H, 2 * KS), (NH + 1) * kTile), std::max(256 + LMAX, 2 * q.G));
   q.lds_a = (q.lds_a + 3) & ~3;
-  q.lds_x = (std::max(H, std::max(NHD, KS)) + 63) & ~63;  // even step count: red 16-byte aligned
+  q.lds_x = (std::max(H, KS) + 63) & ~63;  // even step count: red 16-byte aligned
   q.lds_bytes = (size_t)(q.lds_a + q.lds_x) * 4 + (size_t)(q.lds_x / 32) * kStepBytes +
-                (size_t)(2 * (q.lds_x / 32) + kKParts * 64 + 32 + 192) * 4;
+                (size_t)(2 * (q.lds_x / 32) + kKParts * 64 + 32 + kQkvFloats + 2 * kWaves) * 4;
+  int lds_max = 0;
+  if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds_max <= 0)
+    return fail(MIQ_ERR_HIP, "decode_persistent: cannot query the LDS limit");
+  MIQ_REQUIRE(q.lds_bytes <= (size_t)lds_max, MIQ_ERR_UNSUPPORTED,
+              "decode_persistent: %zu bytes of LDS for this shape exceed the device's %d", q.lds_bytes, lds_max);
   size_t off = 256;  // control words
-  auto take = [&](size_t words) {
+  auto take = [&](size_t bytes) {
     const size_t o = off;
-    off += (words * 8 + 255) & ~(size_t)255;
+    off += (bytes + 255) & ~(size_t)255;
     return o;
   };
-  q.off_tq = take(NQ);
-  // att, the down projection's K-slices and hmid back to back: one base for the o role's poll
-  q.off_tatt = take(NHD + (size_t)(q.ksd + 1) * H);
-  q.off_tdown = q.off_tatt + (size_t)NHD * 8;
-  q.off_thmid = q.off_tdown + (size_t)q.ksd * H * 8;
-  q.off_tgu = take(2 * (size_t)I);
-  q.off_tamax = take(2 * (size_t)q.G);
+  q.off_tq = take((size_t)NQ * 8);
+  q.off_tpart = take((size_t)NH * H * 8);
+  q.off_thmid = take((size_t)H * 8);
+  q.off_tgu = take(2 * (size_t)I * 8);
+  q.off_tamax = take(2 * (size_t)q.G * 8);
+  const size_t n = (size_t)L * H;  // h(l + 1) words of every layer
+  q.bank_words = ((n * 12 + 255) & ~(size_t)255) / 8;
+  q.off_fx = take(2 * q.bank_words * 8);
+  q.off_side = take((size_t)(q.ksd + 1) * n * 4);
   q.ws_bytes = off;
   *pl = q;
   return MIQ_OK;
@@ -811,10 +921,9 @@ extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* em
   // 32-k steps per k-part (wave) of the K = H projections and of a down K-slice, rounded up to the
   // instantiated register capacities
   void (*kfn)(pd::Params) = nullptr;
-  if (pl.spa <= 2 && pl.spd <= 4) kfn = pd::decode_persistent_kernel<2, 4>;
-  else if (pl.spa <= 4 && pl.spd <= 4) kfn = pd::decode_persistent_kernel<4, 4>;
-  else if (pl.spa <= 4) kfn = pd::decode_persistent_kernel<4, 8>;
-  else kfn = pd::decode_persistent_kernel<8, 8>;
+  // (H <= 1024 keeps spa <= 2)
+  if (pl.spd <= 4) kfn = pd::decode_persistent_kernel<2, 4>;
+  else kfn = pd::decode_persistent_kernel<2, 8>;
   auto kern = reinterpret_cast<const void*>(kfn);
   if (hipGetDevice(&dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, pd::kThreads, pl.lds_bytes) != hipSuccess)
@@ -837,11 +946,13 @@ extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* em
   p.logits = logits;
   p.ctl = reinterpret_cast<uint32_t*>(w);
   p.tq = reinterpret_cast<uint64_t*>(w + pl.off_tq);
-  p.tatt = reinterpret_cast<uint64_t*>(w + pl.off_tatt);
+  p.tpart = reinterpret_cast<uint64_t*>(w + pl.off_tpart);
   p.thmid = reinterpret_cast<uint64_t*>(w + pl.off_thmid);
   p.tgu = reinterpret_cast<uint64_t*>(w + pl.off_tgu);
-  p.tdown = reinterpret_cast<uint64_t*>(w + pl.off_tdown);
   p.tamax = reinterpret_cast<uint64_t*>(w + pl.off_tamax);
+  p.fx = reinterpret_cast<unsigned long long*>(w + pl.off_fx);
+  p.fside = reinterpret_cast<float*>(w + pl.off_side);
+  p.bank_words = pl.bank_words;
   p.L = L;
   p.H = H;
   p.NH = NH;

@@ -220,6 +220,30 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// ---- loads through pointers of unknown address space --------------------------------------
+// A pointer read from memory (a layer table entry, say) is generic to the compiler, and a
+// generic access is a flat instruction, which counts in lgkmcnt as well as vmcnt: every later
+// wait for LDS (each barrier waits for lgkmcnt 0) would then also wait for that global load's
+// round trip. These helpers load through a global (address space 1) pointer instead; the
+// 16- and 8-byte forms go through native vector types, which keep the address space.
+#define MIQ_GLOBAL __attribute__((address_space(1)))
+typedef uint32_t miq_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t miq_u32x4 __attribute__((ext_vector_type(4)));
+template <typename T> __device__ __forceinline__ T ldg(const T* p) { return *(const MIQ_GLOBAL T*)p; }
+__device__ __forceinline__ uint4 ldg4(const void* p) {
+  const miq_u32x4 v = *(const MIQ_GLOBAL miq_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ldgf4(const void* p) {
+  const miq_u32x4 v = *(const MIQ_GLOBAL miq_u32x4*)p;
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ __forceinline__ uint2 ldg2(const void* p) {
+  const miq_u32x2 v = *(const MIQ_GLOBAL miq_u32x2*)p;
+  return make_uint2(v.x, v.y);
+}
+template <typename T> __device__ __forceinline__ void stg(T* p, T v) { *(MIQ_GLOBAL T*)p = v; }
+
 // Uniform (scalar) copy of a value that is the same in every lane.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 

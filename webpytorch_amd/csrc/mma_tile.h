@@ -62,7 +62,7 @@ __device__ __forceinline__ u32x4 b_bf16(uint32_t q, const BMasks& k) {
 template <typename ST> struct Scales4;
 template <> struct Scales4<__half> {
   using T = uint2;
-  static __device__ __forceinline__ T load(const __half* p) { return *reinterpret_cast<const uint2*>(p); }
+  static __device__ __forceinline__ T load(const __half* p) { return ldg2(p); }
   static __device__ __forceinline__ float get(const T& v, int t) {
     const uint32_t w = t < 2 ? v.x : v.y;
     return __half2float(__ushort_as_half((unsigned short)((t & 1) ? w >> 16 : w & 0xFFFFu)));
@@ -70,7 +70,7 @@ template <> struct Scales4<__half> {
 };
 template <> struct Scales4<float> {
   using T = uint4;
-  static __device__ __forceinline__ T load(const float* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ T load(const float* p) { return ldg4(p); }
   static __device__ __forceinline__ float get(const T& v, int t) {
     return __uint_as_float(t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w);
   }
@@ -124,33 +124,34 @@ __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw,
     for (int i = 0; i < SPQ; ++i) {
       const int ii = min(i, t.ns - 1);
       const int g = (r0 + 4 * ii) >> gsh;
-      t.w[i] = *reinterpret_cast<const uint4*>(wp + (uint32_t)(4 * ii * N));
+      t.w[i] = ldg4(wp + (uint32_t)(4 * ii * N));
       t.s[i] = Scales4<ST>::load(sc + (uint32_t)(g * N + c));
-      t.z[i] = qz[(uint32_t)(g * (N >> 3) + (c >> 3))];
+      t.z[i] = ldg(qz + (uint32_t)(g * (N >> 3) + (c >> 3)));
     }
     if (PIN) pin(t);
   }
 }
 
 // This wave's share of sum_k x_k W[k][c] for its 4 columns (valid in lanes 0..15: columns
-// c0 + 4 lane + t). The A fragment and step sums of step i + 2 are read from LDS while step i
-// computes (reads clamped to the wave's last step, so they need no guard); the four MFMA chains
-// of a quantization group share each step's A fragment, and each group is folded into acc with
-// its scales and zero points.
-template <typename ST, int SPQ>
-__device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float2* cx, int rb,
-                                           int c0, int lgs, float zoff) {
+// c0 + 4 lane + t), the codes of step i given by wsrc(i). The A fragment and step sums of step
+// i + 2 are read from LDS while step i computes (reads clamped to the wave's last step, so they
+// need no guard); the four MFMA chains of a quantization group share each step's A fragment,
+// and each group is folded into acc with its scales and zero points.
+template <typename ST, int SPQ, typename WSRC>
+__device__ __forceinline__ float4 tile_mma_core(const WSRC& wsrc, const uint32_t* tz, const typename Scales4<ST>::T* ts,
+                                                int st0, int ns, const unsigned char* xa, const float2* cx, int rb,
+                                                int c0, int lgs, float zoff) {
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  if (t.ns == 0) return make_float4(0.f, 0.f, 0.f, 0.f);  // wave-uniform: a k-part past the end of K
+  if (ns == 0) return make_float4(0.f, 0.f, 0.f, 0.f);  // wave-uniform: a k-part past the end of K
   const int tid = opaque_tid();
   const int lane = tid & 63;
   const int sh = ((c0 + 4 * (lane & 15)) & 7) * 4;
   // Only A rows 0-2 (lanes with lane % 16 < 3) carry data: D rows 3-15 are never read, so the
   // other lanes skip the LDS read and feed whatever their registers hold.
   const bool arow = (lane & 15) < 3;
-  const unsigned char* ap = xa + t.st0 * kStepBytes + (lane >> 4) * 64 + (lane & 15) * 16;
-  const float2* cp = cx + t.st0;
-  const int last = t.ns - 1;
+  const unsigned char* ap = xa + st0 * kStepBytes + (lane >> 4) * 64 + (lane & 15) * 16;
+  const float2* cp = cx + st0;
+  const int last = ns - 1;
   const BMasks bm = b_masks();
   bf16x8 a0, a1;
   if (arow) {
@@ -158,7 +159,7 @@ __device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigne
     a1 = *reinterpret_cast<const bf16x8*>(ap + min(1, last) * kStepBytes);
   }
   float2 x0 = cp[0], x1 = cp[min(1, last)];
-  const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
+  const int r0 = rb + 4 * st0, gsh = lgs - 3;
   floatx4 d[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) d[q] = (floatx4){0.f, 0.f, 0.f, 0.f};
@@ -168,8 +169,9 @@ __device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigne
     bf16x8 a2;
     if (arow) a2 = *reinterpret_cast<const bf16x8*>(ap + min(i + 2, last) * kStepBytes);
     const float2 x2 = cp[min(i + 2, last)];
-    if (i < t.ns) {
-      const uint32_t wt[4] = {t.w[i].x, t.w[i].y, t.w[i].z, t.w[i].w};
+    if (i < ns) {
+      const uint4 wv = wsrc(i);
+      const uint32_t wt[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const u32x4 bw = b_bf16(wt[q], bm);
@@ -178,12 +180,12 @@ __device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigne
       cs += x0.x;
       xs += x0.y;
       const int r = r0 + 4 * i;
-      if (i + 1 == t.ns || ((r + 4) >> gsh) != (r >> gsh)) {  // last step of this group
+      if (i + 1 == ns || ((r + 4) >> gsh) != (r >> gsh)) {  // last step of this group
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float pv = (d[q][0] + d[q][1]) + d[q][2];
-          const float zc = (float)((t.z[i] >> (sh + 4 * q)) & 15u) + zoff;
-          acc[q] = fmaf(Scales4<ST>::get(t.s[i], q), pv - fmaf(zc, xs, cs), acc[q]);
+          const float zc = (float)((tz[i] >> (sh + 4 * q)) & 15u) + zoff;
+          acc[q] = fmaf(Scales4<ST>::get(ts[i], q), pv - fmaf(zc, xs, cs), acc[q]);
           d[q] = (floatx4){0.f, 0.f, 0.f, 0.f};
         }
         cs = 0.f;
@@ -197,7 +199,11 @@ __device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigne
   }
   return make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
-
+template <typename ST, int SPQ>
+__device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float2* cx, int rb,
+                                           int c0, int lgs, float zoff) {
+  return tile_mma_core<ST, SPQ>([&](int i) { return t.w[i]; }, t.z, t.s, t.st0, t.ns, xa, cx, rb, c0, lgs, zoff);
+}
 // Sums the kKParts k-parts of each column in wave order; valid in threads 0..63 (column
 // c0 + thread). red holds kKParts x 64 floats, 16-byte aligned.
 __device__ __forceinline__ float tile_sum(float4 acc, float* red) {
