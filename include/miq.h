@@ -260,6 +260,11 @@ int miq_decode_state_words(void);
  * Replaces: `CausalLM._embed_ids` (webtorch/llm.py:1530-1536). */
 int miq_embed(const int32_t* ids, const void* embed, float* out, int T, int H, int V, void* stream);
 
+/* miq_embed over an fp32 table [V][H]: the token_embd of a GGUF model, dequantized once at load
+ * so that every row is the exact fp32 the file's blocks decode to.
+ * Replaces: `_QuantRows` row lookups (webtorch/llm.py:355-375, 1045). */
+int miq_embed_f32(const int32_t* ids, const float* embed, float* out, int T, int H, int V, void* stream);
+
 /* out[t] = (x[t] / sqrt(mean(x[t]^2) + eps)) * w, fp32.
  * Replaces: `CausalLM._rms` (webtorch/llm.py:1259-1268) and `rmsnorm` (webtorch/_core.py:2234-2263). */
 int miq_rmsnorm(const float* x, const float* w, float* out, int T, int H, float eps, void* stream);

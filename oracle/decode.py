@@ -10,6 +10,12 @@ SwiGLU (`llm.py:1489-1496`, `silu` `_core.py:503-504`), the tied head re-quantiz
 `generate` with no end token yields the prefill's token then one per decode step
 (`llm.py:1775-1787`).
 
+A layer given as {"W": fp32 (out, in)[, "bias"]} instead of GPTQ tensors is multiplied in
+float32 as given: the reference's native GGUF layers compute x @ dequant(W)^T
+(`GGMLLinear` / `UnquantizedLinear`, `webtorch/_core.py:4377-4406, 4462-4481`), and so does a
+model whose weights carry "head_W" (a dense head) or "head_q" (GPTQ head blocks) instead of
+re-quantizing the head from the embedding.
+
 Pins: golden token ids written by the reference's own `CausalLM` CPU path at a reduced
 shape (`tests/golden/`); every building block is also pinned on its own (RMSNorm, RoPE and
 softmax closed forms, `gptq.gptq_matmul_np`).
@@ -31,9 +37,14 @@ class Qwen2Oracle:
         self.layers = weights["layers"]
         self.embed = weights["embed"]                      # (V, H) fp16
         self.final_norm = np.asarray(weights["final_norm"], np.float32)
-        # an untied model quantizes its own fp16 lm_head the same way (`webtorch/llm.py:604-612`)
-        head = weights.get("head")
-        self.head = self.quantize_head(self.embed if head is None else np.asarray(head, np.float16), head_block)
+        if weights.get("head_W") is not None:
+            self.head = [{"W": np.asarray(weights["head_W"], np.float32)}]
+        elif weights.get("head_q") is not None:
+            self.head = list(weights["head_q"])
+        else:
+            # an untied model quantizes its own fp16 lm_head the same way (`webtorch/llm.py:604-612`)
+            head = weights.get("head")
+            self.head = self.quantize_head(self.embed if head is None else np.asarray(head, np.float16), head_block)
 
     def quantize_head(self, emb, blk):
         out = []
@@ -53,12 +64,15 @@ class Qwen2Oracle:
     def lin(self, d, x, zoff=None):
         """AutoGPTQ layers use zero offset 1 (`from_autogptq`); layers quantized on load carry
         their own (0, `_gquant`)."""
-        if zoff is None:
-            zoff = d.get("zoff", 1.0)
-        y = gptq.gptq_matmul_np(x, d["qweight"], d["qzeros"], d["scales"], d["K"], d["N"],
-                                d["gs"], d["bits"], zoff)
+        if "W" in d:
+            y = np.asarray(x, np.float32) @ np.ascontiguousarray(np.asarray(d["W"], np.float32).T)
+        else:
+            if zoff is None:
+                zoff = d.get("zoff", 1.0)
+            y = gptq.gptq_matmul_np(x, d["qweight"], d["qzeros"], d["scales"], d["K"], d["N"],
+                                    d["gs"], d["bits"], zoff)
         b = d.get("bias")
-        return y + (np.zeros(d["N"], np.float32) if b is None else np.asarray(b, np.float32))
+        return y if b is None else y + np.asarray(b, np.float32)
 
     def rope_tables(self, pos, T):
         inv = 1.0 / (self.theta ** (np.arange(0, self.HD, 2, dtype=np.float64) / self.HD))

@@ -37,6 +37,7 @@ SIGNATURES = {
     "miq_moe_down": [_p, _p, _i, _i, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _p],
     "miq_moe_combine": [_p, _p, _i, _i, _i, _p, _i, _p],
     "miq_embed": [_p, _p, _p, _i, _i, _i, _p],
+    "miq_embed_f32": [_p, _p, _p, _i, _i, _i, _p],
     "miq_rmsnorm": [_p, _p, _p, _i, _i, _f, _p],
     "miq_head_rmsnorm": [_p, _p, _p, _i, _i, _i, _i, _f, _p],
     "miq_rope_kv": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],

@@ -442,3 +442,168 @@ def fp16_weights(path, bits, gs=128):
     if not cfg.get("tie_word_embeddings", False):
         w["head"] = st.rows_f16("lm_head.weight")
     return w, cfg.get("max_position_embeddings")
+
+
+# ---- GGUF models -----------------------------------------------------------------------------
+
+def gguf_source_bits(g):
+    """The integer width that keeps what a GGUF stores (`_source_bits`, `webtorch/llm.py:296-320`):
+    8 when the block type holding the most layer weights (counted by element) takes more than 4.5
+    bits per weight, else 4."""
+    weight = {}
+    for name, t in g.infos.items():
+        if name.startswith("blk."):
+            weight[t["type"]] = weight.get(t["type"], 0) + int(np.prod([int(d) for d in t["dims"]], dtype=np.int64))
+    if not weight:
+        return 4
+    dom = max(weight, key=weight.get)
+    return 8 if tensor_nbytes(dom, 4096) * 8.0 / 4096 > 4.5 else 4
+
+
+def gguf_dequant(raw, ttype, n):
+    """fp32 device tensor of the first n values of a GGUF byte stream of type `ttype` (id):
+    block types through the device decoders (bit-exact with `ggufload.dequant`), F32 / F16 / BF16
+    by conversion."""
+    import torch
+    name = GGML_NAMES.get(int(ttype), "type%d" % int(ttype))
+    b = np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray, memoryview)) else np.asarray(raw, np.uint8)
+    if name == "F32":
+        return torch.from_numpy(b[:4 * n].view(np.float32).copy()).to(core.device())
+    if name == "F16":
+        return torch.from_numpy(b[:2 * n].view(np.float16).copy()).to(core.device()).float()
+    if name == "BF16":
+        u = b[:2 * n].view(np.uint16).astype(np.uint32) << 16
+        return torch.from_numpy(u.view(np.float32)).to(core.device())
+    nb = tensor_nbytes(int(ttype), n)
+    blocks = torch.from_numpy(b[:nb].copy()).to(core.device())
+    vals = GGML_TYPES[int(ttype)][1]
+    if name == "Q4_K":
+        return core.q4k_dequant(blocks, n // vals)
+    if not core.ggml_native_supported(name):
+        raise NotImplementedError("GGUF type %s has no decoder here" % name)
+    return core.ggml_dequant(blocks, name, n // vals)
+
+
+def _gguf_requant(W, bits, gs, bias):
+    """fp32 (out, in) device weight -> GPTQ layer dict quantized on the device (`_gquant`,
+    `webtorch/llm.py:835-853`: zero offset 0, fp32 scales)."""
+    N, K = int(W.shape[0]), int(W.shape[1])
+    if K % gs or N % (32 // bits):
+        raise NotImplementedError("(%d, %d) weight needs padding to the group / pack size" % (N, K))
+    qw, qz, sc, _, _ = core.gptq_quantize(W, gs, bits, from_out_in=True)
+    return {"qweight": qw, "qzeros": qz, "scales": sc, "zoff": 0.0, "bias": bias}
+
+
+def _gguf_linear(g, name, bits, gs, weights, bias=None):
+    """One 2-D GGUF weight as a layer: uploaded unchanged for a native kernel (`_gload_native`,
+    `webtorch/llm.py:763-785`) when `weights` is "native" and its type has one, else decoded on the
+    device and quantized to int`bits` (`_gload_quant`, `webtorch/llm.py:787-833`)."""
+    if weights == "native":
+        lin = g.linear(name, bias)
+        if lin is not None:
+            return lin
+    t = g.infos[name]
+    shape = g.shape(name)
+    if len(shape) != 2:
+        raise NotImplementedError("%s is %d-D, a linear weight is 2-D" % (name, len(shape)))
+    W = gguf_dequant(g.raw(name), t["type"], shape[0] * shape[1]).reshape(shape)
+    return _gguf_requant(W, bits, gs, bias)
+
+
+def _gguf_experts(g, name, bits, gs):
+    """The experts of a stacked `ffn_*_exps` tensor (ggml dims in, out, E), one at a time: each
+    expert's bytes are a block-aligned slice (`_gexperts`, `webtorch/llm.py:731-760`), decoded on
+    the device and quantized to int`bits` for the grouped expert kernels."""
+    t = g.infos[name]
+    E, N, K = g.shape(name)
+    per = N * K
+    nb = tensor_nbytes(t["type"], per)
+    raw = g.raw(name)
+    return [_gguf_requant(gguf_dequant(raw[e * nb:(e + 1) * nb], t["type"], per).reshape(N, K), bits, gs, None)
+            for e in range(E)]
+
+
+def gguf_weights(path, bits=None, weights="native", gs=128):
+    """Engine weights of a llama.cpp GGUF decoder (`CausalLM.from_gguf`, `webtorch/llm.py:
+    856-1129`): shape, RoPE and norm settings from the file's `{arch}.*` metadata, QK-norm and
+    sparse-MoE blocks detected from the tensors. Returns (weights, declared context length).
+
+    `bits=None` takes the width from the file (`gguf_source_bits`). `weights="native"` keeps every
+    2-D weight whose block type has a kernel here in its file encoding (GGMLLinear) and quantizes
+    the rest to int`bits`; "requant" quantizes all of them. The embedding is decoded once to an
+    exact fp32 table on the device; the head is the file's `output.weight` or, when absent, the
+    embedding (tied), native or quantized like the other weights. Experts are always quantized
+    (the grouped expert kernels read GPTQ). Recurrent / state-space blocks and partial RoPE are
+    not part of this engine and raise NotImplementedError."""
+    if weights not in ("native", "requant"):
+        raise ValueError("weights must be 'native' or 'requant', got %r" % (weights,))
+    g = GGUFFile(path)
+    arch = g.meta.get("general.architecture")
+    if not arch:
+        raise ValueError("GGUF has no general.architecture")
+    A = arch + "."
+
+    def m(key, default=None, required=True):
+        if A + key in g.meta:
+            return g.meta[A + key]
+        if default is not None or not required:
+            return default
+        raise NotImplementedError("GGUF arch %r is missing %r" % (arch, key))
+
+    bad = sorted({GGML_NAMES.get(t["type"], "type%d" % t["type"]) for t in g.infos.values()
+                  if t["type"] not in GGML_TYPES})
+    if bad:
+        raise NotImplementedError("GGUF uses quantization type(s) %s this package cannot decode" % ", ".join(bad))
+    H = int(m("embedding_length"))
+    L = int(m("block_count")) - int(m("nextn_predict_layers", 0) or 0)
+    NH = int(m("attention.head_count"))
+    NKV = int(m("attention.head_count_kv", NH) or NH)
+    HD = int(m("attention.key_length", 0, required=False) or H // NH)
+    if int(m("rope.dimension_count", 0, required=False) or HD) != HD:
+        raise NotImplementedError("partial RoPE (rope.dimension_count < head dim) is not part of this engine")
+    if m("full_attention_interval", 0, required=False) or m("attention.recurrent_layers", None, required=False) \
+            or any(n.startswith("blk.0.ssm_") for n in g.infos):
+        raise NotImplementedError("recurrent / state-space blocks are not part of this engine")
+    bits = int(bits) if bits else gguf_source_bits(g)
+    if bits not in (4, 8):
+        raise ValueError("bits must be 4 or 8")
+    f32 = lambda n: gguf_dequant(g.raw(n), g.infos[n]["type"], int(np.prod(g.shape(n))))  # noqa: E731
+    opt = lambda n: f32(n) if n in g.infos else None  # noqa: E731
+    lin = lambda n, b=None: _gguf_linear(g, n, bits, gs, weights, b)  # noqa: E731
+    top_k = int(m("expert_used_count", 0, required=False) or 0)
+    layers, I = [], int(m("feed_forward_length", 0, required=False) or 0)
+    moe_I = int(m("expert_feed_forward_length", 0, required=False) or 0)
+    for i in range(L):
+        p = "blk.%d." % i
+        post = next((n for n in ("ffn_norm", "post_attention_norm") if p + n + ".weight" in g.infos), None)
+        if post is None or p + "attn_norm.weight" not in g.infos:
+            raise NotImplementedError("GGUF block %d lacks attn_norm / ffn_norm" % i)
+        if not all(p + "attn_%s.weight" % x in g.infos for x in ("q", "k", "v")):
+            raise NotImplementedError("GGUF block %d has no separate attn_q / attn_k / attn_v" % i)
+        lay = {"in_ln": f32(p + "attn_norm.weight"), "post_ln": f32(p + post + ".weight"),
+               "qn": opt(p + "attn_q_norm.weight"), "kn": opt(p + "attn_k_norm.weight")}
+        for key, nm in (("q", "attn_q"), ("k", "attn_k"), ("v", "attn_v"), ("o", "attn_output")):
+            lay[key] = lin(p + nm + ".weight", opt(p + nm + ".bias"))
+        if p + "ffn_gate_inp.weight" in g.infos:  # sparse MoE: router + stacked experts
+            ex = {k: _gguf_experts(g, p + "ffn_%s_exps.weight" % k, bits, gs) for k in ("gate", "up", "down")}
+            E = len(ex["gate"])
+            moe_I = moe_I or g.shape(p + "ffn_gate_exps.weight")[1]
+            lay["moe"] = {"router": lin(p + "ffn_gate_inp.weight"), "top_k": top_k or 2,
+                          "experts": [{k: ex[k][e] for k in ex} for e in range(E)]}
+        else:
+            for key, nm in (("gate", "ffn_gate"), ("up", "ffn_up"), ("down", "ffn_down")):
+                lay[key] = lin(p + nm + ".weight")
+            I = I or g.shape(p + "ffn_gate.weight")[0]
+        layers.append(lay)
+    V, He = g.shape("token_embd.weight")
+    if He != H:
+        raise ValueError("token_embd is (%d, %d), embedding_length %d" % (V, He, H))
+    embed = f32("token_embd.weight").reshape(V, H)
+    head = lin("output.weight" if "output.weight" in g.infos else "token_embd.weight")
+    cfg = dict(L=L, H=H, NH=NH, NKV=NKV, HD=HD, I=I or moe_I, V=V, gs=gs, bits=bits,
+               eps=float(m("attention.layer_norm_rms_epsilon", 1e-6, required=False)),
+               theta=float(m("rope.freq_base", 10000.0, required=False)))
+    if moe_I:
+        cfg.update(n_experts=len(layers[-1]["moe"]["experts"]) if "moe" in layers[-1] else 0, moe_I=moe_I, top_k=top_k)
+    return ({"layers": layers, "embed": embed, "head_linear": head, "final_norm": f32("output_norm.weight"),
+             "cfg": cfg}, m("context_length", None, required=False))

@@ -504,7 +504,8 @@ class GGMLLinear:
         self.type_name = type_name
         self.Kt, self.Nt = int(K), int(N)
         self.packed = ggml_transpose(raw, self.Nt, _row_bytes(type_name, self.Kt))
-        self.bias = None if bias is None else to_device(np.asarray(bias, np.float32))
+        self.bias = None if bias is None else (to_device(bias, torch.float32) if isinstance(bias, torch.Tensor)
+                                               else to_device(np.asarray(bias, np.float32)))
 
     def forward(self, x, out_dtype=torch.float32):
         xt = as_activation(x)

@@ -36,6 +36,16 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
   out[(size_t)t * H + c] = (id >= 0 && id < V) ? __half2float(emb[(size_t)id * H + c]) : 0.f;
 }
 
+// fp32 table: the rows of a dequantized GGUF token_embd, kept exact
+__global__ __launch_bounds__(256) void embed_f32_kernel(const int32_t* __restrict__ ids, const float* __restrict__ emb,
+                                                        float* __restrict__ out, int H, int V) {
+  const int t = blockIdx.y;
+  const int id = ids[t];
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= H) return;
+  out[(size_t)t * H + c] = (id >= 0 && id < V) ? emb[(size_t)id * H + c] : 0.f;
+}
+
 // out = (x / sqrt(mean(x^2) + eps)) * w, one workgroup per row
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       float* __restrict__ out, int H, float eps) {
@@ -414,6 +424,15 @@ extern "C" int miq_embed(const int32_t* ids, const void* embed, float* out, int 
   hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256, T), dim3(256), 0, static_cast<hipStream_t>(stream), ids,
                      static_cast<const __half*>(embed), out, H, V);
   return check_launch("embed");
+}
+
+extern "C" int miq_embed_f32(const int32_t* ids, const float* embed, float* out, int T, int H, int V, void* stream) {
+  MIQ_REQUIRE(T >= 0 && H > 0 && V > 0, MIQ_ERR_INVALID, "embed_f32: T=%d H=%d V=%d", T, H, V);
+  if (T == 0) return MIQ_OK;
+  MIQ_REQUIRE(ids && embed && out, MIQ_ERR_INVALID, "embed_f32: null pointer");
+  hipLaunchKernelGGL(embed_f32_kernel, dim3((H + 255) / 256, T), dim3(256), 0, static_cast<hipStream_t>(stream), ids,
+                     embed, out, H, V);
+  return check_launch("embed_f32");
 }
 
 extern "C" int miq_rmsnorm(const float* x, const float* w, float* out, int T, int H, float eps, void* stream) {

@@ -87,6 +87,42 @@ class _Lin:
         self.zoff = float(d.get("zoff", 1.0) if zoff is None else zoff)
 
 
+def _lin_n(lin):
+    return int(lin.Nt) if isinstance(lin, core.GGMLLinear) else int(lin.N)
+
+
+class _Group:
+    """Linears that share their input and fill consecutive column ranges of one output: the
+    q|k|v (or gate|up) of a GGUF layer whose tensors use different block types, so that their
+    bytes cannot be concatenated into one matrix."""
+
+    def __init__(self, parts):
+        self.parts = parts
+        self.N = sum(_lin_n(q) for q in parts)
+        self.bias = None
+
+
+def _fuse(parts, K, gs, bits):
+    """One layer for projections that share K: GPTQ dicts concatenated along the output
+    dimension; GGUF layers of one block type likewise (their rows are whole blocks); a mix as a
+    _Group."""
+    if all(isinstance(q, dict) for q in parts):
+        return _Lin(_cat_layers(parts, gs, bits), K, gs, bits)
+    lins = [q if isinstance(q, core.GGMLLinear) else _Lin(q, K, gs, bits) for q in parts]
+    if all(isinstance(q, core.GGMLLinear) for q in lins) and len({q.type_name for q in lins}) == 1:
+        N = sum(q.Nt for q in lins)
+        bias = None
+        if any(q.bias is not None for q in lins):
+            bias = torch.cat([q.bias if q.bias is not None else torch.zeros(q.Nt, device=core.device())
+                              for q in lins])
+        return core.GGMLLinear(torch.cat([q.packed for q in lins]), lins[0].type_name, K, N, bias)
+    return _Group(lins)
+
+
+def _mk_lin(d, K, gs, bits):
+    return d if isinstance(d, core.GGMLLinear) else _Lin(d, K, gs, bits)
+
+
 class CausalLM:
     """Qwen2-shaped GPTQ decoder with device-resident decode (see module docstring).
 
@@ -111,31 +147,46 @@ class CausalLM:
         vec = lambda v: None if v is None else core.to_device(v if isinstance(v, torch.Tensor) else  # noqa: E731
                                                               np.asarray(v, np.float32), torch.float32)
         for lay in weights["layers"]:
-            d = {"qkv": _Lin(_cat_layers([lay["q"], lay["k"], lay["v"]], self.gs, self.bits), self.H, self.gs, self.bits),
-                 "o": _Lin(lay["o"], self.NH * self.HD, self.gs, self.bits),
+            d = {"qkv": _fuse([lay["q"], lay["k"], lay["v"]], self.H, self.gs, self.bits),
+                 "o": _mk_lin(lay["o"], self.NH * self.HD, self.gs, self.bits),
                  "in_ln": vec(lay["in_ln"]), "post_ln": vec(lay["post_ln"]),
                  "qn": vec(lay.get("qn")), "kn": vec(lay.get("kn"))}
             mo = lay.get("moe")
             if mo:  # sparse MoE MLP (`CausalLM._mlp` -> `moe_mlp`, `webtorch/llm.py:1489-1496`)
                 lin = lambda e: _gptq_dict(e, self.gs, self.bits)  # noqa: E731
-                d["moe"] = {"router": _Lin(mo["router"], self.H, self.gs, self.bits),
+                d["moe"] = {"router": _mk_lin(mo["router"], self.H, self.gs, self.bits),
                             "experts": core.MoEExperts([{k: lin(e[k]) for k in ("gate", "up", "down")}
                                                         for e in mo["experts"]]),
                             "top_k": int(mo["top_k"]),
                             "shared": core.SharedExpert({k: lin(mo["shared"][k]) for k in ("gate", "up", "down")},
                                                         mo.get("shared_gate")) if mo.get("shared") else None}
             else:
-                d["gate_up"] = _Lin(_cat_layers([lay["gate"], lay["up"]], self.gs, self.bits), self.H, self.gs, self.bits)
-                d["down"] = _Lin(lay["down"], self.I, self.gs, self.bits)
+                d["gate_up"] = _fuse([lay["gate"], lay["up"]], self.H, self.gs, self.bits)
+                d["down"] = _mk_lin(lay["down"], self.I, self.gs, self.bits)
             self.layers.append(d)
         self.has_moe = any("moe" in lay for lay in self.layers)
         self.has_qk_norm = any(lay["qn"] is not None or lay["kn"] is not None for lay in self.layers)
-        self.embed = core.to_device(np.asarray(weights["embed"], np.float16))
-        self.final_norm = core.to_device(np.asarray(weights["final_norm"], np.float32))
-        head = weights.get("head")
-        if head is not None and tuple(np.shape(head)) != (self.V, self.H):
-            raise ValueError("head must be (V, H) = (%d, %d), got %s" % (self.V, self.H, np.shape(head)))
-        self.head = self._quantize_head(None if head is None else core.to_device(np.asarray(head, np.float16)))
+        emb = weights["embed"]
+        if isinstance(emb, torch.Tensor) and emb.dtype == torch.float32:
+            self.embed = core.to_device(emb)  # a GGUF token_embd decoded to exact fp32
+        else:
+            self.embed = core.to_device(np.asarray(emb, np.float16))
+        self.final_norm = core.to_device(weights["final_norm"], torch.float32) if isinstance(
+            weights["final_norm"], torch.Tensor) else core.to_device(np.asarray(weights["final_norm"], np.float32))
+        if weights.get("head_linear") is not None:  # a GGUF head: native, or already quantized
+            self.head = _mk_lin(weights["head_linear"], self.H, self.gs, self.bits)
+        else:
+            head = weights.get("head")
+            if head is not None and tuple(np.shape(head)) != (self.V, self.H):
+                raise ValueError("head must be (V, H) = (%d, %d), got %s" % (self.V, self.H, np.shape(head)))
+            self.head = self._quantize_head(None if head is None else core.to_device(np.asarray(head, np.float16)))
+        # layers kept in a GGUF block encoding run the unfused launch sequence (the fused and
+        # persistent one-token kernels read GPTQ tensors)
+        lins = [self.head] + [lay[k] for lay in self.layers for k in ("qkv", "o", "gate_up", "down") if k in lay]
+        lins += [lay["moe"]["router"] for lay in self.layers if "moe" in lay]
+        self.native_gguf = any(not isinstance(q, _Lin) for q in lins)
+        if self.native_gguf:
+            self.fused = False
         self._alloc()
         self._graph = None
 
@@ -167,6 +218,19 @@ class CausalLM:
         c = w["cfg"]
         return cls(w, checkpoint.auto_lmax(lmax, declared, c["L"], c["NKV"], c["HD"]), fused, persistent)
 
+    @classmethod
+    def from_gguf(cls, path, lmax=None, bits=None, weights="native", persistent=None):
+        """Load a llama.cpp GGUF decoder (`CausalLM.from_gguf`, `webtorch/llm.py:856-1129`).
+        `weights="native"` (the default) keeps every weight whose block type has a kernel here
+        in the file's own encoding and runs the unfused launch sequence; "requant" decodes each
+        weight on the device and quantizes it to int`bits` (the file's own width when None),
+        which runs the fused GPTQ path. `lmax=None` takes the context length the file declares,
+        capped by the KV-cache budget."""
+        from . import checkpoint
+        w, declared = checkpoint.gguf_weights(path, bits, weights)
+        c = w["cfg"]
+        return cls(w, checkpoint.auto_lmax(lmax, declared, c["L"], c["NKV"], c["HD"]), True, persistent)
+
     # ---- load-time ----
     def _quantize_head(self, head=None):
         """The head (the fp16 embedding when tied, else the model's fp16 (V, H) head) quantized
@@ -185,7 +249,7 @@ class CausalLM:
         if not all("moe" in lay for lay in self.layers):
             self.buf.update(gu=z(T, 2 * self.I), act=z(T, self.I))
         if self.has_moe:
-            E = max(int(lay["moe"]["router"].N) for lay in self.layers if "moe" in lay)
+            E = max(_lin_n(lay["moe"]["router"]) for lay in self.layers if "moe" in lay)
             self.buf["rlog"] = z(T, E)
         self.kc = torch.zeros((self.L, self.NKV, self.lmax, self.HD), dtype=f32, device=dev)
         self.vc = torch.zeros_like(self.kc)
@@ -199,14 +263,18 @@ class CausalLM:
         self.state = torch.zeros(_lib.lib().miq_decode_state_words(), dtype=torch.int32, device=dev)
         # one split-K workspace sized for every projection at T = 1 and at the largest prefill
         # (the need is not monotonic in the row count: wide enough layers stop splitting K)
-        need = core.gemv_workspace_bytes(1, self.head.K, self.head.N, self.gs, self.bits, _lib.MIQ_F32)
+        need = 0
+        if isinstance(self.head, _Lin):
+            need = core.gemv_workspace_bytes(1, self.head.K, self.head.N, self.gs, self.bits, _lib.MIQ_F32)
         lins = {}
         for lay in self.layers:
             for k in ("qkv", "o", "gate_up", "down"):
                 if k in lay:
-                    lins[k] = lay[k]
+                    for i, q in enumerate(lay[k].parts if isinstance(lay[k], _Group) else [lay[k]]):
+                        lins[(k, i)] = q
             if "moe" in lay:
                 lins["router"] = lay["moe"]["router"]
+        lins = {k: q for k, q in lins.items() if isinstance(q, _Lin)}  # GGUF kernels need no workspace
         for M in range(1, T + 1):  # the head only ever sees the last token
             for lin in lins.values():
                 need = max(need, core.gemv_workspace_bytes(M, lin.K, lin.N, lin.gs, lin.bits, _lib.MIQ_F32))
@@ -264,8 +332,33 @@ class CausalLM:
 
     # ---- one forward over T tokens at the device position ----
     def _linear(self, lin, x, out, bias=None):
-        core._gptq_matmul(x, lin.qweight, lin.qzeros, lin.scales, lin.K, lin.N, lin.gs, lin.bits, lin.zoff,
-                          bias=lin.bias if bias is None else bias, out=out, ws=self.ws)
+        if isinstance(lin, core.GGMLLinear):
+            core.ggml_matmul(x, lin.packed, lin.type_name, lin.Kt, lin.Nt, bias=lin.bias if bias is None else bias,
+                             out=out)
+        elif isinstance(lin, _Group):
+            # part outputs land in column ranges: directly for one row (the range is contiguous),
+            # through a temporary for more
+            c0, M = 0, int(x.shape[0])
+            for part in lin.parts:
+                n = _lin_n(part)
+                if M == 1:
+                    self._linear(part, x, out[:, c0:c0 + n])
+                else:
+                    tmp = torch.empty((M, n), dtype=out.dtype, device=out.device)
+                    self._linear(part, x, tmp)
+                    out[:, c0:c0 + n].copy_(tmp)
+                c0 += n
+        else:
+            core._gptq_matmul(x, lin.qweight, lin.qzeros, lin.scales, lin.K, lin.N, lin.gs, lin.bits, lin.zoff,
+                              bias=lin.bias if bias is None else bias, out=out, ws=self.ws)
+
+    def _embed(self, T):
+        if self.embed.dtype == torch.float32:
+            _lib.call("miq_embed_f32", ptr(self.ids), ptr(self.embed), ptr(self.buf["h"]), T, self.H, self.V,
+                      stream_handle())
+        else:
+            _lib.call("miq_embed", ptr(self.ids), ptr(self.embed), ptr(self.buf["h"]), T, self.H, self.V,
+                      stream_handle())
 
     def _fused(self, lin, x, mode, norm_w, out, bias=None):
         """One-token GEMV with RMSNorm (mode 1) or SwiGLU (mode 2) applied to x while staging."""
@@ -289,7 +382,7 @@ class CausalLM:
                       float(self.head.zoff), st)
             return
         h = b["h"][:1]
-        _lib.call("miq_embed", ptr(self.ids), ptr(self.embed), ptr(h), 1, self.H, self.V, st)
+        self._embed(1)
         scale = 1.0 / math.sqrt(self.HD)
         for i, lay in enumerate(self.layers):
             self._fused(lay["qkv"], h, _lib.MIQ_X_RMSNORM, lay["in_ln"], b["qkv"])
@@ -314,7 +407,7 @@ class CausalLM:
         b, st = self.buf, stream_handle()
         H, NH, NKV, HD, I = self.H, self.NH, self.NKV, self.HD, self.I
         h, xn = b["h"][:T], b["xn"][:T]
-        _lib.call("miq_embed", ptr(self.ids), ptr(self.embed), ptr(h), T, H, self.V, st)
+        self._embed(T)
         scale = 1.0 / math.sqrt(HD)
         for i, lay in enumerate(self.layers):
             _lib.call("miq_rmsnorm", ptr(h), ptr(lay["in_ln"]), ptr(xn), T, H, self.eps, st)
@@ -355,7 +448,7 @@ class CausalLM:
         mo = lay["moe"]
         xn = b["xn"][:T]
         _lib.call("miq_rmsnorm", ptr(h), ptr(lay["post_ln"]), ptr(xn), T, self.H, self.eps, st)
-        E = mo["router"].N
+        E = _lin_n(mo["router"])
         logits = b["rlog"][:T, :E] if b["rlog"].shape[1] == E else b["rlog"].view(-1)[:T * E].view(T, E)
         self._linear(mo["router"], xn, logits)
         out = mo["experts"](xn, logits, mo["top_k"], True)
