@@ -184,6 +184,18 @@ int miq_q4k_dequant_f32(const uint8_t* blocks, float* out, int64_t n_blocks, voi
 int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out,
                  int out_dtype, int M, int K, int N, void* stream);
 
+/* out[M][N] = x[M][K] @ W^T + bias on the matrix cores, for prefill rows: W = N rows of K/256
+ * native Q4_K super-blocks (K <= 16384), x fp16 or fp32 (fp32 as row-scaled fp16 hi/lo row
+ * pairs), each 32-weight sub-block applied exactly as d1 (sum x c) - m1 (sum x). The workspace
+ * (miq_q4k_gemm_workspace bytes, 256-byte aligned) holds the staged rows and the fp32 result
+ * after its first 4 MiB, which it leaves alone (the split-K counter region), so the GEMV's
+ * workspace can be shared. Results are deterministic.
+ * Replaces: `ggml_matmul` / `_ggml_run` with the batched kernel `_GGML_GEMM_*` + `_Q4K_DEC`
+ * (webtorch/_core.py:2908-2975, 3117-3133, 3720-3779). */
+int miq_q4k_gemm_workspace(int M, int K, int N, int x_dtype, size_t* bytes);
+int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out, int out_dtype,
+                 int M, int K, int N, void* workspace, size_t ws_bytes, void* stream);
+
 /* out[M][N] = x[M][K] @ W^T + bias for the native GGUF block types beside Q4_K, by ggml type id:
  * 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 20 IQ4_NL (32 weights per block: 18, 20, 22, 24, 34,
  * 18 bytes) and 10 Q2_K, 11 Q3_K, 13 Q5_K, 14 Q6_K, 23 IQ4_XS (256 per super-block: 84, 110, 176,

@@ -230,3 +230,48 @@ def test_new_type_prefill_rows(gpu, type_name):
     ref = ggml.ggml_matmul(x, W, type_name, K, N)
     assert _rel(got, ref) < 1e-5
     assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+
+
+# ---- Q4_K prefill rows on the matrix cores ------------------------------------------------
+
+@pytest.mark.parametrize("M,K,N", [(9, 256, 64), (100, 768, 70), (64, 4096, 14336), (300, 2048, 512)])
+@pytest.mark.parametrize("xdt", [np.float32, np.float16])
+def test_q4k_gemm_prefill_rows(gpu, M, K, N, xdt):
+    """Rows above the GEMV's take the matrix-core GEMM (exact sub-block decomposition); against
+    the oracle's dequant times x at row-tile and column-tile tails, with bias and fp16 output."""
+    import torch
+    from webpytorch_amd import core
+    W = synth.q4k_layer(M + K, K, N)
+    b = np.linspace(-1, 1, N).astype(np.float32)
+    lin = core.GGMLLinear(W, "Q4_K", K, N, bias=b)
+    x = synth.activations(M, M, K, xdt)
+    ref = q4k.q4k_matmul(x.astype(np.float32), W, K, N) + b
+    got = lin(torch.from_numpy(x)).cpu().numpy()
+    assert _rel(got, ref) < 1e-5
+    assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+    got16 = lin.forward(torch.from_numpy(x), out_dtype=torch.float16).cpu().numpy()
+    assert np.all(np.abs(got16.astype(np.float32) - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+    assert np.array_equal(lin(torch.from_numpy(x)).cpu().numpy(), got)  # deterministic
+
+
+def test_q4k_gemm_row_scales_and_nonfinite(gpu):
+    """fp32 rows of very different magnitude keep their relative accuracy (each row is split
+    at its own scale); a row holding NaN gives NaN and an Inf row gives non-finite outputs,
+    while the other rows are unaffected."""
+    import torch
+    from webpytorch_amd import core
+    K, N, M = 1024, 192, 24
+    W = synth.q4k_layer(5, K, N)
+    lin = core.GGMLLinear(W, "Q4_K", K, N)
+    x = synth.activations(5, M, K, np.float32)
+    x *= np.logspace(-6, 6, M, dtype=np.float32)[:, None]
+    ref = q4k.q4k_matmul(x, W, K, N)
+    got = lin(torch.from_numpy(x)).cpu().numpy()
+    for m in range(M):
+        assert np.abs(got[m] - ref[m]).max() <= 1e-5 * np.abs(ref[m]).max(), m
+    x[3, 7] = np.nan
+    x[5, 9] = np.inf
+    got = lin(torch.from_numpy(x)).cpu().numpy()
+    assert np.isnan(got[3]).all() and not np.isfinite(got[5]).any()
+    keep = [m for m in range(M) if m not in (3, 5)]
+    assert np.abs(got[keep] - ref[keep]).max() <= 1e-5 * np.abs(ref[keep]).max()

@@ -437,9 +437,23 @@ def rows_from_transposed(words, n, rowb):
     return rows[:, :rowb].contiguous()
 
 
+# Q4_K rows above this count go to the matrix-core GEMM (the other types stay on the GEMV)
+GGML_GEMV_MAX_M = 8
+
+
+def q4k_gemm_workspace_bytes(M, K, N, x_dtype):
+    key = ("q4kgemm", M, K, N, x_dtype)
+    b = _WS_BYTES.get(key)
+    if b is None:
+        n = ctypes.c_size_t(0)
+        _lib.call("miq_q4k_gemm_workspace", M, K, N, x_dtype, ctypes.byref(n))
+        b = _WS_BYTES[key] = int(n.value)
+    return b
+
+
 def _ggml_selfcheck(type_name, mode):
-    """Multiply two random blocks of `type_name` with the kernel of `mode` (rows 1, 2, or 0 for
-    3 and more) and compare against the device's exact dequant of the same bytes times x in
+    """Multiply two random blocks of `type_name` with the kernel of `mode` (rows 1, 2, 0 for 3
+    to GGML_GEMV_MAX_M, -1 for the matrix-core GEMM) and compare against the device's exact dequant of the same bytes times x in
     float64; RuntimeError on a mismatch (`_ggml_selfcheck`, `webtorch/_core.py:3684-3717`).
     Code and sub-scale bytes are uniform random (every byte pattern is a legal block); the fp16
     scale fields are drawn small and finite, where the reference redraws until they are."""
@@ -448,10 +462,10 @@ def _ggml_selfcheck(type_name, mode):
     raw = torch.from_numpy(synth.ggml_layer(type_name, 0, vals, 2, scale=0.01)).to(device())
     W = ggml_dequant(raw.reshape(-1), type_name, 2).reshape(2, vals)
     g = np.random.default_rng(vals)
-    M = mode if mode else 3
+    M = {0: 3, -1: 2 * GGML_GEMV_MAX_M + 1}.get(mode, mode)
     x = torch.from_numpy(g.standard_normal((M, vals)).astype(np.float32)).to(device())
     got = ggml_matmul(x, raw, type_name, vals, 2, _check=False)
-    _check_close("the native ggml %s kernel for %s" % ("gemv" if mode else "gemm", type_name), got,
+    _check_close("the native ggml %s kernel for %s" % ("gemm" if mode < 0 else "gemv", type_name), got,
                  _reference_product(x, W.t()))
 
 
@@ -478,12 +492,18 @@ def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32,
                                                                            int(N) * rowb))
     xf = aligned16(as_activation(xf).contiguous())
     M = int(xf.shape[0])
-    mode = M if M <= 2 else 0
+    gemm = type_name == "Q4_K" and M > GGML_GEMV_MAX_M
+    mode = -1 if gemm else (M if M <= 2 else 0)
     if _check and M and _first_use(("ggml", type_name, mode)):
         _ggml_selfcheck(type_name, mode)
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=xf.device)
-    if type_name == "Q4_K":
+    if gemm:  # prefill rows on the matrix cores
+        need = q4k_gemm_workspace_bytes(M, int(K), int(N), dtype_code(xf))
+        ws = workspace(need)
+        _lib.call("miq_q4k_gemm", ptr(xf), dtype_code(xf), ptr(packed), ptr(bias), ptr(out), dtype_code(out), M,
+                  int(K), int(N), ptr(ws), ws.numel(), stream_handle())
+    elif type_name == "Q4_K":
         _lib.call("miq_q4k_gemv", ptr(xf), dtype_code(xf), ptr(packed), ptr(bias), ptr(out), dtype_code(out),
                   M, int(K), int(N), stream_handle())
     else:
