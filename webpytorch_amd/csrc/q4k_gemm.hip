@@ -4,12 +4,10 @@
 // A Q4_K sub-block of 32 weights holds w = d1 c - m1 (d1 = d sc and m1 = dmin m: an fp16 scale
 // times a 6-bit integer, exact in fp32; c the 4-bit code). Per sub-block
 //   sum_k x_k w_k = d1 (sum_k x_k c_k) - m1 (sum_k x_k),
-// and one v_mfma_f32_16x16x32_f16 gives the first sum for a 16 x 16 output tile exactly (an
-// fp16 x times a code below 16 is exact; the matrix core accumulates in fp32). The codes become
-// fp16 B operands by OR-ing them into the mantissa of 1024.0 and subtracting 1024: no
-// conversion instruction per code. The row sums of x come precomputed per sub-block. Each MFMA
-// starts from zero, and its 16 x 16 result is folded into the fp32 accumulators with the
-// column's d1 and m1: two FMAs per output per 32 weights.
+// with d1 = d sc, m1 = dmin m. The codes become fp16 B operands by OR-ing them into the
+// mantissa of 1024.0 and subtracting 1024 (no conversion instruction per code), times sc; the
+// row sums of x come precomputed per sub-block. The matrix cores do both sums (see gemm_kernel)
+// and the accumulators take d and dmin once per super-block of 256 weights.
 //
 // fp32 activations enter as two fp16 rows each, hi = fp16(x 2^s) and lo = fp16(x 2^s - hi),
 // with 2^s per row putting the row's largest |x| near 2^15 (s = 0 for rows holding NaN or Inf);
@@ -23,11 +21,10 @@
 //
 // Tiles: a workgroup of 4 waves computes 64 rows x 64 columns; wave w takes columns 16 w .. +15
 // and all 64 rows (four 16-row MFMA tiles). K is walked one super-block (256 weights) at a
-// time: the workgroup copies the 64 x 256 activation tile into LDS (16-byte chunks XOR-swizzled
-// by row, so the 16 rows that one operand read touches fall in different banks) while each lane
-// holds its column's super-block header and its 4 x 8 code bytes in registers, both loaded one
-// super-block ahead. Workgroups are ordered XCD-major with row tiles fastest, so the row tiles of
-// a column tile share that XCD's L2.
+// time: the 64 x 256 activation tile sits in LDS (16-byte chunks XOR-swizzled by row, so the 16
+// rows that one operand read touches fall in different banks) and each lane holds its column's
+// super-block header and its 4 x 8 code bytes in registers. Workgroups are ordered XCD-major
+// with row tiles fastest, so the row tiles of a column tile share that XCD's L2.
 #include <math.h>
 
 #include <type_traits>
@@ -155,81 +152,100 @@ __device__ __forceinline__ half8v b_codes(uint32_t w0, uint32_t w1) {
 }
 
 // y[r][n] for rows r < Mx of xs. Grid (ntiles * mtiles), 256 threads.
+//
+// Per super-block: P = sum_sb sc_sb (sum_k x_k c_k) on the fp16 matrix cores (the B operand is
+// sc c, an integer below 1024, exact in fp16, so the eight sub-blocks chain in the MFMA
+// accumulator), Q = sum_sb m_sb rs_sb on the fp32 matrix cores (two v_mfma_f32_16x16x4_f32:
+// A the row sums, B the column's 6-bit mins), then acc += d P - dmin Q. The activation tile and
+// the row sums arrive by LDS DMA into one of two buffers while the other is multiplied (the
+// swizzle is applied on the source side: DMA lane l of a 1 KB block lands at slot l); each
+// lane's super-block header and code bytes are loaded into registers one super-block ahead.
 __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs, const float* __restrict__ rs,
                                                    const uint8_t* __restrict__ w, float* __restrict__ y, int Mx, int K,
                                                    int N, int mtiles) {
-  __shared__ __align__(16) __half at[kBM * 256];  // the activation tile, 16-byte chunks swizzled by row
-  __shared__ __align__(16) float rt[8 * kBM];     // sub-block sums [sub-block][row]
+  __shared__ __align__(16) __half at[2][kBM * 256];  // activation tiles, 16-byte chunks swizzled by row
+  __shared__ __align__(16) float rt[2][8 * kBM];     // sub-block sums [sub-block][row]
   const int T = (int)gridDim.x, L = (int)blockIdx.x;
   const int Lp = T % kXCDs == 0 ? (L % kXCDs) * (T / kXCDs) + L / kXCDs : L;
   const int mt = Lp % mtiles, nt = Lp / mtiles;
   const int m0 = mt * kBM, n0 = nt * kBN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, p = lane & 15, kb = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6), p = lane & 15, kb = lane >> 4;
   const int ncol = n0 + 16 * wave + p;
   const int n = min(ncol, N - 1);  // columns past N repeat the last one and are not stored
   const int nsb = K / 256, K32 = K / 32;
   const uint8_t* wr = w + (size_t)n * nsb * 144;
 
+  // this wave's share of the copies of super-block s into buffer b: 8 of the tile's 32 KB
+  // (two rows per 1 KB block) and 2 of its 8 sub-block-sum columns
+  auto issue = [&](int s, int b) __attribute__((always_inline)) {
+    const uint32_t abase = lds_addr(at[b]), rbase = lds_addr(rt[b]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = wave * 8 + i, r = 2 * j + (lane >> 5), c = (lane & 31) ^ (r & 31);
+      dma16(xs + (size_t)min(m0 + r, Mx - 1) * K + s * 256 + c * 8, uniform((int)(abase + j * 1024)));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int sb = wave * 2 + i;
+      dma4(rs + (size_t)min(m0 + lane, Mx - 1) * K32 + s * 8 + sb, uniform((int)(rbase + sb * 256)));
+    }
+  };
   uint4 hdr, hdr_n;
   uint2 cw[4], cw_n[4];
-  uint4 av[8];
-  float rv[2];
-  auto load = [&](int s) __attribute__((always_inline)) {
-    const uint8_t* b = wr + (size_t)s * 144;
-    hdr_n = *reinterpret_cast<const uint4*>(b);
+  auto load_b = [&](int s) __attribute__((always_inline)) {
+    const uint8_t* bp = wr + (size_t)s * 144;
+    hdr_n = *reinterpret_cast<const uint4*>(bp);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) cw_n[g] = *reinterpret_cast<const uint2*>(b + 16 + 32 * g + 8 * kb);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int q = tid + 256 * j, row = q >> 5, ch = q & 31;
-      av[j] = *reinterpret_cast<const uint4*>(xs + (size_t)min(m0 + row, Mx - 1) * K + s * 256 + ch * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int row = tid & 63, sb = (tid >> 6) + 4 * j;
-      rv[j] = rs[(size_t)min(m0 + row, Mx - 1) * K32 + s * 8 + sb];
-    }
+    for (int g = 0; g < 4; ++g) cw_n[g] = *reinterpret_cast<const uint2*>(bp + 16 + 32 * g + 8 * kb);
   };
 
   float4v acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = (float4v){0.f, 0.f, 0.f, 0.f};
-  load(0);
+  issue(0, 0);
+  load_b(0);
   for (int s = 0; s < nsb; ++s) {
-    __syncthreads();  // every wave is done with the previous tile
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int q = tid + 256 * j, row = q >> 5, ch = q & 31;
-      *reinterpret_cast<uint4*>(at + row * 256 + ((ch ^ (row & 31)) * 8)) = av[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) rt[((tid >> 6) + 4 * j) * kBM + (tid & 63)] = rv[j];
+    wait_vmcnt<0>();  // this wave's copies of super-block s (and its header and codes) have landed
+    __syncthreads();  // everyone's copies are in; everyone is done with the other buffer
+    if (s + 1 < nsb) issue(s + 1, (s + 1) & 1);
     hdr = hdr_n;
 #pragma unroll
     for (int g = 0; g < 4; ++g) cw[g] = cw_n[g];
-    if (s + 1 < nsb) load(s + 1);  // in flight while this super-block is multiplied
-    __syncthreads();
-    const float d = __half2float(__ushort_as_half((unsigned short)(hdr.x & 0xFFFFu)));
-    const float dmin = __half2float(__ushort_as_half((unsigned short)(hdr.x >> 16)));
+    if (s + 1 < nsb) load_b(s + 1);
+    const __half* a = at[s & 1];
+    const float* r8 = rt[s & 1];
+    float4v P[4], Q[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) P[t] = Q[t] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
       uint32_t sc, mn;
       scale_min(hdr.y, hdr.z, hdr.w, sb, &sc, &mn);
-      const float d1 = d * (float)sc, m1 = dmin * (float)mn;
       const int sh = 4 * (sb & 1);
-      const half8v bf = b_codes(cw[sb >> 1].x >> sh, cw[sb >> 1].y >> sh);
+      const half8v bf = b_codes(cw[sb >> 1].x >> sh, cw[sb >> 1].y >> sh) * (_Float16)(float)sc;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int r = 16 * t + p;
-        const half8v af = *reinterpret_cast<const half8v*>(at + r * 256 + (((4 * sb + kb) ^ (r & 31)) * 8));
-        const float4v part = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        const float4 xs4 = *reinterpret_cast<const float4*>(rt + sb * kBM + 16 * t + 4 * kb);
-        acc[t][0] = fmaf(-m1, xs4.x, fmaf(d1, part[0], acc[t][0]));
-        acc[t][1] = fmaf(-m1, xs4.y, fmaf(d1, part[1], acc[t][1]));
-        acc[t][2] = fmaf(-m1, xs4.z, fmaf(d1, part[2], acc[t][2]));
-        acc[t][3] = fmaf(-m1, xs4.w, fmaf(d1, part[3], acc[t][3]));
+        const half8v af = *reinterpret_cast<const half8v*>(a + r * 256 + (((4 * sb + kb) ^ (r & 31)) * 8));
+        P[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, P[t], 0, 0, 0);
       }
     }
+    {  // Q = sum over the 8 sub-blocks of rs[row][sb] m[sb][col]: k = kb, then 4 + kb
+      uint32_t sc, m_lo, m_hi;
+      scale_min(hdr.y, hdr.z, hdr.w, kb, &sc, &m_lo);
+      scale_min(hdr.y, hdr.z, hdr.w, 4 + kb, &sc, &m_hi);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[kb * kBM + 16 * t + p], (float)m_lo, Q[t], 0, 0, 0);
+        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[(4 + kb) * kBM + 16 * t + p], (float)m_hi, Q[t], 0, 0, 0);
+      }
+    }
+    const float d = __half2float(__ushort_as_half((unsigned short)(hdr.x & 0xFFFFu)));
+    const float dmin = __half2float(__ushort_as_half((unsigned short)(hdr.x >> 16)));
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[t][q] = fmaf(d, P[t][q], fmaf(-dmin, Q[t][q], acc[t][q]));
   }
   if (ncol >= N) return;
 #pragma unroll
