@@ -170,6 +170,19 @@ def gemm_bench(torch, core, Ms=(16, 128, 512), copies=32, reps=32):
                           "mfma_frac": round(flops / t / 1e12 / MFMA_PEAK_TFLOPS, 4),
                           "GBs": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
         del g
+        # the vendor library's dense fp16 GEMM of the same shape (torch.matmul -> hipBLASLt), over
+        # 8 distinct fp16 weight copies, as a reference point for the matrix-core fraction
+        wd = [torch.randn((K, N), device="cuda").half() for _ in range(8)]
+
+        def dense(x=x, wd=wd):
+            for i in range(reps):
+                torch.matmul(x, wd[i % 8])
+        dense()
+        torch.cuda.synchronize()
+        td = timed(torch, dense, 3) / reps
+        res["M%d" % M]["dense_fp16_library_us"] = round(td * 1e6, 3)
+        res["M%d" % M]["dense_fp16_library_mfma_frac"] = round(flops / td / 1e12 / MFMA_PEAK_TFLOPS, 4)
+        del wd
     return res
 
 
@@ -245,6 +258,63 @@ def decode_full(torch, m, ids, max_new=128):
     r = m.generate(ids, max_new)
     return {"tokens": max_new, "ttft_ms": round(r.ttft_s * 1e3, 3), "decode_tokens_per_s": round(r.decode_tok_s, 1),
             "ms_per_token": round(1e3 / r.decode_tok_s, 4) if r.decode_tok_s else None}
+
+
+QWEN25_7B = dict(L=28, H=3584, NH=28, NKV=4, HD=128, I=18944, V=152064)
+
+
+def device_decoder(torch, L, H, NH, NKV, HD, I, V, gs=GS, seed=7):
+    """Random-init int4 GPTQ decoder of the given shape built directly in device memory (uniform
+    codes and zeros, small fp16 scales so that the residual stream stays finite over the
+    layers, fp16 q/k/v biases, fp32 embedding; the head is tied and quantized on load)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+
+    def lin(K, N, bias=False):
+        d = {"qweight": torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), dtype=torch.int32, device="cuda", generator=g),
+             "qzeros": torch.randint(-2 ** 31, 2 ** 31 - 1, (K // gs, N // 8), dtype=torch.int32, device="cuda",
+                                     generator=g),
+             "scales": (torch.rand((K // gs, N), device="cuda", generator=g) * 0.002 + 0.0005).half()}
+        if bias:
+            d["bias"] = (torch.randn(N, device="cuda", generator=g) * 0.02).half()
+        return d
+
+    def vec(n):
+        return (1.0 + 0.02 * torch.randn(n, device="cuda", generator=g)).float()
+
+    layers = [{"q": lin(H, NH * HD, True), "k": lin(H, NKV * HD, True), "v": lin(H, NKV * HD, True),
+               "o": lin(NH * HD, H), "gate": lin(H, I), "up": lin(H, I), "down": lin(I, H),
+               "in_ln": vec(H), "post_ln": vec(H)} for _ in range(L)]
+    embed = torch.randn((V, H), device="cuda", generator=g) * 0.02
+    cfg = dict(L=L, H=H, NH=NH, NKV=NKV, HD=HD, I=I, V=V, gs=gs, bits=4)
+    return {"layers": layers, "embed": embed, "final_norm": vec(H), "cfg": cfg}
+
+
+def decode_7b(torch, llm, prompt=64, max_new=128):
+    """Greedy decode of a random-init Qwen2.5-7B-shaped int4 model (28 layers, hidden 3584,
+    28/4 heads of 128, intermediate 18944, vocab 152064; the shape of the reference's own
+    published capture-replay figure): a 64-token prompt and 128 tokens through the engine's
+    captured launch sequence (the persistent step covers hidden sizes up to 1024), timed on the
+    host around `generate` (second run). Reports the weight bytes streamed per token over the
+    decode time as GB/s."""
+    c = QWEN25_7B
+    w = device_decoder(torch, **c)
+    m = llm.CausalLM.from_weights(w, lmax=prompt + max_new + 2)
+    del w
+    ids = torch.randint(0, c["V"], (prompt,), generator=torch.Generator().manual_seed(7)).numpy()
+    m.generate(ids, max_new)
+    r = m.generate(ids, max_new)
+    finite = bool(torch.isfinite(m.buf["logits"]).all())
+    lb = [m.head] + [lay[k] for lay in m.layers for k in ("qkv", "o", "gate_up", "down")]
+    wbytes = sum(q.qweight.numel() * 4 + q.qzeros.numel() * 4 + q.scales.numel() * q.scales.element_size() +
+                 (q.bias.numel() * 4 if q.bias is not None else 0) for q in lb)
+    del m
+    torch.cuda.empty_cache()
+    return {"tokens": max_new, "ttft_ms": round(r.ttft_s * 1e3, 2), "decode_tokens_per_s": round(r.decode_tok_s, 1),
+            "ms_per_token": round(1e3 / r.decode_tok_s, 3), "weight_bytes_per_token": wbytes,
+            "weight_GBs": round(wbytes * r.decode_tok_s / 1e9, 1),
+            "hbm_frac": round(wbytes * r.decode_tok_s / 1e9 / HBM_PEAK_GBS, 4), "finite_logits": finite,
+            "path": "captured launch sequence"}
 
 
 def moe_bench(torch, core, reps=8):
@@ -521,7 +591,7 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the token's GEMVs alone and a plain 1 GiB copy, for hardware-counter runs")
     ap.add_argument("--gemv-large", action="store_true", help="only the GEMV operator on 7B-class shapes")
-    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "moe", "config0"],
+    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "moe", "config0", "decode7b"],
                     help="one kernel benchmark and a plain 1 GiB copy, for profiler runs")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the persistent decode step and a plain 1 GiB copy, for hardware-counter runs")
@@ -541,7 +611,7 @@ def main():
     if a.only:
         fn = {"gemm": lambda: gemm_bench(torch, core, Ms=(512,)), "gemm_int8": lambda: gemm_int8_bench(torch, core),
               "q4k": lambda: q4k_bench(torch, core), "moe": lambda: moe_bench(torch, core),
-              "config0": lambda: config0_bench(torch, core)}[a.only]
+              "config0": lambda: config0_bench(torch, core), "decode7b": lambda: decode_7b(torch, llm)}[a.only]
         out = {a.only: fn()}
         copy_bytes = copy_calibration(torch)
         out.update({"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes})
@@ -631,6 +701,7 @@ def main():
         res["gptq_gemm_act_order_4096"] = gemm_bench(torch, core)
         res["gptq_gemm_int8_per_channel_4096"] = gemm_int8_bench(torch, core)
         res["moe_qwen3_t256"] = moe_bench(torch, core)
+        res["decode_qwen25_7b_shape"] = decode_7b(torch, llm)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
     print(json.dumps(res), flush=True)

@@ -88,16 +88,19 @@ def test_attention_matches_oracle(gpu, pos, T):
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("pos,LMAX", [(0, 64), (5, 64), (37, 64), (255, 256), (37, 300), (290, 300)])
-def test_attention_decode_fused_rope_kv(gpu, pos, LMAX):
+@pytest.mark.parametrize("pos,LMAX,NH,NKV,HD", [(0, 64, 14, 2, 64), (5, 64, 14, 2, 64), (37, 64, 14, 2, 64),
+                                                (255, 256, 14, 2, 64), (37, 300, 14, 2, 64), (290, 300, 14, 2, 64),
+                                                (0, 64, 28, 4, 128), (63, 200, 28, 4, 128), (191, 200, 28, 4, 128),
+                                                (1000, 1030, 28, 4, 128), (2, 40, 8, 8, 128), (700, 800, 4, 1, 80)])
+def test_attention_decode_fused_rope_kv(gpu, pos, LMAX, NH, NKV, HD):
     """The one-token attention (RoPE + KV write + attention in one launch) against the oracle's
-    rope, cache append and attention; caches of up to 256 positions take the prefetching kernel,
-    longer ones the looping one."""
+    rope, cache append and attention: head dim 64 with caches of up to 256 positions takes the
+    prefetching kernel, head dims 64 and 128 otherwise the row-group kernel (Qwen2.5-7B's 28/4
+    heads of 128 among them), other head dims the looping one."""
     import torch
     from webpytorch_amd import _lib
     from webpytorch_amd.core import ptr
-    NH, NKV, HD = 14, 2, 64
-    o = decode.Qwen2Oracle(synth.decoder_weights(1, L=1, H=128, NH=2, NKV=1, HD=64, I=128, V=64, gs=64), lmax=LMAX)
+    o = decode.Qwen2Oracle(synth.decoder_weights(1, L=1, H=128, NH=2, NKV=1, HD=HD, I=128, V=64, gs=32), lmax=LMAX)
     rng = np.random.default_rng(pos)
     kc = rng.standard_normal((NKV, LMAX, HD)).astype(np.float32)
     vc = rng.standard_normal((NKV, LMAX, HD)).astype(np.float32)

@@ -146,6 +146,48 @@ def test_large_gemv_matrix_core_path(gpu, K, N, xdt, sdt, zoff, bias):
     assert np.array_equal(got, again)
 
 
+@pytest.mark.parametrize("mode,K,N,big", [(1, 3584, 4608, False), (1, 896, 9728, False), (2, 18944, 3584, False),
+                                         (2, 4864, 896, False), (1, 1024, 512, True), (2, 512, 768, True)])
+def test_fused_gemv_matrix_core_path(gpu, mode, K, N, big):
+    """One row through miq_gptq_gemv_fused on the matrix-core GEMV: RMSNorm (mode 1, the row's
+    mean square over all K in every workgroup, x * w staged, partials divided by r) and SwiGLU
+    (mode 2, silu(gate) * up staged) against the oracle's RMSNorm / SwiGLU followed by the numpy
+    dequant product; Qwen2.5-7B and Qwen2-0.5B projection shapes, an in-place residual (bias =
+    out), a row with values near 1e4, and repeat calls bit-identical."""
+    import torch
+    from webpytorch_amd import _lib, core
+    from webpytorch_amd.core import ptr
+    L = synth.gptq_layer(50 + K % 11, K, N, 128, 4)
+    rng = np.random.default_rng(K + N)
+    eps = 1e-6
+    if mode == 1:
+        x = rng.standard_normal(K).astype(np.float32) * (3e3 if big else 1.0)
+        w = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+        xn = (x / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps)).astype(np.float32) * w
+        xin = x
+    else:
+        g = rng.standard_normal(K).astype(np.float32) * (8.0 if big else 1.0)
+        u = rng.standard_normal(K).astype(np.float32)
+        xn = (g / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32) * u
+        xin = np.concatenate([g, u])
+        w = None
+    res = (rng.standard_normal(N) * 0.5).astype(np.float32)
+    ref = gptq.gptq_matmul_np(xn[None, :], L["qweight"], L["qzeros"], L["scales"], K, N, 128, 4, 1.0)[0] + res
+    xd = torch.from_numpy(xin).cuda()
+    wd = None if w is None else torch.from_numpy(w).cuda()
+    qw, qz, sc = core.to_device(L["qweight"]), core.to_device(L["qzeros"]), core.to_device(L["scales"])
+    ws = core.workspace(core.gemv_workspace_bytes(1, K, N, 128, 4, 0))
+    outs = []
+    for _ in range(2):
+        out = torch.from_numpy(res).cuda()
+        _lib.call("miq_gptq_gemv_fused", ptr(xd), mode, None if wd is None else ptr(wd), eps, None, ptr(qw), ptr(qz),
+                  ptr(sc), core.dtype_code(sc), ptr(out), ptr(out), 1, K, N, 128, 4, 1.0, ptr(ws), ws.numel(), None)
+        outs.append(out.cpu().numpy())
+    _close(outs[0], ref)
+    assert _rel(outs[0], ref) < 1e-5
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_int8_per_channel_gemv(gpu):
     import torch
     from webpytorch_amd import core

@@ -197,6 +197,124 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(
   for (int d = tid; d < HD; d += 256) out[(size_t)h * HD + d] = ((red[0][d] + red[1][d]) + red[2][d]) + red[3][d];
 }
 
+// The same for head dimensions 64 and 128 at any cache length, with the cache rows read by
+// whole groups of threads of a 1024-thread workgroup: a position's key row is HD / 4 adjacent
+// threads (one float4 each, the row's partial dot products summed across the group), so a pass
+// covers 4096 / HD positions with coalesced loads, four passes in flight; the weighted sum
+// likewise gives each thread a float4 of the head dimension and a residue of the position
+// modulo 4096 / HD, four positions in flight, the residues combined in order through LDS.
+constexpr int kAttRowThreads = 1024;
+template <int HD>
+__global__ __launch_bounds__(kAttRowThreads) void attention_decode_rows_kernel(
+    const float* __restrict__ qkv, const int32_t* __restrict__ state, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, float* __restrict__ kc, float* __restrict__ vc, float* __restrict__ out, int NH,
+    int NKV, int LMAX, float scale) {
+  constexpr int NT = kAttRowThreads, NW = NT / 64, TPP = HD / 4, PPP = NT / TPP, U = 4, HALF = HD / 2;
+  extern __shared__ float sp[];  // [LMAX] scores -> probabilities
+  __shared__ __align__(16) float qs[HD], kn[HD], vn[HD];
+  __shared__ __align__(16) float4 red[PPP][TPP];
+  __shared__ float wred[2 * NW];
+  const int h = blockIdx.x;
+  const int rep = NH / NKV, kv = h / rep;
+  const int pos = state[0];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (pos >= LMAX) return;  // uniform: the caller never runs past its cache
+  const int S = pos + 1;
+  if (tid < HD) {
+    const int d = tid, j = d < HALF ? d : d - HALF;
+    const float c = cos_t[(size_t)pos * HALF + j], s = sin_t[(size_t)pos * HALF + j];
+    qs[d] = rope1(qkv + h * HD, d, HALF, c, s);
+    kn[d] = rope1(qkv + (NH + kv) * HD, d, HALF, c, s);
+    vn[d] = qkv[(NH + NKV + kv) * HD + d];
+    if (h % rep == 0) {
+      kc[((size_t)kv * LMAX + pos) * HD + d] = kn[d];
+      vc[((size_t)kv * LMAX + pos) * HD + d] = vn[d];
+    }
+  }
+  __syncthreads();
+  const float4* K4 = reinterpret_cast<const float4*>(kc + (size_t)kv * LMAX * HD);
+  const float4* V4 = reinterpret_cast<const float4*>(vc + (size_t)kv * LMAX * HD);
+  const int c = tid % TPP, r = tid / TPP;
+  const float4 q4 = reinterpret_cast<const float4*>(qs)[c];
+  float mx = -INFINITY;
+  for (int j0 = 0; j0 < S; j0 += PPP * U) {
+    float4 k4[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = min(j0 + u * PPP + r, S - 1);
+      k4[u] = j == pos ? reinterpret_cast<const float4*>(kn)[c] : K4[(size_t)j * TPP + c];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float a = fmaf(q4.w, k4[u].w, fmaf(q4.z, k4[u].z, fmaf(q4.y, k4[u].y, q4.x * k4[u].x)));
+#pragma unroll
+      for (int m = TPP / 2; m >= 1; m >>= 1) a += __shfl_xor(a, m, TPP);
+      a *= scale;
+      const int j = j0 + u * PPP + r;
+      if (j < S) {
+        if (c == 0) sp[j] = a;
+        mx = fmaxf(mx, a);
+      }
+    }
+  }
+  mx = wave_max(mx);
+  if (lane == 0) wred[wave] = mx;
+  __syncthreads();
+  mx = wred[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, wred[w]);
+  float sum = 0.f;
+  for (int j = tid; j < S; j += NT) {
+    const float e = expf(sp[j] - mx);
+    sp[j] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) wred[NW + wave] = sum;
+  __syncthreads();
+  sum = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) sum += wred[NW + w];
+  for (int j = tid; j < S; j += NT) sp[j] = sp[j] / sum;
+  __syncthreads();
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j0 = r; j0 < S; j0 += PPP * U) {
+    float4 v4[U];
+    float pj[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = min(j0 + u * PPP, S - 1);
+      v4[u] = j == pos ? reinterpret_cast<const float4*>(vn)[c] : V4[(size_t)j * TPP + c];
+      pj[u] = j0 + u * PPP < S ? sp[j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      o.x = fmaf(pj[u], v4[u].x, o.x);
+      o.y = fmaf(pj[u], v4[u].y, o.y);
+      o.z = fmaf(pj[u], v4[u].z, o.z);
+      o.w = fmaf(pj[u], v4[u].w, o.w);
+    }
+  }
+  red[r][c] = o;
+  __syncthreads();
+  if (tid < TPP) {
+    float4 t = red[0][tid];
+#pragma unroll
+    for (int i = 1; i < PPP; ++i) {
+      const float4 v = red[i][tid];
+      t.x += v.x;
+      t.y += v.y;
+      t.z += v.z;
+      t.w += v.w;
+    }
+    float* o4 = out + (size_t)h * HD + 4 * tid;
+    o4[0] = t.x;
+    o4[1] = t.y;
+    o4[2] = t.z;
+    o4[3] = t.w;
+  }
+}
+
 // The same for head dimension 64 and caches of at most 256 positions, with every load that does
 // not depend on the position issued at entry: the key row of position tid, the value column of
 // lane for positions wave + 4 i, and the new q/k/v. The kernel then waits for memory about twice
@@ -479,6 +597,14 @@ extern "C" int miq_attention_decode(const float* qkv, const int32_t* state, cons
   if (HD == 64 && LMAX <= 256)
     hipLaunchKernelGGL(attention_decode_small_kernel, dim3(NH), dim3(256), 0, static_cast<hipStream_t>(stream), qkv,
                        state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV, LMAX, scale);
+  else if (HD == 64)
+    hipLaunchKernelGGL(attention_decode_rows_kernel<64>, dim3(NH), dim3(kAttRowThreads), (size_t)LMAX * 4,
+                       static_cast<hipStream_t>(stream), qkv, state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV,
+                       LMAX, scale);
+  else if (HD == 128)
+    hipLaunchKernelGGL(attention_decode_rows_kernel<128>, dim3(NH), dim3(kAttRowThreads), (size_t)LMAX * 4,
+                       static_cast<hipStream_t>(stream), qkv, state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV,
+                       LMAX, scale);
   else
     hipLaunchKernelGGL(attention_decode_kernel, dim3(NH), dim3(256), (size_t)LMAX * 4, static_cast<hipStream_t>(stream),
                        qkv, state, cos_tab, sin_tab, kcache, vcache, out, NH, NKV, HD, LMAX, scale);

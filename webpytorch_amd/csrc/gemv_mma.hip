@@ -18,6 +18,12 @@
 // |p| >= 2^22) reach the last slice exactly through escape slots (mma_tile.h). Layers with more columns than the counter region
 // has words use fp32 partials and a per-tile arrival counter instead (three round trips). Several
 // workgroups per CU keep ~50-100 KB of weights in flight per CU.
+//
+// Input transforms (XM) for the decode step's fused launches, applied while x is staged:
+// RMSNorm (1): x * w is staged, every workgroup computes the row's mean square over all K from
+// loads issued ahead of its weights, and each slice's partial is divided by
+// r = sqrt(mean(x^2) + eps) before it is summed (RMSNorm(x) @ W = ((x * w) @ W) / r, r one
+// scalar per row); SwiGLU (2): x is a [gate | up] row of 2K values and silu(gate) * up is staged.
 #include <algorithm>
 
 #include "miq_common.h"
@@ -38,19 +44,24 @@ constexpr size_t kMaxFixCols = kFixMaxWords;
 // step (a wave load covers 4 rows x 256 contiguous bytes), and feeds them to four MFMAs that
 // share the step's A fragment: MFMA t's column l & 15 is the lane's column 4 (l & 15) + t. Each
 // lane thus holds whole column results for 4 columns; no reduction across waves is needed.
-template <typename XT, typename ST, typename OT, int SPQ, bool PERM>
+constexpr int kNormLoads = 8;  // float4 loads per thread of an RMSNorm row issued up front (K <= 8192)
+
+template <typename XT, typename ST, typename OT, int SPQ, bool PERM, int XM>
 __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restrict__ x, const int32_t* __restrict__ perm,
                                                              const uint32_t* __restrict__ qw,
                                                              const uint32_t* __restrict__ qz, const ST* __restrict__ sc,
                                                              const float* __restrict__ bias, OT* __restrict__ out,
                                                              float* __restrict__ partials, int* __restrict__ counters,
                                                              unsigned long long* __restrict__ fixacc, int K, int N,
-                                                             float zoff, int slice_steps) {
+                                                             float zoff, int slice_steps, const float* __restrict__ nw,
+                                                             float eps) {
+  static_assert(XM == 0 || (sizeof(XT) == 4 && !PERM), "input transforms take fp32 rows in k order");
   constexpr int NG = SPQ / 4;  // groups per slice
   using SV = typename Scales4<ST>::T;
   __shared__ __align__(16) unsigned char xa[SPQ * kStepBytes];
   __shared__ float2 cx[SPQ];
   __shared__ int is_last;
+  __shared__ float ssw[kThreadsG / 64];
   const int tile = blockIdx.x, sl = blockIdx.y, kslices = gridDim.y;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int st0 = sl * slice_steps;
@@ -68,6 +79,18 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   const uint4* src = PERM ? reinterpret_cast<const uint4*>(perm + k0) : reinterpret_cast<const uint4*>(x + k0);
   const uint4 xr0 = src[0];
   const uint4 xr1 = src[(PERM || sizeof(XT) == 4) ? 1 : 0];
+  uint4 ur0, ur1;  // SwiGLU: the up half of the chunk
+  if constexpr (XM == 2) {
+    const uint4* usrc = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(x) + K + k0);
+    ur0 = usrc[0];
+    ur1 = usrc[1];
+  }
+  float4 xf[kNormLoads];  // RMSNorm: the whole row, for its mean square (clamped loads, masked below)
+  if constexpr (XM == 1) {
+    const float4* xq = reinterpret_cast<const float4*>(x);
+#pragma unroll
+    for (int j = 0; j < kNormLoads; ++j) xf[j] = xq[min((int)threadIdx.x + j * kThreadsG, K / 4 - 1)];
+  }
   // every step's codes and every group's scales and zeros of this wave, issued up front
   uint4 w[SPQ];
   SV sv[NG];
@@ -99,8 +122,32 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(r[j]);
   }
+  if constexpr (XM == 1) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormLoads; ++j)
+      if ((int)threadIdx.x + j * kThreadsG < K / 4)
+        ss += xf[j].x * xf[j].x + xf[j].y * xf[j].y + xf[j].z * xf[j].z + xf[j].w * xf[j].w;
+    const float4* xq = reinterpret_cast<const float4*>(x);
+    for (int i = threadIdx.x + kNormLoads * kThreadsG; i < K / 4; i += kThreadsG) {
+      const float4 t = xq[i];
+      ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) ssw[wave] = ss;
+    const float4 w0 = reinterpret_cast<const float4*>(nw + k0)[0], w1 = reinterpret_cast<const float4*>(nw + k0)[1];
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * wv[j];
+  } else if constexpr (XM == 2) {
+    const uint32_t u[8] = {ur0.x, ur0.y, ur0.z, ur0.w, ur1.x, ur1.y, ur1.z, ur1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (v[j] * (1.f / (1.f + expf(-v[j])))) * __uint_as_float(u[j]);
+  }
   stage_chunk(ch, v, xa, cx);
   __syncthreads();
+  float rn = 1.f;  // RMSNorm: r of the row (the same value in every workgroup)
+  if constexpr (XM == 1) rn = sqrtf((((ssw[0] + ssw[1]) + ssw[2]) + ssw[3]) / (float)K + eps);
   // A rows 0-2 are read by lanes 0-2 of each 16; the other rows of D are never used
   const bool arow = (lane & 15) < 3;
   const BMasks bm = b_masks();
@@ -136,6 +183,10 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
         acc[t] = fmaf(Scales4<ST>::get(sv[gi], t), pv - fmaf(zc, xs, cs), acc[t]);
       }
     }
+  }
+  if constexpr (XM == 1) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = acc[t] / rn;
   }
   const bool mine = lane < 16 && c < N;
   if (kslices == 1) {
@@ -184,7 +235,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
 }
 
 // Launch shape: ~4 workgroups per CU, K-slices of a multiple of 4 steps (whole groups), at most
-// 16 steps and 32 slices; SPQ is the slice length rounded up to an instantiated capacity.
+// 24 steps and 32 slices; SPQ is the slice length rounded up to an instantiated capacity.
 struct Plan {
   int tiles, kslices, slice_steps, spq;
   bool fixed;  // split K reduced in fixed-point words of the counter region
@@ -199,11 +250,11 @@ static bool plan(int K, int N, Plan* p) {
   ks = std::min(ks, std::min(kMaxSlices, steps / 4));
   int ss = (steps + ks - 1) / ks;
   ss = (ss + 3) & ~3;
-  if (ss > 16) return false;
+  if (ss > 24) return false;
   p->slice_steps = ss;
   p->kslices = (steps + ss - 1) / ss;
   if (p->kslices > kMaxSlices || (p->kslices > 1 && p->tiles > kMaxCounters)) return false;
-  p->spq = ss <= 4 ? 4 : ss <= 8 ? 8 : ss <= 12 ? 12 : 16;
+  p->spq = ss <= 4 ? 4 : ss <= 8 ? 8 : ss <= 12 ? 12 : ss <= 16 ? 16 : 24;
   p->fixed = p->kslices > 1 && (size_t)N <= kMaxFixCols;
   // after the counter region: fp32 partials [kslices][N] (slow path) or the fixed-point
   // words' escape slots, same shape
@@ -211,30 +262,36 @@ static bool plan(int K, int N, Plan* p) {
   return true;
 }
 
-template <typename XT, typename ST, typename OT>
+template <typename XT, typename ST, typename OT, int XM>
 static int launch(const Plan& pl, const void* x, const int32_t* perm, const int32_t* qw, const int32_t* qz,
-                  const void* sc, const float* bias, void* out, void* ws, int K, int N, float zoff, hipStream_t st) {
+                  const void* sc, const float* bias, void* out, void* ws, int K, int N, float zoff, const float* nw,
+                  float eps, hipStream_t st) {
   const bool slow = pl.kslices > 1 && !pl.fixed;
   int* counters = slow ? static_cast<int*>(ws) : nullptr;
   float* partials = pl.kslices > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes) : nullptr;
   unsigned long long* fixacc = pl.fixed ? static_cast<unsigned long long*>(ws) : nullptr;
   dim3 grid(pl.tiles, pl.kslices);
 #define MIQ_GM_LAUNCH(S, P)                                                                                        \
-  hipLaunchKernelGGL((gemv_mma_kernel<XT, ST, OT, S, P>), grid, dim3(kThreadsG), 0, st, static_cast<const XT*>(x), \
-                     perm, reinterpret_cast<const uint32_t*>(qw), reinterpret_cast<const uint32_t*>(qz),           \
-                     static_cast<const ST*>(sc), bias, static_cast<OT*>(out), partials, counters, fixacc, K, N, zoff, \
-                     pl.slice_steps)
-#define MIQ_GM_SPQ(S)          \
-  {                            \
-    if (perm)                  \
-      MIQ_GM_LAUNCH(S, true);  \
-    else                       \
-      MIQ_GM_LAUNCH(S, false); \
+  hipLaunchKernelGGL((gemv_mma_kernel<XT, ST, OT, S, P, XM>), grid, dim3(kThreadsG), 0, st,                     \
+                     static_cast<const XT*>(x), perm, reinterpret_cast<const uint32_t*>(qw),                         \
+                     reinterpret_cast<const uint32_t*>(qz), static_cast<const ST*>(sc), bias, static_cast<OT*>(out), \
+                     partials, counters, fixacc, K, N, zoff, pl.slice_steps, nw, eps)
+#define MIQ_GM_SPQ(S)            \
+  {                              \
+    if constexpr (XM == 0) {     \
+      if (perm)                  \
+        MIQ_GM_LAUNCH(S, true);  \
+      else                       \
+        MIQ_GM_LAUNCH(S, false); \
+    } else {                     \
+      MIQ_GM_LAUNCH(S, false);   \
+    }                            \
   }
   if (pl.spq == 4) MIQ_GM_SPQ(4)
   else if (pl.spq == 8) MIQ_GM_SPQ(8)
   else if (pl.spq == 12) MIQ_GM_SPQ(12)
-  else MIQ_GM_SPQ(16)
+  else if (pl.spq == 16) MIQ_GM_SPQ(16)
+  else MIQ_GM_SPQ(24)
 #undef MIQ_GM_SPQ
 #undef MIQ_GM_LAUNCH
   return check_launch("gemv_mma");
@@ -246,14 +303,25 @@ static int launch(const Plan& pl, const void* x, const int32_t* perm, const int3
 // Returns MIQ_ERR_UNSUPPORTED (before launching anything) for shapes it does not cover.
 int gemv_mma(const void* x, int xd, const int32_t* perm, const int32_t* qw, const int32_t* qz, const void* sc,
              int sd, const float* bias, void* out, int od, int K, int N, int gs, float zoff, void* ws,
-             size_t ws_bytes, hipStream_t st) {
+             size_t ws_bytes, hipStream_t st, int xmode, const float* norm_w, float eps) {
   if (gs != 128 || K % 128 || N % 8 || !aligned(qw, 16) || !aligned(sc, 16) || !aligned(x, 16) ||
       (perm && !aligned(perm, 16)))
+    return MIQ_ERR_UNSUPPORTED;
+  if (xmode != 0 && (xd != MIQ_F32 || od != MIQ_F32 || perm || (xmode == 1 && (!norm_w || !aligned(norm_w, 16)))))
     return MIQ_ERR_UNSUPPORTED;
   gm::Plan pl;
   if (!gm::plan(K, N, &pl)) return MIQ_ERR_UNSUPPORTED;
   if (pl.kslices > 1 && (!ws || ws_bytes < pl.ws_bytes)) return MIQ_ERR_UNSUPPORTED;
-#define MIQ_GM_TYPES(XT, ST, OT) return gm::launch<XT, ST, OT>(pl, x, perm, qw, qz, sc, bias, out, ws, K, N, zoff, st)
+  if (xmode == 1) {
+    if (sd == MIQ_F16) return gm::launch<float, __half, float, 1>(pl, x, perm, qw, qz, sc, bias, out, ws, K, N, zoff, norm_w, eps, st);
+    return gm::launch<float, float, float, 1>(pl, x, perm, qw, qz, sc, bias, out, ws, K, N, zoff, norm_w, eps, st);
+  }
+  if (xmode == 2) {
+    if (sd == MIQ_F16) return gm::launch<float, __half, float, 2>(pl, x, perm, qw, qz, sc, bias, out, ws, K, N, zoff, nullptr, 0.f, st);
+    return gm::launch<float, float, float, 2>(pl, x, perm, qw, qz, sc, bias, out, ws, K, N, zoff, nullptr, 0.f, st);
+  }
+#define MIQ_GM_TYPES(XT, ST, OT) \
+  return gm::launch<XT, ST, OT, 0>(pl, x, perm, qw, qz, sc, bias, out, ws, K, N, zoff, nullptr, 0.f, st)
   if (xd == MIQ_F16) {
     if (sd == MIQ_F16) { if (od == MIQ_F16) MIQ_GM_TYPES(__half, __half, __half); MIQ_GM_TYPES(__half, __half, float); }
     if (od == MIQ_F16) MIQ_GM_TYPES(__half, float, __half);

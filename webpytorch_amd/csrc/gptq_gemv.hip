@@ -666,6 +666,13 @@ extern "C" int miq_gptq_gemv_fused(const float* x, int x_mode, const float* norm
   int rc = gemv_check("gptq_gemv_fused", x, MIQ_F32, qweight, qzeros, scales, scales_dtype, out, MIQ_F32, M, K, N, gs,
                       bits);
   if (rc || M == 0) return rc;
+  // one row of an int4 layer in k order: the matrix-core GEMV with the transform in its staging
+  if (M == 1 && bits == 4 && !perm && (workspace == nullptr || aligned(workspace, 256))) {
+    rc = gemv_mma(x, MIQ_F32, nullptr, qweight, qzeros, scales, scales_dtype, bias, out, MIQ_F32, K, N, gs,
+                  zero_offset, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                  x_mode == MIQ_X_RMSNORM ? 1 : 2, norm_w, eps);
+    if (rc != MIQ_ERR_UNSUPPORTED) return rc;
+  }
   GemvPlan p;
   rc = gemv_plan(M, K, N, gs, bits, MIQ_F32, workspace != nullptr, &p);
   if (rc) return rc;

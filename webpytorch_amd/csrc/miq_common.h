@@ -22,11 +22,12 @@ int require_lds(const char* what, size_t bytes);
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
-// One-row int4 GEMV on the matrix cores (gemv_mma.hip), used by miq_gptq_gemv for large layers;
-// returns MIQ_ERR_UNSUPPORTED without launching for shapes it does not cover.
+// One-row int4 GEMV on the matrix cores (gemv_mma.hip), used by miq_gptq_gemv and by
+// miq_gptq_gemv_fused (xmode 1 RMSNorm with norm_w and eps, 2 SwiGLU of a [gate | up] row);
+// returns MIQ_ERR_UNSUPPORTED without launching for shapes and modes it does not cover.
 int gemv_mma(const void* x, int xd, const int32_t* perm, const int32_t* qw, const int32_t* qz, const void* sc,
              int sd, const float* bias, void* out, int od, int K, int N, int gs, float zoff, void* ws,
-             size_t ws_bytes, hipStream_t st);
+             size_t ws_bytes, hipStream_t st, int xmode = 0, const float* norm_w = nullptr, float eps = 0.f);
 size_t gemv_mma_workspace(int K, int N);
 // Few-row (M <= 16) int4 product on the matrix cores (gemm_small.hip), used by miq_gptq_gemm;
 // MIQ_ERR_UNSUPPORTED for shapes it does not cover. xg: gathered copy of x (act-order) or null.
