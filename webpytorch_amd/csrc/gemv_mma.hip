@@ -44,6 +44,12 @@ constexpr size_t kMaxFixCols = kFixMaxWords;
 // step (a wave load covers 4 rows x 256 contiguous bytes), and feeds them to four MFMAs that
 // share the step's A fragment: MFMA t's column l & 15 is the lane's column 4 (l & 15) + t. Each
 // lane thus holds whole column results for 4 columns; no reduction across waves is needed.
+#ifndef MIQ_GM_WPC
+#define MIQ_GM_WPC 4  // workgroups per CU the planner aims for
+#endif
+#ifndef MIQ_GM_DEPTH
+#define MIQ_GM_DEPTH 4  // steps of codes in flight per wave (0: all of the slice, issued at entry)
+#endif
 constexpr int kNormLoads = 8;  // float4 loads per thread of an RMSNorm row issued up front (K <= 8192)
 
 template <typename XT, typename ST, typename OT, int SPQ, bool PERM, int XM>
@@ -98,14 +104,20 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   const uint32_t* wp = qw + (size_t)(rb + (lane >> 4)) * N + cl;
   // steps past the slice's end reload its last step (a select, not a branch: a branch around a
   // load makes the compiler's wait counts conservative at the join)
-#pragma unroll
-  for (int i = 0; i < SPQ; ++i) w[i] = *reinterpret_cast<const uint4*>(wp + (size_t)(4 * min(i, ns - 1)) * N);
+  auto wload = [&](int i) __attribute__((always_inline)) {
+    return *reinterpret_cast<const uint4*>(wp + (size_t)(4 * min(i, ns - 1)) * N);
+  };
+  // the scales and zeros first (the first group's fold needs them), then the codes of the first
+  // DEPTH steps; each group issues the codes DEPTH steps ahead of it
+  constexpr int DEPTH = (MIQ_GM_DEPTH > 0 && MIQ_GM_DEPTH < SPQ) ? MIQ_GM_DEPTH : SPQ;
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     const int g = (rb >> 4) + min(gi, (ns >> 2) - 1);  // 16 packed rows per group
     sv[gi] = Scales4<ST>::load(sc + (size_t)g * N + cl);
     zw[gi] = qz[(size_t)g * (N >> 3) + (cl >> 3)];
   }
+#pragma unroll
+  for (int i = 0; i < DEPTH; ++i) w[i] = wload(i);
   __builtin_amdgcn_sched_barrier(0);  // the scheduler keeps every load above the conversions
   float v[8];
   const uint32_t r[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
@@ -156,6 +168,14 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
+    if constexpr (DEPTH < SPQ) {
+      if (4 * gi + DEPTH < SPQ) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) w[4 * gi + DEPTH + s4] = wload(4 * gi + DEPTH + s4);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     if (4 * gi < ns) {
       floatx4 d[4];
 #pragma unroll
@@ -245,7 +265,7 @@ struct Plan {
 static bool plan(int K, int N, Plan* p) {
   const int steps = K / 32;
   p->tiles = (N + 255) / 256;
-  int ks = (4 * kCUs + p->tiles - 1) / p->tiles;
+  int ks = (MIQ_GM_WPC * kCUs + p->tiles - 1) / p->tiles;
   ks = std::max(ks, (steps + 15) / 16);
   ks = std::min(ks, std::min(kMaxSlices, steps / 4));
   int ss = (steps + ks - 1) / ks;
