@@ -15,6 +15,10 @@
 
 namespace miq {
 
+#ifndef MIQ_Q4K_DEPTH
+#define MIQ_Q4K_DEPTH 1  // rows of a wave's blocks in flight ahead of the one computed (0: all)
+#endif
+
 struct Q4kScales {
   float d1, m1, d2, m2;  // d*sc and dmin*m for sub-blocks 2q and 2q+1
 };
@@ -79,8 +83,10 @@ __global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restr
 // code group q: 64 weights of sub-blocks 2q (low nibbles) and 2q + 1 (high nibbles), at
 // activations b * 256 + 64 q .. + 63. The workgroup stages x once in LDS (fp16 in the pair
 // order of the nibble unpack, or fp32) with sums over each 32 activations; a lane reads its 64
-// activations once per pass and reuses them for the R rows. The weight loads of the first step
-// are issued before x is staged.
+// activations once per pass and reuses them for the R rows. The blocks of one row are issued
+// ahead of the row computed (the first before x is staged): with every row of a wave in flight
+// at once the arithmetic only starts when the memory phase is over, one row ahead lets it run
+// under the loads of the next (4096 -> 14336: 13.1 -> 10.4 us, with 8 rows a wave).
 template <int R, int MR, typename XT, typename OT>
 __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x, const uint8_t* __restrict__ w,
                                                        const float* __restrict__ bias, OT* __restrict__ out,
@@ -102,16 +108,28 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
   int grp = blockIdx.x * 4 + wave;
 
   uint4 hd[R], c0[R], c1[R];
-  auto load_rows = [&](int g, int pass) {
+  // row r's block of a pass; the first D rows are issued ahead, row r + D when row r is computed
+  constexpr int D = (MIQ_Q4K_DEPTH > 0 && MIQ_Q4K_DEPTH < R) ? MIQ_Q4K_DEPTH : R;
+  auto load_row = [&](int g, int pass, int r) __attribute__((always_inline)) {
     const int b = pass * 16 + slot;
+    const int n = g * R + r;
+    if (n < N && b < nb) {
+      const uint8_t* blk = w + (size_t)n * row_bytes + (size_t)b * 144;
+      hd[r] = *reinterpret_cast<const uint4*>(blk);
+      c0[r] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * q);
+      c1[r] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * q);
+    }
+  };
+  auto load_rows = [&](int g, int pass) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = g * R + r;
-      if (n < N && b < nb) {
-        const uint8_t* blk = w + (size_t)n * row_bytes + (size_t)b * 144;
-        hd[r] = *reinterpret_cast<const uint4*>(blk);
-        c0[r] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * q);
-        c1[r] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * q);
+    for (int r = 0; r < D; ++r) load_row(g, pass, r);
+  };
+  auto load_ahead = [&](int g, int pass, int r) __attribute__((always_inline)) {
+    if constexpr (D < R) {
+      if (r + D < R) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_row(g, pass, r + D);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
@@ -172,6 +190,7 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
 #pragma unroll
             for (int r = 0; r < R; ++r) {
               const int n = grp * R + r;
+              if (m == 0) load_ahead(grp, pass, r);
               if (n >= N) break;
               uint4 h4 = hd[r];
               uint32_t cw[8] = {c0[r].x, c0[r].y, c0[r].z, c0[r].w, c1[r].x, c1[r].y, c1[r].z, c1[r].w};
@@ -199,6 +218,7 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
 #pragma unroll
             for (int r = 0; r < R; ++r) {
               const int n = grp * R + r;
+              if (m == 0) load_ahead(grp, pass, r);
               if (n >= N) break;
               uint4 h4 = hd[r];
               uint32_t cw[8] = {c0[r].x, c0[r].y, c0[r].z, c0[r].w, c1[r].x, c1[r].y, c1[r].z, c1[r].w};
@@ -276,7 +296,7 @@ static int launch_q4k(const void* x, const uint8_t* w, const float* bias, void* 
 template <int MR>
 static int q4k_types(const void* x, int xd, const uint8_t* w, const float* bias, void* out, int od, int M,
                      int K, int N, hipStream_t st) {
-  constexpr int R = 4;
+  constexpr int R = 8;
   if (xd == MIQ_F16) {
     if (od == MIQ_F16) return launch_q4k<R, MR, __half, __half>(x, w, bias, out, M, K, N, st);
     return launch_q4k<R, MR, __half, float>(x, w, bias, out, M, K, N, st);
