@@ -32,6 +32,7 @@ namespace miq {
 
 constexpr int kMoeBM = 32;      // rows per tile (two 16-row MFMA blocks)
 constexpr int kMoeMaxTK = 4096;  // T * k handled by the single-workgroup router
+constexpr int kSlotWaves = 16;   // waves of the slot kernel (1024 threads), one chunk of picks each
 
 // Offsets (in 4-byte words) of the route buffer's arrays.
 struct RouteLayout {
@@ -182,13 +183,11 @@ __global__ __launch_bounds__(1024) void moe_slots_kernel(int T, int E, int k, in
   float* sw = reinterpret_cast<float*>(lds_i + TK);  // [TK] their weights
   int* cnt = lds_i + 2 * TK;                         // [E + 1] picks per expert
   int* off = cnt + E + 1;                            // [E + 1] first slot per expert
-  int* run = off + E + 1;                            // [E + 1] slots assigned so far
-  int* wsum = run + E + 1;                           // [2][16] wave totals of the scans
+  int* wsum = off + E + 1;                           // [2][16] wave totals of the scans
+  int* cw = wsum + 32;                               // [16][E + 1] per wave chunk: picks, then first slots
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    cnt[e] = 0;
-    run[e] = 0;
-  }
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
+  for (int i = threadIdx.x; i < kSlotWaves * (E + 1); i += blockDim.x) cw[i] = 0;
   for (int i = threadIdx.x; i < TK; i += blockDim.x) route[L.slot_max + i] = 0;  // gate_up's row maxima
   for (int i = threadIdx.x; i < TK; i += blockDim.x) {
     se[i] = topk_e[i];
@@ -234,14 +233,29 @@ __global__ __launch_bounds__(1024) void moe_slots_kernel(int T, int E, int k, in
       *ntiles = t0 + ntl;
     }
   }
+  // the picks in order, in 16 consecutive chunks (one per wave): each chunk's picks per expert,
+  // then per expert the chunks' first slots (its offset plus the earlier chunks' picks), so that
+  // every wave can walk its chunk at once and the slots come out as one walk in order would give
+  const int C = ((TK + kSlotWaves - 1) / kSlotWaves + 63) & ~63;
+  const int i0w = wave * C, i1w = min(TK, i0w + C);
+  int* runw = cw + wave * (E + 1);
+  for (int i = i0w + lane; i < i1w; i += 64) atomicAdd(&runw[se[i]], 1);  // counts: order-free
   __syncthreads();
-  if (wave != 0) return;
-  // one wave walks the picks in order, 64 at a time: a pick's slot is its expert's offset, plus
-  // the slots that expert already gave out, plus the earlier lanes with the same expert (the
-  // lanes that match it, from ballots over the bits of the expert index)
-  for (int i0 = 0; i0 < TK; i0 += 64) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int base = off[e];
+    for (int w = 0; w < kSlotWaves; ++w) {
+      const int t = cw[w * (E + 1) + e];
+      cw[w * (E + 1) + e] = base;
+      base += t;
+    }
+  }
+  __syncthreads();
+  // a wave walks its chunk 64 picks at a time: a pick's slot is the chunk's next slot for its
+  // expert plus the earlier lanes with the same expert (the lanes that match it, from ballots
+  // over the bits of the expert index)
+  for (int i0 = i0w; i0 < i1w; i0 += 64) {
     const int i = i0 + lane;
-    const bool valid = i < TK;
+    const bool valid = i < i1w;
     const int e = valid ? se[i] : E;  // E: a sentinel with its own (unused) counter
     uint64_t m = ~0ull;
 #pragma unroll
@@ -251,14 +265,14 @@ __global__ __launch_bounds__(1024) void moe_slots_kernel(int T, int E, int k, in
       m &= bit ? bb : ~bb;
     }
     const int rank = __popcll(m & ((1ull << lane) - 1));
-    const int base = run[e];
+    const int base = runw[e];
     if (valid) {
-      const int sl = off[e] + base + rank;
+      const int sl = base + rank;
       slot_of[i] = sl;
       sorted_tok[sl] = i / k;
       sorted_w[sl] = sw[i];
     }
-    if (rank == 0) run[e] = base + __popcll(m);
+    if (rank == 0) runw[e] = base + __popcll(m);
   }
 }
 
@@ -611,8 +625,9 @@ extern "C" int miq_moe_route(const float* logits, int T, int E, int k, int norm_
   else if (E <= 256) hipLaunchKernelGGL(moe_topk_kernel<4>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
   else if (E <= 512) hipLaunchKernelGGL(moe_topk_kernel<8>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
   else hipLaunchKernelGGL(moe_topk_kernel<16>, g, dim3(256), 0, st, logits, T, E, k, norm_topk, r);
-  // se, sw [T*k]; cnt, off, run [E+1]; wave sums [32]
-  const size_t lds = (2 * (size_t)T * k + 3 * ((size_t)E + 1) + 32) * 4;
+  // se, sw [T*k]; cnt, off [E+1]; wave sums [32]; per chunk counters [16][E+1]
+  const size_t lds = (2 * (size_t)T * k + (2 + kSlotWaves) * ((size_t)E + 1) + 32) * 4;
+  if (lds > 64 * 1024 && (rc = require_lds("moe_route", lds))) return rc;
   hipLaunchKernelGGL(moe_slots_kernel, dim3(1), dim3(1024), lds, st, T, E, k, r);
   return check_launch("moe_route");
 }
