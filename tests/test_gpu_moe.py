@@ -233,6 +233,24 @@ def test_moe_more_picks_than_one_routing_pass(gpu):
     _check(got.cpu().numpy(), ref, rel=1e-5)
 
 
+def test_moe_nan_logits_row_routes_to_real_experts(gpu, small_moe):
+    """A token whose router logits hold a NaN has NaN probabilities everywhere; it is still sent
+    to k real experts (the first ones) with NaN weights, so its output is NaN like the
+    reference's and the other tokens' routing and outputs are untouched."""
+    import torch
+    from webpytorch_amd import core
+    w = small_moe
+    x = np.random.default_rng(9).standard_normal((48, 512)).astype(np.float32)
+    logits = w["logits"].copy()
+    logits[5, 2] = np.nan
+    ref = moe.moe_mlp_np(x, logits, [moe.gptq_expert(e) for e in w["experts"]], 4)
+    got = core.MoEExperts(w["experts"])(torch.from_numpy(x).cuda(), torch.from_numpy(logits).cuda(),
+                                        4).cpu().numpy()
+    assert np.isnan(ref[5]).all() and np.isnan(got[5]).all()
+    keep = np.arange(48) != 5
+    _check(got[keep], ref[keep], rel=2e-5)
+
+
 def test_moe_nan_row_stays_in_its_token(gpu, small_moe):
     import torch
     from webpytorch_amd import core

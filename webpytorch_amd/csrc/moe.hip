@@ -126,8 +126,14 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
       }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    // a NaN probability (NaN logits) ranks below every number but above a taken pick (-1), so
+    // such experts are still picked in index order and keep NaN as their weight
+    constexpr double kNanRank = -0.5;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) pv[i] = lane + 64 * i < E ? pv[i] / sum : -1.0;
+    for (int i = 0; i < EPL; ++i) {
+      const double pr = pv[i] / sum;
+      pv[i] = lane + 64 * i < E ? (pr != pr ? kNanRank : pr) : -1.0;
+    }
     // lane j keeps pick j (k <= 32), so no per-lane array is indexed at run time
     int my_e = E;
     double my_p = 0.0;
@@ -150,11 +156,12 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
 #pragma unroll
       for (int i = 0; i < EPL; ++i)
         if (lane + 64 * i == be) pv[i] = -1.0;
+      const double bw = best == kNanRank ? __longlong_as_double(0x7FF8000000000000ll) : best;
       if (lane == j) {
         my_e = be;
-        my_p = best;
+        my_p = bw;
       }
-      psum += best;
+      psum += bw;
     }
     // ascending expert order: a pick's rank is the number of picks with a smaller expert
     int rank = 0;
