@@ -606,7 +606,10 @@ def main():
     torch.cuda.set_device(0)
     torch.manual_seed(0)
     if a.gemv_large:
-        print(json.dumps(gemv_large(torch, core)), flush=True)
+        out = gemv_large(torch, core)
+        copy_bytes = copy_calibration(torch)
+        out.update({"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes})
+        print(json.dumps(out), flush=True)
         return
     if a.only:
         fn = {"gemm": lambda: gemm_bench(torch, core, Ms=(512,)), "gemm_int8": lambda: gemm_int8_bench(torch, core),

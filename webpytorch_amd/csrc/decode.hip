@@ -202,10 +202,7 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(
 // threads (one float4 each, the row's partial dot products summed across the group), so a pass
 // covers 4096 / HD positions with coalesced loads, four passes in flight; the weighted sum
 // likewise gives each thread a float4 of the head dimension and a residue of the position
-// modulo 4096 / HD, four positions in flight, the residues combined in order through LDS. The
-// key and value rows of the first four passes do not depend on the position and are loaded at
-// entry, before the position and the new q/k/v are waited for (rows past the position are read
-// in bounds and masked; the new position's row always comes from LDS).
+// modulo 4096 / HD, four positions in flight, the residues combined in order through LDS.
 constexpr int kAttRowThreads = 1024;
 template <int HD>
 __global__ __launch_bounds__(kAttRowThreads) void attention_decode_rows_kernel(
@@ -223,13 +220,6 @@ __global__ __launch_bounds__(kAttRowThreads) void attention_decode_rows_kernel(
   const int c = tid % TPP, r = tid / TPP;
   const float4* K4 = reinterpret_cast<const float4*>(kc + (size_t)kv * LMAX * HD);
   const float4* V4 = reinterpret_cast<const float4*>(vc + (size_t)kv * LMAX * HD);
-  float4 kp[U], vp[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int j = min(u * PPP + r, LMAX - 1);
-    kp[u] = K4[(size_t)j * TPP + c];
-    vp[u] = V4[(size_t)j * TPP + c];
-  }
   const int pos = state[0];
   if (pos >= LMAX) return;  // uniform: the caller never runs past its cache
   const int S = pos + 1;
@@ -252,7 +242,7 @@ __global__ __launch_bounds__(kAttRowThreads) void attention_decode_rows_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = min(j0 + u * PPP + r, S - 1);
-      k4[u] = j == pos ? reinterpret_cast<const float4*>(kn)[c] : j0 == 0 ? kp[u] : K4[(size_t)j * TPP + c];
+      k4[u] = j == pos ? reinterpret_cast<const float4*>(kn)[c] : K4[(size_t)j * TPP + c];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -294,7 +284,7 @@ __global__ __launch_bounds__(kAttRowThreads) void attention_decode_rows_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = min(j0 + u * PPP, S - 1);
-      v4[u] = j == pos ? reinterpret_cast<const float4*>(vn)[c] : j0 == r ? vp[u] : V4[(size_t)j * TPP + c];
+      v4[u] = j == pos ? reinterpret_cast<const float4*>(vn)[c] : V4[(size_t)j * TPP + c];
       pj[u] = j0 + u * PPP < S ? sp[j] : 0.f;
     }
 #pragma unroll
