@@ -368,6 +368,22 @@ int miq_decode_persistent(const uint64_t* layer_table, const void* embed, const 
                           int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits,
                           float eps, float zoff, float head_zoff, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Capture and replay (replaces WebGPUPlatform.beginCapture / endCapture / replay,
+ * `webtorch/platform.py:45-56`, which `CausalLM.capture` records one decode step with)
+ * ------------------------------------------------------------------------------------- */
+/* Starts recording the launches made on `stream` (not the null stream) by the calling thread:
+ * nothing recorded runs until it is replayed. Every buffer the recorded launches use must stay
+ * allocated while the graph exists. */
+int miq_graph_begin(void* stream);
+/* Stops recording on `stream` and returns the executable recording in *graph (an opaque
+ * handle, hipGraphExec_t). */
+int miq_graph_end(void* stream, void** graph);
+/* Replays a recording on `stream` (asynchronous, stream-ordered). */
+int miq_graph_launch(void* graph, void* stream);
+/* Frees a recording (null: nothing). */
+int miq_graph_destroy(void* graph);
+
 #ifdef __cplusplus
 }
 #endif

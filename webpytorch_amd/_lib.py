@@ -19,6 +19,10 @@ _d = ctypes.c_double
 
 # name -> argument types (restype is int for every compute entry point)
 SIGNATURES = {
+    "miq_graph_begin": [_p],
+    "miq_graph_end": [_p, _p],
+    "miq_graph_launch": [_p, _p],
+    "miq_graph_destroy": [_p],
     "miq_gptq_dequant_f32": [_p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _f, _p],
     "miq_gptq_repack_rows": [_p, _p, _p, _i, _i, _i, _p],
     "miq_gptq_gemv_workspace": [_i, _i, _i, _i, _i, _i, _p],

@@ -1,0 +1,50 @@
+// Capture and replay of a launch sequence through the C ABI, for hosts without torch: the
+// reference's WebGPUPlatform.beginCapture / endCapture / replay (`webtorch/platform.py:45-56`)
+// as HIP stream capture. Everything a caller launches on the stream between miq_graph_begin and
+// miq_graph_end is recorded (the library's kernels read their shapes and pointers at launch, so
+// the buffers must stay alive while the graph exists); miq_graph_launch replays the recording on
+// any stream. The decode kernels keep their state (position, token ids) in device memory, so a
+// replayed one-token step advances the sequence by itself.
+#include "miq_common.h"
+
+using namespace miq;
+
+extern "C" int miq_graph_begin(void* stream) {
+  MIQ_REQUIRE(stream, MIQ_ERR_INVALID, "graph_begin: capture needs a stream other than the null stream");
+  const hipError_t e = hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_begin: hipStreamBeginCapture: %s", hipGetErrorString(e));
+  return MIQ_OK;
+}
+
+extern "C" int miq_graph_end(void* stream, void** graph) {
+  MIQ_REQUIRE(stream && graph, MIQ_ERR_INVALID, "graph_end: null stream or output");
+  *graph = nullptr;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
+  if (e != hipSuccess || !g)
+    return fail(MIQ_ERR_HIP, "graph_end: hipStreamEndCapture: %s", hipGetErrorString(e != hipSuccess ? e : hipErrorUnknown));
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  const hipError_t d = hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_end: hipGraphInstantiate: %s", hipGetErrorString(e));
+  if (d != hipSuccess) {
+    (void)hipGraphExecDestroy(x);
+    return fail(MIQ_ERR_HIP, "graph_end: hipGraphDestroy: %s", hipGetErrorString(d));
+  }
+  *graph = x;
+  return MIQ_OK;
+}
+
+extern "C" int miq_graph_launch(void* graph, void* stream) {
+  MIQ_REQUIRE(graph, MIQ_ERR_INVALID, "graph_launch: null graph");
+  const hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(graph), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_launch: hipGraphLaunch: %s", hipGetErrorString(e));
+  return MIQ_OK;
+}
+
+extern "C" int miq_graph_destroy(void* graph) {
+  if (!graph) return MIQ_OK;
+  const hipError_t e = hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_destroy: hipGraphExecDestroy: %s", hipGetErrorString(e));
+  return MIQ_OK;
+}
