@@ -112,9 +112,11 @@ __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw,
                                            int N, int c0, int rb, int nsteps, int lgs) {
   const int tid = opaque_tid();
   const int wave = uniform(tid >> 6), lane = tid & 63;
-  const int spq = (nsteps + kKParts - 1) / kKParts;
-  t.st0 = wave * spq;
-  t.ns = max(0, min(spq, nsteps - t.st0));
+  // contiguous step ranges, the first nsteps % kKParts waves one step longer: wave w runs on
+  // SIMD w % 4, so every SIMD gets the same step count to within one
+  const int base = nsteps / kKParts, extra = nsteps % kKParts;
+  t.st0 = wave * base + min(wave, extra);
+  t.ns = base + (wave < extra ? 1 : 0);
   const int c = min(c0 + 4 * (lane & 15), N - 4);
   const int r0 = rb + 4 * t.st0, gsh = lgs - 3;
   const uint32_t* wp = qw + (uint32_t)((r0 + (lane >> 4)) * N + c);
