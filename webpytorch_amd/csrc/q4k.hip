@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restr
 // activations once per pass and reuses them for the R rows. The blocks of one row are issued
 // ahead of the row computed (the first before x is staged): with every row of a wave in flight
 // at once the arithmetic only starts when the memory phase is over, one row ahead lets it run
-// under the loads of the next (4096 -> 14336: 13.1 -> 10.4 us, with 8 rows a wave).
+// under the loads of the next (4096 -> 14336: 13.1 -> 10.4 us with 8 rows a wave; 10.3 us with 7).
 template <int R, int MR, typename XT, typename OT>
 __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x, const uint8_t* __restrict__ w,
                                                        const float* __restrict__ bias, OT* __restrict__ out,
@@ -293,10 +293,9 @@ static int launch_q4k(const void* x, const uint8_t* w, const float* bias, void* 
   return check_launch("q4k_gemv");
 }
 
-template <int MR>
+template <int R, int MR>
 static int q4k_types(const void* x, int xd, const uint8_t* w, const float* bias, void* out, int od, int M,
                      int K, int N, hipStream_t st) {
-  constexpr int R = 8;
   if (xd == MIQ_F16) {
     if (od == MIQ_F16) return launch_q4k<R, MR, __half, __half>(x, w, bias, out, M, K, N, st);
     return launch_q4k<R, MR, __half, float>(x, w, bias, out, M, K, N, st);
@@ -330,6 +329,14 @@ extern "C" int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const 
   MIQ_REQUIRE(x_dtype == MIQ_F16 || x_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "q4k_gemv: x dtype");
   MIQ_REQUIRE(out_dtype == MIQ_F16 || out_dtype == MIQ_F32, MIQ_ERR_UNSUPPORTED, "q4k_gemv: out dtype");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (M >= 2) return q4k_types<2>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
-  return q4k_types<1>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
+  // Rows per wave: 8, or 7 where that gives the busiest CU fewer rows (its workgroups, four
+  // waves each, rounded up over the CUs): 4096 -> 14336 is 448 workgroups at 8 rows (two on
+  // most CUs, one on the rest) but 512 at 7, two on every CU.
+  auto busiest = [&](int R) { return R * (((N + R - 1) / R + 4 * kCUs - 1) / (4 * kCUs)); };
+  if (busiest(7) < busiest(8)) {
+    if (M >= 2) return q4k_types<7, 2>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
+    return q4k_types<7, 1>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
+  }
+  if (M >= 2) return q4k_types<8, 2>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
+  return q4k_types<8, 1>(x, x_dtype, w, bias, out, out_dtype, M, K, N, st);
 }
