@@ -34,19 +34,20 @@ namespace gg {
 constexpr int kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ5_K = 13, kQ6_K = 14,
               kIQ4_NL = 20, kIQ4_XS = 23;
 
-// Values and bytes per block; lanes per block and values per lane of the GEMV.
+// Values and bytes per block; lanes per block and values per lane of the GEMV; rows a wave
+// walks (the fastest of 1, 2 and 4 per type at 4096 -> 14336).
 template <int T> struct Blk;
-template <> struct Blk<kQ8_0> { static constexpr int VALS = 32, BYTES = 34, LPB = 4, VPL = 8; };
-template <> struct Blk<kQ6_K> { static constexpr int VALS = 256, BYTES = 210, LPB = 16, VPL = 16; };
-template <> struct Blk<kQ4_0> { static constexpr int VALS = 32, BYTES = 18, LPB = 4, VPL = 8; };
-template <> struct Blk<kQ4_1> { static constexpr int VALS = 32, BYTES = 20, LPB = 4, VPL = 8; };
-template <> struct Blk<kQ5_0> { static constexpr int VALS = 32, BYTES = 22, LPB = 4, VPL = 8; };
-template <> struct Blk<kQ5_1> { static constexpr int VALS = 32, BYTES = 24, LPB = 4, VPL = 8; };
-template <> struct Blk<kIQ4_NL> { static constexpr int VALS = 32, BYTES = 18, LPB = 4, VPL = 8; };
-template <> struct Blk<kIQ4_XS> { static constexpr int VALS = 256, BYTES = 136, LPB = 16, VPL = 16; };
-template <> struct Blk<kQ5_K> { static constexpr int VALS = 256, BYTES = 176, LPB = 16, VPL = 16; };
-template <> struct Blk<kQ2_K> { static constexpr int VALS = 256, BYTES = 84, LPB = 16, VPL = 16; };
-template <> struct Blk<kQ3_K> { static constexpr int VALS = 256, BYTES = 110, LPB = 16, VPL = 16; };
+template <> struct Blk<kQ8_0> { static constexpr int VALS = 32, BYTES = 34, LPB = 4, VPL = 8, ROWS = 2; };
+template <> struct Blk<kQ6_K> { static constexpr int VALS = 256, BYTES = 210, LPB = 16, VPL = 16, ROWS = 1; };
+template <> struct Blk<kQ4_0> { static constexpr int VALS = 32, BYTES = 18, LPB = 4, VPL = 8, ROWS = 4; };
+template <> struct Blk<kQ4_1> { static constexpr int VALS = 32, BYTES = 20, LPB = 4, VPL = 8, ROWS = 2; };
+template <> struct Blk<kQ5_0> { static constexpr int VALS = 32, BYTES = 22, LPB = 4, VPL = 8, ROWS = 2; };
+template <> struct Blk<kQ5_1> { static constexpr int VALS = 32, BYTES = 24, LPB = 4, VPL = 8, ROWS = 4; };
+template <> struct Blk<kIQ4_NL> { static constexpr int VALS = 32, BYTES = 18, LPB = 4, VPL = 8, ROWS = 2; };
+template <> struct Blk<kIQ4_XS> { static constexpr int VALS = 256, BYTES = 136, LPB = 16, VPL = 16, ROWS = 2; };
+template <> struct Blk<kQ5_K> { static constexpr int VALS = 256, BYTES = 176, LPB = 16, VPL = 16, ROWS = 1; };
+template <> struct Blk<kQ2_K> { static constexpr int VALS = 256, BYTES = 84, LPB = 16, VPL = 16, ROWS = 2; };
+template <> struct Blk<kQ3_K> { static constexpr int VALS = 256, BYTES = 110, LPB = 16, VPL = 16, ROWS = 1; };
 
 __device__ __forceinline__ uint32_t ld32(const uint8_t* w, size_t a) {
   return *reinterpret_cast<const uint32_t*>(w + a);  // a % 4 == 0
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(256) void ggml_gemv_kernel(const XT* __restrict__ x
                                                         const float* __restrict__ bias, OT* __restrict__ out,
                                                         int K, int N) {
   using B = Blk<T>;
-  constexpr int R = 4, BPP = 64 / B::LPB, VPL = B::VPL;
+  constexpr int R = B::ROWS, BPP = 64 / B::LPB, VPL = B::VPL;
   extern __shared__ __align__(16) float lds_f[];
   float* xs = lds_f;       // K activations
   float* xg = lds_f + K;   // K / VPL sums of each lane's run
@@ -341,7 +342,7 @@ static int launch(const void* x, const uint8_t* w, const float* bias, void* out,
     const int rc = require_lds("ggml_gemv", lds);
     if (rc) return rc;
   }
-  const int groups = (N + 3) / 4;
+  const int groups = (N + Blk<T>::ROWS - 1) / Blk<T>::ROWS;
   int wgs = (groups + 3) / 4;
   if (wgs > 4 * kCUs) wgs = 4 * kCUs;
   hipLaunchKernelGGL(kern, dim3(wgs, M), dim3(256), lds, st, static_cast<const XT*>(x), w, bias,
