@@ -10,7 +10,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _check(got, ref, rel=1e-4):
-    """North-star bar elementwise (|d| <= 1e-3 + 1e-2 |ref|) and a tight max-relative bound."""
+    """Output parity bar elementwise (|d| <= 1e-3 + 1e-2 |ref|) and a tight max-relative bound."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     bad = np.abs(got - ref) > 1e-3 + 1e-2 * np.abs(ref)

@@ -12,7 +12,7 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
 def _close(got, ref, rtol=1e-2, atol=1e-3):
-    """|got - ref| <= atol + rtol * |ref| elementwise."""
+    """Output parity bar (fp32 accumulate): |got - ref| <= atol + rtol * |ref| elementwise."""
     got = np.asarray(got, np.float64); ref = np.asarray(ref, np.float64)
     bad = np.abs(got - ref) > atol + rtol * np.abs(ref)
     assert not bad.any(), "max err %.3g at %s" % (np.abs(got - ref).max(), np.argwhere(bad)[:3])
