@@ -77,9 +77,22 @@ def test_capture_replay_matches_eager(gpu):
 
 
 def test_graph_errors_are_reported(gpu):
-    from webpytorch_amd import _lib
+    import torch
+    from webpytorch_amd import _lib, core
     with pytest.raises(ValueError, match="null stream"):
         _lib.call("miq_graph_begin", None)
     with pytest.raises(ValueError, match="null graph"):
         _lib.call("miq_graph_launch", None, None)
     _lib.call("miq_graph_destroy", None)
+    # ending a recording that was never begun fails with the runtime's reason, and leaves no
+    # error behind for the next launch
+    side = torch.cuda.Stream()
+    graph = ctypes.c_void_p()
+    with pytest.raises(RuntimeError, match="graph_end"):
+        _lib.call("miq_graph_end", ctypes.c_void_p(side.cuda_stream), ctypes.byref(graph))
+    assert not graph.value
+    x = torch.ones((1, 8), device="cuda")
+    out = torch.empty((1, 8), device="cuda")
+    _lib.call("miq_add", core.ptr(out.copy_(x)), core.ptr(x), 8, core.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(out, 2 * x)

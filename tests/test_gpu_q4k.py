@@ -49,7 +49,8 @@ def test_config1_gemv(gpu, M):
     assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
 
 
-@pytest.mark.parametrize("K,N", [(256, 2), (768, 33), (8192, 70)])
+# (512, 8000): a width where the kernel walks 8 rows a wave (7 elsewhere)
+@pytest.mark.parametrize("K,N", [(256, 2), (768, 33), (8192, 70), (512, 8000)])
 def test_gemv_ragged_shapes_and_bias(gpu, K, N):
     import torch
     from webpytorch_amd import core

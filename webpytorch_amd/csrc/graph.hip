@@ -9,10 +9,17 @@
 
 using namespace miq;
 
+// A failed runtime call is reported through the return code; the runtime's last-error state is
+// cleared so that it does not surface later as the failure of an unrelated launch.
+static int hip_fail(const char* what, hipError_t e) {
+  (void)hipGetLastError();
+  return fail(MIQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
 extern "C" int miq_graph_begin(void* stream) {
   MIQ_REQUIRE(stream, MIQ_ERR_INVALID, "graph_begin: capture needs a stream other than the null stream");
   const hipError_t e = hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal);
-  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_begin: hipStreamBeginCapture: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return hip_fail("graph_begin: hipStreamBeginCapture", e);
   return MIQ_OK;
 }
 
@@ -21,15 +28,14 @@ extern "C" int miq_graph_end(void* stream, void** graph) {
   *graph = nullptr;
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
-  if (e != hipSuccess || !g)
-    return fail(MIQ_ERR_HIP, "graph_end: hipStreamEndCapture: %s", hipGetErrorString(e != hipSuccess ? e : hipErrorUnknown));
+  if (e != hipSuccess || !g) return hip_fail("graph_end: hipStreamEndCapture", e != hipSuccess ? e : hipErrorUnknown);
   hipGraphExec_t x = nullptr;
   e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
   const hipError_t d = hipGraphDestroy(g);
-  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_end: hipGraphInstantiate: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return hip_fail("graph_end: hipGraphInstantiate", e);
   if (d != hipSuccess) {
     (void)hipGraphExecDestroy(x);
-    return fail(MIQ_ERR_HIP, "graph_end: hipGraphDestroy: %s", hipGetErrorString(d));
+    return hip_fail("graph_end: hipGraphDestroy", d);
   }
   *graph = x;
   return MIQ_OK;
@@ -38,13 +44,13 @@ extern "C" int miq_graph_end(void* stream, void** graph) {
 extern "C" int miq_graph_launch(void* graph, void* stream) {
   MIQ_REQUIRE(graph, MIQ_ERR_INVALID, "graph_launch: null graph");
   const hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(graph), static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_launch: hipGraphLaunch: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return hip_fail("graph_launch: hipGraphLaunch", e);
   return MIQ_OK;
 }
 
 extern "C" int miq_graph_destroy(void* graph) {
   if (!graph) return MIQ_OK;
   const hipError_t e = hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
-  if (e != hipSuccess) return fail(MIQ_ERR_HIP, "graph_destroy: hipGraphExecDestroy: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return hip_fail("graph_destroy: hipGraphExecDestroy", e);
   return MIQ_OK;
 }
