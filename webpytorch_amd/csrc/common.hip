@@ -20,6 +20,9 @@ int fail(int code, const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
+  // a runtime failure is reported here; the runtime's own last-error state is cleared so that it
+  // does not surface later as the failure of an unrelated launch
+  if (code == MIQ_ERR_HIP) (void)hipGetLastError();
   return code;
 }
 

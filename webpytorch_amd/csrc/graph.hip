@@ -9,12 +9,9 @@
 
 using namespace miq;
 
-// A failed runtime call is reported through the return code; the runtime's last-error state is
-// cleared so that it does not surface later as the failure of an unrelated launch.
-static int hip_fail(const char* what, hipError_t e) {
-  (void)hipGetLastError();
-  return fail(MIQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-}
+// A failed runtime call, reported through the return code (fail() also clears the runtime's
+// last-error state, so it does not surface later as the failure of an unrelated launch).
+static int hip_fail(const char* what, hipError_t e) { return fail(MIQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e)); }
 
 extern "C" int miq_graph_begin(void* stream) {
   MIQ_REQUIRE(stream, MIQ_ERR_INVALID, "graph_begin: capture needs a stream other than the null stream");
