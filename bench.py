@@ -591,7 +591,7 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the token's GEMVs alone and a plain 1 GiB copy, for hardware-counter runs")
     ap.add_argument("--gemv-large", action="store_true", help="only the GEMV operator on 7B-class shapes")
-    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "moe", "config0", "decode7b"],
+    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "moe", "config0", "decode7b", "ggml"],
                     help="one kernel benchmark and a plain 1 GiB copy, for profiler runs")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the persistent decode step and a plain 1 GiB copy, for hardware-counter runs")
@@ -614,7 +614,8 @@ def main():
     if a.only:
         fn = {"gemm": lambda: gemm_bench(torch, core, Ms=(512,)), "gemm_int8": lambda: gemm_int8_bench(torch, core),
               "q4k": lambda: q4k_bench(torch, core), "moe": lambda: moe_bench(torch, core),
-              "config0": lambda: config0_bench(torch, core), "decode7b": lambda: decode_7b(torch, llm)}[a.only]
+              "config0": lambda: config0_bench(torch, core), "decode7b": lambda: decode_7b(torch, llm),
+              "ggml": lambda: {t: ggml_bench(torch, core, t) for t in ("Q6_K", "Q8_0")}}[a.only]
         out = {a.only: fn()}
         copy_bytes = copy_calibration(torch)
         out.update({"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes})
