@@ -45,7 +45,7 @@ constexpr size_t kMaxFixCols = kFixMaxWords;
 // share the step's A fragment: MFMA t's column l & 15 is the lane's column 4 (l & 15) + t. Each
 // lane thus holds whole column results for 4 columns; no reduction across waves is needed.
 #ifndef MIQ_GM_WPC
-#define MIQ_GM_WPC 4  // workgroups per CU the planner aims for
+#define MIQ_GM_WPC 4  // workgroups resident per CU in the planner's cost (one per SIMD each)
 #endif
 #ifndef MIQ_GM_DEPTH
 #define MIQ_GM_DEPTH 4  // steps of codes in flight per wave (0: all of the slice, issued at entry)
@@ -254,23 +254,38 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Launch shape: ~4 workgroups per CU, K-slices of a multiple of 4 steps (whole groups), at most
-// 24 steps and 32 slices; SPQ is the slice length rounded up to an instantiated capacity.
+// Launch shape: K-slices of a multiple of 4 steps (whole groups), at most 24 steps and 32
+// slices, chosen by a cost in steps per CU: the rounds of workgroups over MIQ_GM_WPC per CU times
+// (slice steps + kWgSteps, the per-workgroup cost of staging and reduction in step units); on a
+// tie the longer slice. A shape whose workgroups just overflow one round (3584 -> 37888 at 16
+// steps: 1036 workgroups for 1024 places) takes longer slices instead (20 steps: 888). SPQ is
+// the slice length rounded up to an instantiated capacity.
 struct Plan {
   int tiles, kslices, slice_steps, spq;
   bool fixed;  // split K reduced in fixed-point words of the counter region
   size_t ws_bytes;
 };
 
+constexpr int kWgSteps = 8;
+
 static bool plan(int K, int N, Plan* p) {
   const int steps = K / 32;
   p->tiles = (N + 255) / 256;
-  int ks = (MIQ_GM_WPC * kCUs + p->tiles - 1) / p->tiles;
-  ks = std::max(ks, (steps + 15) / 16);
-  ks = std::min(ks, std::min(kMaxSlices, steps / 4));
-  int ss = (steps + ks - 1) / ks;
-  ss = (ss + 3) & ~3;
-  if (ss > 24) return false;
+  const long slots = (long)MIQ_GM_WPC * kCUs;
+  int ss = 0;
+  long best = 0;
+  for (int c = 4; c <= 24; c += 4) {
+    const int ks = (steps + c - 1) / c;
+    if (ks <= kMaxSlices) {
+      const long cost = (((long)p->tiles * ks + slots - 1) / slots) * (c + kWgSteps);
+      if (!ss || cost <= best) {
+        ss = c;
+        best = cost;
+      }
+    }
+    if (c >= steps) break;  // one slice already covers K
+  }
+  if (!ss) return false;
   p->slice_steps = ss;
   p->kslices = (steps + ss - 1) / ss;
   if (p->kslices > kMaxSlices || (p->kslices > 1 && p->tiles > kMaxCounters)) return false;
