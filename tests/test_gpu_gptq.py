@@ -119,9 +119,9 @@ def test_act_order_gemv(gpu, M):
 
 
 @pytest.mark.parametrize("K,N,xdt,sdt,zoff,bias", [
-    (4096, 11008, np.float16, "f16", 1.0, False),   # 6 K-slices
-    (11008, 4096, np.float32, "f16", 1.0, True),    # 16 K-slices of 22 steps
-    (896, 65536, np.float32, "f32", 0.0, False),    # one K-slice (a tied-head shape)
+    (4096, 11008, np.float16, "f16", 1.0, False),   # a 7B up projection
+    (11008, 4096, np.float32, "f16", 1.0, True),    # a 7B down projection (344 steps of K)
+    (896, 65536, np.float32, "f32", 0.0, False),    # a tied-head shape
     (2048, 4096, np.float16, "f32", 1.0, True),
 ])
 def test_large_gemv_matrix_core_path(gpu, K, N, xdt, sdt, zoff, bias):
@@ -147,7 +147,8 @@ def test_large_gemv_matrix_core_path(gpu, K, N, xdt, sdt, zoff, bias):
 
 
 @pytest.mark.parametrize("mode,K,N,big", [(1, 3584, 4608, False), (1, 896, 9728, False), (2, 18944, 3584, False),
-                                         (2, 4864, 896, False), (1, 1024, 512, True), (2, 512, 768, True)])
+                                         (2, 4864, 896, False), (1, 1024, 512, True), (2, 512, 768, True),
+                                         (1, 3584, 37888, False)])
 def test_fused_gemv_matrix_core_path(gpu, mode, K, N, big):
     """One row through miq_gptq_gemv_fused on the matrix-core GEMV: RMSNorm (mode 1, the row's
     mean square over all K in every workgroup, x * w staged, partials divided by r) and SwiGLU
