@@ -344,6 +344,10 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   // matrices (columns past N, the chunk after the last), so no branch surrounds them and the
   // compiler's wait counts stay exact; such values are never used.
   constexpr int XCN = kMoeBM * KC / 8;  // 8-value activation pieces per chunk
+  // An activation row of a chunk is KC / 8 16-byte pieces; piece c of row r sits in slot
+  // c ^ (r % CPR), so that the 16 rows one MFMA operand read touches fall in different banks
+  // (unswizzled, rows KC * 2 bytes apart map to the same banks).
+  constexpr int CPR = KC / 8;
   constexpr int XCH = (XCN + 255) / 256;  // per thread
   const int ncl = min(ncol, N - 4);
   size_t xsrc[XCH];  // element offset of each piece's row
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
     const int rr = min(r, nrows - 1);
     const size_t row = (size_t)row_id(rr);
     xsrc[j] = row * K + kk;
-    xdst[j] = ci < XCN ? r * KC + kk : -1;
+    xdst[j] = ci < XCN ? r * KC + (((kk >> 3) ^ (r % CPR)) << 3) : -1;
     xz[j] = r >= nrows;
     xrs[j] = XF32 ? row_scale(row_max[row]) : 1.f;
   }
@@ -443,7 +447,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
         for (int pl = 0; pl < NA; ++pl)
 #pragma unroll
           for (int t = 0; t < TM; ++t) {
-            const half8v af = *reinterpret_cast<const half8v*>(xs[pl] + (16 * t + p) * KC + st * 32 + 8 * kb);
+            const int row = 16 * t + p;
+            const half8v af = *reinterpret_cast<const half8v*>(xs[pl] + row * KC + (((st * 4 + kb) ^ (row % CPR)) << 3));
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4)
               part[t][s4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[s4], part[t][s4], 0, 0, 0);
