@@ -93,9 +93,14 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
                                                        int M, int K, int N) {
   constexpr bool kHalf = std::is_same<XT, __half>::value;
   extern __shared__ __align__(16) unsigned char lds_raw[];
+  // Each 64-value group of x sits in LDS with 16 bytes of padding after it (QG elements per
+  // group): lane (slot, q) reads group 4 (pass 16 + slot) + q, and unpadded those groups lie
+  // a multiple of 128 (fp16) or 256 (fp32) bytes apart, all on the same banks.
+  constexpr int QG = kHalf ? 72 : 68;
+  const int rowq = K / 64 * QG;  // elements per staged row
   _Float16* xs_h = reinterpret_cast<_Float16*>(lds_raw);
   float* xs_f = reinterpret_cast<float*>(lds_raw);
-  float* xsum = reinterpret_cast<float*>(lds_raw + (size_t)MR * K * (kHalf ? 2 : 4));
+  float* xsum = reinterpret_cast<float*>(lds_raw + (size_t)MR * rowq * (kHalf ? 2 : 4));
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -153,11 +158,11 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
       // activations c0..c0+7 of a 64-wide group land in code words wq and wq+1 (wq = (c0 % 32) / 4)
       // at slots 4h..4h+3 (h = c0 / 32), in the order (x0, x2, x1, x3)
       const int c0 = k & 63, h = c0 >> 5, wq = (c0 & 31) >> 2;
-      _Float16* base = xs_h + (size_t)m * K + (k & ~63) + wq * 8 + h * 4;
+      _Float16* base = xs_h + (size_t)m * rowq + (k >> 6) * QG + wq * 8 + h * 4;
       *reinterpret_cast<uint2*>(base) = make_uint2(pack_h2(v[0], v[2]), pack_h2(v[1], v[3]));
       *reinterpret_cast<uint2*>(base + 8) = make_uint2(pack_h2(v[4], v[6]), pack_h2(v[5], v[7]));
     } else {
-      float4* d = reinterpret_cast<float4*>(xs_f + (size_t)m * K + k);
+      float4* d = reinterpret_cast<float4*>(xs_f + (size_t)m * rowq + (k >> 6) * QG + (k & 63));
       d[0] = make_float4(v[0], v[1], v[2], v[3]);
       d[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
@@ -181,7 +186,7 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
           const float sA = xsum[m * (K / 32) + kb / 32], sB = xsum[m * (K / 32) + kb / 32 + 1];
           if constexpr (kHalf) {
             half2v xv[8][4];
-            const uint4* xp = reinterpret_cast<const uint4*>(xs_h + (size_t)m * K + kb);
+            const uint4* xp = reinterpret_cast<const uint4*>(xs_h + (size_t)m * rowq + (kb >> 6) * QG);
 #pragma unroll
             for (int wq = 0; wq < 8; ++wq) {
               const uint4 t = xp[wq];
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
               acc[m][r] += fmaf(-s.m2, sB, t);
             }
           } else {
-            const float* xf = xs_f + (size_t)m * K + kb;
+            const float* xf = xs_f + (size_t)m * rowq + (kb >> 6) * QG;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
               const int n = grp * R + r;
@@ -278,7 +283,7 @@ template <int R, int MR, typename XT, typename OT>
 static int launch_q4k(const void* x, const uint8_t* w, const float* bias, void* out, int M, int K, int N,
                       hipStream_t st) {
   auto kern = q4k_gemv_kernel<R, MR, XT, OT>;
-  const size_t lds = (size_t)MR * K * sizeof(XT) + (size_t)MR * (K / 32) * 4;
+  const size_t lds = (size_t)MR * (K / 64) * (std::is_same<XT, __half>::value ? 144 : 272) + (size_t)MR * (K / 32) * 4;
   MIQ_REQUIRE(lds <= 160 * 1024, MIQ_ERR_UNSUPPORTED, "q4k_gemv: K=%d too large to stage", K);
   if (lds > 64 * 1024) {
     const int rc = require_lds("q4k_gemv", lds);
