@@ -38,7 +38,11 @@ __device__ __forceinline__ int opaque_tid() {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kStepBytes = 256;
+// LDS bytes per staged 32-k step: 4 k-blocks of 3 rows x 16 bytes = 192 bytes of A, laid out
+// 64 bytes per k-block and padded to 272 so that the 16 staging threads of a phase (four steps
+// of four k-blocks) write 16 different bank groups (at 256 they wrote 4: 415.2 -> 410.6 us per
+// Qwen2-0.5B decode token).
+constexpr int kStepBytes = 272;
 
 // The B fragment of one packed word: halves (c0, c4) (8 c1, 8 c5) (c2, c6) (8 c3, 8 c7) over 128,
 // three shifts and four v_and_or_b32. Written in C++ so that the compiler's hazard tracking
