@@ -164,7 +164,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs
                                                    const uint8_t* __restrict__ w, float* __restrict__ y, int Mx, int K,
                                                    int N, int mtiles) {
   __shared__ __align__(16) __half at[2][kBM * 256];  // activation tiles, 16-byte chunks swizzled by row
-  __shared__ __align__(16) float rt[2][8 * kBM];     // sub-block sums [sub-block][row]
+  // sub-block sums [sub-block][row], rows of kRT floats: the lanes of one read take rows p and
+  // sub-blocks kb, and at 64 floats (256 bytes) per sub-block the four kb share their banks
+  constexpr int kRT = kBM + 16;
+  __shared__ __align__(16) float rt[2][8 * kRT];
   const int T = (int)gridDim.x, L = (int)blockIdx.x;
   const int Lp = T % kXCDs == 0 ? (L % kXCDs) * (T / kXCDs) + L / kXCDs : L;
   const int mt = Lp % mtiles, nt = Lp / mtiles;
@@ -187,7 +190,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int sb = wave * 2 + i;
-      dma4(rs + (size_t)min(m0 + lane, Mx - 1) * K32 + s * 8 + sb, uniform((int)(rbase + sb * 256)));
+      dma4(rs + (size_t)min(m0 + lane, Mx - 1) * K32 + s * 8 + sb, uniform((int)(rbase + sb * kRT * 4)));
     }
   };
   uint4 hdr, hdr_n;
@@ -236,8 +239,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs
       scale_min(hdr.y, hdr.z, hdr.w, 4 + kb, &sc, &m_hi);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[kb * kBM + 16 * t + p], (float)m_lo, Q[t], 0, 0, 0);
-        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[(4 + kb) * kBM + 16 * t + p], (float)m_hi, Q[t], 0, 0, 0);
+        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[kb * kRT + 16 * t + p], (float)m_lo, Q[t], 0, 0, 0);
+        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[(4 + kb) * kRT + 16 * t + p], (float)m_hi, Q[t], 0, 0, 0);
       }
     }
     const float d = __half2float(__ushort_as_half((unsigned short)(hdr.x & 0xFFFFu)));
