@@ -231,3 +231,39 @@ def test_errors_are_raised(gpu):
                              None, 30, 8, 30, 8, 32, 4)
     with pytest.raises(ValueError, match="g_idx"):
         core.act_order_perm(np.zeros(64, np.int32), 32)
+
+
+def _random_gemv_cases(n=14, seed=2026):
+    """Seeded one-row GEMV cases over the shapes the matrix-core planner handles differently:
+    K from one group to 64 groups (one to 32 K-slices, every slice capacity), N from one
+    packed word to past 16k columns (ragged last tiles), both activation and scale dtypes, both
+    zero offsets, with and without bias."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        K = 128 * int(rng.choice([1, 2, 3, 7, 8, 28, 29, 32, 43, 64]))
+        N = 8 * int(rng.integers(1, 40) if i % 2 else rng.integers(500, 2200))
+        cases.append((i, K, N, bool(rng.integers(2)), str(rng.choice(["f16", "f32"])), float(rng.integers(2)),
+                      bool(rng.integers(2))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_gemv_cases(), ids=lambda c: "K%d-N%d" % (c[1], c[2]))
+def test_gemv_random_shapes(gpu, case):
+    """One row through the drop-in GEMV (matrix-core path for gs 128) against the oracle's
+    numpy-fallback product, on seeded random shapes, dtypes, zero offsets and biases."""
+    import torch
+    from webpytorch_amd import core
+    i, K, N, xf16, sdt, zoff, bias = case
+    L = synth.gptq_layer(300 + i, K, N, 128, 4)
+    sc = L["scales"] if sdt == "f16" else L["scales"].astype(np.float32) * np.float32(0.83)
+    x = synth.activations(400 + i, 1, K, np.float16 if xf16 else np.float32)
+    b = np.linspace(-0.5, 0.5, N).astype(np.float32) if bias else None
+    ref = gptq.gptq_matmul_np(x.astype(np.float32), L["qweight"], L["qzeros"], sc, K, N, 128, 4, zoff)
+    if b is not None:
+        ref = ref + b
+    got = core._gptq_matmul(torch.from_numpy(x).cuda(), core.to_device(L["qweight"]), core.to_device(L["qzeros"]),
+                            core.to_device(sc), K, N, 128, 4, zoff,
+                            bias=None if b is None else core.to_device(b), out_dtype=torch.float32).cpu().numpy()
+    _close(got, ref)
+    assert _rel(got, ref) < 1e-5
