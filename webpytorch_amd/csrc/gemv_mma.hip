@@ -44,9 +44,6 @@ constexpr size_t kMaxFixCols = kFixMaxWords;
 // step (a wave load covers 4 rows x 256 contiguous bytes), and feeds them to four MFMAs that
 // share the step's A fragment: MFMA t's column l & 15 is the lane's column 4 (l & 15) + t. Each
 // lane thus holds whole column results for 4 columns; no reduction across waves is needed.
-#ifndef MIQ_GM_WPC
-#define MIQ_GM_WPC 4  // workgroups resident per CU in the planner's cost (one per SIMD each)
-#endif
 #ifndef MIQ_GM_DEPTH
 #define MIQ_GM_DEPTH 4  // steps of codes in flight per wave (0: all of the slice, issued at entry)
 #endif
@@ -255,11 +252,14 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
 }
 
 // Launch shape: K-slices of a multiple of 4 steps (whole groups), at most 24 steps and 32
-// slices, chosen by a cost in steps per CU: the rounds of workgroups over MIQ_GM_WPC per CU times
-// (slice steps + kWgSteps, the per-workgroup cost of staging and reduction in step units); on a
-// tie the longer slice. A shape whose workgroups just overflow one round (3584 -> 37888 at 16
-// steps: 1036 workgroups for 1024 places) takes longer slices instead (20 steps: 888). SPQ is
-// the slice length rounded up to an instantiated capacity.
+// slices, chosen by a cost in steps per CU: the workgroups a CU runs (rounded up over the CUs)
+// times (slice steps + kWgSteps, the per-workgroup cost of staging and reduction in step units),
+// and a quarter more per 8 slice steps when a CU runs a single workgroup (its waves have no
+// partner to overlap their loads and arithmetic with); on a tie the longer slice. Measured over
+// slice lengths on 12 shapes of the 0.5B and 7B decoders (a one-row activation), this picks the
+// fastest or within 2.5% on each; the earlier rule (four workgroups per CU) left 3584 -> 37888
+// 12 workgroups over a round (16.6 us at 16 steps against 15.2 us at 24) and 3584 -> 4608 at
+// 4 steps (4.5 us against 4.4 at 8). SPQ is the slice length rounded up to an instantiated capacity.
 struct Plan {
   int tiles, kslices, slice_steps, spq;
   bool fixed;  // split K reduced in fixed-point words of the counter region
@@ -271,13 +271,13 @@ constexpr int kWgSteps = 8;
 static bool plan(int K, int N, Plan* p) {
   const int steps = K / 32;
   p->tiles = (N + 255) / 256;
-  const long slots = (long)MIQ_GM_WPC * kCUs;
   int ss = 0;
   long best = 0;
   for (int c = 4; c <= 24; c += 4) {
     const int ks = (steps + c - 1) / c;
     if (ks <= kMaxSlices) {
-      const long cost = (((long)p->tiles * ks + slots - 1) / slots) * (c + kWgSteps);
+      const long per_cu = ((long)p->tiles * ks + kCUs - 1) / kCUs;
+      const long cost = per_cu * (c + kWgSteps) * (per_cu == 1 ? 32 + c : 32);
       if (!ss || cost <= best) {
         ss = c;
         best = cost;
