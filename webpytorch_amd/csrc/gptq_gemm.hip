@@ -84,8 +84,8 @@ template <int BITS> __device__ __forceinline__ uint4 pair_order8(uint4 v) {
 //
 // One workgroup per row of x; every thread issues four 16-byte loads before it stores anything.
 // With perm (act-order columns), the row goes to LDS first (coalesced) and each output chunk
-// gathers its 8 values from there through its 8 permutation indices, which are loaded while the
-// row is in flight. Grid (M), dynamic LDS 2 K bytes with perm.
+// gathers its 8 values from there through its 8 permutation indices, which are loaded before
+// the row. Grid (M), dynamic LDS 2 K bytes with perm.
 template <int BITS, bool PERM>
 __global__ __launch_bounds__(256) void stage_rows_kernel(const __half* __restrict__ x, const int32_t* __restrict__ perm,
                                                          __half* __restrict__ xp, int M, int K, int KC) {
@@ -98,6 +98,19 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const __half* __restric
     return reinterpret_cast<uint4*>(xp + ((size_t)(k / KC) * M + m) * KC + k % KC);
   };
   if constexpr (PERM) {
+    // rows up to 256 U chunks (K <= 8192) keep their permutation indices in registers across
+    // the barrier; longer rows reload them per pass
+    const int4* p4 = reinterpret_cast<const int4*>(perm);
+    int4 pa[U], pb[U];
+    auto load_perm = [&](int q0) {
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int i = min(q0 + 256 * j, nch - 1);
+        pa[j] = p4[2 * i];
+        pb[j] = p4[2 * i + 1];
+      }
+    };
+    load_perm(threadIdx.x);
     for (int q0 = threadIdx.x; q0 < nch; q0 += 256 * U) {
       uint4 v[U];
 #pragma unroll
@@ -107,15 +120,8 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const __half* __restric
         if (q0 + 256 * j < nch) reinterpret_cast<uint4*>(srow)[q0 + 256 * j] = v[j];
     }
     __syncthreads();
-    const int4* p4 = reinterpret_cast<const int4*>(perm);
     for (int q0 = threadIdx.x; q0 < nch; q0 += 256 * U) {
-      int4 pa[U], pb[U];
-#pragma unroll
-      for (int j = 0; j < U; ++j) {
-        const int i = min(q0 + 256 * j, nch - 1);
-        pa[j] = p4[2 * i];
-        pb[j] = p4[2 * i + 1];
-      }
+      if (q0 != (int)threadIdx.x) load_perm(q0);
 #pragma unroll
       for (int j = 0; j < U; ++j) {
         if (q0 + 256 * j >= nch) break;
