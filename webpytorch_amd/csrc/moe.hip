@@ -13,7 +13,7 @@
 // The combine order (experts ascending, starting from zero) and the fp32 weight multiply are the
 // reference's (`webtorch/lm_engine.py:294-333`). The GEMMs use the prefill GEMM's exact
 // dequantization and MFMA mapping (see gptq_gemm.hip); a workgroup takes one row tile of one
-// expert (up to kMoeBM rows) and 256 (down) or 128 (gate_up) output columns.
+// expert (up to kMoeBM rows) and 512 (down) or 128 (gate_up) output columns.
 //
 // fp32 activations (the intermediate h always; x when the caller's is fp32) go through the fp16
 // matrix cores as two fp16 planes of a row scaled by a power of two: v = a * 2^s with s chosen so
@@ -33,6 +33,11 @@ namespace miq {
 constexpr int kMoeBM = 32;      // rows per tile (two 16-row MFMA blocks)
 constexpr int kMoeMaxTK = 4096;  // T * k handled by the single-workgroup router
 constexpr int kSlotWaves = 16;   // waves of the slot kernel (1024 threads), one chunk of picks each
+// waves per grouped-GEMM workgroup (measured: eight down waves sharing a staged h chunk cut
+// the down GEMM 44.4 -> 43.2 us at T = 256, H = 2048, 128 experts; eight gate_up waves made it
+// slower, 56.8 -> 62.4 us)
+constexpr int kMoeWavesGateUp = 4;
+constexpr int kMoeWavesDown = 8;
 
 // Offsets (in 4-byte words) of the route buffer's arrays.
 struct RouteLayout {
@@ -288,9 +293,11 @@ __global__ __launch_bounds__(1024) void moe_slots_kernel(int T, int E, int k, in
 // gathered through the sorted slots), epilogue h = silu(g) * u in fp32 plus each row's max |h|.
 // Otherwise (down): one set over h, epilogue y = w[slot] * acc in fp32. XF32: the activations
 // are fp32 and are staged as the row-scaled fp16 hi and lo planes (two MFMAs per weight
-// fragment); else (gate_up with fp16 x) they are staged as they are.
-template <int BITS, int KC, bool GATE_UP, bool XF32, typename ST>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(
+// fragment); else (gate_up with fp16 x) they are staged as they are. NW waves share each staged
+// activation chunk: 64 columns each (gate_up: half the waves gate, half up, 64 columns of each
+// per pair), so more waves per workgroup read the activation rows fewer times.
+template <int BITS, int KC, bool GATE_UP, bool XF32, typename ST, int NW>
+__global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
     const void* __restrict__ a_in, int* __restrict__ route, int T, int E, int k,
     const uint32_t* __restrict__ qw0, const uint32_t* __restrict__ qz0, const ST* __restrict__ sc0,
     const uint32_t* __restrict__ qw1, const uint32_t* __restrict__ qz1, const ST* __restrict__ sc1,
@@ -300,8 +307,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   constexpr int TM = kMoeBM / 16;
   constexpr int STEPS = KC / 32;
   constexpr int RB = BITS == 4 ? 1 : 2;
-  constexpr int NSET = 1;  // weight sets per wave (gate_up: waves 0-1 gate, 2-3 up)
-  constexpr int WCOLS = GATE_UP ? 128 : 256;  // columns per workgroup
+  constexpr int NSET = 1;  // weight sets per wave (gate_up: the first NW / 2 waves gate, the rest up)
+  constexpr int NT = 64 * NW;
+  constexpr int WCOLS = (GATE_UP ? 32 : 64) * NW;  // columns per workgroup
   constexpr int NA = XF32 ? 2 : 1;            // activation planes (hi and lo)
   constexpr int XW = XF32 ? 2 : 1;            // 16-byte words per 8-value piece
   static_assert(GATE_UP || XF32, "the down projection reads fp32 h");
@@ -321,7 +329,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int p = lane & 15, kb = lane >> 4;
-  const int cw = GATE_UP ? (wave & 1) : wave, set = GATE_UP ? (wave >> 1) : 0;
+  const int cw = GATE_UP ? wave % (NW / 2) : wave, set = GATE_UP ? wave / (NW / 2) : 0;
   const int ncol = blockIdx.x * WCOLS + cw * 64 + 4 * p;
   const bool colok = ncol < N;
   const bool wave_active = blockIdx.x * WCOLS + cw * 64 < N;
@@ -348,7 +356,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   // c ^ (r % CPR), so that the 16 rows one MFMA operand read touches fall in different banks
   // (unswizzled, rows KC * 2 bytes apart map to the same banks).
   constexpr int CPR = KC / 8;
-  constexpr int XCH = (XCN + 255) / 256;  // per thread
+  constexpr int XCH = (XCN + NT - 1) / NT;  // per thread
   const int ncl = min(ncol, N - 4);
   size_t xsrc[XCH];  // element offset of each piece's row
   int xdst[XCH];     // its LDS offset (row, k) in each plane, -1: none
@@ -356,7 +364,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
   float xrs[XCH];    // its row scale (fp32 activations)
 #pragma unroll
   for (int j = 0; j < XCH; ++j) {
-    const int ci = threadIdx.x + 256 * j;
+    const int ci = threadIdx.x + NT * j;
     const int cc = min(ci, XCN - 1);
     const int r = cc / (KC / 8), kk = (cc - r * (KC / 8)) * 8;
     const int rr = min(r, nrows - 1);
@@ -483,7 +491,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(
 
   if constexpr (GATE_UP) {
     // the up waves hand their sums to the gate waves of the same columns through LDS
-    __shared__ float4v ux[2][TM][4][64];
+    __shared__ float4v ux[NW / 2][TM][4][64];
     if (set == 1)
 #pragma unroll
       for (int t = 0; t < TM; ++t)
@@ -558,15 +566,17 @@ static int launch_moe_gemm(const void* a, int* route, int T, int E, int k, const
   const RouteLayout L = route_layout(T, E, k);
   const int per = 32 / BITS;
   const size_t qws = (size_t)(K / per) * N, qzs = (size_t)(K / gs) * (N / per), scs = (size_t)(K / gs) * N;
-  dim3 grid(GATE_UP ? (N + 127) / 128 : (N + 255) / 256, L.max_tiles);
+  constexpr int NW = GATE_UP ? kMoeWavesGateUp : kMoeWavesDown;
+  constexpr int WCOLS = (GATE_UP ? 32 : 64) * NW;
+  dim3 grid((N + WCOLS - 1) / WCOLS, L.max_tiles);
   const uint32_t *w0 = reinterpret_cast<const uint32_t*>(qw0), *z0 = reinterpret_cast<const uint32_t*>(qz0);
   const uint32_t *w1 = reinterpret_cast<const uint32_t*>(qw1), *z1 = reinterpret_cast<const uint32_t*>(qz1);
   if (sdt == MIQ_F16)
-    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, __half>), grid, dim3(256), 0, st, a, route, T, E, k,
+    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, __half, NW>), grid, dim3(64 * NW), 0, st, a, route, T, E, k,
                        w0, z0, static_cast<const __half*>(sc0), w1, z1, static_cast<const __half*>(sc1), qws, qzs,
                        scs, out, K, N, gs, zoff);
   else
-    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, float>), grid, dim3(256), 0, st, a, route, T, E, k,
+    hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, float, NW>), grid, dim3(64 * NW), 0, st, a, route, T, E, k,
                        w0, z0, static_cast<const float*>(sc0), w1, z1, static_cast<const float*>(sc1), qws, qzs, scs,
                        out, K, N, gs, zoff);
   return check_launch(GATE_UP ? "moe_gate_up" : "moe_down");
