@@ -313,7 +313,7 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
   constexpr int NA = XF32 ? 2 : 1;            // activation planes (hi and lo)
   constexpr int XW = XF32 ? 2 : 1;            // 16-byte words per 8-value piece
   static_assert(GATE_UP || XF32, "the down projection reads fp32 h");
-  __shared__ __align__(16) _Float16 xs[NA][kMoeBM * KC];
+  __shared__ __align__(16) _Float16 xs[2][NA][kMoeBM * KC];  // chunks alternate between two buffers
 
   const RouteLayout L = route_layout(T, E, k);
   const int tile = blockIdx.y;
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
       return make_uint4((w.x & 0xFFFFu) | (w.y << 16), (w.x >> 16) | (w.y & 0xFFFF0000u),
                         (w.z & 0xFFFFu) | (w.w << 16), (w.z >> 16) | (w.w & 0xFFFF0000u));
   };
-  auto stage = [&](const Chunk& c) {
+  auto stage = [&](const Chunk& c, int b) {
 #pragma unroll
     for (int j = 0; j < XCH; ++j) {
       if (xdst[j] < 0) continue;
@@ -428,15 +428,15 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
           lo[i] = (uint32_t)__half_as_ushort(__float2half_rn(v0 - __half2float(h0))) |
                   ((uint32_t)__half_as_ushort(__float2half_rn(v1 - __half2float(h1))) << 16);
         }
-        *reinterpret_cast<uint4*>(&xs[0][0] + xdst[j]) = pair_order(make_uint4(hi[0], hi[1], hi[2], hi[3]));
-        *reinterpret_cast<uint4*>(&xs[NA - 1][0] + xdst[j]) = pair_order(make_uint4(lo[0], lo[1], lo[2], lo[3]));
+        *reinterpret_cast<uint4*>(&xs[b][0][0] + xdst[j]) = pair_order(make_uint4(hi[0], hi[1], hi[2], hi[3]));
+        *reinterpret_cast<uint4*>(&xs[b][NA - 1][0] + xdst[j]) = pair_order(make_uint4(lo[0], lo[1], lo[2], lo[3]));
       } else {
-        *reinterpret_cast<uint4*>(&xs[0][0] + xdst[j]) =
+        *reinterpret_cast<uint4*>(&xs[b][0][0] + xdst[j]) =
             pair_order(xz[j] ? make_uint4(0u, 0u, 0u, 0u) : c.xv[j][0]);
       }
     }
   };
-  auto multiply = [&](const Chunk& c) {
+  auto multiply = [&](const Chunk& c, int b) {
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
       half2v zl[4], zh[4];
@@ -456,7 +456,7 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
 #pragma unroll
           for (int t = 0; t < TM; ++t) {
             const int row = 16 * t + p;
-            const half8v af = *reinterpret_cast<const half8v*>(xs[pl] + row * KC + (((st * 4 + kb) ^ (row % CPR)) << 3));
+            const half8v af = *reinterpret_cast<const half8v*>(xs[b][pl] + row * KC + (((st * 4 + kb) ^ (row % CPR)) << 3));
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4)
               part[t][s4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[s4], part[t][s4], 0, 0, 0);
@@ -472,13 +472,15 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
           for (int r = 0; r < 4; ++r) acc[q][t][s4][r] = fmaf(sf[s4], part[t][s4][r], acc[q][t][s4][r]);
     }
   };
-  // chunk i is multiplied while chunks i + 1 and i + 2 are in flight (three register sets)
+  // chunk i is multiplied while chunks i + 1 and i + 2 are in flight (three register sets). It
+  // is staged in LDS buffer i % 2, last read by chunk i - 2's multiply, which every wave has
+  // finished once it passed chunk i - 1's barrier: one barrier per chunk.
   auto iter = [&](int kc0, Chunk& cur, Chunk& ahead2) {
-    __syncthreads();  // the previous chunk's activation reads are done
-    stage(cur);
+    const int b = (kc0 / KC) & 1;
+    stage(cur, b);
     __syncthreads();
     load_chunk(min(kc0 + 2 * KC, K - KC), ahead2);
-    if (wave_active) multiply(cur);
+    if (wave_active) multiply(cur, b);
   };
   Chunk c0, c1, c2;
   load_chunk(0, c0);
