@@ -101,6 +101,57 @@ __global__ __launch_bounds__(256) void moe_xmax_kernel(const float* __restrict__
 // each expert's picks (LDS atomics: sums do not depend on order), turns the counts into offsets
 // and row tiles (prefix sums over the experts), and then one wave walks the picks in order and
 // hands out each expert's slots, so each expert's rows are in ascending token order.
+// Float64 (value, expert) steps within each row of 16 lanes by DPP moves (quad_perm [1,0,3,2],
+// [2,3,0,1], row_half_mirror, row_mirror), then the four row results by v_readlane. Maximum and
+// arg-max (larger value, then smaller expert) are exact in any pairing, so every lane ends with
+// the value a butterfly of shuffles would give. All 64 lanes active.
+template <int CTRL> __device__ __forceinline__ double dpp_move_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double lane_at_f64(double v, int l) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_max_f64(double v) {
+  v = fmax(v, dpp_move_f64<0xB1>(v));
+  v = fmax(v, dpp_move_f64<0x4E>(v));
+  v = fmax(v, dpp_move_f64<0x141>(v));
+  v = fmax(v, dpp_move_f64<0x140>(v));
+  return fmax(fmax(lane_at_f64(v, 0), lane_at_f64(v, 16)), fmax(lane_at_f64(v, 32), lane_at_f64(v, 48)));
+}
+template <int CTRL> __device__ __forceinline__ void pick_step(double& b, int& e) {
+  const double ob = dpp_move_f64<CTRL>(b);
+  const int oe = __builtin_amdgcn_update_dpp(0, e, CTRL, 0xF, 0xF, false);
+  if (ob > b || (ob == b && oe < e)) {
+    b = ob;
+    e = oe;
+  }
+}
+__device__ __forceinline__ void wave_pick(double& b, int& e) {
+  pick_step<0xB1>(b, e);
+  pick_step<0x4E>(b, e);
+  pick_step<0x141>(b, e);
+  pick_step<0x140>(b, e);
+  double bb = lane_at_f64(b, 0);
+  int be = __builtin_amdgcn_readlane(e, 0);
+#pragma unroll
+  for (int r = 16; r < 64; r += 16) {
+    const double ob = lane_at_f64(b, r);
+    const int oe = __builtin_amdgcn_readlane(e, r);
+    if (ob > bb || (ob == bb && oe < be)) {
+      bb = ob;
+      be = oe;
+    }
+  }
+  b = bb;
+  e = be;
+}
+
 template <int EPL>  // experts per lane: E <= 64 * EPL
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                        int norm_topk, int* __restrict__ route) {
@@ -120,8 +171,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
       pv[i] = e < E ? (double)lt[e] : -INFINITY;
       mx = fmax(mx, pv[i]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+    mx = wave_max_f64(mx);
     double sum = 0.0;
 #pragma unroll
     for (int i = 0; i < EPL; ++i)
@@ -152,12 +202,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
           best = pv[i];
           be = lane + 64 * i;
         }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const double ob = __shfl_xor(best, o, 64);
-        const int oe = __shfl_xor(be, o, 64);
-        if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; }
-      }
+      wave_pick(best, be);
 #pragma unroll
       for (int i = 0; i < EPL; ++i)
         if (lane + 64 * i == be) pv[i] = -1.0;
@@ -170,7 +215,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
     }
     // ascending expert order: a pick's rank is the number of picks with a smaller expert
     int rank = 0;
-    for (int i = 0; i < k; ++i) rank += __shfl(my_e, i, 64) < my_e;
+    for (int i = 0; i < k; ++i) rank += __builtin_amdgcn_readlane(my_e, i) < my_e;
     if (lane < k) {
       topk_e[t * k + rank] = my_e;
       topk_w[t * k + rank] = (float)(norm_topk ? my_p / psum : my_p);
