@@ -19,12 +19,13 @@
 // v_and_or_b32 takes the nibbles of bytes 0 and 2, then of bytes 1 and 3); rs[r][k / 32] the
 // sub-block sums of the staged fp16 values (fp32).
 //
-// Tiles: a workgroup of 4 waves computes 64 rows x 64 columns; wave w takes columns 16 w .. +15
-// and all 64 rows (four 16-row MFMA tiles). K is walked one super-block (256 weights) at a
-// time: the 64 x 256 activation tile sits in LDS (16-byte chunks XOR-swizzled by row, so the 16
-// rows that one operand read touches fall in different banks) and each lane holds its column's
-// super-block header and its 4 x 8 code bytes in registers. Workgroups are ordered XCD-major
-// with row tiles fastest, so the row tiles of a column tile share that XCD's L2.
+// Tiles: a workgroup of 4 waves computes 64 rows x 64 CG columns; wave w takes the CG groups of
+// 16 columns from 16 CG w and all 64 rows (four 16-row MFMA tiles per group). K is walked one
+// super-block (256 weights) at a time: the 64 x 256 activation tile sits in LDS (16-byte chunks
+// XOR-swizzled by row, so the 16 rows that one operand read touches fall in different banks)
+// and each lane holds its columns' super-block headers and 4 x 8 code bytes in registers.
+// Workgroups are ordered XCD-major with row tiles fastest, so the row tiles of a column tile
+// share that XCD's L2.
 #include <math.h>
 
 #include <type_traits>
@@ -35,7 +36,8 @@ namespace miq {
 namespace q4g {
 
 constexpr int kXCDs = 8;
-constexpr int kBM = 64, kBN = 64;
+constexpr int kBM = 64;
+constexpr int kCUs = 256;
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
@@ -160,6 +162,7 @@ __device__ __forceinline__ half8v b_codes(uint32_t w0, uint32_t w1) {
 // the row sums arrive by LDS DMA into one of two buffers while the other is multiplied (the
 // swizzle is applied on the source side: DMA lane l of a 1 KB block lands at slot l); each
 // lane's super-block header and code bytes are loaded into registers one super-block ahead.
+template <int CG>
 __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs, const float* __restrict__ rs,
                                                    const uint8_t* __restrict__ w, float* __restrict__ y, int Mx, int K,
                                                    int N, int mtiles) {
@@ -171,12 +174,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs
   const int T = (int)gridDim.x, L = (int)blockIdx.x;
   const int Lp = T % kXCDs == 0 ? (L % kXCDs) * (T / kXCDs) + L / kXCDs : L;
   const int mt = Lp % mtiles, nt = Lp / mtiles;
-  const int m0 = mt * kBM, n0 = nt * kBN;
+  const int m0 = mt * kBM, n0 = nt * 64 * CG;
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6), p = lane & 15, kb = lane >> 4;
-  const int ncol = n0 + 16 * wave + p;
-  const int n = min(ncol, N - 1);  // columns past N repeat the last one and are not stored
   const int nsb = K / 256, K32 = K / 32;
-  const uint8_t* wr = w + (size_t)n * nsb * 144;
+  // wave w takes the column groups CG w .. CG w + CG - 1 (16 columns each); every operand read
+  // of the activation tile feeds one MFMA per group
+  int ncol[CG];
+  const uint8_t* wr[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    ncol[c] = n0 + 16 * (CG * wave + c) + p;
+    const int n = min(ncol[c], N - 1);  // columns past N repeat the last one and are not stored
+    wr[c] = w + (size_t)n * nsb * 144;
+  }
 
   // this wave's share of the copies of super-block s into buffer b: 8 of the tile's 32 KB
   // (two rows per 1 KB block) and 2 of its 8 sub-block-sum columns
@@ -193,71 +203,102 @@ __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs
       dma4(rs + (size_t)min(m0 + lane, Mx - 1) * K32 + s * 8 + sb, uniform((int)(rbase + sb * kRT * 4)));
     }
   };
-  uint4 hdr, hdr_n;
-  uint2 cw[4], cw_n[4];
+  uint4 hdr[CG], hdr_n[CG];
+  uint2 cw[CG][4], cw_n[CG][4];
   auto load_b = [&](int s) __attribute__((always_inline)) {
-    const uint8_t* bp = wr + (size_t)s * 144;
-    hdr_n = *reinterpret_cast<const uint4*>(bp);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) cw_n[g] = *reinterpret_cast<const uint2*>(bp + 16 + 32 * g + 8 * kb);
+    for (int c = 0; c < CG; ++c) {
+      const uint8_t* bp = wr[c] + (size_t)s * 144;
+      hdr_n[c] = *reinterpret_cast<const uint4*>(bp);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) cw_n[c][g] = *reinterpret_cast<const uint2*>(bp + 16 + 32 * g + 8 * kb);
+    }
   };
 
-  float4v acc[4];
+  float4v acc[CG][4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = (float4v){0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < CG; ++c)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[c][t] = (float4v){0.f, 0.f, 0.f, 0.f};
   issue(0, 0);
   load_b(0);
   for (int s = 0; s < nsb; ++s) {
     wait_vmcnt<0>();  // this wave's copies of super-block s (and its header and codes) have landed
     __syncthreads();  // everyone's copies are in; everyone is done with the other buffer
     if (s + 1 < nsb) issue(s + 1, (s + 1) & 1);
-    hdr = hdr_n;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) cw[g] = cw_n[g];
+    for (int c = 0; c < CG; ++c) {
+      hdr[c] = hdr_n[c];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) cw[c][g] = cw_n[c][g];
+    }
     if (s + 1 < nsb) load_b(s + 1);
     const __half* a = at[s & 1];
     const float* r8 = rt[s & 1];
-    float4v P[4], Q[4];
+    float4v P[CG][4], Q[CG][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) P[t] = Q[t] = (float4v){0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < CG; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) P[c][t] = Q[c][t] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
-      uint32_t sc, mn;
-      scale_min(hdr.y, hdr.z, hdr.w, sb, &sc, &mn);
       const int sh = 4 * (sb & 1);
-      const half8v bf = b_codes(cw[sb >> 1].x >> sh, cw[sb >> 1].y >> sh) * (_Float16)(float)sc;
+      half8v bf[CG];
+#pragma unroll
+      for (int c = 0; c < CG; ++c) {
+        uint32_t sc, mn;
+        scale_min(hdr[c].y, hdr[c].z, hdr[c].w, sb, &sc, &mn);
+        bf[c] = b_codes(cw[c][sb >> 1].x >> sh, cw[c][sb >> 1].y >> sh) * (_Float16)(float)sc;
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int r = 16 * t + p;
         const half8v af = *reinterpret_cast<const half8v*>(a + r * 256 + (((4 * sb + kb) ^ (r & 31)) * 8));
-        P[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, P[t], 0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < CG; ++c) P[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c], P[c][t], 0, 0, 0);
       }
     }
     {  // Q = sum over the 8 sub-blocks of rs[row][sb] m[sb][col]: k = kb, then 4 + kb
-      uint32_t sc, m_lo, m_hi;
-      scale_min(hdr.y, hdr.z, hdr.w, kb, &sc, &m_lo);
-      scale_min(hdr.y, hdr.z, hdr.w, 4 + kb, &sc, &m_hi);
+      float m_lo[CG], m_hi[CG];
+#pragma unroll
+      for (int c = 0; c < CG; ++c) {
+        uint32_t sc, mlo, mhi;
+        scale_min(hdr[c].y, hdr[c].z, hdr[c].w, kb, &sc, &mlo);
+        scale_min(hdr[c].y, hdr[c].z, hdr[c].w, 4 + kb, &sc, &mhi);
+        m_lo[c] = (float)mlo;
+        m_hi[c] = (float)mhi;
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[kb * kRT + 16 * t + p], (float)m_lo, Q[t], 0, 0, 0);
-        Q[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(r8[(4 + kb) * kRT + 16 * t + p], (float)m_hi, Q[t], 0, 0, 0);
+        const float rlo = r8[kb * kRT + 16 * t + p], rhi = r8[(4 + kb) * kRT + 16 * t + p];
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+          Q[c][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(rlo, m_lo[c], Q[c][t], 0, 0, 0);
+          Q[c][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(rhi, m_hi[c], Q[c][t], 0, 0, 0);
+        }
       }
     }
-    const float d = __half2float(__ushort_as_half((unsigned short)(hdr.x & 0xFFFFu)));
-    const float dmin = __half2float(__ushort_as_half((unsigned short)(hdr.x >> 16)));
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const float d = __half2float(__ushort_as_half((unsigned short)(hdr[c].x & 0xFFFFu)));
+      const float dmin = __half2float(__ushort_as_half((unsigned short)(hdr[c].x >> 16)));
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[c][t][q] = fmaf(d, P[c][t][q], fmaf(-dmin, Q[c][t][q], acc[c][t][q]));
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    if (ncol[c] >= N) continue;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[t][q] = fmaf(d, P[t][q], fmaf(-dmin, Q[t][q], acc[t][q]));
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + 16 * t + 4 * kb + r;
+        if (row < Mx) y[(size_t)row * N + ncol[c]] = acc[c][t][r];
+      }
   }
-  if (ncol >= N) return;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + 16 * t + 4 * kb + r;
-      if (row < Mx) y[(size_t)row * N + ncol] = acc[t][r];
-    }
 }
 
 // out[m][n] = (y[R m][n] (+ y[R m + 1][n]) 2^-s(m)) + bias[n]. Grid (ceil(N / 256), M).
@@ -334,9 +375,16 @@ extern "C" int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const 
   }
   int rc = check_launch("q4k_gemm staging");
   if (rc) return rc;
-  const int mtiles = (Mx + q4g::kBM - 1) / q4g::kBM, ntiles = (N + q4g::kBN - 1) / q4g::kBN;
-  hipLaunchKernelGGL(q4g::gemm_kernel, dim3((unsigned)(mtiles * ntiles)), dim3(256), 0, st, xs, rs, w, y, Mx, K, N,
-                     mtiles);
+  // two 16-column groups per wave (each activation operand read feeds two MFMAs) when that grid
+  // still gives every CU two workgroups; otherwise one (measured at 4096 -> 14336: fp32 rows at
+  // M = 512 288 -> 250 us, fp16 152 -> 149 us; at M = 64 the halved grid was slower, 36 -> 51 us)
+  const int mtiles = (Mx + q4g::kBM - 1) / q4g::kBM;
+  const long wide = (long)mtiles * ((N + 127) / 128);
+  if (wide >= 2 * q4g::kCUs)
+    hipLaunchKernelGGL(q4g::gemm_kernel<2>, dim3((unsigned)wide), dim3(256), 0, st, xs, rs, w, y, Mx, K, N, mtiles);
+  else
+    hipLaunchKernelGGL(q4g::gemm_kernel<1>, dim3((unsigned)(mtiles * ((N + 63) / 64))), dim3(256), 0, st, xs, rs, w, y,
+                       Mx, K, N, mtiles);
   rc = check_launch("q4k_gemm");
   if (rc) return rc;
   const dim3 g((N + 255) / 256, M);
