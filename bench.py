@@ -17,8 +17,8 @@ activations, KV rows, over its launch time); the drop-in GEMV kernel on the toke
 replayed alone over two alternating weight copies (522 MB, above the 256 MB Infinity Cache, so
 from HBM), with per-shape timings; config 0 exactly (fp16 in and out, 256 launches over distinct
 copies, plus single-launch latency); the full 128-token decode of the end-to-end config; the GGUF
-Q4_K GEMV (Llama-3-8B up_proj), the act-order prefill GEMM (K = N = 4096) in int4 and in
-per-channel int8, and the Qwen3-MoE expert block; and `cpu_baseline`: the reference's numpy
+Q4_K GEMV (Llama-3-8B up_proj) and its prefill GEMM (M = 64 and 512), the act-order prefill GEMM
+(K = N = 4096) in int4 and in per-channel int8, and the Qwen3-MoE expert block; and `cpu_baseline`: the reference's numpy
 fallback (restated in `oracle/`) timed on this host on bounded samples of every config.
 """
 import argparse
@@ -143,6 +143,37 @@ def ggml_bench(torch, core, type_name, copies=12, reps=24):
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
+
+
+def q4k_gemm_bench(torch, core, copies=4, reps=8):
+    """GGUF Q4_K prefill GEMM at the Llama-3-8B up_proj shape: x (M, 4096) fp16 or fp32 -> y fp32
+    (M, 14336) on the matrix cores, over `copies` distinct weight copies; TFLOP/s and the fraction
+    of the dense fp16 peak."""
+    K, N = 4096, 14336
+    nb = N * K // 256
+    w = torch.randint(0, 256, (copies, nb, 144), dtype=torch.uint8, device="cuda")
+    w[:, :, 1] &= 0x3B  # finite fp16 d and dmin
+    w[:, :, 3] &= 0x3B
+    w = w.reshape(copies, N, -1)
+    res = {}
+    for M, dt in ((64, torch.float16), (512, torch.float16), (512, torch.float32)):
+        x = torch.randn((M, K), device="cuda").to(dt)
+        out = torch.empty((M, N), device="cuda")
+
+        def run(x=x, out=out):
+            for i in range(reps):
+                core.ggml_matmul(x, w[i % copies], "Q4_K", K, N, out=out)
+        run()
+        torch.cuda.synchronize()
+        g = capture(torch, run)
+        t = timed(torch, g.replay, 5) / reps
+        del g
+        flops = 2.0 * M * K * N
+        res["M%d_%s" % (M, "f16" if dt == torch.float16 else "f32")] = {
+            "us": round(t * 1e6, 2), "TFLOPs": round(flops / t / 1e12, 1),
+            "mfma_frac": round(flops / t / 1e12 / MFMA_PEAK_TFLOPS, 4)}
+    return res
+
 
 
 def gemm_bench(torch, core, Ms=(16, 128, 512), copies=32, reps=32):
@@ -591,7 +622,7 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the token's GEMVs alone and a plain 1 GiB copy, for hardware-counter runs")
     ap.add_argument("--gemv-large", action="store_true", help="only the GEMV operator on 7B-class shapes")
-    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "moe", "config0", "decode7b", "ggml"],
+    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "q4k_gemm", "moe", "config0", "decode7b", "ggml"],
                     help="one kernel benchmark and a plain 1 GiB copy, for profiler runs")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the persistent decode step and a plain 1 GiB copy, for hardware-counter runs")
@@ -613,7 +644,8 @@ def main():
         return
     if a.only:
         fn = {"gemm": lambda: gemm_bench(torch, core, Ms=(512,)), "gemm_int8": lambda: gemm_int8_bench(torch, core),
-              "q4k": lambda: q4k_bench(torch, core), "moe": lambda: moe_bench(torch, core),
+              "q4k": lambda: q4k_bench(torch, core), "q4k_gemm": lambda: q4k_gemm_bench(torch, core),
+              "moe": lambda: moe_bench(torch, core),
               "config0": lambda: config0_bench(torch, core), "decode7b": lambda: decode_7b(torch, llm),
               "ggml": lambda: {t: ggml_bench(torch, core, t) for t in ("Q6_K", "Q8_0")}}[a.only]
         out = {a.only: fn()}
@@ -702,6 +734,7 @@ def main():
         res["q4k_gemv_llama3_8b_up"] = q4k_bench(torch, core)
         res["q6k_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q6_K")
         res["q8_0_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q8_0")
+        res["q4k_gemm_llama3_8b_up"] = q4k_gemm_bench(torch, core)
         res["gptq_gemm_act_order_4096"] = gemm_bench(torch, core)
         res["gptq_gemm_int8_per_channel_4096"] = gemm_int8_bench(torch, core)
         res["moe_qwen3_t256"] = moe_bench(torch, core)

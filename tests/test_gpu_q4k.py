@@ -235,11 +235,13 @@ def test_new_type_prefill_rows(gpu, type_name):
 
 # ---- Q4_K prefill rows on the matrix cores ------------------------------------------------
 
-@pytest.mark.parametrize("M,K,N", [(9, 256, 64), (100, 768, 70), (64, 4096, 14336), (300, 2048, 512)])
+@pytest.mark.parametrize("M,K,N", [(9, 256, 64), (100, 768, 70), (64, 4096, 14336), (300, 2048, 512),
+                                   (520, 256, 7200)])
 @pytest.mark.parametrize("xdt", [np.float32, np.float16])
 def test_q4k_gemm_prefill_rows(gpu, M, K, N, xdt):
     """Rows above the GEMV's take the matrix-core GEMM (exact sub-block decomposition); against
-    the oracle's dequant times x at row-tile and column-tile tails, with bias and fp16 output."""
+    the oracle's dequant times x at row-tile and column-tile tails, with bias and fp16 output.
+    (520, 256, 7200) has grid enough for two 16-column groups per wave (9 x 57 tiles)."""
     import torch
     from webpytorch_amd import core
     W = synth.q4k_layer(M + K, K, N)

@@ -162,10 +162,12 @@ __device__ __forceinline__ half8v b_codes(uint32_t w0, uint32_t w1) {
 // the row sums arrive by LDS DMA into one of two buffers while the other is multiplied (the
 // swizzle is applied on the source side: DMA lane l of a 1 KB block lands at slot l); each
 // lane's super-block header and code bytes are loaded into registers one super-block ahead.
-template <int CG>
+// y[row][n] = acc (+ bias[n]) as OT: the output itself for fp16 rows (one staged row each), the
+// fp32 hi/lo row pairs for the combine pass otherwise (bias null).
+template <int CG, typename OT>
 __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs, const float* __restrict__ rs,
-                                                   const uint8_t* __restrict__ w, float* __restrict__ y, int Mx, int K,
-                                                   int N, int mtiles) {
+                                                   const uint8_t* __restrict__ w, OT* __restrict__ y,
+                                                   const float* __restrict__ bias, int Mx, int K, int N, int mtiles) {
   __shared__ __align__(16) __half at[2][kBM * 256];  // activation tiles, 16-byte chunks swizzled by row
   // sub-block sums [sub-block][row], rows of kRT floats: the lanes of one read take rows p and
   // sub-blocks kb, and at 64 floats (256 bytes) per sub-block the four kb share their banks
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + 16 * t + 4 * kb + r;
-        if (row < Mx) y[(size_t)row * N + ncol[c]] = acc[c][t][r];
+        if (row < Mx) y[(size_t)row * N + ncol[c]] = from_f32<OT>(bias ? acc[c][t][r] + bias[ncol[c]] : acc[c][t][r]);
       }
   }
 }
@@ -380,24 +382,27 @@ extern "C" int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const 
   // M = 512 288 -> 250 us, fp16 152 -> 149 us; at M = 64 the halved grid was slower, 36 -> 51 us)
   const int mtiles = (Mx + q4g::kBM - 1) / q4g::kBM;
   const long wide = (long)mtiles * ((N + 127) / 128);
-  if (wide >= 2 * q4g::kCUs)
-    hipLaunchKernelGGL(q4g::gemm_kernel<2>, dim3((unsigned)wide), dim3(256), 0, st, xs, rs, w, y, Mx, K, N, mtiles);
-  else
-    hipLaunchKernelGGL(q4g::gemm_kernel<1>, dim3((unsigned)(mtiles * ((N + 63) / 64))), dim3(256), 0, st, xs, rs, w, y,
-                       Mx, K, N, mtiles);
-  rc = check_launch("q4k_gemm");
+  const dim3 grid((unsigned)(wide >= 2 * q4g::kCUs ? wide : mtiles * ((N + 63) / 64)));
+  // fp16 rows: the GEMM writes the output (+ bias) itself; fp32 rows: hi/lo pairs into y, then
+  // the combine pass
+  auto gemm = [&](auto* dst, const float* b) {
+    using OT = std::remove_pointer_t<decltype(dst)>;
+    if (wide >= 2 * q4g::kCUs)
+      hipLaunchKernelGGL((q4g::gemm_kernel<2, OT>), grid, dim3(256), 0, st, xs, rs, w, dst, b, Mx, K, N, mtiles);
+    else
+      hipLaunchKernelGGL((q4g::gemm_kernel<1, OT>), grid, dim3(256), 0, st, xs, rs, w, dst, b, Mx, K, N, mtiles);
+    return check_launch("q4k_gemm");
+  };
+  if (R == 1) {
+    if (out_dtype == MIQ_F16) return gemm(static_cast<__half*>(out), bias);
+    return gemm(static_cast<float*>(out), bias);
+  }
+  rc = gemm(y, nullptr);
   if (rc) return rc;
   const dim3 g((N + 255) / 256, M);
-  if (R == 2) {
-    if (out_dtype == MIQ_F16)
-      hipLaunchKernelGGL((q4g::combine_kernel<2, __half>), g, dim3(256), 0, st, y, rmax, bias, static_cast<__half*>(out), N);
-    else
-      hipLaunchKernelGGL((q4g::combine_kernel<2, float>), g, dim3(256), 0, st, y, rmax, bias, static_cast<float*>(out), N);
-  } else {
-    if (out_dtype == MIQ_F16)
-      hipLaunchKernelGGL((q4g::combine_kernel<1, __half>), g, dim3(256), 0, st, y, rmax, bias, static_cast<__half*>(out), N);
-    else
-      hipLaunchKernelGGL((q4g::combine_kernel<1, float>), g, dim3(256), 0, st, y, rmax, bias, static_cast<float*>(out), N);
-  }
+  if (out_dtype == MIQ_F16)
+    hipLaunchKernelGGL((q4g::combine_kernel<2, __half>), g, dim3(256), 0, st, y, rmax, bias, static_cast<__half*>(out), N);
+  else
+    hipLaunchKernelGGL((q4g::combine_kernel<2, float>), g, dim3(256), 0, st, y, rmax, bias, static_cast<float*>(out), N);
   return check_launch("q4k_gemm combine");
 }
