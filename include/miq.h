@@ -187,9 +187,9 @@ int miq_q4k_gemv(const void* x, int x_dtype, const uint8_t* w, const float* bias
 /* out[M][N] = x[M][K] @ W^T + bias on the matrix cores, for prefill rows: W = N rows of K/256
  * native Q4_K super-blocks (K <= 16384), x fp16 or fp32 (fp32 as row-scaled fp16 hi/lo row
  * pairs), each 32-weight sub-block applied exactly as d1 (sum x c) - m1 (sum x). The workspace
- * (miq_q4k_gemm_workspace bytes, 256-byte aligned) holds the staged rows and the fp32 result
- * after its first 4 MiB, which it leaves alone (the split-K counter region), so the GEMV's
- * workspace can be shared. Results are deterministic.
+ * (miq_q4k_gemm_workspace bytes, 256-byte aligned) holds the staged rows, their sub-block sums
+ * and row scales after its first 4 MiB, which it leaves alone (the split-K counter region), so
+ * the GEMV's workspace can be shared. Results are deterministic.
  * Replaces: `ggml_matmul` / `_ggml_run` with the batched kernel `_GGML_GEMM_*` + `_Q4K_DEC`
  * (webtorch/_core.py:2908-2975, 3117-3133, 3720-3779). */
 int miq_q4k_gemm_workspace(int M, int K, int N, int x_dtype, size_t* bytes);

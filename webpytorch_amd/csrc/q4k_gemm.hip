@@ -11,8 +11,8 @@
 //
 // fp32 activations enter as two fp16 rows each, hi = fp16(x 2^s) and lo = fp16(x 2^s - hi),
 // with 2^s per row putting the row's largest |x| near 2^15 (s = 0 for rows holding NaN or Inf);
-// the staging pass writes them and their sub-block sums as rows 2m and 2m + 1, and the combine
-// pass adds the pair and scales back. fp16 activations are staged as they are.
+// the staging pass writes them and their sub-block sums as rows 2m and 2m + 1, and the GEMM's
+// epilogue adds the pair and scales back. fp16 activations are staged as they are.
 //
 // Staged rows: xs[r][k] fp16, each 8-wide k block in the order (0, 2, 1, 3, 4, 6, 5, 7) that
 // the code unpack produces (byte j of a code word holds value j in one nibble, and one
@@ -162,12 +162,14 @@ __device__ __forceinline__ half8v b_codes(uint32_t w0, uint32_t w1) {
 // the row sums arrive by LDS DMA into one of two buffers while the other is multiplied (the
 // swizzle is applied on the source side: DMA lane l of a 1 KB block lands at slot l); each
 // lane's super-block header and code bytes are loaded into registers one super-block ahead.
-// y[row][n] = acc (+ bias[n]) as OT: the output itself for fp16 rows (one staged row each), the
-// fp32 hi/lo row pairs for the combine pass otherwise (bias null).
-template <int CG, typename OT>
+// The output (+ bias[n]) as OT. fp16 rows (PAIR false): y[row][n] = acc. fp32 rows (PAIR true):
+// staged rows 2m and 2m + 1 are the hi and lo planes of row m, held by the same lane (rows
+// 4 kb + r of a 16-row tile), so y[m][n] = (acc[2m] + acc[2m + 1]) 2^-s(m), s from rmax[m].
+template <int CG, typename OT, bool PAIR>
 __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs, const float* __restrict__ rs,
                                                    const uint8_t* __restrict__ w, OT* __restrict__ y,
-                                                   const float* __restrict__ bias, int Mx, int K, int N, int mtiles) {
+                                                   const float* __restrict__ bias, const float* __restrict__ rmax,
+                                                   int Mx, int K, int N, int mtiles) {
   __shared__ __align__(16) __half at[2][kBM * 256];  // activation tiles, 16-byte chunks swizzled by row
   // sub-block sums [sub-block][row], rows of kRT floats: the lanes of one read take rows p and
   // sub-blocks kb, and at 64 floats (256 bytes) per sub-block the four kb share their banks
@@ -296,26 +298,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(const __half* __restrict__ xs
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < 4; r += PAIR ? 2 : 1) {
         const int row = m0 + 16 * t + 4 * kb + r;
-        if (row < Mx) y[(size_t)row * N + ncol[c]] = from_f32<OT>(bias ? acc[c][t][r] + bias[ncol[c]] : acc[c][t][r]);
+        if (row >= Mx) continue;
+        float v = acc[c][t][r];
+        if constexpr (PAIR) v = (v + acc[c][t][r + 1]) * ldexpf(1.f, -row_exp(rmax[row >> 1]));
+        y[(size_t)(PAIR ? row >> 1 : row) * N + ncol[c]] = from_f32<OT>(bias ? v + bias[ncol[c]] : v);
       }
   }
 }
 
-// out[m][n] = (y[R m][n] (+ y[R m + 1][n]) 2^-s(m)) + bias[n]. Grid (ceil(N / 256), M).
-template <int R, typename OT>
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const float* __restrict__ rmax,
-                                                      const float* __restrict__ bias, OT* __restrict__ out, int N) {
-  const int m = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= N) return;
-  float v = y[(size_t)R * m * N + n];
-  if constexpr (R == 2) v = (v + y[((size_t)R * m + 1) * N + n]) * ldexpf(1.f, -row_exp(rmax[m]));
-  out[(size_t)m * N + n] = from_f32<OT>(bias ? v + bias[n] : v);
-}
 
 struct Ws {
-  size_t xs, rs, rmax, y, bytes;
+  size_t xs, rs, rmax, bytes;
 };
 // workspace layout after the shared counter region: staged rows, sub-block sums, row maxima, y
 static Ws layout(int M, int K, int N, int x_dtype) {
@@ -325,8 +320,7 @@ static Ws layout(int M, int K, int N, int x_dtype) {
   w.xs = kCounterBytes;
   w.rs = w.xs + up(Mx * K * 2);
   w.rmax = w.rs + up(Mx * (K / 32) * 4);
-  w.y = w.rmax + up((size_t)M * 4);
-  w.bytes = w.y + up(Mx * (size_t)N * 4);
+  w.bytes = w.rmax + up((size_t)M * 4);
   return w;
 }
 
@@ -362,7 +356,6 @@ extern "C" int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const 
   __half* xs = reinterpret_cast<__half*>(b + L.xs);
   float* rs = reinterpret_cast<float*>(b + L.rs);
   float* rmax = reinterpret_cast<float*>(b + L.rmax);
-  float* y = reinterpret_cast<float*>(b + L.y);
   const int R = x_dtype == MIQ_F32 ? 2 : 1, Mx = R * M;
   if (x_dtype == MIQ_F32) {
     if ((size_t)K * 4 > 64 * 1024) {
@@ -383,26 +376,22 @@ extern "C" int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const 
   const int mtiles = (Mx + q4g::kBM - 1) / q4g::kBM;
   const long wide = (long)mtiles * ((N + 127) / 128);
   const dim3 grid((unsigned)(wide >= 2 * q4g::kCUs ? wide : mtiles * ((N + 63) / 64)));
-  // fp16 rows: the GEMM writes the output (+ bias) itself; fp32 rows: hi/lo pairs into y, then
-  // the combine pass
-  auto gemm = [&](auto* dst, const float* b) {
+  // the GEMM writes the output (+ bias) itself; fp32 rows add their hi/lo row pairs there
+  auto gemm = [&](auto* dst, auto pair) {
     using OT = std::remove_pointer_t<decltype(dst)>;
+    constexpr bool P = decltype(pair)::value;
     if (wide >= 2 * q4g::kCUs)
-      hipLaunchKernelGGL((q4g::gemm_kernel<2, OT>), grid, dim3(256), 0, st, xs, rs, w, dst, b, Mx, K, N, mtiles);
+      hipLaunchKernelGGL((q4g::gemm_kernel<2, OT, P>), grid, dim3(256), 0, st, xs, rs, w, dst, bias, rmax, Mx, K, N,
+                         mtiles);
     else
-      hipLaunchKernelGGL((q4g::gemm_kernel<1, OT>), grid, dim3(256), 0, st, xs, rs, w, dst, b, Mx, K, N, mtiles);
+      hipLaunchKernelGGL((q4g::gemm_kernel<1, OT, P>), grid, dim3(256), 0, st, xs, rs, w, dst, bias, rmax, Mx, K, N,
+                         mtiles);
     return check_launch("q4k_gemm");
   };
   if (R == 1) {
-    if (out_dtype == MIQ_F16) return gemm(static_cast<__half*>(out), bias);
-    return gemm(static_cast<float*>(out), bias);
+    if (out_dtype == MIQ_F16) return gemm(static_cast<__half*>(out), std::false_type{});
+    return gemm(static_cast<float*>(out), std::false_type{});
   }
-  rc = gemm(y, nullptr);
-  if (rc) return rc;
-  const dim3 g((N + 255) / 256, M);
-  if (out_dtype == MIQ_F16)
-    hipLaunchKernelGGL((q4g::combine_kernel<2, __half>), g, dim3(256), 0, st, y, rmax, bias, static_cast<__half*>(out), N);
-  else
-    hipLaunchKernelGGL((q4g::combine_kernel<2, float>), g, dim3(256), 0, st, y, rmax, bias, static_cast<float*>(out), N);
-  return check_launch("q4k_gemm combine");
+  if (out_dtype == MIQ_F16) return gemm(static_cast<__half*>(out), std::true_type{});
+  return gemm(static_cast<float*>(out), std::true_type{});
 }
