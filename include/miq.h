@@ -95,7 +95,9 @@ int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, const int32_t
  * no counterpart in the reference. The split-K workspace is a fixed array in the library's
  * device memory, miq_gptq_gemv_noalloc_max_bytes() (16 MiB) on each GPU the library runs on,
  * held until the process ends; the first call on a GPU looks its address up and clears its
- * counter region (a fill kernel on `stream`). The call itself allocates nothing. A problem
+ * counter region (a fill kernel on `stream`), so that first call must be made outside graph
+ * capture: made while `stream` captures, it fails with MIQ_ERR_INVALID and sets nothing up
+ * (later calls, captured or not, are fine). The call itself allocates nothing. A problem
  * whose workspace (miq_gptq_gemv_workspace) exceeds the array fails with MIQ_ERR_INVALID
  * before launching anything. Every call on a GPU shares that GPU's array: calls that overlap
  * on one GPU (two streams, two threads) race and may give wrong results; calls issued on one
@@ -196,22 +198,30 @@ int miq_q4k_gemm_workspace(int M, int K, int N, int x_dtype, size_t* bytes);
 int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out, int out_dtype,
                  int M, int K, int N, void* workspace, size_t ws_bytes, void* stream);
 
-/* out[M][N] = x[M][K] @ W^T + bias for the native GGUF block types beside Q4_K, by ggml type id:
- * 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 20 IQ4_NL (32 weights per block: 18, 20, 22, 24, 34,
- * 18 bytes) and 10 Q2_K, 11 Q3_K, 13 Q5_K, 14 Q6_K, 23 IQ4_XS (256 per super-block: 84, 110, 176,
- * 210, 136 bytes). W = N rows of K / (weights per block) blocks as the file stores them; w and x
- * 16-byte aligned; M <= 65535. Other types: MIQ_ERR_UNSUPPORTED.
+/* out[M][N] = x[M][K] @ W^T + bias for the native GGUF types, by ggml type id:
+ *   32-value blocks: 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 20 IQ4_NL (18, 20, 22, 24, 34, 18
+ *     bytes), 39 MXFP4 (17);
+ *   256-value super-blocks: 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K, 23 IQ4_XS (84, 110, 144,
+ *     176, 210, 136 bytes), 16 IQ2_XXS, 17 IQ2_XS, 22 IQ2_S, 18 IQ3_XXS, 21 IQ3_S, 19 IQ1_S,
+ *     29 IQ1_M (66, 74, 82, 98, 110, 50, 56), 34 TQ1_0, 35 TQ2_0 (54, 66);
+ *   40 NVFP4 (64 values, 36 bytes), 41 Q1_0 (128, 18), 42 Q2_0 (64, 18);
+ *   unquantized matrices: 0 F32, 1 F16, 30 BF16 (any K).
+ * W = N rows of K / (values per block) blocks as the file stores them; w and x 16-byte aligned;
+ * M <= 65535. Q4_K also has miq_q4k_gemv / miq_q4k_gemm (faster). Other types:
+ * MIQ_ERR_UNSUPPORTED.
  * Replaces: `ggml_matmul` / `_ggml_run` for these types (webtorch/_core.py:3720-3779) with the
  * decode kernel `_GGML_GEMV_*` (webtorch/_core.py:2985-3044) and the type's decoder
  * (`_Q8_0_DEC` 3072, `_IQ4NL_DEC` 3080, `_IQ4XS_DEC` 3094, `_Q5K_DEC` 3137, `_Q6K_DEC` 3159,
- * `_Q3K_DEC` 3182, `_Q2K_DEC` 3214, `_Q4_0_DEC` .. `_Q5_1_DEC` 3419-3468). */
+ * `_Q3K_DEC` 3182, `_Q2K_DEC` 3214, the i-quant grid decoders 3256-3418, `_Q4_0_DEC` ..
+ * `_Q5_1_DEC` 3419-3468, `_F16_DEC` / `_F32_DEC` / `_BF16_DEC`, `_TQ1_0_DEC`, `_TQ2_0_DEC`,
+ * `_MXFP4_DEC`, `_NVFP4_DEC`, `_Q1_0_DEC`, `_Q2_0_DEC` 3470-3607; table 3609-3637). */
 int miq_ggml_gemv(const void* x, int x_dtype, const uint8_t* w, int ggml_type, const float* bias,
                   void* out, int out_dtype, int M, int K, int N, void* stream);
 
-/* Dequant n_blocks blocks of ggml_type 12 (Q4_K) or any type miq_ggml_gemv takes to fp32,
- * bit-exact (every value is one fp32 rounding of exact products). blocks 2-byte aligned (16
- * for Q4_K). Other types: MIQ_ERR_UNSUPPORTED.
- * Replaces: `ggufload.dequant` for the same types (webtorch/ggufload.py:133-320). */
+/* Dequant n_blocks blocks of any type miq_ggml_gemv takes to fp32 (for F32 / F16 / BF16 a
+ * block is one value), bit-exact (every value is one fp32 rounding of exact products). blocks
+ * 2-byte aligned (16 for Q4_K, 4 for F32). Other types: MIQ_ERR_UNSUPPORTED.
+ * Replaces: `ggufload.dequant` / `_dequant_iq` for the same types (webtorch/ggufload.py:133-505). */
 int miq_ggml_dequant_f32(const uint8_t* blocks, int ggml_type, float* out, int64_t n_blocks, void* stream);
 
 /* ---------------------------------------------------------------------------------------
@@ -235,20 +245,22 @@ int miq_moe_route(const float* logits, int T, int E, int k, int norm_topk, void*
  * fp16 planes of each row scaled by a power of two (hi = fp16(x 2^s), lo = fp16(x 2^s - hi): about
  * 22 significant bits relative to the row's largest value, no fp16 range limit). Also records
  * each slot row's max |h| in the route buffer for miq_moe_down (route must come from
- * miq_moe_route of the same call sequence).
+ * miq_moe_route of the same call sequence). bias_gate / bias_up: the experts' fp32 biases
+ * stacked [E][I] (both or neither), added to each projection's product before the SwiGLU.
  * Replaces: the per-expert `silu(exp["gate"](xe)) * exp["up"](xe)` of `moe_mlp`
  * (webtorch/lm_engine.py:310-316). */
 int miq_moe_gate_up(const void* x, int x_dtype, void* route, int T, int E, int k, const int32_t* qw_gate,
                     const int32_t* qz_gate, const void* sc_gate, const int32_t* qw_up, const int32_t* qz_up,
-                    const void* sc_up, int scales_dtype, float* h, int H, int I, int gs, int bits,
-                    float zero_offset, void* stream);
+                    const void* sc_up, int scales_dtype, const float* bias_gate, const float* bias_up, float* h,
+                    int H, int I, int gs, int bits, float zero_offset, void* stream);
 
-/* y[T*k][H] fp32 = routing weight * (h @ Wdown[e]) per sorted slot, h as written by
- * miq_moe_gate_up (fp32, entering the matrix cores as row-scaled fp16 hi and lo planes).
+/* y[T*k][H] fp32 = routing weight * (h @ Wdown[e] + bias[e]) per sorted slot (bias: fp32 [E][H]
+ * or null), h as written by miq_moe_gate_up (fp32, entering the matrix cores as row-scaled fp16
+ * hi and lo planes).
  * Replaces: `exp["down"](...)` and `ye * w` of `moe_mlp` (webtorch/lm_engine.py:316-318). */
 int miq_moe_down(const float* h, void* route, int T, int E, int k, const int32_t* qw,
-                 const int32_t* qz, const void* sc, int scales_dtype, float* y, int I, int H, int gs,
-                 int bits, float zero_offset, void* stream);
+                 const int32_t* qz, const void* sc, int scales_dtype, const float* bias, float* y, int I, int H,
+                 int gs, int bits, float zero_offset, void* stream);
 
 /* out[T][H] += ys * sigmoid(gate_logits[t]) (gate_logits fp32 [T], or NULL: out += ys), the
  * shared expert's contribution.
@@ -260,6 +272,19 @@ int miq_moe_shared_add(float* out, const float* ys, const float* gate_logits, in
  * (webtorch/lm_engine.py:308-321). */
 int miq_moe_combine(const float* y, const void* route, int T, int E, int k, float* out, int H,
                     void* stream);
+
+/* The experts of a GGUF sparse-MoE layer kept in their file encoding: out[slot][N] (fp32) = row
+ * @ W_e^T over the T * k slots of a route buffer (miq_moe_route), e the slot's expert, W_e at
+ * w + e * expert_stride (N rows of K / (values per block) blocks of ggml_type, any block type
+ * miq_ggml_gemv takes). The row is x[token of the slot] (gather = 1: gate / up over x (T, K)) or
+ * row `slot` of x (gather = 0: down over h (T * k, K)); weighted = 1 multiplies each result by
+ * the slot's routing weight (the down projection, before miq_moe_combine). x, w, route 16-byte
+ * aligned; expert_stride >= one expert's bytes, a multiple of 4 (any for MXFP4).
+ * Replaces: the per-expert `GGMLLinear` calls of `moe_mlp` for experts `_gexperts` keeps native
+ * (webtorch/lm_engine.py:294-329; webtorch/llm.py:731-760). */
+int miq_moe_ggml_gemv(const void* x, int x_dtype, const void* route, int T, int E, int k, int gather,
+                      int weighted, const uint8_t* w, int ggml_type, size_t expert_stride, float* out,
+                      int K, int N, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Decode-step operators (fp32 activations). Positions and token ids live in a device

@@ -69,8 +69,11 @@ class Qwen2Oracle:
         else:
             if zoff is None:
                 zoff = d.get("zoff", 1.0)
+            x = np.asarray(x, np.float32)
+            if d.get("Kt", d["K"]) != d["K"]:  # `QuantizedLinear.forward` pads x to Kp (`_core.py:4450-4451`)
+                x = np.pad(x, ((0, 0), (0, d["K"] - d["Kt"])))
             y = gptq.gptq_matmul_np(x, d["qweight"], d["qzeros"], d["scales"], d["K"], d["N"],
-                                    d["gs"], d["bits"], zoff)
+                                    d["gs"], d["bits"], zoff)[:, :d.get("Nt", d["N"])]
         b = d.get("bias")
         return y if b is None else y + np.asarray(b, np.float32)
 
@@ -182,18 +185,34 @@ def fp16q_weights(tensors, config, bits, gs=128):
     from_out_in, zero offset 0, fp32 scales); the tied head re-quantized from the embedding."""
     c = config
     H, L = c["hidden_size"], c["num_hidden_layers"]
+    per = 32 // bits
+    kmul = gs if gs % per == 0 else gs * per
+
+    def quant(prefix):
+        """`_gquant`: (out, in) fp32 zero-padded to (Np, Kp) -- K to the group multiple, N to the
+        pack width (`webtorch/llm.py:843-849`) -- then quantized; the layer keeps Kt / Nt."""
+        W = tensors[prefix + ".weight"].astype(np.float32)
+        N, K = W.shape
+        Kp, Np = K + (-K) % kmul, N + (-N) % per
+        qw, qz, sc, _, _ = gptq.gptq_quantize(np.pad(W, ((0, Np - N), (0, Kp - K))), gs, bits, from_out_in=True)
+        b = tensors.get(prefix + ".bias")
+        return {"qweight": qw, "qzeros": qz, "scales": sc, "K": Kp, "N": Np, "Kt": K, "Nt": N, "gs": gs, "bits": bits,
+                "zoff": 0.0, "bias": None if b is None else b.astype(np.float32)}
+    n_exp = int(c.get("num_experts", 0) or 0)
     layers = []
     for i in range(L):
         p = "model.layers.%d." % i
         lay = {"in_ln": tensors[p + "input_layernorm.weight"].astype(np.float32),
                "post_ln": tensors[p + "post_attention_layernorm.weight"].astype(np.float32)}
+        sparse = n_exp and i not in (c.get("mlp_only_layers") or []) and (i + 1) % int(c.get("decoder_sparse_step", 1)) == 0
         for nm, hf in HF_PROJ:
-            W = tensors[p + hf + ".weight"].astype(np.float32)
-            N, K = W.shape
-            qw, qz, sc, _, _ = gptq.gptq_quantize(W, gs, bits, from_out_in=True)
-            b = tensors.get(p + hf + ".bias")
-            lay[nm] = {"qweight": qw, "qzeros": qz, "scales": sc, "K": K, "N": N, "gs": gs, "bits": bits,
-                       "zoff": 0.0, "bias": None if b is None else b.astype(np.float32)}
+            if sparse and hf.startswith("mlp."):
+                continue
+            lay[nm] = quant(p + hf)
+        if sparse:  # `_build_layer`'s sparse block (`webtorch/llm.py:522-534`)
+            lay["moe"] = {"router": quant(p + "mlp.gate"), "top_k": int(c["num_experts_per_tok"]),
+                          "experts": [{n: quant(p + "mlp.experts.%d.%s_proj" % (e, n)) for n in ("gate", "up", "down")}
+                                      for e in range(n_exp)]}
         layers.append(lay)
     NH = c["num_attention_heads"]
     cfg = dict(L=L, H=H, NH=NH, NKV=c.get("num_key_value_heads", NH), HD=c.get("head_dim") or H // NH,

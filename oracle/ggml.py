@@ -222,3 +222,11 @@ F16_FIELDS = {"Q8_0": (0,), "Q6_K": (208,), "Q4_0": (0,), "Q4_1": (0, 2), "Q5_0"
               "IQ4_NL": (0,), "IQ4_XS": (0,), "Q5_K": (0, 2), "Q2_K": (80, 82), "Q3_K": (108,)}
 CODE_BYTES = {"Q8_0": 2, "Q6_K": 0, "Q4_0": 2, "Q4_1": 4, "Q5_0": 6, "Q5_1": 8, "IQ4_NL": 2, "IQ4_XS": 8,
               "Q5_K": 48, "Q2_K": 16, "Q3_K": 32}
+
+
+# the types beyond the K-quants (i-quant grids, ternary, fp4, 1/2-bit, unquantized matrices)
+from . import ggml_ext as _ext  # noqa: E402
+
+for _name, _f in _ext.DEQUANT.items():
+    DEQUANT[_name] = (_f,) + _ext.BLOCKS[_name]
+F16_FIELDS.update(_ext.F16_FIELDS)

@@ -9,7 +9,11 @@ Only functions that no closed form pins are recorded here:
     at the full Qwen2-0.5B shape, for uniform-code and Gaussian-quantized AutoGPTQ models, with
     each step's top-1/top-2 logit gap -- `webtorch/llm.py:1716-1787`
   * the same for a plain fp16 model quantized on load to int4 and int8 (`from_fp16(quantize=)`,
-    `webtorch/llm.py:1211-1257, 835-853`)
+    `webtorch/llm.py:1211-1257, 835-853`), also at sizes the quantizer pads (K and N,
+    `webtorch/llm.py:843-849`) with a sparse-MoE layer
+  * `ggufload.dequant` of random blocks of the GGUF types beyond the K-quants (the i-quant
+    grids, TQ1_0/TQ2_0, MXFP4/NVFP4, Q1_0/Q2_0, F32/F16/BF16), whose bit layouts no closed
+    form fixes -- `webtorch/ggufload.py:133-505`
 
 Inputs are regenerated from seeds by `webpytorch_amd.synth`; the fixtures hold the seeds,
 the shapes and the reference's outputs. Usage: python tests/golden/make_golden.py [--full] [--only name,...]
@@ -36,6 +40,45 @@ def import_reference():
     from webtorch import lm_engine, llm
     assert wt.xp is np and not wt.GPU, "reference did not take its numpy fallback"
     return wt, lm_engine, llm
+
+
+# ggml type ids of the types the ggml_ext fixture covers
+EXT_TYPES = {"IQ2_XXS": 16, "IQ2_XS": 17, "IQ3_XXS": 18, "IQ1_S": 19, "IQ3_S": 21, "IQ2_S": 22, "IQ1_M": 29,
+             "BF16": 30, "TQ1_0": 34, "TQ2_0": 35, "MXFP4": 39, "NVFP4": 40, "Q1_0": 41, "Q2_0": 42,
+             "F32": 0, "F16": 1}
+
+
+def ext_cases():
+    """(type, raw bytes, n values): seeded random blocks with finite scale fields, plus blocks
+    with the scale encodings' edge patterns (MXFP4 exponents 0, 1, 2, 254; NVFP4 scale bytes 0,
+    0x7F, 0x80, 0xFF, 0x07, 0x08)."""
+    cases = []
+    for name in EXT_TYPES:
+        vals = synth.GGML_BLOCKS[name][0] if name in synth.GGML_BLOCKS else 1
+        K = max(256, 4 * vals) if vals > 1 else 64
+        raw = synth.ggml_layer(name, 77, K, 6 if vals > 1 else 3, scale=0.01)
+        cases.append((name, raw.tobytes(), raw.size // (synth.GGML_BLOCKS[name][1] if vals > 1 else
+                                                         synth.DENSE_TYPES[name]) * vals))
+    g = np.random.default_rng(78)
+    mx = g.integers(0, 256, (4, 17), dtype=np.uint8)
+    mx[:, 0] = [0, 1, 2, 254]
+    cases.append(("MXFP4", mx.tobytes(), 4 * 32))
+    nv = g.integers(0, 256, (2, 36), dtype=np.uint8)
+    nv[:, 0:4] = [[0, 0x7F, 0x80, 0xFF], [0x07, 0x08, 0x3F, 0x79]]
+    cases.append(("NVFP4", nv.tobytes(), 2 * 64))
+    return cases
+
+
+def make_ggml_ext(out):
+    sys.path.insert(0, REF)
+    from webtorch import ggufload
+    d = {}
+    for i, (name, raw, n) in enumerate(ext_cases()):
+        y = ggufload.dequant(EXT_TYPES[name], raw, n)
+        d["c%02d.type" % i] = np.array(name)
+        d["c%02d.raw" % i] = np.frombuffer(raw, np.uint8)
+        d["c%02d.y" % i] = np.asarray(y, np.float32)
+    np.savez_compressed(out, **d)
 
 
 def quantize_cases():
@@ -195,20 +238,26 @@ def build_reference_fp16q(wt, llm, model, bits, lmax, gs=128):
     m.layers = []
     for i in range(c["num_hidden_layers"]):
         p = "model.layers.%d." % i
-        m.layers.append({"in_ln": wt.Tensor(t[p + "input_layernorm.weight"].astype(np.float32)),
-                         "post_ln": wt.Tensor(t[p + "post_attention_layernorm.weight"].astype(np.float32)),
-                         "q": lin(p + "self_attn.q_proj"), "k": lin(p + "self_attn.k_proj"),
-                         "v": lin(p + "self_attn.v_proj"), "o": lin(p + "self_attn.o_proj"), "qn": None,
-                         "kn": None, "gate": lin(p + "mlp.gate_proj"), "up": lin(p + "mlp.up_proj"),
-                         "down": lin(p + "mlp.down_proj")})
+        lay = {"in_ln": wt.Tensor(t[p + "input_layernorm.weight"].astype(np.float32)),
+               "post_ln": wt.Tensor(t[p + "post_attention_layernorm.weight"].astype(np.float32)),
+               "q": lin(p + "self_attn.q_proj"), "k": lin(p + "self_attn.k_proj"),
+               "v": lin(p + "self_attn.v_proj"), "o": lin(p + "self_attn.o_proj"), "qn": None, "kn": None}
+        if m._is_moe_layer(i):  # the sparse block `_build_layer` makes (`llm.py:522-534`)
+            lay["moe"] = {"gate": lin(p + "mlp.gate"), "top_k": m.top_k, "norm_topk": m.norm_topk,
+                          "experts": [{n: lin(p + "mlp.experts.%d.%s_proj" % (e, n)) for n in ("gate", "up", "down")}
+                                      for e in range(m.n_experts)]}
+        else:
+            lay.update({"gate": lin(p + "mlp.gate_proj"), "up": lin(p + "mlp.up_proj"),
+                        "down": lin(p + "mlp.down_proj")})
+        m.layers.append(lay)
     m.final_norm = wt.Tensor(t["model.norm.weight"].astype(np.float32))
     m._init_state()
     return m
 
 
-def make_fp16q(wt, llm, out, seed, shape, prompt_len, max_new, lmax):
+def make_fp16q(wt, llm, out, seed, shape, prompt_len, max_new, lmax, **moe):
     """Greedy ids of a plain fp16 model loaded with quantize-on-load to int4 and to int8."""
-    model = synth.fp16_decoder(seed, **shape)
+    model = synth.fp16_decoder(seed, **shape, **moe)
     ids = synth.prompt_ids(seed, prompt_len, shape["V"])
     d = {}
     for bits in (4, 8):
@@ -219,7 +268,9 @@ def make_fp16q(wt, llm, out, seed, shape, prompt_len, max_new, lmax):
         d["tokens_int%d" % bits] = np.asarray(toks, np.int64)
         d["margins_int%d" % bits] = margins
     np.savez_compressed(out, seed=seed, prompt_len=prompt_len, max_new=max_new, lmax=lmax,
-                        shape=np.array([shape[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V")]), **d)
+                        shape=np.array([shape[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V")]),
+                        moe=np.array([moe.get("n_experts", 0), moe.get("moe_I", 0), moe.get("top_k", 0)]),
+                        mlp_only=np.array(sorted(moe.get("mlp_only", ())), np.int64), **d)
 
 
 SMALL = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
@@ -236,6 +287,8 @@ def main():
 
     def want(name, default):
         return name in only if only else default
+    if want("ggml_ext", not a.full_only):
+        make_ggml_ext(os.path.join(HERE, "ggml_ext.npz"))
     if want("gptq_quantize", not a.full_only):
         make_quantize(wt, os.path.join(HERE, "gptq_quantize.npz"))
     if want("moe_small", not a.full_only):
@@ -253,6 +306,11 @@ def main():
                     n_experts=8, moe_I=128, top_k=2, qk_norm=1)
     if want("decode_fp16q_small", not a.full_only):
         make_fp16q(wt, llm, os.path.join(HERE, "decode_fp16q_small.npz"), 21, SMALL, 16, 32, 64)
+    # sizes the quantizer pads: intermediate 200 (the down projection's K to 256) and a 60-expert
+    # router (N to 64 at int4) in a model whose layer 0 is dense and layer 1 sparse
+    if want("decode_fp16q_pad_moe_small", not a.full_only):
+        make_fp16q(wt, llm, os.path.join(HERE, "decode_fp16q_pad_moe_small.npz"), 23,
+                   dict(SMALL, I=200), 16, 24, 64, n_experts=60, moe_I=128, top_k=4, mlp_only=(0,))
     if want("decode_qwen2_05b", a.full or a.full_only):
         make_decode(wt, llm, os.path.join(HERE, "decode_qwen2_05b.npz"), 5, dict(synth.QWEN2_05B),
                     64, 128, 256)

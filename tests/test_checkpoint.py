@@ -280,8 +280,12 @@ def test_gguf_tensor_sizes():
         checkpoint.tensor_nbytes("Q4_K", 100)
     assert checkpoint.tensor_nbytes(23, 512) == 2 * 136          # IQ4_XS
     assert checkpoint.tensor_nbytes("IQ4_NL", 64) == 2 * 18
+    assert checkpoint.tensor_nbytes(16, 512) == 2 * 66           # IQ2_XXS
+    assert checkpoint.tensor_nbytes("MXFP4", 64) == 2 * 17
+    assert checkpoint.tensor_nbytes("NVFP4", 128) == 2 * 36
+    assert checkpoint.tensor_nbytes(29, 256) == 56               # IQ1_M
     with pytest.raises(NotImplementedError):
-        checkpoint.tensor_nbytes(16, 256)                         # IQ2_XXS: not known here
+        checkpoint.tensor_nbytes(15, 256)                         # Q8_K: not a weight type of the format's files
 
 
 # ---- GPU -------------------------------------------------------------------------------------
@@ -377,6 +381,29 @@ def test_from_pretrained_quantizes_fp16_dir_like_the_reference(gpu, tmp_path, bi
     m.fused = False
     assert m.generate(ids, n, use_graph=False).tokens == want
     m.fused = True
+    assert m.generate(ids, n).tokens == want
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits", [4, 8])
+def test_from_pretrained_pads_like_the_reference(gpu, tmp_path, bits):
+    """A plain fp16 directory whose sizes the quantizer pads -- a dense layer of intermediate 200
+    (the down projection's K padded to 256) and a sparse layer of 60 experts (the router's N
+    padded to 64 at int4) -- loads with `dtype="int4"|"int8"` and decodes the reference's greedy
+    ids (`from_fp16(quantize=bits)` with `_gquant`'s padding, `webtorch/llm.py:843-849`), eager
+    and graph-replayed."""
+    from test_oracle_moe_decode import pad_moe_model
+    from webpytorch_amd import llm
+    g, sh, model = pad_moe_model()
+    write_fp16_dir(str(tmp_path), model)
+    m = llm.AutoModelForCausalLM.from_pretrained(str(tmp_path), dtype="int%d" % bits, lmax=int(g["lmax"]))
+    dn, router = m.layers[0]["down"], m.layers[1]["moe"]["router"]
+    assert m.padded and not m.fused and (dn.K, dn.Kt) == (256, 200)
+    assert (router.N, router.Nt) == ((64, 60) if bits == 4 else (60, 60))
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    want = [int(t) for t in g["tokens_int%d" % bits]]
+    n = int(g["max_new"])
+    assert m.generate(ids, n, use_graph=False).tokens == want
     assert m.generate(ids, n).tokens == want
 
 

@@ -39,7 +39,7 @@ def test_prefill_gemm_config2(gpu, M, act):
     _check(y16.float().cpu().numpy(), ref, rel=2e-3)
 
 
-@pytest.mark.parametrize("M", [16, 128])
+@pytest.mark.parametrize("M", [16, 128, 512])
 def test_int8_per_channel_gemm(gpu, M):
     import torch
     from webpytorch_amd import core
@@ -49,6 +49,9 @@ def test_int8_per_channel_gemm(gpu, M):
     got = ql.forward(torch.from_numpy(x), out_dtype=torch.float32).cpu().numpy()
     ref = gptq.gptq_matmul_np(x, L["qweight"], L["qzeros"], L["scales"], 4096, 4096, 4096, 8, 1.0)
     _check(got, ref)
+    # the benchmarked call: fp16 out of the same kernel
+    got16 = ql.forward(torch.from_numpy(x), out_dtype=torch.float16).float().cpu().numpy()
+    _check(got16, ref, rel=2e-3)
 
 
 @pytest.mark.parametrize("K,N,gs,bits,M", [(256, 264, 32, 4, 20), (384, 136, 64, 4, 33), (512, 520, 128, 8, 17),

@@ -1,8 +1,8 @@
 """GGUF decoders through `CausalLM.from_gguf` (`webtorch/llm.py:856-1129`): small Qwen2-shaped
 GGUF files laid out by hand from the format's spec (the writer in test_checkpoint.py), with the
-block types mixed per layer as a Q4_K_M file mixes them (Q4_K q/k/o/gate/up, Q6_K v/down, a Q8_0
-token embedding, F32 norms and q/k/v biases), decoded by the engine and by the CPU decode oracle
-over the same weights:
+block types mixed per layer as a Q4_K_M file mixes them (Q4_K q/k/gate/up, Q6_K v/down, a Q8_0
+token embedding, F32 norms and q/k/v biases) plus an F16 o projection, decoded by the engine and
+by the CPU decode oracle over the same weights:
   * weights="native": the engine multiplies the file's blocks; the oracle multiplies their exact
     fp32 dequant (the reference's native layers, `GGMLLinear`);
   * weights="requant": both quantize the dequantized weights to GPTQ int4 (group 128, zero
@@ -20,10 +20,11 @@ from webpytorch_amd import synth
 pytestmark = pytest.mark.gpu
 
 SH = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048)
-TYPES = {"attn_q": "Q4_K", "attn_k": "Q4_K", "attn_v": "Q6_K", "attn_output": "Q4_K",
+TYPES = {"attn_q": "Q4_K", "attn_k": "Q4_K", "attn_v": "Q6_K", "attn_output": "F16",
          "ffn_gate": "Q4_K", "ffn_up": "Q4_K", "ffn_down": "Q6_K"}
-IDS = {"F32": 0, "Q8_0": 8, "Q4_K": 12, "Q6_K": 14}
-SCALE = {"Q4_K": 1.5e-4, "Q6_K": 3e-5, "Q8_0": 5e-4}  # fp16 block scales giving |w| ~ 0.02-0.05
+IDS = {"F32": 0, "F16": 1, "Q8_0": 8, "Q4_K": 12, "Q6_K": 14}
+# fp16 block scales giving |w| ~ 0.02-0.05 (F16: values ~N(0, 0.04^2))
+SCALE = {"Q4_K": 1.5e-4, "Q6_K": 3e-5, "Q8_0": 5e-4, "F16": 0.01}
 
 
 def _dequant(type_name, raw, n):
@@ -89,8 +90,9 @@ def make_model(path, seed=3, moe=None):
 
 
 def oracle_weights(mats, floats, mode, moe=None):
-    """Oracle weights over the file's tensors: dense exact dequant (native) or GPTQ int4 of it
-    (requant)."""
+    """Oracle weights over the file's tensors, built the reference's way: every matrix, the MoE
+    router and each expert included, as its exact fp32 dequant (native: `_gload_native`,
+    `_gexperts`, `webtorch/llm.py:731-783`) or as GPTQ int4 of it (requant: `_gload_quant`)."""
     L, H, NH, NKV, HD, I, V = (SH[k] for k in ("L", "H", "NH", "NKV", "HD", "I", "V"))
 
     def dense(name):
@@ -100,14 +102,13 @@ def oracle_weights(mats, floats, mode, moe=None):
     def layer(W, bias=None):
         if mode == "native":
             return {"W": W, "bias": bias}
-        qw, qz, sc, _, _ = gptq.gptq_quantize(np.ascontiguousarray(W), 128, 4, from_out_in=True)
-        return {"qweight": qw, "qzeros": qz, "scales": sc, "K": W.shape[1], "N": W.shape[0], "gs": 128, "bits": 4,
+        N, K = W.shape  # `_gload_quant` pads N to the pack width (a 4-expert router: 4 -> 8)
+        Np = N + (-N) % 8
+        qw, qz, sc, _, _ = gptq.gptq_quantize(np.ascontiguousarray(np.pad(W, ((0, Np - N), (0, 0)))), 128, 4,
+                                              from_out_in=True)
+        return {"qweight": qw, "qzeros": qz, "scales": sc, "K": K, "N": Np, "Nt": N, "gs": 128, "bits": 4,
                 "zoff": 0.0, "bias": bias}
 
-    def requant(W):  # experts are quantized in both modes
-        qw, qz, sc, _, _ = gptq.gptq_quantize(np.ascontiguousarray(W), 128, 4, from_out_in=True)
-        return {"qweight": qw, "qzeros": qz, "scales": sc, "K": W.shape[1], "N": W.shape[0], "gs": 128, "bits": 4,
-                "zoff": 0.0}
 
     layers = []
     for i in range(L):
@@ -118,7 +119,7 @@ def oracle_weights(mats, floats, mode, moe=None):
         if moe:
             st = {k: dense(p + "ffn_%s_exps.weight" % k) for k in ("gate", "up", "down")}
             lay["moe"] = {"router": layer(dense(p + "ffn_gate_inp.weight")), "top_k": moe["k"],
-                          "experts": [{k: requant(st[k][e]) for k in st} for e in range(moe["E"])]}
+                          "experts": [{k: layer(st[k][e]) for k in st} for e in range(moe["E"])]}
         else:
             for key, nm in (("gate", "ffn_gate"), ("up", "ffn_up"), ("down", "ffn_down")):
                 lay[key] = layer(dense(p + nm + ".weight"))
@@ -160,32 +161,39 @@ def _compare(m, ora, ids, steps, tol=1e-4):
 def test_gguf_decoder_matches_oracle(gpu, tmp_path, mode):
     from webpytorch_amd import llm
     path = tmp_path / "m.gguf"
-    mats, floats = make_model(path)
+    mats, floats = make_model(path, seed=4)  # seed 4: no oracle near-tie in the first 11 steps
     m = llm.CausalLM.from_gguf(str(path), lmax=64, weights=mode)
     assert m.native_gguf == (mode == "native") and m.bits == 4
     if mode == "native":
-        # v (Q6_K) next to q/k (Q4_K): a column group; gate|up share Q4_K: one concatenated matrix
+        # v (Q6_K) next to q/k (Q4_K): a column group; gate|up share Q4_K: one concatenated matrix;
+        # the F16 o projection multiplied as stored
         from webpytorch_amd import core
         assert isinstance(m.layers[0]["qkv"], llm._Group)
         assert isinstance(m.layers[0]["gate_up"], core.GGMLLinear) and m.layers[0]["gate_up"].Nt == 2 * SH["I"]
         assert isinstance(m.head, core.GGMLLinear) and m.head.type_name == "Q8_0"
+        assert isinstance(m.layers[0]["o"], core.GGMLLinear) and m.layers[0]["o"].type_name == "F16"
     ora = decode.Qwen2Oracle(oracle_weights(mats, floats, mode), lmax=64)
-    ids = synth.prompt_ids(3, 9, SH["V"])
+    ids = synth.prompt_ids(4, 9, SH["V"])
     _compare(m, ora, ids, 10)
     # the captured step replays the same ids
     want = m.generate(ids, 8, use_graph=False).tokens
     assert m.generate(ids, 8, use_graph=True).tokens == want
 
 
-def test_gguf_moe_decoder_matches_oracle(gpu, tmp_path):
+@pytest.mark.parametrize("mode", ["native", "requant"])
+def test_gguf_moe_decoder_matches_oracle(gpu, tmp_path, mode):
+    """Native: the Q8_0 router and the Q4_K / Q6_K experts stay in their encoding (the grouped
+    GGUF expert GEMV); requant: all quantized to GPTQ int4 (the GPTQ expert GEMMs)."""
     from webpytorch_amd import llm
     moe = dict(E=4, k=2, I=256)
     path = tmp_path / "moe.gguf"
     mats, floats = make_model(path, seed=5, moe=moe)
-    m = llm.CausalLM.from_gguf(str(path), lmax=64)  # native router (Q8_0), quantized experts
-    assert m.has_moe
-    ora = decode.Qwen2Oracle(oracle_weights(mats, floats, "native", moe), lmax=64)
+    m = llm.CausalLM.from_gguf(str(path), lmax=64, weights=mode)
+    assert m.has_moe and m.layers[0]["moe"]["experts"].native == (mode == "native")
+    ora = decode.Qwen2Oracle(oracle_weights(mats, floats, mode, moe), lmax=64)
     _compare(m, ora, synth.prompt_ids(5, 7, SH["V"]), 8)
+    want = m.generate(synth.prompt_ids(5, 7, SH["V"]), 6, use_graph=False).tokens
+    assert m.generate(synth.prompt_ids(5, 7, SH["V"]), 6, use_graph=True).tokens == want
 
 
 def test_gguf_from_pretrained_and_source_bits(gpu, tmp_path):

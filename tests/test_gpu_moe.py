@@ -223,6 +223,31 @@ def test_moe_shared_expert_fp32(gpu, small_moe):
     assert np.abs(nog - got).max() > 1e-3
 
 
+@pytest.mark.parametrize("xdt", [np.float16, np.float32])
+def test_moe_experts_with_bias(gpu, small_moe, xdt):
+    """Experts whose linears carry fp32 biases (`QuantizedLinear` experts of `_build_layer`,
+    `webtorch/llm.py:522-534`): gate / up biases enter before the SwiGLU, the down bias before the
+    routing weight, as each expert's forward adds its bias."""
+    import torch
+    from webpytorch_amd import core
+    w = small_moe
+    g = np.random.default_rng(21)
+    experts, ora = [], []
+    for e in w["experts"]:
+        d = {n: dict(v, bias=(g.standard_normal(v["N"]) * 0.5).astype(np.float32)) for n, v in e.items()}
+        experts.append({n: core.QuantizedLinear.from_autogptq(v["qweight"], v["qzeros"], v["scales"], v["bias"],
+                                                              v["gs"], v["bits"]) for n, v in d.items()})
+        ora.append(moe.gptq_expert(d))
+    x = w["x"].astype(xdt)
+    ex = core.MoEExperts(experts)
+    assert ex.b["gate"] is not None
+    got = ex(torch.from_numpy(x).cuda(), torch.from_numpy(w["logits"]).cuda(), 4).cpu().numpy()
+    ref = moe.moe_mlp_np(x.astype(np.float32), w["logits"], ora, 4)
+    _check(got, ref, rel=2e-5)
+    nob = core.MoEExperts(w["experts"])(torch.from_numpy(x).cuda(), torch.from_numpy(w["logits"]).cuda(), 4)
+    assert np.abs(nob.cpu().numpy() - got).max() > 1e-2  # the biases matter
+
+
 def test_moe_more_picks_than_one_routing_pass(gpu):
     """T * k = 4800 > 4096: routed in blocks of tokens, identical to the oracle."""
     import torch

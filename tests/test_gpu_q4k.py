@@ -66,9 +66,12 @@ def test_gemv_ragged_shapes_and_bias(gpu, K, N):
 def test_unsupported_type_raises(gpu):
     from webpytorch_amd import core
     assert core.ggml_native_supported("Q4_K") and core.ggml_native_supported("Q5_K")
-    assert not core.ggml_native_supported("IQ2_XXS")
+    assert not core.ggml_native_supported("Q8_K")  # the K-quants' activation type, never a weight's
     with pytest.raises(NotImplementedError):
-        core.GGMLLinear(b"\0" * 66, "IQ2_XXS", 256, 1)
+        core.GGMLLinear(b"\0" * 292, "Q8_K", 256, 1)
+    from webpytorch_amd import _lib
+    with pytest.raises(NotImplementedError):  # the C ABI refuses an id it has no decoder for
+        _lib.call("miq_ggml_dequant_f32", None, 15, None, 1, None)
 
 
 # ---- Q8_0 and Q6_K (the other types of a Q4_K_M file) ------------------------------------

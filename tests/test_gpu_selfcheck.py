@@ -76,3 +76,29 @@ def test_no_check_under_graph_capture(gpu, monkeypatch):
     ref = ql(x)  # eager: now checked
     assert core._CHECKED
     assert torch.allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_capture_runs_the_one_row_checks_first(gpu, monkeypatch):
+    """`CausalLM.capture` runs the one-row check of each product class its step uses before
+    capturing (checks are skipped under capture): here fp32-scaled, zero-offset-0 layers (the
+    quantize-on-load and tied-head class) and the AutoGPTQ fp16-scaled class."""
+    import torch
+    from webpytorch_amd import llm
+    core = _fresh(monkeypatch)
+    w = synth.decoder_weights(3, L=1, H=256, NH=4, NKV=2, HD=64, I=512, V=1024, gs=128, bits=4)
+    m = llm.CausalLM.from_weights(w, lmax=32, persistent=False)
+    m.capture()
+    dev = torch.cuda.current_device()
+    keys = {k for k in core._CHECKED if k[0] == "gptq" and k[-1] == dev}
+    assert ("gptq", 4, 128, 1, torch.float32, torch.float32, 0.0, dev) in keys   # the tied head
+    assert ("gptq", 4, 128, 1, torch.float32, torch.float16, 1.0, dev) in keys   # the layers
+
+
+def test_quantized_linear_nbytes_is_the_reference_count(gpu):
+    """`QuantizedLinear.nbytes` counts 4 bytes per scale whatever dtype holds them, as the
+    reference does (`webtorch/_core.py:4458-4459`)."""
+    from webpytorch_amd import core, synth
+    L = synth.gptq_layer(9, 256, 64, 128, 4)
+    ql = core.QuantizedLinear.from_autogptq(L["qweight"], L["qzeros"], L["scales"], None, 128, 4)
+    assert ql.scales.dtype.itemsize == 2
+    assert ql.nbytes() == (32 * 64 + 2 * 8 + 2 * 64 + 64) * 4

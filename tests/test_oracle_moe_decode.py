@@ -126,6 +126,33 @@ def test_fp16_quantize_on_load_matches_reference_golden(bits):
     assert toks == want and len(set(want)) >= 16
 
 
+def pad_moe_model():
+    """The fixture model whose sizes the quantizer pads: intermediate 200 in the dense layer 0
+    (the down projection's K to 256) and a 60-expert router in the sparse layer 1 (N to 64 at
+    int4, unpadded at int8)."""
+    g = np.load(os.path.join(GOLDEN, "decode_fp16q_pad_moe_small.npz"))
+    sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V"], [int(v) for v in g["shape"]]))
+    ne, mi, k = [int(v) for v in g["moe"]]
+    model = synth.fp16_decoder(int(g["seed"]), **sh, n_experts=ne, moe_I=mi, top_k=k,
+                               mlp_only=tuple(int(v) for v in g["mlp_only"]))
+    return g, sh, model
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_fp16_quantize_on_load_pads_like_the_reference(bits):
+    """Quantize-on-load pads K to the group multiple and N to the pack width and slices the
+    outputs back (`_gquant`, `webtorch/llm.py:843-849`; `QuantizedLinear.forward`,
+    `webtorch/_core.py:4446-4456`): the reference's greedy ids for such a model."""
+    g, sh, model = pad_moe_model()
+    w = decode.fp16q_weights(model["tensors"], model["config"], bits)
+    assert w["layers"][0]["down"]["K"] == 256 and w["layers"][0]["down"]["Kt"] == 200
+    assert w["layers"][1]["moe"]["router"]["N"] == (64 if bits == 4 else 60)
+    o = decode.Qwen2Oracle(w, lmax=int(g["lmax"]))
+    ids = synth.prompt_ids(int(g["seed"]), int(g["prompt_len"]), sh["V"])
+    toks, _ = o.generate(ids, int(g["max_new"]))
+    assert toks == [int(t) for t in g["tokens_int%d" % bits]]
+
+
 def _moe_fixture():
     g = np.load(os.path.join(GOLDEN, "decode_moe_qknorm_small.npz"))
     sh = dict(zip(["L", "H", "NH", "NKV", "HD", "I", "V", "gs", "bits"], [int(v) for v in g["shape"]]))

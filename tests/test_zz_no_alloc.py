@@ -1,8 +1,13 @@
 """GPU: `miq_gptq_gemv_noalloc` (the GEMV whose split-K workspace is the library's fixed device
 array) gives the same bits as `miq_gptq_gemv` with a caller workspace, on two calls in a row
 (the second smaller, reusing the array the first left behind), both matching the oracle; a
-problem too large for the array fails before launching anything. Calls go through the C ABI."""
+problem too large for the array fails before launching anything; a first call made under graph
+capture is refused, and after one eager call captured calls replay correctly. Calls go through
+the C ABI."""
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -76,3 +81,64 @@ def test_noalloc_rejects_problems_beyond_the_array(gpu):
                   K, N, 128, 4, 1.0, core.stream_handle())
     torch.cuda.synchronize()
     assert not out.any()
+
+
+_CAPTURE_CHILD = r"""
+import ctypes, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from oracle import gptq
+from webpytorch_amd import _lib, core, synth
+L = _lib.lib()
+M, K, N = 1, 896, 4864
+lay = synth.gptq_layer(61, K, N, 128, 4)
+x = synth.activations(61, M, K, np.float32)
+dev = {k: core.to_device(lay[k]) for k in ("qweight", "qzeros", "scales")}
+xt = core.to_device(x)
+out = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+ref = gptq.gptq_matmul_np(x, lay["qweight"], lay["qzeros"], lay["scales"], K, N, 128, 4, 1.0)
+s = torch.cuda.Stream()
+P = lambda t: ctypes.c_void_p(t.data_ptr())
+def call():
+    return L.miq_gptq_gemv_noalloc(P(xt), 0, None, P(dev["qweight"]), P(dev["qzeros"]), P(dev["scales"]), 1, None,
+                                   P(out), 0, M, K, N, 128, 4, 1.0, ctypes.c_void_p(s.cuda_stream))
+def capture():
+    g = ctypes.c_void_p()
+    assert L.miq_graph_begin(ctypes.c_void_p(s.cuda_stream)) == 0
+    rc = call()
+    end = L.miq_graph_end(ctypes.c_void_p(s.cuda_stream), ctypes.byref(g))
+    assert rc != 0 or end == 0
+    return rc, g
+torch.cuda.synchronize()
+rc, g = capture()  # the process's first noalloc call, under capture: refused, nothing recorded
+print("first captured call rc", rc, L.miq_last_error().decode(), flush=True)
+assert rc == -1 and b"outside graph capture" in L.miq_last_error()
+assert L.miq_graph_destroy(g) == 0
+assert call() == 0  # one eager call sets the array up
+s.synchronize()
+rc, g = capture()
+assert rc == 0
+for rep in range(2):  # replays, with eager work on the device between them
+    out.zero_()
+    torch.cuda.synchronize()
+    assert L.miq_graph_launch(g, ctypes.c_void_p(s.cuda_stream)) == 0
+    s.synchronize()
+    got = out.cpu().numpy()
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    print("replay", rep, "rel err", err, flush=True)
+    assert err < 1e-5 and np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+    torch.ones(1 << 20, device="cuda").sum().item()
+assert L.miq_graph_destroy(g) == 0
+print("ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_in_fresh_process(gpu):
+    """In a fresh process: the first call under capture is refused (its one-time set-up cannot be
+    recorded), an eager call then sets the array up, and a captured call replays twice matching
+    the oracle."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, root], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok")

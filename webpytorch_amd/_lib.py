@@ -36,10 +36,11 @@ SIGNATURES = {
     "miq_gptq_quantize": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p],
     "miq_moe_route_bytes": [_i, _i, _i, _p],
     "miq_moe_route": [_p, _i, _i, _i, _i, _p, _sz, _p],
-    "miq_moe_gate_up": [_p, _i, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _p],
+    "miq_moe_gate_up": [_p, _i, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _f, _p],
     "miq_moe_shared_add": [_p, _p, _p, _i, _i, _p],
-    "miq_moe_down": [_p, _p, _i, _i, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _p],
+    "miq_moe_down": [_p, _p, _i, _i, _i, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _f, _p],
     "miq_moe_combine": [_p, _p, _i, _i, _i, _p, _i, _p],
+    "miq_moe_ggml_gemv": [_p, _i, _p, _i, _i, _i, _i, _i, _p, _i, _sz, _p, _i, _i, _p],
     "miq_q4k_gemm_workspace": [_i, _i, _i, _i, _p],
     "miq_q4k_gemm": [_p, _i, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p],
     "miq_embed": [_p, _p, _p, _i, _i, _i, _p],

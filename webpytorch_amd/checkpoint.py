@@ -276,8 +276,11 @@ _SCALAR = {GGUF_U8: "<B", GGUF_I8: "<b", GGUF_U16: "<H", GGUF_I16: "<h", GGUF_U3
 GGML_TYPES = {0: ("F32", 1, 4), 1: ("F16", 1, 2), 2: ("Q4_0", 32, 18), 3: ("Q4_1", 32, 20),
               6: ("Q5_0", 32, 22), 7: ("Q5_1", 32, 24), 8: ("Q8_0", 32, 34), 10: ("Q2_K", 256, 84),
               11: ("Q3_K", 256, 110), 12: ("Q4_K", 256, 144), 13: ("Q5_K", 256, 176),
-              14: ("Q6_K", 256, 210), 20: ("IQ4_NL", 32, 18), 23: ("IQ4_XS", 256, 136),
-              30: ("BF16", 1, 2)}
+              14: ("Q6_K", 256, 210), 16: ("IQ2_XXS", 256, 66), 17: ("IQ2_XS", 256, 74),
+              18: ("IQ3_XXS", 256, 98), 19: ("IQ1_S", 256, 50), 20: ("IQ4_NL", 32, 18),
+              21: ("IQ3_S", 256, 110), 22: ("IQ2_S", 256, 82), 23: ("IQ4_XS", 256, 136),
+              29: ("IQ1_M", 256, 56), 30: ("BF16", 1, 2), 34: ("TQ1_0", 256, 54), 35: ("TQ2_0", 256, 66),
+              39: ("MXFP4", 32, 17), 40: ("NVFP4", 64, 36), 41: ("Q1_0", 128, 18), 42: ("Q2_0", 64, 18)}
 GGML_NAMES = {k: v[0] for k, v in GGML_TYPES.items()}
 GGML_IDS = {v[0]: k for k, v in GGML_TYPES.items()}
 
@@ -405,20 +408,37 @@ class GGUFFile:
         return core.GGMLLinear(self.raw(name), nm, K, N, bias)
 
 
+def padded_dims(K, N, gs, bits):
+    """(Kp, Np): K padded to the group multiple (group times pack factor when the group is not a
+    multiple of it) and N to the pack factor, as `_gquant` / `_gload_quant` pad
+    (`webtorch/llm.py:805-828, 843-849`)."""
+    per = 32 // bits
+    kmul = gs if gs % per == 0 else gs * per
+    return K + (-K) % kmul, N + (-N) % per
+
+
+def _quantize_out_in(W, gs, bits, bias=None):
+    """(N, K) float device weight -> GPTQ layer dict quantized on the device (`_gquant`,
+    `webtorch/llm.py:835-853`: zero offset 0, fp32 scales), zero-padded to (Np, Kp) first. The
+    padded rows quantize to codes equal to their zero point (value 0 exactly) and the padded
+    columns are dropped by the layer; the dict carries the true K and N as "Kt" / "Nt"."""
+    import torch
+    N, K = int(W.shape[0]), int(W.shape[1])
+    Kp, Np = padded_dims(K, N, gs, bits)
+    if (Kp, Np) != (K, N):
+        W = torch.nn.functional.pad(W, (0, Kp - K, 0, Np - N))
+    qw, qz, sc, _, _ = core.gptq_quantize(W.contiguous(), gs, bits, from_out_in=True)
+    return {"qweight": qw, "qzeros": qz, "scales": sc, "zoff": 0.0, "bias": bias, "Kt": K, "Nt": N}
+
+
 def _quantize_linear(st, prefix, gs, bits):
     """One float (out, in) linear of a safetensors directory quantized on the device in its file
-    encoding (`_gquant`, `webtorch/llm.py:835-853`: gs 128, zero offset 0, fp32 scales)."""
+    encoding (`_gquant`, `webtorch/llm.py:835-853`: gs 128, zero offset 0, fp32 scales, K and N
+    padded to the group / pack size)."""
     import torch
-    info, _ = st.info(prefix + ".weight")
-    N, K = (int(d) for d in info["shape"])
-    if K % gs or N % (32 // bits):
-        raise NotImplementedError("%s: (%d, %d) needs padding to the group / pack size" % (prefix, N, K))
-    W = torch.from_numpy(st.array(prefix + ".weight", keep_f16=True))
-    qw, qz, sc, _, _ = core.gptq_quantize(W, gs, bits, from_out_in=True)
-    d = {"qweight": qw, "qzeros": qz, "scales": sc, "zoff": 0.0}
-    if prefix + ".bias" in st:
-        d["bias"] = st.array(prefix + ".bias")
-    return d
+    W = torch.from_numpy(st.array(prefix + ".weight", keep_f16=True)).to(core.device())
+    b = st.array(prefix + ".bias") if prefix + ".bias" in st else None
+    return _quantize_out_in(W, gs, bits, b)
 
 
 def fp16_weights(path, bits, gs=128):
@@ -485,13 +505,9 @@ def gguf_dequant(raw, ttype, n):
 
 
 def _gguf_requant(W, bits, gs, bias):
-    """fp32 (out, in) device weight -> GPTQ layer dict quantized on the device (`_gquant`,
-    `webtorch/llm.py:835-853`: zero offset 0, fp32 scales)."""
-    N, K = int(W.shape[0]), int(W.shape[1])
-    if K % gs or N % (32 // bits):
-        raise NotImplementedError("(%d, %d) weight needs padding to the group / pack size" % (N, K))
-    qw, qz, sc, _, _ = core.gptq_quantize(W, gs, bits, from_out_in=True)
-    return {"qweight": qw, "qzeros": qz, "scales": sc, "zoff": 0.0, "bias": bias}
+    """fp32 (out, in) device weight -> GPTQ layer dict quantized on the device (`_gload_quant`,
+    `webtorch/llm.py:787-833`: zero offset 0, fp32 scales, padded to the group / pack size)."""
+    return _quantize_out_in(W, gs, bits, bias)
 
 
 def _gguf_linear(g, name, bits, gs, weights, bias=None):
@@ -510,15 +526,21 @@ def _gguf_linear(g, name, bits, gs, weights, bias=None):
     return _gguf_requant(W, bits, gs, bias)
 
 
-def _gguf_experts(g, name, bits, gs):
+def _gguf_experts(g, name, bits, gs, weights):
     """The experts of a stacked `ffn_*_exps` tensor (ggml dims in, out, E), one at a time: each
-    expert's bytes are a block-aligned slice (`_gexperts`, `webtorch/llm.py:731-760`), decoded on
-    the device and quantized to int`bits` for the grouped expert kernels."""
+    expert's bytes are a block-aligned slice (`_gexperts`, `webtorch/llm.py:731-760`). With
+    `weights="native"` a slice whose block type has a kernel here (and whose K is a whole number
+    of blocks) stays in its encoding as a GGMLLinear, as the reference uploads it; otherwise it is
+    decoded on the device and quantized to int`bits` for the GPTQ expert kernels."""
     t = g.infos[name]
     E, N, K = g.shape(name)
     per = N * K
     nb = tensor_nbytes(t["type"], per)
     raw = g.raw(name)
+    nm = GGML_NAMES.get(t["type"])
+    if weights == "native" and core.ggml_native_supported(nm) and nm not in core.DENSE_TYPES \
+            and K % GGML_TYPES[t["type"]][1] == 0:
+        return [core.GGMLLinear(raw[e * nb:(e + 1) * nb], nm, K, N) for e in range(E)]
     return [_gguf_requant(gguf_dequant(raw[e * nb:(e + 1) * nb], t["type"], per).reshape(N, K), bits, gs, None)
             for e in range(E)]
 
@@ -532,9 +554,11 @@ def gguf_weights(path, bits=None, weights="native", gs=128):
     2-D weight whose block type has a kernel here in its file encoding (GGMLLinear) and quantizes
     the rest to int`bits`; "requant" quantizes all of them. The embedding is decoded once to an
     exact fp32 table on the device; the head is the file's `output.weight` or, when absent, the
-    embedding (tied), native or quantized like the other weights. Experts are always quantized
-    (the grouped expert kernels read GPTQ). Recurrent / state-space blocks and partial RoPE are
-    not part of this engine and raise NotImplementedError."""
+    embedding (tied), native or quantized like the other weights. Experts follow the same rule
+    (`_gexperts`): native slices run the grouped GGUF expert GEMV; should one projection of a
+    layer be native and another not (a K that is not a whole number of blocks), the layer's
+    experts are all quantized, since one layer runs one expert kernel. Recurrent / state-space
+    blocks and partial RoPE are not part of this engine and raise NotImplementedError."""
     if weights not in ("native", "requant"):
         raise ValueError("weights must be 'native' or 'requant', got %r" % (weights,))
     g = GGUFFile(path)
@@ -585,7 +609,9 @@ def gguf_weights(path, bits=None, weights="native", gs=128):
         for key, nm in (("q", "attn_q"), ("k", "attn_k"), ("v", "attn_v"), ("o", "attn_output")):
             lay[key] = lin(p + nm + ".weight", opt(p + nm + ".bias"))
         if p + "ffn_gate_inp.weight" in g.infos:  # sparse MoE: router + stacked experts
-            ex = {k: _gguf_experts(g, p + "ffn_%s_exps.weight" % k, bits, gs) for k in ("gate", "up", "down")}
+            ex = {k: _gguf_experts(g, p + "ffn_%s_exps.weight" % k, bits, gs, weights) for k in ("gate", "up", "down")}
+            if len({isinstance(ex[k][0], core.GGMLLinear) for k in ex}) != 1:  # one expert kernel per layer
+                ex = {k: _gguf_experts(g, p + "ffn_%s_exps.weight" % k, bits, gs, "requant") for k in ex}
             E = len(ex["gate"])
             moe_I = moe_I or g.shape(p + "ffn_gate_exps.weight")[1]
             lay["moe"] = {"router": lin(p + "ffn_gate_inp.weight"), "top_k": top_k or 2,

@@ -169,20 +169,29 @@ def _check_close(what, got, want):
         raise RuntimeError("%s is wrong on this device (rel err %.3g against the exact dequant)" % (what, err))
 
 
-def _selfcheck_gptq(M, xdt, bits, gs):
-    """Known-answer check of the kernel `_gptq_matmul` picks for M rows of `xdt` activations."""
+def _selfcheck_gptq(M, xdt, bits, gs, sdt=torch.float16, zoff=1.0):
+    """Known-answer check of the kernel `_gptq_matmul` picks for M rows of `xdt` activations,
+    with scales of dtype `sdt` and zero offset `zoff` (each pair is its own instantiation)."""
     g = np.random.default_rng(0x5e1f + M + 31 * bits)
     K, N = 256, 256
     per = 32 // bits
     qw = torch.from_numpy(g.integers(0, 1 << 32, (K // per, N), dtype=np.uint64).astype(np.uint32).view(np.int32))
     qz = torch.from_numpy(g.integers(0, 1 << 32, (K // gs, N // per), dtype=np.uint64).astype(np.uint32).view(np.int32))
-    sc = torch.from_numpy((np.abs(g.standard_normal((K // gs, N))) * 0.01 + 1e-3).astype(np.float16))
+    sc = torch.from_numpy((np.abs(g.standard_normal((K // gs, N))) * 0.01 + 1e-3).astype(np.float32)).to(sdt)
     x = torch.from_numpy(g.standard_normal((M, K)).astype(np.float32)).to(device(), xdt)
     qw, qz, sc = qw.to(device()), qz.to(device()), sc.to(device())
-    got = _gptq_matmul(x, qw, qz, sc, K, N, gs, bits, 1.0, out_dtype=torch.float32, _check=False)
-    want = _reference_product(x, gptq_dequant(qw, qz, sc, K, N, gs, bits, 1.0))
-    _check_close("the GPTQ int%d product kernel for %d rows of %s" % (bits, M, str(xdt).replace("torch.", "")),
-                 got, want)
+    got = _gptq_matmul(x, qw, qz, sc, K, N, gs, bits, zoff, out_dtype=torch.float32, _check=False)
+    want = _reference_product(x, gptq_dequant(qw, qz, sc, K, N, gs, bits, zoff))
+    _check_close("the GPTQ int%d product kernel for %d rows of %s (%s scales, zero offset %g)" % (
+        bits, M, str(xdt).replace("torch.", ""), str(sdt).replace("torch.", ""), zoff), got, want)
+
+
+def selfcheck_gptq(M, xdt, bits, gs, sdt, zoff):
+    """Run the first-use check of the product class for (M rows of xdt, bits, gs, scales dtype,
+    zero offset) now, if it has not run on this device: for callers about to capture a graph,
+    where checks are skipped."""
+    if M and 256 % gs == 0 and _first_use(("gptq", bits, gs, _gptq_path(M, xdt), xdt, sdt, float(zoff))):
+        _selfcheck_gptq(_gptq_path(M, xdt), xdt, bits, gs, sdt, float(zoff))
 
 
 def _gptq_path(M, xdt):
@@ -211,8 +220,8 @@ def _gptq_matmul(xf, qweight, qzeros, scales, K, N, gs, bits, zoff=0.0, *, bias=
     first call of each kernel class on a device runs its known-answer check (RuntimeError if
     it fails)."""
     M = int(xf.shape[0])
-    if _check and M and 256 % gs == 0 and _first_use(("gptq", bits, gs, _gptq_path(M, xf.dtype), xf.dtype)):
-        _selfcheck_gptq(_gptq_path(M, xf.dtype), xf.dtype, bits, gs)
+    if _check:
+        selfcheck_gptq(M, xf.dtype, bits, gs, scales.dtype, zoff)
     od = out_dtype or torch.float32
     if out is None:
         out = torch.empty((M, N), dtype=od, device=xf.device)
@@ -367,8 +376,10 @@ class QuantizedLinear:
         return out
 
     def nbytes(self):
-        return int(self.qweight.numel() * 4 + self.qzeros.numel() * 4 +
-                   self.scales.numel() * self.scales.element_size() + self.bias.numel() * 4)
+        """The reference's count (`webtorch/_core.py:4458-4459`): int32 qweight and qzeros, fp32
+        scales and bias -- 4 bytes each, whatever dtype the scales are held in here."""
+        return int(self.qweight.numel() * 4 + self.qzeros.numel() * 4 + self.scales.numel() * 4 +
+                   self.bias.numel() * 4)
 
 
 # ---- GGUF native ---------------------------------------------------------------------
@@ -376,14 +387,22 @@ class QuantizedLinear:
 _NATIVE_TYPES = {"Q4_K": (256, 144, 12), "Q6_K": (256, 210, 14), "Q8_0": (32, 34, 8),
                  "Q4_0": (32, 18, 2), "Q4_1": (32, 20, 3), "Q5_0": (32, 22, 6), "Q5_1": (32, 24, 7),
                  "IQ4_NL": (32, 18, 20), "IQ4_XS": (256, 136, 23), "Q5_K": (256, 176, 13),
-                 "Q2_K": (256, 84, 10), "Q3_K": (256, 110, 11)}
+                 "Q2_K": (256, 84, 10), "Q3_K": (256, 110, 11),
+                 "IQ2_XXS": (256, 66, 16), "IQ2_XS": (256, 74, 17), "IQ2_S": (256, 82, 22),
+                 "IQ3_XXS": (256, 98, 18), "IQ3_S": (256, 110, 21), "IQ1_S": (256, 50, 19),
+                 "IQ1_M": (256, 56, 29), "TQ1_0": (256, 54, 34), "TQ2_0": (256, 66, 35),
+                 "MXFP4": (32, 17, 39), "NVFP4": (64, 36, 40), "Q1_0": (128, 18, 41), "Q2_0": (64, 18, 42),
+                 "F32": (1, 4, 0), "F16": (1, 2, 1), "BF16": (1, 2, 30)}
+# types a 2-D weight is stored in without quantization (multiplied as stored)
+DENSE_TYPES = ("F32", "F16", "BF16")
 
 
 def ggml_native_supported(type_name):
     """Can this ggml type be multiplied straight from the file's bytes
-    (`webtorch/_core.py:3644-3646`)? The llama.cpp block types Q4_0, Q4_1, Q5_0, Q5_1, Q8_0,
-    IQ4_NL, IQ4_XS, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K are; the reference's codebook-grid
-    i-quants (IQ1/IQ2/IQ3), ternary (TQ) and fp4 (MXFP4/NVFP4) types are not built here."""
+    (`webtorch/_core.py:3644-3646`, table 3609-3637)? Every type of the reference's table is:
+    the K-quants and legacy block types, the codebook-grid i-quants (IQ1_S, IQ1_M, IQ2_XXS,
+    IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS), the ternary TQ1_0 / TQ2_0, the fp4 MXFP4 /
+    NVFP4, Q1_0 / Q2_0, and unquantized F32 / F16 / BF16 matrices."""
     return type_name in _NATIVE_TYPES
 
 
@@ -459,12 +478,13 @@ def _ggml_selfcheck(type_name, mode):
     scale fields are drawn small and finite, where the reference redraws until they are."""
     from . import synth
     vals = _NATIVE_TYPES[type_name][0]
-    raw = torch.from_numpy(synth.ggml_layer(type_name, 0, vals, 2, scale=0.01)).to(device())
-    W = ggml_dequant(raw.reshape(-1), type_name, 2).reshape(2, vals)
+    K = vals if vals > 1 else 72  # an unquantized row: 72 values (a ragged count of 16-byte words)
+    raw = torch.from_numpy(synth.ggml_layer(type_name, 0, K, 2, scale=0.01)).to(device())
+    W = ggml_dequant(raw.reshape(-1), type_name, 2 * K // vals).reshape(2, K)
     g = np.random.default_rng(vals)
     M = {0: 3, -1: 2 * GGML_GEMV_MAX_M + 1}.get(mode, mode)
-    x = torch.from_numpy(g.standard_normal((M, vals)).astype(np.float32)).to(device())
-    got = ggml_matmul(x, raw, type_name, vals, 2, _check=False)
+    x = torch.from_numpy(g.standard_normal((M, K)).astype(np.float32)).to(device())
+    got = ggml_matmul(x, raw, type_name, K, 2, _check=False)
     _check_close("the native ggml %s kernel for %s" % ("gemm" if mode < 0 else "gemv", type_name), got,
                  _reference_product(x, W.t()))
 
@@ -562,6 +582,10 @@ class MoEExperts:
     stream with no host synchronisation."""
 
     def __init__(self, experts):
+        self.native = all(isinstance(e[k], GGMLLinear) for e in experts for k in ("gate", "up", "down"))
+        if self.native:
+            self._init_native(experts)
+            return
         exps = [{k: _as_linear(e[k]) for k in ("gate", "up", "down")} for e in experts]
         g0 = exps[0]["gate"]
         self.E = len(exps)
@@ -574,14 +598,75 @@ class MoEExperts:
                     raise ValueError("experts must share shapes, group size, bits and zero offset")
                 if q.perm is not None:
                     raise NotImplementedError("act-order (g_idx) experts")
-                if q.bias is not None and bool(torch.any(q.bias != 0)):
-                    raise NotImplementedError("expert linears with a bias")
+                if (q.Kt, q.Nt) != (q.Kp, q.Np):
+                    raise NotImplementedError("expert linears stored padded (K %d of %d, N %d of %d)" % (
+                        q.Kt, q.Kp, q.Nt, q.Np))
         self.sdt = exps[0]["gate"].scales.dtype
         self.w = {}
         for name in ("gate", "up", "down"):
             self.w[name] = tuple(torch.stack([getattr(e[name], a).to(self.sdt) if a == "scales" else getattr(e[name], a)
                                               for e in exps]).contiguous()
                                  for a in ("qweight", "qzeros", "scales"))
+        # the experts' fp32 biases (`QuantizedLinear.forward` adds them to the product), stacked
+        # [E][N] per projection; none when every bias is zero (the kernels then skip the adds)
+        biased = any(bool(torch.any(e[n].bias != 0)) for e in exps for n in ("gate", "up", "down"))
+        self.b = {n: torch.stack([e[n].bias for e in exps]).contiguous() if biased else None
+                  for n in ("gate", "up", "down")}
+
+    def _init_native(self, experts):
+        """GGUF experts kept in their file encoding (`_gexperts` on the native path,
+        `webtorch/llm.py:731-760`): each projection's experts stacked as [E][rows of blocks]; gate
+        and up of one block type are stacked per expert as one (2I)-row matrix so one launch
+        computes both."""
+        self.E = len(experts)
+        g0, d0 = experts[0]["gate"], experts[0]["down"]
+        self.H, self.I = g0.Kt, g0.Nt
+        for e in experts:
+            for name, (K, N) in (("gate", (self.H, self.I)), ("up", (self.H, self.I)), ("down", (self.I, self.H))):
+                q = e[name]
+                if (q.Kt, q.Nt) != (K, N) or q.type_name != experts[0][name].type_name:
+                    raise ValueError("experts must share shapes and block types per projection")
+                if q.bias is not None:
+                    raise NotImplementedError("GGUF expert linears with a bias")
+                if q.type_name in DENSE_TYPES:
+                    raise NotImplementedError("unquantized (%s) GGUF experts" % q.type_name)
+        self.types = {n: experts[0][n].type_name for n in ("gate", "up", "down")}
+        self.fused_gate_up = self.types["gate"] == self.types["up"]
+        stack = lambda names: torch.stack([torch.cat([e[n].packed.reshape(-1) for n in names])  # noqa: E731
+                                           for e in experts]).contiguous()
+        if self.fused_gate_up:
+            self.wb = {"gate_up": stack(("gate", "up"))}
+        else:
+            self.wb = {"gate": stack(("gate",)), "up": stack(("up",))}
+        self.wb["down"] = stack(("down",))
+        self.sdt = None
+
+    def _block_native(self, xt, lg, k, norm_topk_prob, out):
+        T = int(xt.shape[0])
+        st = stream_handle()
+        route = torch.empty(moe_route_bytes(T, self.E, k), dtype=torch.uint8, device=xt.device)
+        gu = torch.empty((T * k, 2 * self.I), dtype=torch.float32, device=xt.device)
+        h = torch.empty((T * k, self.I), dtype=torch.float32, device=xt.device)
+        y = torch.empty((T * k, self.H), dtype=torch.float32, device=xt.device)
+        _lib.call("miq_moe_route", ptr(lg), T, self.E, k, int(bool(norm_topk_prob)), ptr(route), route.numel(), st)
+
+        def run(xin, gather, weighted, wb, tname, o, K, N):
+            _lib.call("miq_moe_ggml_gemv", ptr(xin), dtype_code(xin), ptr(route), T, self.E, k, gather, weighted,
+                      ptr(wb), _NATIVE_TYPES[tname][2], wb.shape[1], ptr(o), K, N, st)
+        if self.fused_gate_up:
+            run(xt, 1, 0, self.wb["gate_up"], self.types["gate"], gu, self.H, 2 * self.I)
+        else:
+            g, u = gu[:, :self.I], gu[:, self.I:]
+            gtmp = torch.empty((T * k, self.I), dtype=torch.float32, device=xt.device)
+            utmp = torch.empty((T * k, self.I), dtype=torch.float32, device=xt.device)
+            run(xt, 1, 0, self.wb["gate"], self.types["gate"], gtmp, self.H, self.I)
+            run(xt, 1, 0, self.wb["up"], self.types["up"], utmp, self.H, self.I)
+            g.copy_(gtmp)
+            u.copy_(utmp)
+        _lib.call("miq_silu_mul", ptr(gu), ptr(h), T * k, self.I, st)
+        run(h, 0, 1, self.wb["down"], self.types["down"], y, self.I, self.H)
+        _lib.call("miq_moe_combine", ptr(y), ptr(route), T, self.E, k, ptr(out), self.H, st)
+        self.last_route = route
 
     # tokens per routing pass: the router handles T * k <= MAX_ROUTED picks at a time
     MAX_ROUTED = 4096
@@ -603,6 +688,8 @@ class MoEExperts:
         return out
 
     def _block(self, xt, lg, k, norm_topk_prob, out):
+        if self.native:
+            return self._block_native(xt, lg, k, norm_topk_prob, out)
         T = int(xt.shape[0])
         route = torch.empty(moe_route_bytes(T, self.E, k), dtype=torch.uint8, device=xt.device)
         h = torch.empty((T * k, self.I), dtype=torch.float32, device=xt.device)
@@ -613,9 +700,10 @@ class MoEExperts:
         _lib.call("miq_moe_route", ptr(lg), T, self.E, k, int(bool(norm_topk_prob)), ptr(route), route.numel(), st)
         g, u, d = self.w["gate"], self.w["up"], self.w["down"]
         _lib.call("miq_moe_gate_up", ptr(xt), dtype_code(xt), ptr(route), T, self.E, k, ptr(g[0]), ptr(g[1]), ptr(g[2]),
-                  ptr(u[0]), ptr(u[1]), ptr(u[2]), sd, ptr(h), self.H, self.I, self.gs, self.bits, float(self.zoff), st)
-        _lib.call("miq_moe_down", ptr(h), ptr(route), T, self.E, k, ptr(d[0]), ptr(d[1]), ptr(d[2]), sd, ptr(y),
-                  self.I, self.H, self.gs, self.bits, float(self.zoff), st)
+                  ptr(u[0]), ptr(u[1]), ptr(u[2]), sd, ptr(self.b["gate"]), ptr(self.b["up"]), ptr(h), self.H, self.I,
+                  self.gs, self.bits, float(self.zoff), st)
+        _lib.call("miq_moe_down", ptr(h), ptr(route), T, self.E, k, ptr(d[0]), ptr(d[1]), ptr(d[2]), sd,
+                  ptr(self.b["down"]), ptr(y), self.I, self.H, self.gs, self.bits, float(self.zoff), st)
         _lib.call("miq_moe_combine", ptr(y), ptr(route), T, self.E, k, ptr(out), self.H, st)
         self.last_route = route
 

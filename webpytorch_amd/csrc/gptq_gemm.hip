@@ -153,7 +153,7 @@ __device__ __forceinline__ int f32_row_exp(float m) {
   if (!(m > 0.f) || !(m <= 3.4e38f)) return 0;
   int ex;
   frexpf(m, &ex);
-  return min(max(15 - ex, -100), 100);
+  return min(max(15 - ex, -126), 126);  // any finite maximum lands below 2^15; 2^s stays finite
 }
 
 // Stage row m of fp32 x (gathered through perm if PERM) as hi (row m) and lo (row M + m) of the

@@ -696,7 +696,9 @@ extern "C" int miq_gptq_gemv_fused(const float* x, int x_mode, const float* norm
 // device is current (the array's name in host code is a host-side stand-in, not a device
 // address). Each device's address is looked up once, on the first call made on it, which also
 // clears the array's counter region with a fill kernel on the caller's stream (the kernels
-// leave it zero after every call).
+// leave it zero after every call). That first call must run eagerly: under graph capture the
+// clear would only be recorded, so a first call made while the stream captures is refused
+// (MIQ_ERR_INVALID) and sets nothing up.
 namespace miq {
 namespace na {
 
@@ -713,28 +715,32 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint4* p, size_t n) {
 std::mutex g_lock;
 void* g_ptr[kMaxDevices];
 
-// The current device's copy of the scratch array (set up on its first use), or null with the
-// error recorded.
-void* device_scratch(hipStream_t st) {
+// The current device's copy of the scratch array (set up on its first use) in *out; 0 or the
+// error code, with the error recorded.
+int device_scratch(hipStream_t st, void** out) {
+  *out = nullptr;
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    fail(MIQ_ERR_HIP, "gptq_gemv_noalloc: hipGetDevice: %s (device %d)", hipGetErrorString(e), dev);
-    return nullptr;
-  }
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(MIQ_ERR_HIP, "gptq_gemv_noalloc: hipGetDevice: %s (device %d)", hipGetErrorString(e), dev);
   std::lock_guard<std::mutex> g(g_lock);
   if (!g_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return fail(MIQ_ERR_HIP, "gptq_gemv_noalloc: hipStreamIsCapturing: %s", hipGetErrorString(e));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(MIQ_ERR_INVALID, "gptq_gemv_noalloc: the first call on a device sets up its scratch array and must "
+                                   "run outside graph capture (make one eager call first)");
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) {
-      fail(MIQ_ERR_HIP, "gptq_gemv_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
-      return nullptr;
-    }
+    if (e != hipSuccess || !p) return fail(MIQ_ERR_HIP, "gptq_gemv_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
     hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, st, static_cast<uint4*>(p), kCounterBytes / 16);
-    if (check_launch("gptq_gemv_noalloc scratch clear")) return nullptr;
+    const int rc = check_launch("gptq_gemv_noalloc scratch clear");
+    if (rc) return rc;
     g_ptr[dev] = p;
   }
-  return g_ptr[dev];
+  *out = g_ptr[dev];
+  return MIQ_OK;
 }
 
 }  // namespace na
@@ -757,8 +763,9 @@ extern "C" int miq_gptq_gemv_noalloc(const void* x, int x_dtype, const int32_t* 
               "(use miq_gptq_gemv with a workspace)",
               M, K, N, need, na::kScratchBytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  void* ws = na::device_scratch(st);
-  if (!ws) return MIQ_ERR_HIP;
+  void* ws = nullptr;
+  rc = na::device_scratch(st, &ws);
+  if (rc) return rc;
   return miq_gptq_gemv(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, M, K, N, gs,
                        bits, zero_offset, ws, na::kScratchBytes, stream);
 }

@@ -27,11 +27,10 @@
 #include <type_traits>
 
 #include "miq_common.h"
+#include "moe_route.h"
 
 namespace miq {
 
-constexpr int kMoeBM = 32;      // rows per tile (two 16-row MFMA blocks)
-constexpr int kMoeMaxTK = 4096;  // T * k handled by the single-workgroup router
 constexpr int kSlotWaves = 16;   // waves of the slot kernel (1024 threads), one chunk of picks each
 // waves per grouped-GEMM workgroup (measured: eight down waves sharing a staged h chunk cut
 // the down GEMM 44.4 -> 43.2 us at T = 256, H = 2048, 128 experts; eight gate_up waves made it
@@ -39,37 +38,13 @@ constexpr int kSlotWaves = 16;   // waves of the slot kernel (1024 threads), one
 constexpr int kMoeWavesGateUp = 4;
 constexpr int kMoeWavesDown = 8;
 
-// Offsets (in 4-byte words) of the route buffer's arrays.
-struct RouteLayout {
-  size_t topk_e, topk_w, slot_of, sorted_tok, sorted_w, expert_off, ntiles, tiles, slot_max, x_scale, words;
-  int max_tiles;
-};
-
-__host__ __device__ inline RouteLayout route_layout(int T, int E, int k) {
-  RouteLayout L;
-  const size_t tk = (size_t)T * k;
-  L.max_tiles = (int)((tk + kMoeBM - 1) / kMoeBM) + E;
-  L.topk_e = 0;
-  L.topk_w = L.topk_e + tk;
-  L.slot_of = L.topk_w + tk;
-  L.sorted_tok = L.slot_of + tk;
-  L.sorted_w = L.sorted_tok + tk;
-  L.expert_off = L.sorted_w + tk;
-  L.ntiles = L.expert_off + E + 1;
-  L.tiles = (L.ntiles + 1 + 3) & ~(size_t)3;  // 16-byte aligned int4 entries
-  L.slot_max = L.tiles + 4 * (size_t)L.max_tiles;  // [T*k] max |h| of each slot's row (fp32 bits)
-  L.x_scale = L.slot_max + tk;                        // [T] row scale of fp32 x
-  L.words = L.x_scale + (size_t)T;
-  return L;
-}
-
 // 2^s with s making m * 2^s just below 2^15 (1 for zero, NaN or infinite m): the row scale of
 // the fp16 hi/lo planes. Its inverse is row_unscale(m), also exact.
 __device__ __forceinline__ int row_scale_exp(float m) {
   if (!(m > 0.f) || !(m <= 3.4e38f)) return 0;
   int ex;
   frexpf(m, &ex);  // m < 2^ex
-  return min(max(15 - ex, -100), 100);
+  return min(max(15 - ex, -126), 126);  // any finite maximum lands below 2^15; 2^s stays finite
 }
 __device__ __forceinline__ float row_scale(float m) { return ldexpf(1.f, row_scale_exp(m)); }
 __device__ __forceinline__ float row_unscale(float m) { return ldexpf(1.f, -row_scale_exp(m)); }
@@ -346,8 +321,8 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
     const void* __restrict__ a_in, int* __restrict__ route, int T, int E, int k,
     const uint32_t* __restrict__ qw0, const uint32_t* __restrict__ qz0, const ST* __restrict__ sc0,
     const uint32_t* __restrict__ qw1, const uint32_t* __restrict__ qz1, const ST* __restrict__ sc1,
-    size_t qw_stride, size_t qz_stride, size_t sc_stride, float* __restrict__ out, int K, int N, int gs,
-    float zoff) {
+    size_t qw_stride, size_t qz_stride, size_t sc_stride, const float* __restrict__ b0, const float* __restrict__ b1,
+    float* __restrict__ out, int K, int N, int gs, float zoff) {
   constexpr int PER = 32 / BITS;
   constexpr int TM = kMoeBM / 16;
   constexpr int STEPS = KC / 32;
@@ -558,7 +533,11 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
         float hv[4];
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
-          const float g = acc[0][t][s4][r] * un, u = ux[cw][t][s4][lane][r] * un;
+          float g = acc[0][t][s4][r] * un, u = ux[cw][t][s4][lane][r] * un;
+          if (b0) {  // the experts' fp32 biases, added to each projection's product
+            g += colok ? b0[(size_t)e * N + ncol + s4] : 0.f;
+            u += colok ? b1[(size_t)e * N + ncol + s4] : 0.f;
+          }
           hv[s4] = g * (1.f / (1.f + expf(-g))) * u;
           m = fmaxf(m, fabsf(hv[s4]));  // NaN: the word check below
           if (hv[s4] != hv[s4]) m = __int_as_float(0x7FC00000);
@@ -582,10 +561,16 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_kernel(
         const int row = 16 * t + 4 * kb + r;
         if (row >= nrows) continue;
         const size_t slot = (size_t)slot0 + row;
-        const float wsc = sorted_w[slot] * row_unscale(row_max[slot]);
         float* y = out + slot * N + ncol;
+        if (b0) {  // (h @ Wd + bias) * w, as the expert's linear then the routing weight
+          const float un = row_unscale(row_max[slot]), w = sorted_w[slot];
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) y[s4] = acc[0][t][s4][r] * wsc;
+          for (int s4 = 0; s4 < 4; ++s4) y[s4] = (acc[0][t][s4][r] * un + b0[(size_t)e * N + ncol + s4]) * w;
+        } else {
+          const float wsc = sorted_w[slot] * row_unscale(row_max[slot]);
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) y[s4] = acc[0][t][s4][r] * wsc;
+        }
       }
   }
 }
@@ -608,8 +593,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 
 template <int BITS, int KC, bool GATE_UP, bool XF32>
 static int launch_moe_gemm(const void* a, int* route, int T, int E, int k, const int32_t* qw0, const int32_t* qz0,
-                           const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt, float* out,
-                           int K, int N, int gs, float zoff, hipStream_t st) {
+                           const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt,
+                           const float* b0, const float* b1, float* out, int K, int N, int gs, float zoff,
+                           hipStream_t st) {
   const RouteLayout L = route_layout(T, E, k);
   const int per = 32 / BITS;
   const size_t qws = (size_t)(K / per) * N, qzs = (size_t)(K / gs) * (N / per), scs = (size_t)(K / gs) * N;
@@ -621,24 +607,24 @@ static int launch_moe_gemm(const void* a, int* route, int T, int E, int k, const
   if (sdt == MIQ_F16)
     hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, __half, NW>), grid, dim3(64 * NW), 0, st, a, route, T, E, k,
                        w0, z0, static_cast<const __half*>(sc0), w1, z1, static_cast<const __half*>(sc1), qws, qzs,
-                       scs, out, K, N, gs, zoff);
+                       scs, b0, b1, out, K, N, gs, zoff);
   else
     hipLaunchKernelGGL((moe_gemm_kernel<BITS, KC, GATE_UP, XF32, float, NW>), grid, dim3(64 * NW), 0, st, a, route, T, E, k,
                        w0, z0, static_cast<const float*>(sc0), w1, z1, static_cast<const float*>(sc1), qws, qzs, scs,
-                       out, K, N, gs, zoff);
+                       b0, b1, out, K, N, gs, zoff);
   return check_launch(GATE_UP ? "moe_gate_up" : "moe_down");
 }
 
 template <bool GATE_UP, bool XF32>
 static int moe_gemm(const void* a, int* route, int T, int E, int k, const int32_t* qw0, const int32_t* qz0,
-                    const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt, float* out, int K,
-                    int N, int gs, int bits, float zoff, hipStream_t st) {
+                    const void* sc0, const int32_t* qw1, const int32_t* qz1, const void* sc1, int sdt, const float* b0,
+                    const float* b1, float* out, int K, int N, int gs, int bits, float zoff, hipStream_t st) {
   const int kc = gs % 128 == 0 ? 128 : (gs == 64 ? 64 : (gs == 32 ? 32 : 0));
   MIQ_REQUIRE(kc, MIQ_ERR_UNSUPPORTED, "moe: group size %d (32, 64 or a multiple of 128)", gs);
 #define MIQ_MOE_CASE(B, C)                                                                                        \
   if (bits == B && kc == C)                                                                                       \
-  return launch_moe_gemm<B, C, GATE_UP, XF32>(a, route, T, E, k, qw0, qz0, sc0, qw1, qz1, sc1, sdt, out, K, N, gs, \
-                                              zoff, st)
+  return launch_moe_gemm<B, C, GATE_UP, XF32>(a, route, T, E, k, qw0, qz0, sc0, qw1, qz1, sc1, sdt, b0, b1, out, K, \
+                                              N, gs, zoff, st)
   MIQ_MOE_CASE(4, 128); MIQ_MOE_CASE(4, 64); MIQ_MOE_CASE(4, 32);
   MIQ_MOE_CASE(8, 128); MIQ_MOE_CASE(8, 64); MIQ_MOE_CASE(8, 32);
 #undef MIQ_MOE_CASE
@@ -703,8 +689,8 @@ extern "C" int miq_moe_route(const float* logits, int T, int E, int k, int norm_
 
 extern "C" int miq_moe_gate_up(const void* x, int x_dtype, void* route, int T, int E, int k, const int32_t* qw_gate,
                                const int32_t* qz_gate, const void* sc_gate, const int32_t* qw_up, const int32_t* qz_up,
-                               const void* sc_up, int scales_dtype, float* h, int H, int I, int gs, int bits,
-                               float zero_offset, void* stream) {
+                               const void* sc_up, int scales_dtype, const float* bias_gate, const float* bias_up,
+                               float* h, int H, int I, int gs, int bits, float zero_offset, void* stream) {
   int rc = moe_check("moe_gate_up", T, E, k);
   if (rc) return rc;
   rc = check_gptq_dims("moe_gate_up", H, I, gs, bits);
@@ -717,22 +703,23 @@ extern "C" int miq_moe_gate_up(const void* x, int x_dtype, void* route, int T, i
               MIQ_ERR_ALIGN, "moe_gate_up: alignment (x, h, weights, route 16 bytes; I %% 4, H %% 32)");
   MIQ_REQUIRE(zero_offset == (float)(int)zero_offset && zero_offset >= 0.f && zero_offset <= 8.f, MIQ_ERR_UNSUPPORTED,
               "moe_gate_up: zero_offset %g", zero_offset);
+  MIQ_REQUIRE(!bias_gate == !bias_up, MIQ_ERR_INVALID, "moe_gate_up: give both expert biases or neither");
   const hipStream_t st = static_cast<hipStream_t>(stream);
   int* r = static_cast<int*>(route);
   if (x_dtype == MIQ_F32) {
     hipLaunchKernelGGL(moe_xmax_kernel, dim3((T + 3) / 4), dim3(256), 0, st, static_cast<const float*>(x), T, H, E, k, r);
     rc = check_launch("moe_gate_up row scales");
     if (rc) return rc;
-    return moe_gemm<true, true>(x, r, T, E, k, qw_gate, qz_gate, sc_gate, qw_up, qz_up, sc_up, scales_dtype, h, H, I, gs,
-                                bits, zero_offset, st);
+    return moe_gemm<true, true>(x, r, T, E, k, qw_gate, qz_gate, sc_gate, qw_up, qz_up, sc_up, scales_dtype, bias_gate,
+                                bias_up, h, H, I, gs, bits, zero_offset, st);
   }
-  return moe_gemm<true, false>(x, r, T, E, k, qw_gate, qz_gate, sc_gate, qw_up, qz_up, sc_up, scales_dtype, h, H, I, gs,
-                               bits, zero_offset, st);
+  return moe_gemm<true, false>(x, r, T, E, k, qw_gate, qz_gate, sc_gate, qw_up, qz_up, sc_up, scales_dtype, bias_gate,
+                               bias_up, h, H, I, gs, bits, zero_offset, st);
 }
 
 extern "C" int miq_moe_down(const float* h, void* route, int T, int E, int k, const int32_t* qw, const int32_t* qz,
-                            const void* sc, int scales_dtype, float* y, int I, int H, int gs, int bits, float zero_offset,
-                            void* stream) {
+                            const void* sc, int scales_dtype, const float* bias, float* y, int I, int H, int gs, int bits,
+                            float zero_offset, void* stream) {
   int rc = moe_check("moe_down", T, E, k);
   if (rc) return rc;
   rc = check_gptq_dims("moe_down", I, H, gs, bits);
@@ -743,7 +730,8 @@ extern "C" int miq_moe_down(const float* h, void* route, int T, int E, int k, co
   MIQ_REQUIRE(zero_offset == (float)(int)zero_offset && zero_offset >= 0.f && zero_offset <= 8.f, MIQ_ERR_UNSUPPORTED,
               "moe_down: zero_offset %g", zero_offset);
   return moe_gemm<false, true>(h, static_cast<int*>(route), T, E, k, qw, qz, sc, nullptr, nullptr, nullptr,
-                               scales_dtype, y, I, H, gs, bits, zero_offset, static_cast<hipStream_t>(stream));
+                               scales_dtype, bias, nullptr, y, I, H, gs, bits, zero_offset,
+                               static_cast<hipStream_t>(stream));
 }
 
 extern "C" int miq_moe_shared_add(float* out, const float* ys, const float* gate_logits, int T, int H, void* stream) {

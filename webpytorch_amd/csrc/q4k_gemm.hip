@@ -46,7 +46,7 @@ __device__ __forceinline__ int row_exp(float m) {
   if (!(m > 0.f) || !(m <= 3.4e38f)) return 0;
   int ex;
   frexpf(m, &ex);
-  return min(max(15 - ex, -100), 100);
+  return min(max(15 - ex, -126), 126);  // any finite maximum lands below 2^15; 2^s stays finite
 }
 
 // fp16 pair (a, b) as one word

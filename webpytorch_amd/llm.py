@@ -68,27 +68,43 @@ def _gptq_dict(d, gs, bits):
     """A GPTQ layer dict as a QuantizedLinear with its own zero offset (AutoGPTQ tensors: 1)."""
     per = 32 // bits
     K, N = int(np.shape(d["qweight"])[0]) * per, int(np.shape(d["qweight"])[1])
-    return core.QuantizedLinear(d["qweight"], d["qzeros"], d["scales"], d.get("bias"), K, N, K, N, gs, bits,
-                                zero_offset=float(d.get("zoff", 1.0)))
+    return core.QuantizedLinear(d["qweight"], d["qzeros"], d["scales"], d.get("bias"), d.get("Kt", K), d.get("Nt", N),
+                                K, N, gs, bits, zero_offset=float(d.get("zoff", 1.0)))
 
 
 class _Lin:
     """Device tensors of one (possibly fused) GPTQ linear. The zero offset is the layer's own:
-    1 for AutoGPTQ tensors (stored zero - 1), 0 for layers quantized on load."""
+    1 for AutoGPTQ tensors (stored zero - 1), 0 for layers quantized on load. K and N are the
+    stored (padded) sizes; Kt and Nt the layer's own (a layer quantized on load pads K to the
+    group multiple and N to the pack width: `padded` layers take Kt inputs and give Nt outputs)."""
 
     def __init__(self, d, K, gs, bits, zoff=None):
         self.qweight = core.to_device(d["qweight"], torch.int32)
         self.qzeros = core.to_device(d["qzeros"], torch.int32)
         self.scales = core.to_device(d["scales"])
+        self.K, self.N = int(self.qweight.shape[0]) * (32 // bits), int(self.qweight.shape[1])
+        self.Kt, self.Nt = int(d.get("Kt", self.K)), int(d.get("Nt", self.N))
+        if self.Kt != K:
+            raise ValueError("layer takes %d inputs where %d are expected" % (self.Kt, K))
+        self.padded = (self.Kt, self.Nt) != (self.K, self.N)
         b = d.get("bias")
-        self.bias = None if b is None else core.to_device(b, torch.float32)
-        self.K, self.N = K, int(self.qweight.shape[1])
+        self.bias = None
+        if b is not None:
+            bt = core.to_device(b, torch.float32).reshape(-1)
+            self.bias = bt if bt.numel() == self.N else torch.nn.functional.pad(bt, (0, self.N - bt.numel()))
         self.gs, self.bits = gs, bits
         self.zoff = float(d.get("zoff", 1.0) if zoff is None else zoff)
 
 
 def _lin_n(lin):
-    return int(lin.Nt) if isinstance(lin, core.GGMLLinear) else int(lin.N)
+    return int(lin.Nt) if isinstance(lin, (core.GGMLLinear, _Lin)) else int(lin.N)
+
+
+def _dict_padded(d, bits):
+    """Does a GPTQ layer dict store more rows or columns than the layer has (quantize-on-load
+    padding)?"""
+    K, N = int(np.shape(d["qweight"])[0]) * (32 // bits), int(np.shape(d["qweight"])[1])
+    return int(d.get("Kt", K)) != K or int(d.get("Nt", N)) != N
 
 
 class _Group:
@@ -106,7 +122,7 @@ def _fuse(parts, K, gs, bits):
     """One layer for projections that share K: GPTQ dicts concatenated along the output
     dimension; GGUF layers of one block type likewise (their rows are whole blocks); a mix as a
     _Group."""
-    if all(isinstance(q, dict) for q in parts):
+    if all(isinstance(q, dict) for q in parts) and not any(_dict_padded(q, bits) for q in parts):
         return _Lin(_cat_layers(parts, gs, bits), K, gs, bits)
     lins = [q if isinstance(q, core.GGMLLinear) else _Lin(q, K, gs, bits) for q in parts]
     if all(isinstance(q, core.GGMLLinear) for q in lins) and len({q.type_name for q in lins}) == 1:
@@ -153,7 +169,7 @@ class CausalLM:
                  "qn": vec(lay.get("qn")), "kn": vec(lay.get("kn"))}
             mo = lay.get("moe")
             if mo:  # sparse MoE MLP (`CausalLM._mlp` -> `moe_mlp`, `webtorch/llm.py:1489-1496`)
-                lin = lambda e: _gptq_dict(e, self.gs, self.bits)  # noqa: E731
+                lin = lambda e: e if isinstance(e, core.GGMLLinear) else _gptq_dict(e, self.gs, self.bits)  # noqa: E731
                 d["moe"] = {"router": _mk_lin(mo["router"], self.H, self.gs, self.bits),
                             "experts": core.MoEExperts([{k: lin(e[k]) for k in ("gate", "up", "down")}
                                                         for e in mo["experts"]]),
@@ -184,8 +200,12 @@ class CausalLM:
         # persistent one-token kernels read GPTQ tensors)
         lins = [self.head] + [lay[k] for lay in self.layers for k in ("qkv", "o", "gate_up", "down") if k in lay]
         lins += [lay["moe"]["router"] for lay in self.layers if "moe" in lay]
-        self.native_gguf = any(not isinstance(q, _Lin) for q in lins)
-        if self.native_gguf:
+        parts = [p for q in lins for p in (q.parts if isinstance(q, _Group) else [q])]
+        self.native_gguf = any(isinstance(p, core.GGMLLinear) for p in parts)
+        # the fused one-token kernels (RMSNorm / SwiGLU staging, persistent step) read K inputs and
+        # write N outputs: layers stored padded run the launch sequence
+        self.padded = any(getattr(p, "padded", False) for p in parts)
+        if self.native_gguf or self.padded:
             self.fused = False
         self._alloc()
         self._graph = None
@@ -348,6 +368,16 @@ class CausalLM:
                     self._linear(part, x, tmp)
                     out[:, c0:c0 + n].copy_(tmp)
                 c0 += n
+        elif lin.padded:
+            # the reference's QuantizedLinear.forward: x zero-padded to Kp, the output sliced to Nt
+            # (`webtorch/_core.py:4446-4456`)
+            xp = x if lin.Kt == lin.K else torch.nn.functional.pad(x, (0, lin.K - lin.Kt))
+            tmp = torch.empty((int(x.shape[0]), lin.N), dtype=out.dtype, device=out.device)
+            core._gptq_matmul(xp.contiguous(), lin.qweight, lin.qzeros, lin.scales, lin.K, lin.N, lin.gs, lin.bits,
+                              lin.zoff, bias=lin.bias, out=tmp, ws=self.ws)
+            if bias is not None:
+                raise ValueError("a padded layer takes no bias override (its residual adds separately)")
+            out.copy_(tmp[:, :lin.Nt])
         else:
             core._gptq_matmul(x, lin.qweight, lin.qzeros, lin.scales, lin.K, lin.N, lin.gs, lin.bits, lin.zoff,
                               bias=lin.bias if bias is None else bias, out=out, ws=self.ws)
@@ -458,7 +488,7 @@ class CausalLM:
 
     def _residual(self, lin, x, h, T):
         """h += x @ W: fused into the GEMV (bias = out = h) for one token, an add otherwise."""
-        if T == 1 and lin.bias is None:
+        if T == 1 and lin.bias is None and not getattr(lin, "padded", False):
             self._linear(lin, x, h, bias=h)
         else:
             tmp = self.buf["tmp"][:T]
@@ -468,7 +498,15 @@ class CausalLM:
     # ---- capture-replay ----
     def capture(self):
         """Record one decode step (T = 1) as a HIP graph (`beginCapture`/`endCapture`,
-        `webgpu/wgpy_backends/webgpu/platform.py:45-56`). Nothing in it depends on the host."""
+        `webgpu/wgpy_backends/webgpu/platform.py:45-56`). Nothing in it depends on the host.
+        First-use checks read results back, so they are skipped under capture: the one-row check
+        of every GPTQ product class the step can run (bits, group size, scale dtype, zero offset)
+        runs here, eagerly, first."""
+        lins = [self.head] + [lay[k] for lay in self.layers for k in ("qkv", "o", "gate_up", "down") if k in lay]
+        lins += [lay["moe"]["router"] for lay in self.layers if "moe" in lay]
+        for q in {(p.bits, p.gs, p.scales.dtype, p.zoff): p for q in lins
+                  for p in (q.parts if isinstance(q, _Group) else [q]) if isinstance(p, _Lin)}:
+            core.selfcheck_gptq(1, torch.float32, *q)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):

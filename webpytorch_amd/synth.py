@@ -137,21 +137,54 @@ def q6k_layer(seed, K, N, name="q6k"):
 GGML_BLOCKS = {"Q4_0": (32, 18, (0,)), "Q4_1": (32, 20, (0, 2)), "Q5_0": (32, 22, (0,)),
                "Q5_1": (32, 24, (0, 2)), "Q8_0": (32, 34, (0,)), "IQ4_NL": (32, 18, (0,)),
                "IQ4_XS": (256, 136, (0,)), "Q2_K": (256, 84, (80, 82)), "Q3_K": (256, 110, (108,)),
-               "Q4_K": (256, 144, (0, 2)), "Q5_K": (256, 176, (0, 2)), "Q6_K": (256, 210, (208,))}
+               "Q4_K": (256, 144, (0, 2)), "Q5_K": (256, 176, (0, 2)), "Q6_K": (256, 210, (208,)),
+               "IQ2_XXS": (256, 66, (0,)), "IQ2_XS": (256, 74, (0,)), "IQ2_S": (256, 82, (0,)),
+               "IQ3_XXS": (256, 98, (0,)), "IQ3_S": (256, 110, (0,)), "IQ1_S": (256, 50, (0,)),
+               "IQ1_M": (256, 56, ()), "TQ1_0": (256, 54, (52,)), "TQ2_0": (256, 66, (64,)),
+               "MXFP4": (32, 17, ()), "NVFP4": (64, 36, ()), "Q1_0": (128, 18, (0,)), "Q2_0": (64, 18, (0,))}
+# unquantized matrices: bytes per value
+DENSE_TYPES = {"F32": 4, "F16": 2, "BF16": 2}
+
+
+def _scale_fields(type_name, b, g, scale):
+    """Scale fields that are not a plain fp16: MXFP4's E8M0 exponent byte, NVFP4's four UE4M3
+    bytes and IQ1_M's fp16 d spread over the top nibbles of its scale words, drawn so the values
+    stay finite and near `scale`."""
+    nb = b.shape[0]
+    if type_name == "MXFP4":  # value = code * 2^(e - 128), codes up to 12
+        e0 = int(round(128 + np.log2(scale / 4)))
+        b[:, 0] = np.clip(e0 + g.integers(-2, 3, nb), 1, 254).astype(np.uint8)
+    elif type_name == "NVFP4":  # value = code * (8 + m) 2^(e - 11), e > 0
+        e0 = int(round(11 + np.log2(scale / 48)))
+        e = np.clip(e0 + g.integers(-1, 2, (nb, 4)), 0, 14)
+        b[:, 0:4] = ((e << 3) | g.integers(0, 8, (nb, 4))).astype(np.uint8)
+    elif type_name == "IQ1_M":  # d's fp16 bits: nibble k in the top of scale word k
+        d = (np.abs(g.standard_normal(nb)) * scale).astype(np.float16).view(np.uint16).astype(np.int64)
+        for k in range(4):
+            hi = 49 + 2 * k
+            b[:, hi] = ((b[:, hi] & 0x0F) | (((d >> (4 * k)) & 15) << 4)).astype(np.uint8)
 
 
 def ggml_layer(type_name, seed, K, N, scale=0.002):
     """N rows of K / block-values blocks of a GGUF type: uniform code and sub-scale bytes, every
     fp16 scale field |N(0,1)| * scale (finite, so the weight is too), as a uint8 (N, row bytes)
     array."""
+    g = rng(seed, "ggml-" + type_name)
+    if type_name in DENSE_TYPES:  # values ~ N(0, (4 scale)^2) in the stored encoding
+        w = (g.standard_normal((N, K)) * 4 * scale).astype(np.float32)
+        if type_name == "F16":
+            w = w.astype(np.float16)
+        elif type_name == "BF16":
+            w = (w.view(np.uint32) >> 16).astype(np.uint16)
+        return np.ascontiguousarray(w).view(np.uint8).reshape(N, K * DENSE_TYPES[type_name])
     vals, nbytes, f16 = GGML_BLOCKS[type_name]
     if K % vals:
         raise ValueError("%s needs K %% %d == 0" % (type_name, vals))
-    g = rng(seed, "ggml-" + type_name)
     nb = N * (K // vals)
     b = g.integers(0, 256, (nb, nbytes), dtype=np.uint8)
     for off in f16:
         b[:, off:off + 2] = (np.abs(g.standard_normal(nb)) * scale).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    _scale_fields(type_name, b, g, scale)
     return b.reshape(N, (K // vals) * nbytes)
 
 
@@ -249,11 +282,13 @@ def prompt_ids(seed, T=64, V=151936):
 
 
 def fp16_decoder(seed, L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, eps=1e-6, theta=1e6, max_pos=4096,
-                 **_):
+                 n_experts=0, moe_I=0, top_k=0, mlp_only=(), **_):
     """A plain (unquantized) fp16 Qwen2-shaped model as a HuggingFace directory holds it: the
     tensors by their HF names, (out, in) projection weights ~N(0, 1/in), q/k/v biases, RMSNorm
     weights near 1, embeddings ~N(0, 0.02**2) with the head tied to them, and the config.json
-    fields. Returns {"tensors": {name: fp16 array}, "config": dict}."""
+    fields. With `n_experts`, the layers not in `mlp_only` are Qwen-MoE sparse blocks: a router
+    `mlp.gate` (E, H) ~N(0, 1/H) and experts `mlp.experts.{e}.{gate,up,down}_proj` of
+    intermediate `moe_I`. Returns {"tensors": {name: fp16 array}, "config": dict}."""
     t = {"model.embed_tokens.weight": (rng(seed, "embed").standard_normal((V, H)) * 0.02).astype(np.float16),
          "model.norm.weight": (1.0 + 0.02 * rng(seed, "final_norm").standard_normal(H)).astype(np.float16)}
     projs = (("self_attn.q_proj", NH * HD, H, True), ("self_attn.k_proj", NKV * HD, H, True),
@@ -261,10 +296,20 @@ def fp16_decoder(seed, L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, eps=1e-6, 
              ("mlp.gate_proj", I, H, False), ("mlp.up_proj", I, H, False), ("mlp.down_proj", H, I, False))
     for i in range(L):
         p = "model.layers.%d." % i
+        sparse = n_experts and i not in mlp_only
         for nm, n_out, n_in, bias in projs:
+            if sparse and nm.startswith("mlp."):
+                continue
             t[p + nm + ".weight"] = (rng(seed, p + nm).standard_normal((n_out, n_in)) / np.sqrt(n_in)).astype(np.float16)
             if bias:
                 t[p + nm + ".bias"] = (rng(seed, p + nm + ".bias").standard_normal(n_out) * 0.02).astype(np.float16)
+        if sparse:
+            t[p + "mlp.gate.weight"] = (rng(seed, p + "router").standard_normal((n_experts, H)) / np.sqrt(H)).astype(
+                np.float16)
+            for e in range(n_experts):
+                for nm, n_out, n_in in (("gate_proj", moe_I, H), ("up_proj", moe_I, H), ("down_proj", H, moe_I)):
+                    q = p + "mlp.experts.%d.%s" % (e, nm)
+                    t[q + ".weight"] = (rng(seed, q).standard_normal((n_out, n_in)) / np.sqrt(n_in)).astype(np.float16)
         t[p + "input_layernorm.weight"] = (1.0 + 0.02 * rng(seed, p + "in_ln").standard_normal(H)).astype(np.float16)
         t[p + "post_attention_layernorm.weight"] = (
             1.0 + 0.02 * rng(seed, p + "post_ln").standard_normal(H)).astype(np.float16)
@@ -273,4 +318,8 @@ def fp16_decoder(seed, L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, eps=1e-6, 
            "num_key_value_heads": NKV, "head_dim": HD, "vocab_size": V, "rms_norm_eps": eps,
            "rope_theta": theta, "tie_word_embeddings": True, "max_position_embeddings": max_pos,
            "torch_dtype": "float16"}
+    if n_experts:
+        cfg.update({"architectures": ["Qwen2MoeForCausalLM"], "model_type": "qwen2_moe", "num_experts": n_experts,
+                    "num_experts_per_tok": top_k, "moe_intermediate_size": moe_I, "norm_topk_prob": True,
+                    "decoder_sparse_step": 1, "mlp_only_layers": sorted(mlp_only)})
     return {"tensors": t, "config": cfg}
