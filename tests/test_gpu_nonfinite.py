@@ -121,3 +121,37 @@ def test_escape_keeps_the_fixed_point_slices(gpu, M, dt):
     assert np.abs(ref - exact).max() / big < 1e-5
     got2, _ = _run(L, x, scales=sc)  # deterministic: the same bits on a second call
     assert np.array_equal(got, got2)
+
+
+def test_rows_near_the_fp32_range_through_the_hi_lo_paths(gpu):
+    """fp32 rows enter the fp16 matrix cores as hi/lo planes scaled by a power of two chosen per
+    row; a finite row whose largest value is ~1e35 (past 2^115) and one of ~1e-30 must come back
+    finite and accurate to their own magnitude -- through the GPTQ prefill GEMM (24 fp32 rows),
+    the Q4_K prefill GEMM (fp32 rows) and the MoE expert GEMMs (fp32 x)."""
+    import torch
+    from oracle import moe, q4k
+    from webpytorch_amd import core
+    M = 24
+    mag = np.ones(M, np.float32)
+    mag[2], mag[7] = 1e35, 1e-30
+
+    def rows_ok(got, ref):
+        assert np.isfinite(got).all()
+        for m in range(M):
+            assert np.abs(got[m] - ref[m]).max() <= 1e-5 * np.abs(ref[m]).max(), m
+    L = _layer()
+    x = synth.activations(12, M, K, np.float32) * mag[:, None]
+    got, ref = _run(L, x)
+    rows_ok(got, ref)
+    W = synth.q4k_layer(13, 1024, 256)
+    xq = synth.activations(13, M, 1024, np.float32) * mag[:, None]
+    got = core.GGMLLinear(W, "Q4_K", 1024, 256)(torch.from_numpy(xq)).cpu().numpy()
+    rows_ok(got, q4k.q4k_matmul(xq, W, 1024, 256))
+    # MoE: h = silu(g) u squares the scale, so x rows of 1e17 make h rows of ~1e35 (the down
+    # projection's row scale) and x rows of 1e-15 make h rows of ~1e-30
+    w = synth.moe_workload(14, T=M, H=256, E=8, I=128, top_k=2, gs=128)
+    mm = np.ones(M, np.float32)
+    mm[2], mm[7] = 1e17, 1e-15
+    xm = w["x"].astype(np.float32) * mm[:, None]
+    got = core.MoEExperts(w["experts"])(torch.from_numpy(xm).cuda(), torch.from_numpy(w["logits"]).cuda(), 2)
+    rows_ok(got.cpu().numpy(), moe.moe_mlp_np(xm, w["logits"], [moe.gptq_expert(e) for e in w["experts"]], 2))

@@ -3,15 +3,15 @@
 //
 // Every workgroup (1024 threads, one per CU) has a role for all layers:
 //   * a 64-column tile of the q|k|v projection;
-//   * a query head: RoPE, attention over the cache, and the head's share of the o projection
-//     (its 64 rows of Wo, all H columns);
-//   * a 64-column chunk of hmid(l) = h(l) + the sum of the heads' o shares;
+//   * a query head: RoPE and attention over the cache, publishing the head's 64 outputs;
+//   * a 64-column tile of the o projection over all heads' outputs, plus the residual:
+//     hmid(l) = h(l) + att @ Wo;
 //   * a 64-column tile of the gate|up projection;
 //   * a (64-column tile, K-slice) of the down projection.
-// A layer is five dependent hops: h(l) -> q|k|v -> heads -> hmid chunks -> gate|up -> down ->
+// A layer is five dependent hops: h(l) -> q|k|v -> heads -> o tiles (hmid) -> gate|up -> down ->
 // h(l + 1).
 //
-// Single-writer results (q|k|v, the heads' o shares, hmid, gate|up) are (tag << 32) | fp32 bits
+// Single-writer results (q|k|v, the heads' outputs, hmid, gate|up) are (tag << 32) | fp32 bits
 // words written and read at device scope (they bypass the per-XCD L2); a tag names (token,
 // layer, phase) and never repeats between consecutive tokens, so no reset is needed.
 // h(l + 1) = hmid(l) + the down projection's K-slices is summed in fixed point instead: each
@@ -23,7 +23,10 @@
 // escape of mma_tile.h (an fp32 side slot read back in term order). The words of a token sit in
 // one of two banks (by the parity of the token's epoch); each step zeroes the other bank for the
 // next step, and the kernel boundary orders the two. (Terms that many workgroups add to the same
-// words serialize at the coherence point, so the heads' o reduction is a hop of its own.)
+// words serialize at the coherence point, so the o projection is a hop of its own: the heads
+// publish their 64 outputs each and every o tile reads all of them, NH * 64 words, where heads
+// publishing their shares of the o projection (H words each, summed by the tiles) made a
+// 2.6 us hop against 0.9 us for the q|k|v -> heads one.)
 // A role's weights for layer l are issued as soon as its layer l-1 work is done, a whole layer
 // ahead of their use, so the HBM traffic of the weights overlaps the chain of dependent steps.
 //
@@ -75,7 +78,7 @@ struct Params {
   int32_t* state;
   float* logits;
   uint32_t* ctl;
-  uint64_t *tq, *tpart, *thmid, *tgu, *tamax;  // q|k|v, heads' o shares [NH][H], hmid, gate|up, arg-max
+  uint64_t *tq, *tatt, *thmid, *tgu, *tamax;  // q|k|v, heads' outputs [NH][64], hmid, gate|up, arg-max
   unsigned long long* fx;  // bank 0 of the fixed-point words of h(l + 1) (bank 1 at fx + bank_words)
   float* fside;            // escape slots: term s of word i at fside + s * LH + i
   size_t bank_words;       // 64-bit words per bank: LH sums, then LH 32-bit masks
@@ -303,55 +306,9 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   i = bi;
 }
 
-// ---- a head's share of the o projection ---------------------------------------------------
-// Column n of Wo over the head's 64 rows: 8 packed words (rows 8i .. 8i + 7 in nibbles 0-7),
-// and the scale and zero point of the one or two quantization groups the rows span (two when
-// the group size is 32: rows 0-31 and 32-63), as raw fp16 bits and nibbles.
-struct OCol {
-  uint32_t q[8];
-  uint32_t s;  // fp16 scale of rows 0-31 | fp16 scale of rows 32-63 << 16
-  uint32_t z;  // zero nibble of rows 0-31 | zero nibble of rows 32-63 << 8
-};
-__device__ __forceinline__ void ocol_issue(OCol& o, const uint32_t* qw, const uint32_t* qz, const __half* sc, int hq,
-                                           int H, int n, int lgs) {
-  n = min(n, H - 1);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o.q[i] = ldg(qw + (uint32_t)((hq * 8 + i) * H + n));
-  const int g0 = (hq * 64) >> lgs, g1 = (hq * 64 + 32) >> lgs;
-  const unsigned short* s16 = reinterpret_cast<const unsigned short*>(sc);
-  o.s = (uint32_t)ldg(s16 + (uint32_t)(g0 * H + n)) | ((uint32_t)ldg(s16 + (uint32_t)(g1 * H + n)) << 16);
-  const int sh = 4 * (n & 7);
-  o.z = ((ldg(qz + (uint32_t)(g0 * (H >> 3) + (n >> 3))) >> sh) & 15u) |
-        (((ldg(qz + (uint32_t)(g1 * (H >> 3) + (n >> 3))) >> sh) & 15u) << 8);
-}
-// sum_k att[k] Wo[64 hq + k][n]: per half of the rows, scale * (sum att c - (z + zoff) sum att),
-// with the halves' attention sums at att[64], att[65].
-__device__ __forceinline__ float ocol_dot(const OCol& o, const float* att, float zoff) {
-  float a[2] = {0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 x0 = *reinterpret_cast<const float4*>(att + 8 * i);
-    const float4 x1 = *reinterpret_cast<const float4*>(att + 8 * i + 4);
-    const uint32_t lo = o.q[i] & 0x0F0F0F0Fu, hi = (o.q[i] >> 4) & 0x0F0F0F0Fu;  // rows 0,2,4,6 / 1,3,5,7
-    float& r = a[i >> 2];
-    r = fmaf(x0.x, (float)(lo & 0xFFu), r);
-    r = fmaf(x0.y, (float)(hi & 0xFFu), r);
-    r = fmaf(x0.z, (float)((lo >> 8) & 0xFFu), r);
-    r = fmaf(x0.w, (float)((hi >> 8) & 0xFFu), r);
-    r = fmaf(x1.x, (float)((lo >> 16) & 0xFFu), r);
-    r = fmaf(x1.y, (float)((hi >> 16) & 0xFFu), r);
-    r = fmaf(x1.z, (float)(lo >> 24), r);
-    r = fmaf(x1.w, (float)(hi >> 24), r);
-  }
-  const float s0 = __half2float(__ushort_as_half((unsigned short)(o.s & 0xFFFFu)));
-  const float s1 = __half2float(__ushort_as_half((unsigned short)(o.s >> 16)));
-  const float z0 = (float)(o.z & 0xFFu) + zoff, z1 = (float)(o.z >> 8) + zoff;
-  return s0 * (a[0] - z0 * att[64]) + s1 * (a[1] - z1 * att[65]);
-}
-
 // LDS carve-up: hin (exchange words and scratch), xs (fp32 activations), xa (A operand steps),
 // cx (bias and x sums per step), red (16 k-parts x 64 columns), red16 (wave scalars), qkv
-// (rotated q, k, the new v, the attention output and its half sums), flags (wait votes).
+// (rotated q, k and the new v), flags (wait votes).
 struct Lds {
   float *hin, *xs;
   unsigned char* xa;
@@ -359,7 +316,7 @@ struct Lds {
   float *red, *red16, *qkv;
   int* flags;  // two sets of wait votes
 };
-constexpr int kQkvFloats = 272;
+constexpr int kQkvFloats = 192;
 
 #define MIQ_PD_INLINE __device__ __attribute__((always_inline)) inline
 
@@ -429,19 +386,16 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
 
 // Query head hq at position pos over positions 0..pos, all layers: RoPE of q and of the kv
 // head's new k (the first query head of each group writes k and v into the caches), scores
-// (q . k) * scale, softmax, sum p v, then the head's o share (all H columns) as tagged words.
-// Four threads per position for the scores, a wave per residue of the position mod 16 and a
-// lane per dimension for the weighted sum. The cache rows of the first 256 positions, the RoPE
-// row and the head's Wo rows are loaded before q/k/v are waited for.
+// (q . k) * scale, softmax, sum p v, published as the head's 64 tagged outputs. Four threads per
+// position for the scores, a wave per residue of the position mod 16 and a lane per dimension
+// for the weighted sum. The cache rows of the first 256 positions and the RoPE row are loaded
+// before q/k/v are waited for.
 MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq, int pos) {
-  float zo = p.zoff;
-  pin(zo);
-  const int H = p.H, NH = p.NH, NKV = p.NKV, LMAX = p.LMAX, rep = NH / NKV, g = hq / rep, S = pos + 1;
+  const int NH = p.NH, NKV = p.NKV, LMAX = p.LMAX, rep = NH / NKV, g = hq / rep, S = pos + 1;
   float* sp = s.hin + 256;  // scores -> probabilities [S]
   float* qs = s.qkv;
   float* kn = s.qkv + 64;
   float* vn = s.qkv + 128;
-  float* att = s.qkv + 192;  // 64 values, then the sums of its halves
   const int jr = (threadIdx.x & 63) < 32 ? (threadIdx.x & 63) : (threadIdx.x & 63) - 32;
   const float cs = p.cos_t[(size_t)pos * 32 + jr], sn = p.sin_t[(size_t)pos * 32 + jr];
   for (int l = 0; l < p.L; ++l) {
@@ -464,8 +418,6 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
     for (int i = 0; i < 4; ++i) pin(kr[i]);
 #pragma unroll
     for (int i = 0; i < 16; ++i) pin(vr[i]);
-    OCol oc;  // the head's Wo rows for column tid
-    ocol_issue(oc, (const uint32_t*)lt[O_QW], (const uint32_t*)lt[O_QZ], (const __half*)lt[O_SC], hq, H, tid, p.lgs);
     const uint32_t tg = c.tag(l, P_QKV);
     PD_MARK(l, 0);
     const bool ok = wait_tagged<1>(
@@ -540,34 +492,35 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
         }
       }
     }
-    // 16 waves' partial sums, combined in wave order, then divided by the softmax denominator
+    // 16 waves' partial sums, combined in wave order, then divided by the softmax denominator.
+    // (The next layer's reads of red and red16 follow its wait's barrier, which this wave joins
+    // only after the reads below.)
     s.red[wave * 64 + lane] = o;
     __syncthreads();
     if (tid < 64) {
       float y = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) y += s.red[w * 64 + tid];
-      y = y / s.red16[16];
-      att[tid] = y;
-      const float lo = wave_sum(tid < 32 ? y : 0.f), hi = wave_sum(tid < 32 ? 0.f : y);
-      if (tid == 0) {
-        att[64] = lo;
-        att[65] = hi;
-      }
+      tput(p.tatt + hq * 64 + tid, c.tag(l, P_ATT), y / s.red16[16]);
     }
-    __syncthreads();
-    PD_MARK(l, 5);
-    if (tid < H) tput(p.tpart + (size_t)hq * H + tid, c.tag(l, P_ATT), ocol_dot(oc, att, zo));
     PD_MARK(l, 2);
   }
   return true;
 }
 
-// hmid(l) of columns [64 t, 64 t + 64): h(l) plus the heads' o shares, summed in head order.
-// h(l) of the chunk is waited for first (it is ready a whole head step earlier).
+// hmid(l) of columns [64 t, 64 t + 64): h(l) plus the o projection of all heads' outputs
+// (K = NH * 64), a tile like the q|k|v one. h(l) of the chunk is waited for first (it is ready a
+// whole head step earlier).
+template <int SA>
 MIQ_PD_INLINE bool role_ored(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
-  const int H = p.H, NH = p.NH, c0 = t * kTile;
+  float zo = p.zoff;
+  pin(zo);
+  const int H = p.H, KO = p.NH * 64, c0 = t * kTile;
   for (int l = 0; l < p.L; ++l) {
+    const uint64_t* lt = p.layers + (size_t)l * kSlots;
+    Tile<__half, SA> w;
+    tile_issue(w, (const uint32_t*)lt[O_QW], (const uint32_t*)lt[O_QZ], (const __half*)lt[O_SC], H, c0, 0, KO / 32,
+               p.lgs);
     float hres = 0.f;
     PD_MARK(l, 0);
     if (l == 0) {
@@ -578,16 +531,22 @@ MIQ_PD_INLINE bool role_ored(const Params& p, const Ctx& c, const Lds& s, int t,
     }
     const uint32_t ta = c.tag(l, P_ATT);
     // (its own vote flags: the flags above may still be read by a slower wave)
-    if (!wait_tagged<2>(
-            NH * kTile, c, p.tpart, [&](int i) { return (i >> 6) * H + c0 + (i & 63); }, [=](int) { return ta; },
-            s.hin + kTile, s.flags + kWaves))
+    if (!wait_tagged<1>(
+            KO, c, p.tatt, [](int i) { return i; }, [=](int) { return ta; }, s.xs, s.flags + kWaves))
       return false;
     PD_MARK(l, 1);
-    if (threadIdx.x < 64) {
-      float y = hres;
-      for (int h = 0; h < NH; ++h) y += s.hin[kTile + h * kTile + threadIdx.x];
-      tput(p.thmid + c0 + threadIdx.x, c.tag(l, P_HMID), y);
+    const int ch = threadIdx.x;
+    if (ch < KO / 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = s.xs[ch * 8 + j];
+      stage_chunk(ch, v, s.xa, s.cx);
     }
+    __syncthreads();
+    PD_MARK(l, 3);
+    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
+    PD_MARK(l, 4);
+    if (threadIdx.x < 64) tput(p.thmid + c0 + threadIdx.x, c.tag(l, P_HMID), hres + y);
     PD_MARK(l, 2);
     __syncthreads();
   }
@@ -797,7 +756,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   } else if ((r -= p.nq) < p.na) {
     ok = role_attn(p, c, s, r, pos);
   } else if ((r -= p.na) < p.no) {
-    ok = role_ored(p, c, s, r, tok);
+    ok = role_ored<SA>(p, c, s, r, tok);
   } else if ((r -= p.no) < p.ngu) {
     ok = role_gu<SA>(p, c, s, r);
   } else if ((r -= p.ngu) < p.nd) {
@@ -813,7 +772,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
 struct Plan {
   int G, nq, na, no, ngu, ksd, nd, lds_a, lds_x, spa, spd;
   size_t lds_bytes, ws_bytes, bank_words;
-  size_t off_tq, off_tpart, off_thmid, off_tgu, off_tamax, off_fx, off_side;
+  size_t off_tq, off_tatt, off_thmid, off_tgu, off_tamax, off_fx, off_side;
 };
 
 static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits, Plan* pl) {
@@ -831,8 +790,9 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
               "decode_persistent: H, NH*HD and I must be multiples of the group size %d", gs);
   // K in 32-value steps, at most kMaxSPQ per k-part of a tile
   auto rows_ok = [&](int K) { return K % 32 == 0 && K <= 32 * kKParts * kMaxSPQ; };
-  MIQ_REQUIRE(rows_ok(H) && H <= kThreads && LMAX <= 8192, MIQ_ERR_UNSUPPORTED,
-              "decode_persistent: H=%d / NH=%d / LMAX=%d out of range", H, NH, LMAX);
+  MIQ_REQUIRE(rows_ok(H) && H <= kThreads && LMAX <= 8192 && NHD <= kThreads &&
+                  (NHD / 32 + kKParts - 1) / kKParts <= (H / 32 + kKParts - 1) / kKParts,
+              MIQ_ERR_UNSUPPORTED, "decode_persistent: H=%d / NH=%d / LMAX=%d out of range", H, NH, LMAX);
   int cus = 0, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
@@ -858,7 +818,7 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
   q.spd = (KS / 32 + kKParts - 1) / kKParts;
   q.lds_a = std::max(std::max(std::max(H, 2 * KS), (NH + 1) * kTile), std::max(256 + LMAX, 2 * q.G));
   q.lds_a = (q.lds_a + 3) & ~3;
-  q.lds_x = (std::max(H, KS) + 63) & ~63;  // even step count: red 16-byte aligned
+  q.lds_x = (std::max(std::max(H, KS), NHD) + 63) & ~63;  // even step count: red 16-byte aligned
   q.lds_bytes = (size_t)(q.lds_a + q.lds_x) * 4 + (size_t)(q.lds_x / 32) * kStepBytes +
                 (size_t)(2 * (q.lds_x / 32) + kKParts * 64 + 32 + kQkvFloats + 2 * kWaves) * 4;
   int lds_max = 0;
@@ -873,7 +833,7 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
     return o;
   };
   q.off_tq = take((size_t)NQ * 8);
-  q.off_tpart = take((size_t)NH * H * 8);
+  q.off_tatt = take((size_t)NH * 64 * 8);
   q.off_thmid = take((size_t)H * 8);
   q.off_tgu = take(2 * (size_t)I * 8);
   q.off_tamax = take(2 * (size_t)q.G * 8);
@@ -946,7 +906,7 @@ extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* em
   p.logits = logits;
   p.ctl = reinterpret_cast<uint32_t*>(w);
   p.tq = reinterpret_cast<uint64_t*>(w + pl.off_tq);
-  p.tpart = reinterpret_cast<uint64_t*>(w + pl.off_tpart);
+  p.tatt = reinterpret_cast<uint64_t*>(w + pl.off_tatt);
   p.thmid = reinterpret_cast<uint64_t*>(w + pl.off_thmid);
   p.tgu = reinterpret_cast<uint64_t*>(w + pl.off_tgu);
   p.tamax = reinterpret_cast<uint64_t*>(w + pl.off_tamax);
