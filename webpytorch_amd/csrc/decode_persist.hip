@@ -355,7 +355,7 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
   for (int l = 0; l < p.L; ++l) {
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
     Tile<__half, SA> w;
-    tile_issue(w, (const uint32_t*)lt[QKV_QW], (const uint32_t*)lt[QKV_QZ], (const __half*)lt[QKV_SC], NQ, c0, 0,
+    tile_issue<__half, SA, true, true>(w, (const uint32_t*)lt[QKV_QW], (const uint32_t*)lt[QKV_QZ], (const __half*)lt[QKV_SC], NQ, c0, 0,
                H / 32, p.lgs);
     float4 nw[2];
     norm_prefetch(nw, (const float*)lt[IN_LN], H);
@@ -368,10 +368,12 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
     PD_MARK(l, 1);
     const int ch = threadIdx.x;
     norm_stage(v, nw, s.red16);
-    if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
+    if (ch < H / 8) stage_digits(ch, v, s.xa, s.cx);
     __syncthreads();
     PD_MARK(l, 3);
-    float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
+    const float4 acc = tile_mma_i8(w, s.xa, s.cx, 0, c0, p.lgs, zo);
+    PD_MARK(l, 5);
+    float y = tile_sum(acc, s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < NQ) {
       y = y / norm_r(s.red16, H, p.eps);
@@ -519,7 +521,7 @@ MIQ_PD_INLINE bool role_ored(const Params& p, const Ctx& c, const Lds& s, int t,
   for (int l = 0; l < p.L; ++l) {
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
     Tile<__half, SA> w;
-    tile_issue(w, (const uint32_t*)lt[O_QW], (const uint32_t*)lt[O_QZ], (const __half*)lt[O_SC], H, c0, 0, KO / 32,
+    tile_issue<__half, SA, true, true>(w, (const uint32_t*)lt[O_QW], (const uint32_t*)lt[O_QZ], (const __half*)lt[O_SC], H, c0, 0, KO / 32,
                p.lgs);
     float hres = 0.f;
     PD_MARK(l, 0);
@@ -540,11 +542,11 @@ MIQ_PD_INLINE bool role_ored(const Params& p, const Ctx& c, const Lds& s, int t,
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = s.xs[ch * 8 + j];
-      stage_chunk(ch, v, s.xa, s.cx);
+      stage_digits(ch, v, s.xa, s.cx);
     }
     __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
+    const float y = tile_sum(tile_mma_i8(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64) tput(p.thmid + c0 + threadIdx.x, c.tag(l, P_HMID), hres + y);
     PD_MARK(l, 2);
@@ -563,7 +565,7 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
   for (int l = 0; l < p.L; ++l) {
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
     Tile<__half, SA> w;
-    tile_issue(w, (const uint32_t*)lt[GU_QW], (const uint32_t*)lt[GU_QZ], (const __half*)lt[GU_SC], N, c0, 0, H / 32,
+    tile_issue<__half, SA, true, true>(w, (const uint32_t*)lt[GU_QW], (const uint32_t*)lt[GU_QZ], (const __half*)lt[GU_SC], N, c0, 0, H / 32,
                p.lgs);
     float4 nw[2];
     norm_prefetch(nw, (const float*)lt[POST_LN], H);
@@ -582,10 +584,10 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = ch < H / 8 ? s.xs[ch * 8 + j] : 0.f;
     norm_stage(v, nw, s.red16);
-    if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
+    if (ch < H / 8) stage_digits(ch, v, s.xa, s.cx);
     __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
+    const float y = tile_sum(tile_mma_i8(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < N)
       tput(p.tgu + c0 + threadIdx.x, c.tag(l, P_GU), y / norm_r(s.red16, H, p.eps));
@@ -605,7 +607,7 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
   for (int l = 0; l < p.L; ++l) {
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
     Tile<__half, SD> w;
-    tile_issue(w, (const uint32_t*)lt[D_QW], (const uint32_t*)lt[D_QZ], (const __half*)lt[D_SC], H, c0, rb, KS / 32,
+    tile_issue<__half, SD, true, true>(w, (const uint32_t*)lt[D_QW], (const uint32_t*)lt[D_QZ], (const __half*)lt[D_SC], H, c0, rb, KS / 32,
                p.lgs);
     const uint32_t tg = c.tag(l, P_GU);
     PD_MARK(l, 0);
@@ -622,11 +624,11 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
         const float gv = s.hin[ch * 8 + j], u = s.hin[KS + ch * 8 + j];
         v[j] = (gv * (1.f / (1.f + expf(-gv)))) * u;
       }
-      stage_chunk(ch, v, s.xa, s.cx);
+      stage_digits(ch, v, s.xa, s.cx);
     }
     __syncthreads();
     PD_MARK(l, 3);
-    const float y = tile_sum(tile_mma(w, s.xa, s.cx, rb, c0, p.lgs, zo), s.red);
+    const float y = tile_sum(tile_mma_i8(w, s.xa, s.cx, rb, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
     if (threadIdx.x < 64 && c0 + (int)threadIdx.x < H) fx_put(fx_row(p, c.ep, l), c0 + threadIdx.x, y, sl);
     PD_MARK(l, 2);
@@ -646,8 +648,8 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   // three tiles in flight: b and b + G are loaded before the wait for h; then each step issues
   // the tile two steps ahead and holds (pins) the next one once the current one is computed
   Tile<float, SA> t0, t1, t2;
-  if (b < ntile) tile_issue(t0, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
-  if (b + G < ntile) tile_issue(t1, p.head_qw, p.head_qz, p.head_sc, V, (b + G) * kTile, 0, H / 32, p.lgs);
+  if (b < ntile) tile_issue<float, SA, true, true>(t0, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
+  if (b + G < ntile) tile_issue<float, SA, true, true>(t1, p.head_qw, p.head_qz, p.head_sc, V, (b + G) * kTile, 0, H / 32, p.lgs);
   float4 nw[2];
   norm_prefetch(nw, p.final_norm, H);
   PD_MARK(p.L, 0);
@@ -656,7 +658,7 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   PD_MARK(p.L, 1);
   const int ch = threadIdx.x;
   norm_stage(v, nw, s.red16);
-  if (ch < H / 8) stage_chunk(ch, v, s.xa, s.cx);
+  if (ch < H / 8) stage_digits(ch, v, s.xa, s.cx);
   __syncthreads();
   const float rn = norm_r(s.red16, H, p.eps);
   float bv = -INFINITY;
@@ -665,9 +667,9 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
                   __attribute__((always_inline)) {
     if (t >= ntile) return;  // uniform
     if (t + 2 * G < ntile)
-      tile_issue<float, SA, false>(ahead, p.head_qw, p.head_qz, p.head_sc, V, (t + 2 * G) * kTile, 0, H / 32, p.lgs);
+      tile_issue<float, SA, false, true>(ahead, p.head_qw, p.head_qz, p.head_sc, V, (t + 2 * G) * kTile, 0, H / 32, p.lgs);
     const int n = t * kTile + (int)threadIdx.x;
-    const float y = tile_sum(tile_mma(cur, s.xa, s.cx, 0, t * kTile, p.lgs, zo), s.red) / rn;
+    const float y = tile_sum(tile_mma_i8(cur, s.xa, s.cx, 0, t * kTile, p.lgs, zo), s.red) / rn;
     if (threadIdx.x < 64 && n < V) {
       p.logits[n] = y;
       if (better(y, n, bv, bi) || (bv != bv && y == y)) { bv = y; bi = n; }
@@ -782,16 +784,16 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
   MIQ_REQUIRE(bits == 4 && HD == 64, MIQ_ERR_UNSUPPORTED, "decode_persistent: needs int4 and head dim 64 (bits=%d HD=%d)",
               bits, HD);
   const int NQ = (NH + 2 * NKV) * HD, NHD = NH * HD;
-  MIQ_REQUIRE(H % kTile == 0 && NQ % kTile == 0 && (2 * I) % kTile == 0 && gs >= 32 && (gs & (gs - 1)) == 0 &&
+  MIQ_REQUIRE(H % kTile == 0 && NQ % kTile == 0 && (2 * I) % kTile == 0 && gs >= 64 && (gs & (gs - 1)) == 0 &&
                   V % 8 == 0,
               MIQ_ERR_UNSUPPORTED,
-              "decode_persistent: H, q|k|v width and 2I must be multiples of 64, gs a power of two >= 32, V of 8");
+              "decode_persistent: H, q|k|v width and 2I must be multiples of 64, gs a power of two >= 64, V of 8");
   MIQ_REQUIRE(H % gs == 0 && NHD % gs == 0 && I % gs == 0, MIQ_ERR_UNSUPPORTED,
               "decode_persistent: H, NH*HD and I must be multiples of the group size %d", gs);
-  // K in 32-value steps, at most kMaxSPQ per k-part of a tile
-  auto rows_ok = [&](int K) { return K % 32 == 0 && K <= 32 * kKParts * kMaxSPQ; };
+  // K in 64-value steps (the int8 digit tile), at most kMaxSPQ / 2 per k-part of a tile
+  auto rows_ok = [&](int K) { return K % 64 == 0 && K <= 32 * kKParts * kMaxSPQ; };
   MIQ_REQUIRE(rows_ok(H) && H <= kThreads && LMAX <= 8192 && NHD <= kThreads &&
-                  (NHD / 32 + kKParts - 1) / kKParts <= (H / 32 + kKParts - 1) / kKParts,
+                  NHD % 64 == 0 && (NHD / 64 + kKParts - 1) / kKParts <= (H / 64 + kKParts - 1) / kKParts,
               MIQ_ERR_UNSUPPORTED, "decode_persistent: H=%d / NH=%d / LMAX=%d out of range", H, NH, LMAX);
   int cus = 0, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -805,7 +807,7 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
   q.ngu = 2 * I / kTile;
   q.ksd = 0;
   for (int k = 8; k >= 1; k >>= 1) {
-    if (I % (8 * k) || !rows_ok(I / k) || 2 * (I / k) > 4 * kThreads) continue;
+    if (I % (64 * k) || !rows_ok(I / k) || 2 * (I / k) > 4 * kThreads) continue;
     if (q.nq + q.na + q.no + q.ngu + q.no * k > q.G) continue;
     q.ksd = k;
     break;
@@ -814,8 +816,8 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
               "decode_persistent: the roles of this shape do not fit %d workgroups", q.G);
   q.nd = q.no * q.ksd;
   const int KS = I / q.ksd;
-  q.spa = (H / 32 + kKParts - 1) / kKParts;
-  q.spd = (KS / 32 + kKParts - 1) / kKParts;
+  q.spa = 2 * ((H / 64 + kKParts - 1) / kKParts);  // 32-k halves per k-part (64-k steps dealt whole)
+  q.spd = 2 * ((KS / 64 + kKParts - 1) / kKParts);
   q.lds_a = std::max(std::max(std::max(H, 2 * KS), (NH + 1) * kTile), std::max(256 + LMAX, 2 * q.G));
   q.lds_a = (q.lds_a + 3) & ~3;
   q.lds_x = (std::max(std::max(H, KS), NHD) + 63) & ~63;  // even step count: red 16-byte aligned
