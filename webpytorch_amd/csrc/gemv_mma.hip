@@ -6,9 +6,10 @@
 // Grid (tiles of 256 columns, K-slices); a 256-thread workgroup holds 4 waves, one per 64
 // columns, each taking every 32-k step of its K-slice. A wave issues the loads of all its steps
 // (16 bytes of codes per lane per step, scales and zeros per group) at entry, then the
-// workgroup stages its slice of x in LDS as exact three-term bf16 splits (the A operand of the
-// shared tile code, mma_tile.h) and the waves run four MFMA chains that share each step's A
-// fragment. With one K-slice the workgroup writes y. With several, the slices of a column meet
+// workgroup stages its slice of x in LDS as four int8 digit rows per 64-k step (30-bit fixed
+// point at the step's own scale, the int8 digit tile of mma_tile.h) and the waves run four
+// v_mfma_i32_16x16x64_i8 per 64-k step that share its A fragment, the codes entering as int8.
+// With one K-slice the workgroup writes y. With several, the slices of a column meet
 // in one 64-bit word of the workspace's zeroed counter region: each adds its partial as a
 // fixed-point integer (2^-24 resolution, offset to stay non-negative) together with a count in
 // the top bits, by one agent-scope atomic whose return value tells the last slice that it is
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   static_assert(XM == 0 || (sizeof(XT) == 4 && !PERM), "input transforms take fp32 rows in k order");
   constexpr int NG = SPQ / 4;  // groups per slice
   using SV = typename Scales4<ST>::T;
-  __shared__ __align__(16) unsigned char xa[SPQ * kStepBytes];
+  __shared__ __align__(16) unsigned char xa[(SPQ / 2) * kStep8Bytes];
   __shared__ float2 cx[SPQ];
   __shared__ int is_last;
   __shared__ float ssw[kThreadsG / 64];
@@ -153,13 +154,14 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = (v[j] * (1.f / (1.f + expf(-v[j])))) * __uint_as_float(u[j]);
   }
-  stage_chunk(ch, v, xa, cx);
+  stage_digits(ch, v, xa, cx);
   __syncthreads();
   float rn = 1.f;  // RMSNorm: r of the row (the same value in every workgroup)
   if constexpr (XM == 1) rn = sqrtf((((ssw[0] + ssw[1]) + ssw[2]) + ssw[3]) / (float)K + eps);
-  // A rows 0-2 are read by lanes 0-2 of each 16; the other rows of D are never used
-  const bool arow = (lane & 15) < 3;
-  const BMasks bm = b_masks();
+  // A rows 0-3 (the digits) are read by lanes 0-3 of each 16; the other rows of D are never used
+  const bool arow = (lane & 15) < 4;
+  uint32_t mk = 0x0F0F0F0Fu;
+  asm volatile("" : "+v"(mk));
   const unsigned char* ap = xa + (lane >> 4) * 64 + (lane & 15) * 16;
   const int zsh = (cl & 7) * 4;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -174,30 +176,33 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
       }
     }
     if (4 * gi < ns) {
-      floatx4 d[4];
+      float pg[4] = {0.f, 0.f, 0.f, 0.f};
+      float xs = 0.f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) d[t] = (floatx4){0.f, 0.f, 0.f, 0.f};
-      float cs = 0.f, xs = 0.f;
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const int i = 4 * gi + s4;
-        bf16x8 av;
-        if (arow) av = *reinterpret_cast<const bf16x8*>(ap + i * kStepBytes);
-        const float2 cxi = cx[i];
-        cs += cxi.x;
-        xs += cxi.y;
-        const uint32_t wt[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+      for (int h = 0; h < 2; ++h) {  // the group's two 64-k steps
+        const int j = 2 * gi + h;
+        i32x4 av = {0, 0, 0, 0};
+        if (arow) av = *reinterpret_cast<const i32x4*>(ap + j * kStep8Bytes);
+        const float2 cxj = cx[j];
+        xs += cxj.y;
+        const uint32_t qa[4] = {w[2 * j].x, w[2 * j].y, w[2 * j].z, w[2 * j].w};
+        const uint32_t qb[4] = {w[2 * j + 1].x, w[2 * j + 1].y, w[2 * j + 1].z, w[2 * j + 1].w};
+        i32x4 dq[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const u32x4 bw = b_bf16(wt[t], bm);
-          d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bw), d[t], 0, 0, 0);
+          const i32x4 b = {(int)(qa[t] & mk), (int)((qa[t] >> 4) & mk), (int)(qb[t] & mk), (int)((qb[t] >> 4) & mk)};
+          dq[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, (i32x4){0, 0, 0, 0}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int lo = dq[t][0] + (dq[t][1] << 8), hi = dq[t][2] + (dq[t][3] << 8);
+          pg[t] = fmaf(fmaf((float)hi, 65536.f, (float)lo), cxj.x, pg[t]);
         }
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const float pv = (d[t][0] + d[t][1]) + d[t][2];
         const float zc = (float)((zw[gi] >> (zsh + 4 * t)) & 15u) + zoff;
-        acc[t] = fmaf(Scales4<ST>::get(sv[gi], t), pv - fmaf(zc, xs, cs), acc[t]);
+        acc[t] = fmaf(Scales4<ST>::get(sv[gi], t), pg[t] - zc * xs, acc[t]);
       }
     }
   }
