@@ -145,24 +145,24 @@ def ggml_bench(torch, core, type_name, copies=12, reps=24):
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
 
 
-def q4k_gemm_bench(torch, core, copies=4, reps=8):
-    """GGUF Q4_K prefill GEMM at the Llama-3-8B up_proj shape: x (M, 4096) fp16 or fp32 -> y fp32
-    (M, 14336) on the matrix cores, over `copies` distinct weight copies; TFLOP/s and the fraction
-    of the dense fp16 peak."""
+def ggml_gemm_bench(torch, core, type_name="Q4_K", reps=10):
+    """GGUF prefill GEMM (`miq_ggml_gemm`) at the Llama-3-8B up_proj shape: x (M, 4096) fp16 or
+    fp32 -> y fp32 (M, 14336) on the matrix cores, over enough distinct weight copies (>= 330 MB,
+    above the 256 MB Infinity Cache) that every launch reads its weights from HBM; TFLOP/s and
+    the fraction of the dense fp16 peak."""
     K, N = 4096, 14336
-    nb = N * K // 256
-    w = torch.randint(0, 256, (copies, nb, 144), dtype=torch.uint8, device="cuda")
-    w[:, :, 1] &= 0x3B  # finite fp16 d and dmin
-    w[:, :, 3] &= 0x3B
-    w = w.reshape(copies, N, -1)
-    res = {}
+    vals, blk = {"Q4_K": (256, 144), "Q5_K": (256, 176), "Q6_K": (256, 210), "Q8_0": (32, 34)}[type_name]
+    nb = N * K // vals
+    copies = max(2, -(-330_000_000 // (nb * blk)))
+    w = random_blocks(torch, type_name, copies, nb, blk).reshape(copies, N, -1)
+    res = {"copies": copies, "weight_bytes": nb * blk}
     for M, dt in ((64, torch.float16), (512, torch.float16), (512, torch.float32)):
         x = torch.randn((M, K), device="cuda").to(dt)
         out = torch.empty((M, N), device="cuda")
 
         def run(x=x, out=out):
             for i in range(reps):
-                core.ggml_matmul(x, w[i % copies], "Q4_K", K, N, out=out)
+                core.ggml_matmul(x, w[i % copies], type_name, K, N, out=out)
         run()
         torch.cuda.synchronize()
         g = capture(torch, run)
@@ -175,10 +175,65 @@ def q4k_gemm_bench(torch, core, copies=4, reps=8):
     return res
 
 
+def random_blocks(torch, type_name, copies, nb, blk):
+    """Uniform random block bytes on the device with every fp16 scale field small and finite."""
+    w = torch.randint(0, 256, (copies, nb, blk), dtype=torch.uint8, device="cuda")
+    for off in {"Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,), "Q8_0": (0,)}[type_name]:
+        w[:, :, off + 1] &= 0x17  # fp16 exponent field <= 5: |scale| < 2^-9
+    return w
 
-def gemm_bench(torch, core, Ms=(16, 128, 512), copies=32, reps=32):
+
+def prefill_ttft(torch, llm, core, T=64, reps=5):
+    """Time to first token of a T-token prompt on a Llama-3-8B-shaped decoder whose weights stay
+    in a Q4_K_M file's mix of GGUF encodings: q, k, o, gate and up in Q4_K; v and down in Q6_K on
+    the layers that recipe gives more bits (the first and last eighth of the layers and every
+    third one between), Q4_K elsewhere; the output head in Q6_K (random blocks; the embedding
+    table as a GGUF file's decoded fp32 one).
+    One prefill = embedding, 32 layers of RMSNorm, q|k|v, RoPE + KV write, attention, o, RMSNorm,
+    gate|up, SwiGLU and down (the projections at T rows on the matrix cores), then the last row's
+    head GEMV and arg-max."""
+    L, H, NH, NKV, HD, I, V = 32, 4096, 32, 8, 128, 14336, 128256
+    more_bits = lambda i: i < L // 8 or i >= 7 * L // 8 or (i - L // 8) % 3 == 2  # noqa: E731
+
+    def lin(t, K, N):
+        vals, blk = (256, 144) if t == "Q4_K" else (256, 210)
+        return core.GGMLLinear(random_blocks(torch, t, 1, N * K // vals, blk).reshape(-1), t, K, N)
+    layers = []
+    for i in range(L):
+        hi = "Q6_K" if more_bits(i) else "Q4_K"
+        layers.append({"q": lin("Q4_K", H, NH * HD), "k": lin("Q4_K", H, NKV * HD), "v": lin(hi, H, NKV * HD),
+                       "o": lin("Q4_K", NH * HD, H), "gate": lin("Q4_K", H, I), "up": lin("Q4_K", H, I),
+                       "down": lin(hi, I, H), "in_ln": torch.ones(H), "post_ln": torch.ones(H)})
+    w = {"layers": layers, "embed": torch.randn((V, H), device="cuda") * 0.02,
+         "final_norm": torch.ones(H), "head_linear": lin("Q6_K", H, V),
+         "cfg": dict(L=L, H=H, NH=NH, NKV=NKV, HD=HD, I=I, V=V, gs=128, bits=4, eps=1e-5, theta=500000.0)}
+    m = llm.CausalLM.from_weights(w, lmax=256)
+    nbytes = sum(p.packed.numel() for lay in m.layers for k in ("qkv", "o", "gate_up", "down")
+                 for p in (lay[k].parts if hasattr(lay[k], "parts") else [lay[k]]))
+    ids = torch.randint(0, V, (T,), dtype=torch.int32, device="cuda")
+    ts = []
+    for _ in range(reps + 1):
+        m.reset()
+        m.ids[:T].copy_(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m._step(T)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts[1:])[len(ts[1:]) // 2]
+    flops = 2.0 * T * L * (H * (NH + 2 * NKV) * HD + NH * HD * H + 3 * H * I)
+    res = {"prompt_tokens": T, "ttft_ms": round(t * 1e3, 3), "prefill_tokens_per_s": round(T / t, 1),
+           "layer_weight_bytes": int(nbytes), "projection_TFLOPs": round(flops / t / 1e12, 1),
+           "model": "Llama-3-8B shape (32 layers, hidden 4096, 32/8 heads of 128, intermediate 14336, vocab 128256)"}
+    del m, w, layers
+    torch.cuda.empty_cache()
+    return res
+
+
+def gemm_bench(torch, core, Ms=(16, 128, 512), copies=40, reps=40):
     """GPTQ int4 prefill GEMM, act-order (rows repacked at load), K = N = 4096, gs = 128:
-    x fp16 (M, 4096) -> y fp16 (M, 4096), over `copies` distinct weight copies."""
+    x fp16 (M, 4096) -> y fp16 (M, 4096), over `copies` distinct weight copies (40 x 8.4 MB, well
+    above the 256 MB Infinity Cache)."""
     K = N = 4096
     perm = torch.randperm(K, device="cuda").int()
     ws = [make_layer(torch, K, N, "f16", False) for _ in range(copies)]
@@ -622,7 +677,8 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the token's GEMVs alone and a plain 1 GiB copy, for hardware-counter runs")
     ap.add_argument("--gemv-large", action="store_true", help="only the GEMV operator on 7B-class shapes")
-    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "q4k_gemm", "moe", "config0", "decode7b", "ggml"],
+    ap.add_argument("--only", choices=["gemm", "gemm_int8", "q4k", "q4k_gemm", "kq_gemm", "prefill", "moe", "config0",
+                                      "decode7b", "ggml"],
                     help="one kernel benchmark and a plain 1 GiB copy, for profiler runs")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the persistent decode step and a plain 1 GiB copy, for hardware-counter runs")
@@ -644,7 +700,9 @@ def main():
         return
     if a.only:
         fn = {"gemm": lambda: gemm_bench(torch, core, Ms=(512,)), "gemm_int8": lambda: gemm_int8_bench(torch, core),
-              "q4k": lambda: q4k_bench(torch, core), "q4k_gemm": lambda: q4k_gemm_bench(torch, core),
+              "q4k": lambda: q4k_bench(torch, core), "q4k_gemm": lambda: ggml_gemm_bench(torch, core, "Q4_K"),
+              "kq_gemm": lambda: {t: ggml_gemm_bench(torch, core, t) for t in ("Q5_K", "Q6_K", "Q8_0")},
+              "prefill": lambda: prefill_ttft(torch, llm, core),
               "moe": lambda: moe_bench(torch, core),
               "config0": lambda: config0_bench(torch, core), "decode7b": lambda: decode_7b(torch, llm),
               "ggml": lambda: {t: ggml_bench(torch, core, t) for t in ("Q6_K", "Q8_0")}}[a.only]
@@ -734,7 +792,10 @@ def main():
         res["q4k_gemv_llama3_8b_up"] = q4k_bench(torch, core)
         res["q6k_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q6_K")
         res["q8_0_gemv_llama3_8b_up"] = ggml_bench(torch, core, "Q8_0")
-        res["q4k_gemm_llama3_8b_up"] = q4k_gemm_bench(torch, core)
+        res["q4k_gemm_llama3_8b_up"] = ggml_gemm_bench(torch, core, "Q4_K")
+        for t in ("Q5_K", "Q6_K", "Q8_0"):
+            res["%s_gemm_llama3_8b_up" % t.lower()] = ggml_gemm_bench(torch, core, t)
+        res["prefill64_ttft_llama3_8b_q4_k_m"] = prefill_ttft(torch, llm, core)
         res["gptq_gemm_act_order_4096"] = gemm_bench(torch, core)
         res["gptq_gemm_int8_per_channel_4096"] = gemm_int8_bench(torch, core)
         res["moe_qwen3_t256"] = moe_bench(torch, core)

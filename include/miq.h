@@ -198,6 +198,20 @@ int miq_q4k_gemm_workspace(int M, int K, int N, int x_dtype, size_t* bytes);
 int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const float* bias, void* out, int out_dtype,
                  int M, int K, int N, void* workspace, size_t ws_bytes, void* stream);
 
+/* The same matrix-core prefill GEMM for the four types of a Q4_K_M / Q5_K_M file, by ggml type
+ * id: 12 Q4_K, 13 Q5_K, 14 Q6_K, 8 Q8_0 (8 consecutive blocks per 256-value step); K a multiple
+ * of 256 (<= 16384); miq_q4k_gemm is this call with type 12. Every code enters the fp16 matrix
+ * cores as an exact integer: Q5_K as sc c (< 2048), Q6_K as (c - 32) sl and (c - 32) 16 sh with
+ * sc = 16 sh + sl (two products into one accumulator), Q8_0 as q with d applied per block. The
+ * workspace (miq_ggml_gemm_workspace bytes) is laid out as miq_q4k_gemm's. Other types:
+ * MIQ_ERR_UNSUPPORTED.
+ * Replaces: `ggml_matmul` / `_ggml_run` with the batched kernel `_GGML_GEMM_*` and the type's
+ * decoder (`_Q4K_DEC` 3117, `_Q5K_DEC` 3137, `_Q6K_DEC` 3159, `_Q8_0_DEC` 3072)
+ * (webtorch/_core.py:2904-2975, 3720-3779). */
+int miq_ggml_gemm_workspace(int M, int K, int N, int x_dtype, int ggml_type, size_t* bytes);
+int miq_ggml_gemm(const void* x, int x_dtype, const uint8_t* w, int ggml_type, const float* bias, void* out,
+                  int out_dtype, int M, int K, int N, void* workspace, size_t ws_bytes, void* stream);
+
 /* out[M][N] = x[M][K] @ W^T + bias for the native GGUF types, by ggml type id:
  *   32-value blocks: 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 20 IQ4_NL (18, 20, 22, 24, 34, 18
  *     bytes), 39 MXFP4 (17);
@@ -207,8 +221,8 @@ int miq_q4k_gemm(const void* x, int x_dtype, const uint8_t* w, const float* bias
  *   40 NVFP4 (64 values, 36 bytes), 41 Q1_0 (128, 18), 42 Q2_0 (64, 18);
  *   unquantized matrices: 0 F32, 1 F16, 30 BF16 (any K).
  * W = N rows of K / (values per block) blocks as the file stores them; w and x 16-byte aligned;
- * M <= 65535. Q4_K also has miq_q4k_gemv / miq_q4k_gemm (faster). Other types:
- * MIQ_ERR_UNSUPPORTED.
+ * M <= 65535 (each row a GEMV pass). Q4_K also has miq_q4k_gemv, and Q4_K, Q5_K, Q6_K and Q8_0
+ * rows beyond a few run faster through miq_ggml_gemm. Other types: MIQ_ERR_UNSUPPORTED.
  * Replaces: `ggml_matmul` / `_ggml_run` for these types (webtorch/_core.py:3720-3779) with the
  * decode kernel `_GGML_GEMV_*` (webtorch/_core.py:2985-3044) and the type's decoder
  * (`_Q8_0_DEC` 3072, `_IQ4NL_DEC` 3080, `_IQ4XS_DEC` 3094, `_Q5K_DEC` 3137, `_Q6K_DEC` 3159,

@@ -379,9 +379,31 @@ def test_persistent_step_wait_timeout_drains(gpu, monkeypatch):
     monkeypatch.delenv("MIQ_PD_SPIN_TICKS")
     assert a.persistent_error() & 1
     assert torch.equal(a.state[:4], state[:4])
+    a._step(1)  # the normal bound again: a step after a failed one leaves at entry
+    torch.cuda.synchronize()
+    assert a.persistent_error() & 1
+    assert torch.equal(a.state[:4], state[:4])
     a.reset()
     assert a.persistent_error() == 0
-    assert a.generate(ids, 8, use_graph=False).tokens == want
+    assert a.generate(ids, 8, use_graph=False).tokens == want and a.fallback_steps == 0
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_persistent_timeout_falls_back_to_the_launch_sequence(gpu, monkeypatch, use_graph):
+    """Steps that time out (a spin bound of one tick, as when another kernel keeps workgroups off
+    their CUs) leave the decode state alone, and generate() finishes the sequence with the
+    launch sequence: the launch sequence's ids, a RuntimeWarning, every decode step counted."""
+    sh = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+    a, b, ids = _persistent_pair(sh, 15, 64, 16)
+    want = b.generate(ids, 8).tokens
+    monkeypatch.setenv("MIQ_PD_SPIN_TICKS", "1")
+    a._graph = None  # captured now, with the one-tick bound
+    with pytest.warns(RuntimeWarning, match="launch sequence"):
+        got = a.generate(ids, 8, use_graph=use_graph)
+    monkeypatch.delenv("MIQ_PD_SPIN_TICKS")
+    assert got.tokens == want and a.fallback_steps == 7 and a.persistent_error() == 0
+    a._graph = None
+    assert a.generate(ids, 8).tokens == want and a.fallback_steps == 0
 
 
 def test_persistent_step_graph_replay_and_position_guard(gpu):

@@ -281,3 +281,70 @@ def test_q4k_gemm_row_scales_and_nonfinite(gpu):
     assert np.isnan(got[3]).all() and not np.isfinite(got[5]).any()
     keep = [m for m in range(M) if m not in (3, 5)]
     assert np.abs(got[keep] - ref[keep]).max() <= 1e-5 * np.abs(ref[keep]).max()
+
+
+# ---- Q5_K / Q6_K / Q8_0 prefill rows on the matrix cores -----------------------------------
+
+KQ_GEMM_CASES = [(9, 256, 64, np.float32), (100, 768, 70, np.float16), (100, 768, 70, np.float32),
+                 (33, 1280, 1000, np.float32), (520, 256, 7200, np.float16), (64, 4096, 14336, np.float16),
+                 (300, 2048, 512, np.float32)]
+
+
+@pytest.mark.parametrize("type_name", ["Q5_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("M,K,N,xdt", KQ_GEMM_CASES)
+def test_kquant_gemm_prefill_rows(gpu, type_name, M, K, N, xdt):
+    """Rows above the GEMV's take `miq_ggml_gemm`: against the oracle's exact dequant times x,
+    at row- and column-tile tails, with bias and fp16 output. K = 768 and 1280 give rows of an odd
+    number of super-blocks, so Q6_K's 210-byte blocks start at both 2-byte residues; (520, 256,
+    7200) takes two 16-column groups per wave. Block bytes are uniform random: Q6_K scales cover
+    -128..127 and codes 0..63, Q8_0 codes -128..127."""
+    import torch
+    from oracle import ggml
+    from webpytorch_amd import core
+    assert core._ggml_gemm_taken(type_name, M, K)
+    W = synth.ggml_layer(type_name, M + K + N, K, N)
+    b = np.linspace(-1, 1, N).astype(np.float32)
+    lin = core.GGMLLinear(W, type_name, K, N, bias=b)
+    x = synth.activations(M + 1, M, K, xdt)
+    ref = ggml.ggml_matmul(x.astype(np.float32), W, type_name, K, N) + b
+    got = lin(torch.from_numpy(x)).cpu().numpy()
+    assert _rel(got, ref) < 1e-5
+    assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+    got16 = lin.forward(torch.from_numpy(x), out_dtype=torch.float16).cpu().numpy()
+    assert np.all(np.abs(got16.astype(np.float32) - ref) <= 1e-3 + 1e-2 * np.abs(ref))
+    assert np.array_equal(lin(torch.from_numpy(x)).cpu().numpy(), got)  # deterministic
+
+
+@pytest.mark.parametrize("type_name", ["Q5_K", "Q6_K", "Q8_0"])
+def test_kquant_gemm_extreme_codes_and_row_scales(gpu, type_name):
+    """Every code and scale at its extreme (Q6_K: codes 0 and 63, scales -128 and 127; Q8_0:
+    codes -128 and 127; Q5_K: codes 31 with 6-bit scales 63), fp32 rows of very different
+    magnitude, and NaN / Inf rows that leave the other rows alone."""
+    import torch
+    from oracle import ggml
+    from webpytorch_amd import core
+    K, N, M = 1024, 96, 24
+    W = synth.ggml_layer(type_name, 9, K, N).reshape(-1, ggml.DEQUANT[type_name][2]).copy()
+    g = np.random.default_rng(9)
+    if type_name == "Q6_K":
+        W[:, 0:192] = g.choice(np.array([0x00, 0xFF], np.uint8), W[:, 0:192].shape)
+        W[:, 192:208] = g.choice(np.array([0x80, 0x7F], np.uint8), W[:, 192:208].shape)
+    elif type_name == "Q8_0":
+        W[:, 2:34] = g.choice(np.array([0x80, 0x7F], np.uint8), W[:, 2:34].shape)
+    else:
+        W[:, 4:176] = 0xFF
+    W = W.reshape(-1)
+    lin = core.GGMLLinear(W, type_name, K, N)
+    x = synth.activations(5, M, K, np.float32)
+    x *= np.logspace(-6, 6, M, dtype=np.float32)[:, None]
+    ref = ggml.ggml_matmul(x, W, type_name, K, N)
+    got = lin(torch.from_numpy(x)).cpu().numpy()
+    for m in range(M):
+        assert np.abs(got[m] - ref[m]).max() <= 1e-5 * np.abs(ref[m]).max(), m
+    x[3, 7] = np.nan
+    x[5, 9] = np.inf
+    got = lin(torch.from_numpy(x)).cpu().numpy()
+    assert np.isnan(got[3]).all() and not np.isfinite(got[5]).any()
+    keep = [m for m in range(M) if m not in (3, 5)]
+    for m in keep:
+        assert np.abs(got[m] - ref[m]).max() <= 1e-5 * np.abs(ref[m]).max(), m

@@ -29,8 +29,13 @@ def test_ggml_check_runs_once_per_mode(gpu, monkeypatch, type_name):
         lin(torch.from_numpy(synth.activations(1, M, K, np.float32)))
         assert ("ggml", type_name, mode, dev) in core._CHECKED
     assert len([k for k in core._CHECKED if k[0] == "ggml"]) == 3
-    lin(torch.from_numpy(synth.activations(1, 24, K, np.float32)))  # prefill rows: Q4_K's GEMM
-    assert (("ggml", type_name, -1, dev) in core._CHECKED) == (type_name == "Q4_K")
+    lin(torch.from_numpy(synth.activations(1, 24, K, np.float32)))  # prefill rows: the matrix-core GEMM
+    assert ("ggml", type_name, -1, dev) in core._CHECKED
+    if type_name == "Q8_0":  # K not a multiple of 256: prefill rows take the GEMV row by row
+        core._CHECKED.discard(("ggml", type_name, -1, dev))
+        lin96 = core.GGMLLinear(synth.q8_0_layer(2, 96, N), "Q8_0", 96, N)
+        lin96(torch.from_numpy(synth.activations(2, 24, 96, np.float32)))
+        assert ("ggml", type_name, -1, dev) not in core._CHECKED
 
 
 @pytest.mark.parametrize("M,dt", [(1, "float32"), (4, "float32"), (12, "float16"), (40, "float16"), (1, "float16")])

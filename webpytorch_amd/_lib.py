@@ -43,6 +43,8 @@ SIGNATURES = {
     "miq_moe_ggml_gemv": [_p, _i, _p, _i, _i, _i, _i, _i, _p, _i, _sz, _p, _i, _i, _p],
     "miq_q4k_gemm_workspace": [_i, _i, _i, _i, _p],
     "miq_q4k_gemm": [_p, _i, _p, _p, _p, _i, _i, _i, _i, _p, _sz, _p],
+    "miq_ggml_gemm_workspace": [_i, _i, _i, _i, _i, _p],
+    "miq_ggml_gemm": [_p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _p, _sz, _p],
     "miq_embed": [_p, _p, _p, _i, _i, _i, _p],
     "miq_embed_f32": [_p, _p, _p, _i, _i, _i, _p],
     "miq_rmsnorm": [_p, _p, _p, _i, _i, _f, _p],

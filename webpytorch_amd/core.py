@@ -460,14 +460,27 @@ def rows_from_transposed(words, n, rowb):
 GGML_GEMV_MAX_M = 8
 
 
-def q4k_gemm_workspace_bytes(M, K, N, x_dtype):
-    key = ("q4kgemm", M, K, N, x_dtype)
+# Types whose rows above GGML_GEMV_MAX_M run on the matrix cores (`miq_ggml_gemm`), for K a
+# multiple of 256: the four types of a Q4_K_M / Q5_K_M file
+GGML_GEMM_TYPES = ("Q4_K", "Q5_K", "Q6_K", "Q8_0")
+
+
+def ggml_gemm_workspace_bytes(M, K, N, x_dtype, type_name="Q4_K"):
+    key = ("ggmlgemm", M, K, N, x_dtype, type_name)
     b = _WS_BYTES.get(key)
     if b is None:
         n = ctypes.c_size_t(0)
-        _lib.call("miq_q4k_gemm_workspace", M, K, N, x_dtype, ctypes.byref(n))
+        _lib.call("miq_ggml_gemm_workspace", M, K, N, x_dtype, _NATIVE_TYPES[type_name][2], ctypes.byref(n))
         b = _WS_BYTES[key] = int(n.value)
     return b
+
+
+def q4k_gemm_workspace_bytes(M, K, N, x_dtype):
+    return ggml_gemm_workspace_bytes(M, K, N, x_dtype, "Q4_K")
+
+
+def _ggml_gemm_taken(type_name, M, K):
+    return type_name in GGML_GEMM_TYPES and M > GGML_GEMV_MAX_M and K % 256 == 0
 
 
 def _ggml_selfcheck(type_name, mode):
@@ -479,6 +492,8 @@ def _ggml_selfcheck(type_name, mode):
     from . import synth
     vals = _NATIVE_TYPES[type_name][0]
     K = vals if vals > 1 else 72  # an unquantized row: 72 values (a ragged count of 16-byte words)
+    if mode < 0:
+        K = 256  # the GEMM walks K in 256-value steps (8 blocks of a 32-value type)
     raw = torch.from_numpy(synth.ggml_layer(type_name, 0, K, 2, scale=0.01)).to(device())
     W = ggml_dequant(raw.reshape(-1), type_name, 2 * K // vals).reshape(2, K)
     g = np.random.default_rng(vals)
@@ -512,17 +527,17 @@ def ggml_matmul(xf, packed, type_name, K, N, bias=None, out_dtype=torch.float32,
                                                                            int(N) * rowb))
     xf = aligned16(as_activation(xf).contiguous())
     M = int(xf.shape[0])
-    gemm = type_name == "Q4_K" and M > GGML_GEMV_MAX_M
+    gemm = _ggml_gemm_taken(type_name, M, int(K))
     mode = -1 if gemm else (M if M <= 2 else 0)
     if _check and M and _first_use(("ggml", type_name, mode)):
         _ggml_selfcheck(type_name, mode)
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=xf.device)
     if gemm:  # prefill rows on the matrix cores
-        need = q4k_gemm_workspace_bytes(M, int(K), int(N), dtype_code(xf))
+        need = ggml_gemm_workspace_bytes(M, int(K), int(N), dtype_code(xf), type_name)
         ws = workspace(need)
-        _lib.call("miq_q4k_gemm", ptr(xf), dtype_code(xf), ptr(packed), ptr(bias), ptr(out), dtype_code(out), M,
-                  int(K), int(N), ptr(ws), ws.numel(), stream_handle())
+        _lib.call("miq_ggml_gemm", ptr(xf), dtype_code(xf), ptr(packed), _NATIVE_TYPES[type_name][2], ptr(bias),
+                  ptr(out), dtype_code(out), M, int(K), int(N), ptr(ws), ws.numel(), stream_handle())
     elif type_name == "Q4_K":
         _lib.call("miq_q4k_gemv", ptr(xf), dtype_code(xf), ptr(packed), ptr(bias), ptr(out), dtype_code(out),
                   M, int(K), int(N), stream_handle())

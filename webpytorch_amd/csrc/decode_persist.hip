@@ -35,8 +35,9 @@
 // token id, appends it to the history and advances the position, exactly as argmax_kernel does.
 //
 // Waits are bounded: a workgroup that is still waiting `spin_limit` wall-clock ticks after it
-// started sets an error bit and leaves, so every wait chain ends and the grid drains (the host
-// reads the bit; a step that failed leaves its bank dirty, so the caller resets the workspace).
+// started sets an error bit and leaves, so every wait chain ends and the grid drains. A step that
+// failed leaves its exchange words and bank dirty: later steps see the bit and leave at entry,
+// and the host resets the workspace and runs the rest of the sequence as the launch sequence.
 // All workgroups must be resident at once; the host sizes the grid to the CU count and checks
 // occupancy, and the step must not share the GPU with other work.
 //
@@ -746,6 +747,15 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(p.ctl + 1, 2u);
     return;
   }
+  // After a timed-out step the exchange words and fixed-point banks are dirty (its epoch is
+  // reused), so every later step leaves at entry without touching the decode state until the
+  // workspace is reset; the host then finishes the sequence with the launch sequence. One
+  // thread reads the bit and the workgroup follows it, so its waves cannot split on it.
+  if (threadIdx.x == 0) s.flags[0] = (int)__hip_atomic_load(p.ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const bool failed_before = s.flags[0] & 1;
+  __syncthreads();
+  if (failed_before) return;
   {  // the next token's bank back to zero (this token's was zeroed by the previous step)
     unsigned long long* z = p.fx + ((c.ep + 1u) & 1u) * p.bank_words;
     for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < p.bank_words; i += (size_t)gridDim.x * kThreads)

@@ -16,7 +16,10 @@ persistent launch instead of 5 launches per layer: one workgroup per CU with a f
 (a 64-column tile of a projection, a query head, or a tile and K-slice of the down
 projection); the workgroups exchange activations through tagged device-scope words, so the
 step has no kernel boundary and each projection's weights are fetched a layer ahead.
-`persistent=False` keeps the launch sequence; prefill always uses it.
+`persistent=False` keeps the launch sequence; prefill always uses it. The persistent step needs
+every workgroup resident at once: if other work on the GPU keeps one off its CU, the step's
+bounded waits time out, it and the steps after it leave the decode state alone, and
+`generate` finishes the sequence with the launch sequence (with a RuntimeWarning).
 
 Layout choices: q, k and v (and gate and up) share their input, so their GPTQ tensors are
 concatenated along the output dimension at load time and run as one GEMV (per-column groups
@@ -27,6 +30,7 @@ per-column quantization makes the reference's 4096-row blocks, `llm.py:594-602`,
 import ctypes
 import math
 import time
+import warnings
 
 import numpy as np
 import torch
@@ -209,6 +213,7 @@ class CausalLM:
             self.fused = False
         self._alloc()
         self._graph = None
+        self.fallback_steps = 0  # tokens of the last generate() that a timed-out persistent step left
 
     @classmethod
     def from_weights(cls, weights, lmax=256, fused=True, persistent=None):
@@ -527,6 +532,29 @@ class CausalLM:
         if n_prompt + max_new > self.lmax:
             raise ValueError("prompt (%d) + max_new (%d) exceeds lmax %d" % (n_prompt, max_new, self.lmax))
 
+    def _finish_after_timeout(self, max_new):
+        """After the steps of a sequence: if a persistent step timed out waiting (it shared the
+        GPU with other work, so its workgroups were not all resident), that step and every later
+        one left the decode state alone; reset the exchange workspace and run the remaining
+        tokens as the launch sequence. Returns how many tokens took that path."""
+        err = self.persistent_error()
+        if not err:
+            return 0
+        if err & 2:
+            raise _lib.MiqError("persistent decode step failed (error bits %d): position past the KV cache" % err)
+        left = max_new - int(self.state[1].item())
+        warnings.warn("persistent decode step timed out waiting (another kernel on the GPU?); the remaining %d "
+                      "token(s) run as the launch sequence" % left, RuntimeWarning, stacklevel=3)
+        pws, self.pws = self.pws, None
+        try:
+            pws.zero_()
+            for _ in range(left):
+                self._step(1)
+            torch.cuda.synchronize()
+        finally:
+            self.pws = pws
+        return left
+
     def generate(self, ids, max_new, use_graph=True):
         """Greedy decode with no end token (`webtorch/llm.py:1716-1817` with do_sample off):
         prefill the prompt, then max_new - 1 decode steps. Returns a GenResult whose `tokens`
@@ -549,11 +577,8 @@ class CausalLM:
             else:
                 self._step(1)
         torch.cuda.synchronize()
+        self.fallback_steps = self._finish_after_timeout(max_new)
         dt = time.perf_counter() - t1
-        err = self.persistent_error()
-        if err:
-            raise _lib.MiqError("persistent decode step failed (error bits %d): %s" % (
-                err, "a workgroup timed out waiting" if err & 1 else "position past the KV cache"))
         toks = [int(t) for t in self.history[:max_new].cpu().numpy()]
         rate = (max_new - 1) / dt if max_new > 1 and dt > 0 else 0.0
         return GenResult("", toks, ttft, rate)
