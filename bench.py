@@ -300,7 +300,33 @@ def config0_bench(torch, core, reps=256):
     torch.cuda.empty_cache()
     return {"K": K, "N": N, "x": "fp16 (1, 896)", "y": "fp16 (1, 4864)", "bytes": nb, "launches": reps,
             "us_per_call": round(t * 1e6, 3), "GBs": round(nb / t / 1e9, 1),
-            "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4), "single_launch_us": round(lat * 1e6, 3)}
+            "frac": round(nb / t / 1e9 / HBM_PEAK_GBS, 4), "single_launch_us": round(lat * 1e6, 3),
+            "replay_floor": replay_floor(torch, nb, reps)}
+
+
+def replay_floor(torch, nbytes, reps=256):
+    """What R back-to-back launches in one graph cost with (almost) no work, per launch: an
+    empty kernel (torch's spin kernel with 0 cycles), a one-wave 16-byte copy, and a copy of
+    nbytes / 2 bytes (nbytes moved, as a GEMV of nbytes reads) over R distinct sources (above the
+    Infinity Cache in total, so the reads come from HBM)."""
+    def per_launch(fn):
+        fn()
+        torch.cuda.synchronize()
+        g = capture(torch, fn)
+        t = timed(torch, g.replay, 3) / reps
+        del g
+        return round(t * 1e6, 3)
+    empty = per_launch(lambda: [torch.cuda._sleep(0) for _ in range(reps)])
+    s4, d4 = torch.ones(4, device="cuda"), torch.empty(4, device="cuda")
+    tiny = per_launch(lambda: [d4.copy_(s4) for _ in range(reps)])
+    n = nbytes // 2 // 4
+    srcs = torch.ones((reps, n), device="cuda")
+    dst = torch.empty(n, device="cuda")
+    copy = per_launch(lambda: [dst.copy_(srcs[i]) for i in range(reps)])
+    del srcs
+    torch.cuda.empty_cache()
+    return {"empty_kernel_us": empty, "copy_16B_us": tiny, "copy_us": copy, "copy_bytes_moved": 2 * n * 4,
+            "kernels": "torch spin kernel (0 cycles); torch elementwise copy"}
 
 
 def gemm_int8_bench(torch, core, Ms=(16, 128, 512), copies=24, reps=24):
@@ -712,7 +738,7 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if a.decode_only:
-        m = llm.CausalLM.from_weights(synth.decoder_weights(5, **synth.QWEN2_05B), lmax=256)
+        m = llm.CausalLM.from_weights(synth.decoder_weights(5, **synth.QWEN2_05B), lmax=max(256, 64 + a.steps + 8))
         t, _, _ = decode_step_time(torch, m, synth.prompt_ids(5, 64, synth.QWEN2_05B["V"]), 2, a.steps)
         copy_bytes = copy_calibration(torch)
         print(json.dumps({"decode_step_us": round(t * 1e6, 2), "copy_bytes_read": copy_bytes,

@@ -396,8 +396,11 @@ int miq_argmax_advance(const float* logits, int V, int32_t* ids, int32_t* histor
  * error bits (1: a workgroup waited more than 100 ms -- not all workgroups were resident --
  * 2: state[0] >= LMAX), read by the caller after the step. The environment variable
  * MIQ_PD_SPIN_TICKS (wall-clock ticks, read at each call) shortens the 100 ms bound, so that
- * tests can drive the timeout path; after such a step the workspace must be zeroed again. Steps on one workspace must not
- * overlap, and the step must not share the GPU with other kernels. */
+ * tests can drive the timeout path. After a step that timed out, every later step on the
+ * workspace leaves at entry without touching the decode state (its exchange words are dirty)
+ * until the workspace is zeroed; the caller then continues the sequence, e.g. with the launch
+ * sequence above. Steps on one workspace must not overlap, and the step must not share the
+ * GPU with other kernels. */
 int miq_decode_persistent_plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs,
                                int bits, int* grid, size_t* ws_bytes);
 int miq_decode_persistent(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
@@ -406,6 +409,22 @@ int miq_decode_persistent(const uint64_t* layer_table, const void* embed, const 
                           int hist_len, int32_t* state, float* logits, void* ws, size_t ws_bytes, int L,
                           int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits,
                           float eps, float zoff, float head_zoff, void* stream);
+
+/* The same step with its phase timeline: thread 0 of every workgroup stores the GPU wall clock
+ * (s_memrealtime ticks) at each phase mark into trace[(wg (L + 2) + l) 8 + k] (uint64, 8-byte
+ * aligned, at least grid (L + 2) 8 words, zeroed by the caller; unvisited slots stay 0): for
+ * layer l < L, k = 0 role weights issued, 1 inputs received, 3 inputs staged, 5 (q|k|v tiles)
+ * matrix product done, 4 tile summed (attention: q|k|v staged), 2 result published; l = L the
+ * head (0 issued, 1 h(L) received, 2 arg-max published); l = L + 1 the kernel (0 entry,
+ * 1 exit). Results are those of miq_decode_persistent. A diagnostic with no counterpart in the
+ * reference, for the per-hop latency figures of the step (`python -m webpytorch_amd.pd_trace`). */
+int miq_decode_persistent_trace(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
+                                const int32_t* head_qzeros, const float* head_scales, const float* final_norm,
+                                const float* cos_tab, const float* sin_tab, int32_t* ids, int32_t* history,
+                                int hist_len, int32_t* state, float* logits, void* ws, size_t ws_bytes, int L,
+                                int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits,
+                                float eps, float zoff, float head_zoff, uint64_t* trace, size_t trace_words,
+                                void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Capture and replay (replaces WebGPUPlatform.beginCapture / endCapture / replay,

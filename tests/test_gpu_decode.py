@@ -424,3 +424,33 @@ def test_persistent_step_graph_replay_and_position_guard(gpu):
     a.reset()
     assert a.persistent_error() == 0
     assert a.generate(ids, 20).tokens == want
+
+
+def test_persistent_trace_matches_untraced_step(gpu):
+    """`miq_decode_persistent_trace` computes what `miq_decode_persistent` does (same logits,
+    bit for bit, and the same token) and leaves ordered phase marks: for every role workgroup and
+    layer, weights issued <= inputs received <= result published, and the kernel's exit after its
+    entry; `pd_trace.summarize` reads them."""
+    import io
+    import torch
+    from webpytorch_amd import llm, pd_trace
+    sh = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+    w = synth.decoder_weights(16, gaussian=True, **sh)
+    ids = synth.prompt_ids(16, 20, sh["V"])
+    a = llm.CausalLM.from_weights(w, lmax=64, persistent=True)
+    b = llm.CausalLM.from_weights(w, lmax=64, persistent=True)
+    for m in (a, b):
+        m.generate(ids, 1, use_graph=False)
+    t, _ = pd_trace.trace_steps(a, 1)
+    b._step(1)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.buf["logits"].cpu().numpy(), b.buf["logits"].cpu().numpy())
+    assert torch.equal(a.state[:4], b.state[:4]) and a.persistent_error() == 0
+    roles = pd_trace.role_ranges(a, t)
+    for r in roles.values():
+        assert len(r) > 0
+        for l in range(a.L):
+            assert np.all(t[r, l, 0] > 0) and np.all(t[r, l, 0] <= t[r, l, 1]) and np.all(t[r, l, 1] <= t[r, l, 2])
+    assert np.all(t[:, a.L + 1, 1] >= t[:, a.L + 1, 0]) and np.all(t[:, a.L, 1] > 0)
+    res = pd_trace.summarize(a, t, out=io.StringIO())
+    assert set(res["hops"]) == {"qkv->attn", "attn->ored", "ored->gu", "gu->down", "down->qkv"}

@@ -58,6 +58,7 @@ SIGNATURES = {
     "miq_q4k_dequant_f32": [_p, _p, _i64, _p],
     "miq_decode_persistent_plan": [_i] * 10 + [_p, _p],
     "miq_decode_persistent": [_p] * 10 + [_i, _p, _p, _p, _sz] + [_i] * 10 + [_f] * 3 + [_p],
+    "miq_decode_persistent_trace": [_p] * 10 + [_i, _p, _p, _p, _sz] + [_i] * 10 + [_f] * 3 + [_p, _sz, _p],
     "miq_q4k_gemv": [_p, _i, _p, _p, _p, _i, _i, _i, _i, _p],
     "miq_ggml_gemv": [_p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _p],
     "miq_ggml_dequant_f32": [_p, _i, _p, _i64, _p],

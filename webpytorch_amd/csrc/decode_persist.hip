@@ -88,22 +88,16 @@ struct Params {
   int lds_a, lds_x;      // LDS regions (floats): exchange/staging, activations
   float eps, scale, zoff, head_zoff;
   long long spin_limit;
-#ifdef MIQ_PD_TRACE
-  unsigned long long* trace;  // [G][L + 2][8] wall-clock stamps of the phase marks below
-#endif
+  unsigned long long* trace;  // null, or [G][L + 2][8] wall-clock stamps of the phase marks below
 };
 
-// Phase marks (stage k of layer l of this workgroup); empty unless built with MIQ_PD_TRACE.
-#ifdef MIQ_PD_TRACE
-#define PD_MARK(l, k)                                                                          \
-  do {                                                                                         \
-    if (threadIdx.x == 0) p.trace[((size_t)blockIdx.x * (p.L + 2) + (l)) * 8 + (k)] = wall_clock64(); \
+// Phase mark k of layer l of this workgroup (miq_decode_persistent_trace): thread 0 stores the
+// wall clock. Without a trace buffer the mark is one scalar test of a kernel argument.
+#define PD_MARK(l, k)                                                                                \
+  do {                                                                                               \
+    if (p.trace && threadIdx.x == 0)                                                                 \
+      p.trace[((size_t)blockIdx.x * (p.L + 2) + (l)) * 8 + (k)] = wall_clock64();                   \
   } while (0)
-#else
-#define PD_MARK(l, k) \
-  do {                \
-  } while (0)
-#endif
 
 __device__ __forceinline__ void tput(uint64_t* p, uint32_t tag, float v) {
   __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -873,12 +867,12 @@ extern "C" int miq_decode_persistent_plan(int L, int H, int NH, int NKV, int HD,
   return MIQ_OK;
 }
 
-extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
-                                     const int32_t* head_qzeros, const float* head_scales, const float* final_norm,
-                                     const float* cos_tab, const float* sin_tab, int32_t* ids, int32_t* history,
-                                     int hist_len, int32_t* state, float* logits, void* ws, size_t ws_bytes, int L,
-                                     int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits, float eps,
-                                     float zoff, float head_zoff, void* stream) {
+static int decode_persistent(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
+                             const int32_t* head_qzeros, const float* head_scales, const float* final_norm,
+                             const float* cos_tab, const float* sin_tab, int32_t* ids, int32_t* history, int hist_len,
+                             int32_t* state, float* logits, void* ws, size_t ws_bytes, int L, int H, int NH, int NKV,
+                             int HD, int I, int V, int LMAX, int gs, int bits, float eps, float zoff, float head_zoff,
+                             void* stream, uint64_t* trace) {
   pd::Plan pl;
   const int rc = pd::plan(L, H, NH, NKV, HD, I, V, LMAX, gs, bits, &pl);
   if (rc != MIQ_OK) return rc;
@@ -948,6 +942,7 @@ extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* em
   p.scale = 1.0f / sqrtf((float)HD);
   p.zoff = zoff;
   p.head_zoff = head_zoff;
+  p.trace = reinterpret_cast<unsigned long long*>(trace);
   p.spin_limit = (long long)khz * 100;  // 100 ms
   if (const char* e = getenv("MIQ_PD_SPIN_TICKS")) {  // a shorter bound, for tests of the error path
     const long long t = atoll(e);
@@ -956,4 +951,33 @@ extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* em
   hipLaunchKernelGGL(kfn, dim3(pl.G), dim3(pd::kThreads), pl.lds_bytes,
                      static_cast<hipStream_t>(stream), p);
   return check_launch("decode_persistent");
+}
+
+extern "C" int miq_decode_persistent(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
+                                     const int32_t* head_qzeros, const float* head_scales, const float* final_norm,
+                                     const float* cos_tab, const float* sin_tab, int32_t* ids, int32_t* history,
+                                     int hist_len, int32_t* state, float* logits, void* ws, size_t ws_bytes, int L,
+                                     int H, int NH, int NKV, int HD, int I, int V, int LMAX, int gs, int bits, float eps,
+                                     float zoff, float head_zoff, void* stream) {
+  return decode_persistent(layer_table, embed, head_qweight, head_qzeros, head_scales, final_norm, cos_tab, sin_tab, ids,
+                           history, hist_len, state, logits, ws, ws_bytes, L, H, NH, NKV, HD, I, V, LMAX, gs, bits, eps,
+                           zoff, head_zoff, stream, nullptr);
+}
+
+extern "C" int miq_decode_persistent_trace(const uint64_t* layer_table, const void* embed, const int32_t* head_qweight,
+                                           const int32_t* head_qzeros, const float* head_scales,
+                                           const float* final_norm, const float* cos_tab, const float* sin_tab,
+                                           int32_t* ids, int32_t* history, int hist_len, int32_t* state, float* logits,
+                                           void* ws, size_t ws_bytes, int L, int H, int NH, int NKV, int HD, int I, int V,
+                                           int LMAX, int gs, int bits, float eps, float zoff, float head_zoff,
+                                           uint64_t* trace, size_t trace_words, void* stream) {
+  int grid = 0;
+  const int rc = miq_decode_persistent_plan(L, H, NH, NKV, HD, I, V, LMAX, gs, bits, &grid, nullptr);
+  if (rc != MIQ_OK) return rc;
+  MIQ_REQUIRE(trace && aligned(trace, 8), MIQ_ERR_INVALID, "decode_persistent_trace: null or unaligned trace buffer");
+  MIQ_REQUIRE(trace_words >= (size_t)grid * (L + 2) * 8, MIQ_ERR_INVALID,
+              "decode_persistent_trace: trace holds %zu words, need %zu", trace_words, (size_t)grid * (L + 2) * 8);
+  return decode_persistent(layer_table, embed, head_qweight, head_qzeros, head_scales, final_norm, cos_tab, sin_tab, ids,
+                           history, hist_len, state, logits, ws, ws_bytes, L, H, NH, NKV, HD, I, V, LMAX, gs, bits, eps,
+                           zoff, head_zoff, stream, trace);
 }

@@ -4,7 +4,9 @@
 // y[n] = sum_k x[k] W[k][n] (+ bias), W[k][n] = s[g][n] (q[k][n] - (z[g][n] + zoff)).
 //
 // Grid (tiles of 256 columns, K-slices); a 256-thread workgroup holds 4 waves, one per 64
-// columns, each taking every 32-k step of its K-slice. A wave issues the loads of all its steps
+// columns, each taking every 32-k step of its K-slice. For K of 4 to 12 groups the grid is
+// instead tiles of 64 columns with the whole K: the four waves take a quarter of the groups
+// each and add their partials through LDS, so no reduction crosses workgroups (WS). A wave issues the loads of all its steps
 // (16 bytes of codes per lane per step, scales and zeros per group) at entry, then the
 // workgroup stages its slice of x in LDS as four int8 digit rows per 64-k step (30-bit fixed
 // point at the step's own scale, the int8 digit tile of mma_tile.h) and the waves run four
@@ -50,7 +52,7 @@ constexpr size_t kMaxFixCols = kFixMaxWords;
 #endif
 constexpr int kNormLoads = 8;  // float4 loads per thread of an RMSNorm row issued up front (K <= 8192)
 
-template <typename XT, typename ST, typename OT, int SPQ, bool PERM, int XM>
+template <typename XT, typename ST, typename OT, int SPQ, bool PERM, int XM, bool WS>
 __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restrict__ x, const int32_t* __restrict__ perm,
                                                              const uint32_t* __restrict__ qw,
                                                              const uint32_t* __restrict__ qz, const ST* __restrict__ sc,
@@ -60,18 +62,24 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
                                                              float zoff, int slice_steps, const float* __restrict__ nw,
                                                              float eps) {
   static_assert(XM == 0 || (sizeof(XT) == 4 && !PERM), "input transforms take fp32 rows in k order");
-  constexpr int NG = SPQ / 4;  // groups per slice
+  constexpr int NG = SPQ / 4;            // groups per wave
+  constexpr int XS = WS ? 4 * SPQ : SPQ;  // staged steps per workgroup
   using SV = typename Scales4<ST>::T;
-  __shared__ __align__(16) unsigned char xa[(SPQ / 2) * kStep8Bytes];
-  __shared__ float2 cx[SPQ];
+  __shared__ __align__(16) unsigned char xa[(XS / 2) * kStep8Bytes];
+  __shared__ float2 cx[XS];
   __shared__ int is_last;
   __shared__ float ssw[kThreadsG / 64];
+  __shared__ float wsum[WS ? kThreadsG : 1];
   const int tile = blockIdx.x, sl = blockIdx.y, kslices = gridDim.y;
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int st0 = sl * slice_steps;
-  const int ns = min(slice_steps, K / 32 - st0);  // a multiple of 4, > 0 by the planner
-  const int rb = st0 * 4;                          // first packed row of the slice
-  const int c = tile * 256 + wave * 64 + (lane & 15) * 4;
+  const int ns = min(slice_steps, K / 32 - st0);  // the workgroup's steps: a multiple of 4, > 0 by the planner
+  // WS: the four waves share the tile's 64 columns and split the slice's groups (the first
+  // waves one group fewer when they do not divide); else each wave takes 64 of 256 columns
+  const int gw0 = WS ? wave * (ns / 4) / 4 : 0, gw1 = WS ? (wave + 1) * (ns / 4) / 4 : ns / 4;
+  const int wns = 4 * (gw1 - gw0);               // this wave's steps (> 0: the planner gives WS >= 4 groups)
+  const int rb = (st0 + 4 * gw0) * 4;            // first packed row of the wave's steps
+  const int c = WS ? tile * 64 + (lane & 15) * 4 : tile * 256 + wave * 64 + (lane & 15) * 4;
   const int cl = min(c, N - 4);                    // loads stay in bounds past N
   // this thread's 8 activations of the slice (or their permutation indices) as raw 16-byte
   // loads, issued before the weights; gathering and converting wait until the weight loads are
@@ -103,14 +111,14 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   // steps past the slice's end reload its last step (a select, not a branch: a branch around a
   // load makes the compiler's wait counts conservative at the join)
   auto wload = [&](int i) __attribute__((always_inline)) {
-    return *reinterpret_cast<const uint4*>(wp + (size_t)(4 * min(i, ns - 1)) * N);
+    return *reinterpret_cast<const uint4*>(wp + (size_t)(4 * min(i, wns - 1)) * N);
   };
   // the scales and zeros first (the first group's fold needs them), then the codes of the first
   // DEPTH steps; each group issues the codes DEPTH steps ahead of it
   constexpr int DEPTH = (MIQ_GM_DEPTH > 0 && MIQ_GM_DEPTH < SPQ) ? MIQ_GM_DEPTH : SPQ;
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
-    const int g = (rb >> 4) + min(gi, (ns >> 2) - 1);  // 16 packed rows per group
+    const int g = (rb >> 4) + min(gi, (wns >> 2) - 1);  // 16 packed rows per group
     sv[gi] = Scales4<ST>::load(sc + (size_t)g * N + cl);
     zw[gi] = qz[(size_t)g * (N >> 3) + (cl >> 3)];
   }
@@ -162,7 +170,8 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   const bool arow = (lane & 15) < 4;
   uint32_t mk = 0x0F0F0F0Fu;
   asm volatile("" : "+v"(mk));
-  const unsigned char* ap = xa + (lane >> 4) * 64 + (lane & 15) * 16;
+  const unsigned char* ap = xa + (lane >> 4) * 64 + (lane & 15) * 16 + (size_t)(2 * gw0) * kStep8Bytes;
+  const float2* cw = cx + 2 * gw0;  // the wave's 64-k steps among the staged ones
   const int zsh = (cl & 7) * 4;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -175,7 +184,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (4 * gi < ns) {
+    if (4 * gi < wns) {
       float pg[4] = {0.f, 0.f, 0.f, 0.f};
       float xs = 0.f;
 #pragma unroll
@@ -183,7 +192,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
         const int j = 2 * gi + h;
         i32x4 av = {0, 0, 0, 0};
         if (arow) av = *reinterpret_cast<const i32x4*>(ap + j * kStep8Bytes);
-        const float2 cxj = cx[j];
+        const float2 cxj = cw[j];
         xs += cxj.y;
         const uint32_t qa[4] = {w[2 * j].x, w[2 * j].y, w[2 * j].z, w[2 * j].w};
         const uint32_t qb[4] = {w[2 * j + 1].x, w[2 * j + 1].y, w[2 * j + 1].z, w[2 * j + 1].w};
@@ -211,6 +220,18 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
     for (int t = 0; t < 4; ++t) acc[t] = acc[t] / rn;
   }
   const bool mine = lane < 16 && c < N;
+  if constexpr (WS) {  // the waves' partials of the same 64 columns, summed in wave order
+    if (lane < 16)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) wsum[wave * 64 + lane * 4 + t] = acc[t];
+    __syncthreads();
+    const int n = tile * 64 + (int)threadIdx.x;
+    if (threadIdx.x < 64 && n < N) {
+      const float y = ((wsum[threadIdx.x] + wsum[64 + threadIdx.x]) + wsum[128 + threadIdx.x]) + wsum[192 + threadIdx.x];
+      out[n] = from_f32<OT>(bias ? y + bias[n] : y);
+    }
+    return;
+  }
   if (kslices == 1) {
     if (mine)
 #pragma unroll
@@ -268,6 +289,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
 struct Plan {
   int tiles, kslices, slice_steps, spq;
   bool fixed;  // split K reduced in fixed-point words of the counter region
+  bool ws;     // 64-column tiles, K split over the workgroup's waves (no reduction across workgroups)
   size_t ws_bytes;
 };
 
@@ -296,6 +318,20 @@ static bool plan(int K, int N, Plan* p) {
   if (p->kslices > kMaxSlices || (p->kslices > 1 && p->tiles > kMaxCounters)) return false;
   p->spq = ss <= 4 ? 4 : ss <= 8 ? 8 : ss <= 12 ? 12 : ss <= 16 ? 16 : 24;
   p->fixed = p->kslices > 1 && (size_t)N <= kMaxFixCols;
+  // K of 4 to 12 groups: 64-column tiles whose four waves split K and add their partials in LDS,
+  // with no reduction across workgroups (measured on one-row graphs, us per call: 896 -> 4864
+  // 3.51 -> 3.20, 896 -> 1152 3.20 -> 2.92, 896 -> 9728 4.04 -> 3.43, 896 -> 151936 15.5 -> 14.3,
+  // 1536 -> 8960 4.21 -> 4.06; at 16 groups the split slices were faster: 2048 -> 8192 4.35
+  // against 4.56, 2048 -> 2048 3.35 against 4.04)
+  const int groups = steps / 4;
+  p->ws = groups >= 4 && groups <= 12;
+  if (p->ws) {
+    p->tiles = (N + 63) / 64;
+    p->kslices = 1;
+    p->slice_steps = steps;
+    p->spq = 4 * ((groups + 3) / 4);
+    p->fixed = false;
+  }
   // after the counter region: fp32 partials [kslices][N] (slow path) or the fixed-point
   // words' escape slots, same shape
   p->ws_bytes = p->kslices == 1 ? 0 : kCounterBytes + (size_t)p->kslices * N * 4;
@@ -312,7 +348,14 @@ static int launch(const Plan& pl, const void* x, const int32_t* perm, const int3
   unsigned long long* fixacc = pl.fixed ? static_cast<unsigned long long*>(ws) : nullptr;
   dim3 grid(pl.tiles, pl.kslices);
 #define MIQ_GM_LAUNCH(S, P)                                                                                        \
-  hipLaunchKernelGGL((gemv_mma_kernel<XT, ST, OT, S, P, XM>), grid, dim3(kThreadsG), 0, st,                     \
+  if (pl.ws) {                                                                                                     \
+    if constexpr (S <= 16)                                                                                         \
+      hipLaunchKernelGGL((gemv_mma_kernel<XT, ST, OT, S, P, XM, true>), grid, dim3(kThreadsG), 0, st,             \
+                         static_cast<const XT*>(x), perm, reinterpret_cast<const uint32_t*>(qw),                     \
+                         reinterpret_cast<const uint32_t*>(qz), static_cast<const ST*>(sc), bias,                    \
+                         static_cast<OT*>(out), partials, counters, fixacc, K, N, zoff, pl.slice_steps, nw, eps);    \
+  } else                                                                                                           \
+  hipLaunchKernelGGL((gemv_mma_kernel<XT, ST, OT, S, P, XM, false>), grid, dim3(kThreadsG), 0, st,              \
                      static_cast<const XT*>(x), perm, reinterpret_cast<const uint32_t*>(qw),                         \
                      reinterpret_cast<const uint32_t*>(qz), static_cast<const ST*>(sc), bias, static_cast<OT*>(out), \
                      partials, counters, fixacc, K, N, zoff, pl.slice_steps, nw, eps)
