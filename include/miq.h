@@ -69,9 +69,10 @@ int miq_gptq_repack_rows(const int32_t* qweight, const int32_t* perm, int32_t* o
  * follow them. One workspace must not serve two calls that run concurrently.
  * Split-K sums are exact for every input: a K-slice partial that is NaN, infinite or of
  * magnitude >= 2^22 (beyond the fixed-point words) reaches the final sum as an fp32 value, so
- * NaN and infinities propagate as in an fp32 sum. (The one-row int4 kernel computes with exact
- * bf16 splits of x against biased codes, in which an infinite activation meets itself with the
- * opposite sign: an infinite x gives NaN, not +-Inf, in the outputs it reaches.) */
+ * NaN and infinities propagate as in an fp32 sum. (The one-row int4 kernel holds each 64-k step
+ * of x in fixed point at the step's own scale, which a non-finite value has not: such a step
+ * scales its products by NaN, so an infinite x gives NaN, not +-Inf, in the outputs it
+ * reaches.) */
 int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, int x_dtype, size_t* bytes);
 
 /* Decode GEMV / skinny GEMM: out[M][N] = x[M][K] (gathered through perm if non-NULL)

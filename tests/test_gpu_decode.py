@@ -355,8 +355,8 @@ def test_persistent_step_matches_launch_sequence(gpu, sh, prompt, steps, lmax):
     assert a.persistent_error() == 0
     assert np.array_equal(a.state[:4].cpu().numpy(), b.state[:4].cpu().numpy())
     # the caches the persistent step wrote are the ones the launch sequence wrote (both fp32
-    # accumulations; the persistent step's bf16-split matrix-core products carry a 128-bias
-    # that cancels to ~1e-6 of the values' scale)
+    # accumulations, in different orders; the persistent step's int8 matrix-core products hold x
+    # in 30-bit fixed point per 64-k step, within 2^-31 of the step's largest value)
     n = prompt + steps
     for ca, cb in ((a.kc, b.kc), (a.vc, b.vc)):
         ga, gb = ca[:, :, :n].cpu().numpy(), cb[:, :, :n].cpu().numpy()

@@ -165,10 +165,12 @@ def test_gguf_decoder_matches_oracle(gpu, tmp_path, mode):
     m = llm.CausalLM.from_gguf(str(path), lmax=64, weights=mode)
     assert m.native_gguf == (mode == "native") and m.bits == 4
     if mode == "native":
-        # v (Q6_K) next to q/k (Q4_K): a column group; gate|up share Q4_K: one concatenated matrix;
-        # the F16 o projection multiplied as stored
+        # v (Q6_K) next to q/k (Q4_K): a column group of q|k concatenated and v; gate|up share
+        # Q4_K: one concatenated matrix; the F16 o projection multiplied as stored
         from webpytorch_amd import core
-        assert isinstance(m.layers[0]["qkv"], llm._Group)
+        g = m.layers[0]["qkv"]
+        assert isinstance(g, llm._Group) and [p.type_name for p in g.parts] == ["Q4_K", "Q6_K"]
+        assert g.parts[0].Nt == (SH["NH"] + SH["NKV"]) * SH["HD"]
         assert isinstance(m.layers[0]["gate_up"], core.GGMLLinear) and m.layers[0]["gate_up"].Nt == 2 * SH["I"]
         assert isinstance(m.head, core.GGMLLinear) and m.head.type_name == "Q8_0"
         assert isinstance(m.layers[0]["o"], core.GGMLLinear) and m.layers[0]["o"].type_name == "F16"

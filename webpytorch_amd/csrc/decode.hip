@@ -51,20 +51,53 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
                                                       float* __restrict__ out, int H, float eps) {
   __shared__ float red[4];
   const float* xr = x + (size_t)blockIdx.x * H;
+  float* o = out + (size_t)blockIdx.x * H;
   float s = 0.f;
-  for (int c = threadIdx.x; c < H; c += 256) s = s + xr[c] * xr[c];  // products rounded
+  // rows of up to 8192 values 16-byte aligned: every load of the thread issued before the first
+  // is used, the values kept for the scaling pass (a strided loop waits on each load in turn)
+  constexpr int U = 8;
+  const int n4 = H / 4;
+  const bool vec = (H & 3) == 0 && n4 <= U * 256 && (reinterpret_cast<uintptr_t>(xr) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(o) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+  float4 v[U];
+  if (vec) {
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int i = threadIdx.x + j * 256;
+      v[j] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      s = s + v[j].x * v[j].x;  // products rounded
+      s = s + v[j].y * v[j].y;
+      s = s + v[j].z * v[j].z;
+      s = s + v[j].w * v[j].w;
+    }
+  } else {
+    for (int c = threadIdx.x; c < H; c += 256) s = s + xr[c] * xr[c];
+  }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
   const float ms = ((red[0] + red[1]) + (red[2] + red[3])) / (float)H;
   const float r = sqrtf(ms + eps);
-  float* o = out + (size_t)blockIdx.x * H;
-  for (int c = threadIdx.x; c < H; c += 256) o[c] = (xr[c] / r) * w[c];
+  if (vec) {
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4* o4 = reinterpret_cast<float4*>(o);
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int i = threadIdx.x + j * 256;
+      if (i < n4) {
+        const float4 ww = w4[i];
+        o4[i] = make_float4((v[j].x / r) * ww.x, (v[j].y / r) * ww.y, (v[j].z / r) * ww.z, (v[j].w / r) * ww.w);
+      }
+    }
+  } else {
+    for (int c = threadIdx.x; c < H; c += 256) o[c] = (xr[c] / r) * w[c];
+  }
 }
 
-// Per-head RMSNorm (QK-norm) in place on fused q|k|v rows [T][(NH + 2 NKV) HD]: each of the NH
-// query heads by qn [HD], each of the NKV key heads by kn [HD] (null: that part untouched); the v
-// heads are left alone. One wave per (token, head), HD <= 256.
 __global__ __launch_bounds__(256) void head_rmsnorm_kernel(float* __restrict__ qkv, const float* __restrict__ qn,
                                                            const float* __restrict__ kn, int T, int NH, int NKV,
                                                            int HD, float eps) {
@@ -111,17 +144,18 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const float* __restrict__ 
   const int W = (NH + 2 * NKV) * HD;
   const float* row = qkv + (size_t)t * W;
   const int half = HD / 2;
-  for (int i = threadIdx.x; i < W; i += 256) {
-    const int head = i / HD, d = i - head * HD;
-    if (head >= NH + NKV) {  // v: copied into the cache
-      vc[((size_t)(head - NH - NKV) * LMAX + pos) * HD + d] = row[i];
-      continue;
-    }
-    const int j = d < half ? d : d - half;
-    const float y = rope1(row + head * HD, d, half, cos_t[(size_t)pos * half + j], sin_t[(size_t)pos * half + j]);
-    if (head < NH) q_out[((size_t)t * NH + head) * HD + d] = y;
-    else kc[((size_t)(head - NH) * LMAX + pos) * HD + d] = y;
+  // one value per thread (grid.x covers the row), so no thread waits on a chain of loads
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= W) return;
+  const int head = i / HD, d = i - head * HD;
+  if (head >= NH + NKV) {  // v: copied into the cache
+    vc[((size_t)(head - NH - NKV) * LMAX + pos) * HD + d] = row[i];
+    return;
   }
+  const int j = d < half ? d : d - half;
+  const float y = rope1(row + head * HD, d, half, cos_t[(size_t)pos * half + j], sin_t[(size_t)pos * half + j]);
+  if (head < NH) q_out[((size_t)t * NH + head) * HD + d] = y;
+  else kc[((size_t)(head - NH) * LMAX + pos) * HD + d] = y;
 }
 
 // One decode token: RoPE of its q head and of the kv head's new k, the new k and v written
@@ -580,7 +614,8 @@ extern "C" int miq_rope_kv(const float* qkv, const int32_t* state, const float* 
               "rope_kv: T=%d NH=%d NKV=%d HD=%d LMAX=%d", T, NH, NKV, HD, LMAX);
   if (T == 0) return MIQ_OK;
   MIQ_REQUIRE(qkv && state && cos_tab && sin_tab && q_out && kcache && vcache, MIQ_ERR_INVALID, "rope_kv: null pointer");
-  hipLaunchKernelGGL(rope_kv_kernel, dim3(1, T), dim3(256), 0, static_cast<hipStream_t>(stream), qkv, state, cos_tab,
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(((NH + 2 * NKV) * HD + 255) / 256, T), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), qkv, state, cos_tab,
                      sin_tab, q_out, kcache, vcache, NH, NKV, HD, LMAX);
   return check_launch("rope_kv");
 }

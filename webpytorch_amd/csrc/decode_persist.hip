@@ -725,7 +725,7 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   s.hin = lds;
   s.xs = s.hin + p.lds_a;
   s.xa = reinterpret_cast<unsigned char*>(s.xs + p.lds_x);
-  s.cx = reinterpret_cast<float2*>(s.xa + (size_t)(p.lds_x / 32) * kStepBytes);
+  s.cx = reinterpret_cast<float2*>(s.xa + (size_t)(p.lds_x / 32) * kStep8Bytes);
   s.red = reinterpret_cast<float*>(s.cx + p.lds_x / 32);
   s.red16 = s.red + kKParts * 64;
   s.qkv = s.red16 + 32;
@@ -825,7 +825,7 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
   q.lds_a = std::max(std::max(std::max(H, 2 * KS), (NH + 1) * kTile), std::max(256 + LMAX, 2 * q.G));
   q.lds_a = (q.lds_a + 3) & ~3;
   q.lds_x = (std::max(std::max(H, KS), NHD) + 63) & ~63;  // even step count: red 16-byte aligned
-  q.lds_bytes = (size_t)(q.lds_a + q.lds_x) * 4 + (size_t)(q.lds_x / 32) * kStepBytes +
+  q.lds_bytes = (size_t)(q.lds_a + q.lds_x) * 4 + (size_t)(q.lds_x / 32) * kStep8Bytes +
                 (size_t)(2 * (q.lds_x / 32) + kKParts * 64 + 32 + kQkvFloats + 2 * kWaves) * 4;
   int lds_max = 0;
   if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds_max <= 0)

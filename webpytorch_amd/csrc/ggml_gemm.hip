@@ -101,6 +101,7 @@ __global__ __launch_bounds__(256) void stage_kernel(const XT* __restrict__ x, __
     const float* src = x + (size_t)m * K;
     float mx = 0.f;
     bool nan = false;
+#pragma unroll 4
     for (int q = threadIdx.x; q < K / 4; q += 256) {
       const float4 v = reinterpret_cast<const float4*>(src)[q];
       reinterpret_cast<float4*>(frow)[q] = v;
@@ -518,9 +519,11 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
   const size_t Mx = (size_t)M * (PAIR ? 2 : 1), slice = Mx * N;
   const size_t r0 = (size_t)(PAIR ? 2 * m : m) * N + n;
   float v = 0.f;
+#pragma unroll 8
   for (int z = 0; z < ksplit; ++z) v += part[z * slice + r0];
   if constexpr (PAIR) {
     float lo = 0.f;
+#pragma unroll 8
     for (int z = 0; z < ksplit; ++z) lo += part[z * slice + r0 + N];
     v = (v + lo) * ldexpf(1.f, -row_exp(rmax[m]));
   }

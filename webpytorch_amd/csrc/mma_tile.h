@@ -15,52 +15,14 @@ __device__ __forceinline__ int opaque_tid() {
   return v;
 }
 
-// ---- 64-column int4 tile on the matrix cores ----------------------------------------------
-// The activations x (fp32) are split exactly into three bf16 terms, x = b1 + b2 + b3 (b1 =
-// bf16(x), b2 = bf16(x - b1), b3 = x - b1 - b2, which fits bf16), which become rows 0-2 of the
-// A operand of v_mfma_f32_16x16x32_bf16; the codes become the B operand with no conversion
-// instruction per value: OR-ing a code c into mantissa bits 0-3 of 128.0 (bf16 0x4300, whose
-// mantissa step is 1) gives 128 + c; a code of the upper nibble of a byte, shifted down one bit
-// into mantissa bits 3-6 (bf16 has 7 mantissa bits, so bit 7 is the exponent's), gives
-// 128 + 8c, matched by x / 8 in A. Products of bf16 values are exact in fp32, so rows 0-2 of D
-// sum to sum_k x_k (128 + c_k) or (x_k / 8)(128 + 8 c_k) in fp32; the per-step bias sums (128
-// or 16 times the x of each kind) and x sums are subtracted per quantization group with the
-// zero point: acc += s_g * (p - (bias + z_g * sum x)).
-//
-// A 32-k step of A is staged in LDS as 4 k-blocks (one per 16 lanes) x 4 slots of 8 values
-// (the three bf16 terms; the fourth slot is unused), 256 bytes.
+// ---- 64-column int4 tiles on the matrix cores ---------------------------------------------
 // A tile of 64 columns is computed by the 16 waves of a workgroup, each taking all 64 columns
 // and one k-part (a sixteenth) of the steps: lane l loads 16 bytes of packed row (l >> 4) of
-// each step -- columns 4 (l & 15) .. + 3 -- and feeds MFMA t the word of column 4 (l & 15) + t,
-// which is exactly its B fragment (column l & 15 of MFMA t, k 8 (l >> 4) .. + 7). The four
-// MFMAs of a step share the A fragment, so the per-step work (A read, sums, addresses) is paid
-// once per four MFMAs.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-// LDS bytes per staged 32-k step: 4 k-blocks of 3 rows x 16 bytes = 192 bytes of A, laid out
-// 64 bytes per k-block and padded to 272 so that the 16 staging threads of a phase (four steps
-// of four k-blocks) write 16 different bank groups (at 256 they wrote 4: 415.2 -> 410.6 us per
-// Qwen2-0.5B decode token).
-constexpr int kStepBytes = 272;
-
-// The B fragment of one packed word: halves (c0, c4) (8 c1, 8 c5) (c2, c6) (8 c3, 8 c7) over 128,
-// three shifts and four v_and_or_b32. Written in C++ so that the compiler's hazard tracking
-// covers the conversion (an inline-asm version once read stale operands: the compiler neither
-// pads an asm VALU write before the MFMA that reads it nor delays the next asm write of a
-// register an issued MFMA is still reading). The masks and the 128.0 pattern are held in
-// registers (opaque to the compiler), so each pair is one v_and_or_b32 with no literals.
-struct BMasks {
-  uint32_t lo, hi, mg;
-};
-__device__ __forceinline__ BMasks b_masks() {
-  uint32_t lo = 0x000F000Fu, hi = 0x00780078u, mg = 0x43004300u;
-  asm volatile("" : "+v"(lo), "+v"(hi), "+v"(mg));
-  return {lo, hi, mg};
-}
-__device__ __forceinline__ u32x4 b_bf16(uint32_t q, const BMasks& k) {
-  return (u32x4){(q & k.lo) | k.mg, ((q >> 1) & k.hi) | k.mg, ((q >> 8) & k.lo) | k.mg, ((q >> 9) & k.hi) | k.mg};
-}
+// each 32-k step -- columns 4 (l & 15) .. + 3 -- and feeds MFMA t the word of column
+// 4 (l & 15) + t, which holds exactly its B fragment (column l & 15 of MFMA t, the 8 codes of
+// packed row l >> 4). The four MFMAs of a step share the A fragment, so the per-step work (A
+// read, sums, addresses) is paid once per four MFMAs. The products themselves run on the int8
+// matrix cores (tile_mma_i8 below).
 
 // Raw scale bits of 4 adjacent columns (fp16: 8 bytes, fp32: 16 bytes), converted when used.
 template <typename ST> struct Scales4;
@@ -141,78 +103,6 @@ __device__ __forceinline__ void tile_issue(Tile<ST, SPQ>& t, const uint32_t* qw,
   }
 }
 
-// This wave's share of sum_k x_k W[k][c] for its 4 columns (valid in lanes 0..15: columns
-// c0 + 4 lane + t), the codes of step i given by wsrc(i). The A fragment and step sums of step
-// i + 2 are read from LDS while step i computes (reads clamped to the wave's last step, so they
-// need no guard); the four MFMA chains of a quantization group share each step's A fragment,
-// and each group is folded into acc with its scales and zero points.
-template <typename ST, int SPQ, typename WSRC>
-__device__ __forceinline__ float4 tile_mma_core(const WSRC& wsrc, const uint32_t* tz, const typename Scales4<ST>::T* ts,
-                                                int st0, int ns, const unsigned char* xa, const float2* cx, int rb,
-                                                int c0, int lgs, float zoff) {
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  if (ns == 0) return make_float4(0.f, 0.f, 0.f, 0.f);  // wave-uniform: a k-part past the end of K
-  const int tid = opaque_tid();
-  const int lane = tid & 63;
-  const int sh = ((c0 + 4 * (lane & 15)) & 7) * 4;
-  // Only A rows 0-2 (lanes with lane % 16 < 3) carry data: D rows 3-15 are never read, so the
-  // other lanes skip the LDS read and feed whatever their registers hold.
-  const bool arow = (lane & 15) < 3;
-  const unsigned char* ap = xa + st0 * kStepBytes + (lane >> 4) * 64 + (lane & 15) * 16;
-  const float2* cp = cx + st0;
-  const int last = ns - 1;
-  const BMasks bm = b_masks();
-  bf16x8 a0, a1;
-  if (arow) {
-    a0 = *reinterpret_cast<const bf16x8*>(ap);
-    a1 = *reinterpret_cast<const bf16x8*>(ap + min(1, last) * kStepBytes);
-  }
-  float2 x0 = cp[0], x1 = cp[min(1, last)];
-  const int r0 = rb + 4 * st0, gsh = lgs - 3;
-  floatx4 d[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) d[q] = (floatx4){0.f, 0.f, 0.f, 0.f};
-  float cs = 0.f, xs = 0.f;
-#pragma unroll
-  for (int i = 0; i < SPQ; ++i) {
-    bf16x8 a2;
-    if (arow) a2 = *reinterpret_cast<const bf16x8*>(ap + min(i + 2, last) * kStepBytes);
-    const float2 x2 = cp[min(i + 2, last)];
-    if (i < ns) {
-      const uint4 wv = wsrc(i);
-      const uint32_t wt[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u32x4 bw = b_bf16(wt[q], bm);
-        d[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, bw), d[q], 0, 0, 0);
-      }
-      cs += x0.x;
-      xs += x0.y;
-      const int r = r0 + 4 * i;
-      if (i + 1 == ns || ((r + 4) >> gsh) != (r >> gsh)) {  // last step of this group
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float pv = (d[q][0] + d[q][1]) + d[q][2];
-          const float zc = (float)((tz[i] >> (sh + 4 * q)) & 15u) + zoff;
-          acc[q] = fmaf(Scales4<ST>::get(ts[i], q), pv - fmaf(zc, xs, cs), acc[q]);
-          d[q] = (floatx4){0.f, 0.f, 0.f, 0.f};
-        }
-        cs = 0.f;
-        xs = 0.f;
-      }
-    }
-    a0 = a1;
-    a1 = a2;
-    x0 = x1;
-    x1 = x2;
-  }
-  return make_float4(acc[0], acc[1], acc[2], acc[3]);
-}
-template <typename ST, int SPQ>
-__device__ __forceinline__ float4 tile_mma(const Tile<ST, SPQ>& t, const unsigned char* xa, const float2* cx, int rb,
-                                           int c0, int lgs, float zoff) {
-  return tile_mma_core<ST, SPQ>([&](int i) { return t.w[i]; }, t.z, t.s, t.st0, t.ns, xa, cx, rb, c0, lgs, zoff);
-}
 // Sums the kKParts k-parts of each column in wave order; valid in threads 0..63 (column
 // c0 + thread). red holds kKParts x 64 floats, 16-byte aligned.
 __device__ __forceinline__ float tile_sum(float4 acc, float* red) {
@@ -227,43 +117,18 @@ __device__ __forceinline__ float tile_sum(float4 acc, float* red) {
   return y;
 }
 
-// Stages one 8-value k-block (chunk ch of K / 8) of the A operand: the three bf16 terms of x in
-// the codes' order (x0, x4, x1 / 8, x5 / 8, x2, x6, x3 / 8, x7 / 8), rows 0-2; the four
-// chunks of a step (consecutive threads, all present since K % 32 == 0) combine their bias
-// sums (128 x the x of low nibbles, 16 x the others) and x sums into cx[step].
-__device__ __forceinline__ void stage_chunk(int ch, const float* v, unsigned char* xa, float2* cx) {
-  const float o[8] = {v[0], v[4], v[1] * 0.125f, v[5] * 0.125f, v[2], v[6], v[3] * 0.125f, v[7] * 0.125f};
-  bf16x8 t1, t2, t3;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const __bf16 b1 = (__bf16)o[j];
-    const float r1 = o[j] - (float)b1;
-    const __bf16 b2 = (__bf16)r1;
-    t1[j] = b1;
-    t2[j] = b2;
-    t3[j] = (__bf16)(r1 - (float)b2);
-  }
-  unsigned char* dst = xa + (ch >> 2) * kStepBytes + (ch & 3) * 64;
-  *reinterpret_cast<bf16x8*>(dst) = t1;
-  *reinterpret_cast<bf16x8*>(dst + 16) = t2;
-  *reinterpret_cast<bf16x8*>(dst + 32) = t3;
-  const float lo = (v[0] + v[2]) + (v[4] + v[6]), hi = (v[1] + v[3]) + (v[5] + v[7]);
-  float cb = 128.f * lo + 16.f * hi, sm = lo + hi;
-  cb = quad_sum(cb);
-  sm = quad_sum(sm);
-  if ((ch & 3) == 0) cx[ch >> 2] = make_float2(cb, sm);
-}
-
 // ---- 64-column int4 tile on the int8 matrix cores ----------------------------------------
-// The same tile with v_mfma_i32_16x16x64_i8: half the matrix-core instructions of the bf16 form
-// per k (64 k per instruction where both use 3-4 of the 16 rows) and 2 VALU per packed word for
-// the B operand instead of 7. Each 64-k step of x is held in fixed point at the step's own
+// v_mfma_i32_16x16x64_i8 (64 k per instruction, of which rows 0-3 are used) with 2 VALU per
+// packed word for the B operand. (An earlier form split fp32 x exactly into three bf16 terms for
+// v_mfma_f32_16x16x32_bf16: twice the matrix-core instructions per k and 7 VALU per packed word
+// to build bf16 codes; the decode token went 387 -> 359 us with this one.) Each 64-k step of x
+// is held in fixed point at the step's own
 // scale: with 2^e > max |x| over the step, X = rint(x 2^(30 - e)) (|X| <= 2^30; the rounding
 // error is at most 2^-31 of the step's largest value), split into four signed 8-bit digits,
 // X = d0 + 2^8 d1 + 2^16 d2 + 2^24 d3 (|d3| <= 64), which are rows 0-3 of A. B holds the codes as
 // int8 (0..15). Row t of D is then the exact integer sum_k d_t c_k, and a step's products are
 // 2^(e - 30) (D0 + 2^8 D1 + 2^16 D2 + 2^24 D3), formed in fp32 from two exact int32 halves.
-// Zero points use the step's fp32 sum of x, as in the bf16 form. A step holding NaN or an
+// Zero points use the step's fp32 sum of x. A step holding NaN or an
 // infinity stores a NaN scale, so its outputs are NaN.
 //
 // A 64-k step of A is 4 lane groups x 4 digit rows x 16 bytes (272 with padding). Lane l (row

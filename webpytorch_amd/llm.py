@@ -129,14 +129,26 @@ def _fuse(parts, K, gs, bits):
     if all(isinstance(q, dict) for q in parts) and not any(_dict_padded(q, bits) for q in parts):
         return _Lin(_cat_layers(parts, gs, bits), K, gs, bits)
     lins = [q if isinstance(q, core.GGMLLinear) else _Lin(q, K, gs, bits) for q in parts]
-    if all(isinstance(q, core.GGMLLinear) for q in lins) and len({q.type_name for q in lins}) == 1:
-        N = sum(q.Nt for q in lins)
-        bias = None
-        if any(q.bias is not None for q in lins):
-            bias = torch.cat([q.bias if q.bias is not None else torch.zeros(q.Nt, device=core.device())
-                              for q in lins])
-        return core.GGMLLinear(torch.cat([q.packed for q in lins]), lins[0].type_name, K, N, bias)
-    return _Group(lins)
+    # adjacent GGUF layers of one block type become one layer (q and k of a Q4_K_M file's layer
+    # whose v is Q6_K: two launches instead of three)
+    runs = []
+    for q in lins:
+        if runs and isinstance(q, core.GGMLLinear) and isinstance(runs[-1][-1], core.GGMLLinear) and \
+                q.type_name == runs[-1][-1].type_name:
+            runs[-1].append(q)
+        else:
+            runs.append([q])
+    merged = [_cat_ggml(r, K) if len(r) > 1 else r[0] for r in runs]
+    return merged[0] if len(merged) == 1 else _Group(merged)
+
+
+def _cat_ggml(lins, K):
+    """GGUF layers of one block type and input width as one layer (rows are whole blocks)."""
+    N = sum(q.Nt for q in lins)
+    bias = None
+    if any(q.bias is not None for q in lins):
+        bias = torch.cat([q.bias if q.bias is not None else torch.zeros(q.Nt, device=core.device()) for q in lins])
+    return core.GGMLLinear(torch.cat([q.packed for q in lins]), lins[0].type_name, K, N, bias)
 
 
 def _mk_lin(d, K, gs, bits):
