@@ -36,12 +36,8 @@ namespace gs {
 
 using namespace mt;
 
-#ifndef MIQ_GS_TARGET_WGS
-#define MIQ_GS_TARGET_WGS 512
-#endif
-#ifndef MIQ_GS_WIDE_MIN_TILES
-#define MIQ_GS_WIDE_MIN_TILES 128
-#endif
+constexpr int kGsTargetWgs = 512;     // split K until the grid has this many workgroups
+constexpr int kGsWideMinTiles = 128;  // from this many column tiles, 16 waves cover all of K
 
 constexpr int kXkc = 128;  // stage width of the gathered copy
 
@@ -214,7 +210,7 @@ static bool plan(int M, int K, int N, Plan* p) {
   if (M < 1 || M > 16 || K % 128 || N % 8) return false;
   const int steps = K / 32;
   p->tiles = (N + 63) / 64;
-  if (p->tiles >= MIQ_GS_WIDE_MIN_TILES && steps <= 16 * 8) {  // LDS: 1 KB of A per step
+  if (p->tiles >= kGsWideMinTiles && steps <= 16 * 8) {  // LDS: 1 KB of A per step
     p->nwv = 16;
     p->spq = steps <= 16 * 4 ? 4 : 8;
     p->kslices = 1;
@@ -225,7 +221,7 @@ static bool plan(int M, int K, int N, Plan* p) {
   p->spq = 4;
   for (int i = 0; i < 3; ++i) {
     const int s = cands[i];
-    if ((long)p->tiles * ((steps + 4 * s - 1) / (4 * s)) >= MIQ_GS_TARGET_WGS) {
+    if ((long)p->tiles * ((steps + 4 * s - 1) / (4 * s)) >= kGsTargetWgs) {
       p->spq = s;
       break;
     }

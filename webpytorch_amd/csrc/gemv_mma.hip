@@ -47,9 +47,7 @@ constexpr size_t kMaxFixCols = kFixMaxWords;
 // step (a wave load covers 4 rows x 256 contiguous bytes), and feeds them to four MFMAs that
 // share the step's A fragment: MFMA t's column l & 15 is the lane's column 4 (l & 15) + t. Each
 // lane thus holds whole column results for 4 columns; no reduction across waves is needed.
-#ifndef MIQ_GM_DEPTH
-#define MIQ_GM_DEPTH 4  // steps of codes in flight per wave (0: all of the slice, issued at entry)
-#endif
+constexpr int kGmDepth = 4;  // steps of codes in flight per wave (0: all of the slice, issued at entry)
 constexpr int kNormLoads = 8;  // float4 loads per thread of an RMSNorm row issued up front (K <= 8192)
 
 template <typename XT, typename ST, typename OT, int SPQ, bool PERM, int XM, bool WS>
@@ -115,7 +113,7 @@ __global__ __launch_bounds__(kThreadsG) void gemv_mma_kernel(const XT* __restric
   };
   // the scales and zeros first (the first group's fold needs them), then the codes of the first
   // DEPTH steps; each group issues the codes DEPTH steps ahead of it
-  constexpr int DEPTH = (MIQ_GM_DEPTH > 0 && MIQ_GM_DEPTH < SPQ) ? MIQ_GM_DEPTH : SPQ;
+  constexpr int DEPTH = (kGmDepth > 0 && kGmDepth < SPQ) ? kGmDepth : SPQ;
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     const int g = (rb >> 4) + min(gi, (wns >> 2) - 1);  // 16 packed rows per group

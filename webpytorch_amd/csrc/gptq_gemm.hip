@@ -46,13 +46,8 @@
 
 namespace miq {
 
-#ifndef MIQ_GEMM_TARGET_WGS
-#define MIQ_GEMM_TARGET_WGS 256
-#endif
+constexpr int kGemmTargetWgs = 256;  // a tile grid of this many workgroups needs no K split
 
-#ifndef MIQ_GEMM_SCHED_PATTERN
-#define MIQ_GEMM_SCHED_PATTERN 0
-#endif
 
 constexpr int kXCDs = 8;
 constexpr int kLdsBytes = 160 * 1024;
@@ -412,15 +407,6 @@ __global__ __attribute__((amdgpu_flat_work_group_size(1, TM * CB <= 4 ? 768 : 51
         for (int s = 0; s < CB; ++s)
           part[t][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[st][t], bf[s], part[t][s], 0, 0, 0);
     }
-#if MIQ_GEMM_SCHED_PATTERN
-    constexpr int kValuPerMfma = (CB * (BITS == 4 ? 9 : 8) + TM * CB - 1) / (TM * CB) + 1;
-    __builtin_amdgcn_sched_group_barrier(0x002, CB * (BITS == 4 ? 9 : 8) + 16, 0);  // zero points, first unpack
-#pragma unroll
-    for (int i = 0; i < STEPS * TM * CB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // then a few VALU
-    }
-#endif
 #pragma unroll
     for (int t = 0; t < TM; ++t)
 #pragma unroll
@@ -626,23 +612,18 @@ static int gemm_plan(int M, int K, int N, int gs, int bits, GemmPlan* p) {
   // the largest wave tile whose grid covers the chip (no K split); failing that, the one with
   // the most tiles, with K split to make up the rest
   int pick = -1;
-#if defined(MIQ_GEMM_TM) && defined(MIQ_GEMM_CB)
-  for (int i = 0; i < kNumWaveTiles; ++i)
-    if (kWaveTiles[i].tm == MIQ_GEMM_TM && kWaveTiles[i].cb == MIQ_GEMM_CB) pick = i;
-#else
   long most = 0;
   int pick_most = 0;
   for (int i = 0; i < kNumWaveTiles; ++i) {
     const long tiles = (long)((M + 16 * kWaveTiles[i].tm - 1) / (16 * kWaveTiles[i].tm)) *
                        ((N + 64 * kWaveTiles[i].cb - 1) / (64 * kWaveTiles[i].cb));
-    if (tiles >= MIQ_GEMM_TARGET_WGS && pick < 0) pick = i;
+    if (tiles >= kGemmTargetWgs && pick < 0) pick = i;
     if (tiles > most) {
       most = tiles;
       pick_most = i;
     }
   }
   if (pick < 0) pick = pick_most;  // no tile fills the chip alone: the most tiles, K split for the rest
-#endif
   p->tm = kWaveTiles[pick].tm;
   p->cb = kWaveTiles[pick].cb;
   if (bits == 8 && p->cb == 4 && p->kc == 128) p->kc = 64;  // two stage pairs of LDS
@@ -650,7 +631,7 @@ static int gemm_plan(int M, int K, int N, int gs, int bits, GemmPlan* p) {
   p->mtiles = (M + 16 * p->tm - 1) / (16 * p->tm);
   const int nst = K / p->kc;
   const int base = p->ntiles * p->mtiles;
-  int ksplit = base <= kMaxCounters ? (MIQ_GEMM_TARGET_WGS + base - 1) / base : 1;
+  int ksplit = base <= kMaxCounters ? (kGemmTargetWgs + base - 1) / base : 1;
   if (ksplit > nst) ksplit = nst;
   if (ksplit < 1) ksplit = 1;
   p->stages_per_wg = (nst + ksplit - 1) / ksplit;

@@ -83,18 +83,10 @@ __global__ __launch_bounds__(256) void gptq_repack_kernel(const uint32_t* __rest
 // the last to arrive (device-scope atomic counter) sums them in ksplit order, adds the bias,
 // writes the output and re-arms the counter to zero, so results are deterministic.
 
-#ifndef MIQ_GEMV_MMA_MIN_BYTES
-#define MIQ_GEMV_MMA_MIN_BYTES 0u  // int4 codes of a layer from which one row takes gemv_mma (every size)
-#endif
-#ifndef MIQ_GEMV_MIN_WGS
-#define MIQ_GEMV_MIN_WGS 1  // split K further while fewer workgroups than this would run
-#endif
-#ifndef MIQ_GEMV_MAX_WAVES
-#define MIQ_GEMV_MAX_WAVES 16  // waves per workgroup (1024 threads)
-#endif
-#ifndef MIQ_GEMV_SPLIT_WAVES
-#define MIQ_GEMV_SPLIT_WAVES 4  // waves per workgroup when K is split across workgroups
-#endif
+constexpr size_t kGemvMmaMinBytes = 0;  // int4 codes of a layer from which one row takes gemv_mma (every size)
+constexpr int kGemvMinWgs = 1;          // split K further while fewer workgroups than this would run
+constexpr int kGemvMaxWaves = 16;       // waves per workgroup (1024 threads)
+constexpr int kGemvSplitWaves = 4;      // waves per workgroup when K is split across workgroups
 constexpr int kGemvStageBytes = 64 * 1024;  // LDS for the staged activations (no workspace)
 
 template <int BITS> struct Codes;
@@ -152,7 +144,7 @@ template <int RPW> struct GemvBatch {
 // weight norm_w (x / sqrt(mean(x^2) + eps) * w, every workgroup recomputes the row's mean
 // square); SwiGLU of a [gate | up] row of 2K values (silu(gate) * up).
 template <int BITS, int MR, int RPW, typename XT, typename ST, typename OT, int XMODE>
-__global__ __launch_bounds__(64 * MIQ_GEMV_MAX_WAVES) void gptq_gemv_kernel(
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void gptq_gemv_kernel(
     const XT* __restrict__ x, const int32_t* __restrict__ perm, const uint32_t* __restrict__ qw,
     const uint32_t* __restrict__ qz, const ST* __restrict__ sc, const float* bias, OT* out,
     float* __restrict__ ws, int* __restrict__ counters, int M, int K, int N, int gs, float zoff, int rows_per_wg,
@@ -165,7 +157,7 @@ __global__ __launch_bounds__(64 * MIQ_GEMV_MAX_WAVES) void gptq_gemv_kernel(
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __shared__ int is_last;
-  __shared__ float ss_red[MIQ_GEMV_MAX_WAVES][MR];
+  __shared__ float ss_red[kGemvMaxWaves][MR];
 
   const int W = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -429,7 +421,7 @@ static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool ha
   p->mblocks = (M + p->mr - 1) / p->mr;
   const int xb = x_dtype == MIQ_F16 ? 2 : 4;
   const int nbt = K / per / rpw;  // batches per column tile
-  const int wmax = MIQ_GEMV_SPLIT_WAVES;
+  const int wmax = kGemvSplitWaves;
   const int base = p->tiles * p->mblocks;
   int waves, ksplit;
   // wide layers fill the chip by columns alone: no K split, each wave streams several batches
@@ -438,14 +430,14 @@ static int gemv_plan(int M, int K, int N, int gs, int bits, int x_dtype, bool ha
     // one batch per wave; fewer waves per workgroup while too few workgroups would run
     waves = nbt < wmax ? nbt : wmax;
     ksplit = (nbt + waves - 1) / waves;
-    while (waves > 1 && base * ksplit < MIQ_GEMV_MIN_WGS) {
+    while (waves > 1 && base * ksplit < kGemvMinWgs) {
       waves = (waves + 1) / 2;
       ksplit = (nbt + waves - 1) / waves;
     }
   } else {
     // every wave takes two batches (both in flight at once): ceil(batches / 2) waves
     waves = (nbt + 1) / 2;
-    waves = waves > MIQ_GEMV_MAX_WAVES ? MIQ_GEMV_MAX_WAVES : waves;
+    waves = waves > kGemvMaxWaves ? kGemvMaxWaves : waves;
     ksplit = 1;
     MIQ_REQUIRE((size_t)p->mr * K * xb <= (size_t)kGemvStageBytes, MIQ_ERR_INVALID,
                 "gptq_gemv: K=%d needs a workspace (see miq_gptq_gemv_workspace)", K);
@@ -618,7 +610,7 @@ extern "C" int miq_gptq_gemv_workspace(int M, int K, int N, int gs, int bits, in
   rc = gemv_plan(M, K, N, gs, bits, x_dtype, true, &p);
   if (rc) return rc;
   *bytes = p.ws_bytes;
-  if (M == 1 && bits == 4 && (size_t)K * N / 2 >= MIQ_GEMV_MMA_MIN_BYTES)
+  if (M == 1 && bits == 4 && (size_t)K * N / 2 >= kGemvMmaMinBytes)
     *bytes = std::max(*bytes, gemv_mma_workspace(K, N));
   return MIQ_OK;
 }
@@ -631,7 +623,7 @@ extern "C" int miq_gptq_gemv(const void* x, int x_dtype, const int32_t* perm, co
                       gs, bits);
   if (rc || M == 0) return rc;
   // one row of an int4 layer: the matrix-core GEMV (it declines shapes it does not cover)
-  if (M == 1 && bits == 4 && (size_t)K * N / 2 >= MIQ_GEMV_MMA_MIN_BYTES &&
+  if (M == 1 && bits == 4 && (size_t)K * N / 2 >= kGemvMmaMinBytes &&
       (workspace == nullptr || aligned(workspace, 256))) {
     rc = gemv_mma(x, x_dtype, perm, qweight, qzeros, scales, scales_dtype, bias, out, out_dtype, K, N, gs,
                   zero_offset, workspace, workspace_bytes, static_cast<hipStream_t>(stream));

@@ -15,9 +15,7 @@
 
 namespace miq {
 
-#ifndef MIQ_Q4K_DEPTH
-#define MIQ_Q4K_DEPTH 1  // rows of a wave's blocks in flight ahead of the one computed (0: all)
-#endif
+constexpr int kQ4kDepth = 1;  // rows of a wave's blocks in flight ahead of the one computed (0: all)
 
 struct Q4kScales {
   float d1, m1, d2, m2;  // d*sc and dmin*m for sub-blocks 2q and 2q+1
@@ -114,7 +112,7 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const XT* __restrict__ x,
 
   uint4 hd[R], c0[R], c1[R];
   // row r's block of a pass; the first D rows are issued ahead, row r + D when row r is computed
-  constexpr int D = (MIQ_Q4K_DEPTH > 0 && MIQ_Q4K_DEPTH < R) ? MIQ_Q4K_DEPTH : R;
+  constexpr int D = (kQ4kDepth > 0 && kQ4kDepth < R) ? kQ4kDepth : R;
   auto load_row = [&](int g, int pass, int r) __attribute__((always_inline)) {
     const int b = pass * 16 + slot;
     const int n = g * R + r;
