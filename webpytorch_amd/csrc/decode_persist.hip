@@ -6,7 +6,8 @@
 //   * a query head: RoPE and attention over the cache, publishing the head's 64 outputs;
 //   * a 64-column tile of the o projection over all heads' outputs, plus the residual:
 //     hmid(l) = h(l) + att @ Wo;
-//   * a 64-column tile of the gate|up projection;
+//   * a 64-column tile of the gate|up projection (32 gate and the matching 32 up columns, whose
+//     silu(gate) * up it publishes);
 //   * a (64-column tile, K-slice) of the down projection.
 // A layer is five dependent hops: h(l) -> q|k|v -> heads -> o tiles (hmid) -> gate|up -> down ->
 // h(l + 1).
@@ -79,7 +80,7 @@ struct Params {
   int32_t* state;
   float* logits;
   uint32_t* ctl;
-  uint64_t *tq, *tatt, *thmid, *tgu, *tamax;  // q|k|v, heads' outputs [NH][64], hmid, gate|up, arg-max
+  uint64_t *tq, *tatt, *thmid, *tgu, *tamax;  // q|k|v, heads' outputs [NH][64], hmid, silu(gate) * up, arg-max
   unsigned long long* fx;  // bank 0 of the fixed-point words of h(l + 1) (bank 1 at fx + bank_words)
   float* fside;            // escape slots: term s of word i at fside + s * LH + i
   size_t bank_words;       // 64-bit words per bank: LH sums, then LH 32-bit masks
@@ -91,12 +92,13 @@ struct Params {
   unsigned long long* trace;  // null, or [G][L + 2][8] wall-clock stamps of the phase marks below
 };
 
-// Phase mark k of layer l of this workgroup (miq_decode_persistent_trace): thread 0 stores the
-// wall clock. Without a trace buffer the mark is one scalar test of a kernel argument.
+// Phase mark k of layer l of this workgroup: in the kernel instantiated with TR (the one
+// miq_decode_persistent_trace launches) thread 0 stores the wall clock; otherwise nothing (a
+// runtime test of the trace pointer at every mark cost 1.7% of the step).
 #define PD_MARK(l, k)                                                                                \
   do {                                                                                               \
-    if (p.trace && threadIdx.x == 0)                                                                 \
-      p.trace[((size_t)blockIdx.x * (p.L + 2) + (l)) * 8 + (k)] = wall_clock64();                   \
+    if constexpr (TR)                                                                                \
+      if (threadIdx.x == 0) p.trace[((size_t)blockIdx.x * (p.L + 2) + (l)) * 8 + (k)] = wall_clock64(); \
   } while (0)
 
 __device__ __forceinline__ void tput(uint64_t* p, uint32_t tag, float v) {
@@ -342,7 +344,7 @@ MIQ_PD_INLINE bool gather_h(const Params& p, const Ctx& c, const Lds& s, int l, 
 }
 
 // q|k|v projection, columns [64 t, 64 t + 64): RMSNorm(h(l)) @ Wqkv + bias.
-template <int SA>
+template <int SA, bool TR>
 MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
   float zo = p.zoff;
   pin(zo);
@@ -387,6 +389,7 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
 // position for the scores, a wave per residue of the position mod 16 and a lane per dimension
 // for the weighted sum. The cache rows of the first 256 positions and the RoPE row are loaded
 // before q/k/v are waited for.
+template <bool TR>
 MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq, int pos) {
   const int NH = p.NH, NKV = p.NKV, LMAX = p.LMAX, rep = NH / NKV, g = hq / rep, S = pos + 1;
   float* sp = s.hin + 256;  // scores -> probabilities [S]
@@ -508,7 +511,7 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
 // hmid(l) of columns [64 t, 64 t + 64): h(l) plus the o projection of all heads' outputs
 // (K = NH * 64), a tile like the q|k|v one. h(l) of the chunk is waited for first (it is ready a
 // whole head step earlier).
-template <int SA>
+template <int SA, bool TR>
 MIQ_PD_INLINE bool role_ored(const Params& p, const Ctx& c, const Lds& s, int t, int tok) {
   float zo = p.zoff;
   pin(zo);
@@ -550,9 +553,10 @@ MIQ_PD_INLINE bool role_ored(const Params& p, const Ctx& c, const Lds& s, int t,
   return true;
 }
 
-// gate|up projection, columns [64 t, 64 t + 64) of 2I: RMSNorm(hmid(l)) @ Wgu. The tile also
+// gate|up projection, columns [64 t, 64 t + 64) of the interleaved 2I (gate 32 t .. + 31, up
+// 32 t .. + 31): RMSNorm(hmid(l)) @ Wgu, published as silu(gate) * up. The tile also
 // adds the residual hmid(l) of column chunks t, t + ngu, ... to h(l + 1) (term ksd).
-template <int SA>
+template <int SA, bool TR>
 MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
   float zo = p.zoff;
   pin(zo);
@@ -584,8 +588,14 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
     PD_MARK(l, 3);
     const float y = tile_sum(tile_mma_i8(w, s.xa, s.cx, 0, c0, p.lgs, zo), s.red);
     PD_MARK(l, 4);
-    if (threadIdx.x < 64 && c0 + (int)threadIdx.x < N)
-      tput(p.tgu + c0 + threadIdx.x, c.tag(l, P_GU), y / norm_r(s.red16, H, p.eps));
+    // the tile's columns are gate 32 t .. + 31 then up 32 t .. + 31 (the host interleaves the
+    // weights' columns so): lane j < 32 of wave 0 pairs its gate with lane j + 32's up and
+    // publishes silu(gate) * up, the down projection's input
+    if (threadIdx.x < 64) {
+      const float gu = y / norm_r(s.red16, H, p.eps);
+      const float u = __shfl_down(gu, 32, 64);
+      if (threadIdx.x < 32) tput(p.tgu + 32 * t + threadIdx.x, c.tag(l, P_GU), (gu * (1.f / (1.f + expf(-gu)))) * u);
+    }
     PD_MARK(l, 2);
     __syncthreads();
   }
@@ -594,7 +604,7 @@ MIQ_PD_INLINE bool role_gu(const Params& p, const Ctx& c, const Lds& s, int t) {
 
 // down projection, columns [64 t, 64 t + 64) of H over K-slice sl of I: the slice's share of
 // silu(gate) * up @ Wd, term sl of h(l + 1).
-template <int SD>
+template <int SD, bool TR>
 MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t, int sl) {
   float zo = p.zoff;
   pin(zo);
@@ -606,19 +616,15 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
                p.lgs);
     const uint32_t tg = c.tag(l, P_GU);
     PD_MARK(l, 0);
-    if (!wait_tagged<4>(
-            2 * KS, c, p.tgu, [&](int i) { return i < KS ? sl * KS + i : I + sl * KS + (i - KS); },
-            [=](int) { return tg; }, s.hin, s.flags))
+    if (!wait_tagged<2>(
+            KS, c, p.tgu, [&](int i) { return sl * KS + i; }, [=](int) { return tg; }, s.hin, s.flags))
       return false;
     PD_MARK(l, 1);
     const int ch = threadIdx.x;
     if (ch < KS / 8) {
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float gv = s.hin[ch * 8 + j], u = s.hin[KS + ch * 8 + j];
-        v[j] = (gv * (1.f / (1.f + expf(-gv)))) * u;
-      }
+      for (int j = 0; j < 8; ++j) v[j] = s.hin[ch * 8 + j];
       stage_digits(ch, v, s.xa, s.cx);
     }
     __syncthreads();
@@ -634,7 +640,7 @@ MIQ_PD_INLINE bool role_down(const Params& p, const Ctx& c, const Lds& s, int t,
 
 // Tied head over 64-column tiles b, b + G, ... (the next tile's loads issued before the current
 // one is computed) with a running arg-max, published as tagged (value, index) words.
-template <int SA>
+template <int SA, bool TR>
 MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int tok) {
   const int H = p.H, V = p.V, G = gridDim.x, b = blockIdx.x;
   const int ntile = (V + kTile - 1) / kTile;
@@ -718,7 +724,7 @@ MIQ_PD_INLINE bool finish_token(const Params& p, const Ctx& c, const Lds& s, int
   return true;
 }
 
-template <int SA, int SD>
+template <int SA, int SD, bool TR>
 __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   extern __shared__ __align__(16) float lds[];
   Lds s;
@@ -758,17 +764,17 @@ __global__ __launch_bounds__(kThreads) void decode_persistent_kernel(Params p) {
   int r = blockIdx.x;
   bool ok = true;
   if (r < p.nq) {
-    ok = role_qkv<SA>(p, c, s, r, tok);
+    ok = role_qkv<SA, TR>(p, c, s, r, tok);
   } else if ((r -= p.nq) < p.na) {
-    ok = role_attn(p, c, s, r, pos);
+    ok = role_attn<TR>(p, c, s, r, pos);
   } else if ((r -= p.na) < p.no) {
-    ok = role_ored<SA>(p, c, s, r, tok);
+    ok = role_ored<SA, TR>(p, c, s, r, tok);
   } else if ((r -= p.no) < p.ngu) {
-    ok = role_gu<SA>(p, c, s, r);
+    ok = role_gu<SA, TR>(p, c, s, r);
   } else if ((r -= p.ngu) < p.nd) {
-    ok = role_down<SD>(p, c, s, r % p.no, r / p.no);
+    ok = role_down<SD, TR>(p, c, s, r % p.no, r / p.no);
   }
-  ok = ok && role_head<SA>(p, c, s, tok);
+  ok = ok && role_head<SA, TR>(p, c, s, tok);
   if (ok && blockIdx.x == 0) ok = finish_token(p, c, s, pos);
   if (!ok && threadIdx.x == 0) atomicOr(p.ctl + 1, 1u);
   PD_MARK(p.L + 1, 1);
@@ -841,7 +847,7 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
   q.off_tq = take((size_t)NQ * 8);
   q.off_tatt = take((size_t)NH * 64 * 8);
   q.off_thmid = take((size_t)H * 8);
-  q.off_tgu = take(2 * (size_t)I * 8);
+  q.off_tgu = take((size_t)I * 8);
   q.off_tamax = take(2 * (size_t)q.G * 8);
   const size_t n = (size_t)L * H;  // h(l + 1) words of every layer
   q.bank_words = ((n * 12 + 255) & ~(size_t)255) / 8;
@@ -888,8 +894,8 @@ static int decode_persistent(const uint64_t* layer_table, const void* embed, con
   // instantiated register capacities
   void (*kfn)(pd::Params) = nullptr;
   // (H <= 1024 keeps spa <= 2)
-  if (pl.spd <= 4) kfn = pd::decode_persistent_kernel<2, 4>;
-  else kfn = pd::decode_persistent_kernel<2, 8>;
+  if (pl.spd <= 4) kfn = trace ? pd::decode_persistent_kernel<2, 4, true> : pd::decode_persistent_kernel<2, 4, false>;
+  else kfn = trace ? pd::decode_persistent_kernel<2, 8, true> : pd::decode_persistent_kernel<2, 8, false>;
   auto kern = reinterpret_cast<const void*>(kfn);
   if (hipGetDevice(&dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, pd::kThreads, pl.lds_bytes) != hipSuccess)

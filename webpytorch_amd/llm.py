@@ -155,6 +155,18 @@ def _mk_lin(d, K, gs, bits):
     return d if isinstance(d, core.GGMLLinear) else _Lin(d, K, gs, bits)
 
 
+def _interleave_gate_up(gu, I):
+    """The fused [gate | up] GPTQ tensors with their columns regrouped by 64: gate columns
+    32 t .. 32 t + 31, then up columns 32 t .. 32 t + 31, for t = 0 .. I / 32 - 1, so that one
+    64-column tile of the persistent step holds matching gate and up columns. A column
+    permutation: qweight and scales gather columns, qzeros (8 columns per word at int4) whole
+    words of 4."""
+    dev = gu.qweight.device
+    cols = torch.arange(2 * I, device=dev).view(2, I // 32, 32).permute(1, 0, 2).reshape(-1)
+    words = torch.arange(2 * I // 8, device=dev).view(2, I // 32, 4).permute(1, 0, 2).reshape(-1)
+    return (gu.qweight[:, cols].contiguous(), gu.qzeros[:, words].contiguous(), gu.scales[:, cols].contiguous())
+
+
 class CausalLM:
     """Qwen2-shaped GPTQ decoder with device-resident decode (see module docstring).
 
@@ -350,11 +362,14 @@ class CausalLM:
         def a(t):
             return 0 if t is None else int(t.data_ptr())
         table = []
+        self._gu_interleaved = []  # the persistent step's copies of gate|up (held for the table)
         for i, lay in enumerate(lays):
             qkv, o, gu, dn = lay["qkv"], lay["o"], lay["gate_up"], lay["down"]
+            gi = _interleave_gate_up(gu, self.I)
+            self._gu_interleaved.append(gi)
             table.append([a(qkv.qweight), a(qkv.qzeros), a(qkv.scales), a(qkv.bias),
                           a(o.qweight), a(o.qzeros), a(o.scales),
-                          a(gu.qweight), a(gu.qzeros), a(gu.scales),
+                          a(gi[0]), a(gi[1]), a(gi[2]),
                           a(dn.qweight), a(dn.qzeros), a(dn.scales),
                           a(lay["in_ln"]), a(lay["post_ln"]), a(self.kc[i]), a(self.vc[i]), 0, 0, 0])
         self.layer_table = torch.tensor(table, dtype=torch.int64, device=core.device())
