@@ -543,11 +543,12 @@ static Plan plan(int M, int K, int N, int x_dtype) {
   const long wide = (long)p.mtiles * ((N + 127) / 128);
   p.cg = wide >= 2 * kCUs ? 2 : 1;
   p.tiles = (int)(p.cg == 2 ? wide : (long)p.mtiles * ((N + 63) / 64));
-  // split only grids that leave CUs idle: at 224 tiles (M = 64 fp16, N = 14336) three slices
-  // ran the GEMM no faster (29.6 against 29.1 us: the activation tiles each column tile copies
-  // through L2 are the same bytes however K is cut) and added a 5.1 us reduce
+  // split only grids that leave a quarter of the CUs or more idle: at 224 tiles (M = 64 fp16,
+  // N = 14336) three slices ran the GEMM no faster (29.7 against 29.1 us: the activation tiles
+  // each column tile copies through L2 are the same bytes however K is cut) and added a 5.0 us
+  // reduce; at 128 tiles and fewer (the 64-row prefill's q, o, k|v and down) the split won
   p.ksplit = 1;
-  if (p.tiles < kCUs && nsb > 1) p.ksplit = std::min(nsb, (2 * kCUs + p.tiles - 1) / p.tiles);
+  if (4 * p.tiles < 3 * kCUs && nsb > 1) p.ksplit = std::min(nsb, (2 * kCUs + p.tiles - 1) / p.tiles);
   p.ksteps = (nsb + p.ksplit - 1) / p.ksplit;
   p.ksplit = (nsb + p.ksteps - 1) / p.ksteps;
   return p;
