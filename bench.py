@@ -638,21 +638,22 @@ def gemv_only(torch, core, steps):
 
 
 def decode_step_time(torch, m, ids, warmup, steps):
-    """Prefill + one step (which captures the decode graph; the first call also runs the
-    kernels' first-use checks, so a second call gives the warm TTFT), `warmup` untimed replays,
-    then the mean time of `steps` replays between events on the replay stream."""
+    """Prefill + one token (the first call also runs the kernels' first-use checks, so a second
+    call gives the warm TTFT), `warmup` untimed decode tokens, then the mean time per token of
+    `steps` decode tokens between events on the replay stream: replays of graphs of
+    `m.graph_tokens` one-token steps (one persistent launch each) and one of the remainder. The
+    graphs are recorded before the timed region."""
     m.generate(ids, 2)
     r = m.generate(ids, 2)
     pos0 = int(m.state[0])
-    g = m._graph
-    for _ in range(warmup):
-        g.replay()
+    for t, _ in m._chunks(steps) + m._chunks(warmup):
+        m.graph(t)
+    m.replay_tokens(warmup)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
-    for _ in range(steps):
-        g.replay()
+    m.replay_tokens(steps)
     ev1.record(stream)
     ev1.synchronize()
     torch.cuda.synchronize()
@@ -759,6 +760,7 @@ def main():
     if m.pws is None:
         raise SystemExit("the persistent decode step is not available for this shape")
     t_step, r, pos0 = decode_step_time(torch, m, ids, a.warmup, a.steps)
+    m_graph_tokens = m.graph_tokens
     if m.persistent_error():
         raise SystemExit("persistent decode step reported error bits %d" % m.persistent_error())
     step_bytes = sum(LAYERS * gemv_bytes(K, N, sdt, b) for k, (K, N, sdt, _, b) in SHAPES.items() if k != "head")
@@ -789,7 +791,7 @@ def main():
         "config": {"workload": "greedy decode, random-init Qwen2-0.5B-shaped int4 GPTQ model (24 layers, "
                                "hidden 896, 14/2 heads, intermediate 4864, vocab 151936, gs=128), 64-token "
                                "prompt; one step = one decode token = one launch of the persistent decode "
-                               "kernel (captured graph replay)",
+                               "kernel (captured graphs of %d steps, replayed)" % m_graph_tokens,
                    "gemv_bytes_per_token": step_bytes, "kernel_bytes_per_token": kernel_bytes,
                    "launches_per_token": 1},
         "decode_tokens_per_s": round(1.0 / t_step, 1),

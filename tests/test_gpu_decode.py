@@ -397,12 +397,12 @@ def test_persistent_timeout_falls_back_to_the_launch_sequence(gpu, monkeypatch, 
     a, b, ids = _persistent_pair(sh, 15, 64, 16)
     want = b.generate(ids, 8).tokens
     monkeypatch.setenv("MIQ_PD_SPIN_TICKS", "1")
-    a._graph = None  # captured now, with the one-tick bound
+    a._graphs.clear()  # captured now, with the one-tick bound
     with pytest.warns(RuntimeWarning, match="launch sequence"):
         got = a.generate(ids, 8, use_graph=use_graph)
     monkeypatch.delenv("MIQ_PD_SPIN_TICKS")
     assert got.tokens == want and a.fallback_steps == 7 and a.persistent_error() == 0
-    a._graph = None
+    a._graphs.clear()
     assert a.generate(ids, 8).tokens == want and a.fallback_steps == 0
 
 
@@ -424,6 +424,50 @@ def test_persistent_step_graph_replay_and_position_guard(gpu):
     a.reset()
     assert a.persistent_error() == 0
     assert a.generate(ids, 20).tokens == want
+
+
+SMALL = dict(L=2, H=256, NH=4, NKV=2, HD=64, I=512, V=2048, gs=128, bits=4)
+
+
+@pytest.mark.parametrize("sh,prompt,n", [(SMALL, 16, 12), (dict(synth.QWEN2_05B), 64, 21)])
+@pytest.mark.parametrize("persistent", [True, False])
+def test_graphs_of_several_steps_match_eager_steps(gpu, sh, prompt, n, persistent):
+    """generate() replays graphs of several one-token steps (full graphs of `graph_tokens` and one
+    of the remainder): the same ids as the steps run eagerly, bit-identical last logits, KV caches
+    and state, for the persistent step and the launch sequence."""
+    import torch
+    from webpytorch_amd import llm
+    seed = 6 if sh["L"] == 24 else 17
+    w = synth.decoder_weights(seed, gaussian=True, **sh)
+    ids = synth.prompt_ids(seed, prompt, sh["V"])
+    a = llm.CausalLM.from_weights(w, lmax=prompt + n + 8, persistent=persistent)
+    b = llm.CausalLM.from_weights(w, lmax=prompt + n + 8, persistent=persistent)
+    a.graph_tokens = 4 if sh["L"] == 2 else 8
+    assert len(a._chunks(n - 1)) == 2  # full graphs and a remainder graph
+    ra, rb = a.generate(ids, n), b.generate(ids, n, use_graph=False)
+    assert ra.tokens == rb.tokens and sorted(a._graphs) == sorted(t for t, _ in a._chunks(n - 1))
+    assert torch.equal(a.state[:4], b.state[:4])
+    assert np.array_equal(a.buf["logits"].cpu().numpy().view(np.uint32), b.buf["logits"].cpu().numpy().view(np.uint32))
+    m = prompt + n - 1
+    for ca, cb in ((a.kc, b.kc), (a.vc, b.vc)):
+        assert np.array_equal(ca[:, :, :m].cpu().numpy().view(np.uint32), cb[:, :, :m].cpu().numpy().view(np.uint32))
+    assert (a.persistent_error(), b.persistent_error()) == (0, 0)
+
+
+def test_persistent_graph_stops_at_the_cache_end(gpu):
+    """A graph of 8 persistent steps replayed 4 positions before LMAX decodes those 4 tokens (as 4
+    eager steps do); the other 4 steps do no work and report error bit 2, the state at LMAX."""
+    import torch
+    a, b, ids = _persistent_pair(SMALL, 18, 64, 60)
+    for m in (a, b):
+        m.generate(ids, 1, use_graph=False)
+    a.graph(8).replay()
+    for _ in range(4):
+        b._step(1)
+    torch.cuda.synchronize()
+    assert a.persistent_error() == 2 and b.persistent_error() == 0
+    assert int(a.state[0]) == a.lmax and torch.equal(a.state[:4], b.state[:4])
+    assert torch.equal(a.history, b.history)
 
 
 def test_persistent_trace_matches_untraced_step(gpu):
