@@ -383,16 +383,30 @@ MIQ_PD_INLINE bool role_qkv(const Params& p, const Ctx& c, const Lds& s, int t, 
   return true;
 }
 
+// q . k over 16 dimensions (q from LDS, k in registers), fused multiply-adds in order.
+__device__ __forceinline__ float dot16(const float* q, const float4* k) {
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a = fmaf(q[4 * i], k[i].x, a);
+    a = fmaf(q[4 * i + 1], k[i].y, a);
+    a = fmaf(q[4 * i + 2], k[i].z, a);
+    a = fmaf(q[4 * i + 3], k[i].w, a);
+  }
+  return a;
+}
+
 // Query head hq at position pos over positions 0..pos, all layers: RoPE of q and of the kv
 // head's new k (the first query head of each group writes k and v into the caches), scores
-// (q . k) * scale, softmax, sum p v, published as the head's 64 tagged outputs. Four threads per
-// position for the scores, a wave per residue of the position mod 16 and a lane per dimension
-// for the weighted sum. The cache rows of the first 256 positions and the RoPE row are loaded
-// before q/k/v are waited for.
+// (q . k) * scale, softmax, sum p v, published as the head's 64 tagged outputs. Each wave takes
+// every 16th position (four threads per position for the scores, a lane per dimension for the
+// weighted sum) with a softmax of its own (running maximum and sum), and the 16 waves' partials
+// are combined once, rescaled to the common maximum: no barrier between the scores, the softmax
+// and the weighted sum. The cache rows of the first 256 positions and the
+// RoPE row are loaded before q/k/v are waited for.
 template <bool TR>
 MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq, int pos) {
   const int NH = p.NH, NKV = p.NKV, LMAX = p.LMAX, rep = NH / NKV, g = hq / rep, S = pos + 1;
-  float* sp = s.hin + 256;  // scores -> probabilities [S]
   float* qs = s.qkv;
   float* kn = s.qkv + 64;
   float* vn = s.qkv + 128;
@@ -401,7 +415,8 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
   for (int l = 0; l < p.L; ++l) {
     // thread indices recomputed per layer (opaque_tid): address math hoisted out of the layer
     // loop would hold registers for the whole token
-    const int tid = opaque_tid(), wave = uniform(tid >> 6), lane = tid & 63, qq = tid & 3, jq = tid >> 2;
+    const int tid = opaque_tid(), wave = uniform(tid >> 6), lane = tid & 63, qq = tid & 3;
+    const int jq = wave + 16 * (lane >> 2);  // this quad's position in a 256-position chunk
     const uint64_t* lt = p.layers + (size_t)l * kSlots;
     float* kc = (float*)lt[KC] + (size_t)g * LMAX * 64;
     float* vc = (float*)lt[VC] + (size_t)g * LMAX * 64;
@@ -437,71 +452,64 @@ MIQ_PD_INLINE bool role_attn(const Params& p, const Ctx& c, const Lds& s, int hq
       }
     }
     __syncthreads();
+    PD_MARK(l, 3);
+    // online softmax per wave: wave w takes positions cb + w + 16 i (i = lane / 4: four lanes
+    // each for the scores) of every 256-position chunk, keeps its running maximum m, sum of
+    // weights ws and weighted sum o (lane = dimension); the partials are combined once at the end.
+    // The wave's positions below S are a prefix i < nw of its 16 (uniform).
+    const float vnl = vn[lane];
+    float m = -INFINITY, ws = 0.f, o = 0.f;
     for (int cb = 0; cb < S; cb += 256) {
-      const int j = cb + jq;
-      float4 k4[4];
+      const int j = cb + jq, nw = min(16, max(0, (S - cb - wave + 15) / 16));
+      if (nw == 0) break;  // uniform: no later chunk has positions of this wave either
+      float a;
       if (cb == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) k4[i] = kr[i];
+        a = dot16(qs + qq * 16, kr);
       } else {
+        float4 k4[4];
         const float* kp = kc + (size_t)min(j, LMAX - 1) * 64 + qq * 16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) k4[i] = ldgf4(kp + 4 * i);
+        a = dot16(qs + qq * 16, k4);
       }
-      if (j == pos) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kn + qq * 16 + 4 * i);
-      }
-      const float* qp = qs + qq * 16;
-      float a = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a = fmaf(qp[4 * i], k4[i].x, a);
-        a = fmaf(qp[4 * i + 1], k4[i].y, a);
-        a = fmaf(qp[4 * i + 2], k4[i].z, a);
-        a = fmaf(qp[4 * i + 3], k4[i].w, a);
-      }
+      if (j == pos) a = dot16(qs + qq * 16, reinterpret_cast<const float4*>(kn + qq * 16));  // one quad
       a = quad_sum(a);
-      if (qq == 0 && j < S) sp[j] = a * p.scale;
-    }
-    __syncthreads();
-    PD_MARK(l, 3);
-    if (wave == 0) {  // softmax in one wave: DPP reductions, one barrier after it
-      float mx = -INFINITY;
-      for (int j = lane; j < S; j += 64) mx = fmaxf(mx, sp[j]);
-      mx = wave_max(mx);
-      float sum = 0.f;
-      for (int j = lane; j < S; j += 64) {
-        const float e = expf(sp[j] - mx);
-        sp[j] = e;
-        sum += e;
-      }
-      sum = wave_sum(sum);
-      if (lane == 0) s.red16[16] = sum;  // the division waits until the weighted sum
-    }
-    __syncthreads();
-    PD_MARK(l, 4);
-    float o = 0.f;
-    for (int cb = 0; cb < S; cb += 256) {
+      const float sc = j < S ? a * p.scale : -INFINITY;
+      const float mn = fmaxf(m, wave_max(sc));  // finite: the wave has a position below S
+      const float r = m == -INFINITY ? 0.f : expf(m - mn);
+      const float pj = expf(sc - mn);
+      ws = ws * r + wave_sum(qq == 0 ? pj : 0.f);
+      o = o * r;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int j = cb + wave + 16 * i;
-        if (j < S) {
-          const float v = j == pos ? vn[lane] : cb == 0 ? vr[i] : ldg(vc + (size_t)j * 64 + lane);
-          o = fmaf(sp[j], v, o);
+        if (i < nw) {  // uniform
+          const int jj = cb + wave + 16 * i;
+          float v = cb == 0 ? vr[i] : ldg(vc + (size_t)jj * 64 + lane);
+          if (jj == pos) v = vnl;  // uniform: the row is written this step
+          o = fmaf(lane_at(pj, 4 * i), v, o);
         }
       }
+      m = mn;
     }
-    // 16 waves' partial sums, combined in wave order, then divided by the softmax denominator.
-    // (The next layer's reads of red and red16 follow its wait's barrier, which this wave joins
-    // only after the reads below.)
+    PD_MARK(l, 4);
+    // the 16 waves' partials, combined in wave order: sum_w e_w o_w / sum_w e_w ws_w with
+    // e_w = e^(m_w - M), lane w of wave 0 taking e_w (the next layer's reads of red and red16
+    // follow its wait's barrier, which this wave joins only after the reads below)
     s.red[wave * 64 + lane] = o;
+    if (lane == 0) {
+      s.red16[wave] = m;
+      s.red16[16 + wave] = ws;
+    }
     __syncthreads();
     if (tid < 64) {
-      float y = 0.f;
+      const float mw = lane < kWaves ? s.red16[lane] : -INFINITY;
+      const float mx = wave_max(mw);
+      const float e = mw == -INFINITY ? 0.f : expf(mw - mx);
+      const float den = wave_sum(lane < kWaves ? e * s.red16[16 + lane] : 0.f);
+      float num = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) y += s.red[w * 64 + tid];
-      tput(p.tatt + hq * 64 + tid, c.tag(l, P_ATT), y / s.red16[16]);
+      for (int w = 0; w < kWaves; ++w) num = fmaf(lane_at(e, w), s.red[w * 64 + tid], num);
+      tput(p.tatt + hq * 64 + tid, c.tag(l, P_ATT), num / den);
     }
     PD_MARK(l, 2);
   }
@@ -828,7 +836,8 @@ static int plan(int L, int H, int NH, int NKV, int HD, int I, int V, int LMAX, i
   const int KS = I / q.ksd;
   q.spa = 2 * ((H / 64 + kKParts - 1) / kKParts);  // 32-k halves per k-part (64-k steps dealt whole)
   q.spd = 2 * ((KS / 64 + kKParts - 1) / kKParts);
-  q.lds_a = std::max(std::max(std::max(H, 2 * KS), (NH + 1) * kTile), std::max(256 + LMAX, 2 * q.G));
+  // hin: exchange words of every role (the heads' q|k|v words: 192), the arg-max partials (2G)
+  q.lds_a = std::max(std::max(std::max(H, 2 * KS), (NH + 1) * kTile), std::max(192, 2 * q.G));
   q.lds_a = (q.lds_a + 3) & ~3;
   q.lds_x = (std::max(std::max(H, KS), NHD) + 63) & ~63;  // even step count: red 16-byte aligned
   q.lds_bytes = (size_t)(q.lds_a + q.lds_x) * 4 + (size_t)(q.lds_x / 32) * kStep8Bytes +
