@@ -655,7 +655,8 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   float zo = p.head_zoff;
   pin(zo);
   // three tiles in flight: b and b + G are loaded before the wait for h; then each step issues
-  // the tile two steps ahead and holds (pins) the next one once the current one is computed
+  // the tile two steps ahead (not pinned: the step's barrier keeps the loads where they are
+  // issued, and a pin would wait for them a step early; 350.7 -> 348.8 us per token)
   Tile<float, SA> t0, t1, t2;
   if (b < ntile) tile_issue<float, SA, true, true>(t0, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
   if (b + G < ntile) tile_issue<float, SA, true, true>(t1, p.head_qw, p.head_qz, p.head_sc, V, (b + G) * kTile, 0, H / 32, p.lgs);
@@ -672,7 +673,7 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   const float rn = norm_r(s.red16, H, p.eps);
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  auto step = [&](Tile<float, SA>& cur, Tile<float, SA>& nxt, Tile<float, SA>& ahead, int t)
+  auto step = [&](Tile<float, SA>& cur, Tile<float, SA>& ahead, int t)
                   __attribute__((always_inline)) {
     if (t >= ntile) return;  // uniform
     if (t + 2 * G < ntile)
@@ -684,12 +685,11 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
       if (better(y, n, bv, bi) || (bv != bv && y == y)) { bv = y; bi = n; }
     }
     __syncthreads();
-    if (t + G < ntile) pin(nxt);  // issued a step ago, computed next
   };
   for (int t = b; t < ntile; t += 3 * G) {
-    step(t0, t1, t2, t);
-    step(t1, t2, t0, t + G);
-    step(t2, t0, t1, t + 2 * G);
+    step(t0, t2, t);
+    step(t1, t0, t + G);
+    step(t2, t1, t + 2 * G);
   }
   if (threadIdx.x < 64) {
     wave_argmax(bv, bi);
