@@ -656,7 +656,7 @@ MIQ_PD_INLINE bool role_head(const Params& p, const Ctx& c, const Lds& s, int to
   pin(zo);
   // three tiles in flight: b and b + G are loaded before the wait for h; then each step issues
   // the tile two steps ahead (not pinned: the step's barrier keeps the loads where they are
-  // issued, and a pin would wait for them a step early; 350.7 -> 348.8 us per token)
+  // issued, and a pin would wait for them a step early)
   Tile<float, SA> t0, t1, t2;
   if (b < ntile) tile_issue<float, SA, true, true>(t0, p.head_qw, p.head_qz, p.head_sc, V, b * kTile, 0, H / 32, p.lgs);
   if (b + G < ntile) tile_issue<float, SA, true, true>(t1, p.head_qw, p.head_qz, p.head_sc, V, (b + G) * kTile, 0, H / 32, p.lgs);
